@@ -1,0 +1,887 @@
+// Paged KV-cache kernels for MI355X (gfx950) behind the C ABI of include/barq_kv.h.
+//
+// Storage of one layer: key/value pages [num_pages, page_size, kv_heads, head_dim], so one
+// token's K (or V) across all heads is one contiguous run of kv_heads*head_dim elements -- the
+// same run HF attention produces ([B, T, H, D] physical, viewed as [B, H, T, D]).  Rows reach
+// their pages through an int32 block table; free pages sit on an int32 stack.  All element
+// traffic is a bit copy, done in the widest vector (16, 8, 4, 2 or 1 bytes) that every
+// address and stride admits.
+//
+// Semantics follow the reference layer (python/barqtrain/kv_cache.py:75-91,120-133): token t
+// of row b is stored at slot seq_lens[b] + t, and a gathered slot s of row b is the value last
+// stored there when s < high_water[b], else zero (the reference cache is zero-initialised,
+// kv_cache.py:66-71, and crop() lowers seq_lens without clearing, :158-164).
+//
+// Page allocation is deterministic: the new blocks of a launch are ranked in (row, block)
+// order and rank k takes free_pages[top - 1 - k].  Every tile can therefore compute the page
+// of any new block on its own; the stack top, block table and row lengths are committed once
+// per launch, by the last tile to finish (arrival counter) or by a one-workgroup launch.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "barq_kv.h"
+#include "fastdiv.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWave = 64;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kUnroll = 8;            // vectors in flight per thread
+constexpr int kMaxTilePages = 64;     // block-table slots a tile stages in LDS
+constexpr int kTileTargetBytes = 32 * 1024;
+
+template <int VB>
+struct VecT;
+template <>
+struct VecT<16> { using T = uint4; };
+template <>
+struct VecT<8> { using T = uint2; };
+template <>
+struct VecT<4> { using T = uint32_t; };
+template <>
+struct VecT<2> { using T = uint16_t; };
+template <>
+struct VecT<1> { using T = uint8_t; };
+
+template <typename T>
+__device__ __forceinline__ T zero_vec() { return T{}; }
+template <>
+__device__ __forceinline__ uint4 zero_vec<uint4>() { return make_uint4(0u, 0u, 0u, 0u); }
+template <>
+__device__ __forceinline__ uint2 zero_vec<uint2>() { return make_uint2(0u, 0u); }
+
+__device__ __forceinline__ int ceil_div_fd(int n, const FastDiv& d) {
+  return n <= 0 ? 0 : (int)d.div((uint32_t)(n + (int)d.d - 1));
+}
+
+// A page id read from the stack or the table, or -1 when it names no page of the pool.
+__device__ __forceinline__ int checked_page(int page, int64_t num_pages) {
+  return (page >= 0 && (int64_t)page < num_pages) ? page : -1;
+}
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Exclusive prefix sum of v over the workgroup's threads; *total gets the sum of all.
+// Uses lds[0 .. kWaves).  Every thread of the workgroup must call it.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* lds, int* total) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int up = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += up;
+  }
+  if (lane == kWave - 1) lds[wave] = incl;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int t = lds[w];
+    if (w < wave) before += t;
+    all += t;
+  }
+  __syncthreads();
+  *total = all;
+  return before + incl - v;
+}
+
+// Number of blocks of row r that an append of `tokens` maps for the first time, and the first
+// of them.  Blocks at or beyond max_blocks are never mapped (the capacity bit reports them).
+struct NewBlocks {
+  int first;
+  int count;
+};
+
+__device__ __forceinline__ NewBlocks new_blocks(int len, int hw, int tokens, int max_blocks,
+                                                const FastDiv& div_page) {
+  NewBlocks nb;
+  nb.first = ceil_div_fd(hw, div_page);
+  const int end = min(ceil_div_fd(len + tokens, div_page), max_blocks);
+  nb.count = tokens > 0 ? max(0, end - nb.first) : 0;
+  return nb;
+}
+
+// Rank of the first new block of row `row`: the number of new blocks of rows [0, row).
+// Called by one whole wave.
+__device__ int wave_rank_base(const barq_kv_pool& p, int row, int tokens,
+                              const FastDiv& div_page) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int acc = 0;
+  for (int r0 = 0; r0 < row; r0 += kWave) {
+    const int r = r0 + lane;
+    int c = 0;
+    if (r < row) c = new_blocks(p.seq_lens[r], p.high_water[r], tokens, (int)p.max_blocks, div_page).count;
+    acc += wave_sum(c);
+  }
+  return acc;
+}
+
+// Commit an append of `tokens` to rows [0, batch): map new blocks to pages in rank order,
+// advance seq_lens and high_water, pop the stack.  Run by one whole workgroup, after every tile
+// that read the old metadata has finished reading it.
+__device__ void commit_append(const barq_kv_pool& p, int batch, int tokens,
+                              const FastDiv& div_page) {
+  __shared__ int lds_scan[kWaves];
+  const int top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
+  const int mb = (int)p.max_blocks;
+  int used = 0;
+  int err = 0;
+  for (int r0 = 0; r0 < batch; r0 += kThreads) {
+    const int r = r0 + (int)threadIdx.x;
+    int len = 0, hw = 0;
+    NewBlocks nb{0, 0};
+    if (r < batch) {
+      len = p.seq_lens[r];
+      hw = p.high_water[r];
+      nb = new_blocks(len, hw, tokens, mb, div_page);
+      if (ceil_div_fd(len + tokens, div_page) > mb) err |= BARQ_KV_ERRBIT_CAPACITY;
+    }
+    int chunk_total = 0;
+    const int excl = block_exclusive_scan(nb.count, lds_scan, &chunk_total);
+    if (r < batch) {
+      for (int j = 0; j < nb.count; ++j) {
+        const int idx = top - 1 - (used + excl + j);
+        const int page = idx >= 0 ? checked_page(p.free_pages[idx], p.num_pages) : -1;
+        if (page < 0) err |= BARQ_KV_ERRBIT_POOL_EXHAUSTED;
+        p.block_table[(int64_t)r * mb + nb.first + j] = page;
+      }
+      p.seq_lens[r] = len + tokens;
+      p.high_water[r] = max(hw, len + tokens);
+    }
+    used += chunk_total;
+  }
+  if (threadIdx.x == 0) p.ctrl[BARQ_KV_CTRL_FREE_TOP] = max(0, top - used);
+  if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Append / gather / update: one tile = one (k|v, row, chunk of positions).
+// ---------------------------------------------------------------------------------------------
+
+struct StreamArgs {
+  barq_kv_pool pool;
+  const char* in_k;
+  const char* in_v;
+  char* out_k;
+  char* out_v;
+  int64_t in_sb, in_sh, in_st;     // bytes
+  int64_t out_sb, out_sh, out_ss;  // bytes
+  int64_t page_bytes;
+  int64_t tok_bytes;
+  int32_t batch;
+  int32_t tokens;
+  int32_t seq_out;   // gather: positions covered by the grid (capacity with SEQ_FROM_DEVICE)
+  int32_t chunk;     // positions per tile (a multiple of page_size when gathering)
+  int32_t chunks;    // tiles per (row, k|v)
+  int32_t gather;    // write the materialised output
+  int32_t seq_from_device;
+  int32_t commit_in_kernel;  // last tile commits the append
+  int32_t hv;        // vectors per token (kv_heads * vr)
+  FastDiv div_hv;    // by hv
+  FastDiv div_vr;    // by vectors per head row
+  FastDiv div_page;  // by page_size
+  FastDiv div_chunks;
+};
+
+template <int VB>
+__global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
+  using V = typename VecT<VB>::T;
+  __shared__ int s_pages[kMaxTilePages + 1];
+  __shared__ int s_meta[6];  // len, hw, lo, hi, blk_lo, last
+
+  const barq_kv_pool& p = a.pool;
+  const int kv = blockIdx.x & 1;
+  const int rest = blockIdx.x >> 1;
+  const int b = (int)a.div_chunks.div((uint32_t)rest);
+  const int c = rest - b * (int)a.div_chunks.d;
+  const int T = a.tokens;
+  const int P = (int)p.page_size;
+
+  if (threadIdx.x < kWave) {
+    const int lane = threadIdx.x;
+    const int len = p.seq_lens[b];
+    const int hw = p.high_water[b];
+    int smax = a.seq_out;
+    if (a.seq_from_device) {
+      int m = 0;
+      for (int r = lane; r < a.batch; r += kWave) m = max(m, p.seq_lens[r] + T);
+      smax = min(wave_max(m), a.seq_out);
+    }
+    int lo, hi;
+    if (a.gather) {
+      lo = c * a.chunk;
+      hi = min(lo + a.chunk, smax);
+    } else {
+      lo = len + c * a.chunk;
+      hi = min(lo + a.chunk, len + T);
+    }
+    int blk_lo = 0, nblk = 0;
+    if (hi > lo) {
+      blk_lo = (int)a.div_page.div((uint32_t)lo);
+      nblk = (int)a.div_page.div((uint32_t)(hi - 1)) - blk_lo + 1;
+    }
+    const NewBlocks nb = new_blocks(len, hw, T, (int)p.max_blocks, a.div_page);
+    const bool touches_new = nb.count > 0 && blk_lo < nb.first + nb.count && blk_lo + nblk > nb.first;
+    int top = 0, base = 0;
+    if (touches_new) {
+      top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
+      base = wave_rank_base(p, b, T, a.div_page);
+    }
+    for (int i = lane; i < nblk; i += kWave) {
+      const int blk = blk_lo + i;
+      int page = -1;
+      if (blk < (int)p.max_blocks) {
+        if (blk < nb.first) {
+          page = checked_page(p.block_table[(int64_t)b * p.max_blocks + blk], p.num_pages);
+        } else if (blk < nb.first + nb.count) {
+          const int idx = top - 1 - (base + blk - nb.first);
+          page = idx >= 0 ? checked_page(p.free_pages[idx], p.num_pages) : -1;
+        }
+      }
+      s_pages[i] = page;
+    }
+    if (lane == 0) {
+      s_meta[0] = len;
+      s_meta[1] = hw;
+      s_meta[2] = lo;
+      s_meta[3] = hi;
+      s_meta[4] = blk_lo;
+    }
+  }
+  __syncthreads();
+
+  const int len = s_meta[0];
+  const int hw = s_meta[1];
+  const int lo = s_meta[2];
+  const int hi = s_meta[3];
+  const int blk_lo = s_meta[4];
+  const int total = (hi > lo ? hi - lo : 0) * a.hv;
+
+  const char* in = kv ? a.in_v : a.in_k;
+  char* pages = (char*)(kv ? p.value_pages : p.key_pages);
+  char* out = kv ? a.out_v : a.out_k;
+  const int64_t in_row = (int64_t)b * a.in_sb;
+  const int64_t out_row = (int64_t)b * a.out_sb;
+
+  for (int i0 = threadIdx.x; i0 < total; i0 += kThreads * kUnroll) {
+    V val[kUnroll];
+    int64_t dst[kUnroll];
+    int64_t pdst[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = i0 + u * kThreads;
+      dst[u] = -1;
+      pdst[u] = -1;
+      val[u] = zero_vec<V>();
+      if (i < total) {
+        const int tok = (int)a.div_hv.div((uint32_t)i);
+        const int hv = i - tok * a.hv;
+        const int s = lo + tok;
+        const int h = (int)a.div_vr.div((uint32_t)hv);
+        const int v = hv - h * (int)a.div_vr.d;
+        const int blk = (int)a.div_page.div((uint32_t)s);
+        const int off = s - blk * P;
+        const int page = s_pages[blk - blk_lo];
+        const int64_t poff = (int64_t)page * a.page_bytes + (int64_t)off * a.tok_bytes + (int64_t)hv * VB;
+        if (s >= len && s < len + T) {
+          val[u] = *(const V*)(in + in_row + (int64_t)h * a.in_sh + (int64_t)(s - len) * a.in_st + (int64_t)v * VB);
+          if (page >= 0) pdst[u] = poff;
+        } else if (s < hw && page >= 0) {
+          val[u] = *(const V*)(pages + poff);
+        }
+        if (a.gather) dst[u] = out_row + (int64_t)h * a.out_sh + (int64_t)s * a.out_ss + (int64_t)v * VB;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (dst[u] >= 0) *(V*)(out + dst[u]) = val[u];
+      if (pdst[u] >= 0) *(V*)(pages + pdst[u]) = val[u];
+    }
+  }
+
+  if (T > 0 && a.commit_in_kernel) {
+    // Every tile read its metadata before the barrier above; arriving after its copy loop, the
+    // last tile to arrive is the only writer of that metadata in this launch.
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int prev = atomicAdd(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 1);
+      s_meta[5] = (prev == (int)gridDim.x - 1);
+    }
+    __syncthreads();
+    if (s_meta[5]) {
+      commit_append(p, a.batch, T, a.div_page);
+      if (threadIdx.x == 0) atomicExch(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 0);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) commit_kernel(const barq_kv_pool p, int batch,
+                                                         int tokens, FastDiv div_page) {
+  commit_append(p, batch, tokens, div_page);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Dense drop-in (reference layout [cache_batch, H, max_blocks, P, D]).
+// ---------------------------------------------------------------------------------------------
+
+struct DenseArgs {
+  char* kc;
+  char* vc;
+  const int32_t* seq_lens;
+  const char* ks;
+  const char* vs;
+  int64_t sb, sh, st;  // bytes
+  int64_t row_bytes;
+  int32_t heads, tokens, max_blocks, page_size;
+  int32_t total;       // batch * heads * tokens * vr
+  FastDiv div_vr, div_tokens, div_heads, div_page;
+};
+
+template <int VB>
+__global__ void __launch_bounds__(kThreads) dense_append_kernel(const DenseArgs a) {
+  using V = typename VecT<VB>::T;
+  const int stride = (int)(gridDim.x * kThreads);
+  for (int i0 = blockIdx.x * kThreads + threadIdx.x; i0 < a.total; i0 += stride * kUnroll) {
+    V kval[kUnroll], vval[kUnroll];
+    int64_t dst[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = i0 + u * stride;
+      dst[u] = -1;
+      kval[u] = zero_vec<V>();
+      vval[u] = zero_vec<V>();
+      if (i < a.total) {
+        // i -> (b, h, t, v) over [batch, heads, tokens, vectors per row]
+        const int row = (int)a.div_vr.div((uint32_t)i);
+        const int v = i - row * (int)a.div_vr.d;
+        const int bh = (int)a.div_tokens.div((uint32_t)row);
+        const int t = row - bh * a.tokens;
+        const int b = (int)a.div_heads.div((uint32_t)bh);
+        const int h = bh - b * a.heads;
+        const int pos = a.seq_lens[b] + t;
+        const int blk = (int)a.div_page.div((uint32_t)pos);
+        if (blk < a.max_blocks) {  // paged_kv_cache.cu:42-44 skips slots past the last block
+          const int off = pos - blk * a.page_size;
+          const int64_t src = (int64_t)b * a.sb + (int64_t)h * a.sh + (int64_t)t * a.st + (int64_t)v * VB;
+          dst[u] = (((int64_t)bh * a.max_blocks + blk) * a.page_size + off) * a.row_bytes + (int64_t)v * VB;
+          kval[u] = *(const V*)(a.ks + src);
+          vval[u] = *(const V*)(a.vs + src);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (dst[u] >= 0) {
+        *(V*)(a.kc + dst[u]) = kval[u];
+        *(V*)(a.vc + dst[u]) = vval[u];
+      }
+    }
+  }
+}
+
+__global__ void dense_bump_kernel(int32_t* seq_lens, int batch, int tokens) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < batch) seq_lens[i] += tokens;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Pool bookkeeping.
+// ---------------------------------------------------------------------------------------------
+
+__global__ void reset_kernel(const barq_kv_pool p, const int32_t* order) {
+  const int64_t n_pages = p.num_pages;
+  const int64_t n_table = p.max_batch * p.max_blocks;
+  int64_t n = n_pages > n_table ? n_pages : n_table;
+  if (n < p.max_batch) n = p.max_batch;
+  if (n < BARQ_KV_CTRL_WORDS) n = BARQ_KV_CTRL_WORDS;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    // Stack entry i is popped (num_pages - 1 - i)-th, so page_order[k] is the k-th page taken.
+    if (i < n_pages) p.free_pages[i] = order ? order[n_pages - 1 - i] : (int32_t)(n_pages - 1 - i);
+    if (i < n_table) p.block_table[i] = -1;
+    if (i < p.max_batch) {
+      p.seq_lens[i] = 0;
+      p.high_water[i] = 0;
+    }
+    if (i < BARQ_KV_CTRL_WORDS) p.ctrl[i] = (i == BARQ_KV_CTRL_FREE_TOP) ? (int32_t)n_pages : 0;
+  }
+}
+
+__global__ void crop_kernel(int32_t* seq_lens, int batch, int max_length) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < batch) seq_lens[i] = min(seq_lens[i], max_length);
+}
+
+// One workgroup: push the pages of the listed rows back on the stack.
+__global__ void __launch_bounds__(kThreads) free_rows_kernel(const barq_kv_pool p,
+                                                            const int32_t* rows, int n,
+                                                            FastDiv div_page) {
+  __shared__ int lds_scan[kWaves];
+  const int top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
+  const int mb = (int)p.max_blocks;
+  int pushed = 0;
+  int err = 0;
+  for (int i0 = 0; i0 < n; i0 += kThreads) {
+    const int i = i0 + (int)threadIdx.x;
+    int r = -1, cnt = 0;
+    if (i < n) {
+      r = rows[i];
+      if (r < 0 || r >= (int)p.max_batch) {
+        err |= BARQ_KV_ERRBIT_BAD_INDEX;
+        r = -1;
+      } else {
+        cnt = min(ceil_div_fd(p.high_water[r], div_page), mb);
+      }
+    }
+    int chunk_total = 0;
+    const int excl = block_exclusive_scan(cnt, lds_scan, &chunk_total);
+    if (r >= 0) {
+      for (int j = 0; j < cnt; ++j) {
+        const int64_t slot = (int64_t)top + pushed + excl + j;
+        int32_t* e = &p.block_table[(int64_t)r * mb + j];
+        if (slot < p.num_pages) p.free_pages[slot] = *e;
+        else err |= BARQ_KV_ERRBIT_BAD_INDEX;
+        *e = -1;
+      }
+      p.seq_lens[r] = 0;
+      p.high_water[r] = 0;
+    }
+    pushed += chunk_total;
+  }
+  if (threadIdx.x == 0) p.ctrl[BARQ_KV_CTRL_FREE_TOP] = (int)min((int64_t)top + pushed, p.num_pages);
+  if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
+}
+
+// Workgroup-wide copy of nvec vectors of VB bytes.
+template <int VB>
+__device__ __forceinline__ void copy_run(const char* src, char* dst, int nvec) {
+  using V = typename VecT<VB>::T;
+  for (int v0 = threadIdx.x; v0 < nvec; v0 += kThreads * kUnroll) {
+    V val[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int v = v0 + u * kThreads;
+      val[u] = v < nvec ? *(const V*)(src + (int64_t)v * VB) : zero_vec<V>();
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int v = v0 + u * kThreads;
+      if (v < nvec) *(V*)(dst + (int64_t)v * VB) = val[u];
+    }
+  }
+}
+
+// Copy rows: tile = (dst row i, block j) copies one K page and one V page.
+struct CopyArgs {
+  barq_kv_pool src;
+  barq_kv_pool dst;
+  const int32_t* rows;
+  int32_t n;
+  int64_t page_bytes;
+  FastDiv div_page;
+  FastDiv div_blocks;
+};
+
+template <int VB>
+__global__ void __launch_bounds__(kThreads) copy_rows_kernel(const CopyArgs a) {
+  using V = typename VecT<VB>::T;
+  __shared__ int s_meta[3];  // src page, dst page, last
+  const int mb = (int)a.src.max_blocks;
+  const int i = (int)a.div_blocks.div(blockIdx.x);
+  const int j = (int)blockIdx.x - i * mb;
+
+  if (threadIdx.x < kWave) {
+    const int lane = threadIdx.x;
+    // Rank base: blocks of dst rows [0, i).
+    int acc = 0;
+    for (int q0 = 0; q0 < i; q0 += kWave) {
+      const int q = q0 + lane;
+      int c = 0;
+      if (q < i) {
+        const int r = a.rows[q];
+        if (r >= 0 && r < (int)a.src.max_batch) c = min(ceil_div_fd(a.src.high_water[r], a.div_page), mb);
+      }
+      acc += wave_sum(c);
+    }
+    if (lane == 0) {
+      const int r = a.rows[i];
+      int sp = -1, dp = -1;
+      if (r >= 0 && r < (int)a.src.max_batch && j < min(ceil_div_fd(a.src.high_water[r], a.div_page), mb)) {
+        sp = checked_page(a.src.block_table[(int64_t)r * mb + j], a.src.num_pages);
+        const int idx = a.dst.ctrl[BARQ_KV_CTRL_FREE_TOP] - 1 - (acc + j);
+        dp = idx >= 0 ? checked_page(a.dst.free_pages[idx], a.dst.num_pages) : -1;
+      }
+      s_meta[0] = sp;
+      s_meta[1] = dp;
+    }
+  }
+  __syncthreads();
+  const int sp = s_meta[0];
+  const int dp = s_meta[1];
+  if (sp >= 0 && dp >= 0) {
+    const int nvec = (int)(a.page_bytes / VB);
+    copy_run<VB>((const char*)a.src.key_pages + (int64_t)sp * a.page_bytes,
+                 (char*)a.dst.key_pages + (int64_t)dp * a.page_bytes, nvec);
+    copy_run<VB>((const char*)a.src.value_pages + (int64_t)sp * a.page_bytes,
+                 (char*)a.dst.value_pages + (int64_t)dp * a.page_bytes, nvec);
+  }
+
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = atomicAdd(&a.dst.ctrl[BARQ_KV_CTRL_ARRIVED], 1);
+    s_meta[2] = (prev == (int)gridDim.x - 1);
+  }
+  __syncthreads();
+  if (!s_meta[2]) return;
+
+  // Last tile: commit dst metadata.
+  __shared__ int lds_scan[kWaves];
+  const int top = a.dst.ctrl[BARQ_KV_CTRL_FREE_TOP];
+  int used = 0, err = 0;
+  for (int q0 = 0; q0 < a.n; q0 += kThreads) {
+    const int q = q0 + (int)threadIdx.x;
+    int r = -1, cnt = 0;
+    if (q < a.n) {
+      r = a.rows[q];
+      if (r < 0 || r >= (int)a.src.max_batch) {
+        err |= BARQ_KV_ERRBIT_BAD_INDEX;
+        r = -1;
+      } else {
+        cnt = min(ceil_div_fd(a.src.high_water[r], a.div_page), mb);
+      }
+    }
+    int chunk_total = 0;
+    const int excl = block_exclusive_scan(cnt, lds_scan, &chunk_total);
+    if (q < a.n) {
+      for (int jj = 0; jj < cnt; ++jj) {
+        const int idx = top - 1 - (used + excl + jj);
+        const int page = idx >= 0 ? checked_page(a.dst.free_pages[idx], a.dst.num_pages) : -1;
+        if (page < 0) err |= BARQ_KV_ERRBIT_POOL_EXHAUSTED;
+        a.dst.block_table[(int64_t)q * mb + jj] = page;
+      }
+      a.dst.seq_lens[q] = r >= 0 ? a.src.seq_lens[r] : 0;
+      a.dst.high_water[q] = r >= 0 ? a.src.high_water[r] : 0;
+    }
+    used += chunk_total;
+  }
+  if (threadIdx.x == 0) {
+    a.dst.ctrl[BARQ_KV_CTRL_FREE_TOP] = max(0, top - used);
+    atomicExch(&a.dst.ctrl[BARQ_KV_CTRL_ARRIVED], 0);
+  }
+  if (err) atomicOr(&a.dst.ctrl[BARQ_KV_CTRL_ERRORS], err);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------------------------
+
+constexpr int64_t kI32Max = 0x7fffffffLL;
+
+int vector_bytes(uint64_t any_bits) {
+  // Largest power of two <= 16 dividing every address and byte stride OR-ed into any_bits.
+  int vb = 16;
+  while (vb > 1 && (any_bits & (uint64_t)(vb - 1))) vb >>= 1;
+  return vb;
+}
+
+bool pool_ok(const barq_kv_pool* p) {
+  if (!p || !p->key_pages || !p->value_pages || !p->block_table || !p->seq_lens ||
+      !p->high_water || !p->free_pages || !p->ctrl)
+    return false;
+  if (p->num_pages < 1 || p->max_batch < 1 || p->max_blocks < 1 || p->page_size < 1 ||
+      p->kv_heads < 1 || p->head_dim < 1)
+    return false;
+  if (!(p->elem_bytes == 1 || p->elem_bytes == 2 || p->elem_bytes == 4 || p->elem_bytes == 8))
+    return false;
+  if (p->num_pages > kI32Max || p->max_batch * p->max_blocks > kI32Max ||
+      p->max_blocks * p->page_size > kI32Max)
+    return false;
+  if (((uintptr_t)p->ctrl) & 255u) return false;
+  const int64_t tok = p->kv_heads * p->head_dim * p->elem_bytes;
+  if (tok * p->page_size > kI32Max) return false;
+  return true;
+}
+
+int launch(const void* fn, dim3 grid, void* arg, hipStream_t stream) {
+  void* args[] = {arg};
+  return hipLaunchKernel(fn, grid, dim3(kThreads), args, 0, stream) == hipSuccess ? BARQ_KV_OK
+                                                                                  : BARQ_KV_ERR_LAUNCH;
+}
+
+#define BARQ_DEFINE_VB_LAUNCH(KERNEL, ARGS)                                                     \
+  int launch_##KERNEL(int vb, dim3 grid, ARGS* arg, hipStream_t stream) {                      \
+    switch (vb) {                                                                               \
+      case 16: return launch((const void*)&KERNEL<16>, grid, arg, stream);                     \
+      case 8: return launch((const void*)&KERNEL<8>, grid, arg, stream);                       \
+      case 4: return launch((const void*)&KERNEL<4>, grid, arg, stream);                       \
+      case 2: return launch((const void*)&KERNEL<2>, grid, arg, stream);                       \
+      default: return launch((const void*)&KERNEL<1>, grid, arg, stream);                      \
+    }                                                                                           \
+  }
+
+BARQ_DEFINE_VB_LAUNCH(stream_kernel, StreamArgs)
+BARQ_DEFINE_VB_LAUNCH(dense_append_kernel, DenseArgs)
+BARQ_DEFINE_VB_LAUNCH(copy_rows_kernel, CopyArgs)
+
+// Shared body of append / gather / update.
+int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t batch,
+               int64_t tokens, int64_t sb, int64_t sh, int64_t st, void* ko, void* vo,
+               int64_t seq_out, int64_t osb, int64_t osh, int64_t oss, int64_t flags,
+               bool gather, void* stream) {
+  if (!pool_ok(pool)) return BARQ_KV_ERR_INVALID;
+  if (batch < 0 || batch > pool->max_batch || tokens < 0 || tokens > kI32Max) return BARQ_KV_ERR_INVALID;
+  if (flags & ~(int64_t)(BARQ_KV_SEQ_FROM_DEVICE | BARQ_KV_SEPARATE_FINALIZE)) return BARQ_KV_ERR_INVALID;
+  const int64_t cap = pool->max_blocks * pool->page_size;
+  if (tokens > 0 && (!ks || !vs)) return BARQ_KV_ERR_INVALID;
+  if (gather && (!ko || !vo || seq_out < 0 || seq_out > cap)) return BARQ_KV_ERR_INVALID;
+  if (tokens > cap) return BARQ_KV_ERR_INVALID;
+  if (batch == 0 || (tokens == 0 && (!gather || seq_out == 0))) return BARQ_KV_OK;
+
+  const int64_t eb = pool->elem_bytes;
+  const int64_t row_bytes = pool->head_dim * eb;
+  const int64_t tok_bytes = pool->kv_heads * row_bytes;
+  uint64_t bits = (uint64_t)row_bytes | (uint64_t)(uintptr_t)pool->key_pages |
+                  (uint64_t)(uintptr_t)pool->value_pages;
+  if (tokens > 0) bits |= (uint64_t)(uintptr_t)ks | (uint64_t)(uintptr_t)vs | (uint64_t)(sb * eb) |
+                          (uint64_t)(sh * eb) | (uint64_t)(st * eb);
+  if (gather) bits |= (uint64_t)(uintptr_t)ko | (uint64_t)(uintptr_t)vo | (uint64_t)(osb * eb) |
+                      (uint64_t)(osh * eb) | (uint64_t)(oss * eb);
+  const int vb = vector_bytes(bits);
+  const int64_t vr = row_bytes / vb;
+  const int64_t hv = pool->kv_heads * vr;
+
+  // Positions per tile: whole pages when gathering, about kTileTargetBytes of each of K and V.
+  const int64_t P = pool->page_size;
+  int64_t pages_per_tile = kTileTargetBytes / (P * tok_bytes);
+  if (pages_per_tile < 1) pages_per_tile = 1;
+  if (pages_per_tile > kMaxTilePages) pages_per_tile = kMaxTilePages;
+  // An append tile starts at an arbitrary slot, so its `chunk` positions touch at most
+  // pages_per_tile + 1 blocks: s_pages holds kMaxTilePages + 1.
+  const int64_t chunk = pages_per_tile * P;
+  if (chunk * hv > kI32Max) return BARQ_KV_ERR_INVALID;
+  const int64_t span = gather ? seq_out : tokens;
+  const int64_t chunks = (span + chunk - 1) / chunk;
+  const int64_t tiles = 2 * batch * chunks;
+  if (tiles > kI32Max || batch * chunks > kI32Max) return BARQ_KV_ERR_INVALID;
+
+  StreamArgs a;
+  a.pool = *pool;
+  a.in_k = (const char*)ks;
+  a.in_v = (const char*)vs;
+  a.out_k = (char*)ko;
+  a.out_v = (char*)vo;
+  a.in_sb = sb * eb;
+  a.in_sh = sh * eb;
+  a.in_st = st * eb;
+  a.out_sb = osb * eb;
+  a.out_sh = osh * eb;
+  a.out_ss = oss * eb;
+  a.page_bytes = P * tok_bytes;
+  a.tok_bytes = tok_bytes;
+  a.batch = (int32_t)batch;
+  a.tokens = (int32_t)tokens;
+  a.seq_out = (int32_t)(gather ? seq_out : 0);
+  a.chunk = (int32_t)chunk;
+  a.chunks = (int32_t)chunks;
+  a.gather = gather ? 1 : 0;
+  a.seq_from_device = (gather && (flags & BARQ_KV_SEQ_FROM_DEVICE)) ? 1 : 0;
+  a.commit_in_kernel = (flags & BARQ_KV_SEPARATE_FINALIZE) ? 0 : 1;
+  a.hv = (int32_t)hv;
+  a.div_hv = FastDiv::make((uint32_t)hv);
+  a.div_vr = FastDiv::make((uint32_t)vr);
+  a.div_page = FastDiv::make((uint32_t)P);
+  a.div_chunks = FastDiv::make((uint32_t)chunks);
+
+  hipStream_t s = (hipStream_t)stream;
+  int rc = launch_stream_kernel(vb, dim3((uint32_t)tiles), &a, s);
+  if (rc != BARQ_KV_OK) return rc;
+  if (tokens > 0 && !a.commit_in_kernel) {
+    barq_kv_pool pc = *pool;
+    int32_t b32 = (int32_t)batch, t32 = (int32_t)tokens;
+    FastDiv dp = a.div_page;
+    void* args[] = {&pc, &b32, &t32, &dp};
+    if (hipLaunchKernel((const void*)&commit_kernel, dim3(1), dim3(kThreads), args, 0, s) != hipSuccess)
+      return BARQ_KV_ERR_LAUNCH;
+  }
+  return BARQ_KV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* barq_kv_version(void) { return "barq_kv 0.1.0 gfx950"; }
+
+const char* barq_kv_status_string(int status) {
+  switch (status) {
+    case BARQ_KV_OK: return "ok";
+    case BARQ_KV_ERR_INVALID: return "invalid argument (pointer, size, stride or alignment)";
+    case BARQ_KV_ERR_LAUNCH: return "HIP kernel launch failed";
+    default: return "unknown status";
+  }
+}
+
+int barq_kv_append_dense(void* key_cache, void* value_cache, int32_t* seq_lens,
+                         const void* key_states, const void* value_states, int64_t batch,
+                         int64_t kv_heads, int64_t tokens, int64_t head_dim, int64_t cache_batch,
+                         int64_t max_blocks, int64_t page_size, int64_t elem_bytes,
+                         int64_t stride_b, int64_t stride_h, int64_t stride_t, void* stream) {
+  if (!key_cache || !value_cache || !seq_lens) return BARQ_KV_ERR_INVALID;
+  if (batch < 0 || kv_heads < 1 || tokens < 0 || head_dim < 1 || max_blocks < 1 || page_size < 1)
+    return BARQ_KV_ERR_INVALID;
+  if (batch > cache_batch) return BARQ_KV_ERR_INVALID;
+  if (!(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8)) return BARQ_KV_ERR_INVALID;
+  if (batch == 0) return BARQ_KV_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (tokens > 0) {
+    if (!key_states || !value_states) return BARQ_KV_ERR_INVALID;
+    const int64_t row_bytes = head_dim * elem_bytes;
+    const uint64_t bits = (uint64_t)row_bytes | (uint64_t)(uintptr_t)key_cache |
+                          (uint64_t)(uintptr_t)value_cache | (uint64_t)(uintptr_t)key_states |
+                          (uint64_t)(uintptr_t)value_states | (uint64_t)(stride_b * elem_bytes) |
+                          (uint64_t)(stride_h * elem_bytes) | (uint64_t)(stride_t * elem_bytes);
+    const int vb = vector_bytes(bits);
+    const int64_t vr = row_bytes / vb;
+    const int64_t total = batch * kv_heads * tokens * vr;
+    if (total > kI32Max || max_blocks * page_size > kI32Max) return BARQ_KV_ERR_INVALID;
+    DenseArgs a;
+    a.kc = (char*)key_cache;
+    a.vc = (char*)value_cache;
+    a.seq_lens = seq_lens;
+    a.ks = (const char*)key_states;
+    a.vs = (const char*)value_states;
+    a.sb = stride_b * elem_bytes;
+    a.sh = stride_h * elem_bytes;
+    a.st = stride_t * elem_bytes;
+    a.row_bytes = row_bytes;
+    a.heads = (int32_t)kv_heads;
+    a.tokens = (int32_t)tokens;
+    a.max_blocks = (int32_t)max_blocks;
+    a.page_size = (int32_t)page_size;
+    a.total = (int32_t)total;
+    a.div_vr = FastDiv::make((uint32_t)vr);
+    a.div_tokens = FastDiv::make((uint32_t)tokens);
+    a.div_heads = FastDiv::make((uint32_t)kv_heads);
+    a.div_page = FastDiv::make((uint32_t)page_size);
+    int64_t blocks = (total + (int64_t)kThreads * kUnroll - 1) / ((int64_t)kThreads * kUnroll);
+    if (blocks > 65536) blocks = 65536;
+    const int rc = launch_dense_append_kernel(vb, dim3((uint32_t)blocks), &a, s);
+    if (rc != BARQ_KV_OK) return rc;
+  }
+  int32_t b32 = (int32_t)batch, t32 = (int32_t)tokens;
+  void* args[] = {&seq_lens, &b32, &t32};
+  if (hipLaunchKernel((const void*)&dense_bump_kernel, dim3((uint32_t)((batch + kThreads - 1) / kThreads)),
+                      dim3(kThreads), args, 0, s) != hipSuccess)
+    return BARQ_KV_ERR_LAUNCH;
+  return BARQ_KV_OK;
+}
+
+int barq_kv_pool_reset(const barq_kv_pool* pool, const int32_t* page_order, void* stream) {
+  if (!pool_ok(pool)) return BARQ_KV_ERR_INVALID;
+  barq_kv_pool p = *pool;
+  const int64_t n = std::max(std::max(p.num_pages, p.max_batch * p.max_blocks),
+                             (int64_t)BARQ_KV_CTRL_WORDS);
+  int64_t blocks = (n + kThreads - 1) / kThreads;
+  if (blocks > 4096) blocks = 4096;
+  const int32_t* order = page_order;
+  void* args[] = {&p, &order};
+  return hipLaunchKernel((const void*)&reset_kernel, dim3((uint32_t)blocks), dim3(kThreads), args, 0,
+                         (hipStream_t)stream) == hipSuccess
+             ? BARQ_KV_OK
+             : BARQ_KV_ERR_LAUNCH;
+}
+
+int barq_kv_append(const barq_kv_pool* pool, const void* key_states, const void* value_states,
+                   int64_t batch, int64_t tokens, int64_t stride_b, int64_t stride_h,
+                   int64_t stride_t, void* stream) {
+  return run_stream(pool, key_states, value_states, batch, tokens, stride_b, stride_h, stride_t,
+                    nullptr, nullptr, 0, 0, 0, 0, 0, false, stream);
+}
+
+int barq_kv_gather(const barq_kv_pool* pool, void* key_out, void* value_out, int64_t batch,
+                   int64_t seq_out, int64_t out_stride_b, int64_t out_stride_h,
+                   int64_t out_stride_s, int64_t flags, void* stream) {
+  return run_stream(pool, nullptr, nullptr, batch, 0, 0, 0, 0, key_out, value_out, seq_out,
+                    out_stride_b, out_stride_h, out_stride_s, flags, true, stream);
+}
+
+int barq_kv_update(const barq_kv_pool* pool, const void* key_states, const void* value_states,
+                   int64_t batch, int64_t tokens, int64_t stride_b, int64_t stride_h,
+                   int64_t stride_t, void* key_out, void* value_out, int64_t seq_out,
+                   int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_s,
+                   int64_t flags, void* stream) {
+  return run_stream(pool, key_states, value_states, batch, tokens, stride_b, stride_h, stride_t,
+                    key_out, value_out, seq_out, out_stride_b, out_stride_h, out_stride_s, flags,
+                    true, stream);
+}
+
+int barq_kv_crop(const barq_kv_pool* pool, int64_t batch, int64_t max_length, void* stream) {
+  if (!pool_ok(pool) || batch < 0 || batch > pool->max_batch || max_length < 0) return BARQ_KV_ERR_INVALID;
+  if (batch == 0) return BARQ_KV_OK;
+  int32_t* lens = pool->seq_lens;
+  int32_t b32 = (int32_t)batch;
+  int32_t m32 = (int32_t)std::min(max_length, kI32Max);
+  void* args[] = {&lens, &b32, &m32};
+  return hipLaunchKernel((const void*)&crop_kernel, dim3((uint32_t)((batch + kThreads - 1) / kThreads)),
+                         dim3(kThreads), args, 0, (hipStream_t)stream) == hipSuccess
+             ? BARQ_KV_OK
+             : BARQ_KV_ERR_LAUNCH;
+}
+
+int barq_kv_free_rows(const barq_kv_pool* pool, const int32_t* rows, int64_t num_rows,
+                      void* stream) {
+  if (!pool_ok(pool) || num_rows < 0 || num_rows > pool->max_batch) return BARQ_KV_ERR_INVALID;
+  if (num_rows == 0) return BARQ_KV_OK;
+  if (!rows) return BARQ_KV_ERR_INVALID;
+  barq_kv_pool p = *pool;
+  int32_t n32 = (int32_t)num_rows;
+  FastDiv dp = FastDiv::make((uint32_t)p.page_size);
+  void* args[] = {&p, &rows, &n32, &dp};
+  return hipLaunchKernel((const void*)&free_rows_kernel, dim3(1), dim3(kThreads), args, 0,
+                         (hipStream_t)stream) == hipSuccess
+             ? BARQ_KV_OK
+             : BARQ_KV_ERR_LAUNCH;
+}
+
+int barq_kv_copy_rows(const barq_kv_pool* src, const barq_kv_pool* dst, const int32_t* src_rows,
+                      int64_t num_rows, void* stream) {
+  if (!pool_ok(src) || !pool_ok(dst)) return BARQ_KV_ERR_INVALID;
+  if (src->page_size != dst->page_size || src->kv_heads != dst->kv_heads ||
+      src->head_dim != dst->head_dim || src->elem_bytes != dst->elem_bytes ||
+      src->max_blocks != dst->max_blocks)
+    return BARQ_KV_ERR_INVALID;
+  if (num_rows < 0 || num_rows > dst->max_batch) return BARQ_KV_ERR_INVALID;
+  if (num_rows == 0) return BARQ_KV_OK;
+  if (!src_rows) return BARQ_KV_ERR_INVALID;
+  const int64_t tiles = num_rows * src->max_blocks;
+  if (tiles > kI32Max) return BARQ_KV_ERR_INVALID;
+  CopyArgs a;
+  a.src = *src;
+  a.dst = *dst;
+  a.rows = src_rows;
+  a.n = (int32_t)num_rows;
+  a.page_bytes = src->page_size * src->kv_heads * src->head_dim * src->elem_bytes;
+  a.div_page = FastDiv::make((uint32_t)src->page_size);
+  a.div_blocks = FastDiv::make((uint32_t)src->max_blocks);
+  const uint64_t bits = (uint64_t)a.page_bytes | (uint64_t)(uintptr_t)src->key_pages |
+                        (uint64_t)(uintptr_t)src->value_pages | (uint64_t)(uintptr_t)dst->key_pages |
+                        (uint64_t)(uintptr_t)dst->value_pages;
+  return launch_copy_rows_kernel(vector_bytes(bits), dim3((uint32_t)tiles), &a, (hipStream_t)stream);
+}
+
+}  // extern "C"

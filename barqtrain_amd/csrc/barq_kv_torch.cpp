@@ -1,0 +1,242 @@
+// barqtrain_cuda: the PyTorch-ROCm extension module the BarqTrain loader imports
+// (python/barqtrain/_ffi.py:117-121).  It only checks tensors and forwards raw pointers, sizes
+// and the current HIP stream to the C ABI of libbarq_kv.so (include/barq_kv.h); every kernel
+// lives there.  Host-only C++: no device code is compiled into this module.
+
+#include <torch/extension.h>
+
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <string>
+#include <vector>
+
+#include "barq_kv.h"
+
+namespace {
+
+void* current_stream(const at::Tensor& t) {
+  return (void*)c10::hip::getCurrentHIPStream(t.get_device()).stream();
+}
+
+void check_status(int rc, const char* what) {
+  TORCH_CHECK(rc == BARQ_KV_OK, what, ": ", barq_kv_status_string(rc));
+}
+
+int64_t elem_bytes_of(const at::Tensor& t) { return (int64_t)t.element_size(); }
+
+// The pool is passed as (key_pages, value_pages, block_table, seq_lens, high_water, free_pages,
+// ctrl), the tensors of barqtrain_amd.paged.PagePool.
+barq_kv_pool pool_from(const std::vector<at::Tensor>& t) {
+  TORCH_CHECK(t.size() == 7, "a page pool is 7 tensors");
+  const at::Tensor& kp = t[0];
+  const at::Tensor& vp = t[1];
+  TORCH_CHECK(kp.is_cuda() && vp.is_cuda(), "page pool must live on a GPU");
+  TORCH_CHECK(kp.dim() == 4 && vp.sizes() == kp.sizes(),
+              "key/value pages must be [num_pages, page_size, kv_heads, head_dim]");
+  TORCH_CHECK(kp.is_contiguous() && vp.is_contiguous(), "pages must be contiguous");
+  TORCH_CHECK(kp.scalar_type() == vp.scalar_type(), "key/value pages must share dtype");
+  for (size_t i = 2; i < 7; ++i) {
+    TORCH_CHECK(t[i].scalar_type() == at::kInt && t[i].is_contiguous() && t[i].is_cuda() &&
+                    t[i].get_device() == kp.get_device(),
+                "page-pool metadata must be contiguous int32 on the pool's device");
+  }
+  TORCH_CHECK(t[2].dim() == 2, "block_table must be [max_batch, max_blocks]");
+  barq_kv_pool p;
+  p.key_pages = kp.data_ptr();
+  p.value_pages = vp.data_ptr();
+  p.block_table = t[2].data_ptr<int32_t>();
+  p.seq_lens = t[3].data_ptr<int32_t>();
+  p.high_water = t[4].data_ptr<int32_t>();
+  p.free_pages = t[5].data_ptr<int32_t>();
+  p.ctrl = t[6].data_ptr<int32_t>();
+  p.num_pages = kp.size(0);
+  p.page_size = kp.size(1);
+  p.kv_heads = kp.size(2);
+  p.head_dim = kp.size(3);
+  p.elem_bytes = elem_bytes_of(kp);
+  p.max_batch = t[2].size(0);
+  p.max_blocks = t[2].size(1);
+  TORCH_CHECK(t[3].numel() == p.max_batch && t[4].numel() == p.max_batch, "row metadata size mismatch");
+  TORCH_CHECK(t[5].numel() == p.num_pages, "free_pages must hold num_pages entries");
+  TORCH_CHECK(t[6].numel() == BARQ_KV_CTRL_WORDS, "ctrl must hold BARQ_KV_CTRL_WORDS entries");
+  return p;
+}
+
+void check_states(const barq_kv_pool& p, const at::Tensor& pages, const at::Tensor& k,
+                  const at::Tensor& v) {
+  TORCH_CHECK(k.is_cuda() && v.is_cuda() && k.get_device() == pages.get_device(),
+              "key_states and value_states must stay on the cache device");
+  TORCH_CHECK(k.dim() == 4 && v.sizes() == k.sizes(), "key_states and value_states must have identical shapes");
+  TORCH_CHECK(k.scalar_type() == pages.scalar_type() && v.scalar_type() == pages.scalar_type(),
+              "key_states and value_states must stay in the cache dtype");
+  TORCH_CHECK(k.size(1) == p.kv_heads && k.size(3) == p.head_dim, "key_states kv_heads/head_dim mismatch");
+  TORCH_CHECK(k.stride(3) == 1 && v.stride(3) == 1, "head_dim of the states must be contiguous");
+  TORCH_CHECK(k.strides() == v.strides(), "key_states and value_states must share strides");
+}
+
+void check_out(const barq_kv_pool& p, const at::Tensor& pages, const at::Tensor& ko,
+               const at::Tensor& vo, int64_t batch, int64_t seq_out) {
+  TORCH_CHECK(ko.is_cuda() && vo.is_cuda() && ko.get_device() == pages.get_device(),
+              "outputs must be on the cache device");
+  TORCH_CHECK(ko.dim() == 4 && vo.sizes() == ko.sizes() && ko.strides() == vo.strides(),
+              "outputs must be [batch, kv_heads, seq, head_dim] with equal strides");
+  TORCH_CHECK(ko.scalar_type() == pages.scalar_type() && vo.scalar_type() == pages.scalar_type(),
+              "outputs must have the cache dtype");
+  TORCH_CHECK(ko.size(0) >= batch && ko.size(1) == p.kv_heads && ko.size(2) >= seq_out &&
+                  ko.size(3) == p.head_dim,
+              "outputs too small for [batch, kv_heads, seq_out, head_dim]");
+  TORCH_CHECK(ko.stride(3) == 1, "head_dim of the outputs must be contiguous");
+}
+
+// Reference binding: barqtrain_cuda.paged_kv_append_ (csrc/src/bindings.cpp:43-49,74-75) with
+// the checks and messages of paged_kv_append_cuda (csrc/kernels/paged_kv_cache.cu:64-99,127).
+void paged_kv_append_(at::Tensor key_cache, at::Tensor value_cache, at::Tensor seq_lens,
+                      at::Tensor key_states, at::Tensor value_states) {
+  TORCH_CHECK(key_cache.is_cuda(), "key_cache must be a CUDA tensor");
+  TORCH_CHECK(value_cache.is_cuda(), "value_cache must be a CUDA tensor");
+  TORCH_CHECK(seq_lens.is_cuda(), "seq_lens must be a CUDA tensor");
+  TORCH_CHECK(key_states.is_cuda(), "key_states must be a CUDA tensor");
+  TORCH_CHECK(value_states.is_cuda(), "value_states must be a CUDA tensor");
+  TORCH_CHECK(key_cache.dim() == 5, "key_cache must have shape [batch, kv_heads, max_blocks, page_size, head_dim]");
+  TORCH_CHECK(value_cache.sizes() == key_cache.sizes(), "value_cache must match key_cache");
+  TORCH_CHECK(seq_lens.dim() == 1, "seq_lens must have shape [batch]");
+  TORCH_CHECK(key_states.dim() == 4, "key_states must have shape [batch, kv_heads, seq, head_dim]");
+  TORCH_CHECK(value_states.sizes() == key_states.sizes(), "value_states must match key_states");
+  TORCH_CHECK(key_cache.scalar_type() == key_states.scalar_type(), "key_cache and key_states must share dtype");
+  TORCH_CHECK(value_cache.scalar_type() == value_states.scalar_type(), "value_cache and value_states must share dtype");
+  TORCH_CHECK(key_cache.is_contiguous(), "key_cache must be contiguous");
+  TORCH_CHECK(value_cache.is_contiguous(), "value_cache must be contiguous");
+  TORCH_CHECK(key_cache.scalar_type() == value_cache.scalar_type(), "key_cache and value_cache must share dtype");
+
+  const int64_t batch = key_states.size(0);
+  const int64_t heads = key_states.size(1);
+  const int64_t tokens = key_states.size(2);
+  const int64_t head_dim = key_states.size(3);
+  const int64_t max_blocks = key_cache.size(2);
+  const int64_t page_size = key_cache.size(3);
+  const int64_t max_cache_len = max_blocks * page_size;
+  TORCH_CHECK(batch <= key_cache.size(0), "key_cache batch dimension is too small");
+  TORCH_CHECK(heads == key_cache.size(1), "key_cache kv_heads dimension does not match key_states");
+  TORCH_CHECK(head_dim == key_cache.size(4), "key_cache head_dim dimension does not match key_states");
+  TORCH_CHECK(batch <= seq_lens.size(0), "seq_lens batch dimension is too small");
+  if (batch == 0) return;
+
+  c10::DeviceGuard guard(key_cache.device());
+  at::Tensor lens32 = seq_lens.to(at::kInt).contiguous();
+  // The capacity check needs the lengths on the host, as the reference's does (:93).
+  const int64_t max_start = lens32.narrow(0, 0, batch).max().item<int32_t>();
+  TORCH_CHECK(max_start + tokens <= max_cache_len, "paged KV cache capacity exceeded: requested ",
+              max_start + tokens, " tokens, max_cache_len=", max_cache_len);
+
+  at::Tensor ks = key_states.stride(3) == 1 ? key_states : key_states.contiguous();
+  at::Tensor vs = value_states.stride(3) == 1 ? value_states : value_states.contiguous();
+  if (ks.strides() != vs.strides()) {
+    ks = ks.contiguous();
+    vs = vs.contiguous();
+  }
+  const bool same = lens32.data_ptr() == seq_lens.data_ptr();
+  const int rc = barq_kv_append_dense(key_cache.data_ptr(), value_cache.data_ptr(), lens32.data_ptr<int32_t>(),
+                                      ks.data_ptr(), vs.data_ptr(), batch, heads, tokens, head_dim,
+                                      key_cache.size(0), max_blocks, page_size, elem_bytes_of(key_cache),
+                                      ks.stride(0), ks.stride(1), ks.stride(2), current_stream(key_cache));
+  check_status(rc, "paged_kv_append_");
+  if (!same) seq_lens.narrow(0, 0, batch).add_(tokens);  // lens32 was a converted copy
+}
+
+void pool_reset_(std::vector<at::Tensor> pool, c10::optional<at::Tensor> page_order) {
+  barq_kv_pool p = pool_from(pool);
+  c10::DeviceGuard guard(pool[0].device());
+  const int32_t* order = nullptr;
+  if (page_order.has_value() && page_order->defined()) {
+    const at::Tensor& o = *page_order;
+    TORCH_CHECK(o.is_cuda() && o.scalar_type() == at::kInt && o.is_contiguous() && o.numel() == p.num_pages,
+                "page_order must be a contiguous int32 permutation of the pages on the pool's device");
+    order = o.data_ptr<int32_t>();
+  }
+  check_status(barq_kv_pool_reset(&p, order, current_stream(pool[0])), "pool_reset_");
+}
+
+void pool_append_(std::vector<at::Tensor> pool, at::Tensor key_states, at::Tensor value_states) {
+  barq_kv_pool p = pool_from(pool);
+  check_states(p, pool[0], key_states, value_states);
+  c10::DeviceGuard guard(pool[0].device());
+  const int rc = barq_kv_append(&p, key_states.data_ptr(), value_states.data_ptr(), key_states.size(0),
+                                key_states.size(2), key_states.stride(0), key_states.stride(1),
+                                key_states.stride(2), current_stream(pool[0]));
+  check_status(rc, "pool_append_");
+}
+
+void pool_gather(std::vector<at::Tensor> pool, at::Tensor key_out, at::Tensor value_out,
+                 int64_t batch, int64_t seq_out, int64_t flags) {
+  barq_kv_pool p = pool_from(pool);
+  check_out(p, pool[0], key_out, value_out, batch, seq_out);
+  c10::DeviceGuard guard(pool[0].device());
+  const int rc = barq_kv_gather(&p, key_out.data_ptr(), value_out.data_ptr(), batch, seq_out,
+                                key_out.stride(0), key_out.stride(1), key_out.stride(2), flags,
+                                current_stream(pool[0]));
+  check_status(rc, "pool_gather");
+}
+
+void pool_update_(std::vector<at::Tensor> pool, at::Tensor key_states, at::Tensor value_states,
+                  at::Tensor key_out, at::Tensor value_out, int64_t seq_out, int64_t flags) {
+  barq_kv_pool p = pool_from(pool);
+  check_states(p, pool[0], key_states, value_states);
+  const int64_t batch = key_states.size(0);
+  check_out(p, pool[0], key_out, value_out, batch, seq_out);
+  c10::DeviceGuard guard(pool[0].device());
+  const int rc = barq_kv_update(&p, key_states.data_ptr(), value_states.data_ptr(), batch,
+                                key_states.size(2), key_states.stride(0), key_states.stride(1),
+                                key_states.stride(2), key_out.data_ptr(), value_out.data_ptr(), seq_out,
+                                key_out.stride(0), key_out.stride(1), key_out.stride(2), flags,
+                                current_stream(pool[0]));
+  check_status(rc, "pool_update_");
+}
+
+void pool_crop_(std::vector<at::Tensor> pool, int64_t batch, int64_t max_length) {
+  barq_kv_pool p = pool_from(pool);
+  c10::DeviceGuard guard(pool[0].device());
+  check_status(barq_kv_crop(&p, batch, max_length, current_stream(pool[0])), "pool_crop_");
+}
+
+void pool_free_rows_(std::vector<at::Tensor> pool, at::Tensor rows) {
+  barq_kv_pool p = pool_from(pool);
+  TORCH_CHECK(rows.is_cuda() && rows.scalar_type() == at::kInt && rows.is_contiguous() &&
+                  rows.get_device() == pool[0].get_device(),
+              "rows must be contiguous int32 on the pool's device");
+  c10::DeviceGuard guard(pool[0].device());
+  check_status(barq_kv_free_rows(&p, rows.data_ptr<int32_t>(), rows.numel(), current_stream(pool[0])),
+               "pool_free_rows_");
+}
+
+void pool_copy_rows_(std::vector<at::Tensor> src, std::vector<at::Tensor> dst, at::Tensor rows) {
+  barq_kv_pool ps = pool_from(src);
+  barq_kv_pool pd = pool_from(dst);
+  TORCH_CHECK(src[0].scalar_type() == dst[0].scalar_type(), "pools must share dtype");
+  TORCH_CHECK(src[0].get_device() == dst[0].get_device(), "pools must share a device");
+  TORCH_CHECK(rows.is_cuda() && rows.scalar_type() == at::kInt && rows.is_contiguous() &&
+                  rows.get_device() == src[0].get_device(),
+              "rows must be contiguous int32 on the pool's device");
+  c10::DeviceGuard guard(src[0].device());
+  check_status(barq_kv_copy_rows(&ps, &pd, rows.data_ptr<int32_t>(), rows.numel(), current_stream(src[0])),
+               "pool_copy_rows_");
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "BarqTrain paged KV cache on MI355X (gfx950): torch bindings of libbarq_kv.so";
+  m.def("paged_kv_append_", &paged_kv_append_,
+        "Append key/value states into the dense paged KV cache (HIP)");
+  m.def("pool_reset_", &pool_reset_, "Empty a page pool", py::arg("pool"), py::arg("page_order") = py::none());
+  m.def("pool_append_", &pool_append_, "Append tokens into a page pool");
+  m.def("pool_gather", &pool_gather, "Materialise rows of a page pool as [B, H, S, D]");
+  m.def("pool_update_", &pool_update_, "Append then materialise, in one pass");
+  m.def("pool_crop_", &pool_crop_, "Clamp row lengths of a page pool");
+  m.def("pool_free_rows_", &pool_free_rows_, "Return rows' pages to the free stack");
+  m.def("pool_copy_rows_", &pool_copy_rows_, "Build rows of a fresh pool as copies of source rows");
+  m.def("version", []() { return std::string(barq_kv_version()); });
+  m.attr("CTRL_WORDS") = BARQ_KV_CTRL_WORDS;
+  m.attr("SEQ_FROM_DEVICE") = BARQ_KV_SEQ_FROM_DEVICE;
+  m.attr("SEPARATE_FINALIZE") = BARQ_KV_SEPARATE_FINALIZE;
+}

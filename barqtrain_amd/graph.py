@@ -1,0 +1,66 @@
+"""HIP-graph capture of a decode step: every layer's append + gather replayed with one launch.
+
+The captured kernels read row lengths, block tables and the free-page stack from device memory
+and size their output extent on the device (``SEQ_FROM_DEVICE``), so a graph captured once
+serves every step while the sequences grow: no host work per layer and no host sync per step.
+Inputs are static buffers the caller fills before ``replay`` (in a model, the K/V projection
+writes them); outputs are persistent ``[batch, kv_heads, capacity, head_dim]`` buffers whose
+``[:, :, :seq]`` view is returned.  The host-side length shadow of each pool is advanced by the
+same arithmetic the kernels apply.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Sequence
+
+import torch
+
+from barqtrain_amd.paged import SEPARATE_FINALIZE, SEQ_FROM_DEVICE, PagePool
+
+
+class CapturedDecodeStep:
+    def __init__(self, pools: Sequence[PagePool], batch: int, tokens: int = 1,
+                 max_length: Optional[int] = None, separate_commit: bool = False,
+                 inputs: Optional[tuple[torch.Tensor, torch.Tensor]] = None):
+        """`inputs`, if given, are stacked ``[layers, batch, kv_heads, tokens, head_dim]`` K and V
+        buffers (one copy fills every layer); otherwise one buffer per layer is allocated."""
+        if not pools or not all(p.on_gpu for p in pools):
+            raise ValueError("graph capture needs GPU page pools")
+        self.pools = list(pools)
+        self.batch = int(batch)
+        self.tokens = int(tokens)
+        self.max_length = max_length
+        p0 = self.pools[0]
+        self.capacity = p0.capacity if max_length is None else min(p0.capacity, int(max_length))
+        shape_in = (self.batch, p0.kv_heads, self.tokens, p0.head_dim)
+        shape_out = (self.batch, p0.kv_heads, self.capacity, p0.head_dim)
+        if inputs is not None:
+            kin, vin = inputs
+            if tuple(kin.shape) != (len(self.pools), *shape_in) or kin.shape != vin.shape:
+                raise ValueError("stacked inputs must be [layers, batch, kv_heads, tokens, head_dim]")
+            self.key_in = list(kin.unbind(0))
+            self.value_in = list(vin.unbind(0))
+        else:
+            self.key_in = [torch.zeros(shape_in, dtype=p.dtype, device=p.device) for p in self.pools]
+            self.value_in = [torch.zeros(shape_in, dtype=p.dtype, device=p.device) for p in self.pools]
+        self.key_out = [torch.empty(shape_out, dtype=p.dtype, device=p.device) for p in self.pools]
+        self.value_out = [torch.empty(shape_out, dtype=p.dtype, device=p.device) for p in self.pools]
+        self.flags = SEQ_FROM_DEVICE | (SEPARATE_FINALIZE if separate_commit else 0)
+        from barqtrain_amd.paged import _gpu_backend
+
+        backend = _gpu_backend()
+        self.graph = torch.cuda.CUDAGraph()
+        # Capture records the launches without running them; no pool state changes here.
+        with torch.cuda.graph(self.graph):
+            for i, pool in enumerate(self.pools):
+                backend.pool_update_(pool.tensors, self.key_in[i], self.value_in[i],
+                                     self.key_out[i], self.value_out[i], self.capacity, self.flags)
+
+    def replay(self) -> list[tuple[torch.Tensor, torch.Tensor]]:
+        """Run one captured step; returns each layer's (K, V) views ``[batch, H, seq, D]``."""
+        needs = [p.check_append(self.batch, self.tokens, self.max_length) for p in self.pools]
+        self.graph.replay()
+        for p, need in zip(self.pools, needs):
+            p._advance(self.batch, self.tokens, need)
+        seq = self.pools[0].max_len(self.batch)
+        return [(k[:, :, :seq], v[:, :, :seq]) for k, v in zip(self.key_out, self.value_out)]

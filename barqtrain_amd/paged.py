@@ -1,0 +1,437 @@
+"""One layer's page pool: pages, block table, row lengths and the free-page stack.
+
+Device layout (see include/barq_kv.h):
+
+* ``key_pages`` / ``value_pages``: ``[num_pages, page_size, kv_heads, head_dim]`` -- one token's
+  K (or V) over all heads is one contiguous run, the run HF attention produces.
+* ``block_table``: int32 ``[max_batch, max_blocks]``, page id or -1.
+* ``seq_lens`` / ``high_water``: int32 ``[max_batch]``.  Slots ``[0, high_water)`` of a row have
+  been written; a gathered slot at or past ``high_water`` is zero, which reproduces the
+  zero-initialised dense cache of the reference (python/barqtrain/kv_cache.py:66-71) and its
+  crop that keeps data (:158-164).
+* ``free_pages``: int32 stack, ``ctrl[0]`` entries free; ``ctrl``: int32 ``[64]``.
+
+The host keeps a shadow of every row's length and high-water mark and of the free-page count.
+The shadow is updated by the same arithmetic the kernels apply, so capacity and pool checks,
+``get_seq_length`` and output shapes never read the device: a decode step issues no host sync.
+
+GPU tensors (device type ``cuda`` on ROCm PyTorch) always go through the HIP kernels of
+``barqtrain_cuda`` and raise if that module is missing.  Tensors in host memory -- which the
+reference layer also accepts (kv_cache.py:107,118) -- are served by ``_HostOps``, the same
+algorithm (same page-allocation order) written with torch CPU operators.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+CTRL_WORDS = 64
+CTRL_FREE_TOP = 0
+CTRL_ERRORS = 1
+ERRBIT_POOL_EXHAUSTED = 1
+ERRBIT_CAPACITY = 2
+ERRBIT_BAD_INDEX = 4
+SEQ_FROM_DEVICE = 1
+SEPARATE_FINALIZE = 2
+
+
+class PagedKVCapacityError(ValueError, RuntimeError):
+    """A row would exceed the cache capacity.
+
+    The reference raises ``ValueError`` on its CPU path (kv_cache.py:80-83) and
+    ``RuntimeError`` on its CUDA path (paged_kv_cache.cu:94-99); this class is both.
+    """
+
+
+class PagedKVPoolExhausted(PagedKVCapacityError):
+    """The pool has fewer free pages than an append needs."""
+
+
+def _gpu_backend():
+    from barqtrain_amd import kv_cache
+
+    backend = kv_cache._get_cuda_backend()
+    if backend is None or not hasattr(backend, "pool_update_"):
+        raise RuntimeError(
+            "barqtrain: the HIP backend module barqtrain_cuda is not available; build it with "
+            "`python -m barqtrain_amd.build` (GPU tensors have no other code path)"
+        )
+    return backend
+
+
+class PagePool:
+    """Page pool of one cache layer."""
+
+    def __init__(
+        self,
+        *,
+        max_batch: int,
+        max_blocks: int,
+        page_size: int,
+        kv_heads: int,
+        head_dim: int,
+        dtype: torch.dtype,
+        device: torch.device | str,
+        num_pages: Optional[int] = None,
+        page_order: Optional[torch.Tensor] = None,
+    ):
+        self.max_batch = int(max_batch)
+        self.max_blocks = int(max_blocks)
+        self.page_size = int(page_size)
+        self.kv_heads = int(kv_heads)
+        self.head_dim = int(head_dim)
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.num_pages = int(num_pages) if num_pages is not None else self.max_batch * self.max_blocks
+        if min(self.max_batch, self.max_blocks, self.page_size, self.kv_heads, self.head_dim, self.num_pages) < 1:
+            raise ValueError("page pool dimensions must be positive")
+        if self.num_pages >= 2**31 or self.max_batch * self.max_blocks >= 2**31:
+            raise ValueError("page pool too large for int32 page ids")
+        shape = (self.num_pages, self.page_size, self.kv_heads, self.head_dim)
+        # Pages are not cleared: a slot is only ever read after it was written.
+        self.key_pages = torch.empty(shape, dtype=dtype, device=self.device)
+        self.value_pages = torch.empty(shape, dtype=dtype, device=self.device)
+        i32 = dict(dtype=torch.int32, device=self.device)
+        self.block_table = torch.empty((self.max_batch, self.max_blocks), **i32)
+        self.seq_lens = torch.empty((self.max_batch,), **i32)
+        self.high_water = torch.empty((self.max_batch,), **i32)
+        self.free_pages = torch.empty((self.num_pages,), **i32)
+        self.ctrl = torch.empty((CTRL_WORDS,), **i32)
+        self.lens = np.zeros(self.max_batch, dtype=np.int64)
+        self.hw = np.zeros(self.max_batch, dtype=np.int64)
+        self.free_count = self.num_pages
+        self.reset(page_order)
+
+    # ------------------------------------------------------------------ plumbing
+    @property
+    def on_gpu(self) -> bool:
+        return self.device.type == "cuda"
+
+    @property
+    def tensors(self) -> list[torch.Tensor]:
+        return [self.key_pages, self.value_pages, self.block_table, self.seq_lens,
+                self.high_water, self.free_pages, self.ctrl]
+
+    @property
+    def capacity(self) -> int:
+        return self.max_blocks * self.page_size
+
+    def _ops(self):
+        return _gpu_backend() if self.on_gpu else _HostOps
+
+    # ------------------------------------------------------------------ host shadow
+    def new_block_counts(self, batch: int, tokens: int) -> np.ndarray:
+        """Blocks each row [0, batch) maps for the first time when `tokens` are appended."""
+        if tokens <= 0 or batch <= 0:
+            return np.zeros(max(batch, 0), dtype=np.int64)
+        P = self.page_size
+        first = -(-self.hw[:batch] // P)
+        end = np.minimum(-(-(self.lens[:batch] + tokens) // P), self.max_blocks)
+        return np.maximum(end - first, 0)
+
+    def check_append(self, batch: int, tokens: int, max_length: Optional[int] = None) -> int:
+        """Raise if appending would pass `max_length` (default: the block capacity) or drain the
+        pool; return the number of pages the append takes."""
+        limit = self.capacity if max_length is None else int(max_length)
+        if batch > self.max_batch:
+            raise ValueError("batch size exceeds the configured paged KV cache capacity")
+        if batch > 0 and tokens > 0:
+            ends = self.lens[:batch] + tokens
+            worst = int(ends.max())
+            if worst > limit or worst > self.capacity:
+                raise PagedKVCapacityError(
+                    f"paged KV cache capacity exceeded: requested {worst}, max_cache_len={limit}"
+                )
+        need = int(self.new_block_counts(batch, tokens).sum())
+        if need > self.free_count:
+            raise PagedKVPoolExhausted(
+                f"paged KV page pool exhausted: append needs {need} pages, {self.free_count} free"
+            )
+        return need
+
+    def _advance(self, batch: int, tokens: int, need: int) -> None:
+        if batch <= 0 or tokens <= 0:
+            return
+        self.lens[:batch] += tokens
+        np.maximum(self.hw[:batch], self.lens[:batch], out=self.hw[:batch])
+        self.free_count -= need
+
+    def max_len(self, batch: int) -> int:
+        return int(self.lens[:batch].max()) if batch > 0 else 0
+
+    # ------------------------------------------------------------------ operations
+    def reset(self, page_order: Optional[torch.Tensor] = None) -> None:
+        """Free every page; row lengths and high-water marks to zero.  O(metadata)."""
+        if page_order is not None:
+            page_order = page_order.to(device=self.device, dtype=torch.int32).contiguous()
+            if page_order.numel() != self.num_pages or not torch.equal(
+                    torch.sort(page_order).values,
+                    torch.arange(self.num_pages, dtype=torch.int32, device=self.device)):
+                raise ValueError("page_order must list every page of the pool exactly once")
+        self._ops().pool_reset_(self.tensors, page_order)
+        self.lens[:] = 0
+        self.hw[:] = 0
+        self.free_count = self.num_pages
+
+    def _check_states(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        if key_states.dim() != 4 or key_states.shape != value_states.shape:
+            raise ValueError("key_states and value_states must have identical [batch, kv_heads, seq, head_dim] shapes")
+        if key_states.shape[1] != self.kv_heads or key_states.shape[3] != self.head_dim:
+            raise ValueError("key_states kv_heads/head_dim do not match the cache")
+
+    @staticmethod
+    def _compatible_pair(key_states: torch.Tensor, value_states: torch.Tensor):
+        if key_states.stride(-1) != 1 or value_states.stride(-1) != 1 or key_states.stride() != value_states.stride():
+            return key_states.contiguous(), value_states.contiguous()
+        return key_states, value_states
+
+    def append(self, key_states: torch.Tensor, value_states: torch.Tensor,
+               max_length: Optional[int] = None) -> None:
+        self._check_states(key_states, value_states)
+        batch, _, tokens, _ = key_states.shape
+        need = self.check_append(batch, tokens, max_length)
+        if batch == 0 or tokens == 0:
+            return
+        k, v = self._compatible_pair(key_states, value_states)
+        self._ops().pool_append_(self.tensors, k, v)
+        self._advance(batch, tokens, need)
+
+    def _new_out(self, batch: int, seq: int) -> tuple[torch.Tensor, torch.Tensor]:
+        shape = (batch, self.kv_heads, seq, self.head_dim)
+        return (torch.empty(shape, dtype=self.dtype, device=self.device),
+                torch.empty(shape, dtype=self.dtype, device=self.device))
+
+    def gather(self, batch: int, seq_out: Optional[int] = None,
+               out: Optional[tuple[torch.Tensor, torch.Tensor]] = None,
+               flags: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+        """Materialise rows [0, batch) as contiguous ``[batch, kv_heads, seq_out, head_dim]``
+        (default seq_out: the longest row)."""
+        seq = self.max_len(batch) if seq_out is None else int(seq_out)
+        if seq > self.capacity:
+            raise ValueError("seq_out exceeds the cache capacity")
+        ko, vo = out if out is not None else self._new_out(batch, seq)
+        if batch > 0 and seq > 0:
+            self._ops().pool_gather(self.tensors, ko, vo, batch, seq, flags)
+        return ko, vo
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor,
+               max_length: Optional[int] = None, out=None, seq_out: Optional[int] = None,
+               flags: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+        """Append, then materialise rows [0, batch) up to the longest row, in one pass."""
+        self._check_states(key_states, value_states)
+        batch, _, tokens, _ = key_states.shape
+        need = self.check_append(batch, tokens, max_length)
+        if tokens == 0:
+            return self.gather(batch, seq_out, out, flags)
+        ends = self.lens[:batch] + tokens
+        seq = int(ends.max()) if seq_out is None else int(seq_out)
+        ko, vo = out if out is not None else self._new_out(batch, seq)
+        k, v = self._compatible_pair(key_states, value_states)
+        self._ops().pool_update_(self.tensors, k, v, ko, vo, seq, flags)
+        self._advance(batch, tokens, need)
+        return ko, vo
+
+    def crop(self, batch: int, max_length: int) -> None:
+        """seq_lens[:batch] = min(seq_lens, max_length); data and pages are kept."""
+        max_length = max(int(max_length), 0)
+        if batch <= 0:
+            return
+        self._ops().pool_crop_(self.tensors, batch, max_length)
+        np.minimum(self.lens[:batch], max_length, out=self.lens[:batch])
+
+    def free_rows(self, rows: Sequence[int]) -> None:
+        """Return every page of `rows` to the pool; their lengths become 0."""
+        rows = [int(r) for r in rows]
+        if len(set(rows)) != len(rows):
+            raise ValueError("free_rows: rows must be distinct")
+        if any(r < 0 or r >= self.max_batch for r in rows):
+            raise IndexError("free_rows: row out of range")
+        if not rows:
+            return
+        idx = torch.tensor(rows, dtype=torch.int32, device=self.device)
+        self._ops().pool_free_rows_(self.tensors, idx)
+        r = np.asarray(rows)
+        self.free_count += int(np.minimum(-(-self.hw[r] // self.page_size), self.max_blocks).sum())
+        self.lens[r] = 0
+        self.hw[r] = 0
+
+    def copy_rows(self, src_rows: Sequence[int], num_pages: Optional[int] = None) -> "PagePool":
+        """A new pool whose row i copies row src_rows[i] of this one (repeats allowed)."""
+        src_rows = [int(r) for r in src_rows]
+        if any(r < 0 or r >= self.max_batch for r in src_rows):
+            raise IndexError("copy_rows: row out of range")
+        n = len(src_rows)
+        r = np.asarray(src_rows, dtype=np.int64)
+        need = int(np.minimum(-(-self.hw[r] // self.page_size), self.max_blocks).sum()) if n else 0
+        if num_pages is None:
+            scaled = math.ceil(self.num_pages * max(n, 1) / self.max_batch)
+            num_pages = max(need, scaled, 1)
+        if need > num_pages:
+            raise PagedKVPoolExhausted(f"copy_rows needs {need} pages, pool of {num_pages}")
+        dst = PagePool(max_batch=max(n, 1), max_blocks=self.max_blocks, page_size=self.page_size,
+                       kv_heads=self.kv_heads, head_dim=self.head_dim, dtype=self.dtype,
+                       device=self.device, num_pages=num_pages)
+        if n:
+            idx = torch.tensor(src_rows, dtype=torch.int32, device=self.device)
+            self._ops().pool_copy_rows_(self.tensors, dst.tensors, idx)
+            dst.lens[:n] = self.lens[r]
+            dst.hw[:n] = self.hw[r]
+            dst.free_count = num_pages - need
+        return dst
+
+    def errors(self) -> int:
+        """Sticky device error bits (reads the device: a synchronisation point)."""
+        return int(self.ctrl[CTRL_ERRORS].item())
+
+    def to(self, device) -> "PagePool":
+        """Move every tensor of the pool (offload / prefetch)."""
+        device = torch.device(device)
+        for name in ("key_pages", "value_pages", "block_table", "seq_lens", "high_water", "free_pages", "ctrl"):
+            setattr(self, name, getattr(self, name).to(device, non_blocking=True))
+        self.device = device
+        return self
+
+
+class _HostOps:
+    """The pool operations for tensors in host memory, in torch CPU operators.
+
+    Same semantics and page-allocation order as the HIP kernels (barq_kv.hip): new blocks are
+    ranked in (row, block) order and rank k takes ``free_pages[top - 1 - k]``.
+    """
+
+    @staticmethod
+    def _geometry(t):
+        kp, _, bt = t[0], t[1], t[2]
+        return kp.shape[1], bt.shape[1]
+
+    @staticmethod
+    def pool_reset_(t, page_order=None):
+        kp, vp, bt, lens, hw, free, ctrl = t
+        n = kp.shape[0]
+        order = page_order if page_order is not None else torch.arange(n, dtype=torch.int32)
+        free.copy_(order.flip(0))
+        bt.fill_(-1)
+        lens.zero_()
+        hw.zero_()
+        ctrl.zero_()
+        ctrl[CTRL_FREE_TOP] = n
+
+    @staticmethod
+    def _map_new_blocks(t, batch, tokens):
+        kp, vp, bt, lens, hw, free, ctrl = t
+        P, MB = _HostOps._geometry(t)
+        top = int(ctrl[CTRL_FREE_TOP])
+        used = 0
+        err = 0
+        for b in range(batch):
+            ln, h = int(lens[b]), int(hw[b])
+            first = -(-h // P)
+            full_end = -(-(ln + tokens) // P)
+            if full_end > MB:
+                err |= ERRBIT_CAPACITY
+            end = min(full_end, MB)
+            for j in range(first, end):
+                idx = top - 1 - used
+                used += 1
+                page = int(free[idx]) if idx >= 0 else -1
+                if page < 0:
+                    err |= ERRBIT_POOL_EXHAUSTED
+                bt[b, j] = page
+        ctrl[CTRL_FREE_TOP] = max(0, top - used)
+        if err:
+            ctrl[CTRL_ERRORS] |= err
+
+    @staticmethod
+    def _scatter(t, key_states, value_states, old_lens):
+        kp, vp, bt, lens, hw, free, ctrl = t
+        P, MB = _HostOps._geometry(t)
+        batch, _, tokens, _ = key_states.shape
+        pos = old_lens[:, None] + torch.arange(tokens, dtype=torch.int64)[None, :]
+        blk = pos // P
+        ok = blk < MB
+        rows = torch.arange(batch)[:, None].expand_as(pos)
+        page = torch.full_like(pos, -1)
+        page[ok] = bt[rows[ok], blk[ok]].long()
+        ok &= page >= 0
+        off = pos % P
+        ks = key_states.permute(0, 2, 1, 3)  # [B, T, H, D]
+        vs = value_states.permute(0, 2, 1, 3)
+        kp[page[ok], off[ok]] = ks[ok]
+        vp[page[ok], off[ok]] = vs[ok]
+
+    @staticmethod
+    def _commit(t, batch, tokens):
+        kp, vp, bt, lens, hw, free, ctrl = t
+        lens[:batch] += tokens
+        torch.maximum(hw[:batch], lens[:batch], out=hw[:batch])
+
+    @staticmethod
+    def pool_append_(t, key_states, value_states):
+        batch, _, tokens, _ = key_states.shape
+        old = t[3][:batch].long().clone()
+        _HostOps._map_new_blocks(t, batch, tokens)
+        _HostOps._scatter(t, key_states, value_states, old)
+        _HostOps._commit(t, batch, tokens)
+
+    @staticmethod
+    def pool_gather(t, key_out, value_out, batch, seq_out, flags=0):
+        kp, vp, bt, lens, hw, free, ctrl = t
+        P, MB = _HostOps._geometry(t)
+        if flags & SEQ_FROM_DEVICE:
+            seq_out = min(seq_out, int(lens[:batch].max())) if batch else 0
+        s = torch.arange(seq_out, dtype=torch.int64)
+        blk = torch.clamp(s // P, max=MB - 1)
+        page = bt[:batch].long()[:, blk]  # [B, S]
+        valid = (s[None, :] < hw[:batch].long()[:, None]) & (page >= 0) & (s[None, :] < MB * P)
+        off = (s % P)[None, :].expand_as(page)
+        for pages, out in ((kp, key_out), (vp, value_out)):
+            vals = pages[page.clamp(min=0), off]  # [B, S, H, D]
+            vals[~valid] = 0
+            out[:batch, :, :seq_out, :] = vals.permute(0, 2, 1, 3)
+
+    @staticmethod
+    def pool_update_(t, key_states, value_states, key_out, value_out, seq_out, flags=0):
+        _HostOps.pool_append_(t, key_states, value_states)
+        _HostOps.pool_gather(t, key_out, value_out, key_states.shape[0], seq_out, flags)
+
+    @staticmethod
+    def pool_crop_(t, batch, max_length):
+        t[3][:batch].clamp_(max=max_length)
+
+    @staticmethod
+    def pool_free_rows_(t, rows):
+        kp, vp, bt, lens, hw, free, ctrl = t
+        P, MB = _HostOps._geometry(t)
+        top = int(ctrl[CTRL_FREE_TOP])
+        for r in rows.tolist():
+            n = min(-(-int(hw[r]) // P), MB)
+            free[top:top + n] = bt[r, :n]
+            top += n
+            bt[r, :n] = -1
+            lens[r] = 0
+            hw[r] = 0
+        ctrl[CTRL_FREE_TOP] = top
+
+    @staticmethod
+    def pool_copy_rows_(src, dst, rows):
+        skp, svp, sbt, slens, shw, _, _ = src
+        dkp, dvp, dbt, dlens, dhw, dfree, dctrl = dst
+        P, MB = _HostOps._geometry(src)
+        top = int(dctrl[CTRL_FREE_TOP])
+        used = 0
+        for i, r in enumerate(rows.tolist()):
+            n = min(-(-int(shw[r]) // P), MB)
+            for j in range(n):
+                page = int(dfree[top - 1 - used])
+                used += 1
+                sp = int(sbt[r, j])
+                dkp[page] = skp[sp]
+                dvp[page] = svp[sp]
+                dbt[i, j] = page
+            dlens[i] = slens[r]
+            dhw[i] = shw[r]
+        dctrl[CTRL_FREE_TOP] = top - used

@@ -1,0 +1,239 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged KV-cache hot path on one MI355X.
+
+Workload (default, configuration 2 -- the Llama-3-8B KV shape): 32 layers, batch 16, 8 KV heads x
+128, bf16, page 16.  Every row is prefilled with 512 tokens (untimed), then each timed step is
+one decode step of the cache: for every layer, append 1 token per row and materialise the whole
+contiguous [B, H, seq, D] K and V (ctx 513 -> 768 over the 256 steps).  Inputs are N(0, 1) in
+fp32 rounded to bf16 from a seeded generator and already resident in HBM.
+
+A step runs as one replay of a captured HIP graph of the 32 fused append+gather launches
+(--mode graph, default), or as 32 host-launched layer updates (--mode eager, the per-call path
+HF attention takes).  Throughput counts algorithmic bytes per step, summed over layers:
+append 2*B*T*tb (read new, write page) + gather sum_b(ctx_b)*tb (read) + B*S_max*tb (write),
+tb = 2*H*D*esize; metadata is not counted.
+
+Prints ONE JSON line.  The CPU baseline (numpy oracle of the reference path, one thread) runs on a
+bounded sample: one layer for the whole 256-step decode, reported per full step (x layers).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "paged KV append+gather GB/s (% HBM peak); µs per decode-step cache update"
+
+CONFIGS = {
+    1: dict(name="C1 tiny plumbing", layers=2, batch=1, heads=4, dim=64, page=16, dtype="float32",
+            prefill=32, decode=128, seed=1001),
+    2: dict(name="C2 Llama-3-8B KV shape", layers=32, batch=16, heads=8, dim=128, page=16, dtype="bfloat16",
+            prefill=512, decode=256, seed=1002),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None, help="timed decode steps (default: the config's)")
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--mode", choices=["graph", "eager"], default="graph")
+    ap.add_argument("--separate-commit", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--repeat", type=int, default=3, help="timed repetitions; the best is reported")
+    return ap.parse_args()
+
+
+def step_bytes(cfg, ctx_after, tokens=1):
+    """Algorithmic bytes of one step over all layers when every row ends at ctx_after."""
+    import torch
+
+    esize = torch.empty(0, dtype=getattr(torch, cfg["dtype"])).element_size()
+    tb = 2 * cfg["heads"] * cfg["dim"] * esize
+    B = cfg["batch"]
+    append = 2 * B * tokens * tb
+    gather = B * ctx_after * tb + B * ctx_after * tb
+    return cfg["layers"] * (append + gather)
+
+
+def cpu_baseline(cfg, k_dec, v_dec, k_pre, v_pre, steps):
+    """The numpy oracle (reference CPU path + contiguous materialisation) on one layer."""
+    import numpy as np
+
+    from kvgen import to_bits
+    from oracle.kv_oracle import DenseLayerOracle
+
+    cap = cfg["prefill"] + steps
+    oracle = DenseLayerOracle(cfg["batch"], cap, cfg["page"])
+    oracle.append(to_bits(k_pre), to_bits(v_pre))
+    kd = to_bits(k_dec)  # [steps, B, H, 1, D]
+    vd = to_bits(v_dec)
+    t0 = time.perf_counter()
+    for s in range(steps):
+        oracle.update(kd[s], vd[s])
+    dt = time.perf_counter() - t0
+    nbytes = sum(step_bytes(cfg, cfg["prefill"] + s + 1) for s in range(steps)) / cfg["layers"]
+    per_layer_step_s = dt / steps
+    return {
+        "value": round(nbytes / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"layer 0 only, all {steps} decode steps (append 1 token x {cfg['batch']} rows + "
+                  f"materialised gather), numpy restatement of kv_cache.py _python_append + current_tensors; "
+                  f"per full step = x{cfg['layers']} layers",
+        "ms_per_step": round(per_layer_step_s * cfg["layers"] * 1e3, 3),
+        "seconds": round(dt, 2),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (the cache path shards "
+                                   "by sequence/head/layer with no collective; see DESIGN.md)"}))
+        sys.exit(2)
+    import torch
+
+    from barqtrain_amd import _ffi
+    from barqtrain_amd.graph import CapturedDecodeStep
+    from barqtrain_amd.paged import PagePool
+
+    backend = _ffi.load_cuda_backend()
+    if backend is None:
+        raise SystemExit("barqtrain_cuda HIP backend not built (python -m barqtrain_amd.build)")
+    torch.cuda.set_device(0)
+    cfg = CONFIGS[args.config]
+    steps = args.steps if args.steps is not None else cfg["decode"]
+    L, B, H, D, P = cfg["layers"], cfg["batch"], cfg["heads"], cfg["dim"], cfg["page"]
+    dtype = getattr(torch, cfg["dtype"])
+    prefill = cfg["prefill"]
+    cap = prefill + max(steps, args.warmup)
+    dev = torch.device("cuda", 0)
+
+    gen = torch.Generator(device=dev).manual_seed(cfg["seed"])
+
+    def normal(shape):
+        return torch.randn(shape, generator=gen, device=dev, dtype=torch.float32).to(dtype)
+
+    # HF physical layout [B, T, H, D], viewed as [B, H, T, D]
+    k_pre = [normal((B, prefill, H, D)).transpose(1, 2) for _ in range(L)]
+    v_pre = [normal((B, prefill, H, D)).transpose(1, 2) for _ in range(L)]
+    n_in = max(steps, args.warmup)
+    k_dec = normal((n_in, L, B, H, 1, D))
+    v_dec = normal((n_in, L, B, H, 1, D))
+
+    pools = [PagePool(max_batch=B, max_blocks=math.ceil(cap / P), page_size=P, kv_heads=H, head_dim=D,
+                      dtype=dtype, device=dev) for _ in range(L)]
+
+    def prefill_all():
+        for l, pool in enumerate(pools):
+            pool.reset()
+            pool.update(k_pre[l], v_pre[l])
+
+    graph = None
+    if args.mode == "graph":
+        kin = torch.empty((L, B, H, 1, D), dtype=dtype, device=dev)
+        vin = torch.empty_like(kin)
+        graph = CapturedDecodeStep(pools, B, 1, separate_commit=args.separate_commit, inputs=(kin, vin))
+
+        def run_step(s):
+            kin.copy_(k_dec[s])
+            vin.copy_(v_dec[s])
+            graph.replay()
+    else:
+        flags = 2 if args.separate_commit else 0
+
+        def run_step(s):
+            for l, pool in enumerate(pools):
+                pool.update(k_dec[s, l], v_dec[s, l], flags=flags)
+
+    # warmup, then a fresh prefill so the timed steps are exactly ctx 513 -> 512 + steps
+    prefill_all()
+    for s in range(args.warmup):
+        run_step(s)
+    torch.cuda.synchronize()
+
+    best = None
+    for _ in range(max(1, args.repeat)):
+        prefill_all()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for s in range(steps):
+            run_step(s)
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end)
+        best = ms if best is None else min(best, ms)
+    errors = [p.errors() for p in pools]
+    if any(errors):
+        raise SystemExit(f"device error bits set: {errors}")
+
+    total_bytes = sum(step_bytes(cfg, prefill + s + 1) for s in range(steps))
+    gbs = total_bytes / (best / 1e3) / 1e9
+    launches = steps * L
+    avg_launch_us = best * 1e3 / launches
+    bytes_per_launch = total_bytes / launches
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"traffic_config{args.config}.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(best / steps, 4),
+        "us_per_step": round(best * 1e3 / steps, 2),
+        "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg["dtype"].replace("bfloat16", "bf16").replace("float32", "f32"),
+        "data": "synthetic: N(0,1) fp32 rounded to the cache dtype, seeded; inputs resident in HBM",
+        "config": {
+            "workload": f"{cfg['name']}: {L} layers, batch {B}, {H} KV heads x {D}, {cfg['dtype']}, page {P}; "
+                        f"prefill {prefill} (untimed), then {steps} decode steps of 1-token append + full "
+                        f"contiguous gather per layer",
+            "mode": args.mode + (" + separate commit" if args.separate_commit else ""),
+            "layers": L, "batch": B, "kv_heads": H, "head_dim": D, "page_size": P,
+            "prefill": prefill, "decode_steps": steps, "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "stream_kernel<16> (fused append + gather, one launch per layer)",
+            "achieved": round(bytes_per_launch / (avg_launch_us * 1e-6) / 1e9, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(bytes_per_launch / (avg_launch_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "bytes_per_launch": int(bytes_per_launch),
+            "avg_launch_us": round(avg_launch_us, 3),
+        },
+    }
+    if not args.no_cpu_baseline:
+        k0 = k_dec[:steps, 0]
+        v0 = v_dec[:steps, 0]
+        result["cpu_baseline"] = cpu_baseline(cfg, k0, v0, k_pre[0], v_pre[0], steps)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,170 @@
+/*
+ * barq_kv.h -- C ABI of the MI355X (gfx950) paged KV-cache library (libbarq_kv.so).
+ *
+ * Every entry point takes plain device pointers and sizes, enqueues its work on
+ * the HIP stream it is given (NULL = the null stream), allocates nothing, never
+ * synchronises with the host, and returns a barq_kv_status code.  Element data is
+ * moved as raw bits (elem_bytes of 1, 2, 4 or 8), so bf16 / fp16 / fp32 / fp64
+ * caches, NaN payloads included, come back bit-identical.
+ *
+ * Reference interfaces replaced (files under the BarqTrain tree):
+ *   barq_kv_append_dense  <- paged_kv_append_cuda, csrc/kernels/paged_kv_cache.cu:58-128,
+ *                            bound as barqtrain_cuda.paged_kv_append_ at
+ *                            csrc/src/bindings.cpp:43-49,74-75
+ *   barq_kv_append        <- BarqPagedKVCacheLayer.append / _python_append,
+ *                            python/barqtrain/kv_cache.py:75-118 (page-pool layout)
+ *   barq_kv_gather        <- BarqPagedKVCacheLayer._flatten_pages + current_tensors,
+ *                            python/barqtrain/kv_cache.py:120-133 (materialised)
+ *   barq_kv_update        <- BarqPagedKVCacheLayer.update, python/barqtrain/kv_cache.py:135-142
+ *   barq_kv_crop          <- BarqPagedKVCacheLayer.crop, python/barqtrain/kv_cache.py:158-164
+ *   barq_kv_pool_reset    <- BarqPagedKVCacheLayer.lazy_initialization / reset,
+ *                            python/barqtrain/kv_cache.py:53-73,188-194
+ *   barq_kv_copy_rows     <- batch_repeat_interleave / batch_select_indices / reorder_cache,
+ *                            python/barqtrain/kv_cache.py:166-186
+ *   barq_kv_free_rows     <- no reference counterpart: returns a finished sequence's pages
+ *                            to the pool (the page allocator the reference only planned,
+ *                            IMPLEMENTATION_PLAN.md:90-92).
+ *
+ * Calls that name the same pool must be ordered on one stream; calls on different
+ * pools are independent.
+ */
+#ifndef BARQ_KV_H
+#define BARQ_KV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes. */
+#define BARQ_KV_OK 0
+#define BARQ_KV_ERR_INVALID 1 /* a pointer, size, stride or alignment the kernels cannot take */
+#define BARQ_KV_ERR_LAUNCH 2  /* the HIP runtime refused a launch */
+
+/* Words of barq_kv_pool.ctrl (the arrival counter sits on its own 128-byte line). */
+#define BARQ_KV_CTRL_FREE_TOP 0 /* number of entries of free_pages that are free pages */
+#define BARQ_KV_CTRL_ERRORS 1   /* sticky error bits below, set by kernels, cleared by reset */
+#define BARQ_KV_CTRL_ARRIVED 32 /* tile arrival counter of the running launch; 0 between launches */
+#define BARQ_KV_CTRL_WORDS 64
+
+/* Sticky error bits in ctrl[BARQ_KV_CTRL_ERRORS]. */
+#define BARQ_KV_ERRBIT_POOL_EXHAUSTED 1 /* a new block found no free page; its tokens were dropped */
+#define BARQ_KV_ERRBIT_CAPACITY 2       /* a position fell at or beyond max_blocks * page_size */
+#define BARQ_KV_ERRBIT_BAD_INDEX 4      /* a row index outside [0, max_batch) was given */
+
+/* Flags of barq_kv_gather / barq_kv_update. */
+#define BARQ_KV_SEQ_FROM_DEVICE 1 /* seq_out is the output's capacity; the positions written are
+                                     [0, max over rows of seq_lens (after the append)), read on the
+                                     device, so one launch (or a captured graph) serves every step */
+#define BARQ_KV_SEPARATE_FINALIZE 2 /* update the pool's row metadata in a second, one-workgroup
+                                       launch instead of in the last tile of the copy launch */
+
+/*
+ * One layer's page pool.  All pointers are device pointers.
+ *   key_pages / value_pages : [num_pages, page_size, kv_heads, head_dim] elements of elem_bytes
+ *   block_table             : int32 [max_batch, max_blocks], page id of (row, block) or -1
+ *   seq_lens                : int32 [max_batch], tokens visible in each row
+ *   high_water              : int32 [max_batch], slots [0, high_water) of the row have been written
+ *   free_pages              : int32 [num_pages], a stack; entries [0, ctrl[FREE_TOP]) are free
+ *   ctrl                    : int32 [BARQ_KV_CTRL_WORDS], 256-byte aligned
+ * Invariant kept by every entry point: block b of row r holds a page iff b * page_size < high_water[r].
+ */
+typedef struct barq_kv_pool {
+  void* key_pages;
+  void* value_pages;
+  int32_t* block_table;
+  int32_t* seq_lens;
+  int32_t* high_water;
+  int32_t* free_pages;
+  int32_t* ctrl;
+  int64_t num_pages;
+  int64_t max_batch;
+  int64_t max_blocks;
+  int64_t page_size;
+  int64_t kv_heads;
+  int64_t head_dim;
+  int64_t elem_bytes;
+} barq_kv_pool;
+
+/* Library version string. */
+const char* barq_kv_version(void);
+
+/* Human-readable text of a return code. */
+const char* barq_kv_status_string(int status);
+
+/*
+ * Dense drop-in for the reference kernel: key_cache / value_cache are contiguous
+ * [cache_batch, kv_heads, max_blocks, page_size, head_dim]; key_states / value_states are
+ * [batch, kv_heads, tokens, head_dim] with element strides (stride_b, stride_h, stride_t) and a
+ * contiguous last dimension.  Token t of row b lands at slot seq_lens[b] + t; slots whose block
+ * is >= max_blocks are skipped.  Afterwards seq_lens[0, batch) += tokens.
+ * The capacity check of the reference (paged_kv_cache.cu:92-99) is the caller's, on its own
+ * copy of the lengths.
+ */
+int barq_kv_append_dense(void* key_cache, void* value_cache, int32_t* seq_lens,
+                         const void* key_states, const void* value_states, int64_t batch,
+                         int64_t kv_heads, int64_t tokens, int64_t head_dim, int64_t cache_batch,
+                         int64_t max_blocks, int64_t page_size, int64_t elem_bytes,
+                         int64_t stride_b, int64_t stride_h, int64_t stride_t, void* stream);
+
+/*
+ * Empty the pool: every page free, every block unmapped, seq_lens = high_water = 0, errors
+ * cleared.  page_order (device int32 [num_pages], a permutation, or NULL for 0, 1, 2, ...)
+ * is the order in which later appends take pages.
+ */
+int barq_kv_pool_reset(const barq_kv_pool* pool, const int32_t* page_order, void* stream);
+
+/*
+ * Append tokens to rows [0, batch): token t of row b lands at slot seq_lens[b] + t.  Blocks
+ * that become used take pages from the free stack in row order.  Afterwards
+ * seq_lens[b] += tokens and high_water[b] = max(high_water[b], seq_lens[b]).
+ * key_states / value_states: [batch, kv_heads, tokens, head_dim], element strides
+ * (stride_b, stride_h, stride_t), contiguous last dimension.
+ */
+int barq_kv_append(const barq_kv_pool* pool, const void* key_states, const void* value_states,
+                   int64_t batch, int64_t tokens, int64_t stride_b, int64_t stride_h,
+                   int64_t stride_t, void* stream);
+
+/*
+ * Materialise rows [0, batch) into key_out / value_out, [batch, kv_heads, seq, head_dim] with
+ * element strides (out_stride_b, out_stride_h, out_stride_s) and a contiguous last dimension.
+ * Slot s of row b is the value last written there when s < high_water[b], else zero.  Writes
+ * positions [0, seq_out), or with BARQ_KV_SEQ_FROM_DEVICE [0, max_b seq_lens[b]) within a
+ * buffer of capacity seq_out.
+ */
+int barq_kv_gather(const barq_kv_pool* pool, void* key_out, void* value_out, int64_t batch,
+                   int64_t seq_out, int64_t out_stride_b, int64_t out_stride_h,
+                   int64_t out_stride_s, int64_t flags, void* stream);
+
+/* barq_kv_append followed by barq_kv_gather, in one pass over the pool. */
+int barq_kv_update(const barq_kv_pool* pool, const void* key_states, const void* value_states,
+                   int64_t batch, int64_t tokens, int64_t stride_b, int64_t stride_h,
+                   int64_t stride_t, void* key_out, void* value_out, int64_t seq_out,
+                   int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_s,
+                   int64_t flags, void* stream);
+
+/* seq_lens[b] = min(seq_lens[b], max_length) for rows [0, batch).  Page data is kept. */
+int barq_kv_crop(const barq_kv_pool* pool, int64_t batch, int64_t max_length, void* stream);
+
+/*
+ * Return every page of the listed rows (device int32 [num_rows], distinct) to the free stack
+ * and set their seq_lens and high_water to 0.
+ */
+int barq_kv_free_rows(const barq_kv_pool* pool, const int32_t* rows, int64_t num_rows,
+                      void* stream);
+
+/*
+ * Row i of dst, for i in [0, num_rows), becomes a copy of row src_rows[i] of src (device int32
+ * [num_rows]; repeats allowed): lengths, high-water mark and the contents of its pages, which
+ * are taken from dst's free stack.  dst must be empty (just reset), have the geometry of src,
+ * num_rows <= dst->max_batch, and enough free pages.
+ */
+int barq_kv_copy_rows(const barq_kv_pool* src, const barq_kv_pool* dst, const int32_t* src_rows,
+                      int64_t num_rows, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BARQ_KV_H */

@@ -1,0 +1,117 @@
+"""A page pool driven only through the C ABI (ctypes over libbarq_kv.so), for the GPU tests."""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import numpy as np
+import torch
+
+from barqtrain_amd import _capi
+
+CTRL_WORDS = 64
+SEQ_FROM_DEVICE = 1
+SEPARATE_FINALIZE = 2
+
+
+class CPool:
+    def __init__(self, *, max_batch, max_blocks, page_size, heads, dim, dtype,
+                 num_pages: Optional[int] = None, order: Optional[torch.Tensor] = None,
+                 device="cuda"):
+        self.lib = _capi.load_library()
+        self.max_batch, self.max_blocks, self.page_size = max_batch, max_blocks, page_size
+        self.heads, self.dim, self.dtype = heads, dim, dtype
+        self.num_pages = num_pages or max_batch * max_blocks
+        shape = (self.num_pages, page_size, heads, dim)
+        self.kp = torch.empty(shape, dtype=dtype, device=device)
+        self.vp = torch.empty(shape, dtype=dtype, device=device)
+        i32 = dict(dtype=torch.int32, device=device)
+        self.bt = torch.empty((max_batch, max_blocks), **i32)
+        self.lens = torch.empty((max_batch,), **i32)
+        self.hw = torch.empty((max_batch,), **i32)
+        self.free = torch.empty((self.num_pages,), **i32)
+        self.ctrl = torch.empty((CTRL_WORDS,), **i32)
+        elem = torch.empty(0, dtype=dtype).element_size()
+        self.s = _capi.BarqKVPool(self.kp.data_ptr(), self.vp.data_ptr(), self.bt.data_ptr(),
+                                  self.lens.data_ptr(), self.hw.data_ptr(), self.free.data_ptr(),
+                                  self.ctrl.data_ptr(), self.num_pages, max_batch, max_blocks,
+                                  page_size, heads, dim, elem)
+        self.reset(order)
+
+    @property
+    def ref(self):
+        return ctypes.byref(self.s)
+
+    def _stream(self):
+        return _capi.current_stream()
+
+    def reset(self, order=None):
+        self._order = None if order is None else order.to(device=self.kp.device, dtype=torch.int32).contiguous()
+        ptr = self._order.data_ptr() if self._order is not None else None
+        _capi.check(self.lib.barq_kv_pool_reset(self.ref, ptr, self._stream()))
+
+    def append(self, k, v):
+        _capi.check(self.lib.barq_kv_append(self.ref, k.data_ptr(), v.data_ptr(), k.shape[0], k.shape[2],
+                                            k.stride(0), k.stride(1), k.stride(2), self._stream()))
+
+    def gather(self, batch, seq, flags=0, out=None):
+        ko, vo = out or self.new_out(batch, seq)
+        _capi.check(self.lib.barq_kv_gather(self.ref, ko.data_ptr(), vo.data_ptr(), batch, seq,
+                                            ko.stride(0), ko.stride(1), ko.stride(2), flags, self._stream()))
+        return ko, vo
+
+    def update(self, k, v, seq, flags=0, out=None):
+        ko, vo = out or self.new_out(k.shape[0], seq)
+        _capi.check(self.lib.barq_kv_update(self.ref, k.data_ptr(), v.data_ptr(), k.shape[0], k.shape[2],
+                                            k.stride(0), k.stride(1), k.stride(2), ko.data_ptr(), vo.data_ptr(),
+                                            seq, ko.stride(0), ko.stride(1), ko.stride(2), flags, self._stream()))
+        return ko, vo
+
+    def crop(self, batch, max_length):
+        _capi.check(self.lib.barq_kv_crop(self.ref, batch, max_length, self._stream()))
+
+    def free_rows(self, rows):
+        idx = torch.tensor(rows, dtype=torch.int32, device=self.kp.device)
+        _capi.check(self.lib.barq_kv_free_rows(self.ref, idx.data_ptr(), len(rows), self._stream()))
+        torch.cuda.current_stream().synchronize()
+
+    def copy_rows_into(self, dst: "CPool", rows):
+        idx = torch.tensor(rows, dtype=torch.int32, device=self.kp.device)
+        _capi.check(self.lib.barq_kv_copy_rows(self.ref, dst.ref, idx.data_ptr(), len(rows), self._stream()))
+        torch.cuda.current_stream().synchronize()
+
+    def new_out(self, batch, seq):
+        shape = (batch, self.heads, seq, self.dim)
+        return (torch.empty(shape, dtype=self.dtype, device=self.kp.device),
+                torch.empty(shape, dtype=self.dtype, device=self.kp.device))
+
+    def errors(self) -> int:
+        return int(self.ctrl[1].item())
+
+    def free_top(self) -> int:
+        return int(self.ctrl[0].item())
+
+    def check_invariants(self):
+        """Every block below the high-water mark has a distinct page; no free page is mapped."""
+        P = self.page_size
+        bt = self.bt.cpu().numpy()
+        hw = self.hw.cpu().numpy()
+        top = self.free_top()
+        free = set(self.free.cpu().numpy()[:top].tolist())
+        mapped = []
+        for r in range(self.max_batch):
+            n = -(-int(hw[r]) // P)
+            assert (bt[r, :n] >= 0).all(), (r, bt[r, :n])
+            assert (bt[r, n:] == -1).all(), r
+            mapped += bt[r, :n].tolist()
+        assert len(mapped) == len(set(mapped)), "a page is mapped twice"
+        assert not (free & set(mapped)), "a mapped page is on the free stack"
+        assert len(free) + len(mapped) == self.num_pages
+        assert self.ctrl[32].item() == 0, "arrival counter not reset"
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    from kvgen import to_bits
+
+    return to_bits(t)

@@ -1,0 +1,105 @@
+"""The native library without a GPU: it loads, exports exactly what include/barq_kv.h declares,
+the torch binding module loads, and the kernels' invariant-divisor arithmetic is exact."""
+
+import ctypes
+import subprocess
+
+import pytest
+
+from barqtrain_amd import _capi, build
+
+
+@pytest.fixture(scope="module")
+def built():
+    if not build.is_built():
+        build.build()
+    return True
+
+
+def test_library_exports_every_header_function(built):
+    lib = ctypes.CDLL(str(build.lib_path()))
+    declared = _capi.header_functions()
+    assert len(declared) == 10
+    for name in declared:
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", str(build.lib_path())], capture_output=True, text=True).stdout
+    exported = sorted({line.split()[-1] for line in out.splitlines() if " T barq_kv_" in line})
+    assert exported == declared
+
+
+def test_ctypes_signatures_cover_header(built):
+    assert sorted(_capi._SIGNATURES) == _capi.header_functions()
+    lib = _capi.load_library()
+    assert lib.barq_kv_version().decode().endswith("gfx950")
+    assert lib.barq_kv_status_string(1).decode().startswith("invalid")
+
+
+def test_invalid_arguments_rejected_without_gpu(built):
+    """Argument validation happens on the host before any HIP call."""
+    lib = _capi.load_library()
+    assert lib.barq_kv_pool_reset(None, None, None) == 1
+    pool = _capi.BarqKVPool()
+    assert lib.barq_kv_append(ctypes.byref(pool), None, None, 1, 1, 0, 0, 0, None) == 1
+    assert lib.barq_kv_append_dense(None, None, None, None, None, 1, 1, 1, 1, 1, 1, 1, 2, 0, 0, 0, None) == 1
+
+
+def test_torch_binding_module_surface(built):
+    import importlib.util
+
+    import torch  # noqa: F401
+
+    spec = importlib.util.spec_from_file_location("barqtrain_cuda", str(build.ext_path()))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    for name in ("paged_kv_append_", "pool_reset_", "pool_append_", "pool_gather", "pool_update_",
+                 "pool_crop_", "pool_free_rows_", "pool_copy_rows_"):
+        assert callable(getattr(mod, name)), name
+    assert mod.CTRL_WORDS == 64
+
+
+def test_library_is_gfx950_only(built, tmp_path):
+    """The fatbin embedded in the library holds one device code object, for gfx950."""
+    fatbin = tmp_path / "fatbin.bin"
+    subprocess.run(["objcopy", "-O", "binary", "--only-section=.hip_fatbin", str(build.lib_path()), str(fatbin)],
+                   check=True)
+    out = subprocess.run(["/opt/rocm/llvm/bin/clang-offload-bundler", "--list", "--type=o", f"--input={fatbin}"],
+                         capture_output=True, text=True, check=True).stdout.split()
+    devices = [t for t in out if "amdgcn" in t]
+    assert devices == ["hipv4-amdgcn-amd-amdhsa--gfx950"], out
+
+
+FASTDIV_CHECK = r"""
+#include <cstdio>
+#include <cstdint>
+#include "fastdiv.h"
+int main() {
+  const uint32_t ds[] = {1, 2, 3, 5, 7, 10, 16, 24, 48, 64, 80, 96, 127, 128, 160, 255, 256, 257, 516, 1000,
+                         1026, 4097, 65535, 65536, 65537, 1u << 20, (1u << 20) + 1, 2147483647u, 2147483648u,
+                         3000000019u, 4294967295u};
+  uint64_t bad = 0, n_checked = 0;
+  for (uint32_t d : ds) {
+    FastDiv f = FastDiv::make(d);
+    uint32_t probes[] = {0, 1, d - 1, d, d + 1, 2 * d - 1, 2 * d, 4294967295u, 4294967294u, 2147483647u, 2147483648u};
+    for (uint32_t n : probes) { n_checked++; if (f.div(n) != n / d) bad++; }
+    for (uint64_t n = 0; n < 300000; ++n) { n_checked++; if (f.div((uint32_t)n) != (uint32_t)n / d) bad++; }
+    uint64_t x = 0x9E3779B97F4A7C15ull ^ d;
+    for (int i = 0; i < 300000; ++i) {
+      x ^= x << 13; x ^= x >> 7; x ^= x << 17;
+      uint32_t n = (uint32_t)x; n_checked++;
+      if (f.div(n) != n / d) bad++;
+    }
+  }
+  printf("%llu %llu\n", (unsigned long long)bad, (unsigned long long)n_checked);
+  return bad != 0;
+}
+"""
+
+
+def test_fastdiv_is_exact(tmp_path):
+    src = tmp_path / "fd.cpp"
+    src.write_text(FASTDIV_CHECK)
+    exe = tmp_path / "fd"
+    subprocess.run(["g++", "-O2", "-std=c++17", f"-I{build.CSRC}", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    bad, checked = map(int, out.stdout.split())
+    assert bad == 0 and checked > 10_000_000
