@@ -21,6 +21,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <climits>
 
 #include "barq_kv.h"
 #include "fastdiv.h"
@@ -132,9 +133,11 @@ __device__ int wave_rank_base(const barq_kv_pool& p, int row, int tokens,
 }
 
 // Commit an append of `tokens` to rows [0, batch): map new blocks to pages in rank order,
-// advance seq_lens and high_water, pop the stack.  Run by one whole workgroup, after every tile
-// that read the old metadata has finished reading it.
-__device__ void commit_append(const barq_kv_pool& p, int batch, int tokens,
+// advance seq_lens and high_water, pop the stack.  `limit` is the end of the positions the
+// launch covered (an update covers its output extent only); a row whose new end passes it lost
+// tokens and raises the OUT_SHORT bit.  Run by one whole workgroup, after every tile that read
+// the old metadata has finished reading it.
+__device__ void commit_append(const barq_kv_pool& p, int batch, int tokens, int limit,
                               const FastDiv& div_page) {
   __shared__ int lds_scan[kWaves];
   const int top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
@@ -150,6 +153,7 @@ __device__ void commit_append(const barq_kv_pool& p, int batch, int tokens,
       hw = p.high_water[r];
       nb = new_blocks(len, hw, tokens, mb, div_page);
       if (ceil_div_fd(len + tokens, div_page) > mb) err |= BARQ_KV_ERRBIT_CAPACITY;
+      if (len + tokens > limit) err |= BARQ_KV_ERRBIT_OUT_SHORT;
     }
     int chunk_total = 0;
     const int excl = block_exclusive_scan(nb.count, lds_scan, &chunk_total);
@@ -324,15 +328,15 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
     }
     __syncthreads();
     if (s_meta[5]) {
-      commit_append(p, a.batch, T, a.div_page);
+      commit_append(p, a.batch, T, a.gather ? a.seq_out : INT_MAX, a.div_page);
       if (threadIdx.x == 0) atomicExch(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 0);
     }
   }
 }
 
 __global__ void __launch_bounds__(kThreads) commit_kernel(const barq_kv_pool p, int batch,
-                                                         int tokens, FastDiv div_page) {
-  commit_append(p, batch, tokens, div_page);
+                                                         int tokens, int limit, FastDiv div_page) {
+  commit_append(p, batch, tokens, limit, div_page);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -647,10 +651,14 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   if (batch < 0 || batch > pool->max_batch || tokens < 0 || tokens > kI32Max) return BARQ_KV_ERR_INVALID;
   if (flags & ~(int64_t)(BARQ_KV_SEQ_FROM_DEVICE | BARQ_KV_SEPARATE_FINALIZE)) return BARQ_KV_ERR_INVALID;
   const int64_t cap = pool->max_blocks * pool->page_size;
-  if (tokens > 0 && (!ks || !vs)) return BARQ_KV_ERR_INVALID;
-  if (gather && (!ko || !vo || seq_out < 0 || seq_out > cap)) return BARQ_KV_ERR_INVALID;
+  if (gather && (seq_out < 0 || seq_out > cap)) return BARQ_KV_ERR_INVALID;
   if (tokens > cap) return BARQ_KV_ERR_INVALID;
-  if (batch == 0 || (tokens == 0 && (!gather || seq_out == 0))) return BARQ_KV_OK;
+  if (batch == 0) return BARQ_KV_OK;
+  // An update's tiles cover output positions only, so the output must reach the new tokens.
+  if (gather && tokens > seq_out) return BARQ_KV_ERR_INVALID;
+  if (tokens == 0 && (!gather || seq_out == 0)) return BARQ_KV_OK;
+  if (tokens > 0 && (!ks || !vs)) return BARQ_KV_ERR_INVALID;
+  if (gather && (!ko || !vo)) return BARQ_KV_ERR_INVALID;
 
   const int64_t eb = pool->elem_bytes;
   const int64_t row_bytes = pool->head_dim * eb;
@@ -713,8 +721,9 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   if (tokens > 0 && !a.commit_in_kernel) {
     barq_kv_pool pc = *pool;
     int32_t b32 = (int32_t)batch, t32 = (int32_t)tokens;
+    int32_t limit = gather ? a.seq_out : INT_MAX;
     FastDiv dp = a.div_page;
-    void* args[] = {&pc, &b32, &t32, &dp};
+    void* args[] = {&pc, &b32, &t32, &limit, &dp};
     if (hipLaunchKernel((const void*)&commit_kernel, dim3(1), dim3(kThreads), args, 0, s) != hipSuccess)
       return BARQ_KV_ERR_LAUNCH;
   }

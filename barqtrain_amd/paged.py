@@ -35,6 +35,7 @@ CTRL_ERRORS = 1
 ERRBIT_POOL_EXHAUSTED = 1
 ERRBIT_CAPACITY = 2
 ERRBIT_BAD_INDEX = 4
+ERRBIT_OUT_SHORT = 8
 SEQ_FROM_DEVICE = 1
 SEPARATE_FINALIZE = 2
 

@@ -52,6 +52,8 @@ extern "C" {
 #define BARQ_KV_ERRBIT_POOL_EXHAUSTED 1 /* a new block found no free page; its tokens were dropped */
 #define BARQ_KV_ERRBIT_CAPACITY 2       /* a position fell at or beyond max_blocks * page_size */
 #define BARQ_KV_ERRBIT_BAD_INDEX 4      /* a row index outside [0, max_batch) was given */
+#define BARQ_KV_ERRBIT_OUT_SHORT 8      /* an update's output extent ended before a row's new
+                                           tokens; those tokens were not stored */
 
 /* Flags of barq_kv_gather / barq_kv_update. */
 #define BARQ_KV_SEQ_FROM_DEVICE 1 /* seq_out is the output's capacity; the positions written are

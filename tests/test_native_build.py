@@ -43,6 +43,49 @@ def test_invalid_arguments_rejected_without_gpu(built):
     assert lib.barq_kv_append_dense(None, None, None, None, None, 1, 1, 1, 1, 1, 1, 1, 2, 0, 0, 0, None) == 1
 
 
+def _fake_pool():
+    """A pool descriptor with plausible geometry and non-null, never-dereferenced addresses:
+    only calls that return before any launch may be made with it."""
+    addr = 0x7F0000000000
+    return _capi.BarqKVPool(addr, addr + 2**30, addr + 2**31, addr + 2**31 + 2**20,
+                            addr + 2**31 + 2**21, addr + 2**31 + 2**22, addr + 2**31 + 2**23,
+                            64, 4, 8, 16, 8, 128, 2)
+
+
+def test_empty_work_returns_ok_before_any_launch(built):
+    """No-op calls (no rows, no tokens and no output extent) succeed whatever the pointers,
+    including the null data pointer of an empty output tensor."""
+    lib = _capi.load_library()
+    p = ctypes.byref(_fake_pool())
+    assert lib.barq_kv_update(p, None, None, 0, 3, 0, 0, 0, None, None, 0, 0, 0, 0, 0, None) == 0
+    assert lib.barq_kv_gather(p, None, None, 2, 0, 0, 0, 0, 0, None) == 0
+    assert lib.barq_kv_gather(p, None, None, 0, 5, 0, 0, 0, 0, None) == 0
+    assert lib.barq_kv_append(p, None, None, 3, 0, 0, 0, 0, None) == 0
+    assert lib.barq_kv_crop(p, 0, 5, None) == 0
+    assert lib.barq_kv_free_rows(p, None, 0, None) == 0
+
+
+def test_bad_geometry_rejected_before_any_launch(built):
+    lib = _capi.load_library()
+    p = ctypes.byref(_fake_pool())
+    a = 0x7F1000000000
+    # an update whose output extent cannot hold the new tokens
+    assert lib.barq_kv_update(p, a, a, 2, 5, 0, 0, 0, a, a, 4, 0, 0, 0, 0, None) == 1
+    # output extent beyond the capacity (8 blocks x 16 = 128 positions)
+    assert lib.barq_kv_gather(p, a, a, 2, 129, 0, 0, 0, 0, None) == 1
+    # more rows than the pool holds, negative sizes, unknown flags
+    assert lib.barq_kv_append(p, a, a, 5, 1, 0, 0, 0, None) == 1
+    assert lib.barq_kv_append(p, a, a, 1, -1, 0, 0, 0, None) == 1
+    assert lib.barq_kv_gather(p, a, a, 1, 4, 0, 0, 0, 64, None) == 1
+    # missing data pointers when there is work
+    assert lib.barq_kv_append(p, None, a, 1, 1, 0, 0, 0, None) == 1
+    assert lib.barq_kv_gather(p, None, a, 1, 4, 0, 0, 0, 0, None) == 1
+    # ctrl words must be 256-byte aligned
+    bad = _fake_pool()
+    bad.ctrl += 4
+    assert lib.barq_kv_pool_reset(ctypes.byref(bad), None, None) == 1
+
+
 def test_torch_binding_module_surface(built):
     import importlib.util
 
