@@ -15,7 +15,8 @@
 // Page allocation is deterministic: the new blocks of a launch are ranked in (row, block)
 // order and rank k takes free_pages[top - 1 - k].  Every tile can therefore compute the page
 // of any new block on its own; the stack top, block table and row lengths are committed once
-// per launch, by the last tile to finish (arrival counter) or by a one-workgroup launch.
+// per launch, inside the launch by the last tile to have read its metadata (arrival counters),
+// or by a one-workgroup launch.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -28,19 +29,22 @@
 
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;                     // workgroup of the bookkeeping kernels
 constexpr int kWave = 64;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kUnroll = 8;            // vectors in flight per thread
-constexpr int kMaxTilePages = 64;     // block-table slots a tile stages in LDS
-constexpr int kTileTargetBytes = 32 * 1024;
+constexpr int kStreamThreads = kThreads + kWave;  // stream kernel: control wave + 4 copy waves
+constexpr int kUnroll = 16;                       // vectors in flight per copy thread
+constexpr int kMaxTilePages = 64;                 // block-table slots a tile stages in LDS
+// Positions per tile: whole pages, about this many bytes of K (or V).  With kUnroll 16-byte
+// vectors per thread, a 64 KiB tile is loaded by the 256 copy threads in one batch.
+constexpr int kTileTargetBytes = 64 * 1024;
 
 template <int VB>
 struct VecT;
 template <>
-struct VecT<16> { using T = uint4; };
+struct VecT<16> { using T = uint32_t __attribute__((ext_vector_type(4))); };
 template <>
-struct VecT<8> { using T = uint2; };
+struct VecT<8> { using T = uint32_t __attribute__((ext_vector_type(2))); };
 template <>
 struct VecT<4> { using T = uint32_t; };
 template <>
@@ -49,11 +53,18 @@ template <>
 struct VecT<1> { using T = uint8_t; };
 
 template <typename T>
-__device__ __forceinline__ T zero_vec() { return T{}; }
-template <>
-__device__ __forceinline__ uint4 zero_vec<uint4>() { return make_uint4(0u, 0u, 0u, 0u); }
-template <>
-__device__ __forceinline__ uint2 zero_vec<uint2>() { return make_uint2(0u, 0u); }
+__device__ __forceinline__ T zero_vec() { return T(0); }
+
+// Streaming accesses (page reads, input reads, output writes): every byte is touched once per
+// launch, so they carry the nontemporal hint and do not displace other data from the caches.
+template <typename T>
+__device__ __forceinline__ T ld_stream(const char* ptr) {
+  return __builtin_nontemporal_load((const T*)ptr);
+}
+template <typename T>
+__device__ __forceinline__ void st_stream(char* ptr, T v) {
+  __builtin_nontemporal_store(v, (T*)ptr);
+}
 
 __device__ __forceinline__ int ceil_div_fd(int n, const FastDiv& d) {
   return n <= 0 ? 0 : (int)d.div((uint32_t)(n + (int)d.d - 1));
@@ -76,22 +87,27 @@ __device__ __forceinline__ int wave_max(int v) {
   return v;
 }
 
-// Exclusive prefix sum of v over the workgroup's threads; *total gets the sum of all.
-// Uses lds[0 .. kWaves).  Every thread of the workgroup must call it.
-__device__ __forceinline__ int block_exclusive_scan(int v, int* lds, int* total) {
+__device__ __forceinline__ int wave_incl_scan(int v) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  int incl = v;
 #pragma unroll
   for (int o = 1; o < kWave; o <<= 1) {
-    const int up = __shfl_up(incl, o, kWave);
-    if (lane >= o) incl += up;
+    const int up = __shfl_up(v, o, kWave);
+    if (lane >= o) v += up;
   }
-  if (lane == kWave - 1) lds[wave] = incl;
+  return v;
+}
+
+// Exclusive prefix sum of v over the workgroup's NW waves; *total gets the sum of all.
+// Uses lds[0 .. NW).  Every thread of the workgroup must call it.
+template <int NW>
+__device__ __forceinline__ int block_exclusive_scan(int v, int* lds, int* total) {
+  const int wave = threadIdx.x / kWave;
+  const int incl = wave_incl_scan(v);
+  if ((threadIdx.x & (kWave - 1)) == kWave - 1) lds[wave] = incl;
   __syncthreads();
   int before = 0, all = 0;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
+  for (int w = 0; w < NW; ++w) {
     const int t = lds[w];
     if (w < wave) before += t;
     all += t;
@@ -101,7 +117,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* lds, int* total)
   return before + incl - v;
 }
 
-// Number of blocks of row r that an append of `tokens` maps for the first time, and the first
+// Number of blocks of a row that an append of `tokens` maps for the first time, and the first
 // of them.  Blocks at or beyond max_blocks are never mapped (the capacity bit reports them).
 struct NewBlocks {
   int first;
@@ -135,16 +151,17 @@ __device__ int wave_rank_base(const barq_kv_pool& p, int row, int tokens,
 // Commit an append of `tokens` to rows [0, batch): map new blocks to pages in rank order,
 // advance seq_lens and high_water, pop the stack.  `limit` is the end of the positions the
 // launch covered (an update covers its output extent only); a row whose new end passes it lost
-// tokens and raises the OUT_SHORT bit.  Run by one whole workgroup, after every tile that read
-// the old metadata has finished reading it.
+// tokens and raises the OUT_SHORT bit.  Run by a whole workgroup of NTHREADS threads, after
+// every tile that reads the old metadata has read it.
+template <int NTHREADS>
 __device__ void commit_append(const barq_kv_pool& p, int batch, int tokens, int limit,
                               const FastDiv& div_page) {
-  __shared__ int lds_scan[kWaves];
+  __shared__ int lds_scan[NTHREADS / kWave];
   const int top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
   const int mb = (int)p.max_blocks;
   int used = 0;
   int err = 0;
-  for (int r0 = 0; r0 < batch; r0 += kThreads) {
+  for (int r0 = 0; r0 < batch; r0 += NTHREADS) {
     const int r = r0 + (int)threadIdx.x;
     int len = 0, hw = 0;
     NewBlocks nb{0, 0};
@@ -156,7 +173,7 @@ __device__ void commit_append(const barq_kv_pool& p, int batch, int tokens, int 
       if (len + tokens > limit) err |= BARQ_KV_ERRBIT_OUT_SHORT;
     }
     int chunk_total = 0;
-    const int excl = block_exclusive_scan(nb.count, lds_scan, &chunk_total);
+    const int excl = block_exclusive_scan<NTHREADS / kWave>(nb.count, lds_scan, &chunk_total);
     if (r < batch) {
       for (int j = 0; j < nb.count; ++j) {
         const int idx = top - 1 - (used + excl + j);
@@ -173,8 +190,54 @@ __device__ void commit_append(const barq_kv_pool& p, int batch, int tokens, int 
   if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
 }
 
+// The same commit by one wave, from metadata its lanes already hold (batch <= kWave): lane r
+// holds row r's length and high-water mark, lane k holds free_pages[top - 1 - k], the page the
+// k-th new block takes (ranks past the wave are read from the stack).
+__device__ void commit_from_lanes(const barq_kv_pool& p, int batch, int tokens, int limit,
+                                  const FastDiv& div_page, int len, int hw, int top, int free_k) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int mb = (int)p.max_blocks;
+  int err = 0;
+  NewBlocks nb{0, 0};
+  if (lane < batch) {
+    nb = new_blocks(len, hw, tokens, mb, div_page);
+    if (ceil_div_fd(len + tokens, div_page) > mb) err |= BARQ_KV_ERRBIT_CAPACITY;
+    if (len + tokens > limit) err |= BARQ_KV_ERRBIT_OUT_SHORT;
+  }
+  const int incl = wave_incl_scan(nb.count);
+  const int excl = incl - nb.count;
+  const int total = __shfl(incl, kWave - 1, kWave);
+  const int most = wave_max(nb.count);
+  for (int j = 0; j < most; ++j) {
+    const int k = excl + j;
+    const int from_lane = __shfl(free_k, k & (kWave - 1), kWave);
+    if (j < nb.count) {
+      const int idx = top - 1 - k;
+      int page = -1;
+      if (idx >= 0) page = checked_page(k < kWave ? from_lane : p.free_pages[idx], p.num_pages);
+      if (page < 0) err |= BARQ_KV_ERRBIT_POOL_EXHAUSTED;
+      p.block_table[(int64_t)lane * mb + nb.first + j] = page;
+    }
+  }
+  if (lane < batch) {
+    p.seq_lens[lane] = len + tokens;
+    p.high_water[lane] = max(hw, len + tokens);
+  }
+  if (lane == 0) p.ctrl[BARQ_KV_CTRL_FREE_TOP] = max(0, top - total);
+  if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
+}
+
 // ---------------------------------------------------------------------------------------------
-// Append / gather / update: one tile = one (k|v, row, chunk of positions).
+// Append / gather / update.
+//
+// One workgroup = one tile = (K or V, row, chunk of positions); a gather's chunks are whole
+// pages.  Wave 0 is the control wave: it reads the tile's metadata (the row's length and mark,
+// its block-table slice, the pages that new blocks take) into LDS.  After the barrier the copy
+// waves 1..4 stream the tile, while the control wave counts the tile as arrived and, in the
+// last tile to arrive, commits the append: every tile has read the old metadata by then, so the
+// commit overlaps the copies instead of trailing them.  Arrivals go to BARQ_KV_CTRL_SUBCOUNTERS
+// counters on separate 256-byte lines (tile i to counter i % nsub), whose last arrivals count
+// on the main counter: a single counter hit by every tile at once serialises them.
 // ---------------------------------------------------------------------------------------------
 
 struct StreamArgs {
@@ -190,23 +253,28 @@ struct StreamArgs {
   int32_t batch;
   int32_t tokens;
   int32_t seq_out;   // gather: positions covered by the grid (capacity with SEQ_FROM_DEVICE)
-  int32_t chunk;     // positions per tile (a multiple of page_size when gathering)
-  int32_t chunks;    // tiles per (row, k|v)
+  int32_t chunk;     // positions per tile (pages_per_tile * page_size)
+  int32_t ppt;       // pages per tile
   int32_t gather;    // write the materialised output
   int32_t seq_from_device;
-  int32_t commit_in_kernel;  // last tile commits the append
+  int32_t commit_in_kernel;  // the launch commits its own append
   int32_t hv;        // vectors per token (kv_heads * vr)
+  int32_t rstep;     // kThreads / hv, fast mapping only
+  int32_t nsub;      // arrival sub-counters in use
   FastDiv div_hv;    // by hv
   FastDiv div_vr;    // by vectors per head row
   FastDiv div_page;  // by page_size
   FastDiv div_chunks;
 };
 
-template <int VB>
-__global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
+// FAST: hv is 64, 128 or 256 and every lane offset fits 32 bits.  A copy wave then covers whole
+// runs of 64 vectors of one token position at a time, so position, block, page and output row
+// are wave-uniform (scalar registers) and a lane's addresses differ only by its column offset.
+template <int VB, bool FAST>
+__global__ void __launch_bounds__(kStreamThreads) stream_kernel(const StreamArgs a) {
   using V = typename VecT<VB>::T;
-  __shared__ int s_pages[kMaxTilePages + 1];
-  __shared__ int s_meta[6];  // len, hw, lo, hi, blk_lo, last
+  __shared__ int64_t s_pbase[kMaxTilePages + 1];  // byte offset of each block's page, or -1
+  __shared__ int s_meta[6];                       // len, hw, lo, hi, blk_lo, last
 
   const barq_kv_pool& p = a.pool;
   const int kv = blockIdx.x & 1;
@@ -215,15 +283,39 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   const int c = rest - b * (int)a.div_chunks.d;
   const int T = a.tokens;
   const int P = (int)p.page_size;
+  const int mb = (int)p.max_blocks;
+  const bool committing = T > 0 && a.commit_in_kernel;
+  const bool rows_in_lanes = a.batch <= kWave;
+  // Early commit: the commit inputs (every row's length and mark, the stack top) sit in the
+  // control wave's lanes, one row per lane.
+  const bool early = committing && rows_in_lanes;
+
+  int c_len = 0, c_hw = 0, c_top = 0;
 
   if (threadIdx.x < kWave) {
     const int lane = threadIdx.x;
+    // One round of independent loads: this row, the tile's block-table slice (gather tiles are
+    // block aligned), every row's metadata (batch <= kWave) and the stack top.
     const int len = p.seq_lens[b];
     const int hw = p.high_water[b];
+    int pre = -1;
+    const int gb0 = c * a.ppt;
+    if (a.gather && lane < a.ppt && gb0 + lane < mb) pre = p.block_table[(int64_t)b * mb + gb0 + lane];
+    int rl = 0, rh = 0;
+    if (rows_in_lanes && lane < a.batch && (T > 0 || a.seq_from_device)) {
+      rl = p.seq_lens[lane];
+      rh = p.high_water[lane];
+    }
+    const int top = T > 0 ? p.ctrl[BARQ_KV_CTRL_FREE_TOP] : 0;
+
     int smax = a.seq_out;
     if (a.seq_from_device) {
       int m = 0;
-      for (int r = lane; r < a.batch; r += kWave) m = max(m, p.seq_lens[r] + T);
+      if (rows_in_lanes) {
+        if (lane < a.batch) m = rl + T;
+      } else {
+        for (int r = lane; r < a.batch; r += kWave) m = max(m, p.seq_lens[r] + T);
+      }
       smax = min(wave_max(m), a.seq_out);
     }
     int lo, hi;
@@ -239,25 +331,33 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
       blk_lo = (int)a.div_page.div((uint32_t)lo);
       nblk = (int)a.div_page.div((uint32_t)(hi - 1)) - blk_lo + 1;
     }
-    const NewBlocks nb = new_blocks(len, hw, T, (int)p.max_blocks, a.div_page);
+    const NewBlocks nb = new_blocks(len, hw, T, mb, a.div_page);
     const bool touches_new = nb.count > 0 && blk_lo < nb.first + nb.count && blk_lo + nblk > nb.first;
-    int top = 0, base = 0;
+    int base = 0;
     if (touches_new) {
-      top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
-      base = wave_rank_base(p, b, T, a.div_page);
-    }
-    for (int i = lane; i < nblk; i += kWave) {
-      const int blk = blk_lo + i;
-      int page = -1;
-      if (blk < (int)p.max_blocks) {
-        if (blk < nb.first) {
-          page = checked_page(p.block_table[(int64_t)b * p.max_blocks + blk], p.num_pages);
-        } else if (blk < nb.first + nb.count) {
-          const int idx = top - 1 - (base + blk - nb.first);
-          page = idx >= 0 ? checked_page(p.free_pages[idx], p.num_pages) : -1;
-        }
+      if (rows_in_lanes) {
+        base = wave_sum(lane < b ? new_blocks(rl, rh, T, mb, a.div_page).count : 0);
+      } else {
+        base = wave_rank_base(p, b, T, a.div_page);
       }
-      s_pages[i] = page;
+    }
+    // nblk <= kMaxTilePages + 1 (an append chunk may start mid-block): two slots per lane.
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int i = lane + k * kWave;
+      if (i < nblk) {
+        const int blk = blk_lo + i;
+        int page = -1;
+        if (blk < mb) {
+          if (blk < nb.first) {
+            page = checked_page((a.gather && k == 0) ? pre : p.block_table[(int64_t)b * mb + blk], p.num_pages);
+          } else if (blk < nb.first + nb.count) {
+            const int idx = top - 1 - (base + blk - nb.first);
+            page = idx >= 0 ? checked_page(p.free_pages[idx], p.num_pages) : -1;
+          }
+        }
+        s_pbase[i] = page >= 0 ? (int64_t)page * a.page_bytes : (int64_t)-1;
+      }
     }
     if (lane == 0) {
       s_meta[0] = len;
@@ -266,69 +366,151 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
       s_meta[3] = hi;
       s_meta[4] = blk_lo;
     }
+    c_len = rl;
+    c_hw = rh;
+    c_top = top;
   }
   __syncthreads();
+
+  if (early && threadIdx.x < kWave) {
+    // Control wave.  Every metadata value this tile uses was read before the barrier, so the
+    // tile arrives now, and the copy waves never wait for the arrival or the commit.
+    const int lane = threadIdx.x;
+    const int fidx = c_top - 1 - lane;  // the page that the lane-th new block takes
+    const int c_free = fidx >= 0 ? p.free_pages[fidx] : -1;
+    int last = 0;
+    if (lane == 0) {
+      const int nsub = a.nsub;
+      const int sub = (int)blockIdx.x % nsub;
+      const int expect = ((int)gridDim.x - sub + nsub - 1) / nsub;
+      int* counter = &p.ctrl[BARQ_KV_CTRL_SUBCOUNTER0 + sub * BARQ_KV_CTRL_SUBCOUNTER_STRIDE];
+      if (atomicAdd(counter, 1) == expect - 1) {
+        atomicExch(counter, 0);
+        last = atomicAdd(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 1) == nsub - 1;
+      }
+    }
+    if (__shfl(last, 0, kWave)) {
+      commit_from_lanes(p, a.batch, T, a.gather ? a.seq_out : INT_MAX, a.div_page, c_len, c_hw, c_top, c_free);
+      if (lane == 0) atomicExch(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 0);
+    }
+    return;
+  }
 
   const int len = s_meta[0];
   const int hw = s_meta[1];
   const int lo = s_meta[2];
   const int hi = s_meta[3];
   const int blk_lo = s_meta[4];
-  const int total = (hi > lo ? hi - lo : 0) * a.hv;
+  const int npos = hi > lo ? hi - lo : 0;
 
   const char* in = kv ? a.in_v : a.in_k;
   char* pages = (char*)(kv ? p.value_pages : p.key_pages);
   char* out = kv ? a.out_v : a.out_k;
-  const int64_t in_row = (int64_t)b * a.in_sb;
-  const int64_t out_row = (int64_t)b * a.out_sb;
+  const int wave = (int)(threadIdx.x / kWave);
 
-  for (int i0 = threadIdx.x; i0 < total; i0 += kThreads * kUnroll) {
-    V val[kUnroll];
-    int64_t dst[kUnroll];
-    int64_t pdst[kUnroll];
+  if (FAST) {
+    if (wave > 0) {
+      const int lane = (int)(threadIdx.x & (kWave - 1));
+      const int ct0 = (wave - 1) * kWave;
+      const int r0 = __builtin_amdgcn_readfirstlane((int)a.div_hv.div((uint32_t)ct0));
+      const int col = ct0 - r0 * a.hv + lane;
+      const int h = (int)a.div_vr.div((uint32_t)col);
+      const int v = col - h * (int)a.div_vr.d;
+      const uint32_t page_lane = (uint32_t)(col * VB);
+      const uint32_t out_lane = (uint32_t)((int64_t)h * a.out_sh + (int64_t)v * VB);
+      const uint32_t in_lane = (uint32_t)((int64_t)h * a.in_sh + (int64_t)v * VB);
+      const char* in_row = in + (int64_t)b * a.in_sb;
+      char* out_row = out + (int64_t)b * a.out_sb;
+      const int rstep = a.rstep;
+      for (int j0 = r0; j0 < npos; j0 += rstep * kUnroll) {
+        V val[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int i = i0 + u * kThreads;
-      dst[u] = -1;
-      pdst[u] = -1;
-      val[u] = zero_vec<V>();
-      if (i < total) {
-        const int tok = (int)a.div_hv.div((uint32_t)i);
-        const int hv = i - tok * a.hv;
-        const int s = lo + tok;
-        const int h = (int)a.div_vr.div((uint32_t)hv);
-        const int v = hv - h * (int)a.div_vr.d;
-        const int blk = (int)a.div_page.div((uint32_t)s);
-        const int off = s - blk * P;
-        const int page = s_pages[blk - blk_lo];
-        const int64_t poff = (int64_t)page * a.page_bytes + (int64_t)off * a.tok_bytes + (int64_t)hv * VB;
-        if (s >= len && s < len + T) {
-          val[u] = *(const V*)(in + in_row + (int64_t)h * a.in_sh + (int64_t)(s - len) * a.in_st + (int64_t)v * VB);
-          if (page >= 0) pdst[u] = poff;
-        } else if (s < hw && page >= 0) {
-          val[u] = *(const V*)(pages + poff);
+        for (int u = 0; u < kUnroll; ++u) {
+          const int j = j0 + u * rstep;
+          const int s = lo + j;
+          val[u] = zero_vec<V>();
+          if (j < npos) {
+            if ((unsigned)(s - len) < (unsigned)T) {
+              val[u] = ld_stream<V>(in_row + (int64_t)(s - len) * a.in_st + in_lane);
+            } else if (s < hw) {
+              const int blk = (int)a.div_page.div((uint32_t)s);
+              const int64_t pb = __hip_readfirstlane(s_pbase[blk - blk_lo]);
+              if (pb >= 0) val[u] = ld_stream<V>(pages + pb + (int64_t)(s - blk * P) * a.tok_bytes + page_lane);
+            }
+          }
         }
-        if (a.gather) dst[u] = out_row + (int64_t)h * a.out_sh + (int64_t)s * a.out_ss + (int64_t)v * VB;
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          const int j = j0 + u * rstep;
+          const int s = lo + j;
+          if (j < npos) {
+            if (a.gather) st_stream<V>(out_row + (int64_t)s * a.out_ss + out_lane, val[u]);
+            if ((unsigned)(s - len) < (unsigned)T) {
+              const int blk = (int)a.div_page.div((uint32_t)s);
+              const int64_t pb = __hip_readfirstlane(s_pbase[blk - blk_lo]);
+              if (pb >= 0) *(V*)(pages + pb + (int64_t)(s - blk * P) * a.tok_bytes + page_lane) = val[u];
+            }
+          }
+        }
       }
     }
+  } else {
+    // Any geometry: copy thread i of the tile takes vectors i, i + kThreads, ... of the tile's
+    // [positions, kv_heads * vr] run; only the data is held across the batch.
+    const int total = npos * a.hv;
+    const int64_t in_row = (int64_t)b * a.in_sb;
+    const int64_t out_row = (int64_t)b * a.out_sb;
+    for (int i0 = wave > 0 ? (int)threadIdx.x - kWave : total; i0 < total; i0 += kThreads * kUnroll) {
+      V val[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      if (dst[u] >= 0) *(V*)(out + dst[u]) = val[u];
-      if (pdst[u] >= 0) *(V*)(pages + pdst[u]) = val[u];
+      for (int u = 0; u < kUnroll; ++u) {
+        const int i = i0 + u * kThreads;
+        val[u] = zero_vec<V>();
+        if (i < total) {
+          const int tok = (int)a.div_hv.div((uint32_t)i);
+          const int hvi = i - tok * a.hv;
+          const int s = lo + tok;
+          if ((unsigned)(s - len) < (unsigned)T) {
+            const int h = (int)a.div_vr.div((uint32_t)hvi);
+            const int v = hvi - h * (int)a.div_vr.d;
+            val[u] = ld_stream<V>(in + in_row + (int64_t)h * a.in_sh + (int64_t)(s - len) * a.in_st + (int64_t)v * VB);
+          } else if (s < hw) {
+            const int blk = (int)a.div_page.div((uint32_t)s);
+            const int64_t pb = s_pbase[blk - blk_lo];
+            if (pb >= 0) val[u] = ld_stream<V>(pages + pb + (int64_t)(s - blk * P) * a.tok_bytes + (int64_t)hvi * VB);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int i = i0 + u * kThreads;
+        if (i < total) {
+          const int tok = (int)a.div_hv.div((uint32_t)i);
+          const int hvi = i - tok * a.hv;
+          const int s = lo + tok;
+          if (a.gather) {
+            const int h = (int)a.div_vr.div((uint32_t)hvi);
+            const int v = hvi - h * (int)a.div_vr.d;
+            st_stream<V>(out + out_row + (int64_t)h * a.out_sh + (int64_t)s * a.out_ss + (int64_t)v * VB, val[u]);
+          }
+          if ((unsigned)(s - len) < (unsigned)T) {
+            const int blk = (int)a.div_page.div((uint32_t)s);
+            const int64_t pb = s_pbase[blk - blk_lo];
+            if (pb >= 0) *(V*)(pages + pb + (int64_t)(s - blk * P) * a.tok_bytes + (int64_t)hvi * VB) = val[u];
+          }
+        }
+      }
     }
   }
 
-  if (T > 0 && a.commit_in_kernel) {
-    // Every tile read its metadata before the barrier above; arriving after its copy loop, the
-    // last tile to arrive is the only writer of that metadata in this launch.
+  if (committing && !early) {
+    // More rows than a wave has lanes: arrive after the copy; the last tile commits with the
+    // whole workgroup.
     __syncthreads();
-    if (threadIdx.x == 0) {
-      const int prev = atomicAdd(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 1);
-      s_meta[5] = (prev == (int)gridDim.x - 1);
-    }
+    if (threadIdx.x == 0) s_meta[5] = atomicAdd(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 1) == (int)gridDim.x - 1;
     __syncthreads();
     if (s_meta[5]) {
-      commit_append(p, a.batch, T, a.gather ? a.seq_out : INT_MAX, a.div_page);
+      commit_append<kStreamThreads>(p, a.batch, T, a.gather ? a.seq_out : INT_MAX, a.div_page);
       if (threadIdx.x == 0) atomicExch(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 0);
     }
   }
@@ -336,7 +518,7 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
 
 __global__ void __launch_bounds__(kThreads) commit_kernel(const barq_kv_pool p, int batch,
                                                          int tokens, int limit, FastDiv div_page) {
-  commit_append(p, batch, tokens, limit, div_page);
+  commit_append<kThreads>(p, batch, tokens, limit, div_page);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -453,7 +635,7 @@ __global__ void __launch_bounds__(kThreads) free_rows_kernel(const barq_kv_pool 
       }
     }
     int chunk_total = 0;
-    const int excl = block_exclusive_scan(cnt, lds_scan, &chunk_total);
+    const int excl = block_exclusive_scan<kWaves>(cnt, lds_scan, &chunk_total);
     if (r >= 0) {
       for (int j = 0; j < cnt; ++j) {
         const int64_t slot = (int64_t)top + pushed + excl + j;
@@ -570,7 +752,7 @@ __global__ void __launch_bounds__(kThreads) copy_rows_kernel(const CopyArgs a) {
       }
     }
     int chunk_total = 0;
-    const int excl = block_exclusive_scan(cnt, lds_scan, &chunk_total);
+    const int excl = block_exclusive_scan<kWaves>(cnt, lds_scan, &chunk_total);
     if (q < a.n) {
       for (int jj = 0; jj < cnt; ++jj) {
         const int idx = top - 1 - (used + excl + jj);
@@ -621,10 +803,10 @@ bool pool_ok(const barq_kv_pool* p) {
   return true;
 }
 
-int launch(const void* fn, dim3 grid, void* arg, hipStream_t stream) {
+int launch(const void* fn, dim3 grid, void* arg, hipStream_t stream, int threads = kThreads) {
   void* args[] = {arg};
-  return hipLaunchKernel(fn, grid, dim3(kThreads), args, 0, stream) == hipSuccess ? BARQ_KV_OK
-                                                                                  : BARQ_KV_ERR_LAUNCH;
+  return hipLaunchKernel(fn, grid, dim3(threads), args, 0, stream) == hipSuccess ? BARQ_KV_OK
+                                                                                 : BARQ_KV_ERR_LAUNCH;
 }
 
 #define BARQ_DEFINE_VB_LAUNCH(KERNEL, ARGS)                                                     \
@@ -638,7 +820,22 @@ int launch(const void* fn, dim3 grid, void* arg, hipStream_t stream) {
     }                                                                                           \
   }
 
-BARQ_DEFINE_VB_LAUNCH(stream_kernel, StreamArgs)
+int launch_stream_kernel(int vb, bool fast, dim3 grid, StreamArgs* arg, hipStream_t stream) {
+#define BARQ_STREAM_CASE(VB)                                                                       \
+  case VB:                                                                                         \
+    return fast ? launch((const void*)&stream_kernel<VB, true>, grid, arg, stream, kStreamThreads) \
+                : launch((const void*)&stream_kernel<VB, false>, grid, arg, stream, kStreamThreads);
+  switch (vb) {
+    BARQ_STREAM_CASE(16)
+    BARQ_STREAM_CASE(8)
+    BARQ_STREAM_CASE(4)
+    BARQ_STREAM_CASE(2)
+    default:
+      BARQ_STREAM_CASE(1)
+  }
+#undef BARQ_STREAM_CASE
+}
+
 BARQ_DEFINE_VB_LAUNCH(dense_append_kernel, DenseArgs)
 BARQ_DEFINE_VB_LAUNCH(copy_rows_kernel, CopyArgs)
 
@@ -657,8 +854,8 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   // An update's tiles cover output positions only, so the output must reach the new tokens.
   if (gather && tokens > seq_out) return BARQ_KV_ERR_INVALID;
   if (tokens == 0 && (!gather || seq_out == 0)) return BARQ_KV_OK;
-  if (tokens > 0 && (!ks || !vs)) return BARQ_KV_ERR_INVALID;
-  if (gather && (!ko || !vo)) return BARQ_KV_ERR_INVALID;
+  if (tokens > 0 && (!ks || !vs || sb < 0 || sh < 0 || st < 0)) return BARQ_KV_ERR_INVALID;
+  if (gather && (!ko || !vo || osb < 0 || osh < 0 || oss < 0)) return BARQ_KV_ERR_INVALID;
 
   const int64_t eb = pool->elem_bytes;
   const int64_t row_bytes = pool->head_dim * eb;
@@ -673,19 +870,23 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   const int64_t vr = row_bytes / vb;
   const int64_t hv = pool->kv_heads * vr;
 
-  // Positions per tile: whole pages when gathering, about kTileTargetBytes of each of K and V.
+  // Positions per tile: whole pages, about kTileTargetBytes of each of K and V.
   const int64_t P = pool->page_size;
   int64_t pages_per_tile = kTileTargetBytes / (P * tok_bytes);
   if (pages_per_tile < 1) pages_per_tile = 1;
   if (pages_per_tile > kMaxTilePages) pages_per_tile = kMaxTilePages;
   // An append tile starts at an arbitrary slot, so its `chunk` positions touch at most
-  // pages_per_tile + 1 blocks: s_pages holds kMaxTilePages + 1.
+  // pages_per_tile + 1 blocks: s_pbase holds kMaxTilePages + 1.
   const int64_t chunk = pages_per_tile * P;
-  if (chunk * hv > kI32Max) return BARQ_KV_ERR_INVALID;
+  if (chunk * hv > kI32Max - (int64_t)kThreads * kUnroll) return BARQ_KV_ERR_INVALID;
   const int64_t span = gather ? seq_out : tokens;
   const int64_t chunks = (span + chunk - 1) / chunk;
   const int64_t tiles = 2 * batch * chunks;
-  if (tiles > kI32Max || batch * chunks > kI32Max) return BARQ_KV_ERR_INVALID;
+  if (tiles > kI32Max) return BARQ_KV_ERR_INVALID;
+  // The wave-uniform mapping needs whole 64-vector runs per wave and 32-bit lane offsets.
+  const bool fast = (hv == 64 || hv == 128 || hv == 256) &&
+                    (!gather || (pool->kv_heads - 1) * osh * eb + row_bytes <= (int64_t)UINT32_MAX) &&
+                    (tokens == 0 || (pool->kv_heads - 1) * sh * eb + row_bytes <= (int64_t)UINT32_MAX);
 
   StreamArgs a;
   a.pool = *pool;
@@ -705,18 +906,20 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   a.tokens = (int32_t)tokens;
   a.seq_out = (int32_t)(gather ? seq_out : 0);
   a.chunk = (int32_t)chunk;
-  a.chunks = (int32_t)chunks;
+  a.ppt = (int32_t)pages_per_tile;
   a.gather = gather ? 1 : 0;
   a.seq_from_device = (gather && (flags & BARQ_KV_SEQ_FROM_DEVICE)) ? 1 : 0;
   a.commit_in_kernel = (flags & BARQ_KV_SEPARATE_FINALIZE) ? 0 : 1;
   a.hv = (int32_t)hv;
+  a.rstep = fast ? (int32_t)(kThreads / hv) : 0;
+  a.nsub = (int32_t)std::min<int64_t>(tiles, BARQ_KV_CTRL_SUBCOUNTERS);
   a.div_hv = FastDiv::make((uint32_t)hv);
   a.div_vr = FastDiv::make((uint32_t)vr);
   a.div_page = FastDiv::make((uint32_t)P);
   a.div_chunks = FastDiv::make((uint32_t)chunks);
 
   hipStream_t s = (hipStream_t)stream;
-  int rc = launch_stream_kernel(vb, dim3((uint32_t)tiles), &a, s);
+  int rc = launch_stream_kernel(vb, fast, dim3((uint32_t)tiles), &a, s);
   if (rc != BARQ_KV_OK) return rc;
   if (tokens > 0 && !a.commit_in_kernel) {
     barq_kv_pool pc = *pool;

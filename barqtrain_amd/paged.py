@@ -29,7 +29,7 @@ from typing import Optional, Sequence
 import numpy as np
 import torch
 
-CTRL_WORDS = 64
+CTRL_WORDS = 1088  # BARQ_KV_CTRL_WORDS of include/barq_kv.h: 64 + 16 arrival sub-counters x 64
 CTRL_FREE_TOP = 0
 CTRL_ERRORS = 1
 ERRBIT_POOL_EXHAUSTED = 1

@@ -42,11 +42,15 @@ extern "C" {
 #define BARQ_KV_ERR_INVALID 1 /* a pointer, size, stride or alignment the kernels cannot take */
 #define BARQ_KV_ERR_LAUNCH 2  /* the HIP runtime refused a launch */
 
-/* Words of barq_kv_pool.ctrl (the arrival counter sits on its own 128-byte line). */
+/* Words of barq_kv_pool.ctrl.  Counters sit on lines of their own; all counters are 0 between
+   launches. */
 #define BARQ_KV_CTRL_FREE_TOP 0 /* number of entries of free_pages that are free pages */
 #define BARQ_KV_CTRL_ERRORS 1   /* sticky error bits below, set by kernels, cleared by reset */
-#define BARQ_KV_CTRL_ARRIVED 32 /* tile arrival counter of the running launch; 0 between launches */
-#define BARQ_KV_CTRL_WORDS 64
+#define BARQ_KV_CTRL_ARRIVED 32 /* tile arrival counter of the running launch */
+#define BARQ_KV_CTRL_SUBCOUNTER0 64       /* first of the arrival sub-counters ... */
+#define BARQ_KV_CTRL_SUBCOUNTER_STRIDE 64 /* ... one per 256 bytes ... */
+#define BARQ_KV_CTRL_SUBCOUNTERS 16       /* ... this many */
+#define BARQ_KV_CTRL_WORDS (BARQ_KV_CTRL_SUBCOUNTER0 + BARQ_KV_CTRL_SUBCOUNTERS * BARQ_KV_CTRL_SUBCOUNTER_STRIDE)
 
 /* Sticky error bits in ctrl[BARQ_KV_CTRL_ERRORS]. */
 #define BARQ_KV_ERRBIT_POOL_EXHAUSTED 1 /* a new block found no free page; its tokens were dropped */

@@ -10,7 +10,7 @@ import torch
 
 from barqtrain_amd import _capi
 
-CTRL_WORDS = 64
+CTRL_WORDS = 1088
 SEQ_FROM_DEVICE = 1
 SEPARATE_FINALIZE = 2
 
@@ -108,7 +108,9 @@ class CPool:
         assert len(mapped) == len(set(mapped)), "a page is mapped twice"
         assert not (free & set(mapped)), "a mapped page is on the free stack"
         assert len(free) + len(mapped) == self.num_pages
-        assert self.ctrl[32].item() == 0, "arrival counter not reset"
+        ctrl = self.ctrl.cpu()
+        assert ctrl[32].item() == 0, "arrival counter not reset"
+        assert not ctrl[64:].any(), "arrival sub-counters not reset"
 
 
 def bits(t: torch.Tensor) -> np.ndarray:

@@ -86,6 +86,22 @@ def test_bad_geometry_rejected_before_any_launch(built):
     assert lib.barq_kv_pool_reset(ctypes.byref(bad), None, None) == 1
 
 
+def header_define(name: str) -> int:
+    """Value of an integer #define of include/barq_kv.h, expressions of earlier defines allowed."""
+    import re
+
+    defs = {}
+    for m in re.finditer(r"^#define (BARQ_KV_\w+) (.+?)(?:\s*/\*.*)?$", _capi.HEADER.read_text(), flags=re.M):
+        expr = m.group(2).strip()
+        for k, v in defs.items():
+            expr = re.sub(rf"\b{k}\b", str(v), expr)
+        try:
+            defs[m.group(1)] = int(eval(expr, {"__builtins__": {}}))
+        except Exception:
+            pass
+    return defs[name]
+
+
 def test_torch_binding_module_surface(built):
     import importlib.util
 
@@ -97,7 +113,9 @@ def test_torch_binding_module_surface(built):
     for name in ("paged_kv_append_", "pool_reset_", "pool_append_", "pool_gather", "pool_update_",
                  "pool_crop_", "pool_free_rows_", "pool_copy_rows_"):
         assert callable(getattr(mod, name)), name
-    assert mod.CTRL_WORDS == 64
+    from barqtrain_amd import paged
+
+    assert mod.CTRL_WORDS == paged.CTRL_WORDS == header_define("BARQ_KV_CTRL_WORDS")
 
 
 def test_library_is_gfx950_only(built, tmp_path):
