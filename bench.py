@@ -8,13 +8,22 @@ contiguous [B, H, seq, D] K and V (ctx 513 -> 768 over the 256 steps).  Inputs a
 fp32 rounded to bf16 from a seeded generator and already resident in HBM.
 
 A step runs as one replay of a captured HIP graph of the 32 fused append+gather launches
-(--mode graph, default), or as 32 host-launched layer updates (--mode eager, the per-call path
-HF attention takes).  Throughput counts algorithmic bytes per step, summed over layers:
-append 2*B*T*tb (read new, write page) + gather sum_b(ctx_b)*tb (read) + B*S_max*tb (write),
-tb = 2*H*D*esize; metadata is not counted.
+(--mode graph, default; the step's new K/V are first copied into the graph's static input
+buffers, as a model's K/V projection would write them), or as 32 host-launched layer updates
+(--mode eager, the per-call path HF attention takes).  Throughput counts algorithmic bytes per
+step, summed over layers: append 2*B*T*tb (read new, write page) + gather sum_b(ctx_b)*tb
+(read) + B*S_max*tb (write), tb = 2*H*D*esize; metadata is not counted.
 
-Prints ONE JSON line.  The CPU baseline (numpy oracle of the reference path, one thread) runs on a
-bounded sample: one layer for the whole 256-step decode, reported per full step (x layers).
+`roofline` is the dominant kernel alone: the same graph replayed without the input copies, timed
+with HIP events on the stream it runs on; `achieved` = algorithmic bytes per launch / average
+launch duration.  `traffic` (measured HBM bytes per launch) is read from the committed rocprof
+counter summary profiles/stream_kernel_c<N>_decode_traffic.json when present.
+
+`cpu_baseline` is the oracle's numpy restatement of the reference path (per-token
+_python_append + materialised current_tensors) on one host core, over the same inputs.
+
+Prints ONE JSON line.  `--pmc-probe` instead runs the eager workload the rocprof counter runs
+profile: a 64 MiB elementwise pass (calibration), the prefill, then the decode steps.
 """
 
 from __future__ import annotations
@@ -32,6 +41,7 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "paged KV append+gather GB/s (% HBM peak); µs per decode-step cache update"
+KERNEL = "stream_kernel<16, true> (fused append + gather, one launch per layer)"
 
 CONFIGS = {
     1: dict(name="C1 tiny plumbing", layers=2, batch=1, heads=4, dim=64, page=16, dtype="float32",
@@ -50,64 +60,72 @@ def parse():
     ap.add_argument("--mode", choices=["graph", "eager"], default="graph")
     ap.add_argument("--separate-commit", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-layers", type=int, default=None,
+                    help="layers the CPU baseline runs (default: all of the config's)")
     ap.add_argument("--repeat", type=int, default=3, help="timed repetitions; the best is reported")
+    ap.add_argument("--pmc-probe", action="store_true", help="short eager run for rocprof counter passes")
     return ap.parse_args()
+
+
+def tok_bytes(cfg):
+    import torch
+
+    esize = torch.empty(0, dtype=getattr(torch, cfg["dtype"])).element_size()
+    return 2 * cfg["heads"] * cfg["dim"] * esize
 
 
 def step_bytes(cfg, ctx_after, tokens=1):
     """Algorithmic bytes of one step over all layers when every row ends at ctx_after."""
-    import torch
-
-    esize = torch.empty(0, dtype=getattr(torch, cfg["dtype"])).element_size()
-    tb = 2 * cfg["heads"] * cfg["dim"] * esize
+    tb = tok_bytes(cfg)
     B = cfg["batch"]
     append = 2 * B * tokens * tb
     gather = B * ctx_after * tb + B * ctx_after * tb
     return cfg["layers"] * (append + gather)
 
 
-def cpu_baseline(cfg, k_dec, v_dec, k_pre, v_pre, steps):
-    """The numpy oracle (reference CPU path + contiguous materialisation) on one layer."""
-    import numpy as np
-
+def cpu_baseline(cfg, k_dec, v_dec, k_pre, v_pre, steps, layers):
+    """The oracle (reference CPU path + contiguous materialisation), layer by layer, timing the
+    decode steps only."""
     from kvgen import to_bits
     from oracle.kv_oracle import DenseLayerOracle
 
     cap = cfg["prefill"] + steps
-    oracle = DenseLayerOracle(cfg["batch"], cap, cfg["page"])
-    oracle.append(to_bits(k_pre), to_bits(v_pre))
-    kd = to_bits(k_dec)  # [steps, B, H, 1, D]
-    vd = to_bits(v_dec)
-    t0 = time.perf_counter()
-    for s in range(steps):
-        oracle.update(kd[s], vd[s])
-    dt = time.perf_counter() - t0
-    nbytes = sum(step_bytes(cfg, cfg["prefill"] + s + 1) for s in range(steps)) / cfg["layers"]
-    per_layer_step_s = dt / steps
+    total = 0.0
+    for layer in range(layers):
+        oracle = DenseLayerOracle(cfg["batch"], cap, cfg["page"])
+        oracle.append(to_bits(k_pre[layer]), to_bits(v_pre[layer]))
+        kd = to_bits(k_dec[:steps, layer])  # [steps, B, H, 1, D]
+        vd = to_bits(v_dec[:steps, layer])
+        t0 = time.perf_counter()
+        for s in range(steps):
+            oracle.update(kd[s], vd[s])
+        total += time.perf_counter() - t0
+    nbytes = sum(step_bytes(cfg, cfg["prefill"] + s + 1) for s in range(steps)) * layers / cfg["layers"]
+    per_step_ms = total / steps * cfg["layers"] / layers * 1e3
     return {
-        "value": round(nbytes / dt / 1e9, 3),
+        "value": round(nbytes / total / 1e9, 3),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"layer 0 only, all {steps} decode steps (append 1 token x {cfg['batch']} rows + "
-                  f"materialised gather), numpy restatement of kv_cache.py _python_append + current_tensors; "
-                  f"per full step = x{cfg['layers']} layers",
-        "ms_per_step": round(per_layer_step_s * cfg["layers"] * 1e3, 3),
-        "seconds": round(dt, 2),
+        "sample": f"{layers} of {cfg['layers']} layers x all {steps} decode steps (append 1 token x "
+                  f"{cfg['batch']} rows + materialised gather), numpy restatement of the reference "
+                  f"kv_cache.py _python_append + current_tensors, one thread; same input bits",
+        "ms_per_step": round(per_step_ms, 3),
+        "seconds": round(total, 2),
     }
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (the cache path shards "
-                                   "by sequence/head/layer with no collective; see DESIGN.md)"}))
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1. The cache path "
+                                   "shards by sequence, KV head or layer with no collective (see DESIGN.md)."}))
         sys.exit(2)
     import torch
 
     from barqtrain_amd import _ffi
     from barqtrain_amd.graph import CapturedDecodeStep
-    from barqtrain_amd.paged import PagePool
+    from barqtrain_amd.paged import SEPARATE_FINALIZE, PagePool
 
     backend = _ffi.load_cuda_backend()
     if backend is None:
@@ -115,6 +133,8 @@ def main():
     torch.cuda.set_device(0)
     cfg = CONFIGS[args.config]
     steps = args.steps if args.steps is not None else cfg["decode"]
+    if args.pmc_probe:
+        args.warmup, args.mode = 0, "eager"
     L, B, H, D, P = cfg["layers"], cfg["batch"], cfg["heads"], cfg["dim"], cfg["page"]
     dtype = getattr(torch, cfg["dtype"])
     prefill = cfg["prefill"]
@@ -130,16 +150,33 @@ def main():
     k_pre = [normal((B, prefill, H, D)).transpose(1, 2) for _ in range(L)]
     v_pre = [normal((B, prefill, H, D)).transpose(1, 2) for _ in range(L)]
     n_in = max(steps, args.warmup)
-    k_dec = normal((n_in, L, B, H, 1, D))
-    v_dec = normal((n_in, L, B, H, 1, D))
+    k_dec = normal((n_in, L, B, 1, H, D)).transpose(3, 4)
+    v_dec = normal((n_in, L, B, 1, H, D)).transpose(3, 4)
 
     pools = [PagePool(max_batch=B, max_blocks=math.ceil(cap / P), page_size=P, kv_heads=H, head_dim=D,
                       dtype=dtype, device=dev) for _ in range(L)]
 
     def prefill_all():
-        for l, pool in enumerate(pools):
+        for layer, pool in enumerate(pools):
             pool.reset()
-            pool.update(k_pre[l], v_pre[l])
+            pool.update(k_pre[layer], v_pre[layer])
+
+    flags = SEPARATE_FINALIZE if args.separate_commit else 0
+
+    if args.pmc_probe:
+        src = torch.zeros(64 * 2**20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.bitwise_not(src, out=dst)  # calibration: one elementwise kernel, 64 MiB in + 64 MiB out
+        prefill_all()
+        for s in range(steps):
+            for layer, pool in enumerate(pools):
+                pool.update(k_dec[s, layer], v_dec[s, layer], flags=flags)
+        torch.cuda.synchronize()
+        total = sum(step_bytes(cfg, prefill + s + 1) for s in range(steps))
+        print(json.dumps({"pmc_probe": True, "config": cfg["name"], "steps": steps, "launches": steps * L,
+                          "algorithmic_bytes_per_launch": total / (steps * L)}), flush=True)
+        return
 
     graph = None
     if args.mode == "graph":
@@ -152,11 +189,9 @@ def main():
             vin.copy_(v_dec[s])
             graph.replay()
     else:
-        flags = 2 if args.separate_commit else 0
-
         def run_step(s):
-            for l, pool in enumerate(pools):
-                pool.update(k_dec[s, l], v_dec[s, l], flags=flags)
+            for layer, pool in enumerate(pools):
+                pool.update(k_dec[s, layer], v_dec[s, layer], flags=flags)
 
     # warmup, then a fresh prefill so the timed steps are exactly ctx 513 -> 512 + steps
     prefill_all()
@@ -164,31 +199,43 @@ def main():
         run_step(s)
     torch.cuda.synchronize()
 
-    best = None
-    for _ in range(max(1, args.repeat)):
-        prefill_all()
-        torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record()
-        for s in range(steps):
-            run_step(s)
-        end.record()
-        torch.cuda.synchronize()
-        ms = start.elapsed_time(end)
-        best = ms if best is None else min(best, ms)
+    def timed(fn):
+        best = None
+        for _ in range(max(1, args.repeat)):
+            prefill_all()
+            torch.cuda.synchronize()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            for s in range(steps):
+                fn(s)
+            end.record()
+            torch.cuda.synchronize()
+            ms = start.elapsed_time(end)
+            best = ms if best is None else min(best, ms)
+        return best
+
+    best = timed(run_step)
     errors = [p.errors() for p in pools]
     if any(errors):
         raise SystemExit(f"device error bits set: {errors}")
 
+    # The dominant kernel alone: the per-layer launches without the input copies (graph mode),
+    # timed on the stream they run on.
+    if graph is not None:
+        kernel_ms = timed(lambda s: graph.replay())
+    else:
+        kernel_ms = best
+
     total_bytes = sum(step_bytes(cfg, prefill + s + 1) for s in range(steps))
     gbs = total_bytes / (best / 1e3) / 1e9
     launches = steps * L
-    avg_launch_us = best * 1e3 / launches
+    avg_launch_us = kernel_ms * 1e3 / launches
     bytes_per_launch = total_bytes / launches
+    achieved = bytes_per_launch / (avg_launch_us * 1e-6) / 1e9
 
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"traffic_config{args.config}.json")
+    tpath = os.path.join(ROOT, "profiles", f"stream_kernel_c{args.config}_decode_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
@@ -218,20 +265,19 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "stream_kernel<16> (fused append + gather, one launch per layer)",
-            "achieved": round(bytes_per_launch / (avg_launch_us * 1e-6) / 1e9, 2),
+            "kernel": KERNEL,
+            "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(bytes_per_launch / (avg_launch_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "bytes_per_launch": int(bytes_per_launch),
             "avg_launch_us": round(avg_launch_us, 3),
         },
     }
     if not args.no_cpu_baseline:
-        k0 = k_dec[:steps, 0]
-        v0 = v_dec[:steps, 0]
-        result["cpu_baseline"] = cpu_baseline(cfg, k0, v0, k_pre[0], v_pre[0], steps)
+        layers = min(args.cpu_layers or L, L)
+        result["cpu_baseline"] = cpu_baseline(cfg, k_dec, v_dec, k_pre, v_pre, steps, layers)
     print(json.dumps(result), flush=True)
 
 
