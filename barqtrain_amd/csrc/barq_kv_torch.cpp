@@ -25,6 +25,16 @@ void check_status(int rc, const char* what) {
 
 int64_t elem_bytes_of(const at::Tensor& t) { return (int64_t)t.element_size(); }
 
+// Same shape, and the same strides along every dimension of size > 1 (a size-1 dimension's
+// stride never enters an address).  HF decode steps hand over K and V that differ only in the
+// stride of their size-1 sequence dimension.
+bool same_layout(const at::Tensor& a, const at::Tensor& b) {
+  if (a.sizes() != b.sizes()) return false;
+  for (int64_t d = 0; d < a.dim(); ++d)
+    if (a.size(d) > 1 && a.stride(d) != b.stride(d)) return false;
+  return true;
+}
+
 // The pool is passed as (key_pages, value_pages, block_table, seq_lens, high_water, free_pages,
 // ctrl), the tensors of barqtrain_amd.paged.PagePool.
 barq_kv_pool pool_from(const std::vector<at::Tensor>& t) {
@@ -72,14 +82,14 @@ void check_states(const barq_kv_pool& p, const at::Tensor& pages, const at::Tens
               "key_states and value_states must stay in the cache dtype");
   TORCH_CHECK(k.size(1) == p.kv_heads && k.size(3) == p.head_dim, "key_states kv_heads/head_dim mismatch");
   TORCH_CHECK(k.stride(3) == 1 && v.stride(3) == 1, "head_dim of the states must be contiguous");
-  TORCH_CHECK(k.strides() == v.strides(), "key_states and value_states must share strides");
+  TORCH_CHECK(same_layout(k, v), "key_states and value_states must share strides");
 }
 
 void check_out(const barq_kv_pool& p, const at::Tensor& pages, const at::Tensor& ko,
                const at::Tensor& vo, int64_t batch, int64_t seq_out) {
   TORCH_CHECK(ko.is_cuda() && vo.is_cuda() && ko.get_device() == pages.get_device(),
               "outputs must be on the cache device");
-  TORCH_CHECK(ko.dim() == 4 && vo.sizes() == ko.sizes() && ko.strides() == vo.strides(),
+  TORCH_CHECK(ko.dim() == 4 && same_layout(ko, vo),
               "outputs must be [batch, kv_heads, seq, head_dim] with equal strides");
   TORCH_CHECK(ko.scalar_type() == pages.scalar_type() && vo.scalar_type() == pages.scalar_type(),
               "outputs must have the cache dtype");
@@ -131,7 +141,7 @@ void paged_kv_append_(at::Tensor key_cache, at::Tensor value_cache, at::Tensor s
 
   at::Tensor ks = key_states.stride(3) == 1 ? key_states : key_states.contiguous();
   at::Tensor vs = value_states.stride(3) == 1 ? value_states : value_states.contiguous();
-  if (ks.strides() != vs.strides()) {
+  if (!same_layout(ks, vs)) {
     ks = ks.contiguous();
     vs = vs.contiguous();
   }

@@ -186,7 +186,11 @@ class PagePool:
 
     @staticmethod
     def _compatible_pair(key_states: torch.Tensor, value_states: torch.Tensor):
-        if key_states.stride(-1) != 1 or value_states.stride(-1) != 1 or key_states.stride() != value_states.stride():
+        """K and V as views the kernels take: unit stride along head_dim and one layout for both
+        (strides of size-1 dimensions do not count: HF decode steps pass K and V that differ only
+        in the stride of their size-1 sequence dimension).  Copies only when needed."""
+        same = all(n == 1 or a == b for n, a, b in zip(key_states.shape, key_states.stride(), value_states.stride()))
+        if key_states.stride(-1) != 1 or value_states.stride(-1) != 1 or not same:
             return key_states.contiguous(), value_states.contiguous()
         return key_states, value_states
 

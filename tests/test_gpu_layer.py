@@ -1,0 +1,170 @@
+"""GPU tests of the Python surface over the HIP kernels (torch binding `barqtrain_cuda`).
+
+* The reference's cache-layer API (kv_cache.py:37-194) on GPU tensors, driven by seeded random
+  programs, against the CPU oracle -- bit-exact on raw element bits.
+* HIP-graph capture of a decode step (every layer's fused append + gather recorded once,
+  lengths read on the device): every replay, with eager work and synchronisations between
+  replays, against the oracle.
+* Hugging Face `generate` with the paged cache on the GPU: same tokens and bit-identical logits
+  as transformers' DynamicCache.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from kvgen import hf_layout, to_bits
+from oracle.kv_oracle import DenseLayerOracle
+
+pytestmark = pytest.mark.gpu
+
+
+def assert_bits(got: torch.Tensor, want: np.ndarray, what: str):
+    g = to_bits(got)
+    assert g.shape == want.shape, (what, g.shape, want.shape)
+    if not np.array_equal(g, want):
+        bad = np.argwhere(g != want)
+        raise AssertionError(f"{what}: {len(bad)} elements differ, first at {bad[0].tolist()}")
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_layer_api_random_program(hip, seed):
+    """update (ragged batches, multi-token), current_tensors, crop (also negative), beam select /
+    repeat, reset and row release through BarqPagedKVCacheLayer on cuda:0."""
+    from barqtrain_amd.kv_cache import BarqPagedKVCacheLayer
+
+    H, D, P, dtype = 8, 128, 16, torch.bfloat16
+    Bmax, cap = 4, 72
+    rng = np.random.default_rng(100 + seed)
+    gen = torch.Generator().manual_seed(seed)
+    layer = BarqPagedKVCacheLayer(max_batch_size=Bmax, max_cache_len=cap, page_size=P)
+    oracle = DenseLayerOracle(Bmax, cap, P)
+    for it in range(40):
+        r = rng.random()
+        if r < 0.55 or not oracle.is_initialized:
+            b = int(rng.integers(1, layer.max_batch_size + 1))
+            t = int(rng.integers(1, 20)) if rng.random() < 0.3 else 1
+            if oracle.is_initialized and int(oracle.seq_lens[:b].max()) + t > cap:
+                continue
+            k = hf_layout(b, H, t, D, dtype, gen)
+            v = hf_layout(b, H, t, D, dtype, gen)
+            gk, gv = layer.update(k.cuda(), v.cuda())
+            ok, ov = oracle.update(to_bits(k), to_bits(v))
+            assert_bits(gk, ok, f"it{it} update K")
+            assert_bits(gv, ov, f"it{it} update V")
+        elif r < 0.65:
+            m = int(rng.integers(-8, cap))
+            layer.crop(m)
+            oracle.crop(m)
+        elif r < 0.72 and layer.current_batch_size:
+            rows = rng.integers(0, layer.current_batch_size, size=layer.current_batch_size).tolist()
+            layer.batch_select_indices(torch.tensor(rows))
+            oracle.batch_select_indices(rows)
+        elif r < 0.76 and layer.current_batch_size and layer.current_batch_size * 2 <= 8:
+            layer.batch_repeat_interleave(2)
+            oracle.batch_repeat_interleave(2)
+        elif r < 0.82:
+            rows = sorted(rng.choice(layer.max_batch_size, size=1, replace=False).tolist())
+            layer.free_rows(rows)
+            oracle.release_rows(rows)
+        elif r < 0.85:
+            layer.reset()
+            oracle.reset()
+        if layer.current_batch_size:
+            assert layer.get_seq_length() == oracle.get_seq_length()
+            ok, ov = oracle.current_tensors()
+            gk, gv = layer.current_tensors()
+            assert_bits(gk, ok, f"it{it} current K")
+            assert_bits(gv, ov, f"it{it} current V")
+    assert layer.pool.errors() == 0
+
+
+def test_graph_replays_match_oracle(hip):
+    """One captured decode step (3 layers, batch 4), replayed 24 times; between replays the
+    program does its own eager work (random tensors, reductions, an eager gather) and
+    synchronises; every replay's K/V views are compared with the oracle."""
+    from barqtrain_amd.graph import CapturedDecodeStep
+    from barqtrain_amd.paged import PagePool
+
+    L, B, H, D, P, prefill, steps = 3, 4, 8, 128, 16, 40, 24
+    cap = prefill + steps
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator().manual_seed(7)
+    pools = [PagePool(max_batch=B, max_blocks=-(-cap // P), page_size=P, kv_heads=H, head_dim=D,
+                      dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    oracles = [DenseLayerOracle(B, cap, P) for _ in range(L)]
+    for pool, oracle in zip(pools, oracles):
+        k = hf_layout(B, H, prefill, D, torch.bfloat16, gen)
+        v = hf_layout(B, H, prefill, D, torch.bfloat16, gen)
+        pool.update(k.to(dev), v.to(dev))
+        oracle.update(to_bits(k), to_bits(v))
+    kin = torch.zeros((L, B, H, 1, D), dtype=torch.bfloat16, device=dev)
+    vin = torch.zeros_like(kin)
+    step = CapturedDecodeStep(pools, B, 1, inputs=(kin, vin))
+    torch.cuda.synchronize()
+    noise = torch.Generator(device=dev).manual_seed(3)
+    for s in range(steps):
+        ks = [hf_layout(B, H, 1, D, torch.bfloat16, gen) for _ in range(L)]
+        vs = [hf_layout(B, H, 1, D, torch.bfloat16, gen) for _ in range(L)]
+        for layer in range(L):
+            kin[layer].copy_(ks[layer].to(dev))
+            vin[layer].copy_(vs[layer].to(dev))
+        scratch = torch.randn((1 << 20,), generator=noise, device=dev)  # eager work between replays
+        _ = scratch.sum().item()
+        outs = step.replay()
+        torch.cuda.synchronize()
+        for layer in range(L):
+            ok, ov = oracles[layer].update(to_bits(ks[layer]), to_bits(vs[layer]))
+            assert_bits(outs[layer][0], ok, f"replay {s} layer {layer} K")
+            assert_bits(outs[layer][1], ov, f"replay {s} layer {layer} V")
+        if s % 8 == 7:  # an eager gather between replays reads the same state
+            gk, gv = pools[0].gather(B)
+            ok, ov = oracles[0].current_tensors()
+            assert_bits(gk, ok, f"eager gather after replay {s}")
+    assert all(p.errors() == 0 for p in pools)
+    assert [int(x) for x in pools[0].seq_lens.cpu()] == [cap] * B
+
+
+def tiny_llama(seed=0):
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    torch.manual_seed(seed)
+    # head_dim 128, 2 KV heads, fp32: a 1 KiB K row per token, the kernels' wave-uniform path
+    cfg = LlamaConfig(vocab_size=512, hidden_size=512, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=1024,
+                      pad_token_id=0, eos_token_id=None, attn_implementation="eager")
+    return LlamaForCausalLM(cfg).eval(), cfg
+
+
+def test_generate_on_gpu_matches_dynamic_cache(hip, monkeypatch):
+    pytest.importorskip("transformers")
+    from transformers.cache_utils import DynamicCache
+
+    from barqtrain import create_paged_kv_cache, patch_inference
+
+    model, cfg = tiny_llama()
+    model = model.to("cuda")
+    ids = torch.randint(1, 512, (3, 21), generator=torch.Generator().manual_seed(2)).to("cuda")
+    new = 40
+
+    def decode(cache):
+        out = model.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=new, do_sample=False,
+                             past_key_values=cache, return_dict_in_generate=True, output_logits=True)
+        return out.sequences, torch.stack(out.logits)
+
+    ref_seq, ref_logits = decode(DynamicCache(config=cfg))
+    cache = create_paged_kv_cache(model, max_batch_size=3, max_cache_len=21 + new, page_size=16)
+    seq, logits = decode(cache)
+    assert torch.equal(seq, ref_seq)
+    assert torch.equal(logits.view(torch.int32), ref_logits.view(torch.int32))
+    assert all(layer.pool.on_gpu and layer.pool.errors() == 0 for layer in cache.layers)
+
+    # the reference's injection route: patch_inference wraps generate and supplies the cache
+    monkeypatch.setenv("BARQTRAIN_PAGED_KV_MIN_CACHE_LEN", "0")
+    patch_inference(model)
+    model.config._attn_implementation = "eager"
+    out = model.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=new, do_sample=False)
+    assert model._barqtrain_last_generate_used_paged_kv is True
+    assert torch.equal(out, ref_seq)

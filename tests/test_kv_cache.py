@@ -128,3 +128,19 @@ def test_generate_kwargs_gates(monkeypatch):
     assert used and kw["past_key_values"].page_size == 32 and kw["past_key_values"].barqtrain_max_cache_len == 8
     monkeypatch.setattr("barqtrain.kv_cache._get_cuda_backend", lambda: None)
     assert maybe_prepare_paged_kv_generate_kwargs(_model(), (), {"input_ids": prompt})[1] is False
+
+
+def test_decode_step_strides_of_hf_accepted_without_copy():
+    """HF decode hands over K (after RoPE) and V (a transposed view) that differ only in the
+    stride of the size-1 sequence dimension; the pool takes them as they are."""
+    from barqtrain_amd.paged import PagePool
+
+    base_k = torch.randn(3, 2, 1, 128)                    # K: [B, H, 1, D] contiguous
+    base_v = torch.randn(3, 1, 2, 128).transpose(1, 2)    # V: [B, 1, H, D] viewed as [B, H, 1, D]
+    assert base_k.stride() != base_v.stride()
+    k, v = PagePool._compatible_pair(base_k, base_v)
+    assert k.data_ptr() == base_k.data_ptr() and v.data_ptr() == base_v.data_ptr()
+    prefill_k = torch.randn(3, 21, 2, 128).transpose(1, 2)
+    prefill_v = torch.randn(3, 2, 21, 128)                 # genuinely different layouts: copied
+    k, v = PagePool._compatible_pair(prefill_k, prefill_v)
+    assert k.stride() == v.stride() and k.is_contiguous()
