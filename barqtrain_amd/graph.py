@@ -13,9 +13,11 @@ from __future__ import annotations
 
 from typing import Optional, Sequence
 
+import numpy as np
 import torch
 
-from barqtrain_amd.paged import SEPARATE_FINALIZE, SEQ_FROM_DEVICE, PagePool
+from barqtrain_amd.paged import (SEPARATE_FINALIZE, SEQ_FROM_DEVICE, PagedKVCapacityError,
+                                 PagedKVPoolExhausted, PagePool)
 
 
 class CapturedDecodeStep:
@@ -46,6 +48,18 @@ class CapturedDecodeStep:
         self.key_out = [torch.empty(shape_out, dtype=p.dtype, device=p.device) for p in self.pools]
         self.value_out = [torch.empty(shape_out, dtype=p.dtype, device=p.device) for p in self.pools]
         self.flags = SEQ_FROM_DEVICE | (SEPARATE_FINALIZE if separate_commit else 0)
+        geometry = {(p.page_size, p.max_blocks, p.max_batch) for p in self.pools}
+        if len(geometry) != 1:
+            raise ValueError("pools of one captured step must share page size, blocks and rows")
+        if any(p.lens.base is not None or p.hw.base is not None for p in self.pools):
+            raise ValueError("a page pool can belong to one captured step only")
+        # One stacked host shadow for all pools (each pool keeps a row view of it), so a replay
+        # checks and advances every layer with a handful of array operations.
+        self._lens = np.stack([p.lens for p in self.pools])
+        self._hw = np.stack([p.hw for p in self.pools])
+        for i, p in enumerate(self.pools):
+            p.lens = self._lens[i]
+            p.hw = self._hw[i]
         from barqtrain_amd.paged import _gpu_backend
 
         backend = _gpu_backend()
@@ -57,10 +71,27 @@ class CapturedDecodeStep:
                                      self.key_out[i], self.value_out[i], self.capacity, self.flags)
 
     def replay(self) -> list[tuple[torch.Tensor, torch.Tensor]]:
-        """Run one captured step; returns each layer's (K, V) views ``[batch, H, seq, D]``."""
-        needs = [p.check_append(self.batch, self.tokens, self.max_length) for p in self.pools]
+        """Run one captured step; returns each layer's (K, V) views ``[batch, H, seq, D]``.
+        Raises, before anything runs, if any layer would pass its capacity or run out of pages."""
+        B, T = self.batch, self.tokens
+        p0 = self.pools[0]
+        lens = self._lens[:, :B]
+        hw = self._hw[:, :B]
+        ends = lens + T
+        worst = int(ends.max())
+        if worst > self.capacity:
+            raise PagedKVCapacityError(
+                f"paged KV cache capacity exceeded: requested {worst}, max_cache_len={self.capacity}")
+        P = p0.page_size
+        need = np.maximum(np.minimum(-(-ends // P), p0.max_blocks) - (-(-hw // P)), 0).sum(axis=1)
+        for p, n in zip(self.pools, need):
+            if n > p.free_count:
+                raise PagedKVPoolExhausted(
+                    f"paged KV page pool exhausted: append needs {int(n)} pages, {p.free_count} free")
         self.graph.replay()
-        for p, need in zip(self.pools, needs):
-            p._advance(self.batch, self.tokens, need)
-        seq = self.pools[0].max_len(self.batch)
-        return [(k[:, :, :seq], v[:, :, :seq]) for k, v in zip(self.key_out, self.value_out)]
+        lens += T
+        np.maximum(hw, lens, out=hw)
+        for p, n in zip(self.pools, need):
+            p.free_count -= int(n)
+        seqs = ends.max(axis=1).tolist()
+        return [(k[:, :, :n], v[:, :, :n]) for k, v, n in zip(self.key_out, self.value_out, seqs)]

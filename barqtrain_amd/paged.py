@@ -124,6 +124,14 @@ class PagePool:
     def _ops(self):
         return _gpu_backend() if self.on_gpu else _HostOps
 
+    def _index_tensor(self, rows: Sequence[int]) -> torch.Tensor:
+        """Row indices as int32 on the pool's device, copied from pinned memory without waiting
+        for the stream (a plain host-to-device copy would synchronise it)."""
+        host = torch.tensor(rows, dtype=torch.int32)
+        if not self.on_gpu:
+            return host
+        return host.pin_memory().to(self.device, non_blocking=True)
+
     # ------------------------------------------------------------------ host shadow
     def new_block_counts(self, batch: int, tokens: int) -> np.ndarray:
         """Blocks each row [0, batch) maps for the first time when `tokens` are appended."""
@@ -257,8 +265,7 @@ class PagePool:
             raise IndexError("free_rows: row out of range")
         if not rows:
             return
-        idx = torch.tensor(rows, dtype=torch.int32, device=self.device)
-        self._ops().pool_free_rows_(self.tensors, idx)
+        self._ops().pool_free_rows_(self.tensors, self._index_tensor(rows))
         r = np.asarray(rows)
         self.free_count += int(np.minimum(-(-self.hw[r] // self.page_size), self.max_blocks).sum())
         self.lens[r] = 0
@@ -281,8 +288,7 @@ class PagePool:
                        kv_heads=self.kv_heads, head_dim=self.head_dim, dtype=self.dtype,
                        device=self.device, num_pages=num_pages)
         if n:
-            idx = torch.tensor(src_rows, dtype=torch.int32, device=self.device)
-            self._ops().pool_copy_rows_(self.tensors, dst.tensors, idx)
+            self._ops().pool_copy_rows_(self.tensors, dst.tensors, self._index_tensor(src_rows))
             dst.lens[:n] = self.lens[r]
             dst.hw[:n] = self.hw[r]
             dst.free_count = num_pages - need

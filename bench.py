@@ -5,22 +5,30 @@ Workload (default, configuration 2 -- the Llama-3-8B KV shape): 32 layers, batch
 128, bf16, page 16.  Every row is prefilled with 512 tokens (untimed), then each timed step is
 one decode step of the cache: for every layer, append 1 token per row and materialise the whole
 contiguous [B, H, seq, D] K and V (ctx 513 -> 768 over the 256 steps).  Inputs are N(0, 1) in
-fp32 rounded to bf16 from a seeded generator and already resident in HBM.
+fp32 rounded to the cache dtype from a seeded generator and already resident in HBM.
 
-A step runs as one replay of a captured HIP graph of the 32 fused append+gather launches
-(--mode graph, default; the step's new K/V are first copied into the graph's static input
-buffers, as a model's K/V projection would write them), or as 32 host-launched layer updates
-(--mode eager, the per-call path HF attention takes).  Throughput counts algorithmic bytes per
-step, summed over layers: append 2*B*T*tb (read new, write page) + gather sum_b(ctx_b)*tb
-(read) + B*S_max*tb (write), tb = 2*H*D*esize; metadata is not counted.
+`--config 1..5` selects the five configurations of BASELINE.json (C1 tiny plumbing, C2
+Llama-3-8B decode, C3 fragmented ragged batch with a random page permutation, C4 32k chunked
+prefill, C5 80-layer 70B-class share with the pool at 90 % occupancy and seeded row churn).
 
-`roofline` is the dominant kernel alone: the same graph replayed without the input copies, timed
-with HIP events on the stream it runs on; `achieved` = algorithmic bytes per launch / average
-launch duration.  `traffic` (measured HBM bytes per launch) is read from the committed rocprof
-counter summary profiles/stream_kernel_c<N>_decode_traffic.json when present.
+A step runs as one replay of a captured HIP graph of the per-layer fused append+gather launches
+(graph mode, C1-C4; the step's new K/V are first copied into the graph's static input buffers,
+as a model's K/V projection would write them), or as host-launched layer updates (eager mode, the
+per-call path HF attention takes; C5, whose launches move gigabytes each).  Throughput counts
+algorithmic bytes per step, summed over layers: append 2*B*T*tb (read new, write page) + gather
+sum_b(ctx_b)*tb (read) + B*S_max*tb (write, zero padding of short rows included), tb =
+2*H*D*esize; metadata is not counted.  Per-step bytes come from the same length arithmetic the
+kernels apply, run on the host.
+
+`roofline` is the dominant kernel alone: in graph mode the same graph replayed without the input
+copies, timed with HIP events on the stream it runs on; `achieved` = algorithmic bytes per
+launch / average launch duration.  `traffic` (measured HBM bytes per launch) is read from the
+committed rocprof counter summary profiles/stream_kernel_c<N>_decode_traffic.json when present.
 
 `cpu_baseline` is the oracle's numpy restatement of the reference path (per-token
-_python_append + materialised current_tensors) on one host core, over the same inputs.
+_python_append + materialised current_tensors) on one host core over the same input bits (C1/C2:
+all layers and steps; larger configs: the first decode steps of layer 0).  The same run checks
+the GPU's layer-0 K/V after those steps bit for bit against it (`parity`).
 
 Prints ONE JSON line.  `--pmc-probe` instead runs the eager workload the rocprof counter runs
 profile: a 64 MiB elementwise pass (calibration), the prefill, then the decode steps.
@@ -43,11 +51,20 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "paged KV append+gather GB/s (% HBM peak); µs per decode-step cache update"
 KERNEL = "stream_kernel<16, true> (fused append + gather, one launch per layer)"
 
+# prefill: ("uniform", n) | ("ragged", lo, hi, seed) | ("chunks", count, size)
 CONFIGS = {
     1: dict(name="C1 tiny plumbing", layers=2, batch=1, heads=4, dim=64, page=16, dtype="float32",
-            prefill=32, decode=128, seed=1001),
+            prefill=("uniform", 32), decode=128, seed=1001, mode="graph", cpu_steps=None),
     2: dict(name="C2 Llama-3-8B KV shape", layers=32, batch=16, heads=8, dim=128, page=16, dtype="bfloat16",
-            prefill=512, decode=256, seed=1002),
+            prefill=("uniform", 512), decode=256, seed=1002, mode="graph", cpu_steps=None),
+    3: dict(name="C3 fragmented ragged batch", layers=32, batch=64, heads=8, dim=128, page=16, dtype="bfloat16",
+            prefill=("ragged", 128, 4096, 2003), perm_seed=3003, decode=128, seed=1003, mode="graph",
+            cpu_steps=8),
+    4: dict(name="C4 long-context chunked prefill", layers=32, batch=1, heads=8, dim=128, page=32, dtype="float16",
+            prefill=("chunks", 16, 2048), decode=64, seed=1004, mode="graph", cpu_steps=16),
+    5: dict(name="C5 70B-class single-GPU share", layers=80, batch=32, heads=8, dim=128, page=16, dtype="bfloat16",
+            prefill=("uniform", 8192), decode=64, seed=1005, mode="eager", occupancy=0.9,
+            churn=(2, 4005), cpu_steps=4),
 }
 
 
@@ -55,70 +72,177 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed decode steps (default: the config's)")
-    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--warmup", type=int, default=None, help="untimed decode steps (default 16, C3-C5: 2)")
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
-    ap.add_argument("--mode", choices=["graph", "eager"], default="graph")
+    ap.add_argument("--mode", choices=["graph", "eager"], default=None, help="default: the config's")
     ap.add_argument("--separate-commit", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=None,
-                    help="layers the CPU baseline runs (default: all of the config's)")
-    ap.add_argument("--repeat", type=int, default=3, help="timed repetitions; the best is reported")
-    ap.add_argument("--pmc-probe", action="store_true", help="short eager run for rocprof counter passes")
+                    help="layers the CPU baseline runs (C1/C2 default: all)")
+    ap.add_argument("--repeat", type=int, default=None, help="timed repetitions; the best is reported")
+    ap.add_argument("--pmc-probe", action="store_true", help="eager run for rocprof counter passes")
     return ap.parse_args()
 
 
+def elem_size(cfg):
+    return {"float32": 4, "bfloat16": 2, "float16": 2, "float64": 8}[cfg["dtype"]]
+
+
 def tok_bytes(cfg):
-    import torch
-
-    esize = torch.empty(0, dtype=getattr(torch, cfg["dtype"])).element_size()
-    return 2 * cfg["heads"] * cfg["dim"] * esize
+    return 2 * cfg["heads"] * cfg["dim"] * elem_size(cfg)
 
 
-def step_bytes(cfg, ctx_after, tokens=1):
-    """Algorithmic bytes of one step over all layers when every row ends at ctx_after."""
-    tb = tok_bytes(cfg)
-    B = cfg["batch"]
-    append = 2 * B * tokens * tb
-    gather = B * ctx_after * tb + B * ctx_after * tb
-    return cfg["layers"] * (append + gather)
-
-
-def cpu_baseline(cfg, k_dec, v_dec, k_pre, v_pre, steps, layers, gpu_final=None):
-    """The oracle (reference CPU path + contiguous materialisation), layer by layer, timing the
-    decode steps only.  `gpu_final` (layer 0's last K, V from the GPU) is compared bit for bit
-    with the oracle's last output of layer 0."""
+def prefill_lengths(cfg):
+    """Per-row context after the prefill."""
     import numpy as np
 
+    kind = cfg["prefill"]
+    B = cfg["batch"]
+    if kind[0] == "uniform":
+        return [kind[1]] * B
+    if kind[0] == "ragged":  # longest rows first: the reference API appends to rows [0, batch)
+        rng = np.random.default_rng(kind[3])
+        return sorted(rng.integers(kind[1], kind[2] + 1, size=B).tolist(), reverse=True)
+    return [kind[1] * kind[2]] * B
+
+
+def prefill_calls(cfg):
+    """(batch, tokens, gather_after) of the prefill's append calls, in order."""
+    kind = cfg["prefill"]
+    if kind[0] == "uniform":
+        return [(cfg["batch"], kind[1], True)]
+    if kind[0] == "chunks":
+        return [(cfg["batch"], kind[2], True)] * kind[1]
+    lens = prefill_lengths(cfg)
+    calls, done = [], 0
+    for b in range(len(lens), 0, -1):
+        need = lens[b - 1] - done
+        if need > 0:
+            calls.append((b, need, False))
+            done += need
+    return calls
+
+
+def churn_rows(cfg, steps):
+    """Rows freed (and restarted empty) before each decode step."""
+    import numpy as np
+
+    if "churn" not in cfg:
+        return [[] for _ in range(steps)]
+    n, seed = cfg["churn"]
+    rng = np.random.default_rng(seed)
+    return [sorted(rng.choice(cfg["batch"], size=n, replace=False).tolist()) for _ in range(steps)]
+
+
+def step_bytes_all(cfg, steps, churn):
+    """Algorithmic bytes of each decode step (all layers), from the host length arithmetic."""
+    lens = list(prefill_lengths(cfg))
+    tb, B, L = tok_bytes(cfg), cfg["batch"], cfg["layers"]
+    out = []
+    for s in range(steps):
+        for r in churn[s]:
+            lens[r] = 0
+        lens = [x + 1 for x in lens]
+        out.append(L * (2 * B * tb + sum(lens) * tb + B * max(lens) * tb))
+    return out
+
+
+def cpu_baseline(cfg, wl, steps, layers):
+    """The oracle (reference CPU path + contiguous materialisation) on `layers` layers x `steps`
+    decode steps, timing the decode steps only; returns (result, layer-0 K/V after the steps)."""
     from kvgen import to_bits
     from oracle.kv_oracle import DenseLayerOracle
 
-    cap = cfg["prefill"] + steps
+    cap = max(prefill_lengths(cfg)) + wl.steps_cap
     total = 0.0
-    parity = None
+    final = None
     for layer in range(layers):
         oracle = DenseLayerOracle(cfg["batch"], cap, cfg["page"])
-        oracle.append(to_bits(k_pre[layer]), to_bits(v_pre[layer]))
-        kd = to_bits(k_dec[:steps, layer])  # [steps, B, H, 1, D]
-        vd = to_bits(v_dec[:steps, layer])
+        for k, v in wl.prefill_inputs(layer):
+            oracle.append(to_bits(k), to_bits(v))
+        kd = to_bits(wl.k_dec[:steps, layer])  # [steps, B, H, 1, D]
+        vd = to_bits(wl.v_dec[:steps, layer])
         t0 = time.perf_counter()
         for s in range(steps):
+            if wl.churn[s]:
+                oracle.release_rows(wl.churn[s])
             ok, ov = oracle.update(kd[s], vd[s])
         total += time.perf_counter() - t0
-        if layer == 0 and gpu_final is not None:
-            parity = bool(np.array_equal(to_bits(gpu_final[0]), ok) and np.array_equal(to_bits(gpu_final[1]), ov))
-    nbytes = sum(step_bytes(cfg, cfg["prefill"] + s + 1) for s in range(steps)) * layers / cfg["layers"]
-    per_step_ms = total / steps * cfg["layers"] / layers * 1e3
-    return {
+        if layer == 0:
+            final = (ok, ov)
+    nbytes = sum(wl.step_bytes[:steps]) * layers / cfg["layers"]
+    result = {
         "value": round(nbytes / total / 1e9, 3),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"{layers} of {cfg['layers']} layers x all {steps} decode steps (append 1 token x "
+        "sample": f"{layers} of {cfg['layers']} layers x the first {steps} decode steps (append 1 token x "
                   f"{cfg['batch']} rows + materialised gather), numpy restatement of the reference "
                   f"kv_cache.py _python_append + current_tensors, one thread; same input bits",
-        "ms_per_step": round(per_step_ms, 3),
+        "ms_per_step": round(total / steps * cfg["layers"] / layers * 1e3, 3),
         "seconds": round(total, 2),
-    }, parity
+    }
+    return result, final
+
+
+class Workload:
+    """Pools, prefill, per-step inputs and churn of one configuration on cuda:0."""
+
+    def __init__(self, cfg, steps, warmup, dev):
+        import numpy as np
+        import torch
+
+        from barqtrain_amd.paged import PagePool
+
+        self.cfg, self.dev = cfg, dev
+        self.dtype = getattr(torch, cfg["dtype"])
+        L, B, H, D, P = cfg["layers"], cfg["batch"], cfg["heads"], cfg["dim"], cfg["page"]
+        self.steps_cap = max(steps, warmup)
+        lens = prefill_lengths(cfg)
+        cap = max(lens) + self.steps_cap
+        mb = math.ceil(cap / P)
+        num_pages = B * mb
+        if "occupancy" in cfg:  # the prefill's pages fill `occupancy` of the pool
+            live = sum(math.ceil(x / P) for x in lens)
+            num_pages = max(math.ceil(live / cfg["occupancy"]), live + B * math.ceil(self.steps_cap / P) + B)
+        order = None
+        if "perm_seed" in cfg:
+            perm = np.random.default_rng(cfg["perm_seed"]).permutation(num_pages).astype(np.int32)
+            order = torch.from_numpy(perm).to(dev)
+        self.order = order
+        self.pools = [PagePool(max_batch=B, max_blocks=mb, page_size=P, kv_heads=H, head_dim=D, dtype=self.dtype,
+                               device=dev, num_pages=num_pages, page_order=order) for _ in range(L)]
+        gen = torch.Generator(device=dev).manual_seed(cfg["seed"])
+        n_in = self.steps_cap
+        self.k_dec = self._normal(gen, (n_in, L, B, 1, H, D)).transpose(3, 4)
+        self.v_dec = self._normal(gen, (n_in, L, B, 1, H, D)).transpose(3, 4)
+        self.churn = churn_rows(cfg, n_in)
+        self.step_bytes = step_bytes_all(cfg, n_in, self.churn)
+
+    def _normal(self, gen, shape):
+        import torch
+
+        return torch.randn(shape, generator=gen, device=self.dev, dtype=torch.float32).to(self.dtype)
+
+    def prefill_inputs(self, layer):
+        """The prefill's (K, V) per append call of `layer`, HF layout [b, H, t, D] (physical
+        [b, t, H, D]); regenerated identically on every call from a per-layer seed."""
+        import torch
+
+        cfg = self.cfg
+        gen = torch.Generator(device=self.dev).manual_seed(cfg["seed"] * 1000 + layer)
+        for b, t, _ in prefill_calls(cfg):
+            shape = (b, t, cfg["heads"], cfg["dim"])
+            yield self._normal(gen, shape).transpose(1, 2), self._normal(gen, shape).transpose(1, 2)
+
+    def prefill(self):
+        for layer, pool in enumerate(self.pools):
+            pool.reset(self.order)
+            for (b, t, gather), (k, v) in zip(prefill_calls(self.cfg), self.prefill_inputs(layer)):
+                if gather:
+                    pool.update(k, v)
+                else:
+                    pool.append(k, v)
 
 
 def main():
@@ -131,7 +255,7 @@ def main():
 
     from barqtrain_amd import _ffi
     from barqtrain_amd.graph import CapturedDecodeStep
-    from barqtrain_amd.paged import SEPARATE_FINALIZE, PagePool
+    from barqtrain_amd.paged import SEPARATE_FINALIZE
 
     backend = _ffi.load_cuda_backend()
     if backend is None:
@@ -139,34 +263,16 @@ def main():
     torch.cuda.set_device(0)
     cfg = CONFIGS[args.config]
     steps = args.steps if args.steps is not None else cfg["decode"]
+    big = args.config >= 3
+    warmup = args.warmup if args.warmup is not None else (2 if big else 16)
+    repeat = args.repeat if args.repeat is not None else (1 if big else 3)
+    mode = args.mode or cfg["mode"]
     if args.pmc_probe:
-        args.warmup, args.mode = 0, "eager"
+        warmup, mode = 0, "eager"
     L, B, H, D, P = cfg["layers"], cfg["batch"], cfg["heads"], cfg["dim"], cfg["page"]
-    dtype = getattr(torch, cfg["dtype"])
-    prefill = cfg["prefill"]
-    cap = prefill + max(steps, args.warmup)
     dev = torch.device("cuda", 0)
-
-    gen = torch.Generator(device=dev).manual_seed(cfg["seed"])
-
-    def normal(shape):
-        return torch.randn(shape, generator=gen, device=dev, dtype=torch.float32).to(dtype)
-
-    # HF physical layout [B, T, H, D], viewed as [B, H, T, D]
-    k_pre = [normal((B, prefill, H, D)).transpose(1, 2) for _ in range(L)]
-    v_pre = [normal((B, prefill, H, D)).transpose(1, 2) for _ in range(L)]
-    n_in = max(steps, args.warmup)
-    k_dec = normal((n_in, L, B, 1, H, D)).transpose(3, 4)
-    v_dec = normal((n_in, L, B, 1, H, D)).transpose(3, 4)
-
-    pools = [PagePool(max_batch=B, max_blocks=math.ceil(cap / P), page_size=P, kv_heads=H, head_dim=D,
-                      dtype=dtype, device=dev) for _ in range(L)]
-
-    def prefill_all():
-        for layer, pool in enumerate(pools):
-            pool.reset()
-            pool.update(k_pre[layer], v_pre[layer])
-
+    wl = Workload(cfg, steps, warmup, dev)
+    pools = wl.pools
     flags = SEPARATE_FINALIZE if args.separate_commit else 0
 
     if args.pmc_probe:
@@ -174,45 +280,54 @@ def main():
         dst = torch.empty_like(src)
         for _ in range(3):
             torch.bitwise_not(src, out=dst)  # calibration: one elementwise kernel, 64 MiB in + 64 MiB out
-        prefill_all()
+        wl.prefill()
         for s in range(steps):
             for layer, pool in enumerate(pools):
-                pool.update(k_dec[s, layer], v_dec[s, layer], flags=flags)
+                if wl.churn[s]:
+                    pool.free_rows(wl.churn[s])
+                pool.update(wl.k_dec[s, layer], wl.v_dec[s, layer], flags=flags)
         torch.cuda.synchronize()
-        total = sum(step_bytes(cfg, prefill + s + 1) for s in range(steps))
+        total = sum(wl.step_bytes[:steps])
         print(json.dumps({"pmc_probe": True, "config": cfg["name"], "steps": steps, "launches": steps * L,
                           "algorithmic_bytes_per_launch": total / (steps * L)}), flush=True)
         return
 
     graph = None
-    if args.mode == "graph":
-        kin = torch.empty((L, B, H, 1, D), dtype=dtype, device=dev)
+    last = {}
+    if mode == "graph":
+        if any(wl.churn[:wl.steps_cap]):
+            raise SystemExit("graph mode replays a fixed step; configurations with row churn run eager")
+        kin = torch.empty((L, B, H, 1, D), dtype=wl.dtype, device=dev)
         vin = torch.empty_like(kin)
         graph = CapturedDecodeStep(pools, B, 1, separate_commit=args.separate_commit, inputs=(kin, vin))
 
         def run_step(s):
-            kin.copy_(k_dec[s])
-            vin.copy_(v_dec[s])
+            kin.copy_(wl.k_dec[s])
+            vin.copy_(wl.v_dec[s])
             graph.replay()
     else:
-        last = {}
-
         def run_step(s):
             for layer, pool in enumerate(pools):
-                out = pool.update(k_dec[s, layer], v_dec[s, layer], flags=flags)
+                if wl.churn[s]:
+                    pool.free_rows(wl.churn[s])
+                out = pool.update(wl.k_dec[s, layer], wl.v_dec[s, layer], flags=flags)
                 if layer == 0:
                     last["out"] = out
 
-    # warmup, then a fresh prefill so the timed steps are exactly ctx 513 -> 512 + steps
-    prefill_all()
-    for s in range(args.warmup):
+    # The prefill (untimed for the decode metric; reported on its own for chunked prefill).
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    wl.prefill()
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    for s in range(warmup):
         run_step(s)
     torch.cuda.synchronize()
 
     def timed(fn):
         best = None
-        for _ in range(max(1, args.repeat)):
-            prefill_all()
+        for _ in range(max(1, repeat)):
+            wl.prefill()
             torch.cuda.synchronize()
             start = torch.cuda.Event(enable_timing=True)
             end = torch.cuda.Event(enable_timing=True)
@@ -234,13 +349,10 @@ def main():
     errors = [p.errors() for p in pools]
     if any(errors):
         raise SystemExit(f"device error bits set: {errors}")
-    if graph is not None:
-        final = (graph.key_out[0][:, :, :prefill + steps], graph.value_out[0][:, :, :prefill + steps])
-    else:
+    if kernel_ms is None:
         kernel_ms = best
-        final = last["out"]
 
-    total_bytes = sum(step_bytes(cfg, prefill + s + 1) for s in range(steps))
+    total_bytes = sum(wl.step_bytes[:steps])
     gbs = total_bytes / (best / 1e3) / 1e9
     launches = steps * L
     avg_launch_us = kernel_ms * 1e3 / launches
@@ -253,28 +365,36 @@ def main():
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
+    lens = prefill_lengths(cfg)
+    kind = cfg["prefill"]
+    workload = (f"{cfg['name']}: {L} layers, batch {B}, {H} KV heads x {D}, {cfg['dtype']}, page {P}; "
+                f"prefill ({kind[0]}, context {min(lens)}..{max(lens)}, untimed), then {steps} decode steps of "
+                f"1-token append + full contiguous gather per layer")
+    if "perm_seed" in cfg:
+        workload += f"; pages handed out in a seeded random permutation (seed {cfg['perm_seed']})"
+    if "occupancy" in cfg:
+        workload += (f"; pool of {pools[0].num_pages} pages per layer ({cfg['occupancy']:.0%} occupied after the "
+                     f"prefill), {cfg['churn'][0]} seeded rows freed and restarted before every step")
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": args.warmup,
+        "warmup": warmup,
         "ms_per_step": round(best / steps, 4),
         "us_per_step": round(best * 1e3 / steps, 2),
         "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": cfg["dtype"].replace("bfloat16", "bf16").replace("float32", "f32"),
+        "dtype": cfg["dtype"].replace("bfloat16", "bf16").replace("float32", "f32").replace("float16", "f16"),
         "data": "synthetic: N(0,1) fp32 rounded to the cache dtype, seeded; inputs resident in HBM",
         "config": {
-            "workload": f"{cfg['name']}: {L} layers, batch {B}, {H} KV heads x {D}, {cfg['dtype']}, page {P}; "
-                        f"prefill {prefill} (untimed), then {steps} decode steps of 1-token append + full "
-                        f"contiguous gather per layer",
-            "mode": args.mode + (" + separate commit" if args.separate_commit else ""),
+            "workload": workload,
+            "mode": mode + (" + separate commit" if args.separate_commit else ""),
             "layers": L, "batch": B, "kv_heads": H, "head_dim": D, "page_size": P,
-            "prefill": prefill, "decode_steps": steps, "parallelism": "single GPU",
+            "prefill": kind[0], "decode_steps": steps, "parallelism": "single GPU",
         },
         "roofline": {
             "bound": "hbm",
@@ -288,10 +408,34 @@ def main():
             "avg_launch_us": round(avg_launch_us, 3),
         },
     }
+    if kind[0] == "chunks":
+        chunk_bytes = sum(L * (2 * B * kind[2] + 2 * B * (c + 1) * kind[2]) * tok_bytes(cfg) for c in range(kind[1]))
+        result["chunked_prefill"] = {"calls_per_layer": kind[1], "seconds_eager": round(prefill_s, 4),
+                                     "gbs": round(chunk_bytes / prefill_s / 1e9, 1),
+                                     "note": f"{kind[1]} x ({kind[2]}-token append + full gather) per layer, "
+                                             f"host-launched, timed with the host clock around the whole phase"}
+
     if not args.no_cpu_baseline:
-        layers = min(args.cpu_layers or L, L)
-        result["cpu_baseline"], parity = cpu_baseline(cfg, k_dec, v_dec, k_pre, v_pre, steps, layers, final)
-        result["parity"] = {"layer0_final_kv_bit_exact_vs_oracle": parity}
+        import numpy as np
+
+        from kvgen import to_bits
+
+        cpu_steps = cfg["cpu_steps"] or steps
+        layers = 1 if cfg["cpu_steps"] else min(args.cpu_layers or L, L)
+        result["cpu_baseline"], want = cpu_baseline(cfg, wl, cpu_steps, layers)
+        # the GPU's layer 0 after the same steps, from a fresh prefill
+        wl.prefill()
+        for s in range(cpu_steps):
+            run_step(s)
+        torch.cuda.synchronize()
+        if graph is not None:
+            seq = wl.pools[0].max_len(B)
+            got = (graph.key_out[0][:, :, :seq], graph.value_out[0][:, :, :seq])
+        else:
+            got = last["out"]
+        result["parity"] = {"layer0_kv_bit_exact_vs_oracle": bool(
+            np.array_equal(to_bits(got[0]), want[0]) and np.array_equal(to_bits(got[1]), want[1])),
+            "after_decode_steps": cpu_steps}
     print(json.dumps(result), flush=True)
 
 
