@@ -1,12 +1,14 @@
 """HIP-graph capture of a decode step: every layer's append + gather replayed with one launch.
 
 The captured kernels read row lengths, block tables and the free-page stack from device memory
-and size their output extent on the device (``SEQ_FROM_DEVICE``), so a graph captured once
-serves every step while the sequences grow: no host work per layer and no host sync per step.
-Inputs are static buffers the caller fills before ``replay`` (in a model, the K/V projection
-writes them); outputs are persistent ``[batch, kv_heads, capacity, head_dim]`` buffers whose
-``[:, :, :seq]`` view is returned.  The host-side length shadow of each pool is advanced by the
-same arithmetic the kernels apply.
+and size their output extent on the device (``SEQ_FROM_DEVICE``), so a captured graph serves
+every step while the sequences grow: no host work per layer and no host sync per step.  A graph's
+grid covers a fixed extent, so the step keeps one graph per *bucket* of extent (captured on first
+use) and replays the smallest bucket that holds the longest row: tiles past the rows' end are
+never launched.  Inputs are static buffers the caller fills before ``replay`` (in a model, the K/V
+projection writes them); outputs are persistent ``[batch, kv_heads, capacity, head_dim]`` buffers
+whose ``[:, :, :seq]`` view is returned.  The host-side length shadow of each pool is advanced by
+the same arithmetic the kernels apply.
 """
 
 from __future__ import annotations
@@ -23,9 +25,12 @@ from barqtrain_amd.paged import (SEPARATE_FINALIZE, SEQ_FROM_DEVICE, PagedKVCapa
 class CapturedDecodeStep:
     def __init__(self, pools: Sequence[PagePool], batch: int, tokens: int = 1,
                  max_length: Optional[int] = None, separate_commit: bool = False,
-                 inputs: Optional[tuple[torch.Tensor, torch.Tensor]] = None):
+                 inputs: Optional[tuple[torch.Tensor, torch.Tensor]] = None,
+                 bucket: Optional[int] = None):
         """`inputs`, if given, are stacked ``[layers, batch, kv_heads, tokens, head_dim]`` K and V
-        buffers (one copy fills every layer); otherwise one buffer per layer is allocated."""
+        buffers (one copy fills every layer); otherwise one buffer per layer is allocated.
+        `bucket` is the extent granularity of the captured graphs (default: a sixteenth of the
+        capacity, at least 64 positions); `bucket=0` captures one graph over the capacity."""
         if not pools or not all(p.on_gpu for p in pools):
             raise ValueError("graph capture needs GPU page pools")
         self.pools = list(pools)
@@ -60,15 +65,26 @@ class CapturedDecodeStep:
         for i, p in enumerate(self.pools):
             p.lens = self._lens[i]
             p.hw = self._hw[i]
-        from barqtrain_amd.paged import _gpu_backend
+        if bucket is None:
+            bucket = max(64, -(-self.capacity // 16))
+        self.bucket = int(bucket) if bucket else self.capacity
+        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
 
-        backend = _gpu_backend()
-        self.graph = torch.cuda.CUDAGraph()
-        # Capture records the launches without running them; no pool state changes here.
-        with torch.cuda.graph(self.graph):
-            for i, pool in enumerate(self.pools):
-                backend.pool_update_(pool.tensors, self.key_in[i], self.value_in[i],
-                                     self.key_out[i], self.value_out[i], self.capacity, self.flags)
+    def _graph(self, extent: int) -> torch.cuda.CUDAGraph:
+        """The graph whose launches cover output positions [0, extent), captured on first use.
+        Capture records the launches without running them: no pool state changes here."""
+        graph = self.graphs.get(extent)
+        if graph is None:
+            from barqtrain_amd.paged import _gpu_backend
+
+            backend = _gpu_backend()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for i, pool in enumerate(self.pools):
+                    backend.pool_update_(pool.tensors, self.key_in[i], self.value_in[i],
+                                         self.key_out[i], self.value_out[i], extent, self.flags)
+            self.graphs[extent] = graph
+        return graph
 
     def replay(self) -> list[tuple[torch.Tensor, torch.Tensor]]:
         """Run one captured step; returns each layer's (K, V) views ``[batch, H, seq, D]``.
@@ -88,7 +104,7 @@ class CapturedDecodeStep:
             if n > p.free_count:
                 raise PagedKVPoolExhausted(
                     f"paged KV page pool exhausted: append needs {int(n)} pages, {p.free_count} free")
-        self.graph.replay()
+        self._graph(min(self.capacity, -(-worst // self.bucket) * self.bucket)).replay()
         lens += T
         np.maximum(hw, lens, out=hw)
         for p, n in zip(self.pools, need):

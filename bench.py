@@ -81,6 +81,8 @@ def parse():
                     help="layers the CPU baseline runs (C1/C2 default: all)")
     ap.add_argument("--repeat", type=int, default=None, help="timed repetitions; the best is reported")
     ap.add_argument("--pmc-probe", action="store_true", help="eager run for rocprof counter passes")
+    ap.add_argument("--bucket", type=int, default=None,
+                    help="graph extent bucket in positions (default: the step's own; 0: one graph over the capacity)")
     return ap.parse_args()
 
 
@@ -299,7 +301,8 @@ def main():
             raise SystemExit("graph mode replays a fixed step; configurations with row churn run eager")
         kin = torch.empty((L, B, H, 1, D), dtype=wl.dtype, device=dev)
         vin = torch.empty_like(kin)
-        graph = CapturedDecodeStep(pools, B, 1, separate_commit=args.separate_commit, inputs=(kin, vin))
+        graph = CapturedDecodeStep(pools, B, 1, separate_commit=args.separate_commit, inputs=(kin, vin),
+                                   bucket=args.bucket)
 
         def run_step(s):
             kin.copy_(wl.k_dec[s])
