@@ -25,6 +25,7 @@ INCLUDE = REPO_ROOT / "include"
 LIB_NAME = "libbarq_kv.so"
 EXT_NAME = "barqtrain_cuda"
 OFFLOAD_ARCH = "gfx950"
+HIP_SOURCES = ("barq_kv.hip", "barq_kv_attention.hip")
 
 # Packed fp32 instructions stay off in every HIP compile (none are needed: the kernels only
 # move bits, but the flag keeps the compiler from forming them).
@@ -75,7 +76,7 @@ def build_library(verbose: bool = False) -> Path:
     out = lib_path()
     tmp = out.with_suffix(".so.tmp")
     cmd = [_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}",
-           str(CSRC / "barq_kv.hip"), "-o", str(tmp)]
+           *[str(CSRC / name) for name in HIP_SOURCES], "-o", str(tmp)]
     _run(cmd, verbose)
     os.replace(tmp, out)
     return out

@@ -1,0 +1,748 @@
+// Decode attention that reads K and V straight from the page pool through the block table
+// (the "attention reads" of a paged cache), for MI355X (gfx950), behind include/barq_kv.h.
+//
+//   out[b, h, i, :] = softmax_t(scale * q[b, h, i, :] . K[b, h / G, t, :]) V[b, h / G, t, :]
+//   over the positions t <= seq_lens[b] - T + i of row b (the row's own length, causal over the
+//   T new query tokens), G = q_heads / kv_heads (grouped-query attention).
+//
+// Work split (flash decoding): one workgroup of 4 waves per (row, kv head, split of
+// `split_tokens` positions); the waves take the split's 64-position chunks in turn.  The G*T
+// query rows of a kv head share every K/V byte a wave loads, so each byte of the row's pages is
+// read once per launch.  Scores come from the bf16/fp16 16x16x32 MFMA (query rows padded to 16,
+// positions as the 16 columns: one MFMA column block is one 16-position run of a page).  P.V
+// runs on the fp32 4x4x1 MFMA in 16 blocks: a lane's 16-byte load of V holds 8 consecutive head
+// dims of one position, and element e of it is the lane's B operand of the e-th MFMA, so V is
+// consumed in the layout it is stored in (no transpose, no LDS staging of V) and the
+// probabilities stay fp32.  A wave keeps a running max / sum per query row (online softmax,
+// base-2 exponent) and the workgroup merges its waves in LDS.  A row with one split is written
+// by its workgroup; a row with more splits gets one partial record per split, merged by a
+// second launch (the launch boundary makes the records visible: no fences, no counters).
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "barq_kv.h"
+#include "fastdiv.h"
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kHeadDim = 128;              // the one head size this kernel is built for
+constexpr int kSteps = kHeadDim / 32;      // k-steps of the score MFMA
+constexpr int kBlock = 16;                 // positions per score MFMA
+constexpr int kChunkBlocks = 2;            // blocks per softmax update
+constexpr int kChunk = kBlock * kChunkBlocks;
+constexpr int kMaxRows = 16;               // query rows (G * T) one workgroup serves
+constexpr int kWaves = 4;                  // waves per workgroup
+constexpr int kThreads = kWaves * kWave;
+constexpr int kSplitQuantum = kChunk * kWaves;  // positions of a split: a multiple of this
+constexpr int kMaxTable = 1024;            // block-table entries a split stages in LDS
+constexpr int kMaxSplits = 256;            // splits per row
+constexpr int kTargetWorkgroups = 1024;    // the automatic split aims at about this many
+constexpr int kMaxSplitTokens = 1 << 20;
+
+enum : int { kBF16 = 0, kF16 = 1 };
+
+struct AttnArgs {
+  const char* kpages;
+  const char* vpages;
+  const int32_t* block_table;
+  const int32_t* seq_lens;
+  int32_t* errors;
+  int64_t page_bytes;   // bytes between pages
+  int64_t q_sb, q_sh, q_st;  // query strides, bytes
+  int64_t o_sb, o_sh, o_st;  // output strides, bytes
+  const char* q;
+  char* out;
+  float* part;          // [batch * kv_heads, max_splits] records of record_floats(rows)
+  FastDiv page_div;
+  int32_t row_bytes;    // bytes between positions of a page
+  int32_t head_bytes;   // bytes of one head's run (head_dim elements)
+  int32_t num_pages;
+  int32_t max_blocks;
+  int32_t page_size;
+  int32_t kv_heads;
+  int32_t group;
+  int32_t tokens;
+  int32_t rows;
+  int32_t split_tokens;
+  int32_t max_splits;
+  int32_t capacity;     // max_blocks * page_size
+  float scale_log2;     // softmax scale * log2(e)
+};
+
+// A split's partial: rows x head_dim unnormalised sums, then the rows' running maxima and sums,
+// padded to whole 16-byte vectors.
+__host__ __device__ constexpr int64_t record_floats(int64_t rows) {
+  return rows * kHeadDim + (2 * rows + 3) / 4 * 4;
+}
+
+template <int E>
+__device__ __forceinline__ f32x4 mfma_qk(const u32x4 a, const u32x4 b, f32x4 c) {
+  if constexpr (E == kBF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// The 8 elements of a 16-byte vector as fp32 (exact for both 2-byte types).
+template <int E>
+__device__ __forceinline__ void widen8(const u32x4 w, float (&f)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (E == kBF16) {
+      f[2 * i] = __uint_as_float(w[i] << 16);
+      f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    } else {
+      f[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xffffu));
+      f[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
+    }
+  }
+}
+
+template <int E>
+__device__ __forceinline__ uint16_t narrow(float f) {
+  if constexpr (E == kBF16) {
+    // round to nearest even; NaN stays a quiet NaN
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+  } else {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+}
+
+// DPP lane moves within each 16-lane row (quad_perm [1,0,3,2], [2,3,0,1], half-row mirror,
+// row mirror): four steps combine all 16 lanes of a row.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  return fmaxf(v, dpp<0x140>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  return v + dpp<0x140>(v);
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__device__ __forceinline__ u32x4 ld_page(const char* p) {
+  return __builtin_nontemporal_load((const u32x4*)p);
+}
+
+template <typename OutT, int E>
+__device__ __forceinline__ void store_out4(char* p, const f32x4 v) {
+  if constexpr (sizeof(OutT) == 4) {
+    *(f32x4*)p = v;
+  } else {
+    uint2 w;
+    w.x = (uint32_t)narrow<E>(v[0]) | ((uint32_t)narrow<E>(v[1]) << 16);
+    w.y = (uint32_t)narrow<E>(v[2]) | ((uint32_t)narrow<E>(v[3]) << 16);
+    *(uint2*)p = w;
+  }
+}
+
+// Row b's visible length as the launch covers it, and its number of splits.
+__device__ __forceinline__ int row_length(const AttnArgs& a, int b, bool report) {
+  int len = a.seq_lens[b];
+  if (len > a.capacity) {
+    if (report) atomicOr(a.errors, BARQ_KV_ERRBIT_CAPACITY);
+    len = a.capacity;
+  }
+  const int cap = a.max_splits * a.split_tokens;
+  if (len > cap) {
+    if (report) atomicOr(a.errors, BARQ_KV_ERRBIT_ATTN_SHORT);
+    len = cap;
+  }
+  return len < 0 ? 0 : len;
+}
+
+__device__ __forceinline__ char* out_row(const AttnArgs& a, int b, int kvh, int row) {
+  const int hl = row / a.tokens;
+  const int i = row - hl * a.tokens;
+  return a.out + (int64_t)b * a.o_sb + (int64_t)(kvh * a.group + hl) * a.o_sh + (int64_t)i * a.o_st;
+}
+
+// Shared memory of a split workgroup: the split's block-table entries, then the waves'
+// probability staging (main loop) or the waves' results (workgroup merge).
+struct SplitSmem {
+  int32_t table[kMaxTable];
+  union {
+    float p[kWaves][kChunk][kMaxRows];
+    struct {
+      float acc[kWaves][kMaxRows][kHeadDim];
+      float m[kWaves][kMaxRows];
+      float l[kWaves][kMaxRows];
+    } wg;
+  } u;
+};
+
+// K and V of one chunk for this lane (page_size a multiple of 16: one page per 16-position
+// block, its base a scalar).  K: lane (g, n16) holds dims 32 * step + 8 * g .. +7 of position
+// 16j + n16; V: dims 8 * n16 .. +7 of position 16j + 4s + g.  PRED: the chunk ends past the
+// row, so positions >= len load nothing and read as zero.
+template <bool PRED>
+__device__ __forceinline__ void load_chunk_uniform(const AttnArgs& a, const SplitSmem& sm, int blk0,
+                                                   const char* kbase, const char* vbase, int tc,
+                                                   int len, int klane, int vlane, int n16, int g,
+                                                   u32x4 (&kv)[kChunkBlocks][kSteps],
+                                                   u32x4 (&vv)[kChunkBlocks][4]) {
+#pragma unroll
+  for (int j = 0; j < kChunkBlocks; ++j) {
+    const int tb = tc + kBlock * j;
+    if (!PRED || tb < len) {
+      const uint32_t blk = a.page_div.div((uint32_t)tb);
+      const int page = __builtin_amdgcn_readfirstlane(sm.table[blk - blk0]);
+      const int64_t base = (int64_t)page * a.page_bytes +
+                           (int64_t)(tb - (int)(blk * (uint32_t)a.page_size)) * a.row_bytes;
+      const char* kp = kbase + base + klane;
+      const char* vp = vbase + base + vlane;
+      if (!PRED || tb + n16 < len) {
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) kv[j][st] = ld_page(kp + 64 * st);
+      } else {
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) kv[j][st] = u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        vv[j][s] = (!PRED || tb + 4 * s + g < len) ? ld_page(vp + 4 * s * a.row_bytes) : u32x4{0, 0, 0, 0};
+    } else {
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st) kv[j][st] = u32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) vv[j][s] = u32x4{0, 0, 0, 0};
+    }
+  }
+}
+
+// The same for any page size: each lane finds the page of each of its positions.
+__device__ __forceinline__ void load_chunk_general(const AttnArgs& a, const SplitSmem& sm, int blk0,
+                                                   const char* kbase, const char* vbase, int tc,
+                                                   int len, int n16, int g,
+                                                   u32x4 (&kv)[kChunkBlocks][kSteps],
+                                                   u32x4 (&vv)[kChunkBlocks][4]) {
+  auto offset = [&](int t) -> int64_t {
+    const uint32_t blk = a.page_div.div((uint32_t)t);
+    return (int64_t)sm.table[blk - blk0] * a.page_bytes +
+           (int64_t)(t - (int)(blk * (uint32_t)a.page_size)) * a.row_bytes;
+  };
+#pragma unroll
+  for (int j = 0; j < kChunkBlocks; ++j) {
+    const int tb = tc + kBlock * j;
+    const int tk = tb + n16;
+    if (tk < len) {
+      const char* kp = kbase + offset(tk) + 16 * g;
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st) kv[j][st] = ld_page(kp + 64 * st);
+    } else {
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st) kv[j][st] = u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int tv = tb + 4 * s + g;
+      vv[j][s] = tv < len ? ld_page(vbase + offset(tv) + 16 * n16) : u32x4{0, 0, 0, 0};
+    }
+  }
+}
+
+// One workgroup per (split, kv head, row).  UNIFORM: page_size is a multiple of 16.
+// R: groups of 4 query rows (rows <= 4 * R).
+template <int E, int R, bool UNIFORM, typename OutT>
+__global__ __launch_bounds__(kThreads) void attention_split_kernel(const AttnArgs a) {
+  __shared__ SplitSmem sm;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int n16 = lane & 15;
+  const int g = lane >> 4;
+  const int split = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int pair = b * a.kv_heads + kvh;
+
+  const int len = row_length(a, b, split == 0 && kvh == 0 && tid == 0);
+  const int nsplit = len == 0 ? 1 : (len + a.split_tokens - 1) / a.split_tokens;
+  if (split >= nsplit) return;
+
+  const int M = a.rows;
+  const int T = a.tokens;
+  const int t_begin = split * a.split_tokens;
+  const int t_end = min(len, t_begin + a.split_tokens);
+
+  // The split's block-table entries, checked once: an entry naming no page is recorded and
+  // read as page 0, so no access leaves the pool.
+  const int blk0 = (int)a.page_div.div((uint32_t)t_begin);
+  const int nblk = t_end > t_begin ? (int)a.page_div.div((uint32_t)(t_end - 1)) - blk0 + 1 : 0;
+  {
+    const int32_t* bt = a.block_table + (int64_t)b * a.max_blocks + blk0;
+    for (int i = tid; i < nblk; i += kThreads) {
+      int page = bt[i];
+      if ((uint32_t)page >= (uint32_t)a.num_pages) {
+        atomicOr(a.errors, BARQ_KV_ERRBIT_BAD_INDEX);
+        page = 0;
+      }
+      sm.table[i] = page;
+    }
+  }
+
+  // Query rows in the A layout of the score MFMA: lane (row n16, k-group g) holds dims
+  // 32 * step + 8 * g .. +7 of row n16 (zero for padding rows).
+  u32x4 qv[kSteps];
+  if (n16 < M) {
+    const char* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(kvh * a.group + n16 / T) * a.q_sh +
+                     (int64_t)(n16 % T) * a.q_st + 16 * g;
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) qv[st] = *(const u32x4*)(qp + 64 * st);
+  } else {
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) qv[st] = u32x4{0, 0, 0, 0};
+  }
+  __syncthreads();
+
+  const char* kbase = a.kpages + (int64_t)kvh * a.head_bytes;
+  const char* vbase = a.vpages + (int64_t)kvh * a.head_bytes;
+  const int klane = n16 * a.row_bytes + 16 * g;
+  const int vlane = g * a.row_bytes + 16 * n16;
+
+  float m_run[4], l_part[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    m_run[r] = -INFINITY;
+    l_part[r] = 0.f;
+  }
+  f32x4 acc[R][8];
+#pragma unroll
+  for (int r2 = 0; r2 < R; ++r2)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[r2][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  float (*lp)[kMaxRows] = sm.u.p[wave];
+
+  auto load = [&](int tc, u32x4 (&kv)[kChunkBlocks][kSteps], u32x4 (&vv)[kChunkBlocks][4]) {
+    if constexpr (UNIFORM) {
+      if (tc + kChunk <= len)
+        load_chunk_uniform<false>(a, sm, blk0, kbase, vbase, tc, len, klane, vlane, n16, g, kv, vv);
+      else
+        load_chunk_uniform<true>(a, sm, blk0, kbase, vbase, tc, len, klane, vlane, n16, g, kv, vv);
+    } else {
+      load_chunk_general(a, sm, blk0, kbase, vbase, tc, len, n16, g, kv, vv);
+    }
+  };
+
+  auto compute = [&](int tc, const u32x4 (&kv)[kChunkBlocks][kSteps], const u32x4 (&vv)[kChunkBlocks][4]) {
+    // Scores: lane (g, n16), register r = row 4g + r, position tc + 16j + n16; log2 units.
+    float x[kChunkBlocks][4];
+#pragma unroll
+    for (int j = 0; j < kChunkBlocks; ++j) {
+      f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st) sc = mfma_qk<E>(qv[st], kv[j][st], sc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[j][r] = sc[r] * a.scale_log2;
+    }
+    // Every position of the chunk visible to every row?  Else mask (position > len - T + i).
+    if (tc + kChunk + T - 1 > len) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 4 * g + r;
+        const int limit = len - T + row % T;
+#pragma unroll
+        for (int j = 0; j < kChunkBlocks; ++j)
+          if (tc + kBlock * j + n16 > limit) x[j][r] = -INFINITY;
+      }
+    }
+
+    bool rescale = false;
+    float alpha[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float mx = x[0][r];
+#pragma unroll
+      for (int j = 1; j < kChunkBlocks; ++j) mx = fmaxf(mx, x[j][r]);
+      mx = row16_max(mx);
+      const float mnew = fmaxf(m_run[r], mx);
+      const float mu = mnew == -INFINITY ? 0.f : mnew;
+      alpha[r] = __builtin_amdgcn_exp2f(m_run[r] - mu);
+      rescale |= mnew != m_run[r];
+      float ps = 0.f;
+#pragma unroll
+      for (int j = 0; j < kChunkBlocks; ++j) {
+        x[j][r] = __builtin_amdgcn_exp2f(x[j][r] - mu);
+        ps += x[j][r];
+      }
+      l_part[r] = l_part[r] * alpha[r] + ps;
+      m_run[r] = mnew;
+    }
+    if (g < R) {
+#pragma unroll
+      for (int j = 0; j < kChunkBlocks; ++j)
+        *(f32x4*)&lp[kBlock * j + n16][4 * g] = f32x4{x[j][0], x[j][1], x[j][2], x[j][3]};
+    }
+    if (__builtin_amdgcn_ballot_w64(rescale)) {
+#pragma unroll
+      for (int r2 = 0; r2 < R; ++r2)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const float al = lane_value(alpha[m], 16 * r2);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[r2][e][m] *= al;
+        }
+    }
+
+    // P.V: lane 4b' + n of the 4x4x1 MFMA block b' takes position 4s + g of block j.
+#pragma unroll
+    for (int j = 0; j < kChunkBlocks; ++j) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        float vf[8];
+        widen8<E>(vv[j][s], vf);
+#pragma unroll
+        for (int r2 = 0; r2 < R; ++r2) {
+          const float pa = lp[kBlock * j + 4 * s + g][4 * r2 + (lane & 3)];
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            acc[r2][e] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vf[e], acc[r2][e], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  // Two register buffers: the next chunk's loads are in flight while this one is computed.
+  constexpr int kStride = kChunk * kWaves;
+  u32x4 ka[kChunkBlocks][kSteps], va[kChunkBlocks][4];
+  u32x4 kb[kChunkBlocks][kSteps], vb[kChunkBlocks][4];
+  int tc = t_begin + kChunk * wave;
+  if (tc < t_end) load(tc, ka, va);
+  while (tc < t_end) {
+    const int t1 = tc + kStride;
+    if (t1 < t_end) load(t1, kb, vb);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(tc, ka, va);
+    if (t1 >= t_end) break;
+    const int t2 = t1 + kStride;
+    if (t2 < t_end) load(t2, ka, va);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(t1, kb, vb);
+    tc = t2;
+  }
+
+  // Row sums across the 16 lanes of each row group; P.V partials across the 4 position slots.
+#pragma unroll
+  for (int r = 0; r < 4; ++r) l_part[r] = row16_sum(l_part[r]);
+#pragma unroll
+  for (int r2 = 0; r2 < R; ++r2)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        float v = acc[r2][e][m];
+        v += __shfl_xor(v, 16, kWave);
+        v += __shfl_xor(v, 32, kWave);
+        acc[r2][e][m] = v;
+      }
+  // Lanes 0..15 now hold dims 8 * lane .. +7 of every row; lanes 16g .. 16g+15 hold the
+  // maxima and sums of rows 4g .. 4g+3.
+  __syncthreads();  // every wave is past its loop: the staging area becomes the merge area
+#pragma unroll
+  for (int r2 = 0; r2 < R; ++r2)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int row = 4 * r2 + m;
+      if (row < M && lane < 16) {
+        float* dst = &sm.u.wg.acc[wave][row][8 * lane];
+        *(f32x4*)dst = f32x4{acc[r2][0][m], acc[r2][1][m], acc[r2][2][m], acc[r2][3][m]};
+        *(f32x4*)(dst + 4) = f32x4{acc[r2][4][m], acc[r2][5][m], acc[r2][6][m], acc[r2][7][m]};
+      }
+    }
+  if (n16 == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 4 * g + r;
+      if (row < M) {
+        sm.u.wg.m[wave][row] = m_run[r];
+        sm.u.wg.l[wave][row] = l_part[r];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Workgroup merge: thread -> 4 consecutive dims of one row; the result goes to the output
+  // (one split) or to this split's record.
+  const int64_t rec = record_floats(M);
+  float* pr = a.part + ((int64_t)pair * a.max_splits + split) * rec;
+  for (int q = tid; q < M * (kHeadDim / 4); q += kThreads) {
+    const int row = q / (kHeadDim / 4);
+    const int d4 = (q % (kHeadDim / 4)) * 4;
+    float mstar = sm.u.wg.m[0][row];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) mstar = fmaxf(mstar, sm.u.wg.m[w][row]);
+    const float mu = mstar == -INFINITY ? 0.f : mstar;
+    float lsum = 0.f;
+    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float wt = __builtin_amdgcn_exp2f(sm.u.wg.m[w][row] - mu);
+      lsum += wt * sm.u.wg.l[w][row];
+      o += wt * *(const f32x4*)&sm.u.wg.acc[w][row][d4];
+    }
+    if (nsplit == 1) {
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      store_out4<OutT, E>(out_row(a, b, kvh, row) + (int64_t)d4 * sizeof(OutT), o * inv);
+    } else {
+      *(f32x4*)(pr + (int64_t)row * kHeadDim + d4) = o;
+      if (d4 == 0) {
+        pr[(int64_t)M * kHeadDim + row] = mstar;
+        pr[(int64_t)M * kHeadDim + M + row] = lsum;
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const float u = __shfl_xor(v, o, kWave);
+    v = is_max ? fmaxf(v, u) : v + u;
+  }
+  const int wave = threadIdx.x / kWave;
+  __syncthreads();
+  if ((threadIdx.x & (kWave - 1)) == 0) red[wave] = v;
+  __syncthreads();
+  v = red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) v = is_max ? fmaxf(v, red[w]) : v + red[w];
+  return v;
+}
+
+// Merge of one query row's split records: one workgroup per (row, kv head, batch row).
+template <int E, typename OutT>
+__global__ __launch_bounds__(kThreads) void attention_merge_kernel(const AttnArgs a) {
+  __shared__ float w[kMaxSplits];
+  __shared__ float red[kWaves];
+  __shared__ f32x4 part[kThreads];
+
+  const int tid = threadIdx.x;
+  const int row = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int len = row_length(a, b, false);
+  const int nsplit = len == 0 ? 1 : (len + a.split_tokens - 1) / a.split_tokens;
+  if (nsplit <= 1) return;  // written by its split workgroup
+
+  const int M = a.rows;
+  const int64_t rec = record_floats(M);
+  const float* base = a.part + (int64_t)(b * a.kv_heads + kvh) * a.max_splits * rec;
+  const float* ml = base + (int64_t)M * kHeadDim;
+
+  float mx = -INFINITY;
+  for (int s = tid; s < nsplit; s += kThreads) mx = fmaxf(mx, ml[s * rec + row]);
+  mx = block_reduce(mx, red, true);
+  const float mu = mx == -INFINITY ? 0.f : mx;
+  float ls = 0.f;
+  for (int s = tid; s < nsplit; s += kThreads) {
+    const float wt = __builtin_amdgcn_exp2f(ml[s * rec + row] - mu);
+    w[s] = wt;
+    ls += wt * ml[s * rec + M + row];
+  }
+  ls = block_reduce(ls, red, false);  // its barriers also publish w[]
+
+  // Thread -> (4 dims, one of 8 residue classes of splits); the classes are summed in LDS.
+  constexpr int kQuads = kHeadDim / 4;
+  constexpr int kClasses = kThreads / kQuads;
+  const int quad = tid % kQuads;
+  const int cls = tid / kQuads;
+  const float* src = base + (int64_t)row * kHeadDim + 4 * quad;
+  f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+  for (int s = cls; s < nsplit; s += kClasses) o += w[s] * *(const f32x4*)(src + s * rec);
+  part[tid] = o;
+  __syncthreads();
+  if (tid < kQuads) {
+#pragma unroll
+    for (int c = 1; c < kClasses; ++c) o += part[tid + c * kQuads];
+    const float inv = ls > 0.f ? 1.f / ls : 0.f;
+    store_out4<OutT, E>(out_row(a, b, kvh, row) + (int64_t)(4 * quad) * sizeof(OutT), o * inv);
+  }
+}
+
+template <int E, int R, bool U>
+hipError_t launch_split(const AttnArgs& a, bool out_f32, dim3 grid, hipStream_t stream) {
+  if (out_f32)
+    hipLaunchKernelGGL((attention_split_kernel<E, R, U, float>), grid, dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((attention_split_kernel<E, R, U, uint16_t>), grid, dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+template <int E>
+hipError_t launch_dtype(const AttnArgs& a, bool uniform, bool out_f32, dim3 grid, hipStream_t stream) {
+  const int groups = (a.rows + 3) / 4;
+  hipError_t err;
+  if (uniform) {
+    err = groups == 1   ? launch_split<E, 1, true>(a, out_f32, grid, stream)
+          : groups == 2 ? launch_split<E, 2, true>(a, out_f32, grid, stream)
+                        : launch_split<E, 4, true>(a, out_f32, grid, stream);
+  } else {
+    err = groups == 1   ? launch_split<E, 1, false>(a, out_f32, grid, stream)
+          : groups == 2 ? launch_split<E, 2, false>(a, out_f32, grid, stream)
+                        : launch_split<E, 4, false>(a, out_f32, grid, stream);
+  }
+  if (err != hipSuccess || a.max_splits == 1) return err;
+  const dim3 mgrid((unsigned)a.rows, grid.y, grid.z);
+  if (out_f32)
+    hipLaunchKernelGGL((attention_merge_kernel<E, float>), mgrid, dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((attention_merge_kernel<E, uint16_t>), mgrid, dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+struct AttnPlan {
+  int64_t split_tokens;
+  int64_t max_splits;
+  int64_t rows;
+  int64_t bytes;
+};
+
+// Validates the geometry and sizes the launch.  max_seq bounds every row's length (0: the
+// pool's capacity); split_tokens 0 picks a split giving about kTargetWorkgroups workgroups at
+// that bound.
+int plan_attention(const barq_kv_pool* pool, int64_t batch, int64_t q_heads, int64_t tokens,
+                   int64_t max_seq, int64_t split_tokens, AttnPlan* plan) {
+  if (!pool || pool->elem_bytes != 2 || pool->head_dim != kHeadDim || pool->kv_heads <= 0 ||
+      pool->page_size <= 0 || pool->max_blocks <= 0 || pool->num_pages <= 0 ||
+      pool->num_pages > INT32_MAX || pool->max_batch <= 0)
+    return BARQ_KV_ERR_INVALID;
+  if (batch < 0 || batch > pool->max_batch || tokens <= 0 || q_heads <= 0 ||
+      q_heads % pool->kv_heads != 0)
+    return BARQ_KV_ERR_INVALID;
+  const int64_t rows = (q_heads / pool->kv_heads) * tokens;
+  if (rows > kMaxRows) return BARQ_KV_ERR_INVALID;
+  const int64_t capacity = pool->max_blocks * pool->page_size;
+  const int64_t row_bytes = pool->kv_heads * kHeadDim * 2;
+  // Lane offsets within a page are 32-bit; grid dimensions are 16-bit.
+  if (capacity > INT32_MAX / 2 || row_bytes * pool->page_size > INT32_MAX / 2 ||
+      pool->kv_heads > 65535 || pool->max_batch > 65535)
+    return BARQ_KV_ERR_INVALID;
+  if (max_seq <= 0 || max_seq > capacity) max_seq = capacity;
+  if (split_tokens < 0 || split_tokens > kMaxSplitTokens) return BARQ_KV_ERR_INVALID;
+  if (split_tokens == 0) {
+    const int64_t pairs = std::max<int64_t>(1, batch * pool->kv_heads);
+    split_tokens = (pairs * max_seq + kTargetWorkgroups - 1) / kTargetWorkgroups;
+  }
+  // Whole quanta; at most kMaxSplits splits per row; the split's blocks fit the LDS table.
+  split_tokens = std::max<int64_t>(split_tokens, (max_seq + kMaxSplits - 1) / kMaxSplits);
+  split_tokens = (split_tokens + kSplitQuantum - 1) / kSplitQuantum * kSplitQuantum;
+  const int64_t table_limit = (kMaxTable - 2) * pool->page_size / kSplitQuantum * kSplitQuantum;
+  if (split_tokens > table_limit) {
+    if (table_limit < kSplitQuantum || (max_seq + table_limit - 1) / table_limit > kMaxSplits)
+      return BARQ_KV_ERR_INVALID;
+    split_tokens = table_limit;
+  }
+  plan->split_tokens = split_tokens;
+  plan->max_splits = (max_seq + split_tokens - 1) / split_tokens;
+  plan->rows = rows;
+  plan->bytes = plan->max_splits > 1 ? batch * pool->kv_heads * plan->max_splits * record_floats(rows) * 4 : 0;
+  return BARQ_KV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t barq_kv_attention_workspace_bytes(const barq_kv_pool* pool, int64_t batch,
+                                          int64_t q_heads, int64_t tokens, int64_t max_seq,
+                                          int64_t split_tokens) {
+  AttnPlan plan;
+  if (plan_attention(pool, batch, q_heads, tokens, max_seq, split_tokens, &plan) != BARQ_KV_OK)
+    return -1;
+  return plan.bytes;
+}
+
+int barq_kv_decode_attention(const barq_kv_pool* pool, const void* query, int64_t batch,
+                             int64_t q_heads, int64_t tokens, int64_t q_stride_b,
+                             int64_t q_stride_h, int64_t q_stride_t, void* out,
+                             int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_t,
+                             float scale, int64_t max_seq, int64_t split_tokens, int64_t flags,
+                             void* workspace, int64_t workspace_bytes, void* stream) {
+  AttnPlan plan;
+  const int rc = plan_attention(pool, batch, q_heads, tokens, max_seq, split_tokens, &plan);
+  if (rc != BARQ_KV_OK) return rc;
+  if (flags & ~(int64_t)(BARQ_KV_ATTN_FP16 | BARQ_KV_ATTN_OUT_F32)) return BARQ_KV_ERR_INVALID;
+  if (batch == 0) return BARQ_KV_OK;
+  const int64_t out_elem = (flags & BARQ_KV_ATTN_OUT_F32) ? 4 : 2;
+  if (!query || !out || (plan.bytes > 0 && !workspace) || workspace_bytes < plan.bytes ||
+      !pool->key_pages || !pool->value_pages || !pool->block_table || !pool->seq_lens || !pool->ctrl)
+    return BARQ_KV_ERR_INVALID;
+  // 16-byte query rows and 4-element output runs must be aligned for the vector accesses.
+  const int64_t qs[3] = {q_stride_b, q_stride_h, q_stride_t};
+  const int64_t os[3] = {out_stride_b, out_stride_h, out_stride_t};
+  for (int i = 0; i < 3; ++i) {
+    if (qs[i] < 0 || qs[i] % 8 != 0 || os[i] < 0 || os[i] % 8 != 0) return BARQ_KV_ERR_INVALID;
+  }
+  if (((uintptr_t)query | (uintptr_t)pool->key_pages | (uintptr_t)pool->value_pages) % 16 != 0 ||
+      (uintptr_t)out % (out_elem * 4) != 0 || (uintptr_t)workspace % 16 != 0)
+    return BARQ_KV_ERR_INVALID;
+  if (plan.max_splits > 65535) return BARQ_KV_ERR_INVALID;
+
+  AttnArgs a;
+  a.kpages = (const char*)pool->key_pages;
+  a.vpages = (const char*)pool->value_pages;
+  a.block_table = pool->block_table;
+  a.seq_lens = pool->seq_lens;
+  a.errors = pool->ctrl + BARQ_KV_CTRL_ERRORS;
+  a.head_bytes = (int32_t)(pool->head_dim * 2);
+  a.row_bytes = (int32_t)(pool->kv_heads * a.head_bytes);
+  a.page_bytes = pool->page_size * (int64_t)a.row_bytes;
+  a.q_sb = q_stride_b * 2;
+  a.q_sh = q_stride_h * 2;
+  a.q_st = q_stride_t * 2;
+  a.o_sb = out_stride_b * out_elem;
+  a.o_sh = out_stride_h * out_elem;
+  a.o_st = out_stride_t * out_elem;
+  a.q = (const char*)query;
+  a.out = (char*)out;
+  a.part = (float*)workspace;
+  a.page_div = FastDiv::make((uint32_t)pool->page_size);
+  a.num_pages = (int32_t)pool->num_pages;
+  a.max_blocks = (int32_t)pool->max_blocks;
+  a.page_size = (int32_t)pool->page_size;
+  a.kv_heads = (int32_t)pool->kv_heads;
+  a.group = (int32_t)(q_heads / pool->kv_heads);
+  a.tokens = (int32_t)tokens;
+  a.rows = (int32_t)plan.rows;
+  a.split_tokens = (int32_t)plan.split_tokens;
+  a.max_splits = (int32_t)plan.max_splits;
+  a.capacity = (int32_t)(pool->max_blocks * pool->page_size);
+  a.scale_log2 = scale * 1.4426950408889634f;
+
+  const dim3 grid((unsigned)plan.max_splits, (unsigned)pool->kv_heads, (unsigned)batch);
+  const bool uniform = pool->page_size % kBlock == 0;
+  const bool out_f32 = (flags & BARQ_KV_ATTN_OUT_F32) != 0;
+  const hipError_t err = (flags & BARQ_KV_ATTN_FP16)
+                             ? launch_dtype<kF16>(a, uniform, out_f32, grid, (hipStream_t)stream)
+                             : launch_dtype<kBF16>(a, uniform, out_f32, grid, (hipStream_t)stream);
+  return err == hipSuccess ? BARQ_KV_OK : BARQ_KV_ERR_LAUNCH;
+}
+
+}  // extern "C"

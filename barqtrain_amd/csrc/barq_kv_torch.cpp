@@ -232,6 +232,45 @@ void pool_copy_rows_(std::vector<at::Tensor> src, std::vector<at::Tensor> dst, a
                "pool_copy_rows_");
 }
 
+int64_t attention_workspace_bytes(std::vector<at::Tensor> pool, int64_t batch, int64_t q_heads,
+                                  int64_t tokens, int64_t max_seq, int64_t split_tokens) {
+  barq_kv_pool p = pool_from(pool);
+  return barq_kv_attention_workspace_bytes(&p, batch, q_heads, tokens, max_seq, split_tokens);
+}
+
+// query [batch, q_heads, tokens, head_dim] in the pool's dtype; out of the same shape, in the
+// pool's dtype or float32; workspace a zero-filled uint8 buffer (see
+// barq_kv_decode_attention).
+void pool_decode_attention(std::vector<at::Tensor> pool, at::Tensor query, at::Tensor out,
+                           double scale, int64_t max_seq, int64_t split_tokens,
+                           at::Tensor workspace) {
+  barq_kv_pool p = pool_from(pool);
+  const at::Tensor& pages = pool[0];
+  TORCH_CHECK(pages.scalar_type() == at::kBFloat16 || pages.scalar_type() == at::kHalf,
+              "paged decode attention needs a bfloat16 or float16 cache");
+  TORCH_CHECK(query.is_cuda() && out.is_cuda() && workspace.is_cuda() &&
+                  query.get_device() == pages.get_device() && out.get_device() == pages.get_device() &&
+                  workspace.get_device() == pages.get_device(),
+              "query, out and workspace must be on the cache device");
+  TORCH_CHECK(query.dim() == 4 && query.scalar_type() == pages.scalar_type() && query.stride(3) == 1,
+              "query must be [batch, q_heads, tokens, head_dim] in the cache dtype, head_dim contiguous");
+  TORCH_CHECK(out.dim() == 4 && out.sizes() == query.sizes() && out.stride(3) == 1 &&
+                  (out.scalar_type() == pages.scalar_type() || out.scalar_type() == at::kFloat),
+              "out must match the query's shape, in the cache dtype or float32, head_dim contiguous");
+  TORCH_CHECK(workspace.is_contiguous() && workspace.scalar_type() == at::kByte,
+              "workspace must be a contiguous uint8 buffer");
+  int64_t flags = 0;
+  if (pages.scalar_type() == at::kHalf) flags |= BARQ_KV_ATTN_FP16;
+  if (out.scalar_type() == at::kFloat) flags |= BARQ_KV_ATTN_OUT_F32;
+  c10::DeviceGuard guard(pages.device());
+  const int rc = barq_kv_decode_attention(
+      &p, query.data_ptr(), query.size(0), query.size(1), query.size(2), query.stride(0),
+      query.stride(1), query.stride(2), out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
+      (float)scale, max_seq, split_tokens, flags, workspace.data_ptr(), workspace.numel(),
+      current_stream(pages));
+  check_status(rc, "pool_decode_attention");
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -245,6 +284,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("pool_crop_", &pool_crop_, "Clamp row lengths of a page pool");
   m.def("pool_free_rows_", &pool_free_rows_, "Return rows' pages to the free stack");
   m.def("pool_copy_rows_", &pool_copy_rows_, "Build rows of a fresh pool as copies of source rows");
+  m.def("attention_workspace_bytes", &attention_workspace_bytes,
+        "Workspace bytes of a decode-attention launch (-1: arguments rejected)");
+  m.def("pool_decode_attention", &pool_decode_attention,
+        "Decode attention reading K/V from a page pool through its block table");
   m.def("version", []() { return std::string(barq_kv_version()); });
   m.attr("CTRL_WORDS") = BARQ_KV_CTRL_WORDS;
   m.attr("SEQ_FROM_DEVICE") = BARQ_KV_SEQ_FROM_DEVICE;

@@ -36,6 +36,7 @@ ERRBIT_POOL_EXHAUSTED = 1
 ERRBIT_CAPACITY = 2
 ERRBIT_BAD_INDEX = 4
 ERRBIT_OUT_SHORT = 8
+ERRBIT_ATTN_SHORT = 16
 SEQ_FROM_DEVICE = 1
 SEPARATE_FINALIZE = 2
 
@@ -294,6 +295,60 @@ class PagePool:
             dst.free_count = num_pages - need
         return dst
 
+    def attend(self, query: torch.Tensor, scale: Optional[float] = None, *,
+               out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
+               split_tokens: int = 0, max_seq: Optional[int] = None) -> torch.Tensor:
+        """Decode attention of `query` ``[batch, q_heads, tokens, head_dim]`` over rows
+        [0, batch), reading K and V from the pages through the block table (nothing is
+        gathered).  Query token i of row b sits at position seq_lens[b] - tokens + i and sees
+        positions [0, seq_lens[b] - tokens + i]; q head h reads kv head h // (q_heads //
+        kv_heads).  Returns ``[batch, q_heads, tokens, head_dim]`` (a view of a
+        ``[batch, tokens, q_heads, head_dim]`` buffer, the layout attention outputs take next)
+        in `out_dtype` (default the query's).  `max_seq` bounds the rows' lengths (default:
+        the host shadow's longest row; pass the capacity when capturing a graph)."""
+        if query.dim() != 4 or query.shape[3] != self.head_dim or query.shape[1] % self.kv_heads:
+            raise ValueError("query must be [batch, q_heads, tokens, head_dim] with q_heads a "
+                             "multiple of the pool's kv_heads")
+        batch, q_heads, tokens, _ = query.shape
+        if batch > self.max_batch:
+            raise ValueError("query batch exceeds the pool's rows")
+        if query.dtype != self.dtype or query.device != self.key_pages.device:
+            raise ValueError("query must have the pool's dtype and device")
+        scale = 1.0 / math.sqrt(self.head_dim) if scale is None else float(scale)
+        if out is None:
+            dt = out_dtype or query.dtype
+            out = torch.empty((batch, tokens, q_heads, self.head_dim), dtype=dt,
+                              device=query.device).transpose(1, 2)
+        if batch == 0 or tokens == 0:
+            return out
+        if max_seq is None:
+            max_seq = int(self.lens[:batch].max())
+        if not self.on_gpu:
+            _HostOps.pool_decode_attention(self.tensors, query, out, scale, batch)
+            return out
+        backend = _gpu_backend()
+        if query.stride(3) != 1 or query.data_ptr() % 16 or any(s % 8 for s in query.stride()[:3]):
+            query = query.contiguous()
+        need = backend.attention_workspace_bytes(self.tensors, batch, q_heads, tokens,
+                                                 max(int(max_seq), 1), int(split_tokens))
+        if need < 0:
+            raise ValueError(
+                "paged decode attention takes bf16/fp16 pools with head_dim 128 and at most 16 "
+                f"query rows per kv head (got {self.dtype}, head_dim {self.head_dim}, "
+                f"{q_heads // self.kv_heads} x {tokens} rows)")
+        backend.pool_decode_attention(self.tensors, query, out, scale, max(int(max_seq), 1),
+                                      int(split_tokens), self.attention_workspace(need))
+        return out
+
+    def attention_workspace(self, nbytes: int) -> torch.Tensor:
+        """The pool's decode-attention workspace (split records), at least `nbytes`; grown, never
+        shrunk.  Launches on one stream may share it."""
+        ws = getattr(self, "_attn_ws", None)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty((max(int(nbytes), 256),), dtype=torch.uint8, device=self.device)
+            self._attn_ws = ws
+        return ws
+
     def errors(self) -> int:
         """Sticky device error bits (reads the device: a synchronisation point)."""
         return int(self.ctrl[CTRL_ERRORS].item())
@@ -408,6 +463,28 @@ class _HostOps:
     def pool_update_(t, key_states, value_states, key_out, value_out, seq_out, flags=0):
         _HostOps.pool_append_(t, key_states, value_states)
         _HostOps.pool_gather(t, key_out, value_out, key_states.shape[0], seq_out, flags)
+
+    @staticmethod
+    def pool_decode_attention(t, query, out, scale, batch):
+        """Decode attention for a pool in host memory: the gathered rows, float32 arithmetic."""
+        kp, vp, bt, lens, hw, free, ctrl = t
+        _, q_heads, tokens, D = query.shape
+        group = q_heads // kp.shape[2]
+        seq = int(lens[:batch].max())
+        shape = (batch, kp.shape[2], seq, D)
+        ko = torch.empty(shape, dtype=kp.dtype)
+        vo = torch.empty(shape, dtype=kp.dtype)
+        _HostOps.pool_gather(t, ko, vo, batch, seq)
+        for b in range(batch):
+            n = int(lens[b])
+            k = ko[b, :, :n].float().repeat_interleave(group, dim=0)  # [q_heads, n, D]
+            v = vo[b, :, :n].float().repeat_interleave(group, dim=0)
+            s = torch.matmul(query[b].float(), k.transpose(1, 2)) * scale  # [q_heads, T, n]
+            pos = torch.arange(n)[None, :]
+            limit = n - tokens + torch.arange(tokens)[:, None]
+            s = s.masked_fill(pos > limit, float("-inf"))
+            p = torch.softmax(s, dim=-1).nan_to_num(0.0)  # a row that sees nothing gives zeros
+            out[b] = torch.matmul(p, v).to(out.dtype)
 
     @staticmethod
     def pool_crop_(t, batch, max_length):

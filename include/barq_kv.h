@@ -24,6 +24,11 @@
  *   barq_kv_free_rows     <- no reference counterpart: returns a finished sequence's pages
  *                            to the pool (the page allocator the reference only planned,
  *                            IMPLEMENTATION_PLAN.md:90-92).
+ *   barq_kv_decode_attention, barq_kv_attention_workspace_bytes
+ *                         <- no reference counterpart: the "gather/scatter kernels for attention
+ *                            reads" the reference planned (IMPLEMENTATION_PLAN.md:90-91); it
+ *                            replaces current_tensors() followed by attention over the
+ *                            materialised K/V (python/barqtrain/kv_cache.py:120-142).
  *
  * Calls that name the same pool must be ordered on one stream; calls on different
  * pools are independent.
@@ -55,9 +60,12 @@ extern "C" {
 /* Sticky error bits in ctrl[BARQ_KV_CTRL_ERRORS]. */
 #define BARQ_KV_ERRBIT_POOL_EXHAUSTED 1 /* a new block found no free page; its tokens were dropped */
 #define BARQ_KV_ERRBIT_CAPACITY 2       /* a position fell at or beyond max_blocks * page_size */
-#define BARQ_KV_ERRBIT_BAD_INDEX 4      /* a row index outside [0, max_batch) was given */
+#define BARQ_KV_ERRBIT_BAD_INDEX 4      /* a row index outside [0, max_batch) was given, or an
+                                           attention read met a block naming no page */
 #define BARQ_KV_ERRBIT_OUT_SHORT 8      /* an update's output extent ended before a row's new
                                            tokens; those tokens were not stored */
+#define BARQ_KV_ERRBIT_ATTN_SHORT 16    /* a decode-attention launch's max_seq was below a row's
+                                           length; that row attended its first max_seq tokens */
 
 /* Flags of barq_kv_gather / barq_kv_update. */
 #define BARQ_KV_SEQ_FROM_DEVICE 1 /* seq_out is the output's capacity; the positions written are
@@ -168,6 +176,42 @@ int barq_kv_free_rows(const barq_kv_pool* pool, const int32_t* rows, int64_t num
  */
 int barq_kv_copy_rows(const barq_kv_pool* src, const barq_kv_pool* dst, const int32_t* src_rows,
                       int64_t num_rows, void* stream);
+
+/* Flags of barq_kv_decode_attention. */
+#define BARQ_KV_ATTN_FP16 1    /* pages and query hold IEEE binary16; default bfloat16 */
+#define BARQ_KV_ATTN_OUT_F32 2 /* out holds float32; default the pages' element type */
+
+/*
+ * Bytes of workspace barq_kv_decode_attention needs for these arguments (the same batch,
+ * q_heads, tokens, max_seq and split_tokens), or -1 when it would reject them.
+ */
+int64_t barq_kv_attention_workspace_bytes(const barq_kv_pool* pool, int64_t batch,
+                                          int64_t q_heads, int64_t tokens, int64_t max_seq,
+                                          int64_t split_tokens);
+
+/*
+ * Decode attention over rows [0, batch) of a 2-byte (bf16 / fp16) pool with head_dim 128,
+ * reading K and V from the pages:
+ *   out[b, h, i, :] = sum_t softmax_t(scale * q[b, h, i, :] . K[b, h / G, t, :]) V[b, h / G, t, :]
+ * over positions t <= seq_lens[b] - tokens + i (the query tokens are the row's last `tokens`
+ * positions, already appended), G = q_heads / kv_heads.  A row with no visible position gets
+ * zeros.  query: [batch, q_heads, tokens, 128] of the pool's type, element strides (q_stride_b,
+ * q_stride_h, q_stride_t), 16-byte aligned rows; out: [batch, q_heads, tokens, 128] of the
+ * pool's type or float32 (BARQ_KV_ATTN_OUT_F32), element strides (out_stride_*), each a
+ * multiple of 8.  G * tokens <= 16.  max_seq bounds every row's length (0 = the pool's
+ * capacity); split_tokens is the positions per workgroup (0 = chosen from batch, kv_heads and
+ * max_seq; raised to whole multiples of 256 and to at most 256 splits per row).  Rows needing
+ * more than one split keep per-split partial results in workspace (device memory of
+ * barq_kv_attention_workspace_bytes(...) bytes, 16-byte aligned, no initialisation needed; NULL
+ * when that is 0) and are merged by a second launch on the same stream; launches that share a
+ * workspace must not overlap.
+ */
+int barq_kv_decode_attention(const barq_kv_pool* pool, const void* query, int64_t batch,
+                             int64_t q_heads, int64_t tokens, int64_t q_stride_b,
+                             int64_t q_stride_h, int64_t q_stride_t, void* out,
+                             int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_t,
+                             float scale, int64_t max_seq, int64_t split_tokens, int64_t flags,
+                             void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

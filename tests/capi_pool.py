@@ -81,6 +81,23 @@ class CPool:
         _capi.check(self.lib.barq_kv_copy_rows(self.ref, dst.ref, idx.data_ptr(), len(rows), self._stream()))
         torch.cuda.current_stream().synchronize()
 
+    def attend(self, q, *, scale=None, out_f32=False, max_seq=0, split_tokens=0, workspace=None):
+        """barq_kv_decode_attention; returns (out [B, Hq, T, D], workspace)."""
+        B, Hq, T, D = q.shape
+        need = self.lib.barq_kv_attention_workspace_bytes(self.ref, B, Hq, T, max_seq, split_tokens)
+        assert need >= 0, "attention arguments rejected"
+        if workspace is None or workspace.numel() < need:
+            workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=self.kp.device)
+        dt = torch.float32 if out_f32 else self.dtype
+        out = torch.full((B, T, Hq, D), float("nan"), dtype=dt, device=self.kp.device).transpose(1, 2)
+        flags = (1 if self.dtype == torch.float16 else 0) | (2 if out_f32 else 0)
+        scale = D ** -0.5 if scale is None else scale
+        _capi.check(self.lib.barq_kv_decode_attention(
+            self.ref, q.data_ptr(), B, Hq, T, q.stride(0), q.stride(1), q.stride(2), out.data_ptr(),
+            out.stride(0), out.stride(1), out.stride(2), scale, max_seq, split_tokens, flags,
+            workspace.data_ptr(), workspace.numel(), self._stream()))
+        return out, workspace
+
     def new_out(self, batch, seq):
         shape = (batch, self.heads, seq, self.dim)
         return (torch.empty(shape, dtype=self.dtype, device=self.kp.device),

@@ -1,0 +1,212 @@
+"""GPU parity of the paged decode-attention kernel (barq_kv_decode_attention) through the C ABI,
+against the float64 reference over the oracle's gathered K/V (tests/attn_ref.py).
+
+Tolerances: with float32 output, |out - ref| <= 2e-5 + 2e-5 |ref| (scores from exact bf16/fp16
+products summed in fp32, fp32 softmax and P.V); with the cache's own 2-byte output, one rounding
+of that value more: 2^-8 |ref| + 2e-5 for bf16, 2^-11 |ref| + 2e-5 for fp16.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from attn_ref import decode_attention_reference, within_tolerance
+from capi_pool import CPool
+from kvgen import hf_layout
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = dict(rtol=2e-5, atol=2e-5)
+OUT_TOL = {torch.bfloat16: dict(rtol=2.0**-8, atol=2e-5), torch.float16: dict(rtol=2.0**-11, atol=2e-5)}
+
+
+def fill_pool(pool, kd, vd, lens, dtype):
+    """Append each row's K/V: rows sorted by length, longest first, appended in rounds so each
+    call appends `tokens` to rows [0, batch)."""
+    B = len(lens)
+    order = np.argsort(-np.asarray(lens), kind="stable")
+    assert list(order) == list(range(B)), "rows must be given longest first"
+    cur = 0
+    while True:
+        active = [b for b in range(B) if lens[b] > cur]
+        if not active:
+            break
+        batch = len(active)
+        nxt = min(lens[b] for b in active)
+        k = torch.from_numpy(np.ascontiguousarray(kd[:batch, :, cur:nxt])).to(dtype).cuda()
+        v = torch.from_numpy(np.ascontiguousarray(vd[:batch, :, cur:nxt])).to(dtype).cuda()
+        pool.append(k, v)
+        cur = nxt
+
+
+def make_rows(B, Hkv, page, lens, dtype, seed, order_seed=None, cap=None):
+    lens = sorted((int(x) for x in lens), reverse=True)
+    cap = cap or max(max(lens), 1)
+    gen = torch.Generator().manual_seed(seed)
+    max_blocks = -(-cap // page)
+    order = None
+    n_pages = B * max_blocks
+    if order_seed is not None:
+        order = torch.from_numpy(np.random.default_rng(order_seed).permutation(n_pages).astype(np.int32))
+    pool = CPool(max_batch=B, max_blocks=max_blocks, page_size=page, heads=Hkv, dim=128, dtype=dtype,
+                 num_pages=n_pages, order=order)
+    kd = torch.randn(B, Hkv, cap, 128, generator=gen).to(dtype).double().numpy()
+    vd = torch.randn(B, Hkv, cap, 128, generator=gen).to(dtype).double().numpy()
+    fill_pool(pool, kd, vd, lens, dtype)
+    torch.cuda.synchronize()
+    assert pool.errors() == 0
+    return pool, kd, vd, lens
+
+
+def check(pool, kd, vd, lens, G, T, dtype, seed, out_f32=True, split_tokens=0, max_seq=0, ws=None,
+          scale=None):
+    B, Hkv = kd.shape[0], kd.shape[1]
+    gen = torch.Generator().manual_seed(seed)
+    q = hf_layout(B, G * Hkv, T, 128, dtype, gen).cuda()
+    scale = 128 ** -0.5 if scale is None else scale
+    out, ws = pool.attend(q, scale=scale, out_f32=out_f32, split_tokens=split_tokens, max_seq=max_seq,
+                          workspace=ws)
+    torch.cuda.synchronize()
+    want = decode_attention_reference(q.double().cpu().numpy(), kd, vd, lens, scale)
+    got = out.double().cpu().numpy()
+    tol = F32_TOL if out_f32 else OUT_TOL[dtype]
+    ok, ratio = within_tolerance(got, want, **tol)
+    assert ok, f"G={G} T={T} lens={list(lens)[:8]} split={split_tokens}: error {ratio:.3g} x tolerance"
+    return ws
+
+
+@pytest.mark.parametrize("dtype,page", [(torch.bfloat16, 16), (torch.float16, 16), (torch.bfloat16, 32),
+                                        (torch.float16, 32), (torch.bfloat16, 8), (torch.float16, 5),
+                                        (torch.bfloat16, 1)])
+def test_ragged_rows_gqa(dtype, page):
+    """Ragged rows (1 .. 1100 positions, chunk, split and page boundaries on both sides), a
+    random page order, grouped-query factors 1 / 4 / 8 / 16, one to five splits per row."""
+    lens = [1100, 1025, 769, 513, 300, 257, 256, 255, 129, 64, 63, 17, 16, 1]
+    pool, kd, vd, lens = make_rows(len(lens), 2, page, lens, dtype, seed=page, order_seed=page + 1)
+    ws = None
+    for i, (G, split) in enumerate([(4, 0), (1, 256), (8, 512), (16, 256), (4, 768)]):
+        ws = check(pool, kd, vd, lens, G, 1, dtype, seed=100 + i, split_tokens=split, ws=ws)
+    check(pool, kd, vd, lens, 4, 1, dtype, seed=7, out_f32=False)
+    assert pool.errors() == 0
+
+
+@pytest.mark.parametrize("G,T", [(4, 2), (4, 4), (2, 8), (1, 16), (8, 2)])
+def test_multi_token_queries_causal(G, T):
+    """T query tokens at the end of each row: token i sees positions up to len - T + i."""
+    lens = [600, 200, 70, 64, 33, T]
+    pool, kd, vd, lens = make_rows(len(lens), 2, 16, lens, torch.bfloat16, seed=G * T, order_seed=3)
+    check(pool, kd, vd, lens, G, T, torch.bfloat16, seed=1, split_tokens=256)
+    check(pool, kd, vd, lens, G, T, torch.bfloat16, seed=2)
+
+
+def test_llama3_8b_decode_shape():
+    """The benchmark's C2 shape: 16 rows x 8 kv heads x 32 q heads, 513 positions, page 16."""
+    lens = [513] * 16
+    pool, kd, vd, lens = make_rows(16, 8, 16, lens, torch.bfloat16, seed=2002, order_seed=5, cap=768)
+    check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=3, max_seq=513)
+    check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=4, out_f32=False)
+
+
+def test_empty_rows_and_closed_forms():
+    """A row of length 0 (and one shorter than T) gives zeros; equal V rows give that row; a zero
+    query gives the mean of V."""
+    D = 128
+    lens = [40, 3, 0]
+    pool, kd, vd, lens = make_rows(3, 1, 16, lens, torch.bfloat16, seed=9)
+    gen = torch.Generator().manual_seed(1)
+    q = hf_layout(3, 4, 4, D, torch.bfloat16, gen).cuda()
+    out, _ = pool.attend(q, out_f32=True)
+    torch.cuda.synchronize()
+    got = out.double().cpu().numpy()
+    assert np.all(got[2] == 0), "empty row"
+    assert np.all(got[1, :, 0] == 0) and np.any(got[1, :, 1] != 0), "row 1 (3 positions, T=4): token 0 sees none"
+    want = decode_attention_reference(q.double().cpu().numpy(), kd, vd, lens, D ** -0.5)
+    assert within_tolerance(got, want, **F32_TOL)[0]
+
+    same = CPool(max_batch=1, max_blocks=4, page_size=16, heads=1, dim=D, dtype=torch.bfloat16)
+    row = torch.randn(1, 1, 1, D, generator=gen).to(torch.bfloat16)
+    same.append(row.expand(1, 1, 50, D).contiguous().cuda(), row.expand(1, 1, 50, D).contiguous().cuda())
+    q = hf_layout(1, 8, 1, D, torch.bfloat16, gen).cuda() * 4
+    out, _ = same.attend(q, out_f32=True)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(out[0, :, 0].cpu().numpy(), row[0, 0].float().expand(8, D).numpy(), rtol=2e-6)
+
+    zq = torch.zeros(1, 8, 1, D, dtype=torch.bfloat16, device="cuda")
+    gk = torch.randn(1, 1, 50, D, generator=gen).to(torch.bfloat16)
+    gv = torch.randn(1, 1, 50, D, generator=gen).to(torch.bfloat16)
+    mean = CPool(max_batch=1, max_blocks=4, page_size=16, heads=1, dim=D, dtype=torch.bfloat16)
+    mean.append(gk.cuda(), gv.cuda())
+    out, _ = mean.attend(zq, out_f32=True)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(out[0, 0, 0].cpu().numpy(), gv[0, 0].double().mean(0).numpy(), rtol=1e-5, atol=1e-6)
+
+
+def test_short_max_seq_is_flagged():
+    """max_seq 64 sizes the launch to one 256-position split; a 600-position row is flagged."""
+    lens = [600, 50]
+    pool, kd, vd, lens = make_rows(2, 2, 16, lens, torch.bfloat16, seed=4)
+    gen = torch.Generator().manual_seed(0)
+    q = hf_layout(2, 8, 1, 128, torch.bfloat16, gen).cuda()
+    pool.attend(q, out_f32=True, max_seq=64)
+    torch.cuda.synchronize()
+    assert pool.errors() & 16, "ATTN_SHORT bit"
+
+
+def test_page_pool_attend_and_graph_replays(hip):
+    """PagePool.attend through the torch binding, then a captured graph of append + attend over
+    3 layers replayed while rows grow: every replay against the reference."""
+    from barqtrain_amd.paged import PagePool
+
+    L, B, Hkv, G, D, P, prefill, steps = 3, 4, 2, 4, 128, 16, 60, 12
+    cap = prefill + steps
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator().manual_seed(11)
+    pools = [PagePool(max_batch=B, max_blocks=-(-cap // P), page_size=P, kv_heads=Hkv, head_dim=D,
+                      dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    dense_k = np.zeros((L, B, Hkv, cap, D))
+    dense_v = np.zeros((L, B, Hkv, cap, D))
+    for li, pool in enumerate(pools):
+        k = hf_layout(B, Hkv, prefill, D, torch.bfloat16, gen)
+        v = hf_layout(B, Hkv, prefill, D, torch.bfloat16, gen)
+        pool.append(k.to(dev), v.to(dev))
+        dense_k[li, :, :, :prefill] = k.double().numpy()
+        dense_v[li, :, :, :prefill] = v.double().numpy()
+    q = hf_layout(B, G * Hkv, 1, D, torch.bfloat16, gen).to(dev)
+    out = pools[0].attend(q, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    want = decode_attention_reference(q.double().cpu().numpy(), dense_k[0], dense_v[0], [prefill] * B, D ** -0.5)
+    assert within_tolerance(out.double().cpu().numpy(), want, **F32_TOL)[0]
+
+    kin = torch.zeros((L, B, Hkv, 1, D), dtype=torch.bfloat16, device=dev)
+    vin = torch.zeros_like(kin)
+    qin = torch.zeros((L, B, G * Hkv, 1, D), dtype=torch.bfloat16, device=dev)
+    outs = [torch.zeros((B, 1, G * Hkv, D), dtype=torch.float32, device=dev).transpose(1, 2) for _ in range(L)]
+    for pool in pools:  # workspaces sized for the capacity before capture
+        pool.attention_workspace(hip.attention_workspace_bytes(pool.tensors, B, G * Hkv, 1, cap, 0))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for li, pool in enumerate(pools):
+            hip.pool_append_(pool.tensors, kin[li], vin[li])
+            hip.pool_decode_attention(pool.tensors, qin[li], outs[li], D ** -0.5, cap, 0,
+                                      pool.attention_workspace(0))
+    for s in range(steps):
+        ks = [hf_layout(B, Hkv, 1, D, torch.bfloat16, gen) for _ in range(L)]
+        vs = [hf_layout(B, Hkv, 1, D, torch.bfloat16, gen) for _ in range(L)]
+        qs = [hf_layout(B, G * Hkv, 1, D, torch.bfloat16, gen) for _ in range(L)]
+        for li in range(L):
+            kin[li].copy_(ks[li].to(dev))
+            vin[li].copy_(vs[li].to(dev))
+            qin[li].copy_(qs[li].to(dev))
+            dense_k[li, :, :, prefill + s] = ks[li][:, :, 0].double().numpy()
+            dense_v[li, :, :, prefill + s] = vs[li][:, :, 0].double().numpy()
+        _ = torch.randn(1 << 18, device=dev).sum().item()  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        n = prefill + s + 1
+        for li in range(L):
+            want = decode_attention_reference(qs[li].double().numpy(), dense_k[li], dense_v[li], [n] * B, D ** -0.5)
+            ok, ratio = within_tolerance(outs[li].double().cpu().numpy(), want, **F32_TOL)
+            assert ok, f"replay {s} layer {li}: {ratio:.3g} x tolerance"
+    assert all(p.errors() == 0 for p in pools)
