@@ -1,0 +1,104 @@
+"""Attention that reads K and V from the paged cache's pages, as a transformers attention
+implementation (``"barq_paged"``).
+
+A ``BarqPagedKVCache`` built with ``fused_attention=True`` appends in ``update`` and returns, in
+place of materialised K/V, zero-stride views that name their cache layer.  The attention
+function registered here finds the layer on the key view and, for decode (``G * T <= 16`` query
+rows per kv head, no padding mask), runs the pool's decode-attention kernel: softmax(Q K^T) V
+is computed from the pages through the block table, so the per-step gather of the whole history
+(and its write and re-read) disappears.  Prefill and padded batches take the gathered K/V and an
+fp32 attention; calls without a paged cache go to transformers' SDPA path.
+
+The kernel's numbers are fp32 throughout (scores from exact bf16/fp16 products, fp32 softmax and
+P.V), so logits track an fp32 reference more closely than the default bf16 attention does.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+ATTN_IMPLEMENTATION = "barq_paged"
+_KERNEL_MAX_ROWS = 16
+
+
+def paged_kv_view(layer, like: torch.Tensor, seq: int) -> torch.Tensor:
+    """A ``[batch, kv_heads, seq, head_dim]`` zero-stride view carrying the cache layer."""
+    base = getattr(layer, "_fused_base", None)
+    if base is None or base.dtype != like.dtype or base.device != like.device:
+        base = torch.zeros((), dtype=like.dtype, device=like.device)
+        layer._fused_base = base
+    view = base.expand(like.shape[0], like.shape[1], seq, like.shape[3])
+    view._barq_paged_layer = layer
+    return view
+
+
+def _fp32_attention(query, key, value, attention_mask, scale):
+    """Reference-precision attention over gathered K/V: q [B, Hq, T, D], k/v [B, Hkv, S, D];
+    bottom-right causal when no mask is given; returns [B, T, Hq, D] in the query's dtype."""
+    B, Hq, T, D = query.shape
+    group = Hq // key.shape[1]
+    q = query.float()
+    k = key.float().repeat_interleave(group, dim=1)
+    v = value.float().repeat_interleave(group, dim=1)
+    scores = torch.matmul(q, k.transpose(-1, -2).contiguous()) * scale
+    S = k.shape[2]
+    if attention_mask is None:
+        pos = torch.arange(S, device=q.device)
+        limit = S - T + torch.arange(T, device=q.device)
+        scores = scores.masked_fill(pos[None, :] > limit[:, None], float("-inf"))
+    elif attention_mask.dtype == torch.bool:
+        scores = scores.masked_fill(~attention_mask[..., :S], float("-inf"))
+    else:
+        scores = scores + attention_mask[..., :S].float()
+    probs = torch.softmax(scores, dim=-1).nan_to_num(0.0)
+    return torch.matmul(probs, v).transpose(1, 2).contiguous().to(query.dtype)
+
+
+def paged_attention_forward(module: torch.nn.Module, query: torch.Tensor, key: torch.Tensor,
+                            value: torch.Tensor, attention_mask: Optional[torch.Tensor],
+                            scaling: Optional[float] = None, dropout: float = 0.0, **kwargs):
+    """transformers attention interface: returns ``(attn_output [B, T, Hq, D], None)``."""
+    layer = getattr(key, "_barq_paged_layer", None)
+    if layer is None:
+        from transformers.integrations.sdpa_attention import sdpa_attention_forward
+
+        return sdpa_attention_forward(module, query, key, value, attention_mask, scaling=scaling,
+                                      dropout=dropout, **kwargs)
+    pool = layer.pool
+    _, q_heads, tokens, head_dim = query.shape
+    scale = scaling if scaling is not None else 1.0 / math.sqrt(head_dim)
+    rows = (q_heads // pool.kv_heads) * tokens
+    kernel_ok = (attention_mask is None and rows <= _KERNEL_MAX_ROWS and pool.on_gpu
+                 and pool.dtype in (torch.bfloat16, torch.float16) and pool.head_dim == 128)
+    if kernel_ok:
+        return pool.attend(query, scale).transpose(1, 2), None
+    k, v = layer.current_tensors()
+    return _fp32_attention(query, k, v, attention_mask, scale), None
+
+
+def register() -> str:
+    """Make ``"barq_paged"`` a transformers attention implementation (idempotent); its masks are
+    built like SDPA's (none for an unpadded decode step)."""
+    from transformers import AttentionInterface
+    from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
+
+    AttentionInterface.register(ATTN_IMPLEMENTATION, paged_attention_forward)
+    AttentionMaskInterface.register(ATTN_IMPLEMENTATION, sdpa_mask)
+    return ATTN_IMPLEMENTATION
+
+
+def enable_paged_attention(model: torch.nn.Module) -> torch.nn.Module:
+    """Route the model's attention through ``"barq_paged"`` and mark it so that paged caches
+    created for its generate() calls return page views instead of gathered K/V."""
+    register()
+    config = getattr(model, "config", None)
+    if config is not None:
+        config._attn_implementation = ATTN_IMPLEMENTATION
+    model._barqtrain_paged_attention = True
+    return model
+
+
+__all__ = ["ATTN_IMPLEMENTATION", "enable_paged_attention", "paged_attention_forward", "register"]

@@ -10,6 +10,7 @@ ran on the paged cache (``_barqtrain_last_generate_used_paged_kv``), whether the
 
 from __future__ import annotations
 
+import os
 import types
 from typing import Optional
 
@@ -64,10 +65,20 @@ def _configure_attention_backend(model: torch.nn.Module, model_label: str) -> Op
     return backend
 
 
-def patch_inference(model: torch.nn.Module) -> torch.nn.Module:
-    """Decode-time patches: attention backend choice plus the paged-cache generate hook."""
+def patch_inference(model: torch.nn.Module, paged_attention: Optional[bool] = None) -> torch.nn.Module:
+    """Decode-time patches: attention backend choice plus the paged-cache generate hook.
+    paged_attention (default: the BARQTRAIN_PAGED_ATTENTION switch, off) routes attention
+    through "barq_paged", which reads K/V from the cache pages instead of a gathered copy."""
     label = getattr(getattr(model, "config", None), "model_type", None) or "model"
-    _configure_attention_backend(model, label)
+    if paged_attention is None:
+        paged_attention = os.environ.get("BARQTRAIN_PAGED_ATTENTION", "0").strip().lower() in {"1", "true", "yes", "on"}
+    if paged_attention and torch.cuda.is_available():
+        from barqtrain_amd.attention import enable_paged_attention
+
+        enable_paged_attention(model)
+        print(f"BarqTrain: Enabled paged decode attention for {label}")
+    else:
+        _configure_attention_backend(model, label)
     return _patch_generate_with_paged_kv(model, label)
 
 

@@ -41,3 +41,38 @@ def test_generate_matches_dynamic_cache(page):
     assert torch.equal(seq, ref_seq)
     assert torch.equal(logits.view(torch.int32), ref_logits.view(torch.int32))
     assert cache.get_seq_length() == 13 + new - 1
+
+
+def test_generate_with_paged_attention_on_host_pool():
+    """The "barq_paged" attention implementation over a fused-attention cache in host memory
+    (gathered K/V, fp32 attention): same tokens as DynamicCache with eager attention, logits
+    within fp32 rounding; with padding (left-padded batch) the mask is honoured."""
+    from transformers.cache_utils import DynamicCache
+
+    from barqtrain_amd import attention
+
+    model, cfg = tiny_llama()
+    model.config._attn_implementation = "eager"
+    ids = torch.randint(1, 512, (2, 13), generator=torch.Generator().manual_seed(1))
+    new = 18
+    ref_seq, ref_logits = decode(model, ids, DynamicCache(config=cfg), new)
+    attention.enable_paged_attention(model)
+    cache = create_paged_kv_cache(model, max_batch_size=2, max_cache_len=13 + new, page_size=4)
+    assert all(layer.fused_attention for layer in cache.layers)
+    seq, logits = decode(model, ids, cache, new)
+    assert torch.equal(seq, ref_seq)
+    torch.testing.assert_close(logits, ref_logits, rtol=1e-5, atol=1e-5)
+
+    # left padding: row 1 has 4 pad tokens; compare with the eager model on the same mask
+    mask = torch.ones_like(ids)
+    mask[1, :4] = 0
+    model.config._attn_implementation = "eager"
+    ref = model.generate(ids, attention_mask=mask, max_new_tokens=6, do_sample=False,
+                         past_key_values=DynamicCache(config=cfg), return_dict_in_generate=True,
+                         output_logits=True)
+    attention.enable_paged_attention(model)
+    cache = create_paged_kv_cache(model, max_batch_size=2, max_cache_len=13 + 6, page_size=4)
+    got = model.generate(ids, attention_mask=mask, max_new_tokens=6, do_sample=False,
+                         past_key_values=cache, return_dict_in_generate=True, output_logits=True)
+    assert torch.equal(got.sequences, ref.sequences)
+    torch.testing.assert_close(torch.stack(got.logits), torch.stack(ref.logits), rtol=1e-5, atol=1e-5)

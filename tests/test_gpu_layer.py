@@ -168,3 +168,66 @@ def test_generate_on_gpu_matches_dynamic_cache(hip, monkeypatch):
     out = model.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=new, do_sample=False)
     assert model._barqtrain_last_generate_used_paged_kv is True
     assert torch.equal(out, ref_seq)
+
+
+def bf16_llama(seed=0):
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    torch.manual_seed(seed)
+    # 8 query heads over 2 kv heads (G = 4, the Llama-3 ratio), head_dim 128, bf16
+    cfg = LlamaConfig(vocab_size=512, hidden_size=1024, intermediate_size=1024, num_hidden_layers=2,
+                      num_attention_heads=8, num_key_value_heads=2, max_position_embeddings=1024,
+                      pad_token_id=0, eos_token_id=None)
+    return LlamaForCausalLM(cfg).to(torch.bfloat16).eval(), cfg
+
+
+def test_paged_attention_decode_in_a_model(hip, monkeypatch):
+    """A bf16 model whose decode steps read K/V from the pages (the kernel) against the same
+    model on the gather + fp32 attention path, token by token on one sequence: logits agree to
+    bf16 rounding.  Then generate() through patch_inference(paged_attention=True)."""
+    pytest.importorskip("transformers")
+    from barqtrain import create_paged_kv_cache, patch_inference
+    from barqtrain_amd import attention
+
+    model, cfg = bf16_llama()
+    model = model.to("cuda")
+    attention.enable_paged_attention(model)
+    gen = torch.Generator().manual_seed(5)
+    prompt, new = 37, 24
+    seq = torch.randint(1, 512, (3, prompt + new), generator=gen).to("cuda")
+
+    from barqtrain_amd.paged import PagePool
+
+    calls = []
+    attend = PagePool.attend
+    monkeypatch.setattr(PagePool, "attend", lambda self, *a, **k: calls.append(1) or attend(self, *a, **k))
+
+    def run(kernel: bool):
+        monkeypatch.setattr(attention, "_KERNEL_MAX_ROWS", 16 if kernel else 0)
+        cache = create_paged_kv_cache(model, max_batch_size=3, max_cache_len=prompt + new, page_size=16)
+        steps = []
+        with torch.no_grad():
+            out = model(seq[:, :prompt], past_key_values=cache, use_cache=True)
+            steps.append(out.logits[:, -1].float())
+            for t in range(new - 1):
+                out = model(seq[:, prompt + t:prompt + t + 1], past_key_values=cache, use_cache=True)
+                steps.append(out.logits[:, -1].float())
+        assert all(layer.pool.errors() == 0 for layer in cache.layers)
+        return torch.stack(steps)
+
+    fused = run(True)
+    assert len(calls) == cfg.num_hidden_layers * (new - 1), "decode steps ran the kernel"
+    reference = run(False)
+    assert len(calls) == cfg.num_hidden_layers * (new - 1), "the fallback ran no kernel"
+    scale = reference.abs().max().item()
+    err = (fused - reference).abs().max().item()
+    assert err <= 0.02 * scale, f"logits differ by {err} (scale {scale})"
+    assert (fused.argmax(-1) == reference.argmax(-1)).float().mean().item() >= 0.9
+
+    monkeypatch.setattr(attention, "_KERNEL_MAX_ROWS", 16)
+    monkeypatch.setenv("BARQTRAIN_PAGED_KV_MIN_CACHE_LEN", "0")
+    patch_inference(model, paged_attention=True)
+    out = model.generate(seq[:, :prompt], attention_mask=torch.ones_like(seq[:, :prompt]), max_new_tokens=8,
+                         do_sample=False)
+    assert model._barqtrain_last_generate_used_paged_kv is True
+    assert out.shape == (3, prompt + 8)
