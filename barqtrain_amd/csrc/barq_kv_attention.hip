@@ -5,18 +5,20 @@
 //   over the positions t <= seq_lens[b] - T + i of row b (the row's own length, causal over the
 //   T new query tokens), G = q_heads / kv_heads (grouped-query attention).
 //
-// Work split (flash decoding): one workgroup of 4 waves per (row, kv head, split of
-// `split_tokens` positions); the waves take the split's 64-position chunks in turn.  The G*T
-// query rows of a kv head share every K/V byte a wave loads, so each byte of the row's pages is
-// read once per launch.  Scores come from the bf16/fp16 16x16x32 MFMA (query rows padded to 16,
-// positions as the 16 columns: one MFMA column block is one 16-position run of a page).  P.V
-// runs on the fp32 4x4x1 MFMA in 16 blocks: a lane's 16-byte load of V holds 8 consecutive head
-// dims of one position, and element e of it is the lane's B operand of the e-th MFMA, so V is
-// consumed in the layout it is stored in (no transpose, no LDS staging of V) and the
-// probabilities stay fp32.  A wave keeps a running max / sum per query row (online softmax,
-// base-2 exponent) and the workgroup merges its waves in LDS.  A row with one split is written
-// by its workgroup; a row with more splits gets one partial record per split, merged by a
-// second launch (the launch boundary makes the records visible: no fences, no counters).
+// Work split (flash decoding): one wave per (row, kv head, split of `split_tokens` positions),
+// streaming the split in 16-position chunks with the next chunk's loads in flight while the
+// current one is computed.  The G*T query rows of a kv head share every K/V byte the wave loads,
+// so each byte of the row's pages is read once per launch.  A wave starts with its row length,
+// its query rows and the split's block-table entries (one per lane) in flight together; page
+// bases come from the lanes by readlane (scalar) or ds_bpermute (per lane, odd page sizes).
+// Scores come from the bf16/fp16 16x16x32 MFMA (query rows padded to 16, the chunk's positions
+// as the 16 columns).  P.V runs on the fp32 4x4x1 MFMA in 16 blocks: a lane's 16-byte load of V
+// holds 8 consecutive head dims of one position, and element e of it is the lane's B operand of
+// the e-th MFMA, so V is consumed in the layout it is stored in (no transpose, no LDS staging of
+// V) and the probabilities stay fp32.  The wave keeps a running max / sum per query row (online
+// softmax, base-2 exponent).  A row with one split is written by its wave; a row with more
+// splits gets one partial record per split, merged by a second launch (the launch boundary makes
+// the records visible: no fences, no counters).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -37,16 +39,14 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWave = 64;
 constexpr int kHeadDim = 128;              // the one head size this kernel is built for
 constexpr int kSteps = kHeadDim / 32;      // k-steps of the score MFMA
-constexpr int kBlock = 16;                 // positions per score MFMA
-constexpr int kChunkBlocks = 2;            // blocks per softmax update
-constexpr int kChunk = kBlock * kChunkBlocks;
-constexpr int kMaxRows = 16;               // query rows (G * T) one workgroup serves
-constexpr int kWaves = 4;                  // waves per workgroup
-constexpr int kThreads = kWaves * kWave;
-constexpr int kSplitQuantum = kChunk * kWaves;  // positions of a split: a multiple of this
-constexpr int kMaxTable = 1024;            // block-table entries a split stages in LDS
-constexpr int kMaxSplits = 256;            // splits per row
-constexpr int kTargetWorkgroups = 1024;    // the automatic split aims at about this many
+constexpr int kBlock = 16;                 // positions per chunk: one score MFMA's columns
+constexpr int kMaxRows = 16;               // query rows (G * T) one wave serves
+constexpr int kThreads = 256;              // workgroup of the merge kernel
+constexpr int kWaves = kThreads / kWave;
+constexpr int kTableLanes = 62;            // block-table entries of a split, one per lane
+constexpr int kMaxSplits = 1024;           // splits per row
+constexpr int kTargetWaves = 3072;         // the automatic split aims at about this many
+constexpr int kMinSplitTokens = 64;
 constexpr int kMaxSplitTokens = 1 << 20;
 
 enum : int { kBF16 = 0, kF16 = 1 };
@@ -181,144 +181,101 @@ __device__ __forceinline__ char* out_row(const AttnArgs& a, int b, int kvh, int 
   return a.out + (int64_t)b * a.o_sb + (int64_t)(kvh * a.group + hl) * a.o_sh + (int64_t)i * a.o_st;
 }
 
-// Shared memory of a split workgroup: the split's block-table entries, then the waves'
-// probability staging (main loop) or the waves' results (workgroup merge).
-struct SplitSmem {
-  int32_t table[kMaxTable];
-  union {
-    float p[kWaves][kChunk][kMaxRows];
-    struct {
-      float acc[kWaves][kMaxRows][kHeadDim];
-      float m[kWaves][kMaxRows];
-      float l[kWaves][kMaxRows];
-    } wg;
-  } u;
-};
-
-// K and V of one chunk for this lane (page_size a multiple of 16: one page per 16-position
-// block, its base a scalar).  K: lane (g, n16) holds dims 32 * step + 8 * g .. +7 of position
-// 16j + n16; V: dims 8 * n16 .. +7 of position 16j + 4s + g.  PRED: the chunk ends past the
-// row, so positions >= len load nothing and read as zero.
-template <bool PRED>
-__device__ __forceinline__ void load_chunk_uniform(const AttnArgs& a, const SplitSmem& sm, int blk0,
-                                                   const char* kbase, const char* vbase, int tc,
-                                                   int len, int klane, int vlane, int n16, int g,
-                                                   u32x4 (&kv)[kChunkBlocks][kSteps],
-                                                   u32x4 (&vv)[kChunkBlocks][4]) {
+// K and V of one 16-position chunk for this lane.  K: lane (g, n16) holds dims 32 * step + 8 * g
+// .. +7 of position tc + n16; V: dims 8 * n16 .. +7 of position tc + 4s + g.  Positions >= len
+// load nothing and read as zero.  page_j: lane j holds the page of block blk0 + j.
+template <bool UNIFORM, bool PRED>
+__device__ __forceinline__ void load_chunk(const AttnArgs& a, int page_j, int blk0, const char* kbase,
+                                           const char* vbase, int tc, int len, int klane, int vlane,
+                                           int n16, int g, u32x4 (&kv)[kSteps], u32x4 (&vv)[4]) {
+  if constexpr (UNIFORM) {
+    // page_size is a multiple of 16: the chunk lies in one page, its base a scalar.
+    const uint32_t blk = a.page_div.div((uint32_t)tc);
+    const int page = __builtin_amdgcn_readlane(page_j, (int)blk - blk0);
+    const int64_t base = (int64_t)page * a.page_bytes +
+                         (int64_t)(tc - (int)(blk * (uint32_t)a.page_size)) * a.row_bytes;
+    const char* kp = kbase + base + klane;
+    const char* vp = vbase + base + vlane;
 #pragma unroll
-  for (int j = 0; j < kChunkBlocks; ++j) {
-    const int tb = tc + kBlock * j;
-    if (!PRED || tb < len) {
-      const uint32_t blk = a.page_div.div((uint32_t)tb);
-      const int page = __builtin_amdgcn_readfirstlane(sm.table[blk - blk0]);
-      const int64_t base = (int64_t)page * a.page_bytes +
-                           (int64_t)(tb - (int)(blk * (uint32_t)a.page_size)) * a.row_bytes;
-      const char* kp = kbase + base + klane;
-      const char* vp = vbase + base + vlane;
-      if (!PRED || tb + n16 < len) {
+    for (int st = 0; st < kSteps; ++st)
+      kv[st] = (!PRED || tc + n16 < len) ? ld_page(kp + 64 * st) : u32x4{0, 0, 0, 0};
 #pragma unroll
-        for (int st = 0; st < kSteps; ++st) kv[j][st] = ld_page(kp + 64 * st);
-      } else {
+    for (int s = 0; s < 4; ++s)
+      vv[s] = (!PRED || tc + 4 * s + g < len) ? ld_page(vp + 4 * s * a.row_bytes) : u32x4{0, 0, 0, 0};
+  } else {
+    // Any page size: each lane finds the page of its own positions (lane-indexed table read,
+    // all lanes active).
+    const int tk = min(tc + n16, len - 1);
+    const uint32_t bk = a.page_div.div((uint32_t)tk);
+    const int pk = __builtin_amdgcn_ds_bpermute(((int)bk - blk0) << 2, page_j);
+    const char* kp = kbase + (int64_t)pk * a.page_bytes +
+                     (int64_t)(tk - (int)(bk * (uint32_t)a.page_size)) * a.row_bytes + 16 * g;
 #pragma unroll
-        for (int st = 0; st < kSteps; ++st) kv[j][st] = u32x4{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        vv[j][s] = (!PRED || tb + 4 * s + g < len) ? ld_page(vp + 4 * s * a.row_bytes) : u32x4{0, 0, 0, 0};
-    } else {
-#pragma unroll
-      for (int st = 0; st < kSteps; ++st) kv[j][st] = u32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) vv[j][s] = u32x4{0, 0, 0, 0};
-    }
-  }
-}
-
-// The same for any page size: each lane finds the page of each of its positions.
-__device__ __forceinline__ void load_chunk_general(const AttnArgs& a, const SplitSmem& sm, int blk0,
-                                                   const char* kbase, const char* vbase, int tc,
-                                                   int len, int n16, int g,
-                                                   u32x4 (&kv)[kChunkBlocks][kSteps],
-                                                   u32x4 (&vv)[kChunkBlocks][4]) {
-  auto offset = [&](int t) -> int64_t {
-    const uint32_t blk = a.page_div.div((uint32_t)t);
-    return (int64_t)sm.table[blk - blk0] * a.page_bytes +
-           (int64_t)(t - (int)(blk * (uint32_t)a.page_size)) * a.row_bytes;
-  };
-#pragma unroll
-  for (int j = 0; j < kChunkBlocks; ++j) {
-    const int tb = tc + kBlock * j;
-    const int tk = tb + n16;
-    if (tk < len) {
-      const char* kp = kbase + offset(tk) + 16 * g;
-#pragma unroll
-      for (int st = 0; st < kSteps; ++st) kv[j][st] = ld_page(kp + 64 * st);
-    } else {
-#pragma unroll
-      for (int st = 0; st < kSteps; ++st) kv[j][st] = u32x4{0, 0, 0, 0};
-    }
+    for (int st = 0; st < kSteps; ++st)
+      kv[st] = tc + n16 < len ? ld_page(kp + 64 * st) : u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const int tv = tb + 4 * s + g;
-      vv[j][s] = tv < len ? ld_page(vbase + offset(tv) + 16 * n16) : u32x4{0, 0, 0, 0};
+      const int tv = min(tc + 4 * s + g, len - 1);
+      const uint32_t bv = a.page_div.div((uint32_t)tv);
+      const int pv = __builtin_amdgcn_ds_bpermute(((int)bv - blk0) << 2, page_j);
+      const char* vp = vbase + (int64_t)pv * a.page_bytes +
+                       (int64_t)(tv - (int)(bv * (uint32_t)a.page_size)) * a.row_bytes + 16 * n16;
+      vv[s] = tc + 4 * s + g < len ? ld_page(vp) : u32x4{0, 0, 0, 0};
     }
   }
 }
 
-// One workgroup per (split, kv head, row).  UNIFORM: page_size is a multiple of 16.
+// One wave per (split, kv head, row).  UNIFORM: page_size is a multiple of 16.
 // R: groups of 4 query rows (rows <= 4 * R).
 template <int E, int R, bool UNIFORM, typename OutT>
-__global__ __launch_bounds__(kThreads) void attention_split_kernel(const AttnArgs a) {
-  __shared__ SplitSmem sm;
+__global__ __launch_bounds__(kWave) void attention_split_kernel(const AttnArgs a) {
+  __shared__ float lp[kBlock][kMaxRows];  // probabilities, staged for the P.V operand layout
+  __shared__ u32x4 lq[kSteps][kWave];     // the query fragments, re-read for every chunk
 
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
+  const int lane = threadIdx.x;
   const int n16 = lane & 15;
   const int g = lane >> 4;
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
-  const int pair = b * a.kv_heads + kvh;
-
-  const int len = row_length(a, b, split == 0 && kvh == 0 && tid == 0);
-  const int nsplit = len == 0 ? 1 : (len + a.split_tokens - 1) / a.split_tokens;
-  if (split >= nsplit) return;
-
   const int M = a.rows;
   const int T = a.tokens;
   const int t_begin = split * a.split_tokens;
+
+  // Issued together: the split's block-table entries (lane j: block blk0 + j, read whether or
+  // not the row reaches it), the query rows and the row length.
+  const int blk0 = (int)a.page_div.div((uint32_t)t_begin);
+  int page_j = 0;
+  if (lane < kTableLanes && blk0 + lane < a.max_blocks)
+    page_j = a.block_table[(int64_t)b * a.max_blocks + blk0 + lane];
+  // Query rows in the A layout of the score MFMA: lane (row n16, k-group g) holds dims
+  // 32 * step + 8 * g .. +7 of row n16 (zero for padding rows); kept in LDS.
+  {
+    u32x4 qv[kSteps];
+    if (n16 < M) {
+      const char* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(kvh * a.group + n16 / T) * a.q_sh +
+                       (int64_t)(n16 % T) * a.q_st + 16 * g;
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st) qv[st] = *(const u32x4*)(qp + 64 * st);
+    } else {
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st) qv[st] = u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) lq[st][lane] = qv[st];
+  }
+  const int len = row_length(a, b, split == 0 && kvh == 0 && lane == 0);
+  const int nsplit = len == 0 ? 1 : (len + a.split_tokens - 1) / a.split_tokens;
+  if (split >= nsplit) return;
   const int t_end = min(len, t_begin + a.split_tokens);
 
-  // The split's block-table entries, checked once: an entry naming no page is recorded and
-  // read as page 0, so no access leaves the pool.
-  const int blk0 = (int)a.page_div.div((uint32_t)t_begin);
+  // The entries the split uses name pages of the pool; one that does not is recorded and read
+  // as page 0, so no access leaves the pool.
   const int nblk = t_end > t_begin ? (int)a.page_div.div((uint32_t)(t_end - 1)) - blk0 + 1 : 0;
-  {
-    const int32_t* bt = a.block_table + (int64_t)b * a.max_blocks + blk0;
-    for (int i = tid; i < nblk; i += kThreads) {
-      int page = bt[i];
-      if ((uint32_t)page >= (uint32_t)a.num_pages) {
-        atomicOr(a.errors, BARQ_KV_ERRBIT_BAD_INDEX);
-        page = 0;
-      }
-      sm.table[i] = page;
-    }
+  if ((uint32_t)page_j >= (uint32_t)a.num_pages) {
+    if (lane < nblk) atomicOr(a.errors, BARQ_KV_ERRBIT_BAD_INDEX);
+    page_j = 0;
   }
-
-  // Query rows in the A layout of the score MFMA: lane (row n16, k-group g) holds dims
-  // 32 * step + 8 * g .. +7 of row n16 (zero for padding rows).
-  u32x4 qv[kSteps];
-  if (n16 < M) {
-    const char* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(kvh * a.group + n16 / T) * a.q_sh +
-                     (int64_t)(n16 % T) * a.q_st + 16 * g;
-#pragma unroll
-    for (int st = 0; st < kSteps; ++st) qv[st] = *(const u32x4*)(qp + 64 * st);
-  } else {
-#pragma unroll
-    for (int st = 0; st < kSteps; ++st) qv[st] = u32x4{0, 0, 0, 0};
-  }
-  __syncthreads();
 
   const char* kbase = a.kpages + (int64_t)kvh * a.head_bytes;
   const char* vbase = a.vpages + (int64_t)kvh * a.head_bytes;
@@ -337,68 +294,42 @@ __global__ __launch_bounds__(kThreads) void attention_split_kernel(const AttnArg
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[r2][e] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  float (*lp)[kMaxRows] = sm.u.p[wave];
-
-  auto load = [&](int tc, u32x4 (&kv)[kChunkBlocks][kSteps], u32x4 (&vv)[kChunkBlocks][4]) {
-    if constexpr (UNIFORM) {
-      if (tc + kChunk <= len)
-        load_chunk_uniform<false>(a, sm, blk0, kbase, vbase, tc, len, klane, vlane, n16, g, kv, vv);
-      else
-        load_chunk_uniform<true>(a, sm, blk0, kbase, vbase, tc, len, klane, vlane, n16, g, kv, vv);
-    } else {
-      load_chunk_general(a, sm, blk0, kbase, vbase, tc, len, n16, g, kv, vv);
-    }
+  auto load = [&](int tc, u32x4 (&kv)[kSteps], u32x4 (&vv)[4]) {
+    if (tc + kBlock <= len)
+      load_chunk<UNIFORM, false>(a, page_j, blk0, kbase, vbase, tc, len, klane, vlane, n16, g, kv, vv);
+    else
+      load_chunk<UNIFORM, true>(a, page_j, blk0, kbase, vbase, tc, len, klane, vlane, n16, g, kv, vv);
   };
 
-  auto compute = [&](int tc, const u32x4 (&kv)[kChunkBlocks][kSteps], const u32x4 (&vv)[kChunkBlocks][4]) {
-    // Scores: lane (g, n16), register r = row 4g + r, position tc + 16j + n16; log2 units.
-    float x[kChunkBlocks][4];
+  auto compute = [&](int tc, const u32x4 (&kv)[kSteps], const u32x4 (&vv)[4]) {
+    // Scores: lane (g, n16), register r = row 4g + r, position tc + n16; log2 units.
+    f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < kChunkBlocks; ++j) {
-      f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int st = 0; st < kSteps; ++st) sc = mfma_qk<E>(lq[st][lane], kv[st], sc);
+    float x[4];
 #pragma unroll
-      for (int st = 0; st < kSteps; ++st) sc = mfma_qk<E>(qv[st], kv[j][st], sc);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x[j][r] = sc[r] * a.scale_log2;
-    }
+    for (int r = 0; r < 4; ++r) x[r] = sc[r] * a.scale_log2;
     // Every position of the chunk visible to every row?  Else mask (position > len - T + i).
-    if (tc + kChunk + T - 1 > len) {
+    if (tc + kBlock + T - 1 > len) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 4 * g + r;
-        const int limit = len - T + row % T;
-#pragma unroll
-        for (int j = 0; j < kChunkBlocks; ++j)
-          if (tc + kBlock * j + n16 > limit) x[j][r] = -INFINITY;
+        if (tc + n16 > len - T + row % T) x[r] = -INFINITY;
       }
     }
-
     bool rescale = false;
     float alpha[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float mx = x[0][r];
-#pragma unroll
-      for (int j = 1; j < kChunkBlocks; ++j) mx = fmaxf(mx, x[j][r]);
-      mx = row16_max(mx);
-      const float mnew = fmaxf(m_run[r], mx);
+      const float mnew = fmaxf(m_run[r], row16_max(x[r]));
       const float mu = mnew == -INFINITY ? 0.f : mnew;
       alpha[r] = __builtin_amdgcn_exp2f(m_run[r] - mu);
       rescale |= mnew != m_run[r];
-      float ps = 0.f;
-#pragma unroll
-      for (int j = 0; j < kChunkBlocks; ++j) {
-        x[j][r] = __builtin_amdgcn_exp2f(x[j][r] - mu);
-        ps += x[j][r];
-      }
-      l_part[r] = l_part[r] * alpha[r] + ps;
+      x[r] = __builtin_amdgcn_exp2f(x[r] - mu);
+      l_part[r] = l_part[r] * alpha[r] + x[r];
       m_run[r] = mnew;
     }
-    if (g < R) {
-#pragma unroll
-      for (int j = 0; j < kChunkBlocks; ++j)
-        *(f32x4*)&lp[kBlock * j + n16][4 * g] = f32x4{x[j][0], x[j][1], x[j][2], x[j][3]};
-    }
+    if (g < R) *(f32x4*)&lp[n16][4 * g] = f32x4{x[0], x[1], x[2], x[3]};
     if (__builtin_amdgcn_ballot_w64(rescale)) {
 #pragma unroll
       for (int r2 = 0; r2 < R; ++r2)
@@ -409,38 +340,32 @@ __global__ __launch_bounds__(kThreads) void attention_split_kernel(const AttnArg
           for (int e = 0; e < 8; ++e) acc[r2][e][m] *= al;
         }
     }
-
-    // P.V: lane 4b' + n of the 4x4x1 MFMA block b' takes position 4s + g of block j.
+    // P.V: lane 4b' + n of the 4x4x1 MFMA block b' takes position 4s + g of the chunk.
 #pragma unroll
-    for (int j = 0; j < kChunkBlocks; ++j) {
+    for (int s = 0; s < 4; ++s) {
+      float vf[8];
+      widen8<E>(vv[s], vf);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        float vf[8];
-        widen8<E>(vv[j][s], vf);
+      for (int r2 = 0; r2 < R; ++r2) {
+        const float pa = lp[4 * s + g][4 * r2 + (lane & 3)];
 #pragma unroll
-        for (int r2 = 0; r2 < R; ++r2) {
-          const float pa = lp[kBlock * j + 4 * s + g][4 * r2 + (lane & 3)];
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            acc[r2][e] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vf[e], acc[r2][e], 0, 0, 0);
-        }
+        for (int e = 0; e < 8; ++e)
+          acc[r2][e] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vf[e], acc[r2][e], 0, 0, 0);
       }
     }
   };
 
   // Two register buffers: the next chunk's loads are in flight while this one is computed.
-  constexpr int kStride = kChunk * kWaves;
-  u32x4 ka[kChunkBlocks][kSteps], va[kChunkBlocks][4];
-  u32x4 kb[kChunkBlocks][kSteps], vb[kChunkBlocks][4];
-  int tc = t_begin + kChunk * wave;
+  u32x4 ka[kSteps], va[4], kb[kSteps], vb[4];
+  int tc = t_begin;
   if (tc < t_end) load(tc, ka, va);
   while (tc < t_end) {
-    const int t1 = tc + kStride;
+    const int t1 = tc + kBlock;
     if (t1 < t_end) load(t1, kb, vb);
     __builtin_amdgcn_sched_barrier(0);
     compute(tc, ka, va);
     if (t1 >= t_end) break;
-    const int t2 = t1 + kStride;
+    const int t2 = t1 + kBlock;
     if (t2 < t_end) load(t2, ka, va);
     __builtin_amdgcn_sched_barrier(0);
     compute(t1, kb, vb);
@@ -462,61 +387,36 @@ __global__ __launch_bounds__(kThreads) void attention_split_kernel(const AttnArg
         acc[r2][e][m] = v;
       }
   // Lanes 0..15 now hold dims 8 * lane .. +7 of every row; lanes 16g .. 16g+15 hold the
-  // maxima and sums of rows 4g .. 4g+3.
-  __syncthreads();  // every wave is past its loop: the staging area becomes the merge area
+  // maxima and sums of rows 4g .. 4g+3.  One split: the output; else this split's record.
+  const int64_t rec = record_floats(M);
+  float* pr = a.part + ((int64_t)(b * a.kv_heads + kvh) * a.max_splits + split) * rec;
 #pragma unroll
   for (int r2 = 0; r2 < R; ++r2)
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int row = 4 * r2 + m;
-      if (row < M && lane < 16) {
-        float* dst = &sm.u.wg.acc[wave][row][8 * lane];
-        *(f32x4*)dst = f32x4{acc[r2][0][m], acc[r2][1][m], acc[r2][2][m], acc[r2][3][m]};
-        *(f32x4*)(dst + 4) = f32x4{acc[r2][4][m], acc[r2][5][m], acc[r2][6][m], acc[r2][7][m]};
+      if (row >= M) break;
+      const float mr = lane_value(m_run[m], 16 * r2);
+      const float lr = lane_value(l_part[m], 16 * r2);
+      if (nsplit == 1) {
+        if (lane < 16) {
+          const float inv = lr > 0.f ? 1.f / lr : 0.f;
+          char* o = out_row(a, b, kvh, row) + (int64_t)(8 * lane) * sizeof(OutT);
+          store_out4<OutT, E>(o, f32x4{acc[r2][0][m], acc[r2][1][m], acc[r2][2][m], acc[r2][3][m]} * inv);
+          store_out4<OutT, E>(o + 4 * sizeof(OutT),
+                              f32x4{acc[r2][4][m], acc[r2][5][m], acc[r2][6][m], acc[r2][7][m]} * inv);
+        }
+      } else {
+        if (lane < 16) {
+          float* dst = pr + (int64_t)row * kHeadDim + 8 * lane;
+          *(f32x4*)dst = f32x4{acc[r2][0][m], acc[r2][1][m], acc[r2][2][m], acc[r2][3][m]};
+          *(f32x4*)(dst + 4) = f32x4{acc[r2][4][m], acc[r2][5][m], acc[r2][6][m], acc[r2][7][m]};
+        } else if (lane == 16) {
+          pr[(int64_t)M * kHeadDim + row] = mr;
+          pr[(int64_t)M * kHeadDim + M + row] = lr;
+        }
       }
     }
-  if (n16 == 0) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 4 * g + r;
-      if (row < M) {
-        sm.u.wg.m[wave][row] = m_run[r];
-        sm.u.wg.l[wave][row] = l_part[r];
-      }
-    }
-  }
-  __syncthreads();
-
-  // Workgroup merge: thread -> 4 consecutive dims of one row; the result goes to the output
-  // (one split) or to this split's record.
-  const int64_t rec = record_floats(M);
-  float* pr = a.part + ((int64_t)pair * a.max_splits + split) * rec;
-  for (int q = tid; q < M * (kHeadDim / 4); q += kThreads) {
-    const int row = q / (kHeadDim / 4);
-    const int d4 = (q % (kHeadDim / 4)) * 4;
-    float mstar = sm.u.wg.m[0][row];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) mstar = fmaxf(mstar, sm.u.wg.m[w][row]);
-    const float mu = mstar == -INFINITY ? 0.f : mstar;
-    float lsum = 0.f;
-    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float wt = __builtin_amdgcn_exp2f(sm.u.wg.m[w][row] - mu);
-      lsum += wt * sm.u.wg.l[w][row];
-      o += wt * *(const f32x4*)&sm.u.wg.acc[w][row][d4];
-    }
-    if (nsplit == 1) {
-      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-      store_out4<OutT, E>(out_row(a, b, kvh, row) + (int64_t)d4 * sizeof(OutT), o * inv);
-    } else {
-      *(f32x4*)(pr + (int64_t)row * kHeadDim + d4) = o;
-      if (d4 == 0) {
-        pr[(int64_t)M * kHeadDim + row] = mstar;
-        pr[(int64_t)M * kHeadDim + M + row] = lsum;
-      }
-    }
-  }
 }
 
 __device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
@@ -589,9 +489,9 @@ __global__ __launch_bounds__(kThreads) void attention_merge_kernel(const AttnArg
 template <int E, int R, bool U>
 hipError_t launch_split(const AttnArgs& a, bool out_f32, dim3 grid, hipStream_t stream) {
   if (out_f32)
-    hipLaunchKernelGGL((attention_split_kernel<E, R, U, float>), grid, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((attention_split_kernel<E, R, U, float>), grid, dim3(kWave), 0, stream, a);
   else
-    hipLaunchKernelGGL((attention_split_kernel<E, R, U, uint16_t>), grid, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((attention_split_kernel<E, R, U, uint16_t>), grid, dim3(kWave), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -625,7 +525,7 @@ struct AttnPlan {
 };
 
 // Validates the geometry and sizes the launch.  max_seq bounds every row's length (0: the
-// pool's capacity); split_tokens 0 picks a split giving about kTargetWorkgroups workgroups at
+// pool's capacity); split_tokens 0 picks a split giving about kTargetWaves waves at
 // that bound.
 int plan_attention(const barq_kv_pool* pool, int64_t batch, int64_t q_heads, int64_t tokens,
                    int64_t max_seq, int64_t split_tokens, AttnPlan* plan) {
@@ -648,14 +548,14 @@ int plan_attention(const barq_kv_pool* pool, int64_t batch, int64_t q_heads, int
   if (split_tokens < 0 || split_tokens > kMaxSplitTokens) return BARQ_KV_ERR_INVALID;
   if (split_tokens == 0) {
     const int64_t pairs = std::max<int64_t>(1, batch * pool->kv_heads);
-    split_tokens = (pairs * max_seq + kTargetWorkgroups - 1) / kTargetWorkgroups;
+    split_tokens = std::max<int64_t>(kMinSplitTokens, (pairs * max_seq + kTargetWaves - 1) / kTargetWaves);
   }
-  // Whole quanta; at most kMaxSplits splits per row; the split's blocks fit the LDS table.
+  // Whole chunks; at most kMaxSplits splits per row; a split's blocks fit the lanes' table.
   split_tokens = std::max<int64_t>(split_tokens, (max_seq + kMaxSplits - 1) / kMaxSplits);
-  split_tokens = (split_tokens + kSplitQuantum - 1) / kSplitQuantum * kSplitQuantum;
-  const int64_t table_limit = (kMaxTable - 2) * pool->page_size / kSplitQuantum * kSplitQuantum;
+  split_tokens = (split_tokens + kBlock - 1) / kBlock * kBlock;
+  const int64_t table_limit = (kTableLanes - 2) * pool->page_size / kBlock * kBlock;
   if (split_tokens > table_limit) {
-    if (table_limit < kSplitQuantum || (max_seq + table_limit - 1) / table_limit > kMaxSplits)
+    if (table_limit < kBlock || (max_seq + table_limit - 1) / table_limit > kMaxSplits)
       return BARQ_KV_ERR_INVALID;
     split_tokens = table_limit;
   }

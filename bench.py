@@ -30,6 +30,13 @@ _python_append + materialised current_tensors) on one host core over the same in
 all layers and steps; larger configs: the first decode steps of layer 0).  The same run checks
 the GPU's layer-0 K/V after those steps bit for bit against it (`parity`).
 
+`paged_attention` (bf16/fp16 configurations) times the decode-attention kernel that reads K/V
+from the pages through the block table (the step the gathered K/V feed), over the pools as the
+timed run left them: one call per layer with G query heads per KV head (4, the Llama-3-8B ratio;
+8 for the 70B-class C5), captured in a graph and replayed; algorithmic bytes per call = every
+visible K and V element once + query + output.  Layer 0 is checked against an fp32 attention over
+the gathered K/V.
+
 Prints ONE JSON line.  `--pmc-probe` instead runs the eager workload the rocprof counter runs
 profile: a 64 MiB elementwise pass (calibration), the prefill, then the decode steps.
 """
@@ -64,7 +71,7 @@ CONFIGS = {
             prefill=("chunks", 16, 2048), decode=64, seed=1004, mode="graph", cpu_steps=16),
     5: dict(name="C5 70B-class single-GPU share", layers=80, batch=32, heads=8, dim=128, page=16, dtype="bfloat16",
             prefill=("uniform", 8192), decode=64, seed=1005, mode="eager", occupancy=0.9,
-            churn=(2, 4005), cpu_steps=4),
+            churn=(2, 4005), cpu_steps=4, group=8),
 }
 
 
@@ -81,6 +88,7 @@ def parse():
                     help="layers the CPU baseline runs (C1/C2 default: all)")
     ap.add_argument("--repeat", type=int, default=None, help="timed repetitions; the best is reported")
     ap.add_argument("--pmc-probe", action="store_true", help="eager run for rocprof counter passes")
+    ap.add_argument("--no-attention", action="store_true", help="skip the paged decode-attention leg")
     ap.add_argument("--bucket", type=int, default=None,
                     help="graph extent bucket in positions (default: the step's own; 0: one graph over the capacity)")
     return ap.parse_args()
@@ -245,6 +253,87 @@ class Workload:
                     pool.update(k, v)
                 else:
                     pool.append(k, v)
+
+
+def attention_leg(cfg, pools, B, dev, reps=20):
+    """Decode attention over the pools' current rows: one launch per layer, graph-replayed."""
+    import numpy as np
+    import torch
+
+    from barqtrain_amd.paged import _gpu_backend
+
+    backend = _gpu_backend()
+    H, D, L = cfg["heads"], cfg["dim"], len(pools)
+    G = cfg.get("group", 4)
+    dtype = pools[0].dtype
+    esize = torch.empty(0, dtype=dtype).element_size()
+    gen = torch.Generator(device=dev).manual_seed(cfg["seed"] + 17)
+    q = torch.randn((B, G * H, 1, D), generator=gen, device=dev).to(dtype)
+    scale = D ** -0.5
+    lens = [np.asarray(p.lens[:B]).copy() for p in pools]
+    max_seq = max(int(x.max()) for x in lens)
+    outs = [torch.empty((B, 1, G * H, D), dtype=dtype, device=dev).transpose(1, 2) for _ in pools]
+    wss = [p.attention_workspace(backend.attention_workspace_bytes(p.tensors, B, G * H, 1, max_seq, 0))
+           for p in pools]
+
+    def step():
+        for layer, pool in enumerate(pools):
+            backend.pool_decode_attention(pool.tensors, q, outs[layer], scale, max_seq, 0, wss[layer])
+
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    graph.replay()
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(3):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / reps
+        best = ms if best is None else min(best, ms)
+    io = 2 * B * G * H * D * esize  # query read + output written
+    call_bytes = [int(x.sum()) * H * D * 2 * esize + io for x in lens]
+    per_call_us = best * 1e3 / L
+    gbs = sum(call_bytes) / (best / 1e3) / 1e9
+    # layer 0 against an fp32 attention over the gathered K/V (rows 0 and B - 1)
+    k, v = pools[0].gather(B)
+    tol = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    err, ok = 0.0, True
+    for b in sorted({0, B - 1}):
+        n = int(lens[0][b])
+        kk = k[b, :, :n].float().repeat_interleave(G, 0)
+        vv = v[b, :, :n].float().repeat_interleave(G, 0)
+        sc = torch.matmul(q[b].float(), kk.transpose(1, 2).contiguous()) * scale
+        ref = torch.matmul(torch.softmax(sc, -1), vv)
+        diff = (outs[0][b].float() - ref).abs()
+        err = max(err, diff.max().item())
+        ok = ok and bool((diff <= tol * ref.abs() + 2e-5).all().item())
+    torch.cuda.synchronize()
+    if any(p.errors() for p in pools):
+        raise SystemExit("device error bits set by the attention leg")
+    gathered = 3 * (sum(call_bytes) - L * io) / L  # gather reads + writes K/V, attention re-reads
+    return {
+        "kernel": "attention_split_kernel (+ attention_merge_kernel for rows with several splits)",
+        "query_heads_per_kv_head": G,
+        "us_per_layer_call": round(per_call_us, 2),
+        "us_per_step_all_layers": round(best * 1e3, 1),
+        "achieved": round(gbs, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(gbs / HBM_PEAK_GBS, 4),
+        "bytes_per_call": int(sum(call_bytes) / L),
+        "context": f"{int(min(x.min() for x in lens))}..{max_seq}",
+        "gathered_path_bytes_per_call": int(gathered),
+        "parity": {"layer0_max_abs_err_vs_fp32": round(err, 6), "tolerance": f"{tol:g} x |ref| + 2e-5",
+                   "ok": ok},
+    }
 
 
 def main():
@@ -439,6 +528,8 @@ def main():
         result["parity"] = {"layer0_kv_bit_exact_vs_oracle": bool(
             np.array_equal(to_bits(got[0]), want[0]) and np.array_equal(to_bits(got[1]), want[1])),
             "after_decode_steps": cpu_steps}
+    if not args.no_attention and cfg["dtype"] in ("bfloat16", "float16") and D == 128:
+        result["paged_attention"] = attention_leg(cfg, pools, B, dev)
     print(json.dumps(result), flush=True)
 
 
