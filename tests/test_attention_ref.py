@@ -109,11 +109,13 @@ def test_workspace_bytes_and_rejections():
     # one record per (row, kv head, split) when a row can need more than one split:
     # rows x 128 floats + 2 x rows floats padded to a multiple of 4
     rec4 = 4 * 128 + 8
-    assert ws(ref, 2, 32, 1, 100, 0) == 0                     # one split of 256: no records
-    assert ws(ref, 2, 32, 1, 100, 64) == 0                    # 64 rounds up to 256
+    assert ws(ref, 2, 32, 1, 64, 0) == 0                      # one split of 64: no records
+    assert ws(ref, 2, 32, 1, 100, 0) == 2 * 8 * 2 * rec4 * 4  # splits of 64 (the minimum)
+    assert ws(ref, 2, 32, 1, 100, 50) == 2 * 8 * 2 * rec4 * 4  # 50 rounds up to 64
     big = ctypes.byref(_fake_pool(blocks=64))                 # capacity 1024
     assert ws(big, 2, 32, 1, 0, 256) == 2 * 8 * 4 * rec4 * 4  # 0: capacity, 4 splits
-    assert ws(big, 2, 32, 1, 600, 257) == 2 * 8 * 2 * rec4 * 4   # 257 -> 512: 2 splits
+    assert ws(big, 2, 32, 1, 600, 257) == 2 * 8 * 3 * rec4 * 4   # 257 -> 272: 3 splits
+    assert ws(big, 2, 32, 1, 1000, 4096) == 2 * 8 * 2 * rec4 * 4  # capped at 60 pages: 960
     assert ws(big, 2, 128, 1, 600, 256) == 2 * 8 * 3 * (16 * 128 + 32) * 4  # G = 16
     assert ws(big, 2, 8, 1, 600, 256) == 2 * 8 * 3 * (128 + 4) * 4  # G = 1: 2 floats -> 4
     assert ws(ref, 2, 128, 2, 100, 0) == -1   # 32 query rows per kv head
@@ -141,7 +143,7 @@ def test_workspace_bytes_and_rejections():
     assert call(query=buf + 8) == 1              # query rows not 16-byte aligned
     assert call(out=buf + 2, batch=0) == 0       # batch 0 returns before pointer checks
     assert call(out=buf + 2) == 1                # output not aligned
-    assert call(wsb=1000) == 1                   # workspace too small (4 splits of 256)
+    assert call(wsb=1000) == 1                   # workspace too small (splits of 256)
     assert call(ws=buf + 8) == 1                 # workspace not 16-byte aligned
     assert call(flags=4) == 1                    # unknown flag
     assert call(query=0) == 1                    # null query
