@@ -5,20 +5,26 @@
 //   over the positions t <= seq_lens[b] - T + i of row b (the row's own length, causal over the
 //   T new query tokens), G = q_heads / kv_heads (grouped-query attention).
 //
-// Work split (flash decoding): one wave per (row, kv head, split of `split_tokens` positions),
-// streaming the split in 16-position chunks with the next chunk's loads in flight while the
-// current one is computed.  The G*T query rows of a kv head share every K/V byte the wave loads,
-// so each byte of the row's pages is read once per launch.  A wave starts with its row length,
-// its query rows and the split's block-table entries (one per lane) in flight together; page
-// bases come from the lanes by readlane (scalar) or ds_bpermute (per lane, odd page sizes).
-// Scores come from the bf16/fp16 16x16x32 MFMA (query rows padded to 16, the chunk's positions
-// as the 16 columns).  P.V runs on the fp32 4x4x1 MFMA in 16 blocks: a lane's 16-byte load of V
-// holds 8 consecutive head dims of one position, and element e of it is the lane's B operand of
-// the e-th MFMA, so V is consumed in the layout it is stored in (no transpose, no LDS staging of
-// V) and the probabilities stay fp32.  The wave keeps a running max / sum per query row (online
-// softmax, base-2 exponent).  A row with one split is written by its wave; a row with more
-// splits gets one partial record per split, merged by a second launch (the launch boundary makes
-// the records visible: no fences, no counters).
+// Work split (flash decoding over a flat schedule): the launch has one single-wave workgroup per
+// resident wave slot of the GPU.  All (row, kv head) pairs' positions, in 16-position chunks,
+// form one row-major list; it is cut into equal ranges of chunks, one range per wave (or several,
+// grid-stride, when the caller fixes a smaller range).  Every wave therefore streams the same
+// number of bytes and every CU carries the same load, whatever the rows' lengths.  A wave walks
+// its range pair by pair ("pieces"), streaming each piece's chunks with the next chunk's loads in
+// flight while the current one is computed.  The G*T query rows of a kv head share every K/V byte
+// the wave loads, so each byte of the pages is read once per launch.
+//
+// Per piece: the block-table entries (one per lane, a sliding window of kTableEntries blocks)
+// give the page bases by readlane (scalar) or ds_bpermute (per lane, odd page sizes).  Scores
+// come from the bf16/fp16 16x16x32 MFMA (query rows padded to 16, the chunk's positions as the
+// 16 columns).  P.V runs on the fp32 4x4x1 MFMA in 16 blocks: a lane's 16-byte load of V holds 8
+// consecutive head dims of one position, and element e of it is the lane's B operand of the e-th
+// MFMA, so V is consumed in the layout it is stored in (no transpose, no LDS staging of V) and
+// the probabilities stay fp32.  Online softmax per query row (running max / sum, base-2).
+// A piece that is a whole pair writes the output; otherwise it writes a partial record, merged
+// by a second launch (the launch boundary makes the records visible: no fences, no counters).
+// Piece (range r, pair p) owns record r + p: along the schedule r and p never decrease, so no
+// two pieces share a record.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -42,12 +48,11 @@ constexpr int kSteps = kHeadDim / 32;      // k-steps of the score MFMA
 constexpr int kBlock = 16;                 // positions per chunk: one score MFMA's columns
 constexpr int kMaxRows = 16;               // query rows (G * T) one wave serves
 constexpr int kThreads = 256;              // workgroup of the merge kernel
-constexpr int kWaves = kThreads / kWave;
-constexpr int kTableLanes = 62;            // block-table entries of a split, one per lane
-constexpr int kMaxSplits = 1024;           // splits per row
-constexpr int kTargetWaves = 3072;         // the automatic split aims at about this many
-constexpr int kMinSplitTokens = 64;
-constexpr int kMaxSplitTokens = 1 << 20;
+constexpr int kTableRegs = 4;              // block-table window: lanes x registers
+constexpr int kTableEntries = kTableRegs * 64;
+constexpr int kMaxBatch = 1024;            // rows whose lengths the schedule stages in LDS
+constexpr int kMaxWaves = 2048;            // resident waves of an MI355X: 256 CUs x 4 SIMDs x 2
+constexpr int kMinRangeChunks = 4;         // the automatic range never goes below 64 positions
 
 enum : int { kBF16 = 0, kF16 = 1 };
 
@@ -62,7 +67,7 @@ struct AttnArgs {
   int64_t o_sb, o_sh, o_st;  // output strides, bytes
   const char* q;
   char* out;
-  float* part;          // [batch * kv_heads, max_splits] records of record_floats(rows)
+  float* part;          // records of record_floats(rows), indexed range + pair
   FastDiv page_div;
   int32_t row_bytes;    // bytes between positions of a page
   int32_t head_bytes;   // bytes of one head's run (head_dim elements)
@@ -73,13 +78,14 @@ struct AttnArgs {
   int32_t group;
   int32_t tokens;
   int32_t rows;
-  int32_t split_tokens;
-  int32_t max_splits;
-  int32_t capacity;     // max_blocks * page_size
+  int32_t batch;
+  int32_t max_seq;      // rows are read up to this length (longer ones are flagged)
+  int32_t range_chunks; // chunks per range (0: total / waves, at least kMinRangeChunks)
+  int32_t waves;        // the launch's waves (one per resident slot)
   float scale_log2;     // softmax scale * log2(e)
 };
 
-// A split's partial: rows x head_dim unnormalised sums, then the rows' running maxima and sums,
+// A piece's partial: rows x head_dim unnormalised sums, then the rows' running maxima and sums,
 // padded to whole 16-byte vectors.
 __host__ __device__ constexpr int64_t record_floats(int64_t rows) {
   return rows * kHeadDim + (2 * rows + 3) / 4 * 4;
@@ -160,94 +166,148 @@ __device__ __forceinline__ void store_out4(char* p, const f32x4 v) {
   }
 }
 
-// Row b's visible length as the launch covers it, and its number of splits.
-__device__ __forceinline__ int row_length(const AttnArgs& a, int b, bool report) {
-  int len = a.seq_lens[b];
-  if (len > a.capacity) {
-    if (report) atomicOr(a.errors, BARQ_KV_ERRBIT_CAPACITY);
-    len = a.capacity;
-  }
-  const int cap = a.max_splits * a.split_tokens;
-  if (len > cap) {
-    if (report) atomicOr(a.errors, BARQ_KV_ERRBIT_ATTN_SHORT);
-    len = cap;
-  }
-  return len < 0 ? 0 : len;
-}
-
 __device__ __forceinline__ char* out_row(const AttnArgs& a, int b, int kvh, int row) {
   const int hl = row / a.tokens;
   const int i = row - hl * a.tokens;
   return a.out + (int64_t)b * a.o_sb + (int64_t)(kvh * a.group + hl) * a.o_sh + (int64_t)i * a.o_st;
 }
 
+// The schedule, computed identically by both kernels from seq_lens: s_len[b] = row b's length
+// (clamped to max_seq; longer rows are flagged once), s_incl[b] = chunks of rows 0..b times
+// kv_heads.  Run by one wave; returns the total number of chunks.
+__device__ int scan_rows(const AttnArgs& a, int lane, int* s_len, int* s_incl, bool report) {
+  int base = 0;
+  for (int g0 = 0; g0 < a.batch; g0 += kWave) {
+    const int b = g0 + lane;
+    int len = 0;
+    if (b < a.batch) {
+      len = a.seq_lens[b];
+      if (len > a.max_seq) {
+        if (report) atomicOr(a.errors, BARQ_KV_ERRBIT_ATTN_SHORT);
+        len = a.max_seq;
+      }
+      len = len < 0 ? 0 : len;
+    }
+    int v = (len + kBlock - 1) / kBlock * a.kv_heads;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int u = __shfl_up(v, o, kWave);
+      if (lane >= o) v += u;
+    }
+    if (b < a.batch) {
+      s_len[b] = len;
+      s_incl[b] = base + v;
+    }
+    base += __shfl(v, kWave - 1, kWave);
+  }
+  return base;
+}
+
+__device__ __forceinline__ int range_chunks(const AttnArgs& a, int total) {
+  if (a.range_chunks > 0) return a.range_chunks;
+  return max(kMinRangeChunks, (total + a.waves - 1) / a.waves);
+}
+
+// The row holding chunk c: the first b with s_incl[b] > c (c < total).
+__device__ __forceinline__ int find_row(const int* s_incl, int batch, int c) {
+  int lo = 0, hi = batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (s_incl[mid] > c) hi = mid; else lo = mid + 1;
+  }
+  return lo;
+}
+
+// Page of block blk0 + idx from the lanes' table window: idx uniform (a scalar) ...
+__device__ __forceinline__ int table_scalar(const int (&pt)[kTableRegs], int idx) {
+  int page = __builtin_amdgcn_readlane(pt[0], idx & 63);
+#pragma unroll
+  for (int k = 1; k < kTableRegs; ++k)
+    if ((idx >> 6) == k) page = __builtin_amdgcn_readlane(pt[k], idx & 63);
+  return page;
+}
+// ... or per lane (every lane active).
+__device__ __forceinline__ int table_lane(const int (&pt)[kTableRegs], int idx) {
+  int page = 0;
+#pragma unroll
+  for (int k = 0; k < kTableRegs; ++k) {
+    const int v = __builtin_amdgcn_ds_bpermute((idx & 63) << 2, pt[k]);
+    page = (idx >> 6) == k ? v : page;
+  }
+  return page;
+}
+
+// Block-table window of row b: lane j of pt[k] holds block blk0 + 64k + j, for the blocks
+// [blk0, blk_end) the piece reads.  An entry that names no page of the pool is recorded and read
+// as page 0, so no access leaves the pool.
+__device__ __forceinline__ void load_table(const AttnArgs& a, int b, int blk0, int blk_end, int lane,
+                                           int (&pt)[kTableRegs]) {
+  const int n = min(kTableEntries, min(blk_end, a.max_blocks) - blk0);
+#pragma unroll
+  for (int k = 0; k < kTableRegs; ++k) {
+    int page = 64 * k + lane < n ? a.block_table[(int64_t)b * a.max_blocks + blk0 + 64 * k + lane] : 0;
+    if ((uint32_t)page >= (uint32_t)a.num_pages) {
+      atomicOr(a.errors, BARQ_KV_ERRBIT_BAD_INDEX);
+      page = 0;
+    }
+    pt[k] = page;
+  }
+}
+
 // K and V of one 16-position chunk for this lane.  K: lane (g, n16) holds dims 32 * step + 8 * g
-// .. +7 of position tc + n16; V: dims 8 * n16 .. +7 of position tc + 4s + g.  Positions >= len
-// load nothing and read as zero.  page_j: lane j holds the page of block blk0 + j.
+// .. +7 of position tc + n16; V: dims 8 * n16 .. +7 of position tc + 4s + g.  Positions >= end
+// load nothing and read as zero.
 template <bool UNIFORM, bool PRED>
-__device__ __forceinline__ void load_chunk(const AttnArgs& a, int page_j, int blk0, const char* kbase,
-                                           const char* vbase, int tc, int len, int klane, int vlane,
-                                           int n16, int g, u32x4 (&kv)[kSteps], u32x4 (&vv)[4]) {
+__device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kTableRegs], int blk0,
+                                           const char* kbase, const char* vbase, int tc, int end,
+                                           int klane, int vlane, int n16, int g, u32x4 (&kv)[kSteps],
+                                           u32x4 (&vv)[4]) {
   if constexpr (UNIFORM) {
     // page_size is a multiple of 16: the chunk lies in one page, its base a scalar.
     const uint32_t blk = a.page_div.div((uint32_t)tc);
-    const int page = __builtin_amdgcn_readlane(page_j, (int)blk - blk0);
+    const int page = table_scalar(pt, (int)blk - blk0);
     const int64_t base = (int64_t)page * a.page_bytes +
                          (int64_t)(tc - (int)(blk * (uint32_t)a.page_size)) * a.row_bytes;
     const char* kp = kbase + base + klane;
     const char* vp = vbase + base + vlane;
 #pragma unroll
     for (int st = 0; st < kSteps; ++st)
-      kv[st] = (!PRED || tc + n16 < len) ? ld_page(kp + 64 * st) : u32x4{0, 0, 0, 0};
+      kv[st] = (!PRED || tc + n16 < end) ? ld_page(kp + 64 * st) : u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      vv[s] = (!PRED || tc + 4 * s + g < len) ? ld_page(vp + 4 * s * a.row_bytes) : u32x4{0, 0, 0, 0};
+      vv[s] = (!PRED || tc + 4 * s + g < end) ? ld_page(vp + 4 * s * a.row_bytes) : u32x4{0, 0, 0, 0};
   } else {
-    // Any page size: each lane finds the page of its own positions (lane-indexed table read,
-    // all lanes active).
-    const int tk = min(tc + n16, len - 1);
+    const int tk = min(tc + n16, end - 1);
     const uint32_t bk = a.page_div.div((uint32_t)tk);
-    const int pk = __builtin_amdgcn_ds_bpermute(((int)bk - blk0) << 2, page_j);
+    const int pk = table_lane(pt, (int)bk - blk0);
     const char* kp = kbase + (int64_t)pk * a.page_bytes +
                      (int64_t)(tk - (int)(bk * (uint32_t)a.page_size)) * a.row_bytes + 16 * g;
 #pragma unroll
     for (int st = 0; st < kSteps; ++st)
-      kv[st] = tc + n16 < len ? ld_page(kp + 64 * st) : u32x4{0, 0, 0, 0};
+      kv[st] = tc + n16 < end ? ld_page(kp + 64 * st) : u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const int tv = min(tc + 4 * s + g, len - 1);
+      const int tv = min(tc + 4 * s + g, end - 1);
       const uint32_t bv = a.page_div.div((uint32_t)tv);
-      const int pv = __builtin_amdgcn_ds_bpermute(((int)bv - blk0) << 2, page_j);
+      const int pv = table_lane(pt, (int)bv - blk0);
       const char* vp = vbase + (int64_t)pv * a.page_bytes +
                        (int64_t)(tv - (int)(bv * (uint32_t)a.page_size)) * a.row_bytes + 16 * n16;
-      vv[s] = tc + 4 * s + g < len ? ld_page(vp) : u32x4{0, 0, 0, 0};
+      vv[s] = tc + 4 * s + g < end ? ld_page(vp) : u32x4{0, 0, 0, 0};
     }
   }
 }
 
-// One wave per (split, kv head, row).  UNIFORM: page_size is a multiple of 16.
-// R: groups of 4 query rows (rows <= 4 * R).
+// One piece: positions [t_begin, t_end) of (row b, kv head kvh), row length len.  whole: the
+// piece is the whole pair (write the output), else write record `rec_id`.
 template <int E, int R, bool UNIFORM, typename OutT>
-__global__ __launch_bounds__(kWave) void attention_split_kernel(const AttnArgs a) {
-  __shared__ float lp[kBlock][kMaxRows];  // probabilities, staged for the P.V operand layout
-  __shared__ u32x4 lq[kSteps][kWave];     // the query fragments, re-read for every chunk
-
+__device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u32x4 (&lq)[kSteps][kWave],
+                             int b, int kvh, int len, int t_begin, int t_end, bool whole, int64_t rec_id) {
   const int lane = threadIdx.x;
   const int n16 = lane & 15;
   const int g = lane >> 4;
-  const int split = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
   const int M = a.rows;
   const int T = a.tokens;
-  const int t_begin = split * a.split_tokens;
 
-  // Issued together: the split's block-table entries (lane j: block blk0 + j, read whether or
-  // not the row reaches it), the query rows and the row length.
-  const int blk0 = (int)a.page_div.div((uint32_t)t_begin);
-  int page_j = 0;
-  if (lane < kTableLanes && blk0 + lane < a.max_blocks)
-    page_j = a.block_table[(int64_t)b * a.max_blocks + blk0 + lane];
   // Query rows in the A layout of the score MFMA: lane (row n16, k-group g) holds dims
   // 32 * step + 8 * g .. +7 of row n16 (zero for padding rows); kept in LDS.
   {
@@ -264,18 +324,10 @@ __global__ __launch_bounds__(kWave) void attention_split_kernel(const AttnArgs a
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) lq[st][lane] = qv[st];
   }
-  const int len = row_length(a, b, split == 0 && kvh == 0 && lane == 0);
-  const int nsplit = len == 0 ? 1 : (len + a.split_tokens - 1) / a.split_tokens;
-  if (split >= nsplit) return;
-  const int t_end = min(len, t_begin + a.split_tokens);
-
-  // The entries the split uses name pages of the pool; one that does not is recorded and read
-  // as page 0, so no access leaves the pool.
-  const int nblk = t_end > t_begin ? (int)a.page_div.div((uint32_t)(t_end - 1)) - blk0 + 1 : 0;
-  if ((uint32_t)page_j >= (uint32_t)a.num_pages) {
-    if (lane < nblk) atomicOr(a.errors, BARQ_KV_ERRBIT_BAD_INDEX);
-    page_j = 0;
-  }
+  int blk0 = (int)a.page_div.div((uint32_t)t_begin);
+  const int blk_end = t_end > t_begin ? (int)a.page_div.div((uint32_t)(t_end - 1)) + 1 : blk0;
+  int pt[kTableRegs];
+  load_table(a, b, blk0, blk_end, lane, pt);
 
   const char* kbase = a.kpages + (int64_t)kvh * a.head_bytes;
   const char* vbase = a.vpages + (int64_t)kvh * a.head_bytes;
@@ -295,10 +347,16 @@ __global__ __launch_bounds__(kWave) void attention_split_kernel(const AttnArgs a
     for (int e = 0; e < 8; ++e) acc[r2][e] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto load = [&](int tc, u32x4 (&kv)[kSteps], u32x4 (&vv)[4]) {
-    if (tc + kBlock <= len)
-      load_chunk<UNIFORM, false>(a, page_j, blk0, kbase, vbase, tc, len, klane, vlane, n16, g, kv, vv);
+    // Slide the table window when the chunk's last block leaves it (every 254+ blocks).
+    const int last = (int)a.page_div.div((uint32_t)min(tc + kBlock, t_end) - 1u);
+    if (last - blk0 >= kTableEntries) {
+      blk0 = (int)a.page_div.div((uint32_t)tc);
+      load_table(a, b, blk0, blk_end, lane, pt);
+    }
+    if (tc + kBlock <= t_end)
+      load_chunk<UNIFORM, false>(a, pt, blk0, kbase, vbase, tc, t_end, klane, vlane, n16, g, kv, vv);
     else
-      load_chunk<UNIFORM, true>(a, page_j, blk0, kbase, vbase, tc, len, klane, vlane, n16, g, kv, vv);
+      load_chunk<UNIFORM, true>(a, pt, blk0, kbase, vbase, tc, t_end, klane, vlane, n16, g, kv, vv);
   };
 
   auto compute = [&](int tc, const u32x4 (&kv)[kSteps], const u32x4 (&vv)[4]) {
@@ -360,16 +418,15 @@ __global__ __launch_bounds__(kWave) void attention_split_kernel(const AttnArgs a
   int tc = t_begin;
   if (tc < t_end) load(tc, ka, va);
   while (tc < t_end) {
-    const int t1 = tc + kBlock;
-    if (t1 < t_end) load(t1, kb, vb);
+    if (tc + kBlock < t_end) load(tc + kBlock, kb, vb);
     __builtin_amdgcn_sched_barrier(0);
     compute(tc, ka, va);
-    if (t1 >= t_end) break;
-    const int t2 = t1 + kBlock;
-    if (t2 < t_end) load(t2, ka, va);
+    tc += kBlock;
+    if (tc >= t_end) break;
+    if (tc + kBlock < t_end) load(tc + kBlock, ka, va);
     __builtin_amdgcn_sched_barrier(0);
-    compute(t1, kb, vb);
-    tc = t2;
+    compute(tc, kb, vb);
+    tc += kBlock;
   }
 
   // Row sums across the 16 lanes of each row group; P.V partials across the 4 position slots.
@@ -387,9 +444,9 @@ __global__ __launch_bounds__(kWave) void attention_split_kernel(const AttnArgs a
         acc[r2][e][m] = v;
       }
   // Lanes 0..15 now hold dims 8 * lane .. +7 of every row; lanes 16g .. 16g+15 hold the
-  // maxima and sums of rows 4g .. 4g+3.  One split: the output; else this split's record.
+  // maxima and sums of rows 4g .. 4g+3.
   const int64_t rec = record_floats(M);
-  float* pr = a.part + ((int64_t)(b * a.kv_heads + kvh) * a.max_splits + split) * rec;
+  float* pr = a.part + rec_id * rec;
 #pragma unroll
   for (int r2 = 0; r2 < R; ++r2)
 #pragma unroll
@@ -398,7 +455,7 @@ __global__ __launch_bounds__(kWave) void attention_split_kernel(const AttnArgs a
       if (row >= M) break;
       const float mr = lane_value(m_run[m], 16 * r2);
       const float lr = lane_value(l_part[m], 16 * r2);
-      if (nsplit == 1) {
+      if (whole) {
         if (lane < 16) {
           const float inv = lr > 0.f ? 1.f / lr : 0.f;
           char* o = out_row(a, b, kvh, row) + (int64_t)(8 * lane) * sizeof(OutT);
@@ -419,150 +476,206 @@ __global__ __launch_bounds__(kWave) void attention_split_kernel(const AttnArgs a
     }
 }
 
-__device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) {
-    const float u = __shfl_xor(v, o, kWave);
-    v = is_max ? fmaxf(v, u) : v + u;
+// One wave per workgroup, one workgroup per resident slot: ranges r = blockIdx.x, + gridDim.x,
+// ... of the flat chunk list.  UNIFORM: page_size is a multiple of 16.  R: groups of 4 query
+// rows (rows <= 4 * R).
+template <int E, int R, bool UNIFORM, typename OutT>
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(R <= 2 ? 2 : 1, R <= 2 ? 2 : 1)))
+void attention_flat_kernel(const AttnArgs a) {
+  __shared__ float lp[kBlock][kMaxRows];   // probabilities, staged for the P.V operand layout
+  __shared__ u32x4 lq[kSteps][kWave];      // the piece's query fragments
+  __shared__ int s_len[kMaxBatch];
+  __shared__ int s_incl[kMaxBatch];
+
+  const int lane = threadIdx.x;
+  const int total = scan_rows(a, lane, s_len, s_incl, blockIdx.x == 0 && lane == 0);
+  const int per = range_chunks(a, total);
+  for (int r = blockIdx.x; (int64_t)r * per < total; r += gridDim.x) {
+    int c = r * per;
+    const int c_end = min(total, c + per);
+    while (c < c_end) {
+      const int b = find_row(s_incl, a.batch, c);
+      const int row_first = b > 0 ? s_incl[b - 1] : 0;
+      const int len = s_len[b];
+      const int nch = (len + kBlock - 1) / kBlock;
+      const int kvh = (c - row_first) / nch;
+      const int pair_first = row_first + kvh * nch;
+      const int k0 = c - pair_first;
+      const int piece_end = min(c_end, pair_first + nch);
+      const bool whole = k0 == 0 && piece_end == pair_first + nch;
+      attend_piece<E, R, UNIFORM, OutT>(a, lp, lq, b, kvh, len, kBlock * k0,
+                                        min(len, kBlock * (k0 + piece_end - c)), whole,
+                                        (int64_t)r + (int64_t)b * a.kv_heads + kvh);
+      c = piece_end;
+    }
   }
-  const int wave = threadIdx.x / kWave;
-  __syncthreads();
-  if ((threadIdx.x & (kWave - 1)) == 0) red[wave] = v;
-  __syncthreads();
-  v = red[0];
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) v = is_max ? fmaxf(v, red[w]) : v + red[w];
-  return v;
 }
 
-// Merge of one query row's split records: one workgroup per (row, kv head, batch row).
+// Merge of one query row's records: one workgroup per (row, kv head, batch row).  Thread
+// (quad, class) folds the records class, class + 8, ... into a running (max, sum, 4 dims) --
+// every record load is independent -- and the 8 classes are folded through LDS.  Rows of
+// length 0 get zeros here; pairs inside one range were written by their wave.
 template <int E, typename OutT>
 __global__ __launch_bounds__(kThreads) void attention_merge_kernel(const AttnArgs a) {
-  __shared__ float w[kMaxSplits];
-  __shared__ float red[kWaves];
-  __shared__ f32x4 part[kThreads];
+  constexpr int kQuads = kHeadDim / 4;
+  constexpr int kClasses = kThreads / kQuads;
+  __shared__ int s_len[kMaxBatch];
+  __shared__ int s_incl[kMaxBatch];
+  __shared__ int s_total;
+  __shared__ f32x4 po[kThreads];
+  __shared__ float pm[kThreads];
+  __shared__ float pl[kThreads];
 
   const int tid = threadIdx.x;
   const int row = blockIdx.x;
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
-  const int len = row_length(a, b, false);
-  const int nsplit = len == 0 ? 1 : (len + a.split_tokens - 1) / a.split_tokens;
-  if (nsplit <= 1) return;  // written by its split workgroup
+  if (tid < kWave) {
+    const int total = scan_rows(a, tid, s_len, s_incl, false);
+    if (tid == 0) s_total = total;
+  }
+  __syncthreads();
+  const int per = range_chunks(a, s_total);
+  const int nch = (s_len[b] + kBlock - 1) / kBlock;
+  const int pair_first = (b > 0 ? s_incl[b - 1] : 0) + kvh * nch;
+  if (nch == 0) {
+    if (tid < kQuads)
+      store_out4<OutT, E>(out_row(a, b, kvh, row) + (int64_t)(4 * tid) * sizeof(OutT), f32x4{0.f, 0.f, 0.f, 0.f});
+    return;
+  }
+  const int r_first = pair_first / per;
+  const int r_last = (pair_first + nch - 1) / per;
+  if (r_first == r_last) return;
 
   const int M = a.rows;
   const int64_t rec = record_floats(M);
-  const float* base = a.part + (int64_t)(b * a.kv_heads + kvh) * a.max_splits * rec;
-  const float* ml = base + (int64_t)M * kHeadDim;
-
-  float mx = -INFINITY;
-  for (int s = tid; s < nsplit; s += kThreads) mx = fmaxf(mx, ml[s * rec + row]);
-  mx = block_reduce(mx, red, true);
-  const float mu = mx == -INFINITY ? 0.f : mx;
-  float ls = 0.f;
-  for (int s = tid; s < nsplit; s += kThreads) {
-    const float wt = __builtin_amdgcn_exp2f(ml[s * rec + row] - mu);
-    w[s] = wt;
-    ls += wt * ml[s * rec + M + row];
-  }
-  ls = block_reduce(ls, red, false);  // its barriers also publish w[]
-
-  // Thread -> (4 dims, one of 8 residue classes of splits); the classes are summed in LDS.
-  constexpr int kQuads = kHeadDim / 4;
-  constexpr int kClasses = kThreads / kQuads;
+  const int64_t p = (int64_t)b * a.kv_heads + kvh;
   const int quad = tid % kQuads;
   const int cls = tid / kQuads;
-  const float* src = base + (int64_t)row * kHeadDim + 4 * quad;
-  f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+  float mt = -INFINITY, lt = 0.f;
+  f32x4 ot = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
-  for (int s = cls; s < nsplit; s += kClasses) o += w[s] * *(const f32x4*)(src + s * rec);
-  part[tid] = o;
+  for (int r = r_first + cls; r <= r_last; r += kClasses) {
+    const float* rp = a.part + (r + p) * rec;
+    const float ms = rp[(int64_t)M * kHeadDim + row];
+    const float ls = rp[(int64_t)M * kHeadDim + M + row];
+    const f32x4 os = *(const f32x4*)(rp + (int64_t)row * kHeadDim + 4 * quad);
+    const float mn = fmaxf(mt, ms);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float wo = __builtin_amdgcn_exp2f(mt - mu);
+    const float ws = __builtin_amdgcn_exp2f(ms - mu);
+    lt = lt * wo + ls * ws;
+    ot = ot * wo + os * ws;
+    mt = mn;
+  }
+  po[tid] = ot;
+  pm[tid] = mt;
+  pl[tid] = lt;
   __syncthreads();
   if (tid < kQuads) {
+    float mstar = pm[tid];
 #pragma unroll
-    for (int c = 1; c < kClasses; ++c) o += part[tid + c * kQuads];
-    const float inv = ls > 0.f ? 1.f / ls : 0.f;
+    for (int c = 1; c < kClasses; ++c) mstar = fmaxf(mstar, pm[tid + c * kQuads]);
+    const float mu = mstar == -INFINITY ? 0.f : mstar;
+    float l = 0.f;
+    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < kClasses; ++c) {
+      const float w = __builtin_amdgcn_exp2f(pm[tid + c * kQuads] - mu);
+      l += w * pl[tid + c * kQuads];
+      o += w * po[tid + c * kQuads];
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
     store_out4<OutT, E>(out_row(a, b, kvh, row) + (int64_t)(4 * quad) * sizeof(OutT), o * inv);
   }
 }
 
-template <int E, int R, bool U>
-hipError_t launch_split(const AttnArgs& a, bool out_f32, dim3 grid, hipStream_t stream) {
-  if (out_f32)
-    hipLaunchKernelGGL((attention_split_kernel<E, R, U, float>), grid, dim3(kWave), 0, stream, a);
-  else
-    hipLaunchKernelGGL((attention_split_kernel<E, R, U, uint16_t>), grid, dim3(kWave), 0, stream, a);
+// Resident waves of a kernel on the current device (cached per instantiation).
+template <typename K>
+int resident_waves(K kernel) {
+  static int waves = 0;
+  if (waves == 0) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kWave, 0) != hipSuccess)
+      return kMaxWaves;
+    waves = std::min(std::max(cus * per_cu, 1), kMaxWaves);
+  }
+  return waves;
+}
+
+template <int E, int R, bool U, typename OutT>
+hipError_t launch_typed(AttnArgs a, bool merge, hipStream_t stream) {
+  auto* k = attention_flat_kernel<E, R, U, OutT>;
+  a.waves = resident_waves(k);
+  hipLaunchKernelGGL(k, dim3((unsigned)a.waves), dim3(kWave), 0, stream, a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || !merge) return err;
+  hipLaunchKernelGGL((attention_merge_kernel<E, OutT>), dim3((unsigned)a.rows, (unsigned)a.kv_heads, (unsigned)a.batch),
+                     dim3(kThreads), 0, stream, a);
   return hipGetLastError();
+}
+
+template <int E, int R, bool U>
+hipError_t launch_out(const AttnArgs& a, bool out_f32, bool merge, hipStream_t stream) {
+  return out_f32 ? launch_typed<E, R, U, float>(a, merge, stream)
+                 : launch_typed<E, R, U, uint16_t>(a, merge, stream);
 }
 
 template <int E>
-hipError_t launch_dtype(const AttnArgs& a, bool uniform, bool out_f32, dim3 grid, hipStream_t stream) {
+hipError_t launch_dtype(const AttnArgs& a, bool uniform, bool out_f32, bool merge, hipStream_t stream) {
   const int groups = (a.rows + 3) / 4;
-  hipError_t err;
   if (uniform) {
-    err = groups == 1   ? launch_split<E, 1, true>(a, out_f32, grid, stream)
-          : groups == 2 ? launch_split<E, 2, true>(a, out_f32, grid, stream)
-                        : launch_split<E, 4, true>(a, out_f32, grid, stream);
-  } else {
-    err = groups == 1   ? launch_split<E, 1, false>(a, out_f32, grid, stream)
-          : groups == 2 ? launch_split<E, 2, false>(a, out_f32, grid, stream)
-                        : launch_split<E, 4, false>(a, out_f32, grid, stream);
+    return groups == 1   ? launch_out<E, 1, true>(a, out_f32, merge, stream)
+           : groups == 2 ? launch_out<E, 2, true>(a, out_f32, merge, stream)
+                         : launch_out<E, 4, true>(a, out_f32, merge, stream);
   }
-  if (err != hipSuccess || a.max_splits == 1) return err;
-  const dim3 mgrid((unsigned)a.rows, grid.y, grid.z);
-  if (out_f32)
-    hipLaunchKernelGGL((attention_merge_kernel<E, float>), mgrid, dim3(kThreads), 0, stream, a);
-  else
-    hipLaunchKernelGGL((attention_merge_kernel<E, uint16_t>), mgrid, dim3(kThreads), 0, stream, a);
-  return hipGetLastError();
+  return groups == 1   ? launch_out<E, 1, false>(a, out_f32, merge, stream)
+         : groups == 2 ? launch_out<E, 2, false>(a, out_f32, merge, stream)
+                       : launch_out<E, 4, false>(a, out_f32, merge, stream);
 }
 
 struct AttnPlan {
-  int64_t split_tokens;
-  int64_t max_splits;
   int64_t rows;
+  int64_t max_seq;
+  int64_t range_chunks;  // 0: automatic
+  int64_t records;       // record slots the workspace holds
   int64_t bytes;
 };
 
-// Validates the geometry and sizes the launch.  max_seq bounds every row's length (0: the
-// pool's capacity); split_tokens 0 picks a split giving about kTargetWaves waves at
-// that bound.
+// Validates the geometry and sizes the workspace.  max_seq bounds every row's length (0: the
+// pool's capacity); split_tokens fixes the positions of a range (rounded up to 16; 0: the flat
+// schedule's own, total / resident waves).
 int plan_attention(const barq_kv_pool* pool, int64_t batch, int64_t q_heads, int64_t tokens,
                    int64_t max_seq, int64_t split_tokens, AttnPlan* plan) {
   if (!pool || pool->elem_bytes != 2 || pool->head_dim != kHeadDim || pool->kv_heads <= 0 ||
       pool->page_size <= 0 || pool->max_blocks <= 0 || pool->num_pages <= 0 ||
       pool->num_pages > INT32_MAX || pool->max_batch <= 0)
     return BARQ_KV_ERR_INVALID;
-  if (batch < 0 || batch > pool->max_batch || tokens <= 0 || q_heads <= 0 ||
+  if (batch < 0 || batch > pool->max_batch || batch > kMaxBatch || tokens <= 0 || q_heads <= 0 ||
       q_heads % pool->kv_heads != 0)
     return BARQ_KV_ERR_INVALID;
   const int64_t rows = (q_heads / pool->kv_heads) * tokens;
   if (rows > kMaxRows) return BARQ_KV_ERR_INVALID;
   const int64_t capacity = pool->max_blocks * pool->page_size;
   const int64_t row_bytes = pool->kv_heads * kHeadDim * 2;
-  // Lane offsets within a page are 32-bit; grid dimensions are 16-bit.
-  if (capacity > INT32_MAX / 2 || row_bytes * pool->page_size > INT32_MAX / 2 ||
-      pool->kv_heads > 65535 || pool->max_batch > 65535)
-    return BARQ_KV_ERR_INVALID;
   if (max_seq <= 0 || max_seq > capacity) max_seq = capacity;
-  if (split_tokens < 0 || split_tokens > kMaxSplitTokens) return BARQ_KV_ERR_INVALID;
-  if (split_tokens == 0) {
-    const int64_t pairs = std::max<int64_t>(1, batch * pool->kv_heads);
-    split_tokens = std::max<int64_t>(kMinSplitTokens, (pairs * max_seq + kTargetWaves - 1) / kTargetWaves);
-  }
-  // Whole chunks; at most kMaxSplits splits per row; a split's blocks fit the lanes' table.
-  split_tokens = std::max<int64_t>(split_tokens, (max_seq + kMaxSplits - 1) / kMaxSplits);
-  split_tokens = (split_tokens + kBlock - 1) / kBlock * kBlock;
-  const int64_t table_limit = (kTableLanes - 2) * pool->page_size / kBlock * kBlock;
-  if (split_tokens > table_limit) {
-    if (table_limit < kBlock || (max_seq + table_limit - 1) / table_limit > kMaxSplits)
-      return BARQ_KV_ERR_INVALID;
-    split_tokens = table_limit;
-  }
-  plan->split_tokens = split_tokens;
-  plan->max_splits = (max_seq + split_tokens - 1) / split_tokens;
+  // Lane offsets within a page are 32-bit; chunk indices of the whole schedule fit 31 bits.
+  const int64_t pairs = batch * pool->kv_heads;
+  const int64_t max_chunks = pairs * ((max_seq + kBlock - 1) / kBlock);
+  if (capacity > INT32_MAX / 2 || row_bytes * pool->page_size > INT32_MAX / 2 ||
+      max_chunks > INT32_MAX / 2 || pool->kv_heads > 65535)
+    return BARQ_KV_ERR_INVALID;
+  if (split_tokens < 0 || split_tokens > INT32_MAX / 2) return BARQ_KV_ERR_INVALID;
+  const int64_t chunks = split_tokens > 0 ? (split_tokens + kBlock - 1) / kBlock : 0;
+  // Ranges: at most kMaxWaves automatically, else as many as the fixed range length gives.
+  const int64_t ranges = chunks > 0 ? (max_chunks + chunks - 1) / chunks : kMaxWaves;
   plan->rows = rows;
-  plan->bytes = plan->max_splits > 1 ? batch * pool->kv_heads * plan->max_splits * record_floats(rows) * 4 : 0;
+  plan->max_seq = max_seq;
+  plan->range_chunks = chunks;
+  plan->records = ranges + pairs;
+  plan->bytes = plan->records * record_floats(rows) * 4;
   return BARQ_KV_OK;
 }
 
@@ -591,8 +704,8 @@ int barq_kv_decode_attention(const barq_kv_pool* pool, const void* query, int64_
   if (flags & ~(int64_t)(BARQ_KV_ATTN_FP16 | BARQ_KV_ATTN_OUT_F32)) return BARQ_KV_ERR_INVALID;
   if (batch == 0) return BARQ_KV_OK;
   const int64_t out_elem = (flags & BARQ_KV_ATTN_OUT_F32) ? 4 : 2;
-  if (!query || !out || (plan.bytes > 0 && !workspace) || workspace_bytes < plan.bytes ||
-      !pool->key_pages || !pool->value_pages || !pool->block_table || !pool->seq_lens || !pool->ctrl)
+  if (!query || !out || !workspace || workspace_bytes < plan.bytes || !pool->key_pages ||
+      !pool->value_pages || !pool->block_table || !pool->seq_lens || !pool->ctrl)
     return BARQ_KV_ERR_INVALID;
   // 16-byte query rows and 4-element output runs must be aligned for the vector accesses.
   const int64_t qs[3] = {q_stride_b, q_stride_h, q_stride_t};
@@ -603,7 +716,6 @@ int barq_kv_decode_attention(const barq_kv_pool* pool, const void* query, int64_
   if (((uintptr_t)query | (uintptr_t)pool->key_pages | (uintptr_t)pool->value_pages) % 16 != 0 ||
       (uintptr_t)out % (out_elem * 4) != 0 || (uintptr_t)workspace % 16 != 0)
     return BARQ_KV_ERR_INVALID;
-  if (plan.max_splits > 65535) return BARQ_KV_ERR_INVALID;
 
   AttnArgs a;
   a.kpages = (const char*)pool->key_pages;
@@ -631,17 +743,18 @@ int barq_kv_decode_attention(const barq_kv_pool* pool, const void* query, int64_
   a.group = (int32_t)(q_heads / pool->kv_heads);
   a.tokens = (int32_t)tokens;
   a.rows = (int32_t)plan.rows;
-  a.split_tokens = (int32_t)plan.split_tokens;
-  a.max_splits = (int32_t)plan.max_splits;
-  a.capacity = (int32_t)(pool->max_blocks * pool->page_size);
+  a.batch = (int32_t)batch;
+  a.max_seq = (int32_t)plan.max_seq;
+  a.range_chunks = (int32_t)plan.range_chunks;
+  a.waves = kMaxWaves;
   a.scale_log2 = scale * 1.4426950408889634f;
 
-  const dim3 grid((unsigned)plan.max_splits, (unsigned)pool->kv_heads, (unsigned)batch);
   const bool uniform = pool->page_size % kBlock == 0;
   const bool out_f32 = (flags & BARQ_KV_ATTN_OUT_F32) != 0;
-  const hipError_t err = (flags & BARQ_KV_ATTN_FP16)
-                             ? launch_dtype<kF16>(a, uniform, out_f32, grid, (hipStream_t)stream)
-                             : launch_dtype<kBF16>(a, uniform, out_f32, grid, (hipStream_t)stream);
+  const hipError_t err =
+      (flags & BARQ_KV_ATTN_FP16)
+          ? launch_dtype<kF16>(a, uniform, out_f32, true, (hipStream_t)stream)
+          : launch_dtype<kBF16>(a, uniform, out_f32, true, (hipStream_t)stream);
   return err == hipSuccess ? BARQ_KV_OK : BARQ_KV_ERR_LAUNCH;
 }
 

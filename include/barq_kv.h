@@ -198,13 +198,14 @@ int64_t barq_kv_attention_workspace_bytes(const barq_kv_pool* pool, int64_t batc
  * zeros.  query: [batch, q_heads, tokens, 128] of the pool's type, element strides (q_stride_b,
  * q_stride_h, q_stride_t), 16-byte aligned rows; out: [batch, q_heads, tokens, 128] of the
  * pool's type or float32 (BARQ_KV_ATTN_OUT_F32), element strides (out_stride_*), each a
- * multiple of 8.  G * tokens <= 16.  max_seq bounds every row's length (0 = the pool's
- * capacity); split_tokens is the positions per workgroup (0 = chosen from batch, kv_heads and
- * max_seq; raised to whole multiples of 256 and to at most 256 splits per row).  Rows needing
- * more than one split keep per-split partial results in workspace (device memory of
- * barq_kv_attention_workspace_bytes(...) bytes, 16-byte aligned, no initialisation needed; NULL
- * when that is 0) and are merged by a second launch on the same stream; launches that share a
- * workspace must not overlap.
+ * multiple of 8.  G * tokens <= 16, batch <= 1024.  max_seq bounds every row's length (0 = the pool's
+ * capacity; longer rows attend their first max_seq positions and are flagged).  The work is
+ * cut into equal ranges of every row's positions, one per resident wave of the GPU, so ragged
+ * rows cost what their positions cost; split_tokens instead fixes the positions of a range
+ * (rounded up to 16; 0 = automatic).  Ranges that end inside a (row, kv head) keep partial
+ * results in workspace (device memory of barq_kv_attention_workspace_bytes(...) bytes, 16-byte
+ * aligned, no initialisation needed), merged by a second launch on the same stream; launches
+ * that share a workspace must not overlap.
  */
 int barq_kv_decode_attention(const barq_kv_pool* pool, const void* query, int64_t batch,
                              int64_t q_heads, int64_t tokens, int64_t q_stride_b,

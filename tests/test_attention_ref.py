@@ -106,18 +106,18 @@ def test_workspace_bytes_and_rejections():
     ws = lib.barq_kv_attention_workspace_bytes
     pool = _fake_pool()
     ref = ctypes.byref(pool)
-    # one record per (row, kv head, split) when a row can need more than one split:
-    # rows x 128 floats + 2 x rows floats padded to a multiple of 4
+    # one record slot per (range + pair): automatic ranges are at most 2048 (the resident waves
+    # of an MI355X); a fixed range of s positions gives ceil(pairs * ceil(max_seq / 16) / (s / 16))
     rec4 = 4 * 128 + 8
-    assert ws(ref, 2, 32, 1, 64, 0) == 0                      # one split of 64: no records
-    assert ws(ref, 2, 32, 1, 100, 0) == 2 * 8 * 2 * rec4 * 4  # splits of 64 (the minimum)
-    assert ws(ref, 2, 32, 1, 100, 50) == 2 * 8 * 2 * rec4 * 4  # 50 rounds up to 64
-    big = ctypes.byref(_fake_pool(blocks=64))                 # capacity 1024
-    assert ws(big, 2, 32, 1, 0, 256) == 2 * 8 * 4 * rec4 * 4  # 0: capacity, 4 splits
-    assert ws(big, 2, 32, 1, 600, 257) == 2 * 8 * 3 * rec4 * 4   # 257 -> 272: 3 splits
-    assert ws(big, 2, 32, 1, 1000, 4096) == 2 * 8 * 2 * rec4 * 4  # capped at 60 pages: 960
-    assert ws(big, 2, 128, 1, 600, 256) == 2 * 8 * 3 * (16 * 128 + 32) * 4  # G = 16
-    assert ws(big, 2, 8, 1, 600, 256) == 2 * 8 * 3 * (128 + 4) * 4  # G = 1: 2 floats -> 4
+    pairs = 2 * 8
+    assert ws(ref, 2, 32, 1, 100, 0) == (2048 + pairs) * rec4 * 4
+    assert ws(ref, 2, 32, 1, 100, 64) == (pairs * 7 // 4 + pairs) * rec4 * 4  # 7 chunks/pair, 4 per range
+    assert ws(ref, 2, 32, 1, 100, 50) == (pairs * 7 // 4 + pairs) * rec4 * 4  # 50 -> 64
+    big = ctypes.byref(_fake_pool(blocks=64))                 # capacity 1024: 64 chunks per pair
+    assert ws(big, 2, 32, 1, 0, 256) == (pairs * 64 // 16 + pairs) * rec4 * 4
+    assert ws(big, 2, 128, 1, 0, 256) == (pairs * 4 + pairs) * (16 * 128 + 32) * 4  # G = 16
+    assert ws(big, 2, 8, 1, 0, 256) == (pairs * 4 + pairs) * (128 + 4) * 4           # G = 1
+    assert ws(ctypes.byref(_fake_pool(batch=1025, pages=1)), 1025, 32, 1, 0, 0) == -1  # batch > 1024
     assert ws(ref, 2, 128, 2, 100, 0) == -1   # 32 query rows per kv head
     assert ws(ref, 2, 12, 1, 100, 0) == -1    # q_heads not a multiple of kv_heads
     assert ws(ref, 5, 32, 1, 100, 0) == -1    # batch beyond the pool's rows
