@@ -320,7 +320,7 @@ def attention_leg(cfg, pools, B, dev, reps=20):
         raise SystemExit("device error bits set by the attention leg")
     gathered = 3 * (sum(call_bytes) - L * io) / L  # gather reads + writes K/V, attention re-reads
     return {
-        "kernel": "attention_split_kernel (+ attention_merge_kernel for rows with several splits)",
+        "kernel": "attention_flat_kernel + attention_merge_kernel (one launch pair per layer)",
         "query_heads_per_kv_head": G,
         "us_per_layer_call": round(per_call_us, 2),
         "us_per_step_all_layers": round(best * 1e3, 1),
