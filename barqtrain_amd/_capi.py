@@ -31,6 +31,7 @@ class BarqKVPool(ctypes.Structure):
         ("high_water", c_ptr),
         ("free_pages", c_ptr),
         ("ctrl", c_ptr),
+        ("page_shares", c_ptr),
         ("num_pages", c_i64),
         ("max_batch", c_i64),
         ("max_blocks", c_i64),
@@ -53,6 +54,7 @@ _SIGNATURES = {
     "barq_kv_crop": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_i64, c_i64, c_ptr]),
     "barq_kv_free_rows": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_ptr, c_i64, c_ptr]),
     "barq_kv_copy_rows": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), ctypes.POINTER(BarqKVPool), c_ptr, c_i64, c_ptr]),
+    "barq_kv_select_rows": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_ptr, c_i64, c_ptr, c_i64, c_ptr]),
     "barq_kv_attention_workspace_bytes": (c_i64, [ctypes.POINTER(BarqKVPool)] + [c_i64] * 5),
     "barq_kv_decode_attention": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_ptr] + [c_i64] * 6 + [c_ptr]
                                  + [c_i64] * 3 + [ctypes.c_float] + [c_i64] * 3 + [c_ptr, c_i64, c_ptr]),
@@ -98,7 +100,8 @@ def pool_struct(pool) -> BarqKVPool:
     return BarqKVPool(
         pool.key_pages.data_ptr(), pool.value_pages.data_ptr(), pool.block_table.data_ptr(),
         pool.seq_lens.data_ptr(), pool.high_water.data_ptr(), pool.free_pages.data_ptr(),
-        pool.ctrl.data_ptr(), pool.num_pages, pool.max_batch, pool.max_blocks, pool.page_size,
+        pool.ctrl.data_ptr(), pool.page_shares.data_ptr(), pool.num_pages, pool.max_batch,
+        pool.max_blocks, pool.page_size,
         pool.kv_heads, pool.head_dim, pool.key_pages.element_size(),
     )
 

@@ -599,6 +599,7 @@ __global__ void reset_kernel(const barq_kv_pool p, const int32_t* order) {
        i += (int64_t)gridDim.x * blockDim.x) {
     // Stack entry i is popped (num_pages - 1 - i)-th, so page_order[k] is the k-th page taken.
     if (i < n_pages) p.free_pages[i] = order ? order[n_pages - 1 - i] : (int32_t)(n_pages - 1 - i);
+    if (i < n_pages && p.page_shares) p.page_shares[i] = 0;
     if (i < n_table) p.block_table[i] = -1;
     if (i < p.max_batch) {
       p.seq_lens[i] = 0;
@@ -613,7 +614,9 @@ __global__ void crop_kernel(int32_t* seq_lens, int batch, int max_length) {
   if (i < batch) seq_lens[i] = min(seq_lens[i], max_length);
 }
 
-// One workgroup: push the pages of the listed rows back on the stack.
+// One workgroup: drop the listed rows' references.  A page that no block holds any more is
+// pushed back on the stack, in (row, block) order; with page_shares, a shared page only loses
+// a reference (its table entry is first rewritten to -1 when it stays held).
 __global__ void __launch_bounds__(kThreads) free_rows_kernel(const barq_kv_pool p,
                                                             const int32_t* rows, int n,
                                                             FastDiv div_page) {
@@ -624,7 +627,7 @@ __global__ void __launch_bounds__(kThreads) free_rows_kernel(const barq_kv_pool 
   int err = 0;
   for (int i0 = 0; i0 < n; i0 += kThreads) {
     const int i = i0 + (int)threadIdx.x;
-    int r = -1, cnt = 0;
+    int r = -1, cnt = 0, freed = 0;
     if (i < n) {
       r = rows[i];
       if (r < 0 || r >= (int)p.max_batch) {
@@ -632,16 +635,31 @@ __global__ void __launch_bounds__(kThreads) free_rows_kernel(const barq_kv_pool 
         r = -1;
       } else {
         cnt = min(ceil_div_fd(p.high_water[r], div_page), mb);
+        for (int j = 0; j < cnt; ++j) {
+          int32_t* e = &p.block_table[(int64_t)r * mb + j];
+          const int page = checked_page(*e, p.num_pages);
+          bool last = page >= 0;
+          if (last && p.page_shares) {
+            last = atomicSub(&p.page_shares[page], 1) == 0;
+            if (last) p.page_shares[page] = 0;
+            else *e = -1;
+          }
+          freed += last;
+        }
       }
     }
     int chunk_total = 0;
-    const int excl = block_exclusive_scan<kWaves>(cnt, lds_scan, &chunk_total);
+    const int excl = block_exclusive_scan<kWaves>(freed, lds_scan, &chunk_total);
     if (r >= 0) {
+      int k = 0;
       for (int j = 0; j < cnt; ++j) {
-        const int64_t slot = (int64_t)top + pushed + excl + j;
         int32_t* e = &p.block_table[(int64_t)r * mb + j];
-        if (slot < p.num_pages) p.free_pages[slot] = *e;
-        else err |= BARQ_KV_ERRBIT_BAD_INDEX;
+        const int page = checked_page(*e, p.num_pages);
+        if (page >= 0) {
+          const int64_t slot = (int64_t)top + pushed + excl + k++;
+          if (slot < p.num_pages) p.free_pages[slot] = page;
+          else err |= BARQ_KV_ERRBIT_BAD_INDEX;
+        }
         *e = -1;
       }
       p.seq_lens[r] = 0;
@@ -773,6 +791,157 @@ __global__ void __launch_bounds__(kThreads) copy_rows_kernel(const CopyArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// In-place row selection with shared pages (copy-on-write beam ops).  Four launches:
+//   build   -- tile (new row i, block j): a block wholly below the source row's length keeps the
+//              source page and adds a reference; a later block (one an append or crop can still
+//              write) gets a page from the free stack (tails ranked in (row, block) order) and a
+//              copy of the source page.  The new table rows, lengths and marks go to workspace.
+//   commit  -- the stack top drops by the pages the tails took.
+//   release -- every old block drops its reference; pages left unheld are pushed on the stack.
+//   install -- the workspace rows become the table; other rows become empty.
+// References are added before any is dropped, so a page the new rows keep never reaches zero.
+// ---------------------------------------------------------------------------------------------
+
+struct SelectArgs {
+  barq_kv_pool p;
+  const int32_t* rows;
+  int32_t* ws;       // [n * max_blocks] table, then [n] lengths, then [n] marks
+  int32_t n;
+  int64_t page_bytes;
+  FastDiv div_page;
+  FastDiv div_blocks;
+};
+
+// Blocks of source row r that the selection copies (from the one holding seq_lens up to the
+// high-water mark), and where they start.
+__device__ __forceinline__ void tail_blocks(const barq_kv_pool& p, int r, const FastDiv& div_page,
+                                            int* first, int* count) {
+  const int mb = (int)p.max_blocks;
+  const int nb = min(ceil_div_fd(p.high_water[r], div_page), mb);
+  const int f = min((int)div_page.div((uint32_t)max(p.seq_lens[r], 0)), nb);
+  *first = f;
+  *count = nb - f;
+}
+
+template <int VB>
+__global__ void __launch_bounds__(kThreads) select_build_kernel(const SelectArgs a) {
+  __shared__ int s_meta[2];  // source page, new page of a copied block
+  const barq_kv_pool& p = a.p;
+  const int mb = (int)p.max_blocks;
+  const int i = (int)a.div_blocks.div(blockIdx.x);
+  const int j = (int)blockIdx.x - i * mb;
+  if (threadIdx.x < kWave) {
+    const int lane = threadIdx.x;
+    int acc = 0;  // copied blocks of new rows [0, i)
+    for (int q0 = 0; q0 < i; q0 += kWave) {
+      const int q = q0 + lane;
+      int c = 0;
+      if (q < i) {
+        const int r = a.rows[q];
+        if (r >= 0 && r < (int)p.max_batch) {
+          int f;
+          tail_blocks(p, r, a.div_page, &f, &c);
+        }
+      }
+      acc += wave_sum(c);
+    }
+    if (lane == 0) {
+      const int r = a.rows[i];
+      const bool valid = r >= 0 && r < (int)p.max_batch;
+      int src = -1, dst = -1, entry = -1, err = 0;
+      if (!valid) err |= BARQ_KV_ERRBIT_BAD_INDEX;
+      if (valid) {
+        int first, count;
+        tail_blocks(p, r, a.div_page, &first, &count);
+        if (j < first + count) {
+          const int old = checked_page(p.block_table[(int64_t)r * mb + j], p.num_pages);
+          if (j < first) {
+            entry = old;
+            if (old >= 0) atomicAdd(&p.page_shares[old], 1);
+          } else {
+            const int idx = p.ctrl[BARQ_KV_CTRL_FREE_TOP] - 1 - (acc + j - first);
+            dst = idx >= 0 ? checked_page(p.free_pages[idx], p.num_pages) : -1;
+            if (dst < 0) err |= BARQ_KV_ERRBIT_POOL_EXHAUSTED;
+            src = old;
+            entry = dst;
+          }
+        }
+      }
+      a.ws[(int64_t)i * mb + j] = entry;
+      if (j == 0) {
+        a.ws[(int64_t)a.n * mb + i] = valid ? p.seq_lens[r] : 0;
+        a.ws[(int64_t)a.n * mb + a.n + i] = valid ? p.high_water[r] : 0;
+      }
+      if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
+      s_meta[0] = src;
+      s_meta[1] = dst;
+    }
+  }
+  __syncthreads();
+  const int sp = s_meta[0];
+  const int dp = s_meta[1];
+  if (sp >= 0 && dp >= 0) {
+    const int nvec = (int)(a.page_bytes / VB);
+    copy_run<VB>((const char*)p.key_pages + (int64_t)sp * a.page_bytes,
+                 (char*)p.key_pages + (int64_t)dp * a.page_bytes, nvec);
+    copy_run<VB>((const char*)p.value_pages + (int64_t)sp * a.page_bytes,
+                 (char*)p.value_pages + (int64_t)dp * a.page_bytes, nvec);
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) select_commit_kernel(const SelectArgs a) {
+  __shared__ int lds_scan[kWaves];
+  int total = 0;
+  for (int q0 = 0; q0 < a.n; q0 += kThreads) {
+    const int q = q0 + (int)threadIdx.x;
+    int c = 0;
+    if (q < a.n) {
+      const int r = a.rows[q];
+      if (r >= 0 && r < (int)a.p.max_batch) {
+        int f;
+        tail_blocks(a.p, r, a.div_page, &f, &c);
+      }
+    }
+    int chunk_total = 0;
+    block_exclusive_scan<kWaves>(c, lds_scan, &chunk_total);
+    total += chunk_total;
+  }
+  if (threadIdx.x == 0)
+    a.p.ctrl[BARQ_KV_CTRL_FREE_TOP] = max(0, a.p.ctrl[BARQ_KV_CTRL_FREE_TOP] - total);
+}
+
+// Workgroup per old row: its blocks drop their references.
+__global__ void __launch_bounds__(kThreads) select_release_kernel(const SelectArgs a) {
+  const barq_kv_pool& p = a.p;
+  const int r = blockIdx.x;
+  const int mb = (int)p.max_blocks;
+  const int nb = min(ceil_div_fd(p.high_water[r], a.div_page), mb);
+  for (int j = threadIdx.x; j < nb; j += kThreads) {
+    const int page = checked_page(p.block_table[(int64_t)r * mb + j], p.num_pages);
+    if (page < 0) continue;
+    if (atomicSub(&p.page_shares[page], 1) == 0) {
+      p.page_shares[page] = 0;
+      const int slot = atomicAdd(&p.ctrl[BARQ_KV_CTRL_FREE_TOP], 1);
+      if (slot < p.num_pages) p.free_pages[slot] = page;
+      else atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], BARQ_KV_ERRBIT_BAD_INDEX);
+    }
+  }
+}
+
+// Workgroup per row: install the workspace row (rows >= n become empty).
+__global__ void __launch_bounds__(kThreads) select_install_kernel(const SelectArgs a) {
+  const barq_kv_pool& p = a.p;
+  const int r = blockIdx.x;
+  const int mb = (int)p.max_blocks;
+  for (int j = threadIdx.x; j < mb; j += kThreads)
+    p.block_table[(int64_t)r * mb + j] = r < a.n ? a.ws[(int64_t)r * mb + j] : -1;
+  if (threadIdx.x == 0) {
+    p.seq_lens[r] = r < a.n ? a.ws[(int64_t)a.n * mb + r] : 0;
+    p.high_water[r] = r < a.n ? a.ws[(int64_t)a.n * mb + a.n + r] : 0;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------------------------
 
@@ -838,6 +1007,7 @@ int launch_stream_kernel(int vb, bool fast, dim3 grid, StreamArgs* arg, hipStrea
 
 BARQ_DEFINE_VB_LAUNCH(dense_append_kernel, DenseArgs)
 BARQ_DEFINE_VB_LAUNCH(copy_rows_kernel, CopyArgs)
+BARQ_DEFINE_VB_LAUNCH(select_build_kernel, SelectArgs)
 
 // Shared body of append / gather / update.
 int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t batch,
@@ -1068,6 +1238,36 @@ int barq_kv_free_rows(const barq_kv_pool* pool, const int32_t* rows, int64_t num
                          (hipStream_t)stream) == hipSuccess
              ? BARQ_KV_OK
              : BARQ_KV_ERR_LAUNCH;
+}
+
+int barq_kv_select_rows(const barq_kv_pool* pool, const int32_t* src_rows, int64_t num_rows,
+                        int32_t* workspace, int64_t workspace_words, void* stream) {
+  if (!pool_ok(pool) || !pool->page_shares || num_rows < 0 || num_rows > pool->max_batch)
+    return BARQ_KV_ERR_INVALID;
+  if (num_rows > 0 && (!src_rows || !workspace || workspace_words < num_rows * (pool->max_blocks + 2)))
+    return BARQ_KV_ERR_INVALID;
+  if (num_rows * pool->max_blocks > kI32Max) return BARQ_KV_ERR_INVALID;
+  SelectArgs a;
+  a.p = *pool;
+  a.rows = src_rows;
+  a.ws = workspace;
+  a.n = (int32_t)num_rows;
+  a.page_bytes = pool->page_size * pool->kv_heads * pool->head_dim * pool->elem_bytes;
+  a.div_page = FastDiv::make((uint32_t)pool->page_size);
+  a.div_blocks = FastDiv::make((uint32_t)pool->max_blocks);
+  hipStream_t s = (hipStream_t)stream;
+  const uint64_t bits = (uint64_t)a.page_bytes | (uint64_t)(uintptr_t)pool->key_pages |
+                        (uint64_t)(uintptr_t)pool->value_pages;
+  int rc = BARQ_KV_OK;
+  if (num_rows > 0) {
+    rc = launch_select_build_kernel(vector_bytes(bits), dim3((uint32_t)(num_rows * pool->max_blocks)), &a, s);
+    if (rc == BARQ_KV_OK) rc = launch((const void*)&select_commit_kernel, dim3(1), &a, s);
+  }
+  if (rc == BARQ_KV_OK)
+    rc = launch((const void*)&select_release_kernel, dim3((uint32_t)pool->max_batch), &a, s);
+  if (rc == BARQ_KV_OK)
+    rc = launch((const void*)&select_install_kernel, dim3((uint32_t)pool->max_batch), &a, s);
+  return rc;
 }
 
 int barq_kv_copy_rows(const barq_kv_pool* src, const barq_kv_pool* dst, const int32_t* src_rows,

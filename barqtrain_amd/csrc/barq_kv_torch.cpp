@@ -36,9 +36,9 @@ bool same_layout(const at::Tensor& a, const at::Tensor& b) {
 }
 
 // The pool is passed as (key_pages, value_pages, block_table, seq_lens, high_water, free_pages,
-// ctrl), the tensors of barqtrain_amd.paged.PagePool.
+// ctrl, page_shares), the tensors of barqtrain_amd.paged.PagePool.
 barq_kv_pool pool_from(const std::vector<at::Tensor>& t) {
-  TORCH_CHECK(t.size() == 7, "a page pool is 7 tensors");
+  TORCH_CHECK(t.size() == 8, "a page pool is 8 tensors");
   const at::Tensor& kp = t[0];
   const at::Tensor& vp = t[1];
   TORCH_CHECK(kp.is_cuda() && vp.is_cuda(), "page pool must live on a GPU");
@@ -46,7 +46,7 @@ barq_kv_pool pool_from(const std::vector<at::Tensor>& t) {
               "key/value pages must be [num_pages, page_size, kv_heads, head_dim]");
   TORCH_CHECK(kp.is_contiguous() && vp.is_contiguous(), "pages must be contiguous");
   TORCH_CHECK(kp.scalar_type() == vp.scalar_type(), "key/value pages must share dtype");
-  for (size_t i = 2; i < 7; ++i) {
+  for (size_t i = 2; i < 8; ++i) {
     TORCH_CHECK(t[i].scalar_type() == at::kInt && t[i].is_contiguous() && t[i].is_cuda() &&
                     t[i].get_device() == kp.get_device(),
                 "page-pool metadata must be contiguous int32 on the pool's device");
@@ -60,6 +60,7 @@ barq_kv_pool pool_from(const std::vector<at::Tensor>& t) {
   p.high_water = t[4].data_ptr<int32_t>();
   p.free_pages = t[5].data_ptr<int32_t>();
   p.ctrl = t[6].data_ptr<int32_t>();
+  p.page_shares = t[7].data_ptr<int32_t>();
   p.num_pages = kp.size(0);
   p.page_size = kp.size(1);
   p.kv_heads = kp.size(2);
@@ -70,6 +71,7 @@ barq_kv_pool pool_from(const std::vector<at::Tensor>& t) {
   TORCH_CHECK(t[3].numel() == p.max_batch && t[4].numel() == p.max_batch, "row metadata size mismatch");
   TORCH_CHECK(t[5].numel() == p.num_pages, "free_pages must hold num_pages entries");
   TORCH_CHECK(t[6].numel() == BARQ_KV_CTRL_WORDS, "ctrl must hold BARQ_KV_CTRL_WORDS entries");
+  TORCH_CHECK(t[7].numel() == p.num_pages, "page_shares must hold num_pages entries");
   return p;
 }
 
@@ -232,6 +234,20 @@ void pool_copy_rows_(std::vector<at::Tensor> src, std::vector<at::Tensor> dst, a
                "pool_copy_rows_");
 }
 
+void pool_select_rows_(std::vector<at::Tensor> pool, at::Tensor rows, at::Tensor workspace) {
+  barq_kv_pool p = pool_from(pool);
+  TORCH_CHECK(rows.is_cuda() && rows.scalar_type() == at::kInt && rows.is_contiguous() &&
+                  rows.get_device() == pool[0].get_device(),
+              "rows must be contiguous int32 on the pool's device");
+  TORCH_CHECK(workspace.is_cuda() && workspace.scalar_type() == at::kInt && workspace.is_contiguous() &&
+                  workspace.get_device() == pool[0].get_device(),
+              "workspace must be contiguous int32 on the pool's device");
+  c10::DeviceGuard guard(pool[0].device());
+  check_status(barq_kv_select_rows(&p, rows.data_ptr<int32_t>(), rows.numel(), workspace.data_ptr<int32_t>(),
+                                   workspace.numel(), current_stream(pool[0])),
+               "pool_select_rows_");
+}
+
 int64_t attention_workspace_bytes(std::vector<at::Tensor> pool, int64_t batch, int64_t q_heads,
                                   int64_t tokens, int64_t max_seq, int64_t split_tokens) {
   barq_kv_pool p = pool_from(pool);
@@ -284,6 +300,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("pool_crop_", &pool_crop_, "Clamp row lengths of a page pool");
   m.def("pool_free_rows_", &pool_free_rows_, "Return rows' pages to the free stack");
   m.def("pool_copy_rows_", &pool_copy_rows_, "Build rows of a fresh pool as copies of source rows");
+  m.def("pool_select_rows_", &pool_select_rows_, "Rows become selected rows, sharing their full pages");
   m.def("attention_workspace_bytes", &attention_workspace_bytes,
         "Workspace bytes of a decode-attention launch (-1: arguments rejected)");
   m.def("pool_decode_attention", &pool_decode_attention,

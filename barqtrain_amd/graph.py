@@ -18,8 +18,7 @@ from typing import Optional, Sequence
 import numpy as np
 import torch
 
-from barqtrain_amd.paged import (SEPARATE_FINALIZE, SEQ_FROM_DEVICE, PagedKVCapacityError,
-                                 PagedKVPoolExhausted, PagePool)
+from barqtrain_amd.paged import SEPARATE_FINALIZE, SEQ_FROM_DEVICE, PagedKVCapacityError, PagePool
 
 
 class CapturedDecodeStep:
@@ -101,9 +100,7 @@ class CapturedDecodeStep:
         P = p0.page_size
         need = np.maximum(np.minimum(-(-ends // P), p0.max_blocks) - (-(-hw // P)), 0).sum(axis=1)
         for p, n in zip(self.pools, need):
-            if n > p.free_count:
-                raise PagedKVPoolExhausted(
-                    f"paged KV page pool exhausted: append needs {int(n)} pages, {p.free_count} free")
+            p.ensure_free(int(n), "append")
         self._graph(min(self.capacity, -(-worst // self.bucket) * self.bucket)).replay()
         lens += T
         np.maximum(hw, lens, out=hw)

@@ -103,9 +103,12 @@ class PagePool:
         self.high_water = torch.empty((self.max_batch,), **i32)
         self.free_pages = torch.empty((self.num_pages,), **i32)
         self.ctrl = torch.empty((CTRL_WORDS,), **i32)
+        self.page_shares = torch.empty((self.num_pages,), **i32)
         self.lens = np.zeros(self.max_batch, dtype=np.int64)
         self.hw = np.zeros(self.max_batch, dtype=np.int64)
         self.free_count = self.num_pages
+        self.free_exact = True   # free_count equals the device's free stack (else a lower bound)
+        self.shared = False      # some page may be held by more than one block
         self.reset(page_order)
 
     # ------------------------------------------------------------------ plumbing
@@ -116,7 +119,7 @@ class PagePool:
     @property
     def tensors(self) -> list[torch.Tensor]:
         return [self.key_pages, self.value_pages, self.block_table, self.seq_lens,
-                self.high_water, self.free_pages, self.ctrl]
+                self.high_water, self.free_pages, self.ctrl, self.page_shares]
 
     @property
     def capacity(self) -> int:
@@ -157,11 +160,20 @@ class PagePool:
                     f"paged KV cache capacity exceeded: requested {worst}, max_cache_len={limit}"
                 )
         need = int(self.new_block_counts(batch, tokens).sum())
+        self.ensure_free(need, "append")
+        return need
+
+    def ensure_free(self, need: int, what: str) -> None:
+        """Raise PagedKVPoolExhausted unless `need` pages are free.  After shared-page operations
+        the host count is a lower bound; it is refreshed from the device (a synchronisation)
+        only when it would refuse."""
+        if need > self.free_count and not self.free_exact:
+            self.free_count = int(self.ctrl[CTRL_FREE_TOP].item())
+            self.free_exact = True
         if need > self.free_count:
             raise PagedKVPoolExhausted(
-                f"paged KV page pool exhausted: append needs {need} pages, {self.free_count} free"
+                f"paged KV page pool exhausted: {what} needs {need} pages, {self.free_count} free"
             )
-        return need
 
     def _advance(self, batch: int, tokens: int, need: int) -> None:
         if batch <= 0 or tokens <= 0:
@@ -186,6 +198,8 @@ class PagePool:
         self.lens[:] = 0
         self.hw[:] = 0
         self.free_count = self.num_pages
+        self.free_exact = True
+        self.shared = False
 
     def _check_states(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
         if key_states.dim() != 4 or key_states.shape != value_states.shape:
@@ -250,12 +264,15 @@ class PagePool:
         return ko, vo
 
     def crop(self, batch: int, max_length: int) -> None:
-        """seq_lens[:batch] = min(seq_lens, max_length); data and pages are kept."""
+        """seq_lens[:batch] = min(seq_lens, max_length); data and pages are kept.  When rows
+        share pages, the blocks the crop re-opens for writing are given pages of their own."""
         max_length = max(int(max_length), 0)
         if batch <= 0:
             return
         self._ops().pool_crop_(self.tensors, batch, max_length)
         np.minimum(self.lens[:batch], max_length, out=self.lens[:batch])
+        if self.shared:
+            self.select_rows(list(range(self.max_batch)))
 
     def free_rows(self, rows: Sequence[int]) -> None:
         """Return every page of `rows` to the pool; their lengths become 0."""
@@ -268,9 +285,46 @@ class PagePool:
             return
         self._ops().pool_free_rows_(self.tensors, self._index_tensor(rows))
         r = np.asarray(rows)
-        self.free_count += int(np.minimum(-(-self.hw[r] // self.page_size), self.max_blocks).sum())
+        if self.shared:
+            self.free_exact = False  # shared pages stay held: the device knows how many returned
+        else:
+            self.free_count += int(np.minimum(-(-self.hw[r] // self.page_size), self.max_blocks).sum())
         self.lens[r] = 0
         self.hw[r] = 0
+
+    def tail_block_counts(self, rows: np.ndarray) -> np.ndarray:
+        """Blocks of each row that a selection copies: from the one holding seq_lens up to the
+        high-water mark (the blocks an append or a crop can still write)."""
+        nb = np.minimum(-(-self.hw[rows] // self.page_size), self.max_blocks)
+        return nb - np.minimum(self.lens[rows] // self.page_size, nb)
+
+    def select_rows(self, src_rows: Sequence[int]) -> None:
+        """In place: row i becomes row src_rows[i] (repeats allowed), every other row empty.
+        Full blocks are shared (copy-on-write), so the cost is the rows' partial last blocks,
+        not their history (reference: kv_cache.py:166-186, which copies the whole cache)."""
+        src_rows = [int(r) for r in src_rows]
+        n = len(src_rows)
+        if n > self.max_batch:
+            raise ValueError("select_rows: more rows than the pool holds")
+        if any(r < 0 or r >= self.max_batch for r in src_rows):
+            raise IndexError("select_rows: row out of range")
+        r = np.asarray(src_rows, dtype=np.int64)
+        need = int(self.tail_block_counts(r).sum()) if n else 0
+        self.ensure_free(need, "select_rows")
+        words = max(n * (self.max_blocks + 2), 1)
+        ws = getattr(self, "_select_ws", None)
+        if ws is None or ws.numel() < words:
+            ws = torch.empty((words,), dtype=torch.int32, device=self.device)
+            self._select_ws = ws
+        self._ops().pool_select_rows_(self.tensors, self._index_tensor(src_rows or [0])[:n], ws)
+        lens, hw = self.lens[r].copy(), self.hw[r].copy()
+        self.lens[:] = 0
+        self.hw[:] = 0
+        self.lens[:n] = lens
+        self.hw[:n] = hw
+        self.free_count -= need
+        self.free_exact = False   # the released pages return on the device
+        self.shared = True
 
     def copy_rows(self, src_rows: Sequence[int], num_pages: Optional[int] = None) -> "PagePool":
         """A new pool whose row i copies row src_rows[i] of this one (repeats allowed)."""
@@ -356,7 +410,8 @@ class PagePool:
     def to(self, device) -> "PagePool":
         """Move every tensor of the pool (offload / prefetch)."""
         device = torch.device(device)
-        for name in ("key_pages", "value_pages", "block_table", "seq_lens", "high_water", "free_pages", "ctrl"):
+        for name in ("key_pages", "value_pages", "block_table", "seq_lens", "high_water", "free_pages", "ctrl",
+                     "page_shares"):
             setattr(self, name, getattr(self, name).to(device, non_blocking=True))
         self.device = device
         return self
@@ -376,10 +431,11 @@ class _HostOps:
 
     @staticmethod
     def pool_reset_(t, page_order=None):
-        kp, vp, bt, lens, hw, free, ctrl = t
+        kp, vp, bt, lens, hw, free, ctrl, shares = t
         n = kp.shape[0]
         order = page_order if page_order is not None else torch.arange(n, dtype=torch.int32)
         free.copy_(order.flip(0))
+        shares.zero_()
         bt.fill_(-1)
         lens.zero_()
         hw.zero_()
@@ -388,7 +444,7 @@ class _HostOps:
 
     @staticmethod
     def _map_new_blocks(t, batch, tokens):
-        kp, vp, bt, lens, hw, free, ctrl = t
+        kp, vp, bt, lens, hw, free, ctrl, shares = t
         P, MB = _HostOps._geometry(t)
         top = int(ctrl[CTRL_FREE_TOP])
         used = 0
@@ -413,7 +469,7 @@ class _HostOps:
 
     @staticmethod
     def _scatter(t, key_states, value_states, old_lens):
-        kp, vp, bt, lens, hw, free, ctrl = t
+        kp, vp, bt, lens, hw, free, ctrl, shares = t
         P, MB = _HostOps._geometry(t)
         batch, _, tokens, _ = key_states.shape
         pos = old_lens[:, None] + torch.arange(tokens, dtype=torch.int64)[None, :]
@@ -431,7 +487,7 @@ class _HostOps:
 
     @staticmethod
     def _commit(t, batch, tokens):
-        kp, vp, bt, lens, hw, free, ctrl = t
+        kp, vp, bt, lens, hw, free, ctrl, shares = t
         lens[:batch] += tokens
         torch.maximum(hw[:batch], lens[:batch], out=hw[:batch])
 
@@ -445,7 +501,7 @@ class _HostOps:
 
     @staticmethod
     def pool_gather(t, key_out, value_out, batch, seq_out, flags=0):
-        kp, vp, bt, lens, hw, free, ctrl = t
+        kp, vp, bt, lens, hw, free, ctrl, shares = t
         P, MB = _HostOps._geometry(t)
         if flags & SEQ_FROM_DEVICE:
             seq_out = min(seq_out, int(lens[:batch].max())) if batch else 0
@@ -467,7 +523,7 @@ class _HostOps:
     @staticmethod
     def pool_decode_attention(t, query, out, scale, batch):
         """Decode attention for a pool in host memory: the gathered rows, float32 arithmetic."""
-        kp, vp, bt, lens, hw, free, ctrl = t
+        kp, vp, bt, lens, hw, free, ctrl, shares = t
         _, q_heads, tokens, D = query.shape
         group = q_heads // kp.shape[2]
         seq = int(lens[:batch].max())
@@ -491,23 +547,82 @@ class _HostOps:
         t[3][:batch].clamp_(max=max_length)
 
     @staticmethod
+    def _release(t, page, top):
+        """Drop one reference to `page`; push it when none is left.  Returns the new top."""
+        kp, vp, bt, lens, hw, free, ctrl, shares = t
+        if int(shares[page]) > 0:
+            shares[page] -= 1
+            return top
+        free[top] = page
+        return top + 1
+
+    @staticmethod
     def pool_free_rows_(t, rows):
-        kp, vp, bt, lens, hw, free, ctrl = t
+        kp, vp, bt, lens, hw, free, ctrl, shares = t
         P, MB = _HostOps._geometry(t)
         top = int(ctrl[CTRL_FREE_TOP])
         for r in rows.tolist():
             n = min(-(-int(hw[r]) // P), MB)
-            free[top:top + n] = bt[r, :n]
-            top += n
+            for j in range(n):
+                top = _HostOps._release(t, int(bt[r, j]), top)
             bt[r, :n] = -1
             lens[r] = 0
             hw[r] = 0
         ctrl[CTRL_FREE_TOP] = top
 
     @staticmethod
+    def pool_select_rows_(t, rows, workspace=None):
+        """In-place selection with shared full blocks (the algorithm of select_build / commit /
+        release / install in barq_kv.hip)."""
+        kp, vp, bt, lens, hw, free, ctrl, shares = t
+        P, MB = _HostOps._geometry(t)
+        rows = rows.tolist()
+        top = int(ctrl[CTRL_FREE_TOP])
+        new_bt = torch.full((len(rows), MB), -1, dtype=torch.int32)
+        new_lens = torch.zeros(len(rows), dtype=torch.int32)
+        new_hw = torch.zeros(len(rows), dtype=torch.int32)
+        used = 0
+        err = 0
+        for i, r in enumerate(rows):
+            nb = min(-(-int(hw[r]) // P), MB)
+            first = min(int(lens[r]) // P, nb)
+            for j in range(nb):
+                old = int(bt[r, j])
+                if j < first:
+                    new_bt[i, j] = old
+                    shares[old] += 1
+                else:
+                    idx = top - 1 - used
+                    used += 1
+                    page = int(free[idx]) if idx >= 0 else -1
+                    if page < 0:
+                        err |= ERRBIT_POOL_EXHAUSTED
+                    else:
+                        kp[page] = kp[old]
+                        vp[page] = vp[old]
+                    new_bt[i, j] = page
+            new_lens[i] = lens[r]
+            new_hw[i] = hw[r]
+        top = max(0, top - used)
+        for r in range(bt.shape[0]):
+            nb = min(-(-int(hw[r]) // P), MB)
+            for j in range(nb):
+                top = _HostOps._release(t, int(bt[r, j]), top)
+        ctrl[CTRL_FREE_TOP] = top
+        if err:
+            ctrl[CTRL_ERRORS] |= err
+        n = len(rows)
+        bt.fill_(-1)
+        lens.zero_()
+        hw.zero_()
+        bt[:n] = new_bt
+        lens[:n] = new_lens
+        hw[:n] = new_hw
+
+    @staticmethod
     def pool_copy_rows_(src, dst, rows):
-        skp, svp, sbt, slens, shw, _, _ = src
-        dkp, dvp, dbt, dlens, dhw, dfree, dctrl = dst
+        skp, svp, sbt, slens, shw, _, _, _ = src
+        dkp, dvp, dbt, dlens, dhw, dfree, dctrl, _ = dst
         P, MB = _HostOps._geometry(src)
         top = int(dctrl[CTRL_FREE_TOP])
         used = 0

@@ -24,6 +24,9 @@
  *   barq_kv_free_rows     <- no reference counterpart: returns a finished sequence's pages
  *                            to the pool (the page allocator the reference only planned,
  *                            IMPLEMENTATION_PLAN.md:90-92).
+ *   barq_kv_select_rows   <- batch_select_indices / batch_repeat_interleave / reorder_cache,
+ *                            python/barqtrain/kv_cache.py:166-186, in place: rows share their
+ *                            full pages (copy-on-write) instead of copying the cache.
  *   barq_kv_decode_attention, barq_kv_attention_workspace_bytes
  *                         <- no reference counterpart: the "gather/scatter kernels for attention
  *                            reads" the reference planned (IMPLEMENTATION_PLAN.md:90-91); it
@@ -82,7 +85,13 @@ extern "C" {
  *   high_water              : int32 [max_batch], slots [0, high_water) of the row have been written
  *   free_pages              : int32 [num_pages], a stack; entries [0, ctrl[FREE_TOP]) are free
  *   ctrl                    : int32 [BARQ_KV_CTRL_WORDS], 256-byte aligned
- * Invariant kept by every entry point: block b of row r holds a page iff b * page_size < high_water[r].
+ *   page_shares             : int32 [num_pages], references to the page beyond the first (0 for
+ *                             a free page and for a page one block maps), or NULL for a pool
+ *                             whose rows never share pages (barq_kv_select_rows needs it)
+ * Invariants kept by every entry point: block b of row r holds a page iff
+ * b * page_size < high_water[r]; a page is on the free stack iff no block holds it; a page held
+ * by k blocks has page_shares k - 1; only blocks wholly below their row's seq_lens are shared
+ * (barq_kv_crop can break the last one; see there).
  */
 typedef struct barq_kv_pool {
   void* key_pages;
@@ -92,6 +101,7 @@ typedef struct barq_kv_pool {
   int32_t* high_water;
   int32_t* free_pages;
   int32_t* ctrl;
+  int32_t* page_shares;
   int64_t num_pages;
   int64_t max_batch;
   int64_t max_blocks;
@@ -158,15 +168,33 @@ int barq_kv_update(const barq_kv_pool* pool, const void* key_states, const void*
                    int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_s,
                    int64_t flags, void* stream);
 
-/* seq_lens[b] = min(seq_lens[b], max_length) for rows [0, batch).  Page data is kept. */
+/*
+ * seq_lens[b] = min(seq_lens[b], max_length) for rows [0, batch).  Page data is kept.  On a pool
+ * whose rows share pages a crop can leave a shared block at or above its row's new length, where
+ * the next append would write it for every row holding it: call barq_kv_select_rows with
+ * src_rows = 0, 1, ..., max_batch - 1 before that append; it gives such blocks pages of their own.
+ */
 int barq_kv_crop(const barq_kv_pool* pool, int64_t batch, int64_t max_length, void* stream);
 
 /*
- * Return every page of the listed rows (device int32 [num_rows], distinct) to the free stack
- * and set their seq_lens and high_water to 0.
+ * Drop the listed rows' references to their pages (device int32 [num_rows], distinct) and set
+ * their seq_lens and high_water to 0; a page no block holds any more returns to the free stack.
  */
 int barq_kv_free_rows(const barq_kv_pool* pool, const int32_t* rows, int64_t num_rows,
                       void* stream);
+
+/*
+ * In place: row i, for i in [0, num_rows), becomes row src_rows[i] as it was before the call
+ * (src_rows: device int32 [num_rows], values in [0, max_batch), repeats allowed); every other
+ * row becomes empty.  A row's blocks wholly below its seq_lens are shared with the source row
+ * (page_shares counts the extra references); the blocks an append or a crop can still write --
+ * from the one holding position seq_lens up to high_water -- are copied into pages taken from
+ * the free stack, in (row, block) order.  Pages no block holds any more return to the stack.
+ * Needs page_shares, num_rows <= max_batch, and workspace of int32 [num_rows * (max_blocks + 2)].
+ * Launches four kernels on the stream; a pool exhausted midway sets BARQ_KV_ERRBIT_POOL_EXHAUSTED.
+ */
+int barq_kv_select_rows(const barq_kv_pool* pool, const int32_t* src_rows, int64_t num_rows,
+                        int32_t* workspace, int64_t workspace_words, void* stream);
 
 /*
  * Row i of dst, for i in [0, num_rows), becomes a copy of row src_rows[i] of src (device int32

@@ -32,11 +32,12 @@ class CPool:
         self.hw = torch.empty((max_batch,), **i32)
         self.free = torch.empty((self.num_pages,), **i32)
         self.ctrl = torch.empty((CTRL_WORDS,), **i32)
+        self.shares = torch.empty((self.num_pages,), **i32)
         elem = torch.empty(0, dtype=dtype).element_size()
         self.s = _capi.BarqKVPool(self.kp.data_ptr(), self.vp.data_ptr(), self.bt.data_ptr(),
                                   self.lens.data_ptr(), self.hw.data_ptr(), self.free.data_ptr(),
-                                  self.ctrl.data_ptr(), self.num_pages, max_batch, max_blocks,
-                                  page_size, heads, dim, elem)
+                                  self.ctrl.data_ptr(), self.shares.data_ptr(), self.num_pages,
+                                  max_batch, max_blocks, page_size, heads, dim, elem)
         self.reset(order)
 
     @property
@@ -98,6 +99,13 @@ class CPool:
             workspace.data_ptr(), workspace.numel(), self._stream()))
         return out, workspace
 
+    def select_rows(self, rows):
+        idx = torch.tensor(rows, dtype=torch.int32, device=self.kp.device)
+        ws = torch.empty(max(len(rows) * (self.max_blocks + 2), 1), dtype=torch.int32, device=self.kp.device)
+        _capi.check(self.lib.barq_kv_select_rows(self.ref, idx.data_ptr(), len(rows), ws.data_ptr(), ws.numel(),
+                                                 self._stream()))
+        torch.cuda.current_stream().synchronize()
+
     def new_out(self, batch, seq):
         shape = (batch, self.heads, seq, self.dim)
         return (torch.empty(shape, dtype=self.dtype, device=self.kp.device),
@@ -110,24 +118,38 @@ class CPool:
         return int(self.ctrl[0].item())
 
     def check_invariants(self):
-        """Every block below the high-water mark has a distinct page; no free page is mapped."""
-        P = self.page_size
-        bt = self.bt.cpu().numpy()
-        hw = self.hw.cpu().numpy()
-        top = self.free_top()
-        free = set(self.free.cpu().numpy()[:top].tolist())
-        mapped = []
-        for r in range(self.max_batch):
-            n = -(-int(hw[r]) // P)
-            assert (bt[r, :n] >= 0).all(), (r, bt[r, :n])
-            assert (bt[r, n:] == -1).all(), r
-            mapped += bt[r, :n].tolist()
-        assert len(mapped) == len(set(mapped)), "a page is mapped twice"
-        assert not (free & set(mapped)), "a mapped page is on the free stack"
-        assert len(free) + len(mapped) == self.num_pages
-        ctrl = self.ctrl.cpu()
-        assert ctrl[32].item() == 0, "arrival counter not reset"
-        assert not ctrl[64:].any(), "arrival sub-counters not reset"
+        check_pool_invariants(self.bt.cpu().numpy(), self.lens.cpu().numpy(), self.hw.cpu().numpy(),
+                              self.free.cpu().numpy(), self.ctrl.cpu().numpy(), self.shares.cpu().numpy(),
+                              self.page_size)
+
+
+def check_pool_invariants(bt, lens, hw, free, ctrl, shares, P):
+    """Block b of row r holds a page iff b * P < high_water[r]; a page is on the free stack iff
+    no block holds it; page_shares = holders - 1 (0 when free); only blocks wholly below their
+    row's length are shared; arrival counters are back at zero."""
+    import collections
+
+    num_pages = len(free)
+    top = int(ctrl[0])
+    free_set = set(free[:top].tolist())
+    assert len(free_set) == top, "a page is on the free stack twice"
+    holders = collections.defaultdict(list)
+    for r in range(bt.shape[0]):
+        n = -(-int(hw[r]) // P)
+        assert (bt[r, :n] >= 0).all(), (r, bt[r, :n])
+        assert (bt[r, n:] == -1).all(), r
+        for b in range(n):
+            holders[int(bt[r, b])].append((r, b))
+    assert not (free_set & set(holders)), "a held page is on the free stack"
+    assert len(free_set) + len(holders) == num_pages, "a page is neither free nor held"
+    for page in range(num_pages):
+        h = holders.get(page, [])
+        assert int(shares[page]) == max(len(h) - 1, 0), (page, int(shares[page]), h)
+        if len(h) > 1:
+            for r, b in h:
+                assert (b + 1) * P <= int(lens[r]), f"shared page {page} at row {r} block {b} can be written"
+    assert ctrl[32] == 0, "arrival counter not reset"
+    assert not ctrl[64:].any(), "arrival sub-counters not reset"
 
 
 def bits(t: torch.Tensor) -> np.ndarray:

@@ -96,7 +96,7 @@ def _fake_pool(elem=2, dim=128, heads=8, page=16, blocks=8, batch=4, pages=None)
     pages = pages or batch * blocks
     # Non-null but never dereferenced: every call below is rejected or sized on the host.
     p = 1 << 20
-    return _capi.BarqKVPool(p, p, p, p, p, p, p, pages, batch, blocks, page, heads, dim, elem)
+    return _capi.BarqKVPool(p, p, p, p, p, p, p, p, pages, batch, blocks, page, heads, dim, elem)
 
 
 def test_workspace_bytes_and_rejections():

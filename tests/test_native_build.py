@@ -19,7 +19,7 @@ def built():
 def test_library_exports_every_header_function(built):
     lib = ctypes.CDLL(str(build.lib_path()))
     declared = _capi.header_functions()
-    assert len(declared) == 12
+    assert len(declared) == 13
     for name in declared:
         assert hasattr(lib, name), name
     out = subprocess.run(["nm", "-D", "--defined-only", str(build.lib_path())], capture_output=True, text=True).stdout
@@ -49,7 +49,7 @@ def _fake_pool():
     addr = 0x7F0000000000
     return _capi.BarqKVPool(addr, addr + 2**30, addr + 2**31, addr + 2**31 + 2**20,
                             addr + 2**31 + 2**21, addr + 2**31 + 2**22, addr + 2**31 + 2**23,
-                            64, 4, 8, 16, 8, 128, 2)
+                            addr + 2**31 + 2**24, 64, 4, 8, 16, 8, 128, 2)
 
 
 def test_empty_work_returns_ok_before_any_launch(built):
