@@ -37,6 +37,12 @@ timed run left them: one call per layer with G query heads per KV head (4, the L
 visible K and V element once + query + output.  Layer 0 is checked against an fp32 attention over
 the gathered K/V.
 
+`beam_select` times a beam reorder (batch_select_indices / reorder_cache) of every layer one
+decode step past the prefill: the in-place selection that shares full pages and copies each
+row's partial last page (graph-replayed; also as host calls), next to the reference's dense
+keys[indices] over [B, H, blocks, P, D] on the same GPU; layer 0 is checked bit for bit against
+the gathered rows before the selections, and the pool's sharing invariants are checked.
+
 Prints ONE JSON line.  `--pmc-probe` instead runs the eager workload the rocprof counter runs
 profile: a 64 MiB elementwise pass (calibration), the prefill, then the decode steps.
 """
@@ -89,6 +95,7 @@ def parse():
     ap.add_argument("--repeat", type=int, default=None, help="timed repetitions; the best is reported")
     ap.add_argument("--pmc-probe", action="store_true", help="eager run for rocprof counter passes")
     ap.add_argument("--no-attention", action="store_true", help="skip the paged decode-attention leg")
+    ap.add_argument("--no-beam", action="store_true", help="skip the beam-reorder (select_rows) leg")
     ap.add_argument("--bucket", type=int, default=None,
                     help="graph extent bucket in positions (default: the step's own; 0: one graph over the capacity)")
     return ap.parse_args()
@@ -336,6 +343,123 @@ def attention_leg(cfg, pools, B, dev, reps=20):
     }
 
 
+def beam_leg(cfg, wl, dev, reps=20):
+    """Beam reorder (batch_select_indices / reorder_cache) of every layer, one decode step past the
+    prefill so that every row ends in a partial page: in-place selection sharing full pages, timed
+    as a graph replay (device time) and as host calls through PagePool.select_rows; beside it, the
+    reference's own operation on the same GPU -- keys[indices] / values[indices] over the dense
+    [B, H, blocks, P, D] cache (kv_cache.py:175-183) -- timed on one layer and scaled by layers."""
+    import numpy as np
+    import torch
+
+    from barqtrain_amd.paged import _gpu_backend
+    from capi_pool import check_pool_invariants
+
+    backend = _gpu_backend()
+    pools = wl.pools
+    L, B, H, D, P = cfg["layers"], cfg["batch"], cfg["heads"], cfg["dim"], cfg["page"]
+    wl.prefill()
+    for layer, pool in enumerate(pools):
+        pool.update(wl.k_dec[0, layer], wl.v_dec[0, layer])
+    torch.cuda.synchronize()
+    rows = sorted(np.random.default_rng(cfg["seed"] + 29).integers(0, B, size=B).tolist())
+    k0, v0 = (t.clone() for t in pools[0].gather(B))
+    tails = int(pools[0].tail_block_counts(np.asarray(rows)).sum())
+    page_bytes = P * H * D * pools[0].dtype.itemsize
+    sel_bytes = tails * page_bytes * 2 * 2  # K and V pages, read + written
+
+    def host_calls():
+        for pool in pools:
+            pool.select_rows(rows)
+
+    host_calls()  # warm (pinned index buffers, workspaces)
+    torch.cuda.synchronize()
+    host_best = None
+    for _ in range(5):
+        t0 = time.perf_counter()
+        host_calls()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        host_best = dt if host_best is None else min(host_best, dt)
+    idx = torch.tensor(rows, dtype=torch.int32, device=dev)
+    ws = pools[0]._select_ws
+
+    def device_calls():
+        for pool in pools:
+            backend.pool_select_rows_(pool.tensors, idx, ws)
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        device_calls()
+    graph.replay()
+    torch.cuda.synchronize()
+    applied = 6 + 1  # host_calls ran 6 times, the warm replay once
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    graph_ms = start.elapsed_time(end) / reps
+    applied += reps
+    if any(p.errors() for p in pools):
+        raise SystemExit("device error bits set by the beam leg")
+    order = np.arange(B)
+    for _ in range(applied):
+        order = order[np.asarray(rows)]
+    sel = torch.as_tensor(order, device=dev)
+    k1, v1 = pools[0].gather(B, k0.shape[2])  # the host shadow lags the graph replays
+    ok = bool(torch.equal(k1.view(torch.int16), k0[sel].view(torch.int16))
+              and torch.equal(v1.view(torch.int16), v0[sel].view(torch.int16)))
+    pool = pools[0]
+    check_pool_invariants(pool.block_table.cpu().numpy(), pool.seq_lens.cpu().numpy(),
+                          pool.high_water.cpu().numpy(), pool.free_pages.cpu().numpy(),
+                          pool.ctrl.cpu().numpy(), pool.page_shares.cpu().numpy(), P)
+    held = pool.num_pages - int(pool.ctrl[0].item())
+
+    mb = pool.max_blocks
+    kd = torch.empty((B, H, mb, P, D), dtype=pool.dtype, device=dev)
+    vd = torch.empty_like(kd)
+    ko, vo = torch.empty_like(kd), torch.empty_like(vd)
+    lidx = idx.long()
+
+    def dense():
+        torch.index_select(kd, 0, lidx, out=ko)
+        torch.index_select(vd, 0, lidx, out=vo)
+
+    dense()
+    dgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(dgraph):
+        dense()
+    dgraph.replay()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        dgraph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    dense_ms = start.elapsed_time(end) / reps
+    dense_bytes = 2 * 2 * kd.numel() * kd.element_size()
+    del kd, vd, ko, vo
+    return {
+        "kernels": "select_build_kernel + select_commit_kernel + select_release_kernel + select_install_kernel",
+        "selection": f"{B} rows from sorted seeded parents ({len(set(rows))} distinct), context "
+                     f"{int(pool.lens[:B].min())}..{int(pool.lens[:B].max())}",
+        "us_per_layer": round(graph_ms * 1e3 / L, 2),
+        "us_per_step_all_layers": round(graph_ms * 1e3, 1),
+        "host_us_per_step_all_layers": round(host_best * 1e6, 1),
+        "pages_copied_per_layer": tails,
+        "bytes_copied_per_layer": sel_bytes,
+        "pages_held_layer0": held,
+        "reference_dense_index_us_per_layer": round(dense_ms * 1e3, 2),
+        "reference_dense_bytes_per_layer": dense_bytes,
+        "speedup_vs_reference_dense": round(dense_ms / (graph_ms / L), 1),
+        "parity": {"layer0_bit_exact_after_selections": ok, "selections_applied": applied,
+                   "invariants_checked": True},
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -530,6 +654,8 @@ def main():
             "after_decode_steps": cpu_steps}
     if not args.no_attention and cfg["dtype"] in ("bfloat16", "float16") and D == 128:
         result["paged_attention"] = attention_leg(cfg, pools, B, dev)
+    if not args.no_beam:
+        result["beam_select"] = beam_leg(cfg, wl, dev)
     print(json.dumps(result), flush=True)
 
 
