@@ -55,6 +55,9 @@ _SIGNATURES = {
     "barq_kv_free_rows": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_ptr, c_i64, c_ptr]),
     "barq_kv_copy_rows": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), ctypes.POINTER(BarqKVPool), c_ptr, c_i64, c_ptr]),
     "barq_kv_select_rows": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_ptr, c_i64, c_ptr, c_i64, c_ptr]),
+    "barq_kv_select_rows_layers": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_i64, c_ptr, c_i64, c_ptr, c_i64,
+                                                  c_ptr]),
+    "barq_kv_select_workspace_words": (c_i64, [ctypes.POINTER(BarqKVPool), c_i64, c_i64]),
     "barq_kv_attention_workspace_bytes": (c_i64, [ctypes.POINTER(BarqKVPool)] + [c_i64] * 5),
     "barq_kv_decode_attention": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_ptr] + [c_i64] * 6 + [c_ptr]
                                  + [c_i64] * 3 + [ctypes.c_float] + [c_i64] * 3 + [c_ptr, c_i64, c_ptr]),

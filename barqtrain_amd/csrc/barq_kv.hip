@@ -614,9 +614,9 @@ __global__ void crop_kernel(int32_t* seq_lens, int batch, int max_length) {
   if (i < batch) seq_lens[i] = min(seq_lens[i], max_length);
 }
 
-// One workgroup: drop the listed rows' references.  A page that no block holds any more is
-// pushed back on the stack, in (row, block) order; with page_shares, a shared page only loses
-// a reference (its table entry is first rewritten to -1 when it stays held).
+// One workgroup: drop the listed rows' references, a row at a time with its blocks spread over
+// the threads.  A page that no block holds any more is pushed back on the stack, in (row, block)
+// order; with page_shares, a shared page only loses a reference.
 __global__ void __launch_bounds__(kThreads) free_rows_kernel(const barq_kv_pool p,
                                                             const int32_t* rows, int n,
                                                             FastDiv div_page) {
@@ -625,47 +625,40 @@ __global__ void __launch_bounds__(kThreads) free_rows_kernel(const barq_kv_pool 
   const int mb = (int)p.max_blocks;
   int pushed = 0;
   int err = 0;
-  for (int i0 = 0; i0 < n; i0 += kThreads) {
-    const int i = i0 + (int)threadIdx.x;
-    int r = -1, cnt = 0, freed = 0;
-    if (i < n) {
-      r = rows[i];
-      if (r < 0 || r >= (int)p.max_batch) {
-        err |= BARQ_KV_ERRBIT_BAD_INDEX;
-        r = -1;
-      } else {
-        cnt = min(ceil_div_fd(p.high_water[r], div_page), mb);
-        for (int j = 0; j < cnt; ++j) {
-          int32_t* e = &p.block_table[(int64_t)r * mb + j];
-          const int page = checked_page(*e, p.num_pages);
-          bool last = page >= 0;
-          if (last && p.page_shares) {
-            last = atomicSub(&p.page_shares[page], 1) == 0;
-            if (last) p.page_shares[page] = 0;
-            else *e = -1;
-          }
-          freed += last;
-        }
-      }
+  for (int i = 0; i < n; ++i) {
+    const int r = rows[i];
+    if (r < 0 || r >= (int)p.max_batch) {
+      err |= BARQ_KV_ERRBIT_BAD_INDEX;
+      continue;
     }
-    int chunk_total = 0;
-    const int excl = block_exclusive_scan<kWaves>(freed, lds_scan, &chunk_total);
-    if (r >= 0) {
-      int k = 0;
-      for (int j = 0; j < cnt; ++j) {
-        int32_t* e = &p.block_table[(int64_t)r * mb + j];
-        const int page = checked_page(*e, p.num_pages);
-        if (page >= 0) {
-          const int64_t slot = (int64_t)top + pushed + excl + k++;
-          if (slot < p.num_pages) p.free_pages[slot] = page;
-          else err |= BARQ_KV_ERRBIT_BAD_INDEX;
+    const int cnt = min(ceil_div_fd(p.high_water[r], div_page), mb);
+    int32_t* row = p.block_table + (int64_t)r * mb;
+    for (int j0 = 0; j0 < cnt; j0 += kThreads) {
+      const int j = j0 + (int)threadIdx.x;
+      int page = -1, freed = 0;
+      if (j < cnt) {
+        page = checked_page(row[j], p.num_pages);
+        freed = page >= 0;
+        if (freed && p.page_shares) {
+          freed = atomicSub(&p.page_shares[page], 1) == 0;
+          if (freed) p.page_shares[page] = 0;
         }
-        *e = -1;
+        row[j] = -1;
       }
+      int chunk_total = 0;
+      const int excl = block_exclusive_scan<kWaves>(freed, lds_scan, &chunk_total);
+      if (freed) {
+        const int64_t slot = (int64_t)top + pushed + excl;
+        if (slot < p.num_pages) p.free_pages[slot] = page;
+        else err |= BARQ_KV_ERRBIT_BAD_INDEX;
+      }
+      pushed += chunk_total;
+    }
+    __syncthreads();  // every thread has read the row's mark before it is cleared
+    if (threadIdx.x == 0) {
       p.seq_lens[r] = 0;
       p.high_water[r] = 0;
     }
-    pushed += chunk_total;
   }
   if (threadIdx.x == 0) p.ctrl[BARQ_KV_CTRL_FREE_TOP] = (int)min((int64_t)top + pushed, p.num_pages);
   if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
@@ -791,153 +784,253 @@ __global__ void __launch_bounds__(kThreads) copy_rows_kernel(const CopyArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// In-place row selection with shared pages (copy-on-write beam ops).  Four launches:
-//   build   -- tile (new row i, block j): a block wholly below the source row's length keeps the
-//              source page and adds a reference; a later block (one an append or crop can still
-//              write) gets a page from the free stack (tails ranked in (row, block) order) and a
-//              copy of the source page.  The new table rows, lengths and marks go to workspace.
-//   commit  -- the stack top drops by the pages the tails took.
-//   release -- every old block drops its reference; pages left unheld are pushed on the stack.
-//   install -- the workspace rows become the table; other rows become empty.
-// References are added before any is dropped, so a page the new rows keep never reaches zero.
+// In-place row selection with shared pages (copy-on-write beam ops) over up to kSelectPools
+// pools of one geometry -- a model's layers -- per set of three launches.  New row i takes
+// source row rows[i]; its blocks wholly below the source's length are shared (one more
+// reference); its later blocks up to the high-water mark (the ones an append or a crop can still
+// write: the "tail") are moved when i is the first new row taking that source and the page is
+// held by that block alone, and copied into a page from the free stack otherwise.
+//   plan   -- workgroup per pool: first new row of every source row, each new row's copy count
+//             and rank (in row order), the total; if the free stack holds the copies the top
+//             drops by them, else the selection is abandoned (nothing changes, POOL_EXHAUSTED).
+//   build  -- workgroup (new row i, pool): shared blocks gain a reference, moved blocks keep
+//             their page, copied blocks take pages top-1-rank, ... and receive the copies.  The
+//             new table row, length and mark go to the pool's workspace slice.
+//   settle -- workgroup (row r, pool): old row r drops its references -- except its moved tail
+//             blocks, which its first taker holds on -- and a page no block holds any more is
+//             pushed on the stack; then row r becomes workspace row r (rows >= n: empty).  One
+//             workgroup reads and rewrites the row, so no other can race it.
+// Copies are made while every source page is still held, and references are added before any is
+// dropped, so a page the new rows keep never reaches zero.  Only copies need free pages: a beam
+// step whose rows end in partial pages copies one page per repeated source row.
 // ---------------------------------------------------------------------------------------------
 
-struct SelectArgs {
-  barq_kv_pool p;
-  const int32_t* rows;
-  int32_t* ws;       // [n * max_blocks] table, then [n] lengths, then [n] marks
-  int32_t n;
-  int64_t page_bytes;
-  FastDiv div_page;
-  FastDiv div_blocks;
+constexpr int kSelectPools = 32;
+constexpr int kSelectMaxBatch = 8192;  // the plan's first-taker table lives in LDS
+
+struct SelectPool {  // the per-pool pointers of a barq_kv_pool
+  const char* key_pages;
+  const char* value_pages;
+  int32_t* block_table;
+  int32_t* seq_lens;
+  int32_t* high_water;
+  int32_t* free_pages;
+  int32_t* ctrl;
+  int32_t* page_shares;
 };
 
-// Blocks of source row r that the selection copies (from the one holding seq_lens up to the
-// high-water mark), and where they start.
-__device__ __forceinline__ void tail_blocks(const barq_kv_pool& p, int r, const FastDiv& div_page,
+struct SelectArgs {
+  SelectPool pools[kSelectPools];
+  int32_t num_pages[kSelectPools];
+  const int32_t* rows;
+  int32_t* ws;            // per pool, ws_pool_words: see SelectWs
+  int64_t ws_pool_words;
+  int64_t page_bytes;
+  int32_t n;
+  int32_t max_batch;
+  int32_t max_blocks;
+  FastDiv div_page;
+};
+
+// A pool's workspace slice: the new rows' table [n * mb], lengths [n], marks [n], copy ranks
+// [n], the first taker of each old row [max_batch] (-1: not taken), the stack top before the
+// copies, and whether the selection goes ahead.
+struct SelectWs {
+  int32_t* table;
+  int32_t* lens;
+  int32_t* marks;
+  int32_t* rank;
+  int32_t* first;
+  int32_t* top;
+  int32_t* go;
+  __device__ SelectWs(const SelectArgs& a, int pool) {
+    table = a.ws + (int64_t)pool * a.ws_pool_words;
+    lens = table + (int64_t)a.n * a.max_blocks;
+    marks = lens + a.n;
+    rank = marks + a.n;
+    first = rank + a.n;
+    top = first + a.max_batch;
+    go = top + 1;
+  }
+};
+
+int64_t select_ws_pool_words(int64_t n, int64_t max_blocks, int64_t max_batch) {
+  return n * (max_blocks + 3) + max_batch + 2;
+}
+
+// Tail of source row r: blocks [first, first + count), from the one holding seq_lens up to the
+// high-water mark.
+__device__ __forceinline__ void tail_blocks(const SelectPool& p, int r, int mb, const FastDiv& div_page,
                                             int* first, int* count) {
-  const int mb = (int)p.max_blocks;
   const int nb = min(ceil_div_fd(p.high_water[r], div_page), mb);
   const int f = min((int)div_page.div((uint32_t)max(p.seq_lens[r], 0)), nb);
   *first = f;
   *count = nb - f;
 }
 
-template <int VB>
-__global__ void __launch_bounds__(kThreads) select_build_kernel(const SelectArgs a) {
-  __shared__ int s_meta[2];  // source page, new page of a copied block
-  const barq_kv_pool& p = a.p;
-  const int mb = (int)p.max_blocks;
-  const int i = (int)a.div_blocks.div(blockIdx.x);
-  const int j = (int)blockIdx.x - i * mb;
-  if (threadIdx.x < kWave) {
-    const int lane = threadIdx.x;
-    int acc = 0;  // copied blocks of new rows [0, i)
-    for (int q0 = 0; q0 < i; q0 += kWave) {
-      const int q = q0 + lane;
-      int c = 0;
-      if (q < i) {
-        const int r = a.rows[q];
-        if (r >= 0 && r < (int)p.max_batch) {
-          int f;
-          tail_blocks(p, r, a.div_page, &f, &c);
-        }
-      }
-      acc += wave_sum(c);
-    }
-    if (lane == 0) {
-      const int r = a.rows[i];
-      const bool valid = r >= 0 && r < (int)p.max_batch;
-      int src = -1, dst = -1, entry = -1, err = 0;
-      if (!valid) err |= BARQ_KV_ERRBIT_BAD_INDEX;
-      if (valid) {
-        int first, count;
-        tail_blocks(p, r, a.div_page, &first, &count);
-        if (j < first + count) {
-          const int old = checked_page(p.block_table[(int64_t)r * mb + j], p.num_pages);
-          if (j < first) {
-            entry = old;
-            if (old >= 0) atomicAdd(&p.page_shares[old], 1);
-          } else {
-            const int idx = p.ctrl[BARQ_KV_CTRL_FREE_TOP] - 1 - (acc + j - first);
-            dst = idx >= 0 ? checked_page(p.free_pages[idx], p.num_pages) : -1;
-            if (dst < 0) err |= BARQ_KV_ERRBIT_POOL_EXHAUSTED;
-            src = old;
-            entry = dst;
-          }
-        }
-      }
-      a.ws[(int64_t)i * mb + j] = entry;
-      if (j == 0) {
-        a.ws[(int64_t)a.n * mb + i] = valid ? p.seq_lens[r] : 0;
-        a.ws[(int64_t)a.n * mb + a.n + i] = valid ? p.high_water[r] : 0;
-      }
-      if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
-      s_meta[0] = src;
-      s_meta[1] = dst;
-    }
+__global__ void __launch_bounds__(kThreads) select_plan_kernel(const SelectArgs a) {
+  __shared__ int s_first[kSelectMaxBatch];
+  __shared__ int lds_scan[kWaves];
+  const SelectPool& p = a.pools[blockIdx.x];
+  const int num_pages = a.num_pages[blockIdx.x];
+  const SelectWs w(a, blockIdx.x);
+  const int mb = a.max_blocks;
+  for (int r = threadIdx.x; r < a.max_batch; r += kThreads) s_first[r] = INT_MAX;
+  __syncthreads();
+  for (int q = threadIdx.x; q < a.n; q += kThreads) {
+    const int r = a.rows[q];
+    if (r >= 0 && r < a.max_batch) atomicMin(&s_first[r], q);
   }
   __syncthreads();
-  const int sp = s_meta[0];
-  const int dp = s_meta[1];
-  if (sp >= 0 && dp >= 0) {
-    const int nvec = (int)(a.page_bytes / VB);
-    copy_run<VB>((const char*)p.key_pages + (int64_t)sp * a.page_bytes,
-                 (char*)p.key_pages + (int64_t)dp * a.page_bytes, nvec);
-    copy_run<VB>((const char*)p.value_pages + (int64_t)sp * a.page_bytes,
-                 (char*)p.value_pages + (int64_t)dp * a.page_bytes, nvec);
-  }
-}
-
-__global__ void __launch_bounds__(kThreads) select_commit_kernel(const SelectArgs a) {
-  __shared__ int lds_scan[kWaves];
+  for (int r = threadIdx.x; r < a.max_batch; r += kThreads)
+    w.first[r] = s_first[r] == INT_MAX ? -1 : s_first[r];
   int total = 0;
   for (int q0 = 0; q0 < a.n; q0 += kThreads) {
     const int q = q0 + (int)threadIdx.x;
     int c = 0;
     if (q < a.n) {
       const int r = a.rows[q];
-      if (r >= 0 && r < (int)a.p.max_batch) {
-        int f;
-        tail_blocks(a.p, r, a.div_page, &f, &c);
+      if (r >= 0 && r < a.max_batch) {
+        int f, cnt;
+        tail_blocks(p, r, mb, a.div_page, &f, &cnt);
+        if (s_first[r] != q) {
+          c = cnt;
+        } else {
+          for (int t = 0; t < cnt; ++t) {
+            const int page = checked_page(p.block_table[(int64_t)r * mb + f + t], num_pages);
+            c += page < 0 || p.page_shares[page] != 0;
+          }
+        }
       }
     }
     int chunk_total = 0;
-    block_exclusive_scan<kWaves>(c, lds_scan, &chunk_total);
+    const int excl = block_exclusive_scan<kWaves>(c, lds_scan, &chunk_total);
+    if (q < a.n) w.rank[q] = total + excl;
     total += chunk_total;
   }
-  if (threadIdx.x == 0)
-    a.p.ctrl[BARQ_KV_CTRL_FREE_TOP] = max(0, a.p.ctrl[BARQ_KV_CTRL_FREE_TOP] - total);
+  if (threadIdx.x == 0) {
+    const int top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
+    const bool go = total <= top;
+    *w.top = top;
+    *w.go = go;
+    if (go) p.ctrl[BARQ_KV_CTRL_FREE_TOP] = top - total;
+    else atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], BARQ_KV_ERRBIT_POOL_EXHAUSTED);
+  }
 }
 
-// Workgroup per old row: its blocks drop their references.
-__global__ void __launch_bounds__(kThreads) select_release_kernel(const SelectArgs a) {
-  const barq_kv_pool& p = a.p;
+template <int VB>
+__global__ void __launch_bounds__(kThreads) select_build_kernel(const SelectArgs a) {
+  __shared__ int s_meta[6];  // source row (-1: invalid), first tail block, tails, first taker?, rank, top
+  __shared__ int lds_scan[kWaves];
+  __shared__ int s_copy[2 * kThreads];  // (source, destination) pages of a chunk's copies
+  const SelectPool& p = a.pools[blockIdx.y];
+  const int num_pages = a.num_pages[blockIdx.y];
+  const SelectWs w(a, blockIdx.y);
+  const int mb = a.max_blocks;
+  const int i = blockIdx.x;
+  if (!*w.go) return;  // uniform: the plan abandoned the selection
+  if (threadIdx.x == 0) {
+    const int r = a.rows[i];
+    const bool valid = r >= 0 && r < a.max_batch;
+    int f = 0, cnt = 0;
+    if (valid) tail_blocks(p, r, mb, a.div_page, &f, &cnt);
+    else atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], BARQ_KV_ERRBIT_BAD_INDEX);
+    w.lens[i] = valid ? p.seq_lens[r] : 0;
+    w.marks[i] = valid ? p.high_water[r] : 0;
+    s_meta[0] = valid ? r : -1;
+    s_meta[1] = f;
+    s_meta[2] = cnt;
+    s_meta[3] = valid && w.first[r] == i;
+    s_meta[4] = w.rank[i];
+    s_meta[5] = *w.top;
+  }
+  __syncthreads();
+  const int r = s_meta[0], f = s_meta[1], cnt = s_meta[2], taker = s_meta[3], rank = s_meta[4], top = s_meta[5];
+  const int32_t* src_row = p.block_table + (int64_t)max(r, 0) * mb;
+  int32_t* dst_row = w.table + (int64_t)i * mb;
+  int err = 0;
+  for (int j = threadIdx.x; j < mb; j += kThreads) {
+    if (j < f) {
+      const int page = checked_page(src_row[j], num_pages);
+      if (page >= 0) atomicAdd(&p.page_shares[page], 1);
+      else err |= BARQ_KV_ERRBIT_BAD_INDEX;
+      dst_row[j] = page;
+    } else if (j >= f + cnt) {
+      dst_row[j] = -1;
+    }
+  }
+  // The tail, in chunks of one block per thread: moved blocks keep their page, the others take
+  // the next pages of the row's range on the stack and are copied by the whole workgroup.
+  const int nvec = (int)(a.page_bytes / VB);
+  int done = 0;
+  for (int t0 = 0; t0 < cnt; t0 += kThreads) {
+    const int t = t0 + (int)threadIdx.x;
+    int page = -1, copy = 0;
+    if (t < cnt) {
+      page = checked_page(src_row[f + t], num_pages);
+      if (page < 0) err |= BARQ_KV_ERRBIT_BAD_INDEX;
+      copy = !(taker && page >= 0 && p.page_shares[page] == 0);
+    }
+    int chunk_copies = 0;
+    const int k = block_exclusive_scan<kWaves>(copy, lds_scan, &chunk_copies);
+    if (t < cnt) {
+      int entry = page;
+      if (copy) {
+        const int idx = top - 1 - (rank + done + k);
+        entry = idx >= 0 ? checked_page(p.free_pages[idx], num_pages) : -1;
+        if (entry < 0) err |= BARQ_KV_ERRBIT_POOL_EXHAUSTED;
+        s_copy[2 * k] = page;
+        s_copy[2 * k + 1] = entry;
+      }
+      dst_row[f + t] = entry;
+    }
+    __syncthreads();
+    for (int c = 0; c < chunk_copies; ++c) {
+      const int sp = s_copy[2 * c], dp = s_copy[2 * c + 1];
+      if (sp < 0 || dp < 0) continue;
+      copy_run<VB>(p.key_pages + (int64_t)sp * a.page_bytes, (char*)p.key_pages + (int64_t)dp * a.page_bytes,
+                   nvec);
+      copy_run<VB>(p.value_pages + (int64_t)sp * a.page_bytes,
+                   (char*)p.value_pages + (int64_t)dp * a.page_bytes, nvec);
+    }
+    __syncthreads();
+    done += chunk_copies;
+  }
+  if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
+}
+
+__global__ void __launch_bounds__(kThreads) select_settle_kernel(const SelectArgs a) {
+  const SelectPool& p = a.pools[blockIdx.y];
+  const int num_pages = a.num_pages[blockIdx.y];
+  const SelectWs w(a, blockIdx.y);
   const int r = blockIdx.x;
-  const int mb = (int)p.max_blocks;
-  const int nb = min(ceil_div_fd(p.high_water[r], a.div_page), mb);
+  const int mb = a.max_blocks;
+  const int n = a.n;
+  if (!*w.go) return;  // uniform
+  int32_t* row = p.block_table + (int64_t)r * mb;
+  int f, nb;
+  tail_blocks(p, r, mb, a.div_page, &f, &nb);
+  nb += f;
+  const int taker = w.first[r];
+  const int32_t* kept = taker >= 0 ? w.table + (int64_t)taker * mb : nullptr;
+  int err = 0;
   for (int j = threadIdx.x; j < nb; j += kThreads) {
-    const int page = checked_page(p.block_table[(int64_t)r * mb + j], p.num_pages);
+    const int page = checked_page(row[j], num_pages);
     if (page < 0) continue;
+    if (kept && j >= f && kept[j] == page) continue;  // moved to its first taker
     if (atomicSub(&p.page_shares[page], 1) == 0) {
       p.page_shares[page] = 0;
       const int slot = atomicAdd(&p.ctrl[BARQ_KV_CTRL_FREE_TOP], 1);
-      if (slot < p.num_pages) p.free_pages[slot] = page;
-      else atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], BARQ_KV_ERRBIT_BAD_INDEX);
+      if (slot < num_pages) p.free_pages[slot] = page;
+      else err |= BARQ_KV_ERRBIT_BAD_INDEX;
     }
   }
-}
-
-// Workgroup per row: install the workspace row (rows >= n become empty).
-__global__ void __launch_bounds__(kThreads) select_install_kernel(const SelectArgs a) {
-  const barq_kv_pool& p = a.p;
-  const int r = blockIdx.x;
-  const int mb = (int)p.max_blocks;
-  for (int j = threadIdx.x; j < mb; j += kThreads)
-    p.block_table[(int64_t)r * mb + j] = r < a.n ? a.ws[(int64_t)r * mb + j] : -1;
+  if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
+  __syncthreads();  // every read of the old row (and of its length and mark) precedes the rewrite
+  for (int j = threadIdx.x; j < mb; j += kThreads) row[j] = r < n ? w.table[(int64_t)r * mb + j] : -1;
   if (threadIdx.x == 0) {
-    p.seq_lens[r] = r < a.n ? a.ws[(int64_t)a.n * mb + r] : 0;
-    p.high_water[r] = r < a.n ? a.ws[(int64_t)a.n * mb + a.n + r] : 0;
+    p.seq_lens[r] = r < n ? w.lens[r] : 0;
+    p.high_water[r] = r < n ? w.marks[r] : 0;
   }
 }
 
@@ -1240,34 +1333,68 @@ int barq_kv_free_rows(const barq_kv_pool* pool, const int32_t* rows, int64_t num
              : BARQ_KV_ERR_LAUNCH;
 }
 
-int barq_kv_select_rows(const barq_kv_pool* pool, const int32_t* src_rows, int64_t num_rows,
-                        int32_t* workspace, int64_t workspace_words, void* stream) {
-  if (!pool_ok(pool) || !pool->page_shares || num_rows < 0 || num_rows > pool->max_batch)
+int64_t barq_kv_select_workspace_words(const barq_kv_pool* pool, int64_t num_pools, int64_t num_rows) {
+  if (!pool_ok(pool) || num_pools < 1 || num_rows < 0 || num_rows > pool->max_batch ||
+      pool->max_batch > kSelectMaxBatch)
+    return -1;
+  return std::min<int64_t>(num_pools, kSelectPools) *
+         select_ws_pool_words(num_rows, pool->max_blocks, pool->max_batch);
+}
+
+int barq_kv_select_rows_layers(const barq_kv_pool* pools, int64_t num_pools, const int32_t* src_rows,
+                               int64_t num_rows, int32_t* workspace, int64_t workspace_words,
+                               void* stream) {
+  if (!pools || num_pools < 1) return BARQ_KV_ERR_INVALID;
+  const barq_kv_pool& g = pools[0];
+  for (int64_t l = 0; l < num_pools; ++l) {
+    const barq_kv_pool& p = pools[l];
+    if (!pool_ok(&p) || !p.page_shares || p.num_pages > kI32Max) return BARQ_KV_ERR_INVALID;
+    if (p.max_batch != g.max_batch || p.max_blocks != g.max_blocks || p.page_size != g.page_size ||
+        p.kv_heads != g.kv_heads || p.head_dim != g.head_dim || p.elem_bytes != g.elem_bytes)
+      return BARQ_KV_ERR_INVALID;
+    for (int64_t m = 0; m < l; ++m)  // a pool named twice would release its rows twice
+      if (pools[m].block_table == p.block_table || pools[m].ctrl == p.ctrl || pools[m].page_shares == p.page_shares)
+        return BARQ_KV_ERR_INVALID;
+  }
+  if (num_rows < 0 || num_rows > g.max_batch || g.max_batch > kSelectMaxBatch || g.max_blocks > kI32Max)
     return BARQ_KV_ERR_INVALID;
-  if (num_rows > 0 && (!src_rows || !workspace || workspace_words < num_rows * (pool->max_blocks + 2)))
+  const int64_t ws_pool_words = select_ws_pool_words(num_rows, g.max_blocks, g.max_batch);
+  if ((num_rows > 0 && !src_rows) || !workspace ||
+      workspace_words < std::min<int64_t>(num_pools, kSelectPools) * ws_pool_words)
     return BARQ_KV_ERR_INVALID;
-  if (num_rows * pool->max_blocks > kI32Max) return BARQ_KV_ERR_INVALID;
   SelectArgs a;
-  a.p = *pool;
   a.rows = src_rows;
   a.ws = workspace;
+  a.ws_pool_words = ws_pool_words;
+  a.page_bytes = g.page_size * g.kv_heads * g.head_dim * g.elem_bytes;
   a.n = (int32_t)num_rows;
-  a.page_bytes = pool->page_size * pool->kv_heads * pool->head_dim * pool->elem_bytes;
-  a.div_page = FastDiv::make((uint32_t)pool->page_size);
-  a.div_blocks = FastDiv::make((uint32_t)pool->max_blocks);
+  a.max_batch = (int32_t)g.max_batch;
+  a.max_blocks = (int32_t)g.max_blocks;
+  a.div_page = FastDiv::make((uint32_t)g.page_size);
   hipStream_t s = (hipStream_t)stream;
-  const uint64_t bits = (uint64_t)a.page_bytes | (uint64_t)(uintptr_t)pool->key_pages |
-                        (uint64_t)(uintptr_t)pool->value_pages;
   int rc = BARQ_KV_OK;
-  if (num_rows > 0) {
-    rc = launch_select_build_kernel(vector_bytes(bits), dim3((uint32_t)(num_rows * pool->max_blocks)), &a, s);
-    if (rc == BARQ_KV_OK) rc = launch((const void*)&select_commit_kernel, dim3(1), &a, s);
+  for (int64_t l0 = 0; l0 < num_pools && rc == BARQ_KV_OK; l0 += kSelectPools) {
+    const int set = (int)std::min<int64_t>(kSelectPools, num_pools - l0);
+    uint64_t bits = (uint64_t)a.page_bytes;
+    for (int k = 0; k < kSelectPools; ++k) {
+      const barq_kv_pool& p = pools[l0 + std::min(k, set - 1)];
+      a.pools[k] = SelectPool{(const char*)p.key_pages, (const char*)p.value_pages, p.block_table, p.seq_lens,
+                              p.high_water, p.free_pages, p.ctrl, p.page_shares};
+      a.num_pages[k] = (int32_t)p.num_pages;
+      bits |= (uint64_t)(uintptr_t)p.key_pages | (uint64_t)(uintptr_t)p.value_pages;
+    }
+    rc = launch((const void*)&select_plan_kernel, dim3((uint32_t)set), &a, s);
+    if (rc == BARQ_KV_OK && num_rows > 0)
+      rc = launch_select_build_kernel(vector_bytes(bits), dim3((uint32_t)num_rows, (uint32_t)set), &a, s);
+    if (rc == BARQ_KV_OK)
+      rc = launch((const void*)&select_settle_kernel, dim3((uint32_t)g.max_batch, (uint32_t)set), &a, s);
   }
-  if (rc == BARQ_KV_OK)
-    rc = launch((const void*)&select_release_kernel, dim3((uint32_t)pool->max_batch), &a, s);
-  if (rc == BARQ_KV_OK)
-    rc = launch((const void*)&select_install_kernel, dim3((uint32_t)pool->max_batch), &a, s);
   return rc;
+}
+
+int barq_kv_select_rows(const barq_kv_pool* pool, const int32_t* src_rows, int64_t num_rows,
+                        int32_t* workspace, int64_t workspace_words, void* stream) {
+  return barq_kv_select_rows_layers(pool, 1, src_rows, num_rows, workspace, workspace_words, stream);
 }
 
 int barq_kv_copy_rows(const barq_kv_pool* src, const barq_kv_pool* dst, const int32_t* src_rows,

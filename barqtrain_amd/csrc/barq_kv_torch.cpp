@@ -248,6 +248,50 @@ void pool_select_rows_(std::vector<at::Tensor> pool, at::Tensor rows, at::Tensor
                "pool_select_rows_");
 }
 
+// The pools of a model's layers packed as an array of barq_kv_pool (a CPU uint8 tensor), for
+// the batched entry points.  The array holds raw device pointers: the caller keeps the pools'
+// tensors alive and unmoved while it uses it.
+at::Tensor pool_group(std::vector<std::vector<at::Tensor>> pools) {
+  TORCH_CHECK(!pools.empty(), "a pool group needs at least one pool");
+  at::Tensor out = at::empty({(int64_t)(pools.size() * sizeof(barq_kv_pool))}, at::kByte);
+  auto* dst = reinterpret_cast<barq_kv_pool*>(out.data_ptr<uint8_t>());
+  const int64_t device = pools[0][0].get_device();
+  for (size_t i = 0; i < pools.size(); ++i) {
+    dst[i] = pool_from(pools[i]);
+    TORCH_CHECK(pools[i][0].get_device() == device, "the pools of a group must share a device");
+  }
+  return out;
+}
+
+const barq_kv_pool* group_pools(const at::Tensor& group, int64_t* count) {
+  TORCH_CHECK(group.device().is_cpu() && group.scalar_type() == at::kByte && group.is_contiguous() &&
+                  group.numel() > 0 && group.numel() % (int64_t)sizeof(barq_kv_pool) == 0,
+              "not a pool group (see pool_group)");
+  *count = group.numel() / (int64_t)sizeof(barq_kv_pool);
+  return reinterpret_cast<const barq_kv_pool*>(group.data_ptr<uint8_t>());
+}
+
+int64_t select_workspace_words(at::Tensor group, int64_t num_rows) {
+  int64_t n = 0;
+  const barq_kv_pool* pools = group_pools(group, &n);
+  return barq_kv_select_workspace_words(pools, n, num_rows);
+}
+
+// rows: int32 on the pools' device; workspace: int32 of select_workspace_words(group, rows).
+void pool_group_select_rows_(at::Tensor group, at::Tensor rows, at::Tensor workspace) {
+  int64_t n = 0;
+  const barq_kv_pool* pools = group_pools(group, &n);
+  TORCH_CHECK(rows.is_cuda() && rows.scalar_type() == at::kInt && rows.is_contiguous(),
+              "rows must be contiguous int32 on the pools' device");
+  TORCH_CHECK(workspace.is_cuda() && workspace.scalar_type() == at::kInt && workspace.is_contiguous() &&
+                  workspace.get_device() == rows.get_device(),
+              "workspace must be contiguous int32 on the pools' device");
+  c10::DeviceGuard guard(rows.device());
+  check_status(barq_kv_select_rows_layers(pools, n, rows.data_ptr<int32_t>(), rows.numel(),
+                                          workspace.data_ptr<int32_t>(), workspace.numel(), current_stream(rows)),
+               "pool_group_select_rows_");
+}
+
 int64_t attention_workspace_bytes(std::vector<at::Tensor> pool, int64_t batch, int64_t q_heads,
                                   int64_t tokens, int64_t max_seq, int64_t split_tokens) {
   barq_kv_pool p = pool_from(pool);
@@ -301,6 +345,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("pool_free_rows_", &pool_free_rows_, "Return rows' pages to the free stack");
   m.def("pool_copy_rows_", &pool_copy_rows_, "Build rows of a fresh pool as copies of source rows");
   m.def("pool_select_rows_", &pool_select_rows_, "Rows become selected rows, sharing their full pages");
+  m.def("pool_group", &pool_group, "Pack the pools of a model's layers for the batched entry points");
+  m.def("select_workspace_words", &select_workspace_words, "Workspace words of pool_group_select_rows_");
+  m.def("pool_group_select_rows_", &pool_group_select_rows_,
+        "One row selection applied to every pool of a group, sharing full pages");
   m.def("attention_workspace_bytes", &attention_workspace_bytes,
         "Workspace bytes of a decode-attention launch (-1: arguments rejected)");
   m.def("pool_decode_attention", &pool_decode_attention,

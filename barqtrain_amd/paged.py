@@ -88,7 +88,9 @@ class PagePool:
         self.head_dim = int(head_dim)
         self.dtype = dtype
         self.device = torch.device(device)
-        self.num_pages = int(num_pages) if num_pages is not None else self.max_batch * self.max_blocks
+        # Default: every row at capacity, plus one page per row for the copies a beam selection
+        # makes before the pages it drops return (at most one per row while no crop intervenes).
+        self.num_pages = int(num_pages) if num_pages is not None else self.max_batch * (self.max_blocks + 1)
         if min(self.max_batch, self.max_blocks, self.page_size, self.kv_heads, self.head_dim, self.num_pages) < 1:
             raise ValueError("page pool dimensions must be positive")
         if self.num_pages >= 2**31 or self.max_batch * self.max_blocks >= 2**31:
@@ -109,6 +111,8 @@ class PagePool:
         self.free_count = self.num_pages
         self.free_exact = True   # free_count equals the device's free stack (else a lower bound)
         self.shared = False      # some page may be held by more than one block
+        self.tails_shared = False  # a crop may have left shared pages in rows' tails
+        self.generation = 0      # bumped whenever the tensors are replaced (cached pool groups)
         self.reset(page_order)
 
     # ------------------------------------------------------------------ plumbing
@@ -200,6 +204,7 @@ class PagePool:
         self.free_count = self.num_pages
         self.free_exact = True
         self.shared = False
+        self.tails_shared = False
 
     def _check_states(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
         if key_states.dim() != 4 or key_states.shape != value_states.shape:
@@ -272,6 +277,8 @@ class PagePool:
         self._ops().pool_crop_(self.tensors, batch, max_length)
         np.minimum(self.lens[:batch], max_length, out=self.lens[:batch])
         if self.shared:
+            # the identity selection moves every exclusive tail page and copies the shared ones
+            self.tails_shared = True
             self.select_rows(list(range(self.max_batch)))
 
     def free_rows(self, rows: Sequence[int]) -> None:
@@ -293,38 +300,61 @@ class PagePool:
         self.hw[r] = 0
 
     def tail_block_counts(self, rows: np.ndarray) -> np.ndarray:
-        """Blocks of each row that a selection copies: from the one holding seq_lens up to the
-        high-water mark (the blocks an append or a crop can still write)."""
+        """Tail blocks of each row: from the one holding seq_lens up to the high-water mark (the
+        blocks an append or a crop can still write, which a selection moves or copies)."""
         nb = np.minimum(-(-self.hw[rows] // self.page_size), self.max_blocks)
         return nb - np.minimum(self.lens[rows] // self.page_size, nb)
+
+    @staticmethod
+    def repeated_mask(rows: np.ndarray) -> np.ndarray:
+        """True where a selection takes a source row that an earlier new row already took."""
+        mask = np.ones(len(rows), dtype=bool)
+        mask[np.unique(rows, return_index=True)[1]] = False
+        return mask
+
+    def select_copy_bound(self, rows: np.ndarray) -> int:
+        """Pages a selection copies, at most: the tails of repeated takers, plus the first
+        takers' tails when a crop may have left shared pages there."""
+        tails = self.tail_block_counts(rows)
+        return int(tails.sum() if self.tails_shared else tails[self.repeated_mask(rows)].sum())
+
+    def select_workspace_words(self, num_rows: int) -> int:
+        """int32 words of a one-pool selection's workspace (barq_kv_select_workspace_words)."""
+        return num_rows * (self.max_blocks + 3) + self.max_batch + 2
+
+    def _selection(self, src_rows: Sequence[int]) -> np.ndarray:
+        rows = np.asarray([int(r) for r in src_rows], dtype=np.int64)
+        if len(rows) > self.max_batch:
+            raise ValueError("select_rows: more rows than the pool holds")
+        if len(rows) and (rows.min() < 0 or rows.max() >= self.max_batch):
+            raise IndexError("select_rows: row out of range")
+        return rows
+
+    def _selected(self, lens: np.ndarray, hw: np.ndarray, need: int) -> None:
+        """Host shadow after a selection: the new rows' lengths and marks (other rows empty)."""
+        self.lens, self.hw = lens, hw
+        self.free_count -= need
+        self.free_exact = False   # moves, copies and released pages are settled on the device
+        self.shared = True
+        self.tails_shared = False
 
     def select_rows(self, src_rows: Sequence[int]) -> None:
         """In place: row i becomes row src_rows[i] (repeats allowed), every other row empty.
         Full blocks are shared (copy-on-write), so the cost is the rows' partial last blocks,
         not their history (reference: kv_cache.py:166-186, which copies the whole cache)."""
-        src_rows = [int(r) for r in src_rows]
-        n = len(src_rows)
-        if n > self.max_batch:
-            raise ValueError("select_rows: more rows than the pool holds")
-        if any(r < 0 or r >= self.max_batch for r in src_rows):
-            raise IndexError("select_rows: row out of range")
-        r = np.asarray(src_rows, dtype=np.int64)
-        need = int(self.tail_block_counts(r).sum()) if n else 0
+        r = self._selection(src_rows)
+        n = len(r)
+        need = self.select_copy_bound(r) if n else 0
         self.ensure_free(need, "select_rows")
-        words = max(n * (self.max_blocks + 2), 1)
+        words = self.select_workspace_words(n)
         ws = getattr(self, "_select_ws", None)
         if ws is None or ws.numel() < words:
             ws = torch.empty((words,), dtype=torch.int32, device=self.device)
             self._select_ws = ws
-        self._ops().pool_select_rows_(self.tensors, self._index_tensor(src_rows or [0])[:n], ws)
-        lens, hw = self.lens[r].copy(), self.hw[r].copy()
-        self.lens[:] = 0
-        self.hw[:] = 0
-        self.lens[:n] = lens
-        self.hw[:n] = hw
-        self.free_count -= need
-        self.free_exact = False   # the released pages return on the device
-        self.shared = True
+        self._ops().pool_select_rows_(self.tensors, self._index_tensor(r.tolist() or [0])[:n], ws)
+        lens, hw = np.zeros_like(self.lens), np.zeros_like(self.hw)
+        lens[:n], hw[:n] = self.lens[r], self.hw[r]
+        self._selected(lens, hw, need)
 
     def copy_rows(self, src_rows: Sequence[int], num_pages: Optional[int] = None) -> "PagePool":
         """A new pool whose row i copies row src_rows[i] of this one (repeats allowed)."""
@@ -414,7 +444,67 @@ class PagePool:
                      "page_shares"):
             setattr(self, name, getattr(self, name).to(device, non_blocking=True))
         self.device = device
+        self.generation += 1
         return self
+
+
+_GROUPS: dict = {}
+
+
+def _pool_group(pools: list[PagePool]):
+    """(packed pool array, workspace) of a list of GPU pools, cached while their tensors stay."""
+    key = tuple((id(p), p.generation) for p in pools)
+    entry = _GROUPS.get(key)
+    if entry is None:
+        if len(_GROUPS) >= 8:
+            _GROUPS.clear()
+        # the entry holds the pools, so the ids in its key stay theirs
+        entry = {"pools": list(pools), "group": _gpu_backend().pool_group([p.tensors for p in pools]),
+                 "ws": None}
+        _GROUPS[key] = entry
+    return entry
+
+
+def select_rows_layers(pools: Sequence[PagePool], src_rows: Sequence[int]) -> None:
+    """``PagePool.select_rows(src_rows)`` on every pool -- a model's layers, as
+    ``Cache.reorder_cache`` / ``batch_select_indices`` apply one selection to all of them
+    (kv_cache.py:166-186 per layer) -- in one set of launches when the pools are GPU pools of one
+    geometry; every pool is checked for room before any is changed."""
+    pools = list(pools)
+    if not pools:
+        return
+    g = pools[0]
+    geom = (g.device, g.max_batch, g.max_blocks, g.page_size, g.kv_heads, g.head_dim, g.dtype)
+    batched = (len(pools) > 1 and g.on_gpu and len({id(p) for p in pools}) == len(pools)
+               and all((p.device, p.max_batch, p.max_blocks, p.page_size, p.kv_heads, p.head_dim, p.dtype) == geom
+                       for p in pools))
+    if not batched:
+        for p in pools:
+            p._selection(src_rows)
+        for p in pools:
+            p.select_rows(src_rows)
+        return
+    r = g._selection(src_rows)
+    n = len(r)
+    lens = np.stack([p.lens for p in pools])
+    hw = np.stack([p.hw for p in pools])
+    P = g.page_size
+    nb = np.minimum(-(-hw[:, r] // P), g.max_blocks)
+    tails = nb - np.minimum(lens[:, r] // P, nb)
+    repeated = PagePool.repeated_mask(r)
+    need = np.where([p.tails_shared for p in pools], tails.sum(axis=1), tails[:, repeated].sum(axis=1))
+    for p, k in zip(pools, need.tolist()):
+        p.ensure_free(int(k), "select_rows")
+    entry = _pool_group(pools)
+    backend = _gpu_backend()
+    words = int(backend.select_workspace_words(entry["group"], n))
+    if entry["ws"] is None or entry["ws"].numel() < words:
+        entry["ws"] = torch.empty((words,), dtype=torch.int32, device=g.device)
+    backend.pool_group_select_rows_(entry["group"], g._index_tensor(r.tolist() or [0])[:n], entry["ws"])
+    new_lens, new_hw = np.zeros_like(lens), np.zeros_like(hw)
+    new_lens[:, :n], new_hw[:, :n] = lens[:, r], hw[:, r]
+    for l, (p, k) in enumerate(zip(pools, need.tolist())):
+        p._selected(new_lens[l], new_hw[l], int(k))
 
 
 class _HostOps:
@@ -572,46 +662,60 @@ class _HostOps:
 
     @staticmethod
     def pool_select_rows_(t, rows, workspace=None):
-        """In-place selection with shared full blocks (the algorithm of select_build / commit /
-        release / install in barq_kv.hip)."""
+        """In-place selection with shared full blocks and moved or copied tails, all or nothing
+        (the algorithm of select_plan / select_build / select_settle in barq_kv.hip)."""
         kp, vp, bt, lens, hw, free, ctrl, shares = t
         P, MB = _HostOps._geometry(t)
         rows = rows.tolist()
-        top = int(ctrl[CTRL_FREE_TOP])
-        new_bt = torch.full((len(rows), MB), -1, dtype=torch.int32)
-        new_lens = torch.zeros(len(rows), dtype=torch.int32)
-        new_hw = torch.zeros(len(rows), dtype=torch.int32)
-        used = 0
-        err = 0
-        for i, r in enumerate(rows):
+        n, B = len(rows), bt.shape[0]
+
+        def tail(r):
             nb = min(-(-int(hw[r]) // P), MB)
-            first = min(int(lens[r]) // P, nb)
+            f = min(int(lens[r]) // P, nb)
+            return f, nb
+
+        first = {}
+        for i, r in enumerate(rows):
+            first.setdefault(r, i)
+        moved = set()  # (old row, block) whose page its first taker keeps
+        copies = 0
+        for i, r in enumerate(rows):
+            f, nb = tail(r)
+            for j in range(f, nb):
+                if first[r] == i and int(shares[int(bt[r, j])]) == 0:
+                    moved.add((r, j))
+                else:
+                    copies += 1
+        top = int(ctrl[CTRL_FREE_TOP])
+        if copies > top:
+            ctrl[CTRL_ERRORS] |= ERRBIT_POOL_EXHAUSTED
+            return
+        new_bt = torch.full((n, MB), -1, dtype=torch.int32)
+        used = 0
+        for i, r in enumerate(rows):
+            f, nb = tail(r)
             for j in range(nb):
                 old = int(bt[r, j])
-                if j < first:
-                    new_bt[i, j] = old
+                if j < f:
                     shares[old] += 1
+                    new_bt[i, j] = old
+                elif (r, j) in moved and first[r] == i:
+                    new_bt[i, j] = old
                 else:
-                    idx = top - 1 - used
+                    page = int(free[top - 1 - used])
                     used += 1
-                    page = int(free[idx]) if idx >= 0 else -1
-                    if page < 0:
-                        err |= ERRBIT_POOL_EXHAUSTED
-                    else:
-                        kp[page] = kp[old]
-                        vp[page] = vp[old]
+                    kp[page] = kp[old]
+                    vp[page] = vp[old]
                     new_bt[i, j] = page
-            new_lens[i] = lens[r]
-            new_hw[i] = hw[r]
-        top = max(0, top - used)
-        for r in range(bt.shape[0]):
-            nb = min(-(-int(hw[r]) // P), MB)
+        new_lens = lens[rows].clone() if n else torch.zeros(0, dtype=torch.int32)
+        new_hw = hw[rows].clone() if n else torch.zeros(0, dtype=torch.int32)
+        top -= used
+        for r in range(B):
+            _, nb = tail(r)
             for j in range(nb):
-                top = _HostOps._release(t, int(bt[r, j]), top)
+                if (r, j) not in moved:
+                    top = _HostOps._release(t, int(bt[r, j]), top)
         ctrl[CTRL_FREE_TOP] = top
-        if err:
-            ctrl[CTRL_ERRORS] |= err
-        n = len(rows)
         bt.fill_(-1)
         lens.zero_()
         hw.zero_()

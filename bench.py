@@ -37,11 +37,12 @@ timed run left them: one call per layer with G query heads per KV head (4, the L
 visible K and V element once + query + output.  Layer 0 is checked against an fp32 attention over
 the gathered K/V.
 
-`beam_select` times a beam reorder (batch_select_indices / reorder_cache) of every layer one
-decode step past the prefill: the in-place selection that shares full pages and copies each
-row's partial last page (graph-replayed; also as host calls), next to the reference's dense
-keys[indices] over [B, H, blocks, P, D] on the same GPU; layer 0 is checked bit for bit against
-the gathered rows before the selections, and the pool's sharing invariants are checked.
+`beam_select` times a beam reorder (Cache.reorder_cache) of every layer one decode step past
+the prefill: one in-place selection for all layers that shares full pages, moves each taken
+row's partial last page and copies it only for repeated rows (graph-replayed; also as the host
+call), next to the reference's dense keys[indices] over [B, H, blocks, P, D] per layer on the
+same GPU; layer 0 is checked bit for bit against the gathered rows before the selections, and
+the pool's sharing invariants are checked.
 
 Prints ONE JSON line.  `--pmc-probe` instead runs the eager workload the rocprof counter runs
 profile: a 64 MiB elementwise pass (calibration), the prefill, then the decode steps.
@@ -344,15 +345,16 @@ def attention_leg(cfg, pools, B, dev, reps=20):
 
 
 def beam_leg(cfg, wl, dev, reps=20):
-    """Beam reorder (batch_select_indices / reorder_cache) of every layer, one decode step past the
-    prefill so that every row ends in a partial page: in-place selection sharing full pages, timed
-    as a graph replay (device time) and as host calls through PagePool.select_rows; beside it, the
-    reference's own operation on the same GPU -- keys[indices] / values[indices] over the dense
-    [B, H, blocks, P, D] cache (kv_cache.py:175-183) -- timed on one layer and scaled by layers."""
+    """Beam reorder (Cache.reorder_cache / batch_select_indices) of every layer, one decode step
+    past the prefill so that every row ends in a partial page: one selection for all layers in one
+    set of launches (barq_kv_select_rows_layers), timed as a graph replay (device time) and as the
+    host call select_rows_layers; beside it, the reference's own operation on the same GPU --
+    keys[indices] / values[indices] over the dense [B, H, blocks, P, D] cache of every layer
+    (kv_cache.py:175-183), timed on one layer and scaled by the layer count."""
     import numpy as np
     import torch
 
-    from barqtrain_amd.paged import _gpu_backend
+    from barqtrain_amd.paged import _gpu_backend, _pool_group, select_rows_layers
     from capi_pool import check_pool_invariants
 
     backend = _gpu_backend()
@@ -364,36 +366,29 @@ def beam_leg(cfg, wl, dev, reps=20):
     torch.cuda.synchronize()
     rows = sorted(np.random.default_rng(cfg["seed"] + 29).integers(0, B, size=B).tolist())
     k0, v0 = (t.clone() for t in pools[0].gather(B))
-    tails = int(pools[0].tail_block_counts(np.asarray(rows)).sum())
+    r = np.asarray(rows)
+    copies = int(pools[0].tail_block_counts(r)[pools[0].repeated_mask(r)].sum())
     page_bytes = P * H * D * pools[0].dtype.itemsize
-    sel_bytes = tails * page_bytes * 2 * 2  # K and V pages, read + written
+    sel_bytes = copies * page_bytes * 2 * 2  # K and V pages, read + written
 
-    def host_calls():
-        for pool in pools:
-            pool.select_rows(rows)
-
-    host_calls()  # warm (pinned index buffers, workspaces)
+    select_rows_layers(pools, rows)  # warm (pinned index buffer, pool group, workspace)
     torch.cuda.synchronize()
     host_best = None
     for _ in range(5):
         t0 = time.perf_counter()
-        host_calls()
+        select_rows_layers(pools, rows)
         torch.cuda.synchronize()
         dt = time.perf_counter() - t0
         host_best = dt if host_best is None else min(host_best, dt)
+    entry = _pool_group(pools)
     idx = torch.tensor(rows, dtype=torch.int32, device=dev)
-    ws = pools[0]._select_ws
-
-    def device_calls():
-        for pool in pools:
-            backend.pool_select_rows_(pool.tensors, idx, ws)
 
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        device_calls()
+        backend.pool_group_select_rows_(entry["group"], idx, entry["ws"])
     graph.replay()
     torch.cuda.synchronize()
-    applied = 6 + 1  # host_calls ran 6 times, the warm replay once
+    applied = 6 + 1  # host calls 6, warm replay 1
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -407,7 +402,7 @@ def beam_leg(cfg, wl, dev, reps=20):
         raise SystemExit("device error bits set by the beam leg")
     order = np.arange(B)
     for _ in range(applied):
-        order = order[np.asarray(rows)]
+        order = order[r]
     sel = torch.as_tensor(order, device=dev)
     k1, v1 = pools[0].gather(B, k0.shape[2])  # the host shadow lags the graph replays
     ok = bool(torch.equal(k1.view(torch.int16), k0[sel].view(torch.int16))
@@ -442,19 +437,20 @@ def beam_leg(cfg, wl, dev, reps=20):
     dense_ms = start.elapsed_time(end) / reps
     dense_bytes = 2 * 2 * kd.numel() * kd.element_size()
     del kd, vd, ko, vo
+    sets = -(-L // 32)
     return {
-        "kernels": "select_build_kernel + select_commit_kernel + select_release_kernel + select_install_kernel",
+        "kernels": f"select_plan_kernel + select_build_kernel + select_settle_kernel, {sets} set(s) of "
+                   f"launches for {L} layers",
         "selection": f"{B} rows from sorted seeded parents ({len(set(rows))} distinct), context "
                      f"{int(pool.lens[:B].min())}..{int(pool.lens[:B].max())}",
-        "us_per_layer": round(graph_ms * 1e3 / L, 2),
         "us_per_step_all_layers": round(graph_ms * 1e3, 1),
         "host_us_per_step_all_layers": round(host_best * 1e6, 1),
-        "pages_copied_per_layer": tails,
+        "pages_copied_per_layer": copies,
         "bytes_copied_per_layer": sel_bytes,
         "pages_held_layer0": held,
-        "reference_dense_index_us_per_layer": round(dense_ms * 1e3, 2),
+        "reference_dense_index_us_per_step": round(dense_ms * 1e3 * L, 1),
         "reference_dense_bytes_per_layer": dense_bytes,
-        "speedup_vs_reference_dense": round(dense_ms / (graph_ms / L), 1),
+        "speedup_vs_reference_dense": round(dense_ms * L / graph_ms, 1),
         "parity": {"layer0_bit_exact_after_selections": ok, "selections_applied": applied,
                    "invariants_checked": True},
     }

@@ -27,6 +27,11 @@
  *   barq_kv_select_rows   <- batch_select_indices / batch_repeat_interleave / reorder_cache,
  *                            python/barqtrain/kv_cache.py:166-186, in place: rows share their
  *                            full pages (copy-on-write) instead of copying the cache.
+ *   barq_kv_select_rows_layers, barq_kv_select_workspace_words
+ *                         <- Cache.reorder_cache / batch_select_indices / batch_repeat_interleave
+ *                            (transformers cache_utils, which the reference's BarqPagedKVCache
+ *                            inherits, python/barqtrain/kv_cache.py:197-223): one selection for
+ *                            every layer, in one set of launches.
  *   barq_kv_decode_attention, barq_kv_attention_workspace_bytes
  *                         <- no reference counterpart: the "gather/scatter kernels for attention
  *                            reads" the reference planned (IMPLEMENTATION_PLAN.md:90-91); it
@@ -172,7 +177,8 @@ int barq_kv_update(const barq_kv_pool* pool, const void* key_states, const void*
  * seq_lens[b] = min(seq_lens[b], max_length) for rows [0, batch).  Page data is kept.  On a pool
  * whose rows share pages a crop can leave a shared block at or above its row's new length, where
  * the next append would write it for every row holding it: call barq_kv_select_rows with
- * src_rows = 0, 1, ..., max_batch - 1 before that append; it gives such blocks pages of their own.
+ * src_rows = 0, 1, ..., max_batch - 1 before that append; it gives such blocks pages of their own
+ * (and moves, rather than copies, every page only one block holds).
  */
 int barq_kv_crop(const barq_kv_pool* pool, int64_t batch, int64_t max_length, void* stream);
 
@@ -187,14 +193,35 @@ int barq_kv_free_rows(const barq_kv_pool* pool, const int32_t* rows, int64_t num
  * In place: row i, for i in [0, num_rows), becomes row src_rows[i] as it was before the call
  * (src_rows: device int32 [num_rows], values in [0, max_batch), repeats allowed); every other
  * row becomes empty.  A row's blocks wholly below its seq_lens are shared with the source row
- * (page_shares counts the extra references); the blocks an append or a crop can still write --
- * from the one holding position seq_lens up to high_water -- are copied into pages taken from
- * the free stack, in (row, block) order.  Pages no block holds any more return to the stack.
- * Needs page_shares, num_rows <= max_batch, and workspace of int32 [num_rows * (max_blocks + 2)].
- * Launches four kernels on the stream; a pool exhausted midway sets BARQ_KV_ERRBIT_POOL_EXHAUSTED.
+ * (page_shares counts the extra references).  The blocks an append or a crop can still write --
+ * from the one holding position seq_lens up to high_water -- move to the first new row taking
+ * the source when no other block holds their page, and are copied into pages from the free
+ * stack otherwise: a permutation copies nothing, a beam step one partial page per repeated
+ * source.  All or nothing: when the free stack cannot hold the copies, nothing changes and
+ * BARQ_KV_ERRBIT_POOL_EXHAUSTED is set.  Pages no block holds any more return to the stack, in
+ * no fixed order.  Needs page_shares, num_rows <= max_batch <= 8192, and a workspace of
+ * barq_kv_select_workspace_words(pool, 1, num_rows) int32 words (also for num_rows = 0).
+ * Three kernels on the stream.
  */
 int barq_kv_select_rows(const barq_kv_pool* pool, const int32_t* src_rows, int64_t num_rows,
                         int32_t* workspace, int64_t workspace_words, void* stream);
+
+/*
+ * barq_kv_select_rows applied with the same src_rows to each of num_pools pools (a model's
+ * layers, as Cache.reorder_cache / batch_select_indices apply one selection to every layer), in
+ * one set of three launches per 32 pools, each pool all or nothing as in barq_kv_select_rows.
+ * The pools must be distinct, each with page_shares,
+ * and share max_batch, max_blocks, page_size, kv_heads, head_dim and elem_bytes (num_pages may
+ * differ).  Workspace: int32 [barq_kv_select_workspace_words(pools, num_pools, num_rows)].
+ */
+int barq_kv_select_rows_layers(const barq_kv_pool* pools, int64_t num_pools, const int32_t* src_rows,
+                               int64_t num_rows, int32_t* workspace, int64_t workspace_words,
+                               void* stream);
+
+/* Workspace words barq_kv_select_rows_layers needs -- min(num_pools, 32) *
+ * (num_rows * (max_blocks + 3) + max_batch + 2) -- or -1 for arguments it rejects (num_pools < 1,
+ * num_rows outside [0, max_batch], max_batch > 8192).  num_pools = 1 gives barq_kv_select_rows'. */
+int64_t barq_kv_select_workspace_words(const barq_kv_pool* pool, int64_t num_pools, int64_t num_rows);
 
 /*
  * Row i of dst, for i in [0, num_rows), becomes a copy of row src_rows[i] of src (device int32

@@ -101,7 +101,9 @@ class CPool:
 
     def select_rows(self, rows):
         idx = torch.tensor(rows, dtype=torch.int32, device=self.kp.device)
-        ws = torch.empty(max(len(rows) * (self.max_blocks + 2), 1), dtype=torch.int32, device=self.kp.device)
+        words = self.lib.barq_kv_select_workspace_words(self.ref, 1, len(rows))
+        assert words > 0
+        ws = torch.empty(words, dtype=torch.int32, device=self.kp.device)
         _capi.check(self.lib.barq_kv_select_rows(self.ref, idx.data_ptr(), len(rows), ws.data_ptr(), ws.numel(),
                                                  self._stream()))
         torch.cuda.current_stream().synchronize()

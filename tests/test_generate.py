@@ -76,3 +76,24 @@ def test_generate_with_paged_attention_on_host_pool():
                          past_key_values=cache, return_dict_in_generate=True, output_logits=True)
     assert torch.equal(got.sequences, ref.sequences)
     torch.testing.assert_close(torch.stack(got.logits), torch.stack(ref.logits), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("page", [4, 16])
+def test_beam_search_matches_dynamic_cache(page):
+    """num_beams=4: generate reorders the cache after every step (Cache.reorder_cache); the
+    paged cache selects rows in place, sharing full pages between beams, and returns the same
+    beams with the same scores as DynamicCache."""
+    from transformers.cache_utils import DynamicCache
+
+    model, cfg = tiny_llama()
+    model.config._attn_implementation = "eager"
+    ids = torch.randint(1, 512, (2, 13), generator=torch.Generator().manual_seed(4))
+    new = 20
+    kw = dict(attention_mask=torch.ones_like(ids), max_new_tokens=new, do_sample=False, num_beams=4,
+              num_return_sequences=2, return_dict_in_generate=True, output_scores=True)
+    ref = model.generate(ids, past_key_values=DynamicCache(config=cfg), **kw)
+    cache = create_paged_kv_cache(model, max_batch_size=8, max_cache_len=13 + new, page_size=page)
+    got = model.generate(ids, past_key_values=cache, **kw)
+    assert torch.equal(got.sequences, ref.sequences)
+    assert torch.equal(got.sequences_scores, ref.sequences_scores)
+    assert all(layer.pool.shared for layer in cache.layers), "beams never shared pages"
