@@ -42,6 +42,24 @@ class BarqKVPool(ctypes.Structure):
     ]
 
 
+class BarqKVCold(ctypes.Structure):
+    """struct barq_kv_cold"""
+
+    _fields_ = [
+        ("key_codes", c_ptr),
+        ("value_codes", c_ptr),
+        ("key_scales", c_ptr),
+        ("value_scales", c_ptr),
+        ("free_cold", c_ptr),
+        ("num_cold", c_i64),
+        ("window", c_i64),
+        ("element_type", c_i64),
+    ]
+
+
+_POOL = ctypes.POINTER(BarqKVPool)
+_COLD = ctypes.POINTER(BarqKVCold)
+
 _SIGNATURES = {
     "barq_kv_version": (ctypes.c_char_p, []),
     "barq_kv_status_string": (ctypes.c_char_p, [ctypes.c_int]),
@@ -61,6 +79,12 @@ _SIGNATURES = {
     "barq_kv_attention_workspace_bytes": (c_i64, [ctypes.POINTER(BarqKVPool)] + [c_i64] * 5),
     "barq_kv_decode_attention": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_ptr] + [c_i64] * 6 + [c_ptr]
                                  + [c_i64] * 3 + [ctypes.c_float] + [c_i64] * 3 + [c_ptr, c_i64, c_ptr]),
+    "barq_kv_cold_reset": (ctypes.c_int, [_POOL, _COLD, c_ptr]),
+    "barq_kv_compress": (ctypes.c_int, [_POOL, _COLD, c_i64, c_ptr]),
+    "barq_kv_gather_cold": (ctypes.c_int, [_POOL, _COLD, c_ptr, c_ptr] + [c_i64] * 6 + [c_ptr]),
+    "barq_kv_update_cold": (ctypes.c_int, [_POOL, _COLD, c_ptr, c_ptr] + [c_i64] * 5 + [c_ptr, c_ptr]
+                            + [c_i64] * 5 + [c_ptr]),
+    "barq_kv_free_rows_cold": (ctypes.c_int, [_POOL, _COLD, c_ptr, c_i64, c_ptr]),
 }
 
 _LIB: Optional[ctypes.CDLL] = None

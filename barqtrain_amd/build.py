@@ -25,7 +25,7 @@ INCLUDE = REPO_ROOT / "include"
 LIB_NAME = "libbarq_kv.so"
 EXT_NAME = "barqtrain_cuda"
 OFFLOAD_ARCH = "gfx950"
-HIP_SOURCES = ("barq_kv.hip", "barq_kv_attention.hip")
+HIP_SOURCES = ("barq_kv.hip", "barq_kv_attention.hip", "barq_kv_quant.hip")
 
 # Packed fp32 instructions stay off in every HIP compile (none are needed: the kernels only
 # move bits, but the flag keeps the compiler from forming them).

@@ -1,0 +1,606 @@
+// fp8 cold store of a page pool for MI355X (gfx950), behind the C ABI of include/barq_kv.h:
+// blocks behind a row's residual window are quantised (barq_kv_compress) to OCP FP8 E4M3 codes
+// with power-of-two (E8M0) scales -- keys per channel over the page's tokens, values per token
+// over head_dim, KIVI's grouping -- and dequantised on the way out (barq_kv_gather_cold).
+//
+// Power-of-two scales make scaling exact, so a code depends only on its element and its group's
+// largest finite magnitude, and a dequantised value is exactly code * 2^e before the final
+// rounding to the pool's element type: the same numbers on every run and every device.
+//
+// The reference plans this path (IMPLEMENTATION_PLAN.md:106-129: quantized KV storage, a
+// full-precision residual window, dequant-on-read) and has no implementation.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <climits>
+
+#include "barq_kv.h"
+#include "fastdiv.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWave = 64;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kMaxTokenHeads = 4096;  // page_size * kv_heads: a compress workgroup's value maxima
+constexpr int kMaxChannels = 16384;   // kv_heads * head_dim: a compress workgroup's key exponents
+constexpr int kUnroll = 4;            // vectors in flight per gather thread
+constexpr int64_t kI32Max = 0x7fffffffLL;
+
+__device__ __forceinline__ int checked_id(int id, int64_t n) { return (id >= 0 && (int64_t)id < n) ? id : -1; }
+
+__device__ __forceinline__ int ceil_div_fd(int n, const FastDiv& d) {
+  return n <= 0 ? 0 : (int)d.div((uint32_t)(n + (int)d.d - 1));
+}
+
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int up = __shfl_up(v, o, kWave);
+    if (lane >= o) v += up;
+  }
+  return v;
+}
+
+// Exclusive prefix sum over the workgroup; *total gets the sum.  Every thread must call it.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* lds, int* total) {
+  const int wave = threadIdx.x / kWave;
+  const int incl = wave_incl_scan(v);
+  if ((threadIdx.x & (kWave - 1)) == kWave - 1) lds[wave] = incl;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int t = lds[w];
+    if (w < wave) before += t;
+    all += t;
+  }
+  __syncthreads();
+  *total = all;
+  return before + incl - v;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Element types and the E4M3 / E8M0 arithmetic.
+// ---------------------------------------------------------------------------------------------
+
+template <int KIND>
+struct Elem;
+template <>
+struct Elem<BARQ_KV_BF16> {
+  using Bits = uint16_t;
+  __device__ static float to_float(Bits b) { return __uint_as_float((uint32_t)b << 16); }
+  __device__ static Bits from_float(float f) {  // round to nearest even, NaN kept quiet
+    const uint32_t u = __float_as_uint(f);
+    if (f != f) return (Bits)((u >> 16) | 0x40);
+    return (Bits)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+  }
+};
+template <>
+struct Elem<BARQ_KV_FP16> {
+  using Bits = uint16_t;
+  __device__ static float to_float(Bits b) { return (float)__builtin_bit_cast(_Float16, b); }
+  __device__ static Bits from_float(float f) { return __builtin_bit_cast(Bits, (_Float16)f); }
+};
+template <>
+struct Elem<BARQ_KV_FP32> {
+  using Bits = uint32_t;
+  __device__ static float to_float(Bits b) { return __uint_as_float(b); }
+  __device__ static Bits from_float(float f) { return __float_as_uint(f); }
+};
+
+// E4M3 code of a float, rounded to nearest even; finite values beyond 448 saturate, NaN and
+// infinities give the NaN code.
+__device__ __forceinline__ uint32_t e4m3_encode(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const float a = fabsf(x);
+  if (!(a <= 3.402823466e38f)) return sign | 0x7Fu;
+  if (a < 0.015625f) return sign | (uint32_t)rintf(a * 512.0f);  // subnormal codes 0..8
+  const uint32_t au = u & 0x7FFFFFFFu;
+  int e = (int)(au >> 23) - 127;
+  uint32_t m = (au >> 20) & 7u;
+  const uint32_t rem = au & 0xFFFFFu;
+  if (rem > 0x80000u || (rem == 0x80000u && (m & 1u))) {
+    if (++m == 8u) {
+      m = 0;
+      ++e;
+    }
+  }
+  const int code = min(((e + 7) << 3) | (int)m, 0x7E);
+  return sign | (uint32_t)code;
+}
+
+// The exact value of an E4M3 code.
+__device__ __forceinline__ float e4m3_decode(uint32_t c) {
+  const uint32_t c7 = c & 0x7Fu;
+  const uint32_t sign = (c & 0x80u) << 24;
+  if (c7 == 0x7Fu) return __uint_as_float(sign | 0x7FC00000u);
+  const float mag = c7 >= 8u ? __uint_as_float((((c7 >> 3) + 120u) << 23) | ((c7 & 7u) << 20))
+                             : (float)c7 * 0.001953125f;
+  return __uint_as_float(__float_as_uint(mag) | sign);
+}
+
+// Smallest e with a <= 448 * 2^e (0 for a == 0), clamped to [-127, 127]: with a = m * 2^x,
+// m in [0.5, 1), e = x - 9, plus 1 when m > 0.875 (448 = 0.875 * 2^9).
+__device__ __forceinline__ int group_exponent(float a) {
+  if (a == 0.0f) return 0;
+  int x;
+  const float m = frexpf(a, &x);
+  return max(-127, min(127, x - 9 + (m > 0.875f ? 1 : 0)));
+}
+
+__device__ __forceinline__ float finite_abs(float v) {
+  const float a = fabsf(v);
+  return a <= 3.402823466e38f ? a : 0.0f;
+}
+
+struct ColdPtrs {
+  uint8_t* codes[2];   // key, value
+  uint8_t* key_scales;
+  uint8_t* value_scales;
+  int32_t* free_cold;
+  int64_t num_cold;
+  int32_t window;
+};
+
+// ---------------------------------------------------------------------------------------------
+// Compress: workgroup per row.
+// ---------------------------------------------------------------------------------------------
+
+struct CompressArgs {
+  barq_kv_pool p;
+  ColdPtrs c;
+  int32_t batch;
+  FastDiv div_page;
+  FastDiv div_dim;
+};
+
+template <int KIND>
+__global__ void __launch_bounds__(kThreads) compress_kernel(const CompressArgs a) {
+  using E = Elem<KIND>;
+  using Bits = typename E::Bits;
+  __shared__ int lds_scan[kWaves];
+  __shared__ int s_blocks[kThreads];
+  __shared__ int s_cold;
+  __shared__ uint32_t s_vmax[kMaxTokenHeads];
+  __shared__ int8_t s_kexp[kMaxChannels];
+  const barq_kv_pool& p = a.p;
+  const int r = blockIdx.x;
+  const int P = (int)p.page_size, H = (int)p.kv_heads, C = (int)(p.kv_heads * p.head_dim);
+  const int mb = (int)p.max_blocks;
+  const int len = p.seq_lens[r];
+  const int old_len = len - a.c.window;
+  const int jmax = min(old_len > 0 ? (int)a.div_page.div((uint32_t)old_len) : 0,
+                       min(ceil_div_fd(p.high_water[r], a.div_page), mb));
+  int32_t* row = p.block_table + (int64_t)r * mb;
+  const Bits* pages[2] = {(const Bits*)p.key_pages, (const Bits*)p.value_pages};
+  int err = 0;
+  for (int j0 = 0; j0 < jmax; j0 += kThreads) {
+    const int j = j0 + (int)threadIdx.x;
+    int hot = 0;
+    if (j < jmax) {
+      const int page = checked_id(row[j], p.num_pages);
+      hot = page >= 0 && (!p.page_shares || p.page_shares[page] == 0);
+    }
+    int count = 0;
+    const int k = block_exclusive_scan(hot, lds_scan, &count);
+    if (hot) s_blocks[k] = j;
+    __syncthreads();
+    for (int q = 0; q < count; ++q) {
+      const int jb = s_blocks[q];
+      if (threadIdx.x == 0) {
+        int cp = -1;
+        const int before = atomicSub(&p.ctrl[BARQ_KV_CTRL_COLD_TOP], 1);
+        if (before <= 0 || (int64_t)before > a.c.num_cold) {
+          atomicAdd(&p.ctrl[BARQ_KV_CTRL_COLD_TOP], 1);
+          err |= before <= 0 ? BARQ_KV_ERRBIT_POOL_EXHAUSTED : BARQ_KV_ERRBIT_BAD_INDEX;
+        } else {
+          cp = checked_id(a.c.free_cold[before - 1], a.c.num_cold);
+          if (cp < 0) err |= BARQ_KV_ERRBIT_BAD_INDEX;
+        }
+        s_cold = cp;
+      }
+      for (int i = threadIdx.x; i < P * H; i += kThreads) s_vmax[i] = 0;
+      __syncthreads();
+      const int cp = s_cold;
+      const int hp = row[jb];
+      if (cp >= 0) {  // uniform
+        const int64_t src = (int64_t)hp * P * C;
+        const int64_t dst = (int64_t)cp * P * C;
+        // pass 1: key maxima per channel (in registers, then LDS), value maxima per (token, head)
+        for (int ch = threadIdx.x; ch < C; ch += kThreads) {
+          const int h = (int)a.div_dim.div((uint32_t)ch);
+          float kmax = 0.0f;
+          for (int t = 0; t < P; ++t) {
+            kmax = fmaxf(kmax, finite_abs(E::to_float(pages[0][src + (int64_t)t * C + ch])));
+            const float v = finite_abs(E::to_float(pages[1][src + (int64_t)t * C + ch]));
+            atomicMax(&s_vmax[t * H + h], __float_as_uint(v));
+          }
+          s_kexp[ch] = (int8_t)group_exponent(kmax);
+        }
+        __syncthreads();
+        // pass 2: codes and scales
+        for (int ch = threadIdx.x; ch < C; ch += kThreads) {
+          const int h = (int)a.div_dim.div((uint32_t)ch);
+          const bool first_dim = ch == h * (int)a.div_dim.d;
+          const int ke = s_kexp[ch];
+          a.c.key_scales[(int64_t)cp * C + ch] = (uint8_t)(ke + 127);
+          for (int t = 0; t < P; ++t) {
+            const int64_t at = (int64_t)t * C + ch;
+            a.c.codes[0][dst + at] = (uint8_t)e4m3_encode(ldexpf(E::to_float(pages[0][src + at]), -ke));
+            const int ve = group_exponent(__uint_as_float(s_vmax[t * H + h]));
+            a.c.codes[1][dst + at] = (uint8_t)e4m3_encode(ldexpf(E::to_float(pages[1][src + at]), -ve));
+            if (first_dim) a.c.value_scales[((int64_t)cp * P + t) * H + h] = (uint8_t)(ve + 127);
+          }
+        }
+        __syncthreads();  // every thread has read the hot page before it is released
+        if (threadIdx.x == 0) {
+          row[jb] = BARQ_KV_COLD_ENTRY(cp);
+          const int slot = atomicAdd(&p.ctrl[BARQ_KV_CTRL_FREE_TOP], 1);
+          if (slot < p.num_pages) p.free_pages[slot] = hp;
+          else err |= BARQ_KV_ERRBIT_BAD_INDEX;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Gather with dequantisation: tile = (row, block, K or V); a tile's block is hot, cold or
+// unmapped for all its positions, so the branch is uniform.  Vectors of VE elements along
+// head_dim; output [B, H, S, D] with element strides.
+// ---------------------------------------------------------------------------------------------
+
+struct GatherArgs {
+  barq_kv_pool p;
+  ColdPtrs c;
+  char* out[2];
+  int64_t osb, osh, oss;  // elements
+  int32_t batch;
+  int32_t seq_out;
+  int32_t nblk;           // output blocks per row
+  int32_t from_device;
+  FastDiv div_head;       // page_size * head_dim / VE vectors per head
+  FastDiv div_dv;         // head_dim / VE
+  FastDiv div_nblk;
+};
+
+template <int BYTES>
+struct Raw;
+template <>
+struct Raw<16> { using T = uint32_t __attribute__((ext_vector_type(4))); };
+template <>
+struct Raw<8> { using T = uint32_t __attribute__((ext_vector_type(2))); };
+template <>
+struct Raw<4> { using T = uint32_t; };
+template <>
+struct Raw<2> { using T = uint16_t; };
+template <>
+struct Raw<1> { using T = uint8_t; };
+
+template <int KIND, int VE>
+struct Vec {
+  using E = Elem<KIND>;
+  using Bits = typename E::Bits;
+  static constexpr int kBytes = VE * (int)sizeof(Bits);
+  using Out = typename Raw<kBytes>::T;
+  using Codes = typename Raw<VE>::T;
+  union OutU {
+    Out v;
+    Bits e[VE];
+  };
+  union CodeU {
+    Codes v;
+    uint8_t b[VE];
+  };
+};
+
+template <int KIND, int VE>
+__global__ void __launch_bounds__(kThreads) gather_cold_kernel(const GatherArgs a) {
+  using V = Vec<KIND, VE>;
+  using E = Elem<KIND>;
+  using Bits = typename E::Bits;
+  __shared__ int s_seq;
+  const barq_kv_pool& p = a.p;
+  const int kv = blockIdx.x & 1;
+  const int bj = blockIdx.x >> 1;
+  const int b = (int)a.div_nblk.div((uint32_t)bj);
+  const int j = bj - b * a.nblk;
+  const int P = (int)p.page_size, H = (int)p.kv_heads, D = (int)p.head_dim;
+  if (a.from_device) {
+    if (threadIdx.x < kWave) {
+      int m = 0;
+      for (int i = threadIdx.x; i < a.batch; i += kWave) m = max(m, p.seq_lens[i]);
+#pragma unroll
+      for (int o = kWave / 2; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, kWave));
+      if (threadIdx.x == 0) s_seq = min(m, a.seq_out);
+    }
+    __syncthreads();
+  }
+  const int S = a.from_device ? s_seq : a.seq_out;
+  const int pos0 = j * P;
+  if (pos0 >= S) return;  // uniform
+  const int hw = p.high_water[b];
+  const int entry = pos0 < hw ? p.block_table[(int64_t)b * p.max_blocks + j] : -1;
+  const int hot = checked_id(entry, p.num_pages);
+  const int cold = entry <= -2 ? checked_id(-2 - entry, a.c.num_cold) : -1;
+  if (entry <= -2 && cold < 0 && threadIdx.x == 0) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], BARQ_KV_ERRBIT_BAD_INDEX);
+  const int dv_n = (int)a.div_dv.d;
+  const int nvec = H * P * dv_n;
+  Bits* out = (Bits*)a.out[kv] + (int64_t)b * a.osb;
+  const int live = min(S, hw) - pos0;  // positions of this block with data
+  const int end = min(S - pos0, P);    // positions of this block in the output
+  for (int v0 = threadIdx.x; v0 < nvec; v0 += kThreads * kUnroll) {
+    typename V::OutU val[kUnroll];
+    int64_t at[kUnroll];
+    bool in[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int v = v0 + u * kThreads;
+      const int h = (int)a.div_head.div((uint32_t)v);
+      const int rem = v - h * (int)a.div_head.d;
+      const int t = (int)a.div_dv.div((uint32_t)rem);
+      const int dv = rem - t * dv_n;
+      in[u] = v < nvec && t < end;
+      at[u] = (int64_t)h * a.osh + (int64_t)(pos0 + t) * a.oss + (int64_t)dv * VE;
+      val[u].v = typename V::Out(0);
+      if (!in[u] || t >= live) continue;
+      const int64_t el = (((int64_t)(hot >= 0 ? hot : cold) * P + t) * H + h) * D + (int64_t)dv * VE;
+      if (hot >= 0) {
+        const char* base = kv ? (const char*)p.value_pages : (const char*)p.key_pages;
+        val[u].v = __builtin_nontemporal_load((const typename V::Out*)(base + el * (int64_t)sizeof(Bits)));
+      } else if (cold >= 0) {
+        typename V::CodeU codes;
+        codes.v = __builtin_nontemporal_load((const typename V::Codes*)(a.c.codes[kv] + el));
+        if (kv == 0) {
+          typename V::CodeU sc;
+          sc.v = *(const typename V::Codes*)(a.c.key_scales + ((int64_t)cold * H + h) * D + (int64_t)dv * VE);
+#pragma unroll
+          for (int e = 0; e < VE; ++e)
+            val[u].e[e] = E::from_float(ldexpf(e4m3_decode(codes.b[e]), (int)sc.b[e] - 127));
+        } else {
+          const int ve = (int)a.c.value_scales[((int64_t)cold * P + t) * H + h] - 127;
+#pragma unroll
+          for (int e = 0; e < VE; ++e) val[u].e[e] = E::from_float(ldexpf(e4m3_decode(codes.b[e]), ve));
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (in[u]) __builtin_nontemporal_store(val[u].v, (typename V::Out*)(out + at[u]));
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Row release with a cold store: one workgroup, a row at a time; hot pages (shares-aware) go back
+// to free_pages, cold pages to free_cold, each in (row, block) order.
+// ---------------------------------------------------------------------------------------------
+
+struct FreeArgs {
+  barq_kv_pool p;
+  ColdPtrs c;
+  const int32_t* rows;
+  int32_t n;
+  FastDiv div_page;
+};
+
+__global__ void __launch_bounds__(kThreads) free_rows_cold_kernel(const FreeArgs a) {
+  __shared__ int lds_scan[kWaves];
+  const barq_kv_pool& p = a.p;
+  const int hot_top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
+  const int cold_top = p.ctrl[BARQ_KV_CTRL_COLD_TOP];
+  const int mb = (int)p.max_blocks;
+  int hot_pushed = 0, cold_pushed = 0, err = 0;
+  for (int i = 0; i < a.n; ++i) {
+    const int r = a.rows[i];
+    if (r < 0 || r >= (int)p.max_batch) {
+      err |= BARQ_KV_ERRBIT_BAD_INDEX;
+      continue;
+    }
+    const int cnt = min(ceil_div_fd(p.high_water[r], a.div_page), mb);
+    int32_t* row = p.block_table + (int64_t)r * mb;
+    for (int j0 = 0; j0 < cnt; j0 += kThreads) {
+      const int j = j0 + (int)threadIdx.x;
+      int hot = -1, cold = -1;
+      if (j < cnt) {
+        const int e = row[j];
+        hot = checked_id(e, p.num_pages);
+        if (e <= -2) cold = checked_id(-2 - e, a.c.num_cold);
+        if (hot >= 0 && p.page_shares && atomicSub(&p.page_shares[hot], 1) != 0) hot = -1;
+        else if (hot >= 0 && p.page_shares) p.page_shares[hot] = 0;
+        row[j] = -1;
+      }
+      int hot_n = 0, cold_n = 0;
+      const int hk = block_exclusive_scan(hot >= 0, lds_scan, &hot_n);
+      const int ck = block_exclusive_scan(cold >= 0, lds_scan, &cold_n);
+      if (hot >= 0) {
+        const int64_t slot = (int64_t)hot_top + hot_pushed + hk;
+        if (slot < p.num_pages) p.free_pages[slot] = hot;
+        else err |= BARQ_KV_ERRBIT_BAD_INDEX;
+      }
+      if (cold >= 0) {
+        const int64_t slot = (int64_t)cold_top + cold_pushed + ck;
+        if (slot < a.c.num_cold) a.c.free_cold[slot] = cold;
+        else err |= BARQ_KV_ERRBIT_BAD_INDEX;
+      }
+      hot_pushed += hot_n;
+      cold_pushed += cold_n;
+    }
+    __syncthreads();  // every thread has read the row's mark before it is cleared
+    if (threadIdx.x == 0) {
+      p.seq_lens[r] = 0;
+      p.high_water[r] = 0;
+    }
+  }
+  if (threadIdx.x == 0) {
+    p.ctrl[BARQ_KV_CTRL_FREE_TOP] = (int)std::min<int64_t>((int64_t)hot_top + hot_pushed, p.num_pages);
+    p.ctrl[BARQ_KV_CTRL_COLD_TOP] = (int)std::min<int64_t>((int64_t)cold_top + cold_pushed, a.c.num_cold);
+  }
+  if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
+}
+
+__global__ void cold_reset_kernel(ColdPtrs c, int32_t* ctrl) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < c.num_cold) c.free_cold[i] = (int32_t)(c.num_cold - 1 - i);
+  if (i == 0) ctrl[BARQ_KV_CTRL_COLD_TOP] = (int32_t)c.num_cold;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------------------------
+
+bool pool_ok(const barq_kv_pool* p) {
+  if (!p || !p->key_pages || !p->value_pages || !p->block_table || !p->seq_lens || !p->high_water ||
+      !p->free_pages || !p->ctrl)
+    return false;
+  if (p->num_pages < 1 || p->num_pages > kI32Max || p->max_batch < 1 || p->max_batch > kI32Max ||
+      p->max_blocks < 1 || p->page_size < 1 || p->kv_heads < 1 || p->head_dim < 1)
+    return false;
+  if (p->max_batch * p->max_blocks > kI32Max || p->max_blocks * p->page_size > kI32Max) return false;
+  return p->elem_bytes == 2 || p->elem_bytes == 4;
+}
+
+bool cold_ok(const barq_kv_pool* p, const barq_kv_cold* c) {
+  if (!pool_ok(p) || !c || !c->key_codes || !c->value_codes || !c->key_scales || !c->value_scales ||
+      !c->free_cold)
+    return false;
+  if (c->num_cold < 1 || c->num_cold > kI32Max - 2 || c->window < 0 || c->window > kI32Max) return false;
+  const int64_t want = c->element_type == BARQ_KV_FP32 ? 4 : 2;
+  if (c->element_type < BARQ_KV_BF16 || c->element_type > BARQ_KV_FP32 || p->elem_bytes != want) return false;
+  return p->page_size * p->kv_heads <= kMaxTokenHeads && p->kv_heads * p->head_dim <= kMaxChannels;
+}
+
+ColdPtrs cold_ptrs(const barq_kv_cold* c) {
+  ColdPtrs r;
+  r.codes[0] = (uint8_t*)c->key_codes;
+  r.codes[1] = (uint8_t*)c->value_codes;
+  r.key_scales = (uint8_t*)c->key_scales;
+  r.value_scales = (uint8_t*)c->value_scales;
+  r.free_cold = c->free_cold;
+  r.num_cold = c->num_cold;
+  r.window = (int32_t)c->window;
+  return r;
+}
+
+int launch(const void* fn, dim3 grid, void* arg, hipStream_t stream) {
+  void* args[] = {arg};
+  return hipLaunchKernel(fn, grid, dim3(kThreads), args, 0, stream) == hipSuccess ? BARQ_KV_OK
+                                                                                 : BARQ_KV_ERR_LAUNCH;
+}
+
+template <int KIND>
+int launch_gather(int ve, dim3 grid, GatherArgs* a, hipStream_t s) {
+  if constexpr (KIND != BARQ_KV_FP32) {  // 8 two-byte elements: a 16-byte vector
+    if (ve == 8) return launch((const void*)&gather_cold_kernel<KIND, 8>, grid, a, s);
+  }
+  switch (ve) {
+    case 4: return launch((const void*)&gather_cold_kernel<KIND, 4>, grid, a, s);
+    case 2: return launch((const void*)&gather_cold_kernel<KIND, 2>, grid, a, s);
+    default: return launch((const void*)&gather_cold_kernel<KIND, 1>, grid, a, s);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int barq_kv_cold_reset(const barq_kv_pool* pool, const barq_kv_cold* cold, void* stream) {
+  if (!cold_ok(pool, cold)) return BARQ_KV_ERR_INVALID;
+  const int64_t blocks = (cold->num_cold + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(cold_reset_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, (hipStream_t)stream,
+                     cold_ptrs(cold), pool->ctrl);
+  return hipGetLastError() == hipSuccess ? BARQ_KV_OK : BARQ_KV_ERR_LAUNCH;
+}
+
+int barq_kv_compress(const barq_kv_pool* pool, const barq_kv_cold* cold, int64_t batch, void* stream) {
+  if (!cold_ok(pool, cold) || batch < 0 || batch > pool->max_batch) return BARQ_KV_ERR_INVALID;
+  if (batch == 0) return BARQ_KV_OK;
+  CompressArgs a;
+  a.p = *pool;
+  a.c = cold_ptrs(cold);
+  a.batch = (int32_t)batch;
+  a.div_page = FastDiv::make((uint32_t)pool->page_size);
+  a.div_dim = FastDiv::make((uint32_t)pool->head_dim);
+  const void* fn = cold->element_type == BARQ_KV_BF16   ? (const void*)&compress_kernel<BARQ_KV_BF16>
+                   : cold->element_type == BARQ_KV_FP16 ? (const void*)&compress_kernel<BARQ_KV_FP16>
+                                                        : (const void*)&compress_kernel<BARQ_KV_FP32>;
+  return launch(fn, dim3((uint32_t)batch), &a, (hipStream_t)stream);
+}
+
+int barq_kv_gather_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, void* key_out,
+                        void* value_out, int64_t batch, int64_t seq_out, int64_t osb, int64_t osh,
+                        int64_t oss, int64_t flags, void* stream) {
+  if (!cold_ok(pool, cold) || batch < 0 || batch > pool->max_batch) return BARQ_KV_ERR_INVALID;
+  if (flags & ~(int64_t)BARQ_KV_SEQ_FROM_DEVICE) return BARQ_KV_ERR_INVALID;
+  const int64_t cap = pool->max_blocks * pool->page_size;
+  if (seq_out < 0 || seq_out > cap) return BARQ_KV_ERR_INVALID;
+  if (batch == 0 || seq_out == 0) return BARQ_KV_OK;
+  if (!key_out || !value_out || osb < 0 || osh < 0 || oss < 0) return BARQ_KV_ERR_INVALID;
+  const int64_t eb = pool->elem_bytes, D = pool->head_dim;
+  // widest vector of VE elements every address and stride admits
+  const uint64_t bits = (uint64_t)(uintptr_t)key_out | (uint64_t)(uintptr_t)value_out | (uint64_t)(osb * eb) |
+                        (uint64_t)(osh * eb) | (uint64_t)(oss * eb) | (uint64_t)(D * eb) |
+                        (uint64_t)(uintptr_t)pool->key_pages | (uint64_t)(uintptr_t)pool->value_pages;
+  const uint64_t code_bits = (uint64_t)(uintptr_t)cold->key_codes | (uint64_t)(uintptr_t)cold->value_codes |
+                             (uint64_t)(uintptr_t)cold->key_scales | (uint64_t)D;
+  int ve = eb == 2 ? 8 : 4;
+  while (ve > 1 && ((bits & (uint64_t)(ve * eb - 1)) || (code_bits & (uint64_t)(ve - 1)))) ve >>= 1;
+  GatherArgs a;
+  a.p = *pool;
+  a.c = cold_ptrs(cold);
+  a.out[0] = (char*)key_out;
+  a.out[1] = (char*)value_out;
+  a.osb = osb;
+  a.osh = osh;
+  a.oss = oss;
+  a.batch = (int32_t)batch;
+  a.seq_out = (int32_t)seq_out;
+  a.nblk = (int32_t)((seq_out + pool->page_size - 1) / pool->page_size);
+  a.from_device = (flags & BARQ_KV_SEQ_FROM_DEVICE) ? 1 : 0;
+  a.div_head = FastDiv::make((uint32_t)(pool->page_size * (D / ve)));
+  a.div_dv = FastDiv::make((uint32_t)(D / ve));
+  a.div_nblk = FastDiv::make((uint32_t)a.nblk);
+  const int64_t tiles = batch * a.nblk * 2;
+  if (tiles > kI32Max) return BARQ_KV_ERR_INVALID;
+  hipStream_t s = (hipStream_t)stream;
+  switch (cold->element_type) {
+    case BARQ_KV_BF16: return launch_gather<BARQ_KV_BF16>(ve, dim3((uint32_t)tiles), &a, s);
+    case BARQ_KV_FP16: return launch_gather<BARQ_KV_FP16>(ve, dim3((uint32_t)tiles), &a, s);
+    default: return launch_gather<BARQ_KV_FP32>(ve, dim3((uint32_t)tiles), &a, s);
+  }
+}
+
+int barq_kv_update_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, const void* key_states,
+                        const void* value_states, int64_t batch, int64_t tokens, int64_t stride_b,
+                        int64_t stride_h, int64_t stride_t, void* key_out, void* value_out,
+                        int64_t seq_out, int64_t osb, int64_t osh, int64_t oss, int64_t flags,
+                        void* stream) {
+  if (!cold_ok(pool, cold)) return BARQ_KV_ERR_INVALID;
+  int rc = barq_kv_append(pool, key_states, value_states, batch, tokens, stride_b, stride_h, stride_t, stream);
+  if (rc == BARQ_KV_OK) rc = barq_kv_compress(pool, cold, batch, stream);
+  if (rc == BARQ_KV_OK)
+    rc = barq_kv_gather_cold(pool, cold, key_out, value_out, batch, seq_out, osb, osh, oss, flags, stream);
+  return rc;
+}
+
+int barq_kv_free_rows_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, const int32_t* rows,
+                           int64_t num_rows, void* stream) {
+  if (!cold_ok(pool, cold) || num_rows < 0 || num_rows > pool->max_batch) return BARQ_KV_ERR_INVALID;
+  if (num_rows == 0) return BARQ_KV_OK;
+  if (!rows) return BARQ_KV_ERR_INVALID;
+  FreeArgs a;
+  a.p = *pool;
+  a.c = cold_ptrs(cold);
+  a.rows = rows;
+  a.n = (int32_t)num_rows;
+  a.div_page = FastDiv::make((uint32_t)pool->page_size);
+  return launch((const void*)&free_rows_cold_kernel, dim3(1), &a, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -248,6 +248,92 @@ void pool_select_rows_(std::vector<at::Tensor> pool, at::Tensor rows, at::Tensor
                "pool_select_rows_");
 }
 
+// A pool's fp8 cold store as (key_codes, value_codes, key_scales, value_scales, free_cold), the
+// tensors of barqtrain_amd.paged.ColdStore, and its residual window in tokens.
+barq_kv_cold cold_from(const barq_kv_pool& p, const at::Tensor& pages, const std::vector<at::Tensor>& t,
+                       int64_t window) {
+  TORCH_CHECK(t.size() == 5, "a cold store is 5 tensors");
+  for (size_t i = 0; i < 5; ++i)
+    TORCH_CHECK(t[i].is_cuda() && t[i].is_contiguous() && t[i].get_device() == pages.get_device() &&
+                    t[i].scalar_type() == (i < 4 ? at::kByte : at::kInt),
+                "cold-store tensors must be contiguous (uint8 codes and scales, int32 free list) on the pool's device");
+  const int64_t n = t[0].size(0);
+  TORCH_CHECK(t[0].dim() == 4 && t[0].size(1) == p.page_size && t[0].size(2) == p.kv_heads &&
+                  t[0].size(3) == p.head_dim && t[1].sizes() == t[0].sizes(),
+              "codes must be [num_cold, page_size, kv_heads, head_dim]");
+  TORCH_CHECK(t[2].numel() == n * p.kv_heads * p.head_dim && t[3].numel() == n * p.page_size * p.kv_heads &&
+                  t[4].numel() == n,
+              "cold-store scale / free-list sizes do not match num_cold");
+  barq_kv_cold c;
+  c.key_codes = t[0].data_ptr();
+  c.value_codes = t[1].data_ptr();
+  c.key_scales = t[2].data_ptr();
+  c.value_scales = t[3].data_ptr();
+  c.free_cold = t[4].data_ptr<int32_t>();
+  c.num_cold = n;
+  c.window = window;
+  const auto dt = pages.scalar_type();
+  TORCH_CHECK(dt == at::kBFloat16 || dt == at::kHalf || dt == at::kFloat,
+              "quantised pages need a bfloat16, float16 or float32 cache");
+  c.element_type = dt == at::kBFloat16 ? BARQ_KV_BF16 : dt == at::kHalf ? BARQ_KV_FP16 : BARQ_KV_FP32;
+  return c;
+}
+
+void pool_cold_reset_(std::vector<at::Tensor> pool, std::vector<at::Tensor> cold, int64_t window) {
+  barq_kv_pool p = pool_from(pool);
+  barq_kv_cold c = cold_from(p, pool[0], cold, window);
+  c10::DeviceGuard guard(pool[0].device());
+  check_status(barq_kv_cold_reset(&p, &c, current_stream(pool[0])), "pool_cold_reset_");
+}
+
+void pool_compress_(std::vector<at::Tensor> pool, std::vector<at::Tensor> cold, int64_t window, int64_t batch) {
+  barq_kv_pool p = pool_from(pool);
+  barq_kv_cold c = cold_from(p, pool[0], cold, window);
+  c10::DeviceGuard guard(pool[0].device());
+  check_status(barq_kv_compress(&p, &c, batch, current_stream(pool[0])), "pool_compress_");
+}
+
+void pool_gather_cold(std::vector<at::Tensor> pool, std::vector<at::Tensor> cold, int64_t window,
+                      at::Tensor key_out, at::Tensor value_out, int64_t batch, int64_t seq_out, int64_t flags) {
+  barq_kv_pool p = pool_from(pool);
+  barq_kv_cold c = cold_from(p, pool[0], cold, window);
+  check_out(p, pool[0], key_out, value_out, batch, seq_out);
+  c10::DeviceGuard guard(pool[0].device());
+  check_status(barq_kv_gather_cold(&p, &c, key_out.data_ptr(), value_out.data_ptr(), batch, seq_out,
+                                   key_out.stride(0), key_out.stride(1), key_out.stride(2), flags,
+                                   current_stream(pool[0])),
+               "pool_gather_cold");
+}
+
+void pool_update_cold_(std::vector<at::Tensor> pool, std::vector<at::Tensor> cold, int64_t window,
+                       at::Tensor key_states, at::Tensor value_states, at::Tensor key_out, at::Tensor value_out,
+                       int64_t seq_out, int64_t flags) {
+  barq_kv_pool p = pool_from(pool);
+  barq_kv_cold c = cold_from(p, pool[0], cold, window);
+  check_states(p, pool[0], key_states, value_states);
+  const int64_t batch = key_states.size(0);
+  check_out(p, pool[0], key_out, value_out, batch, seq_out);
+  c10::DeviceGuard guard(pool[0].device());
+  check_status(barq_kv_update_cold(&p, &c, key_states.data_ptr(), value_states.data_ptr(), batch,
+                                   key_states.size(2), key_states.stride(0), key_states.stride(1),
+                                   key_states.stride(2), key_out.data_ptr(), value_out.data_ptr(), seq_out,
+                                   key_out.stride(0), key_out.stride(1), key_out.stride(2), flags,
+                                   current_stream(pool[0])),
+               "pool_update_cold_");
+}
+
+void pool_free_rows_cold_(std::vector<at::Tensor> pool, std::vector<at::Tensor> cold, int64_t window,
+                          at::Tensor rows) {
+  barq_kv_pool p = pool_from(pool);
+  barq_kv_cold c = cold_from(p, pool[0], cold, window);
+  TORCH_CHECK(rows.is_cuda() && rows.scalar_type() == at::kInt && rows.is_contiguous() &&
+                  rows.get_device() == pool[0].get_device(),
+              "rows must be contiguous int32 on the pool's device");
+  c10::DeviceGuard guard(pool[0].device());
+  check_status(barq_kv_free_rows_cold(&p, &c, rows.data_ptr<int32_t>(), rows.numel(), current_stream(pool[0])),
+               "pool_free_rows_cold_");
+}
+
 // The pools of a model's layers packed as an array of barq_kv_pool (a CPU uint8 tensor), for
 // the batched entry points.  The array holds raw device pointers: the caller keeps the pools'
 // tensors alive and unmoved while it uses it.
@@ -345,6 +431,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("pool_free_rows_", &pool_free_rows_, "Return rows' pages to the free stack");
   m.def("pool_copy_rows_", &pool_copy_rows_, "Build rows of a fresh pool as copies of source rows");
   m.def("pool_select_rows_", &pool_select_rows_, "Rows become selected rows, sharing their full pages");
+  m.def("pool_cold_reset_", &pool_cold_reset_, "Every page of a pool's fp8 cold store free");
+  m.def("pool_compress_", &pool_compress_, "Quantise blocks behind the residual window into the cold store");
+  m.def("pool_gather_cold", &pool_gather_cold, "Materialise rows of a pool with a cold store, dequantising");
+  m.def("pool_update_cold_", &pool_update_cold_, "Append, compress, materialise (pool with a cold store)");
+  m.def("pool_free_rows_cold_", &pool_free_rows_cold_, "Return rows' hot and cold pages");
   m.def("pool_group", &pool_group, "Pack the pools of a model's layers for the batched entry points");
   m.def("select_workspace_words", &select_workspace_words, "Workspace words of pool_group_select_rows_");
   m.def("pool_group_select_rows_", &pool_group_select_rows_,

@@ -52,6 +52,9 @@ class CapturedDecodeStep:
         self.key_out = [torch.empty(shape_out, dtype=p.dtype, device=p.device) for p in self.pools]
         self.value_out = [torch.empty(shape_out, dtype=p.dtype, device=p.device) for p in self.pools]
         self.flags = SEQ_FROM_DEVICE | (SEPARATE_FINALIZE if separate_commit else 0)
+        self.quantized = [bool(getattr(p, "quantized", False)) for p in self.pools]
+        if separate_commit and any(self.quantized):
+            raise ValueError("pools with quantised pages commit inside their append launch")
         geometry = {(p.page_size, p.max_blocks, p.max_batch) for p in self.pools}
         if len(geometry) != 1:
             raise ValueError("pools of one captured step must share page size, blocks and rows")
@@ -80,8 +83,13 @@ class CapturedDecodeStep:
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
                 for i, pool in enumerate(self.pools):
-                    backend.pool_update_(pool.tensors, self.key_in[i], self.value_in[i],
-                                         self.key_out[i], self.value_out[i], extent, self.flags)
+                    if self.quantized[i]:  # append, quantise what left the window, dequantising gather
+                        backend.pool_update_cold_(pool.tensors, pool.cold_tensors, pool.window, self.key_in[i],
+                                                  self.value_in[i], self.key_out[i], self.value_out[i], extent,
+                                                  self.flags)
+                    else:
+                        backend.pool_update_(pool.tensors, self.key_in[i], self.value_in[i],
+                                             self.key_out[i], self.value_out[i], extent, self.flags)
             self.graphs[extent] = graph
         return graph
 
@@ -101,10 +109,13 @@ class CapturedDecodeStep:
         need = np.maximum(np.minimum(-(-ends // P), p0.max_blocks) - (-(-hw // P)), 0).sum(axis=1)
         for p, n in zip(self.pools, need):
             p.ensure_free(int(n), "append")
+        cold = [p._cold_after(B, T) if q else None for p, q in zip(self.pools, self.quantized)]
         self._graph(min(self.capacity, -(-worst // self.bucket) * self.bucket)).replay()
         lens += T
         np.maximum(hw, lens, out=hw)
-        for p, n in zip(self.pools, need):
+        for p, n, c in zip(self.pools, need, cold):
             p.free_count -= int(n)
+            if c is not None:
+                p._quantised(B, *c)
         seqs = ends.max(axis=1).tolist()
         return [(k[:, :, :n], v[:, :, :n]) for k, v, n in zip(self.key_out, self.value_out, seqs)]

@@ -32,6 +32,7 @@ import torch
 CTRL_WORDS = 1088  # BARQ_KV_CTRL_WORDS of include/barq_kv.h: 64 + 16 arrival sub-counters x 64
 CTRL_FREE_TOP = 0
 CTRL_ERRORS = 1
+CTRL_COLD_TOP = 2  # BARQ_KV_CTRL_COLD_TOP: free entries of a cold store's free_cold
 ERRBIT_POOL_EXHAUSTED = 1
 ERRBIT_CAPACITY = 2
 ERRBIT_BAD_INDEX = 4
@@ -448,6 +449,188 @@ class PagePool:
         return self
 
 
+KV_QUANT_FP8 = "fp8_e4m3"
+_ELEMENT_TYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+class QuantPagePool(PagePool):
+    """A page pool whose blocks behind each row's residual window are kept as fp8 codes.
+
+    Format (``barq_kv_cold`` in include/barq_kv.h): OCP FP8 E4M3 codes, rounded to nearest even,
+    with power-of-two scales stored as E8M0 bytes -- keys one per channel (head, dim) over a
+    page's tokens, values one per token (token, head) over head_dim, KIVI's grouping
+    (arXiv:2402.02750) -- each the smallest 2^e with max |x| <= 448 * 2^e.  Reads dequantise to
+    the cache dtype.  The reference plans this cache (IMPLEMENTATION_PLAN.md:106-129: quantised
+    storage, a full-precision residual window, dequant-on-read) and ships none.
+
+    Full-precision ("hot") pages hold each row's last ``window`` tokens and its partial block: an
+    append writes there, the blocks that left the window are quantised (``barq_kv_compress``)
+    and reads dequantise (``barq_kv_gather_cold``).  Appends longer than ``chunk`` tokens
+    (prefill) run in chunks, so the hot pool needs ``max_batch * (ceil((window + chunk) / P) +
+    2)`` pages (the default); the cold store holds every block of every row by default.  A crop
+    must stay at or above the quantised blocks; beam selection is not available on this pool.
+    """
+
+    quantized = True
+
+    def __init__(self, *, max_batch: int, max_blocks: int, page_size: int, kv_heads: int, head_dim: int,
+                 dtype: torch.dtype, device: torch.device | str, window: int = 128, chunk: int = 256,
+                 num_pages: Optional[int] = None, num_cold: Optional[int] = None,
+                 page_order: Optional[torch.Tensor] = None):
+        if dtype not in _ELEMENT_TYPES:
+            raise ValueError("quantised KV pages need a bfloat16, float16 or float32 cache")
+        if int(window) < 0 or int(chunk) < 1:
+            raise ValueError("window must be >= 0 and chunk >= 1 tokens")
+        self.window = int(window)
+        self.chunk = int(chunk)
+        P = int(page_size)
+        if num_pages is None:
+            num_pages = min(int(max_batch) * (-(-(self.window + self.chunk) // P) + 2),
+                            int(max_batch) * (int(max_blocks) + 1))
+        self.num_cold = int(num_cold) if num_cold is not None else int(max_batch) * int(max_blocks)
+        if not 1 <= self.num_cold < 2**31 - 2:
+            raise ValueError("num_cold out of range")
+        if P * int(kv_heads) > 4096 or int(kv_heads) * int(head_dim) > 16384:
+            raise ValueError("quantised pages need page_size * kv_heads <= 4096 and kv_heads * head_dim <= 16384")
+        dev = torch.device(device)
+        u8 = dict(dtype=torch.uint8, device=dev)
+        self.key_codes = torch.empty((self.num_cold, P, int(kv_heads), int(head_dim)), **u8)
+        self.value_codes = torch.empty_like(self.key_codes)
+        self.key_scales = torch.empty((self.num_cold, int(kv_heads), int(head_dim)), **u8)
+        self.value_scales = torch.empty((self.num_cold, P, int(kv_heads)), **u8)
+        self.free_cold = torch.empty((self.num_cold,), dtype=torch.int32, device=dev)
+        self.cold_blocks = np.zeros(int(max_batch), dtype=np.int64)  # leading quantised blocks per row
+        self.cold_free = self.num_cold
+        super().__init__(max_batch=max_batch, max_blocks=max_blocks, page_size=page_size, kv_heads=kv_heads,
+                         head_dim=head_dim, dtype=dtype, device=device, num_pages=num_pages,
+                         page_order=page_order)
+
+    @property
+    def cold_tensors(self) -> list[torch.Tensor]:
+        return [self.key_codes, self.value_codes, self.key_scales, self.value_scales, self.free_cold]
+
+    def reset(self, page_order: Optional[torch.Tensor] = None) -> None:
+        super().reset(page_order)
+        self._ops().pool_cold_reset_(self.tensors, self.cold_tensors, self.window)
+        self.cold_blocks[:] = 0
+        self.cold_free = self.num_cold
+
+    def _cold_after(self, batch: int, tokens: int) -> tuple[np.ndarray, int]:
+        """(frontier after appending `tokens` to rows [0, batch), blocks it newly quantises)."""
+        frontier = np.maximum(self.lens[:batch] + tokens - self.window, 0) // self.page_size
+        moved = int(np.maximum(frontier - self.cold_blocks[:batch], 0).sum())
+        if moved > self.cold_free:
+            raise PagedKVPoolExhausted(
+                f"paged KV cold store exhausted: quantising needs {moved} pages, {self.cold_free} free")
+        return frontier, moved
+
+    def _quantised(self, batch: int, frontier: np.ndarray, moved: int) -> None:
+        np.maximum(self.cold_blocks[:batch], frontier, out=self.cold_blocks[:batch])
+        self.cold_free -= moved
+        self.free_count += moved  # each quantised block returned its full-precision page
+
+    def append(self, key_states: torch.Tensor, value_states: torch.Tensor,
+               max_length: Optional[int] = None) -> None:
+        self._check_states(key_states, value_states)
+        batch, _, tokens, _ = key_states.shape
+        if tokens > self.chunk:
+            for s0 in range(0, tokens, self.chunk):
+                self.append(key_states[:, :, s0:s0 + self.chunk], value_states[:, :, s0:s0 + self.chunk],
+                            max_length)
+            return
+        need = self.check_append(batch, tokens, max_length)
+        if batch == 0 or tokens == 0:
+            return
+        frontier, moved = self._cold_after(batch, tokens)
+        k, v = self._compatible_pair(key_states, value_states)
+        ops = self._ops()
+        ops.pool_append_(self.tensors, k, v)
+        ops.pool_compress_(self.tensors, self.cold_tensors, self.window, batch)
+        self._advance(batch, tokens, need)
+        self._quantised(batch, frontier, moved)
+
+    def gather(self, batch: int, seq_out: Optional[int] = None,
+               out: Optional[tuple[torch.Tensor, torch.Tensor]] = None,
+               flags: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+        seq = self.max_len(batch) if seq_out is None else int(seq_out)
+        if seq > self.capacity:
+            raise ValueError("seq_out exceeds the cache capacity")
+        ko, vo = out if out is not None else self._new_out(batch, seq)
+        if batch > 0 and seq > 0:
+            self._ops().pool_gather_cold(self.tensors, self.cold_tensors, self.window, ko, vo, batch, seq, flags)
+        return ko, vo
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor,
+               max_length: Optional[int] = None, out=None, seq_out: Optional[int] = None,
+               flags: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+        self._check_states(key_states, value_states)
+        batch, _, tokens, _ = key_states.shape
+        if tokens > self.chunk:
+            self.append(key_states, value_states, max_length)
+            return self.gather(batch, seq_out, out, flags)
+        need = self.check_append(batch, tokens, max_length)
+        if tokens == 0 or batch == 0:
+            return self.gather(batch, seq_out, out, flags)
+        frontier, moved = self._cold_after(batch, tokens)
+        seq = int((self.lens[:batch] + tokens).max()) if seq_out is None else int(seq_out)
+        ko, vo = out if out is not None else self._new_out(batch, seq)
+        k, v = self._compatible_pair(key_states, value_states)
+        self._ops().pool_update_cold_(self.tensors, self.cold_tensors, self.window, k, v, ko, vo, seq, flags)
+        self._advance(batch, tokens, need)
+        self._quantised(batch, frontier, moved)
+        return ko, vo
+
+    def crop(self, batch: int, max_length: int) -> None:
+        """As PagePool.crop; the new lengths must leave every quantised block behind them (an
+        append never writes a quantised page)."""
+        m = max(int(max_length), 0)
+        if batch > 0 and ((np.minimum(self.lens[:batch], m) // self.page_size) < self.cold_blocks[:batch]).any():
+            raise ValueError("crop would reopen a quantised block for writing: crop within the residual window "
+                             f"({self.window} tokens) or use a larger window")
+        super().crop(batch, max_length)
+
+    def free_rows(self, rows: Sequence[int]) -> None:
+        rows = [int(r) for r in rows]
+        if len(set(rows)) != len(rows):
+            raise ValueError("free_rows: rows must be distinct")
+        if any(r < 0 or r >= self.max_batch for r in rows):
+            raise IndexError("free_rows: row out of range")
+        if not rows:
+            return
+        self._ops().pool_free_rows_cold_(self.tensors, self.cold_tensors, self.window, self._index_tensor(rows))
+        r = np.asarray(rows)
+        nb = np.minimum(-(-self.hw[r] // self.page_size), self.max_blocks)
+        cold = np.minimum(self.cold_blocks[r], nb)
+        self.free_count += int((nb - cold).sum())
+        self.cold_free += int(cold.sum())
+        self.lens[r] = 0
+        self.hw[r] = 0
+        self.cold_blocks[r] = 0
+
+    def memory_bytes(self) -> dict:
+        """Bytes the pool holds on its device: hot pages, cold codes and scales, metadata."""
+        def size(ts):
+            return int(sum(t.numel() * t.element_size() for t in ts))
+
+        return {"hot_pages": size(self.tensors[:2]), "cold_store": size(self.cold_tensors[:4]),
+                "metadata": size(self.tensors[2:]) + size(self.cold_tensors[4:])}
+
+    def select_rows(self, src_rows: Sequence[int]) -> None:
+        raise NotImplementedError("beam selection is not available on a pool with quantised (fp8) pages")
+
+    def copy_rows(self, src_rows: Sequence[int], num_pages: Optional[int] = None) -> "PagePool":
+        raise NotImplementedError("beam selection is not available on a pool with quantised (fp8) pages")
+
+    def attend(self, *args, **kwargs):
+        raise NotImplementedError("decode attention reads full-precision pages; gather this pool instead")
+
+    def to(self, device) -> "QuantPagePool":
+        super().to(device)
+        for name in ("key_codes", "value_codes", "key_scales", "value_scales", "free_cold"):
+            setattr(self, name, getattr(self, name).to(self.device, non_blocking=True))
+        return self
+
+
 _GROUPS: dict = {}
 
 
@@ -476,6 +659,7 @@ def select_rows_layers(pools: Sequence[PagePool], src_rows: Sequence[int]) -> No
     g = pools[0]
     geom = (g.device, g.max_batch, g.max_blocks, g.page_size, g.kv_heads, g.head_dim, g.dtype)
     batched = (len(pools) > 1 and g.on_gpu and len({id(p) for p in pools}) == len(pools)
+               and not any(getattr(p, "quantized", False) for p in pools)
                and all((p.device, p.max_batch, p.max_blocks, p.page_size, p.kv_heads, p.head_dim, p.dtype) == geom
                        for p in pools))
     if not batched:
@@ -631,6 +815,122 @@ class _HostOps:
             s = s.masked_fill(pos > limit, float("-inf"))
             p = torch.softmax(s, dim=-1).nan_to_num(0.0)  # a row that sees nothing gives zeros
             out[b] = torch.matmul(p, v).to(out.dtype)
+
+    # -------------------------------------------------------------- fp8 cold store (host memory)
+    @staticmethod
+    def pool_cold_reset_(t, cold, window):
+        free = cold[4]
+        n = free.numel()
+        free.copy_(torch.arange(n - 1, -1, -1, dtype=torch.int32))
+        t[6][CTRL_COLD_TOP] = n
+
+    @staticmethod
+    def _quantise(x: torch.Tensor, dim: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """float32 groups along `dim` -> (E4M3 codes, exponents): 2^e the smallest power of two
+        with max |x| <= 448 * 2^e over finite elements; codes from torch's float8_e4m3fn
+        conversion (round to nearest even) of the exactly scaled values."""
+        a = x.abs()
+        a = torch.where(torch.isfinite(a), a, torch.zeros_like(a)).amax(dim)
+        m, e = torch.frexp(a)
+        e = (e - 9 + (m > 0.875).to(e.dtype)).masked_fill(a == 0, 0).clamp(-127, 127)
+        y = torch.ldexp(x, -e.unsqueeze(dim).to(torch.float32))
+        return y.to(torch.float8_e4m3fn).view(torch.uint8), e
+
+    @staticmethod
+    def _dequantise(codes: torch.Tensor, e: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+        """code * 2^e in the cache dtype; NaN codes give the quiet NaN with the code's sign (the
+        device's result, whatever payload the conversion library picks)."""
+        x = torch.ldexp(codes.view(torch.float8_e4m3fn).float(), e.float())
+        nan = (codes & 0x7F) == 0x7F
+        y = x.masked_fill(nan, 0.0).to(dtype)
+        if nan.any():
+            quiet, width, bits_t = {torch.bfloat16: (0x7FC0, 16, torch.int16), torch.float16: (0x7E00, 16, torch.int16),
+                                    torch.float32: (0x7FC00000, 32, torch.int32)}[dtype]
+            sign = (codes >> 7).to(torch.int64) << (width - 1)
+            bits = (sign | quiet).to(torch.int64)
+            bits = torch.where(bits >= 1 << (width - 1), bits - (1 << width), bits)  # as signed
+            y.view(bits_t)[nan] = bits[nan].to(bits_t)
+        return y
+
+    @staticmethod
+    def pool_compress_(t, cold, window, batch):
+        kp, vp, bt, lens, hw, free, ctrl, shares = t
+        kc, vc, ks, vs, free_cold = cold
+        P, MB = _HostOps._geometry(t)
+        for r in range(batch):
+            jmax = min(max(int(lens[r]) - window, 0) // P, min(-(-int(hw[r]) // P), MB))
+            for j in range(jmax):
+                page = int(bt[r, j])
+                if page < 0 or int(shares[page]) != 0:
+                    continue
+                top = int(ctrl[CTRL_COLD_TOP])
+                if top <= 0:
+                    ctrl[CTRL_ERRORS] |= ERRBIT_POOL_EXHAUSTED
+                    continue
+                c = int(free_cold[top - 1])
+                ctrl[CTRL_COLD_TOP] = top - 1
+                codes, e = _HostOps._quantise(kp[page].float(), 0)
+                kc[c], ks[c] = codes, (e + 127).to(torch.uint8)
+                codes, e = _HostOps._quantise(vp[page].float(), 2)
+                vc[c], vs[c] = codes, (e + 127).to(torch.uint8)
+                bt[r, j] = -2 - c
+                free[int(ctrl[CTRL_FREE_TOP])] = page
+                ctrl[CTRL_FREE_TOP] += 1
+
+    @staticmethod
+    def pool_gather_cold(t, cold, window, key_out, value_out, batch, seq_out, flags=0):
+        kp, vp, bt, lens, hw, free, ctrl, shares = t
+        kc, vc, ks, vs, _ = cold
+        P, MB = _HostOps._geometry(t)
+        if flags & SEQ_FROM_DEVICE:
+            seq_out = min(seq_out, int(lens[:batch].max())) if batch else 0
+        key_out[:batch, :, :seq_out].zero_()
+        value_out[:batch, :, :seq_out].zero_()
+        for b in range(batch):
+            for j in range(min(-(-seq_out // P), MB)):
+                lo = j * P
+                n = min(P, min(seq_out, int(hw[b])) - lo)
+                if n <= 0:
+                    break
+                e = int(bt[b, j])
+                if e >= 0:
+                    kpage, vpage = kp[e], vp[e]
+                elif e <= -2:
+                    c = -2 - e
+                    kpage = _HostOps._dequantise(kc[c], ks[c].long()[None] - 127, kp.dtype)
+                    vpage = _HostOps._dequantise(vc[c], vs[c].long()[..., None] - 127, kp.dtype)
+                else:
+                    continue
+                key_out[b, :, lo:lo + n] = kpage[:n].permute(1, 0, 2)
+                value_out[b, :, lo:lo + n] = vpage[:n].permute(1, 0, 2)
+
+    @staticmethod
+    def pool_update_cold_(t, cold, window, key_states, value_states, key_out, value_out, seq_out, flags=0):
+        _HostOps.pool_append_(t, key_states, value_states)
+        _HostOps.pool_compress_(t, cold, window, key_states.shape[0])
+        _HostOps.pool_gather_cold(t, cold, window, key_out, value_out, key_states.shape[0], seq_out, flags)
+
+    @staticmethod
+    def pool_free_rows_cold_(t, cold, window, rows):
+        kp, vp, bt, lens, hw, free, ctrl, shares = t
+        free_cold = cold[4]
+        P, MB = _HostOps._geometry(t)
+        top = int(ctrl[CTRL_FREE_TOP])
+        ctop = int(ctrl[CTRL_COLD_TOP])
+        for r in rows.tolist():
+            n = min(-(-int(hw[r]) // P), MB)
+            for j in range(n):
+                e = int(bt[r, j])
+                if e >= 0:
+                    top = _HostOps._release(t, e, top)
+                elif e <= -2:
+                    free_cold[ctop] = -2 - e
+                    ctop += 1
+            bt[r, :n] = -1
+            lens[r] = 0
+            hw[r] = 0
+        ctrl[CTRL_FREE_TOP] = top
+        ctrl[CTRL_COLD_TOP] = ctop
 
     @staticmethod
     def pool_crop_(t, batch, max_length):

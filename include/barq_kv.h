@@ -59,6 +59,7 @@ extern "C" {
    launches. */
 #define BARQ_KV_CTRL_FREE_TOP 0 /* number of entries of free_pages that are free pages */
 #define BARQ_KV_CTRL_ERRORS 1   /* sticky error bits below, set by kernels, cleared by reset */
+#define BARQ_KV_CTRL_COLD_TOP 2 /* number of entries of a cold store's free_cold that are free */
 #define BARQ_KV_CTRL_ARRIVED 32 /* tile arrival counter of the running launch */
 #define BARQ_KV_CTRL_SUBCOUNTER0 64       /* first of the arrival sub-counters ... */
 #define BARQ_KV_CTRL_SUBCOUNTER_STRIDE 64 /* ... one per 256 bytes ... */
@@ -268,6 +269,69 @@ int barq_kv_decode_attention(const barq_kv_pool* pool, const void* query, int64_
                              int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_t,
                              float scale, int64_t max_seq, int64_t split_tokens, int64_t flags,
                              void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * ---- Quantised KV pages (fp8), no reference counterpart: the reference plans "quantized KV-cache
+ * storage", a "residual full-precision window plus compressed older pages" and "dequant-on-read"
+ * (IMPLEMENTATION_PLAN.md:106-129, after KIVI) and ships none. ----
+ *
+ * A pool may carry a cold store.  A row's block j is "cold" once it lies wholly before the row's
+ * residual window -- (j + 1) * page_size <= seq_lens - window -- and barq_kv_compress has run:
+ * its K and V then live in the cold store as OCP FP8 E4M3 codes (round to nearest even) with
+ * power-of-two scales stored as E8M0 bytes (2^(s - 127)): keys one scale per channel (head, dim)
+ * over the page's tokens, values one per token (token, head) over head_dim, each the smallest
+ * power of two 2^e with max |x| <= 448 * 2^e over the group's finite elements (e = 0 for a group
+ * with none non-zero, e clamped to [-127, 127]).  Reads dequantise: code * 2^e, rounded to the
+ * pool's element type.  The block table names cold page c as BARQ_KV_COLD_ENTRY(c) (<= -2).
+ * Appends (barq_kv_append) only write at or after seq_lens, which stays in hot pages; a pool with
+ * a cold store is read with barq_kv_gather_cold and released with barq_kv_free_rows_cold.
+ * Element types: bf16, fp16, fp32.  Limits: page_size * kv_heads <= 4096, kv_heads * head_dim
+ * <= 16384, num_cold < 2^31 - 2.
+ */
+#define BARQ_KV_COLD_ENTRY(c) (-2 - (c))
+
+typedef struct barq_kv_cold {
+  void* key_codes;     /* uint8 [num_cold, page_size, kv_heads, head_dim] */
+  void* value_codes;   /* uint8 [num_cold, page_size, kv_heads, head_dim] */
+  void* key_scales;    /* uint8 [num_cold, kv_heads, head_dim]: E8M0, per channel */
+  void* value_scales;  /* uint8 [num_cold, page_size, kv_heads]: E8M0, per token */
+  int32_t* free_cold;  /* int32 [num_cold], a stack; entries [0, ctrl[BARQ_KV_CTRL_COLD_TOP]) free */
+  int64_t num_cold;
+  int64_t window;      /* residual window in tokens, >= 0 */
+  int64_t element_type; /* the pool's elements: BARQ_KV_BF16, BARQ_KV_FP16 or BARQ_KV_FP32 */
+} barq_kv_cold;
+
+#define BARQ_KV_BF16 0
+#define BARQ_KV_FP16 1
+#define BARQ_KV_FP32 2
+
+/* Every cold page free (after barq_kv_pool_reset, which clears ctrl). */
+int barq_kv_cold_reset(const barq_kv_pool* pool, const barq_kv_cold* cold, void* stream);
+
+/*
+ * Rows [0, batch): every hot block wholly before the residual window is quantised into a cold
+ * page taken from free_cold and its hot page returns to free_pages (in no fixed order).  A block
+ * finding no cold page stays hot and sets BARQ_KV_ERRBIT_POOL_EXHAUSTED; a hot page another
+ * block shares (page_shares) stays hot.  One workgroup per row; rows without such a block exit
+ * at once, so it can run after every append (and inside a captured graph).
+ */
+int barq_kv_compress(const barq_kv_pool* pool, const barq_kv_cold* cold, int64_t batch, void* stream);
+
+/* barq_kv_gather for a pool with a cold store: cold blocks are dequantised on the way out. */
+int barq_kv_gather_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, void* key_out,
+                        void* value_out, int64_t batch, int64_t seq_out, int64_t out_stride_b,
+                        int64_t out_stride_h, int64_t out_stride_s, int64_t flags, void* stream);
+
+/* barq_kv_append + barq_kv_compress + barq_kv_gather_cold (three launches). */
+int barq_kv_update_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, const void* key_states,
+                        const void* value_states, int64_t batch, int64_t tokens, int64_t stride_b,
+                        int64_t stride_h, int64_t stride_t, void* key_out, void* value_out,
+                        int64_t seq_out, int64_t out_stride_b, int64_t out_stride_h,
+                        int64_t out_stride_s, int64_t flags, void* stream);
+
+/* barq_kv_free_rows for a pool with a cold store: cold pages return to free_cold. */
+int barq_kv_free_rows_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, const int32_t* rows,
+                           int64_t num_rows, void* stream);
 
 #ifdef __cplusplus
 }

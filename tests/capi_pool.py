@@ -158,3 +158,83 @@ def bits(t: torch.Tensor) -> np.ndarray:
     from kvgen import to_bits
 
     return to_bits(t)
+
+
+ELEMENT_TYPE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+class CColdPool(CPool):
+    """A page pool with an fp8 cold store, driven through the C ABI (barq_kv_cold entry points)."""
+
+    def __init__(self, *, window, num_cold=None, **kw):
+        self.window = int(window)
+        super().__init__(**kw)
+        dev = self.kp.device
+        n = num_cold or self.max_batch * self.max_blocks
+        u8 = dict(dtype=torch.uint8, device=dev)
+        self.kc = torch.empty((n, self.page_size, self.heads, self.dim), **u8)
+        self.vc = torch.empty_like(self.kc)
+        self.ks = torch.empty((n, self.heads, self.dim), **u8)
+        self.vs = torch.empty((n, self.page_size, self.heads), **u8)
+        self.free_cold = torch.empty((n,), dtype=torch.int32, device=dev)
+        self.num_cold = n
+        self.cs = _capi.BarqKVCold(self.kc.data_ptr(), self.vc.data_ptr(), self.ks.data_ptr(), self.vs.data_ptr(),
+                                   self.free_cold.data_ptr(), n, self.window, ELEMENT_TYPE[self.dtype])
+        self.cold_reset()
+
+    @property
+    def cref(self):
+        return ctypes.byref(self.cs)
+
+    def cold_reset(self):
+        _capi.check(self.lib.barq_kv_cold_reset(self.ref, self.cref, self._stream()))
+
+    def reset(self, order=None):
+        super().reset(order)
+        if hasattr(self, "cs"):
+            self.cold_reset()
+
+    def compress(self, batch):
+        _capi.check(self.lib.barq_kv_compress(self.ref, self.cref, batch, self._stream()))
+
+    def gather(self, batch, seq, flags=0, out=None):
+        ko, vo = out or self.new_out(batch, seq)
+        _capi.check(self.lib.barq_kv_gather_cold(self.ref, self.cref, ko.data_ptr(), vo.data_ptr(), batch, seq,
+                                                 ko.stride(0), ko.stride(1), ko.stride(2), flags, self._stream()))
+        return ko, vo
+
+    def update(self, k, v, seq, flags=0, out=None):
+        ko, vo = out or self.new_out(k.shape[0], seq)
+        _capi.check(self.lib.barq_kv_update_cold(self.ref, self.cref, k.data_ptr(), v.data_ptr(), k.shape[0],
+                                                 k.shape[2], k.stride(0), k.stride(1), k.stride(2), ko.data_ptr(),
+                                                 vo.data_ptr(), seq, ko.stride(0), ko.stride(1), ko.stride(2), flags,
+                                                 self._stream()))
+        return ko, vo
+
+    def free_rows(self, rows):
+        idx = torch.tensor(rows, dtype=torch.int32, device=self.kp.device)
+        _capi.check(self.lib.barq_kv_free_rows_cold(self.ref, self.cref, idx.data_ptr(), len(rows), self._stream()))
+        torch.cuda.current_stream().synchronize()
+
+    def check_invariants(self, window=None):
+        """Per row: blocks below the high-water mark hold a page (cold ones first, as a prefix);
+        hot and cold pages each held once and absent from their free stacks, which hold the rest."""
+        P = self.page_size
+        bt = self.bt.cpu().numpy()
+        hw = self.hw.cpu().numpy()
+        ctrl = self.ctrl.cpu().numpy()
+        hot, cold = [], []
+        for r in range(self.max_batch):
+            n = -(-int(hw[r]) // P)
+            row = bt[r, :n]
+            c = int((row <= -2).sum())
+            assert (row[:c] <= -2).all() and (row[c:] >= 0).all(), (r, row)
+            assert (bt[r, n:] == -1).all()
+            cold += (-2 - row[:c]).tolist()
+            hot += row[c:].tolist()
+        free = set(self.free.cpu().numpy()[: int(ctrl[0])].tolist())
+        free_c = set(self.free_cold.cpu().numpy()[: int(ctrl[2])].tolist())
+        assert len(set(hot)) == len(hot) and len(set(cold)) == len(cold)
+        assert not free & set(hot) and not free_c & set(cold)
+        assert len(free) == int(ctrl[0]) and len(free_c) == int(ctrl[2])
+        assert len(hot) + len(free) == self.num_pages and len(cold) + len(free_c) == self.num_cold

@@ -1,0 +1,195 @@
+"""GPU parity of the fp8 cold store (barq_kv_compress / barq_kv_gather_cold / barq_kv_update_cold /
+barq_kv_free_rows_cold), through the C ABI and the layer API, against the oracle
+QuantLayerOracle: bit-exact (codes, scales and every dequantised element), with page accounting
+checked after every operation."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from capi_pool import CColdPool
+from kvgen import hf_layout, to_bits
+from oracle import kv_quant_oracle as q
+
+pytestmark = pytest.mark.gpu
+DT = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
+
+
+def assert_same(pool, oracle, what):
+    ok, ov = oracle.current_tensors()
+    gk, gv = pool.gather(ok.shape[0], ok.shape[2])
+    for g, w, name in ((gk, ok, "K"), (gv, ov, "V")):
+        g = to_bits(g)
+        if not np.array_equal(g, w):
+            bad = np.argwhere(g != w)
+            raise AssertionError(f"{what} {name}: {len(bad)} elements differ, first at {bad[0].tolist()}")
+
+
+CASES = [
+    # dtype, heads, dim, page, window
+    (torch.bfloat16, 2, 16, 4, 8),
+    (torch.float16, 3, 80, 16, 16),
+    (torch.float32, 1, 12, 5, 0),
+    (torch.bfloat16, 8, 128, 16, 32),
+    (torch.bfloat16, 2, 6, 1, 3),   # 2-element vectors, one-token pages
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"{DT[c[0]]}-h{c[1]}d{c[2]}p{c[3]}w{c[4]}")
+@pytest.mark.parametrize("seed", [0, 1])
+def test_random_programs_through_capi(capi, case, seed):
+    dtype, H, D, P, W = case
+    Bmax, cap = 4, 96
+    rng = np.random.default_rng(seed * 7 + P)
+    gen = torch.Generator().manual_seed(seed)
+    pool = CColdPool(window=W, max_batch=Bmax, max_blocks=-(-cap // P), page_size=P, heads=H, dim=D, dtype=dtype)
+    oracle = q.QuantLayerOracle(Bmax, cap, P, W, DT[dtype])
+    for it in range(40):
+        r = rng.random()
+        if r < 0.6 or not oracle.is_initialized:
+            b = int(rng.integers(1, Bmax + 1))
+            t = int(rng.integers(1, 30)) if rng.random() < 0.3 else 1
+            if oracle.is_initialized and int(oracle.seq_lens[:b].max()) + t > cap:
+                continue
+            k, v = hf_layout(b, H, t, D, dtype, gen) * 4, hf_layout(b, H, t, D, dtype, gen)
+            oracle.append(to_bits(k), to_bits(v))
+            if rng.random() < 0.3:  # the three launches one by one
+                pool.append(k.cuda(), v.cuda())
+                pool.compress(b)
+            else:
+                got = pool.update(k.cuda(), v.cuda(), oracle.get_seq_length())
+                ok, ov = oracle.current_tensors()
+                assert np.array_equal(to_bits(got[0]), ok) and np.array_equal(to_bits(got[1]), ov), f"update it{it}"
+        elif r < 0.75 and oracle.current_batch_size:
+            cur = oracle.current_batch_size
+            m = int(rng.integers(int(oracle.cold[:cur].max()) * P, cap))
+            pool.crop(cur, m)
+            oracle.crop(m)
+        elif oracle.current_batch_size:
+            rows = sorted(rng.choice(Bmax, size=int(rng.integers(1, 3)), replace=False).tolist())
+            pool.free_rows(rows)
+            oracle.release_rows(rows)
+        if oracle.current_batch_size:
+            assert_same(pool, oracle, f"it{it}")
+        pool.check_invariants()
+    assert pool.errors() == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_boundary_values_quantise_like_the_oracle(capi, dtype):
+    """Groups whose values sit on E4M3 codes, on the midpoints between them (ties to even) and
+    one float ulp either side, group maxima exactly at and just above 448 * 2^e, NaN, infinities,
+    signed zeros, all-zero groups and groups at the far ends of the exponent range."""
+    H, D, P, W = 2, 64, 16, 0
+    vals = q.e4m3_decode(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)
+    mids = ((vals[:-1] + vals[1:]) / 2).astype(np.float32)
+    pts = np.concatenate([vals.astype(np.float32), mids, np.nextafter(mids, np.float32(0)),
+                          np.nextafter(mids, np.float32(1e9))])
+    rng = np.random.default_rng(3)
+    page = rng.choice(pts, size=(2, P, H, D)).astype(np.float32) * np.where(rng.random((2, P, H, D)) < 0.5, -1, 1)
+    page[0, 0] = 448.0                       # channel maxima exactly 448: exponent 0
+    page[1, 0, 0] = np.float32(448.0) * np.float32(1 + 2 ** -7)   # just above: exponent 1
+    page[0, 3, 1, 5] = np.nan
+    page[1, 4, 0, 7] = np.inf
+    page[1, 5, 1, 9] = -np.inf
+    page[0, 6, 0, :] = 0.0
+    page[0, 6, 1, :] = -0.0
+    scale = np.float32(2.0 ** 20) if dtype == torch.float32 else np.float32(2.0 ** 4)
+    page[1, :, 1, 32:] *= scale              # a loud half-head: per-token value scales follow it
+    if dtype == torch.float32:
+        page[0, 8:, 1, 40:] = np.float32(3e-39)  # a denormal float32 group
+    t = torch.from_numpy(page).to(dtype)     # rounds to the element type first
+    k = t[0][None].permute(0, 2, 1, 3)       # [1, H, P, D]
+    v = t[1][None].permute(0, 2, 1, 3)
+    pool = CColdPool(window=W, max_batch=1, max_blocks=2, page_size=P, heads=H, dim=D, dtype=dtype)
+    oracle = q.QuantLayerOracle(1, 2 * P, P, W, DT[dtype])
+    pool.append(k.contiguous().cuda(), v.contiguous().cuda())
+    pool.compress(1)
+    oracle.append(to_bits(k.contiguous()), to_bits(v.contiguous()))
+    assert oracle.cold.tolist() == [1]
+    c = -2 - int(pool.bt[0, 0])
+    for key, codes, scales in ((True, pool.kc, pool.ks), (False, pool.vc, pool.vs)):
+        want_codes, want_scales = oracle.quantized_page(0, 0, key)
+        assert np.array_equal(codes[c].cpu().numpy(), want_codes), key
+        assert np.array_equal(scales[c].cpu().numpy(), want_scales), key
+    assert_same(pool, oracle, "boundary page")
+
+
+def test_c2_shape_prefill_and_decode(capi):
+    """The Llama-3-8B KV shape (8 heads x 128, bf16, page 16), 16 rows, window 128: a 512-token
+    prefill and 24 decode steps, the last compared element for element."""
+    B, H, D, P, W, cap = 16, 8, 128, 16, 128, 544
+    pool = CColdPool(window=W, max_batch=B, max_blocks=cap // P, page_size=P, heads=H, dim=D, dtype=torch.bfloat16)
+    oracle = q.QuantLayerOracle(B, cap, P, W, "bf16")
+    gen = torch.Generator().manual_seed(12)
+    k, v = hf_layout(B, H, 512, D, torch.bfloat16, gen), hf_layout(B, H, 512, D, torch.bfloat16, gen)
+    oracle.append(to_bits(k), to_bits(v))
+    pool.update(k.cuda(), v.cuda(), 512)
+    for s in range(24):
+        k, v = hf_layout(B, H, 1, D, torch.bfloat16, gen), hf_layout(B, H, 1, D, torch.bfloat16, gen)
+        oracle.append(to_bits(k), to_bits(v))
+        got = pool.update(k.cuda(), v.cuda(), 513 + s)
+    ok, ov = oracle.current_tensors()
+    assert np.array_equal(to_bits(got[0]), ok) and np.array_equal(to_bits(got[1]), ov)
+    assert oracle.cold.tolist() == [(536 - W) // P] * B
+    pool.check_invariants()
+    assert pool.errors() == 0
+
+
+def test_cold_store_exhaustion_keeps_blocks_hot(capi):
+    P = 4
+    pool = CColdPool(window=0, num_cold=3, max_batch=2, max_blocks=4, page_size=P, heads=1, dim=8,
+                     dtype=torch.float32)
+    gen = torch.Generator().manual_seed(1)
+    k, v = hf_layout(2, 1, 9, 8, torch.float32, gen), hf_layout(2, 1, 9, 8, torch.float32, gen)
+    oracle = q.QuantLayerOracle(2, 16, P, 0, "f32")
+    pool.update(k.cuda(), v.cuda(), 9)      # 4 full blocks want 4 cold pages, 3 exist
+    assert pool.errors() == 1               # POOL_EXHAUSTED
+    pool.check_invariants()
+    bt = pool.bt.cpu().numpy()
+    assert int((bt[:, :2] <= -2).sum()) == 3
+    # every block reads back either exactly (hot) or as the oracle's dequantised page (cold)
+    oracle.append(to_bits(k), to_bits(v))
+    gk, _ = pool.gather(2, 9)
+    ok, _ = oracle.current_tensors()
+    exact = to_bits(k)
+    for r in range(2):
+        for j in range(2):
+            sl = slice(j * P, (j + 1) * P)
+            want = ok[r, :, sl] if bt[r, j] <= -2 else exact[r, :, sl]
+            assert np.array_equal(to_bits(gk)[r, :, sl], want), (r, j)
+
+
+def test_layer_api_with_graph_replays(hip):
+    """QuantPagePool through the torch binding, decode steps captured in a HIP graph
+    (CapturedDecodeStep), every replay's output compared with the oracle."""
+    from barqtrain_amd.graph import CapturedDecodeStep
+    from barqtrain_amd.paged import QuantPagePool
+
+    B, H, D, P, W = 3, 2, 64, 8, 16
+    cap = 128
+    pools = [QuantPagePool(max_batch=B, max_blocks=cap // P, page_size=P, kv_heads=H, head_dim=D,
+                           dtype=torch.bfloat16, device="cuda", window=W, chunk=32) for _ in range(2)]
+    oracles = [q.QuantLayerOracle(B, cap, P, W, "bf16") for _ in range(2)]
+    gen = torch.Generator().manual_seed(7)
+    for pool, o in zip(pools, oracles):
+        k, v = hf_layout(B, H, 70, D, torch.bfloat16, gen), hf_layout(B, H, 70, D, torch.bfloat16, gen)
+        pool.update(k.cuda(), v.cuda())
+        o.append(to_bits(k), to_bits(v))
+    step = CapturedDecodeStep(pools, B, 1)
+    for s in range(30):
+        for i, (pool, o) in enumerate(zip(pools, oracles)):
+            k, v = hf_layout(B, H, 1, D, torch.bfloat16, gen), hf_layout(B, H, 1, D, torch.bfloat16, gen)
+            step.key_in[i].copy_(k)
+            step.value_in[i].copy_(v)
+            o.append(to_bits(k), to_bits(v))
+        outs = step.replay()
+        for (gk, gv), o in zip(outs, oracles):
+            ok, ov = o.current_tensors()
+            assert np.array_equal(to_bits(gk), ok) and np.array_equal(to_bits(gv), ov), s
+    for pool in pools:
+        assert pool.errors() == 0
+        assert int(pool.ctrl[0]) == pool.free_count and int(pool.ctrl[2]) == pool.cold_free
+        assert pool.cold_blocks.tolist() == [(100 - W) // P] * B
