@@ -156,28 +156,135 @@ struct CompressArgs {
   ColdPtrs c;
   int32_t batch;
   FastDiv div_page;
-  FastDiv div_dim;
+  FastDiv div_dim;     // head_dim
+  FastDiv div_groups;  // kv_heads * head_dim / VE vectors per token
 };
 
-template <int KIND>
+template <int BYTES>
+struct RawC;
+template <>
+struct RawC<16> { using T = uint32_t __attribute__((ext_vector_type(4))); };
+template <>
+struct RawC<8> { using T = uint32_t __attribute__((ext_vector_type(2))); };
+template <>
+struct RawC<4> { using T = uint32_t; };
+template <>
+struct RawC<2> { using T = uint16_t; };
+template <>
+struct RawC<1> { using T = uint8_t; };
+
+// VE elements of one token, as floats, from a page.
+template <int KIND, int VE>
+struct Lanes {
+  using Bits = typename Elem<KIND>::Bits;
+  using Raw = typename RawC<VE * (int)sizeof(Bits)>::T;
+  union U {
+    Raw v;
+    Bits e[VE];
+  };
+  __device__ static void load(const Bits* src, float* out) {
+    U u;
+    u.v = *(const Raw*)src;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) out[e] = Elem<KIND>::to_float(u.e[e]);
+  }
+};
+
+template <int VE>
+struct CodeVec {
+  using Raw = typename RawC<VE>::T;
+  union U {
+    Raw v;
+    uint8_t b[VE];
+  };
+};
+
+// Quantise hot page hp into cold page cp (keys per channel, values per (token, head)), in vectors
+// of VE elements along head_dim: maxima first (keys: a thread's channels over the page's tokens;
+// values: a thread's (token, head) groups over head_dim), exponents to LDS, then codes.
+template <int KIND, int VE>
+__device__ void quantise_page(const CompressArgs& a, int hp, int cp, int8_t* s_kexp, int8_t* s_vexp) {
+  using Bits = typename Elem<KIND>::Bits;
+  const barq_kv_pool& p = a.p;
+  const int P = (int)p.page_size, H = (int)p.kv_heads, D = (int)p.head_dim, C = H * D;
+  const Bits* __restrict__ kp = (const Bits*)p.key_pages + (int64_t)hp * P * C;
+  const Bits* __restrict__ vp = (const Bits*)p.value_pages + (int64_t)hp * P * C;
+  const int groups = C / VE;
+  for (int g = threadIdx.x; g < groups; g += kThreads) {
+    float m[VE];
+#pragma unroll
+    for (int e = 0; e < VE; ++e) m[e] = 0.0f;
+#pragma unroll 4
+    for (int t = 0; t < P; ++t) {
+      float x[VE];
+      Lanes<KIND, VE>::load(kp + (int64_t)t * C + g * VE, x);
+#pragma unroll
+      for (int e = 0; e < VE; ++e) m[e] = fmaxf(m[e], finite_abs(x[e]));
+    }
+    typename CodeVec<VE>::U sc;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) {
+      const int ex = group_exponent(m[e]);
+      s_kexp[g * VE + e] = (int8_t)ex;
+      sc.b[e] = (uint8_t)(ex + 127);
+    }
+    *(typename CodeVec<VE>::Raw*)(a.c.key_scales + (int64_t)cp * C + g * VE) = sc.v;
+  }
+  const int dv = D / VE;
+  for (int th = threadIdx.x; th < P * H; th += kThreads) {
+    const Bits* src = vp + (int64_t)th * D;  // token t = th / H, head h = th % H: contiguous
+    float m = 0.0f;
+#pragma unroll 4
+    for (int k = 0; k < dv; ++k) {
+      float x[VE];
+      Lanes<KIND, VE>::load(src + k * VE, x);
+#pragma unroll
+      for (int e = 0; e < VE; ++e) m = fmaxf(m, finite_abs(x[e]));
+    }
+    const int ex = group_exponent(m);
+    s_vexp[th] = (int8_t)ex;
+    a.c.value_scales[(int64_t)cp * P * H + th] = (uint8_t)(ex + 127);
+  }
+  __syncthreads();
+  uint8_t* __restrict__ kc = a.c.codes[0] + (int64_t)cp * P * C;
+  uint8_t* __restrict__ vc = a.c.codes[1] + (int64_t)cp * P * C;
+#pragma unroll 2
+  for (int v = threadIdx.x; v < P * groups; v += kThreads) {
+    const int t = (int)a.div_groups.div((uint32_t)v);
+    const int g = v - t * groups;
+    const int ch = g * VE;
+    const int th = t * H + (int)a.div_dim.div((uint32_t)ch);
+    const int64_t at = (int64_t)t * C + ch;
+    float xk[VE], xv[VE];
+    Lanes<KIND, VE>::load(kp + at, xk);
+    Lanes<KIND, VE>::load(vp + at, xv);
+    const int ve = s_vexp[th];
+    typename CodeVec<VE>::U ck, cv;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) {
+      ck.b[e] = (uint8_t)e4m3_encode(ldexpf(xk[e], -(int)s_kexp[ch + e]));
+      cv.b[e] = (uint8_t)e4m3_encode(ldexpf(xv[e], -ve));
+    }
+    *(typename CodeVec<VE>::Raw*)(kc + at) = ck.v;
+    *(typename CodeVec<VE>::Raw*)(vc + at) = cv.v;
+  }
+}
+
+template <int KIND, int VE>
 __global__ void __launch_bounds__(kThreads) compress_kernel(const CompressArgs a) {
-  using E = Elem<KIND>;
-  using Bits = typename E::Bits;
   __shared__ int lds_scan[kWaves];
   __shared__ int s_blocks[kThreads];
   __shared__ int s_cold;
-  __shared__ uint32_t s_vmax[kMaxTokenHeads];
+  __shared__ int8_t s_vexp[kMaxTokenHeads];
   __shared__ int8_t s_kexp[kMaxChannels];
   const barq_kv_pool& p = a.p;
   const int r = blockIdx.x;
-  const int P = (int)p.page_size, H = (int)p.kv_heads, C = (int)(p.kv_heads * p.head_dim);
   const int mb = (int)p.max_blocks;
   const int len = p.seq_lens[r];
   const int old_len = len - a.c.window;
   const int jmax = min(old_len > 0 ? (int)a.div_page.div((uint32_t)old_len) : 0,
                        min(ceil_div_fd(p.high_water[r], a.div_page), mb));
   int32_t* row = p.block_table + (int64_t)r * mb;
-  const Bits* pages[2] = {(const Bits*)p.key_pages, (const Bits*)p.value_pages};
   int err = 0;
   for (int j0 = 0; j0 < jmax; j0 += kThreads) {
     const int j = j0 + (int)threadIdx.x;
@@ -204,39 +311,11 @@ __global__ void __launch_bounds__(kThreads) compress_kernel(const CompressArgs a
         }
         s_cold = cp;
       }
-      for (int i = threadIdx.x; i < P * H; i += kThreads) s_vmax[i] = 0;
       __syncthreads();
       const int cp = s_cold;
       const int hp = row[jb];
       if (cp >= 0) {  // uniform
-        const int64_t src = (int64_t)hp * P * C;
-        const int64_t dst = (int64_t)cp * P * C;
-        // pass 1: key maxima per channel (in registers, then LDS), value maxima per (token, head)
-        for (int ch = threadIdx.x; ch < C; ch += kThreads) {
-          const int h = (int)a.div_dim.div((uint32_t)ch);
-          float kmax = 0.0f;
-          for (int t = 0; t < P; ++t) {
-            kmax = fmaxf(kmax, finite_abs(E::to_float(pages[0][src + (int64_t)t * C + ch])));
-            const float v = finite_abs(E::to_float(pages[1][src + (int64_t)t * C + ch]));
-            atomicMax(&s_vmax[t * H + h], __float_as_uint(v));
-          }
-          s_kexp[ch] = (int8_t)group_exponent(kmax);
-        }
-        __syncthreads();
-        // pass 2: codes and scales
-        for (int ch = threadIdx.x; ch < C; ch += kThreads) {
-          const int h = (int)a.div_dim.div((uint32_t)ch);
-          const bool first_dim = ch == h * (int)a.div_dim.d;
-          const int ke = s_kexp[ch];
-          a.c.key_scales[(int64_t)cp * C + ch] = (uint8_t)(ke + 127);
-          for (int t = 0; t < P; ++t) {
-            const int64_t at = (int64_t)t * C + ch;
-            a.c.codes[0][dst + at] = (uint8_t)e4m3_encode(ldexpf(E::to_float(pages[0][src + at]), -ke));
-            const int ve = group_exponent(__uint_as_float(s_vmax[t * H + h]));
-            a.c.codes[1][dst + at] = (uint8_t)e4m3_encode(ldexpf(E::to_float(pages[1][src + at]), -ve));
-            if (first_dim) a.c.value_scales[((int64_t)cp * P + t) * H + h] = (uint8_t)(ve + 127);
-          }
-        }
+        quantise_page<KIND, VE>(a, hp, cp, s_kexp, s_vexp);
         __syncthreads();  // every thread has read the hot page before it is released
         if (threadIdx.x == 0) {
           row[jb] = BARQ_KV_COLD_ENTRY(cp);
@@ -301,6 +380,47 @@ struct Vec {
   };
 };
 
+// Fast dequantisation of 8 codes into 8 two-byte values: a normal E4M3 code (exponent field E
+// in 1..15) times 2^(s - 127) has the output exponent field E + s - kBias and the code's 3
+// mantissa bits on top of the output mantissa, so the bits are ((c & 0x7F) << kShift) +
+// ((s - kBias) << kExpShift) with the sign moved to bit 15 -- two values per 32-bit word.  It
+// applies when no code is zero, subnormal or NaN and every scale keeps every result a normal
+// number (s in [kBias, kMaxField - 15 + kBias]); other vectors take the per-element path.  Both
+// give the exact product, rounded to the output type, which is exact here.
+template <int KIND>
+struct FastDeq;
+template <>
+struct FastDeq<BARQ_KV_BF16> {
+  static constexpr uint32_t kShift = 4, kExpShift = 7, kBias = 7, kMaxScale = 254 - 15 + 7;
+};
+template <>
+struct FastDeq<BARQ_KV_FP16> {
+  static constexpr uint32_t kShift = 7, kExpShift = 10, kBias = 119, kMaxScale = 30 - 15 + 119;
+};
+
+__device__ __forceinline__ bool codes_normal(uint32_t w) {  // 4 codes: none zero/subnormal or NaN
+  const uint32_t e = w & 0x78787878u;
+  const uint32_t nan = (w & 0x7F7F7F7Fu) ^ 0x7F7F7F7Fu;
+  const uint32_t any_zero = ((e - 0x01010101u) & ~e) | ((nan - 0x01010101u) & ~nan);
+  return (any_zero & 0x80808080u) == 0;
+}
+
+__device__ __forceinline__ uint32_t spread_lo(uint32_t w) { return (w & 0xFFu) | ((w << 8) & 0xFF0000u); }
+__device__ __forceinline__ uint32_t spread_hi(uint32_t w) { return ((w >> 16) & 0xFFu) | ((w >> 8) & 0xFF0000u); }
+
+template <int KIND>
+__device__ __forceinline__ uint32_t fast_pair(uint32_t codes2, uint32_t scales2) {
+  using F = FastDeq<KIND>;
+  const uint32_t bias = F::kBias | (F::kBias << 16);
+  return (((codes2 & 0x007F007Fu) << F::kShift) + ((scales2 - bias) << F::kExpShift)) |
+         ((codes2 & 0x00800080u) << 8);
+}
+
+template <int KIND>
+__device__ __forceinline__ bool scale_fast(uint32_t s) {
+  return s >= FastDeq<KIND>::kBias && s <= FastDeq<KIND>::kMaxScale;
+}
+
 template <int KIND, int VE>
 __global__ void __launch_bounds__(kThreads) gather_cold_kernel(const GatherArgs a) {
   using V = Vec<KIND, VE>;
@@ -358,6 +478,31 @@ __global__ void __launch_bounds__(kThreads) gather_cold_kernel(const GatherArgs 
       } else if (cold >= 0) {
         typename V::CodeU codes;
         codes.v = __builtin_nontemporal_load((const typename V::Codes*)(a.c.codes[kv] + el));
+        if constexpr (VE == 8 && KIND != BARQ_KV_FP32) {
+          const uint32_t w0 = codes.v.x, w1 = codes.v.y;
+          uint32_t s0, s1, s2, s3;  // scale pairs, spread like the code pairs
+          bool fast = codes_normal(w0) && codes_normal(w1);
+          if (kv == 0) {
+            typename V::CodeU sc;
+            sc.v = *(const typename V::Codes*)(a.c.key_scales + ((int64_t)cold * H + h) * D + (int64_t)dv * VE);
+#pragma unroll
+            for (int e = 0; e < VE; ++e) fast = fast && scale_fast<KIND>(sc.b[e]);
+            s0 = spread_lo(sc.v.x);
+            s1 = spread_hi(sc.v.x);
+            s2 = spread_lo(sc.v.y);
+            s3 = spread_hi(sc.v.y);
+          } else {
+            const uint32_t sv = a.c.value_scales[((int64_t)cold * P + t) * H + h];
+            fast = fast && scale_fast<KIND>(sv);
+            s0 = s1 = s2 = s3 = sv | (sv << 16);
+          }
+          if (fast) {
+            uint32_t r[4] = {fast_pair<KIND>(spread_lo(w0), s0), fast_pair<KIND>(spread_hi(w0), s1),
+                             fast_pair<KIND>(spread_lo(w1), s2), fast_pair<KIND>(spread_hi(w1), s3)};
+            val[u].v = *(typename V::Out*)r;
+            continue;
+          }
+        }
         if (kv == 0) {
           typename V::CodeU sc;
           sc.v = *(const typename V::Codes*)(a.c.key_scales + ((int64_t)cold * H + h) * D + (int64_t)dv * VE);
@@ -495,6 +640,24 @@ int launch(const void* fn, dim3 grid, void* arg, hipStream_t stream) {
 }
 
 template <int KIND>
+const void* compress_fn_t(int ve) {
+  if constexpr (KIND != BARQ_KV_FP32) {
+    if (ve == 8) return (const void*)&compress_kernel<KIND, 8>;
+  }
+  switch (ve) {
+    case 4: return (const void*)&compress_kernel<KIND, 4>;
+    case 2: return (const void*)&compress_kernel<KIND, 2>;
+    default: return (const void*)&compress_kernel<KIND, 1>;
+  }
+}
+
+const void* compress_fn(int64_t kind, int ve) {
+  return kind == BARQ_KV_BF16   ? compress_fn_t<BARQ_KV_BF16>(ve)
+         : kind == BARQ_KV_FP16 ? compress_fn_t<BARQ_KV_FP16>(ve)
+                                : compress_fn_t<BARQ_KV_FP32>(ve);
+}
+
+template <int KIND>
 int launch_gather(int ve, dim3 grid, GatherArgs* a, hipStream_t s) {
   if constexpr (KIND != BARQ_KV_FP32) {  // 8 two-byte elements: a 16-byte vector
     if (ve == 8) return launch((const void*)&gather_cold_kernel<KIND, 8>, grid, a, s);
@@ -527,10 +690,15 @@ int barq_kv_compress(const barq_kv_pool* pool, const barq_kv_cold* cold, int64_t
   a.batch = (int32_t)batch;
   a.div_page = FastDiv::make((uint32_t)pool->page_size);
   a.div_dim = FastDiv::make((uint32_t)pool->head_dim);
-  const void* fn = cold->element_type == BARQ_KV_BF16   ? (const void*)&compress_kernel<BARQ_KV_BF16>
-                   : cold->element_type == BARQ_KV_FP16 ? (const void*)&compress_kernel<BARQ_KV_FP16>
-                                                        : (const void*)&compress_kernel<BARQ_KV_FP32>;
-  return launch(fn, dim3((uint32_t)batch), &a, (hipStream_t)stream);
+  // widest vector along head_dim that every page row, code row and scale row admits
+  const int64_t eb = pool->elem_bytes, D = pool->head_dim;
+  const uint64_t bits = (uint64_t)(uintptr_t)pool->key_pages | (uint64_t)(uintptr_t)pool->value_pages;
+  const uint64_t cbits = (uint64_t)(uintptr_t)cold->key_codes | (uint64_t)(uintptr_t)cold->value_codes |
+                         (uint64_t)(uintptr_t)cold->key_scales;
+  int ve = eb == 2 ? 8 : 4;
+  while (ve > 1 && (D % ve || (bits & (uint64_t)(ve * eb - 1)) || (cbits & (uint64_t)(ve - 1)))) ve >>= 1;
+  a.div_groups = FastDiv::make((uint32_t)(pool->kv_heads * D / ve));
+  return launch(compress_fn(cold->element_type, ve), dim3((uint32_t)batch), &a, (hipStream_t)stream);
 }
 
 int barq_kv_gather_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, void* key_out,
@@ -582,10 +750,12 @@ int barq_kv_update_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, cons
                         int64_t seq_out, int64_t osb, int64_t osh, int64_t oss, int64_t flags,
                         void* stream) {
   if (!cold_ok(pool, cold)) return BARQ_KV_ERR_INVALID;
+  if (flags & ~(int64_t)(BARQ_KV_SEQ_FROM_DEVICE | BARQ_KV_NO_COMPRESS)) return BARQ_KV_ERR_INVALID;
   int rc = barq_kv_append(pool, key_states, value_states, batch, tokens, stride_b, stride_h, stride_t, stream);
-  if (rc == BARQ_KV_OK) rc = barq_kv_compress(pool, cold, batch, stream);
+  if (rc == BARQ_KV_OK && !(flags & BARQ_KV_NO_COMPRESS)) rc = barq_kv_compress(pool, cold, batch, stream);
   if (rc == BARQ_KV_OK)
-    rc = barq_kv_gather_cold(pool, cold, key_out, value_out, batch, seq_out, osb, osh, oss, flags, stream);
+    rc = barq_kv_gather_cold(pool, cold, key_out, value_out, batch, seq_out, osb, osh, oss,
+                             flags & BARQ_KV_SEQ_FROM_DEVICE, stream);
   return rc;
 }
 

@@ -18,7 +18,7 @@ from typing import Optional, Sequence
 import numpy as np
 import torch
 
-from barqtrain_amd.paged import SEPARATE_FINALIZE, SEQ_FROM_DEVICE, PagedKVCapacityError, PagePool
+from barqtrain_amd.paged import NO_COMPRESS, SEPARATE_FINALIZE, SEQ_FROM_DEVICE, PagedKVCapacityError, PagePool
 
 
 class CapturedDecodeStep:
@@ -72,10 +72,11 @@ class CapturedDecodeStep:
         self.bucket = int(bucket) if bucket else self.capacity
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
 
-    def _graph(self, extent: int) -> torch.cuda.CUDAGraph:
-        """The graph whose launches cover output positions [0, extent), captured on first use.
-        Capture records the launches without running them: no pool state changes here."""
-        graph = self.graphs.get(extent)
+    def _graph(self, extent: int, compress: bool = False) -> torch.cuda.CUDAGraph:
+        """The graph whose launches cover output positions [0, extent), captured on first use
+        (with `compress`, quantised pools also run their compress launch).  Capture records the
+        launches without running them: no pool state changes here."""
+        graph = self.graphs.get((extent, compress))
         if graph is None:
             from barqtrain_amd.paged import _gpu_backend
 
@@ -86,11 +87,11 @@ class CapturedDecodeStep:
                     if self.quantized[i]:  # append, quantise what left the window, dequantising gather
                         backend.pool_update_cold_(pool.tensors, pool.cold_tensors, pool.window, self.key_in[i],
                                                   self.value_in[i], self.key_out[i], self.value_out[i], extent,
-                                                  self.flags)
+                                                  self.flags | (0 if compress else NO_COMPRESS))
                     else:
                         backend.pool_update_(pool.tensors, self.key_in[i], self.value_in[i],
                                              self.key_out[i], self.value_out[i], extent, self.flags)
-            self.graphs[extent] = graph
+            self.graphs[(extent, compress)] = graph
         return graph
 
     def replay(self) -> list[tuple[torch.Tensor, torch.Tensor]]:
@@ -110,7 +111,8 @@ class CapturedDecodeStep:
         for p, n in zip(self.pools, need):
             p.ensure_free(int(n), "append")
         cold = [p._cold_after(B, T) if q else None for p, q in zip(self.pools, self.quantized)]
-        self._graph(min(self.capacity, -(-worst // self.bucket) * self.bucket)).replay()
+        compress = any(c is not None and c[1] > 0 for c in cold)
+        self._graph(min(self.capacity, -(-worst // self.bucket) * self.bucket), compress).replay()
         lens += T
         np.maximum(hw, lens, out=hw)
         for p, n, c in zip(self.pools, need, cold):

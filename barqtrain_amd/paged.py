@@ -39,6 +39,7 @@ ERRBIT_BAD_INDEX = 4
 ERRBIT_OUT_SHORT = 8
 ERRBIT_ATTN_SHORT = 16
 SEQ_FROM_DEVICE = 1
+NO_COMPRESS = 4  # BARQ_KV_NO_COMPRESS: an update of a quantised pool skips its compress launch
 SEPARATE_FINALIZE = 2
 
 
@@ -467,14 +468,15 @@ class QuantPagePool(PagePool):
     append writes there, the blocks that left the window are quantised (``barq_kv_compress``)
     and reads dequantise (``barq_kv_gather_cold``).  Appends longer than ``chunk`` tokens
     (prefill) run in chunks, so the hot pool needs ``max_batch * (ceil((window + chunk) / P) +
-    2)`` pages (the default); the cold store holds every block of every row by default.  A crop
+    2)`` pages (the default); the cold store defaults to every block that can lie wholly before
+    the window, ``max_batch * (max_blocks - window // P)``.  A crop
     must stay at or above the quantised blocks; beam selection is not available on this pool.
     """
 
     quantized = True
 
     def __init__(self, *, max_batch: int, max_blocks: int, page_size: int, kv_heads: int, head_dim: int,
-                 dtype: torch.dtype, device: torch.device | str, window: int = 128, chunk: int = 256,
+                 dtype: torch.dtype, device: torch.device | str, window: int = 128, chunk: int = 64,
                  num_pages: Optional[int] = None, num_cold: Optional[int] = None,
                  page_order: Optional[torch.Tensor] = None):
         if dtype not in _ELEMENT_TYPES:
@@ -487,7 +489,9 @@ class QuantPagePool(PagePool):
         if num_pages is None:
             num_pages = min(int(max_batch) * (-(-(self.window + self.chunk) // P) + 2),
                             int(max_batch) * (int(max_blocks) + 1))
-        self.num_cold = int(num_cold) if num_cold is not None else int(max_batch) * int(max_blocks)
+        # A row's quantised blocks lie wholly before its last `window` tokens.
+        default_cold = int(max_batch) * max(int(max_blocks) - self.window // P, 1)
+        self.num_cold = int(num_cold) if num_cold is not None else default_cold
         if not 1 <= self.num_cold < 2**31 - 2:
             raise ValueError("num_cold out of range")
         if P * int(kv_heads) > 4096 or int(kv_heads) * int(head_dim) > 16384:
@@ -575,7 +579,8 @@ class QuantPagePool(PagePool):
         seq = int((self.lens[:batch] + tokens).max()) if seq_out is None else int(seq_out)
         ko, vo = out if out is not None else self._new_out(batch, seq)
         k, v = self._compatible_pair(key_states, value_states)
-        self._ops().pool_update_cold_(self.tensors, self.cold_tensors, self.window, k, v, ko, vo, seq, flags)
+        skip = NO_COMPRESS if moved == 0 else 0  # no block leaves the window: no compress launch
+        self._ops().pool_update_cold_(self.tensors, self.cold_tensors, self.window, k, v, ko, vo, seq, flags | skip)
         self._advance(batch, tokens, need)
         self._quantised(batch, frontier, moved)
         return ko, vo
@@ -907,7 +912,8 @@ class _HostOps:
     @staticmethod
     def pool_update_cold_(t, cold, window, key_states, value_states, key_out, value_out, seq_out, flags=0):
         _HostOps.pool_append_(t, key_states, value_states)
-        _HostOps.pool_compress_(t, cold, window, key_states.shape[0])
+        if not flags & NO_COMPRESS:
+            _HostOps.pool_compress_(t, cold, window, key_states.shape[0])
         _HostOps.pool_gather_cold(t, cold, window, key_out, value_out, key_states.shape[0], seq_out, flags)
 
     @staticmethod

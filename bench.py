@@ -44,6 +44,12 @@ call), next to the reference's dense keys[indices] over [B, H, blocks, P, D] per
 same GPU; layer 0 is checked bit for bit against the gathered rows before the selections, and
 the pool's sharing invariants are checked.
 
+`quantized_kv` (`--quant`) runs the same prefill and decode steps on fp8 quantised pages
+(QuantPagePool: blocks behind a 128-token residual window as E4M3 codes with E8M0 scales),
+graph-replayed, and times the dequantising gather alone for its roofline; layer 0 is compared
+bit for bit with the quantisation oracle and, for the error quantisation introduces, with the
+full-precision K/V.
+
 Prints ONE JSON line.  `--pmc-probe` instead runs the eager workload the rocprof counter runs
 profile: a 64 MiB elementwise pass (calibration), the prefill, then the decode steps.
 """
@@ -97,6 +103,7 @@ def parse():
     ap.add_argument("--pmc-probe", action="store_true", help="eager run for rocprof counter passes")
     ap.add_argument("--no-attention", action="store_true", help="skip the paged decode-attention leg")
     ap.add_argument("--no-beam", action="store_true", help="skip the beam-reorder (select_rows) leg")
+    ap.add_argument("--quant", action="store_true", help="add the fp8 quantised-KV leg (not run by default)")
     ap.add_argument("--bucket", type=int, default=None,
                     help="graph extent bucket in positions (default: the step's own; 0: one graph over the capacity)")
     return ap.parse_args()
@@ -456,6 +463,129 @@ def beam_leg(cfg, wl, dev, reps=20):
     }
 
 
+def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10):
+    """fp8 quantised pages (QuantPagePool): every layer prefilled as the configuration does (long
+    appends in 256-token chunks, each followed by quantisation), then `steps` decode steps of
+    append + quantise-what-left-the-window + dequantising gather, graph-replayed; no row churn.
+    The dequantising gather alone is timed from a graph of its launches (the dominant kernel's
+    roofline); layer 0 is compared with the oracle after the steps, and with the full-precision
+    K/V of the main run for the error the quantisation introduces."""
+    import numpy as np
+    import torch
+
+    from barqtrain_amd.graph import CapturedDecodeStep
+    from barqtrain_amd.paged import QuantPagePool, _gpu_backend
+    from kvgen import to_bits
+    from oracle.kv_quant_oracle import QuantLayerOracle
+
+    backend = _gpu_backend()
+    L, B, H, D, P = cfg["layers"], cfg["batch"], cfg["heads"], cfg["dim"], cfg["page"]
+    cap = max(prefill_lengths(cfg)) + wl.steps_cap
+    mb = math.ceil(cap / P)
+    pools = [QuantPagePool(max_batch=B, max_blocks=mb, page_size=P, kv_heads=H, head_dim=D, dtype=wl.dtype,
+                           device=dev, window=window) for _ in range(L)]
+    kin = torch.empty((L, B, H, 1, D), dtype=wl.dtype, device=dev)
+    vin = torch.empty_like(kin)
+    step = CapturedDecodeStep(pools, B, 1, inputs=(kin, vin))
+
+    def prefill():
+        for layer, pool in enumerate(pools):
+            pool.reset()
+            for k, v in wl.prefill_inputs(layer):
+                pool.append(k, v)
+
+    def run(s):
+        kin.copy_(wl.k_dec[s])
+        vin.copy_(wl.v_dec[s])
+        step.replay()
+
+    prefill()
+    for s in range(min(4, steps)):
+        run(s)
+    torch.cuda.synchronize()
+    prefill()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for s in range(steps):
+        run(s)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    if any(p.errors() for p in pools):
+        raise SystemExit("device error bits set by the quantised-KV leg")
+
+    # the dequantising gather alone, over the final state
+    seq = pools[0].max_len(B)
+    outs = [pools[0]._new_out(B, seq) for _ in range(2)]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i, pool in enumerate(pools):
+            ko, vo = outs[i % 2]
+            backend.pool_gather_cold(pool.tensors, pool.cold_tensors, pool.window, ko, vo, B, seq, 0)
+    graph.replay()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    gather_us = start.elapsed_time(end) * 1e3 / reps / L
+    lens = pools[0].lens[:B].astype(np.int64)
+    cold = pools[0].cold_blocks[:B].astype(np.int64)
+    tb = tok_bytes(cfg)
+    esize = elem_size(cfg)
+    cold_tok = cold * P
+    hot_tok = lens - cold_tok
+    gather_bytes = int(hot_tok.sum() * tb + cold_tok.sum() * 2 * H * D       # hot pages, codes
+                       + cold.sum() * (H * D + P * H)                          # scales
+                       + B * seq * tb)                                         # output
+    gbs = gather_bytes / (gather_us * 1e-6) / 1e9
+
+    # parity: layer 0 against the oracle fed the same inputs
+    oracle = QuantLayerOracle(B, cap, P, window, {"bfloat16": "bf16", "float16": "f16"}[cfg["dtype"]])
+    for k, v in wl.prefill_inputs(0):
+        oracle.append(to_bits(k), to_bits(v))
+    for s in range(steps):
+        oracle.append(to_bits(wl.k_dec[s, 0]), to_bits(wl.v_dec[s, 0]))
+    gk, gv = pools[0].gather(B)
+    ok, ov = oracle.current_tensors()
+    bit_exact = bool(np.array_equal(to_bits(gk), ok) and np.array_equal(to_bits(gv), ov))
+    # error against full precision: the main run's pools hold the same tokens (no churn configs)
+    err = None
+    if not any(wl.churn[:steps]):
+        exact = wl.pools[0]
+        exact.reset(wl.order)
+        for k, v in wl.prefill_inputs(0):
+            exact.append(k, v)
+        for s in range(steps):
+            exact.append(wl.k_dec[s, 0], wl.v_dec[s, 0])
+        xk, xv = exact.gather(B)
+        err = {}
+        for name, g, x in (("key", gk, xk), ("value", gv, xv)):
+            d = (g.float() - x.float())
+            err[name] = {"rms_rel": round(float(d.pow(2).mean().sqrt() / x.float().pow(2).mean().sqrt()), 5),
+                         "max_abs": round(float(d.abs().max()), 4)}
+    mem = pools[0].memory_bytes()
+    full = 2 * B * mb * P * H * D * esize
+    return {
+        "kernels": "stream_kernel (append) + compress_kernel + gather_cold_kernel per layer, graph-replayed",
+        "format": f"fp8 E4M3 codes, E8M0 scales (keys per channel, values per token over a page), "
+                  f"residual window {window} tokens",
+        "us_per_step_all_layers": round(ms * 1e3, 1),
+        "full_precision_us_per_step": round(bf16_ms_per_step * 1e3, 1),
+        "gather_cold_kernel": {"avg_launch_us": round(gather_us, 2), "bytes_per_launch": gather_bytes,
+                               "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                               "frac": round(gbs / HBM_PEAK_GBS, 4)},
+        "memory_per_layer_bytes": {**mem, "full_precision_pool": full,
+                                   "ratio": round((mem["hot_pages"] + mem["cold_store"]) / full, 3)},
+        "context": f"{int(lens.min())}..{int(lens.max())}, quantised blocks per row {int(cold.min())}..{int(cold.max())}",
+        "parity": {"layer0_bit_exact_vs_oracle": bit_exact, "after_decode_steps": steps},
+        "error_vs_full_precision": err,
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -650,6 +780,8 @@ def main():
             "after_decode_steps": cpu_steps}
     if not args.no_attention and cfg["dtype"] in ("bfloat16", "float16") and D == 128:
         result["paged_attention"] = attention_leg(cfg, pools, B, dev)
+    if args.quant and cfg["dtype"] in ("bfloat16", "float16"):
+        result["quantized_kv"] = quant_leg(cfg, wl, steps, dev, best / steps)
     if not args.no_beam:
         result["beam_select"] = beam_leg(cfg, wl, dev)
     print(json.dumps(result), flush=True)

@@ -322,7 +322,10 @@ int barq_kv_gather_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, void
                         void* value_out, int64_t batch, int64_t seq_out, int64_t out_stride_b,
                         int64_t out_stride_h, int64_t out_stride_s, int64_t flags, void* stream);
 
-/* barq_kv_append + barq_kv_compress + barq_kv_gather_cold (three launches). */
+/* barq_kv_append + barq_kv_compress + barq_kv_gather_cold (three launches).  flags:
+ * BARQ_KV_SEQ_FROM_DEVICE as for the gather; BARQ_KV_NO_COMPRESS skips the compress launch -- for
+ * a caller that knows no row's block leaves the window in this call (every page_size-th token). */
+#define BARQ_KV_NO_COMPRESS 4
 int barq_kv_update_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, const void* key_states,
                         const void* value_states, int64_t batch, int64_t tokens, int64_t stride_b,
                         int64_t stride_h, int64_t stride_t, void* key_out, void* value_out,

@@ -97,3 +97,22 @@ def test_beam_search_matches_dynamic_cache(page):
     assert torch.equal(got.sequences, ref.sequences)
     assert torch.equal(got.sequences_scores, ref.sequences_scores)
     assert all(layer.pool.shared for layer in cache.layers), "beams never shared pages"
+
+
+def test_generate_on_fp8_quantised_pages_tracks_full_precision():
+    """kv_quant="fp8_e4m3" with an 8-token residual window: most of each row's history is read
+    back from fp8 codes; greedy tokens agree with DynamicCache on at least 90 % of steps (here:
+    all) and the logits stay within 5 % relative (L2) -- quantisation is lossy by design."""
+    from transformers.cache_utils import DynamicCache
+
+    model, cfg = tiny_llama()
+    model.config._attn_implementation = "eager"
+    ids = torch.randint(1, 512, (2, 40), generator=torch.Generator().manual_seed(1))
+    new = 30
+    ref_seq, ref_logits = decode(model, ids, DynamicCache(config=cfg), new)
+    cache = create_paged_kv_cache(model, max_batch_size=2, max_cache_len=40 + new, page_size=4,
+                                  kv_quant="fp8_e4m3", residual_window=8)
+    seq, logits = decode(model, ids, cache, new)
+    assert all(int(layer.pool.cold_blocks.min()) >= 14 for layer in cache.layers)
+    assert (seq[:, 40:] == ref_seq[:, 40:]).float().mean() >= 0.9
+    assert ((logits - ref_logits).norm() / ref_logits.norm()) < 0.05

@@ -193,3 +193,45 @@ def test_layer_api_with_graph_replays(hip):
         assert pool.errors() == 0
         assert int(pool.ctrl[0]) == pool.free_count and int(pool.ctrl[2]) == pool.cold_free
         assert pool.cold_blocks.tolist() == [(100 - W) // P] * B
+
+
+def test_model_on_gpu_with_fp8_pages_tracks_full_precision(hip):
+    """A model's decode steps on fp8 pages (kv_quant="fp8_e4m3", 16-token window) against
+    DynamicCache, teacher-forced on DynamicCache's greedy sequence so both see the same tokens:
+    per-step logits within 5 % relative (L2) and the same argmax on at least 75 % of steps
+    (random weights give near-flat logits).  Then generate() runs on the quantised cache."""
+    pytest.importorskip("transformers")
+    from transformers.cache_utils import DynamicCache
+
+    from barqtrain import create_paged_kv_cache
+    from test_gpu_layer import tiny_llama
+
+    model, cfg = tiny_llama()
+    model = model.to("cuda")
+    prompt, new = 48, 32
+    ids = torch.randint(1, 512, (2, prompt), generator=torch.Generator().manual_seed(3)).to("cuda")
+    seq = model.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=new, do_sample=False,
+                         past_key_values=DynamicCache(config=cfg))
+
+    @torch.no_grad()
+    def forced(cache):
+        out = model(seq[:, :prompt], past_key_values=cache, use_cache=True)
+        logits = [out.logits[:, -1]]
+        for i in range(prompt, prompt + new - 1):
+            out = model(seq[:, i:i + 1], past_key_values=cache, use_cache=True)
+            logits.append(out.logits[:, -1])
+        return torch.stack(logits, 1)
+
+    ref = forced(DynamicCache(config=cfg))
+    cache = create_paged_kv_cache(model, max_batch_size=2, max_cache_len=prompt + new, page_size=16,
+                                  kv_quant="fp8_e4m3", residual_window=16)
+    got = forced(cache)
+    assert all(layer.pool.on_gpu and layer.pool.errors() == 0 and int(layer.pool.cold_blocks.min()) >= 3
+               for layer in cache.layers)
+    assert ((got - ref).norm() / ref.norm()) < 0.05
+    assert (got.argmax(-1) == ref.argmax(-1)).float().mean() >= 0.75
+    cache = create_paged_kv_cache(model, max_batch_size=2, max_cache_len=prompt + new, page_size=16,
+                                  kv_quant="fp8_e4m3", residual_window=16)
+    out = model.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=new, do_sample=False,
+                         past_key_values=cache)
+    assert out.shape == (2, prompt + new) and cache.get_seq_length() == prompt + new - 1
