@@ -85,6 +85,8 @@ _SIGNATURES = {
     "barq_kv_update_cold": (ctypes.c_int, [_POOL, _COLD, c_ptr, c_ptr] + [c_i64] * 5 + [c_ptr, c_ptr]
                             + [c_i64] * 5 + [c_ptr]),
     "barq_kv_free_rows_cold": (ctypes.c_int, [_POOL, _COLD, c_ptr, c_i64, c_ptr]),
+    "barq_kv_decode_attention_cold": (ctypes.c_int, [_POOL, _COLD, c_ptr] + [c_i64] * 6 + [c_ptr] + [c_i64] * 3
+                                      + [ctypes.c_float] + [c_i64] * 3 + [c_ptr, c_i64, c_ptr]),
 }
 
 _LIB: Optional[ctypes.CDLL] = None

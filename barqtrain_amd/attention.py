@@ -72,7 +72,7 @@ def paged_attention_forward(module: torch.nn.Module, query: torch.Tensor, key: t
     scale = scaling if scaling is not None else 1.0 / math.sqrt(head_dim)
     rows = (q_heads // pool.kv_heads) * tokens
     kernel_ok = (attention_mask is None and rows <= _KERNEL_MAX_ROWS and pool.on_gpu
-                 and not getattr(pool, "quantized", False)
+                 and (not getattr(pool, "quantized", False) or pool.page_size % 16 == 0)
                  and pool.dtype in (torch.bfloat16, torch.float16) and pool.head_dim == 128)
     if kernel_ok:
         return pool.attend(query, scale).transpose(1, 2), None

@@ -33,6 +33,7 @@
 #include <cmath>
 
 #include "barq_kv.h"
+#include "barq_kv_fp8.h"
 #include "fastdiv.h"
 
 namespace {
@@ -83,6 +84,13 @@ struct AttnArgs {
   int32_t range_chunks; // chunks per range (0: total / waves, at least kMinRangeChunks)
   int32_t waves;        // the launch's waves (one per resident slot)
   float scale_log2;     // softmax scale * log2(e)
+  // fp8 cold store (quantised pools; page_size a multiple of 16): a table entry -2 - c names
+  // cold page c, whose codes and scales replace the page's K and V.
+  const uint8_t* kcodes;
+  const uint8_t* vcodes;
+  const uint8_t* kscales;
+  const uint8_t* vscales;
+  int32_t num_cold;
 };
 
 // A piece's partial: rows x head_dim unnormalised sums, then the rows' running maxima and sums,
@@ -240,13 +248,15 @@ __device__ __forceinline__ int table_lane(const int (&pt)[kTableRegs], int idx) 
 // Block-table window of row b: lane j of pt[k] holds block blk0 + 64k + j, for the blocks
 // [blk0, blk_end) the piece reads.  An entry that names no page of the pool is recorded and read
 // as page 0, so no access leaves the pool.
+template <bool COLD>
 __device__ __forceinline__ void load_table(const AttnArgs& a, int b, int blk0, int blk_end, int lane,
                                            int (&pt)[kTableRegs]) {
   const int n = min(kTableEntries, min(blk_end, a.max_blocks) - blk0);
 #pragma unroll
   for (int k = 0; k < kTableRegs; ++k) {
     int page = 64 * k + lane < n ? a.block_table[(int64_t)b * a.max_blocks + blk0 + 64 * k + lane] : 0;
-    if ((uint32_t)page >= (uint32_t)a.num_pages) {
+    const bool cold_ok = COLD && page <= -2 && -2 - page < a.num_cold;
+    if ((uint32_t)page >= (uint32_t)a.num_pages && !cold_ok) {
       atomicOr(a.errors, BARQ_KV_ERRBIT_BAD_INDEX);
       page = 0;
     }
@@ -257,15 +267,48 @@ __device__ __forceinline__ void load_table(const AttnArgs& a, int b, int blk0, i
 // K and V of one 16-position chunk for this lane.  K: lane (g, n16) holds dims 32 * step + 8 * g
 // .. +7 of position tc + n16; V: dims 8 * n16 .. +7 of position tc + 4s + g.  Positions >= end
 // load nothing and read as zero.
-template <bool UNIFORM, bool PRED>
+template <bool UNIFORM, bool PRED, bool COLD>
 __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kTableRegs], int blk0,
                                            const char* kbase, const char* vbase, int tc, int end,
-                                           int klane, int vlane, int n16, int g, u32x4 (&kv)[kSteps],
-                                           u32x4 (&vv)[4]) {
+                                           int klane, int vlane, int n16, int g, int kvh, u32x4 (&kv)[kSteps],
+                                           u32x4 (&vv)[4], bool& cold) {
+  cold = false;
   if constexpr (UNIFORM) {
     // page_size is a multiple of 16: the chunk lies in one page, its base a scalar.
     const uint32_t blk = a.page_div.div((uint32_t)tc);
     const int page = table_scalar(pt, (int)blk - blk0);
+    if constexpr (COLD) {
+      if (page < 0) {
+        // Quantised page: raw codes and scales into the chunk registers, decoded just before the
+        // chunk is computed (so the loads stay in flight meanwhile).  K: lane (g, n16) takes 8
+        // codes of dims 32 st + 8 g of position tc + n16, and their 8 per-channel scales; V: 8
+        // codes of dims 8 n16 of position tc + 4 s + g, and that position's scale.
+        cold = true;
+        const int c = -2 - page;
+        const int t0 = tc - (int)(blk * (uint32_t)a.page_size);
+        const int64_t head = (int64_t)kvh * kHeadDim;
+        const int64_t code_page = (int64_t)c * a.page_size * a.kv_heads * kHeadDim;
+        const uint8_t* kc = a.kcodes + code_page + (int64_t)(t0 + n16) * a.kv_heads * kHeadDim + head + 8 * g;
+        const uint8_t* ks = a.kscales + ((int64_t)c * a.kv_heads) * kHeadDim + head + 8 * g;
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) {
+          const bool in = !PRED || tc + n16 < end;
+          const uint2 cw = in ? *(const uint2*)(kc + 32 * st) : uint2{0, 0};
+          const uint2 sw = *(const uint2*)(ks + 32 * st);
+          kv[st] = u32x4{cw.x, cw.y, sw.x, sw.y};
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int t = t0 + 4 * s + g;
+          const bool in = !PRED || tc + 4 * s + g < end;
+          const uint2 cw = in ? *(const uint2*)(a.vcodes + code_page + (int64_t)t * a.kv_heads * kHeadDim + head + 8 * n16)
+                              : uint2{0, 0};
+          const uint32_t sv = in ? a.vscales[((int64_t)c * a.page_size + t) * a.kv_heads + kvh] : 127u;
+          vv[s] = u32x4{cw.x, cw.y, sv, 0};
+        }
+        return;
+      }
+    }
     const int64_t base = (int64_t)page * a.page_bytes +
                          (int64_t)(tc - (int)(blk * (uint32_t)a.page_size)) * a.row_bytes;
     const char* kp = kbase + base + klane;
@@ -299,7 +342,136 @@ __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kT
 
 // One piece: positions [t_begin, t_end) of (row b, kv head kvh), row length len.  whole: the
 // piece is the whole pair (write the output), else write record `rec_id`.
-template <int E, int R, bool UNIFORM, typename OutT>
+// Quantised chunk registers (codes and scales, as load_chunk left them) -> two-byte K and V.
+// When every vector of every lane qualifies, the exponent arithmetic decodes the chunk unrolled;
+// otherwise (a zero, subnormal or NaN code, or an extreme scale somewhere in the wave) one rolled
+// loop takes the vectors one by one -- exponent arithmetic where it applies, the exact element
+// path where not -- picking and putting back each vector with constant-index switches, so the
+// rare path adds no register pressure to the common one.
+template <int E>
+__device__ __forceinline__ u32x4 dequant_vector(const u32x4 x, bool value) {
+  const uint32_t s0 = value ? x[2] * 0x01010101u : x[2];
+  const uint32_t s1 = value ? s0 : x[3];
+  uint32_t o[4];
+  if (barq_fp8::dequant8_fast_ok<E>(x[0], x[1], s0, s1)) {
+    barq_fp8::dequant8_fast<E>(x[0], x[1], s0, s1, o);
+  } else {
+    o[0] = barq_fp8::dequant2_inline<E>(x[0], s0);
+    o[1] = barq_fp8::dequant2_inline<E>(x[0] >> 16, s0 >> 16);
+    o[2] = barq_fp8::dequant2_inline<E>(x[1], s1);
+    o[3] = barq_fp8::dequant2_inline<E>(x[1] >> 16, s1 >> 16);
+  }
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+template <int E>
+__device__ __forceinline__ void dequant_chunk(u32x4 (&kv)[kSteps], u32x4 (&vv)[4]) {
+  static_assert(kSteps == 4, "vectors 0-3 are K steps, 4-7 V position slots");
+  bool fast = true;
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) fast = fast && barq_fp8::dequant8_fast_ok<E>(kv[st][0], kv[st][1], kv[st][2], kv[st][3]);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const uint32_t sv = vv[s][2] * 0x01010101u;
+    fast = fast && barq_fp8::dequant8_fast_ok<E>(vv[s][0], vv[s][1], sv, sv);
+  }
+  if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) {
+      uint32_t o[4];
+      barq_fp8::dequant8_fast<E>(kv[st][0], kv[st][1], kv[st][2], kv[st][3], o);
+      kv[st] = u32x4{o[0], o[1], o[2], o[3]};
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const uint32_t sv = vv[s][2] * 0x01010101u;
+      uint32_t o[4];
+      barq_fp8::dequant8_fast<E>(vv[s][0], vv[s][1], sv, sv, o);
+      vv[s] = u32x4{o[0], o[1], o[2], o[3]};
+    }
+    return;
+  }
+#pragma unroll 1
+  for (int i = 0; i < 8; ++i) {
+    u32x4 x;
+    switch (i) {
+      case 0: x = kv[0]; break;
+      case 1: x = kv[1]; break;
+      case 2: x = kv[2]; break;
+      case 3: x = kv[3]; break;
+      case 4: x = vv[0]; break;
+      case 5: x = vv[1]; break;
+      case 6: x = vv[2]; break;
+      default: x = vv[3]; break;
+    }
+    const u32x4 y = dequant_vector<E>(x, i >= 4);
+    switch (i) {
+      case 0: kv[0] = y; break;
+      case 1: kv[1] = y; break;
+      case 2: kv[2] = y; break;
+      case 3: kv[3] = y; break;
+      case 4: vv[0] = y; break;
+      case 5: vv[1] = y; break;
+      case 6: vv[2] = y; break;
+      default: vv[3] = y; break;
+    }
+  }
+}
+
+// Fast operands from a quantised chunk (scale bytes in [64, 191], checked per chunk): the codes
+// are converted by the hardware (gfx950 decodes OCP E4M3 exactly, zero and subnormal codes
+// included) and multiplied by 2^(s - 127) -- exact in fp32 -- then rounded to the two-byte type
+// as the dequantising gather rounds them (bf16: exact, the top half; fp16: nearest even), so K's
+// operand holds exactly the dequantised value.  V needs no scale here: its per-position scale
+// multiplies the probability (exact: a power of two).  A NaN code reads as NaN either way, and
+// the hardware's +0 for code 0x80 (-0) changes no product or sum.
+__device__ __forceinline__ bool chunk_scales_moderate(const u32x4 (&kv)[kSteps], const u32x4 (&vv)[4]) {
+  uint32_t ok = 0x40404040u;
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) ok &= ((kv[st][2] >> 1) ^ kv[st][2]) & ((kv[st][3] >> 1) ^ kv[st][3]);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) ok &= ((vv[s][2] >> 1) ^ vv[s][2]) | 0x40404000u;
+  return (ok & 0x40404040u) == 0x40404040u;  // every byte's top two bits are 01 or 10: 64..191
+}
+
+__device__ __forceinline__ float e8m0_float(uint32_t s) { return __uint_as_float(s << 23); }
+
+template <int E>
+__device__ __forceinline__ u32x4 k_operand(const u32x4 x) {
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t w = x[j], sw = x[2 + j];
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+    const float f0 = lo[0] * e8m0_float(sw & 0xFFu), f1 = lo[1] * e8m0_float((sw >> 8) & 0xFFu);
+    const float f2 = hi[0] * e8m0_float((sw >> 16) & 0xFFu), f3 = hi[1] * e8m0_float(sw >> 24);
+    if constexpr (E == kBF16) {
+      o[2 * j] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+      o[2 * j + 1] = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
+    } else {  // round to nearest even, as the dequantised values are (fp16's range is narrow)
+      o[2 * j] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f0) |
+                 ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f1) << 16);
+      o[2 * j + 1] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f2) |
+                     ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f3) << 16);
+    }
+  }
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+__device__ __forceinline__ void v_operand(const u32x4 x, float (&f)[8]) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[j], false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[j], true);
+    f[4 * j] = lo[0];
+    f[4 * j + 1] = lo[1];
+    f[4 * j + 2] = hi[0];
+    f[4 * j + 3] = hi[1];
+  }
+}
+
+template <int E, int R, bool UNIFORM, typename OutT, bool COLD>
 __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u32x4 (&lq)[kSteps][kWave],
                              int b, int kvh, int len, int t_begin, int t_end, bool whole, int64_t rec_id) {
   const int lane = threadIdx.x;
@@ -327,7 +499,7 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
   int blk0 = (int)a.page_div.div((uint32_t)t_begin);
   const int blk_end = t_end > t_begin ? (int)a.page_div.div((uint32_t)(t_end - 1)) + 1 : blk0;
   int pt[kTableRegs];
-  load_table(a, b, blk0, blk_end, lane, pt);
+  load_table<COLD>(a, b, blk0, blk_end, lane, pt);
 
   const char* kbase = a.kpages + (int64_t)kvh * a.head_bytes;
   const char* vbase = a.vpages + (int64_t)kvh * a.head_bytes;
@@ -346,24 +518,26 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[r2][e] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto load = [&](int tc, u32x4 (&kv)[kSteps], u32x4 (&vv)[4]) {
+  auto load = [&](int tc, u32x4 (&kv)[kSteps], u32x4 (&vv)[4], bool& cold) {
     // Slide the table window when the chunk's last block leaves it (every 254+ blocks).
     const int last = (int)a.page_div.div((uint32_t)min(tc + kBlock, t_end) - 1u);
     if (last - blk0 >= kTableEntries) {
       blk0 = (int)a.page_div.div((uint32_t)tc);
-      load_table(a, b, blk0, blk_end, lane, pt);
+      load_table<COLD>(a, b, blk0, blk_end, lane, pt);
     }
     if (tc + kBlock <= t_end)
-      load_chunk<UNIFORM, false>(a, pt, blk0, kbase, vbase, tc, t_end, klane, vlane, n16, g, kv, vv);
+      load_chunk<UNIFORM, false, COLD>(a, pt, blk0, kbase, vbase, tc, t_end, klane, vlane, n16, g, kvh, kv, vv, cold);
     else
-      load_chunk<UNIFORM, true>(a, pt, blk0, kbase, vbase, tc, t_end, klane, vlane, n16, g, kv, vv);
+      load_chunk<UNIFORM, true, COLD>(a, pt, blk0, kbase, vbase, tc, t_end, klane, vlane, n16, g, kvh, kv, vv, cold);
   };
 
-  auto compute = [&](int tc, const u32x4 (&kv)[kSteps], const u32x4 (&vv)[4]) {
+  // codes: the chunk registers hold a quantised chunk with moderate scales (see k_operand).
+  auto compute = [&](int tc, const u32x4 (&kv)[kSteps], const u32x4 (&vv)[4], bool codes) {
     // Scores: lane (g, n16), register r = row 4g + r, position tc + n16; log2 units.
     f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int st = 0; st < kSteps; ++st) sc = mfma_qk<E>(lq[st][lane], kv[st], sc);
+    for (int st = 0; st < kSteps; ++st)
+      sc = mfma_qk<E>(lq[st][lane], (COLD && codes) ? k_operand<E>(kv[st]) : kv[st], sc);
     float x[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) x[r] = sc[r] * a.scale_log2;
@@ -402,10 +576,16 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       float vf[8];
-      widen8<E>(vv[s], vf);
+      float vs = 1.0f;  // a quantised position's scale, moved onto its probability
+      if (COLD && codes) {
+        v_operand(vv[s], vf);
+        vs = e8m0_float(vv[s][2]);
+      } else {
+        widen8<E>(vv[s], vf);
+      }
 #pragma unroll
       for (int r2 = 0; r2 < R; ++r2) {
-        const float pa = lp[4 * s + g][4 * r2 + (lane & 3)];
+        const float pa = lp[4 * s + g][4 * r2 + (lane & 3)] * vs;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           acc[r2][e] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vf[e], acc[r2][e], 0, 0, 0);
@@ -415,17 +595,28 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
 
   // Two register buffers: the next chunk's loads are in flight while this one is computed.
   u32x4 ka[kSteps], va[4], kb[kSteps], vb[4];
+  bool cold_a = false, cold_b = false;  // the buffer holds codes and scales (wave-uniform)
   int tc = t_begin;
-  if (tc < t_end) load(tc, ka, va);
+  if (tc < t_end) load(tc, ka, va, cold_a);
   while (tc < t_end) {
-    if (tc + kBlock < t_end) load(tc + kBlock, kb, vb);
+    if (tc + kBlock < t_end) load(tc + kBlock, kb, vb, cold_b);
     __builtin_amdgcn_sched_barrier(0);
-    compute(tc, ka, va);
+    bool codes_a = false;
+    if (COLD && cold_a) {
+      codes_a = __builtin_amdgcn_ballot_w64(!chunk_scales_moderate(ka, va)) == 0;
+      if (!codes_a) dequant_chunk<E>(ka, va);
+    }
+    compute(tc, ka, va, codes_a);
     tc += kBlock;
     if (tc >= t_end) break;
-    if (tc + kBlock < t_end) load(tc + kBlock, ka, va);
+    if (tc + kBlock < t_end) load(tc + kBlock, ka, va, cold_a);
     __builtin_amdgcn_sched_barrier(0);
-    compute(tc, kb, vb);
+    bool codes_b = false;
+    if (COLD && cold_b) {
+      codes_b = __builtin_amdgcn_ballot_w64(!chunk_scales_moderate(kb, vb)) == 0;
+      if (!codes_b) dequant_chunk<E>(kb, vb);
+    }
+    compute(tc, kb, vb, codes_b);
     tc += kBlock;
   }
 
@@ -479,7 +670,7 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
 // One wave per workgroup, one workgroup per resident slot: ranges r = blockIdx.x, + gridDim.x,
 // ... of the flat chunk list.  UNIFORM: page_size is a multiple of 16.  R: groups of 4 query
 // rows (rows <= 4 * R).
-template <int E, int R, bool UNIFORM, typename OutT>
+template <int E, int R, bool UNIFORM, typename OutT, bool COLD>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(R <= 2 ? 2 : 1, R <= 2 ? 2 : 1)))
 void attention_flat_kernel(const AttnArgs a) {
   __shared__ float lp[kBlock][kMaxRows];   // probabilities, staged for the P.V operand layout
@@ -503,7 +694,7 @@ void attention_flat_kernel(const AttnArgs a) {
       const int k0 = c - pair_first;
       const int piece_end = min(c_end, pair_first + nch);
       const bool whole = k0 == 0 && piece_end == pair_first + nch;
-      attend_piece<E, R, UNIFORM, OutT>(a, lp, lq, b, kvh, len, kBlock * k0,
+      attend_piece<E, R, UNIFORM, OutT, COLD>(a, lp, lq, b, kvh, len, kBlock * k0,
                                         min(len, kBlock * (k0 + piece_end - c)), whole,
                                         (int64_t)r + (int64_t)b * a.kv_heads + kvh);
       c = piece_end;
@@ -605,9 +796,9 @@ int resident_waves(K kernel) {
   return waves;
 }
 
-template <int E, int R, bool U, typename OutT>
+template <int E, int R, bool U, typename OutT, bool COLD>
 hipError_t launch_typed(AttnArgs a, bool merge, hipStream_t stream) {
-  auto* k = attention_flat_kernel<E, R, U, OutT>;
+  auto* k = attention_flat_kernel<E, R, U, OutT, COLD>;
   a.waves = resident_waves(k);
   hipLaunchKernelGGL(k, dim3((unsigned)a.waves), dim3(kWave), 0, stream, a);
   hipError_t err = hipGetLastError();
@@ -617,15 +808,20 @@ hipError_t launch_typed(AttnArgs a, bool merge, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int E, int R, bool U>
+template <int E, int R, bool U, bool COLD = false>
 hipError_t launch_out(const AttnArgs& a, bool out_f32, bool merge, hipStream_t stream) {
-  return out_f32 ? launch_typed<E, R, U, float>(a, merge, stream)
-                 : launch_typed<E, R, U, uint16_t>(a, merge, stream);
+  return out_f32 ? launch_typed<E, R, U, float, COLD>(a, merge, stream)
+                 : launch_typed<E, R, U, uint16_t, COLD>(a, merge, stream);
 }
 
 template <int E>
-hipError_t launch_dtype(const AttnArgs& a, bool uniform, bool out_f32, bool merge, hipStream_t stream) {
+hipError_t launch_dtype(const AttnArgs& a, bool uniform, bool cold, bool out_f32, bool merge, hipStream_t stream) {
   const int groups = (a.rows + 3) / 4;
+  if (cold) {  // quantised pools: page_size a multiple of 16 (checked by the caller)
+    return groups == 1   ? launch_out<E, 1, true, true>(a, out_f32, merge, stream)
+           : groups == 2 ? launch_out<E, 2, true, true>(a, out_f32, merge, stream)
+                         : launch_out<E, 4, true, true>(a, out_f32, merge, stream);
+  }
   if (uniform) {
     return groups == 1   ? launch_out<E, 1, true>(a, out_f32, merge, stream)
            : groups == 2 ? launch_out<E, 2, true>(a, out_f32, merge, stream)
@@ -692,12 +888,15 @@ int64_t barq_kv_attention_workspace_bytes(const barq_kv_pool* pool, int64_t batc
   return plan.bytes;
 }
 
-int barq_kv_decode_attention(const barq_kv_pool* pool, const void* query, int64_t batch,
-                             int64_t q_heads, int64_t tokens, int64_t q_stride_b,
-                             int64_t q_stride_h, int64_t q_stride_t, void* out,
-                             int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_t,
-                             float scale, int64_t max_seq, int64_t split_tokens, int64_t flags,
-                             void* workspace, int64_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int decode_attention(const barq_kv_pool* pool, const barq_kv_cold* cold, const void* query, int64_t batch,
+                     int64_t q_heads, int64_t tokens, int64_t q_stride_b, int64_t q_stride_h,
+                     int64_t q_stride_t, void* out, int64_t out_stride_b, int64_t out_stride_h,
+                     int64_t out_stride_t, float scale, int64_t max_seq, int64_t split_tokens, int64_t flags,
+                     void* workspace, int64_t workspace_bytes, void* stream) {
   AttnPlan plan;
   const int rc = plan_attention(pool, batch, q_heads, tokens, max_seq, split_tokens, &plan);
   if (rc != BARQ_KV_OK) return rc;
@@ -748,14 +947,55 @@ int barq_kv_decode_attention(const barq_kv_pool* pool, const void* query, int64_
   a.range_chunks = (int32_t)plan.range_chunks;
   a.waves = kMaxWaves;
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.kcodes = a.vcodes = a.kscales = a.vscales = nullptr;
+  a.num_cold = 0;
 
   const bool uniform = pool->page_size % kBlock == 0;
+  if (cold) {
+    const int64_t want = (flags & BARQ_KV_ATTN_FP16) ? BARQ_KV_FP16 : BARQ_KV_BF16;
+    if (!uniform || cold->element_type != want || !cold->key_codes || !cold->value_codes || !cold->key_scales ||
+        !cold->value_scales || cold->num_cold < 1 || cold->num_cold > INT32_MAX - 2 ||
+        ((uintptr_t)cold->key_codes | (uintptr_t)cold->value_codes | (uintptr_t)cold->key_scales) % 8 != 0)
+      return BARQ_KV_ERR_INVALID;
+    a.kcodes = (const uint8_t*)cold->key_codes;
+    a.vcodes = (const uint8_t*)cold->value_codes;
+    a.kscales = (const uint8_t*)cold->key_scales;
+    a.vscales = (const uint8_t*)cold->value_scales;
+    a.num_cold = (int32_t)cold->num_cold;
+  }
   const bool out_f32 = (flags & BARQ_KV_ATTN_OUT_F32) != 0;
   const hipError_t err =
       (flags & BARQ_KV_ATTN_FP16)
-          ? launch_dtype<kF16>(a, uniform, out_f32, true, (hipStream_t)stream)
-          : launch_dtype<kBF16>(a, uniform, out_f32, true, (hipStream_t)stream);
+          ? launch_dtype<kF16>(a, uniform, cold != nullptr, out_f32, true, (hipStream_t)stream)
+          : launch_dtype<kBF16>(a, uniform, cold != nullptr, out_f32, true, (hipStream_t)stream);
   return err == hipSuccess ? BARQ_KV_OK : BARQ_KV_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" {
+
+int barq_kv_decode_attention(const barq_kv_pool* pool, const void* query, int64_t batch,
+                             int64_t q_heads, int64_t tokens, int64_t q_stride_b,
+                             int64_t q_stride_h, int64_t q_stride_t, void* out,
+                             int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_t,
+                             float scale, int64_t max_seq, int64_t split_tokens, int64_t flags,
+                             void* workspace, int64_t workspace_bytes, void* stream) {
+  return decode_attention(pool, nullptr, query, batch, q_heads, tokens, q_stride_b, q_stride_h, q_stride_t, out,
+                          out_stride_b, out_stride_h, out_stride_t, scale, max_seq, split_tokens, flags, workspace,
+                          workspace_bytes, stream);
+}
+
+int barq_kv_decode_attention_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, const void* query,
+                                  int64_t batch, int64_t q_heads, int64_t tokens, int64_t q_stride_b,
+                                  int64_t q_stride_h, int64_t q_stride_t, void* out, int64_t out_stride_b,
+                                  int64_t out_stride_h, int64_t out_stride_t, float scale, int64_t max_seq,
+                                  int64_t split_tokens, int64_t flags, void* workspace, int64_t workspace_bytes,
+                                  void* stream) {
+  if (!cold) return BARQ_KV_ERR_INVALID;
+  return decode_attention(pool, cold, query, batch, q_heads, tokens, q_stride_b, q_stride_h, q_stride_t, out,
+                          out_stride_b, out_stride_h, out_stride_t, scale, max_seq, split_tokens, flags, workspace,
+                          workspace_bytes, stream);
 }
 
 }  // extern "C"

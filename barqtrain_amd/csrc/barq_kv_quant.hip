@@ -17,6 +17,7 @@
 #include <climits>
 
 #include "barq_kv.h"
+#include "barq_kv_fp8.h"
 #include "fastdiv.h"
 
 namespace {
@@ -63,80 +64,16 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* lds, int* total)
   return before + incl - v;
 }
 
-// ---------------------------------------------------------------------------------------------
-// Element types and the E4M3 / E8M0 arithmetic.
-// ---------------------------------------------------------------------------------------------
-
-template <int KIND>
-struct Elem;
-template <>
-struct Elem<BARQ_KV_BF16> {
-  using Bits = uint16_t;
-  __device__ static float to_float(Bits b) { return __uint_as_float((uint32_t)b << 16); }
-  __device__ static Bits from_float(float f) {  // round to nearest even, NaN kept quiet
-    const uint32_t u = __float_as_uint(f);
-    if (f != f) return (Bits)((u >> 16) | 0x40);
-    return (Bits)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
-  }
-};
-template <>
-struct Elem<BARQ_KV_FP16> {
-  using Bits = uint16_t;
-  __device__ static float to_float(Bits b) { return (float)__builtin_bit_cast(_Float16, b); }
-  __device__ static Bits from_float(float f) { return __builtin_bit_cast(Bits, (_Float16)f); }
-};
-template <>
-struct Elem<BARQ_KV_FP32> {
-  using Bits = uint32_t;
-  __device__ static float to_float(Bits b) { return __uint_as_float(b); }
-  __device__ static Bits from_float(float f) { return __float_as_uint(f); }
-};
-
-// E4M3 code of a float, rounded to nearest even; finite values beyond 448 saturate, NaN and
-// infinities give the NaN code.
-__device__ __forceinline__ uint32_t e4m3_encode(float x) {
-  const uint32_t u = __float_as_uint(x);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  const float a = fabsf(x);
-  if (!(a <= 3.402823466e38f)) return sign | 0x7Fu;
-  if (a < 0.015625f) return sign | (uint32_t)rintf(a * 512.0f);  // subnormal codes 0..8
-  const uint32_t au = u & 0x7FFFFFFFu;
-  int e = (int)(au >> 23) - 127;
-  uint32_t m = (au >> 20) & 7u;
-  const uint32_t rem = au & 0xFFFFFu;
-  if (rem > 0x80000u || (rem == 0x80000u && (m & 1u))) {
-    if (++m == 8u) {
-      m = 0;
-      ++e;
-    }
-  }
-  const int code = min(((e + 7) << 3) | (int)m, 0x7E);
-  return sign | (uint32_t)code;
-}
-
-// The exact value of an E4M3 code.
-__device__ __forceinline__ float e4m3_decode(uint32_t c) {
-  const uint32_t c7 = c & 0x7Fu;
-  const uint32_t sign = (c & 0x80u) << 24;
-  if (c7 == 0x7Fu) return __uint_as_float(sign | 0x7FC00000u);
-  const float mag = c7 >= 8u ? __uint_as_float((((c7 >> 3) + 120u) << 23) | ((c7 & 7u) << 20))
-                             : (float)c7 * 0.001953125f;
-  return __uint_as_float(__float_as_uint(mag) | sign);
-}
-
-// Smallest e with a <= 448 * 2^e (0 for a == 0), clamped to [-127, 127]: with a = m * 2^x,
-// m in [0.5, 1), e = x - 9, plus 1 when m > 0.875 (448 = 0.875 * 2^9).
-__device__ __forceinline__ int group_exponent(float a) {
-  if (a == 0.0f) return 0;
-  int x;
-  const float m = frexpf(a, &x);
-  return max(-127, min(127, x - 9 + (m > 0.875f ? 1 : 0)));
-}
-
-__device__ __forceinline__ float finite_abs(float v) {
-  const float a = fabsf(v);
-  return a <= 3.402823466e38f ? a : 0.0f;
-}
+using barq_fp8::codes_normal;
+using barq_fp8::e4m3_decode;
+using barq_fp8::e4m3_encode;
+using barq_fp8::Elem;
+using barq_fp8::fast_pair;
+using barq_fp8::finite_abs;
+using barq_fp8::group_exponent;
+using barq_fp8::scale_fast;
+using barq_fp8::spread_hi;
+using barq_fp8::spread_lo;
 
 struct ColdPtrs {
   uint8_t* codes[2];   // key, value
@@ -380,47 +317,6 @@ struct Vec {
   };
 };
 
-// Fast dequantisation of 8 codes into 8 two-byte values: a normal E4M3 code (exponent field E
-// in 1..15) times 2^(s - 127) has the output exponent field E + s - kBias and the code's 3
-// mantissa bits on top of the output mantissa, so the bits are ((c & 0x7F) << kShift) +
-// ((s - kBias) << kExpShift) with the sign moved to bit 15 -- two values per 32-bit word.  It
-// applies when no code is zero, subnormal or NaN and every scale keeps every result a normal
-// number (s in [kBias, kMaxField - 15 + kBias]); other vectors take the per-element path.  Both
-// give the exact product, rounded to the output type, which is exact here.
-template <int KIND>
-struct FastDeq;
-template <>
-struct FastDeq<BARQ_KV_BF16> {
-  static constexpr uint32_t kShift = 4, kExpShift = 7, kBias = 7, kMaxScale = 254 - 15 + 7;
-};
-template <>
-struct FastDeq<BARQ_KV_FP16> {
-  static constexpr uint32_t kShift = 7, kExpShift = 10, kBias = 119, kMaxScale = 30 - 15 + 119;
-};
-
-__device__ __forceinline__ bool codes_normal(uint32_t w) {  // 4 codes: none zero/subnormal or NaN
-  const uint32_t e = w & 0x78787878u;
-  const uint32_t nan = (w & 0x7F7F7F7Fu) ^ 0x7F7F7F7Fu;
-  const uint32_t any_zero = ((e - 0x01010101u) & ~e) | ((nan - 0x01010101u) & ~nan);
-  return (any_zero & 0x80808080u) == 0;
-}
-
-__device__ __forceinline__ uint32_t spread_lo(uint32_t w) { return (w & 0xFFu) | ((w << 8) & 0xFF0000u); }
-__device__ __forceinline__ uint32_t spread_hi(uint32_t w) { return ((w >> 16) & 0xFFu) | ((w >> 8) & 0xFF0000u); }
-
-template <int KIND>
-__device__ __forceinline__ uint32_t fast_pair(uint32_t codes2, uint32_t scales2) {
-  using F = FastDeq<KIND>;
-  const uint32_t bias = F::kBias | (F::kBias << 16);
-  return (((codes2 & 0x007F007Fu) << F::kShift) + ((scales2 - bias) << F::kExpShift)) |
-         ((codes2 & 0x00800080u) << 8);
-}
-
-template <int KIND>
-__device__ __forceinline__ bool scale_fast(uint32_t s) {
-  return s >= FastDeq<KIND>::kBias && s <= FastDeq<KIND>::kMaxScale;
-}
-
 template <int KIND, int VE>
 __global__ void __launch_bounds__(kThreads) gather_cold_kernel(const GatherArgs a) {
   using V = Vec<KIND, VE>;
@@ -480,6 +376,52 @@ __global__ void __launch_bounds__(kThreads) gather_cold_kernel(const GatherArgs 
         codes.v = __builtin_nontemporal_load((const typename V::Codes*)(a.c.codes[kv] + el));
         if constexpr (VE == 8 && KIND != BARQ_KV_FP32) {
           const uint32_t w0 = codes.v.x, w1 = codes.v.y;
+          {
+            // Hardware decode (gfx950: OCP E4M3, exact for every finite code) times 2^(s - 127),
+            // exact in fp32 while the scale bytes stay in [64, 191]; rounded to the output type
+            // as from_float does.  NaN codes (the hardware drops their sign) and other scales
+            // take the paths below.
+            uint32_t sk0, sk1;
+            if (kv == 0) {
+              typename V::CodeU sc;
+              sc.v = *(const typename V::Codes*)(a.c.key_scales + ((int64_t)cold * H + h) * D + (int64_t)dv * VE);
+              sk0 = sc.v.x;
+              sk1 = sc.v.y;
+            } else {
+              sk0 = sk1 = (uint32_t)a.c.value_scales[((int64_t)cold * P + t) * H + h] * 0x01010101u;
+            }
+            const uint32_t mid = ((sk0 >> 1) ^ sk0) & ((sk1 >> 1) ^ sk1) & 0x40404040u;
+            const uint32_t n0 = (w0 & 0x7F7F7F7Fu) ^ 0x7F7F7F7Fu, n1 = (w1 & 0x7F7F7F7Fu) ^ 0x7F7F7F7Fu;
+            const uint32_t nan = (((n0 - 0x01010101u) & ~n0) | ((n1 - 0x01010101u) & ~n1)) & 0x80808080u;
+            if (mid == 0x40404040u && nan == 0) {
+#pragma unroll
+              for (int j = 0; j < 2; ++j) {
+                const uint32_t w = j ? w1 : w0, sw = j ? sk1 : sk0;
+                const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+                const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+                const float f[4] = {lo[0] * __uint_as_float((sw & 0xFFu) << 23),
+                                    lo[1] * __uint_as_float(((sw >> 8) & 0xFFu) << 23),
+                                    hi[0] * __uint_as_float(((sw >> 16) & 0xFFu) << 23),
+                                    hi[1] * __uint_as_float((sw >> 24) << 23)};
+                // The hardware reads code 0x80 as +0: every code's sign bit goes back on its value.
+                if constexpr (KIND == BARQ_KV_BF16) {  // exact values: the top halves
+                  const uint32_t p0 = __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u) |
+                                      ((w << 8) & 0x8000u) | ((w << 16) & 0x80000000u);
+                  const uint32_t p1 = __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u) |
+                                      ((w >> 8) & 0x8000u) | (w & 0x80000000u);
+                  val[u].e[4 * j] = (Bits)p0;
+                  val[u].e[4 * j + 1] = (Bits)(p0 >> 16);
+                  val[u].e[4 * j + 2] = (Bits)p1;
+                  val[u].e[4 * j + 3] = (Bits)(p1 >> 16);
+                } else {
+#pragma unroll
+                  for (int e = 0; e < 4; ++e)
+                    val[u].e[4 * j + e] = (Bits)(E::from_float(f[e]) | (((w >> (8 * e + 7)) & 1u) << 15));
+                }
+              }
+              continue;
+            }
+          }
           uint32_t s0, s1, s2, s3;  // scale pairs, spread like the code pairs
           bool fast = codes_normal(w0) && codes_normal(w1);
           if (kv == 0) {

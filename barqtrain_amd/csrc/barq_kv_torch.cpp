@@ -387,9 +387,9 @@ int64_t attention_workspace_bytes(std::vector<at::Tensor> pool, int64_t batch, i
 // query [batch, q_heads, tokens, head_dim] in the pool's dtype; out of the same shape, in the
 // pool's dtype or float32; workspace a zero-filled uint8 buffer (see
 // barq_kv_decode_attention).
-void pool_decode_attention(std::vector<at::Tensor> pool, at::Tensor query, at::Tensor out,
-                           double scale, int64_t max_seq, int64_t split_tokens,
-                           at::Tensor workspace) {
+void decode_attention_into(const std::vector<at::Tensor>& pool, const barq_kv_cold* cold, const at::Tensor& query,
+                           const at::Tensor& out, double scale, int64_t max_seq, int64_t split_tokens,
+                           const at::Tensor& workspace) {
   barq_kv_pool p = pool_from(pool);
   const at::Tensor& pages = pool[0];
   TORCH_CHECK(pages.scalar_type() == at::kBFloat16 || pages.scalar_type() == at::kHalf,
@@ -409,12 +409,32 @@ void pool_decode_attention(std::vector<at::Tensor> pool, at::Tensor query, at::T
   if (pages.scalar_type() == at::kHalf) flags |= BARQ_KV_ATTN_FP16;
   if (out.scalar_type() == at::kFloat) flags |= BARQ_KV_ATTN_OUT_F32;
   c10::DeviceGuard guard(pages.device());
-  const int rc = barq_kv_decode_attention(
-      &p, query.data_ptr(), query.size(0), query.size(1), query.size(2), query.stride(0),
-      query.stride(1), query.stride(2), out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
-      (float)scale, max_seq, split_tokens, flags, workspace.data_ptr(), workspace.numel(),
-      current_stream(pages));
+  const int rc =
+      cold ? barq_kv_decode_attention_cold(&p, cold, query.data_ptr(), query.size(0), query.size(1), query.size(2),
+                                           query.stride(0), query.stride(1), query.stride(2), out.data_ptr(),
+                                           out.stride(0), out.stride(1), out.stride(2), (float)scale, max_seq,
+                                           split_tokens, flags, workspace.data_ptr(), workspace.numel(),
+                                           current_stream(pages))
+           : barq_kv_decode_attention(&p, query.data_ptr(), query.size(0), query.size(1), query.size(2),
+                                      query.stride(0), query.stride(1), query.stride(2), out.data_ptr(),
+                                      out.stride(0), out.stride(1), out.stride(2), (float)scale, max_seq,
+                                      split_tokens, flags, workspace.data_ptr(), workspace.numel(),
+                                      current_stream(pages));
   check_status(rc, "pool_decode_attention");
+}
+
+void pool_decode_attention(std::vector<at::Tensor> pool, at::Tensor query, at::Tensor out, double scale,
+                           int64_t max_seq, int64_t split_tokens, at::Tensor workspace) {
+  decode_attention_into(pool, nullptr, query, out, scale, max_seq, split_tokens, workspace);
+}
+
+// Decode attention over a pool with an fp8 cold store (quantised blocks read as codes).
+void pool_decode_attention_cold(std::vector<at::Tensor> pool, std::vector<at::Tensor> cold, int64_t window,
+                                at::Tensor query, at::Tensor out, double scale, int64_t max_seq,
+                                int64_t split_tokens, at::Tensor workspace) {
+  barq_kv_pool p = pool_from(pool);
+  barq_kv_cold c = cold_from(p, pool[0], cold, window);
+  decode_attention_into(pool, &c, query, out, scale, max_seq, split_tokens, workspace);
 }
 
 }  // namespace
@@ -442,6 +462,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "One row selection applied to every pool of a group, sharing full pages");
   m.def("attention_workspace_bytes", &attention_workspace_bytes,
         "Workspace bytes of a decode-attention launch (-1: arguments rejected)");
+  m.def("pool_decode_attention_cold", &pool_decode_attention_cold,
+        "Decode attention reading a pool's quantised blocks as fp8 codes");
   m.def("pool_decode_attention", &pool_decode_attention,
         "Decode attention reading K/V from a page pool through its block table");
   m.def("version", []() { return std::string(barq_kv_version()); });

@@ -410,7 +410,8 @@ class PagePool:
         if max_seq is None:
             max_seq = int(self.lens[:batch].max())
         if not self.on_gpu:
-            _HostOps.pool_decode_attention(self.tensors, query, out, scale, batch)
+            ko, vo = self.gather(batch, int(self.lens[:batch].max()))
+            _HostOps.attention_over(ko, vo, self.lens, query, out, scale, batch)
             return out
         backend = _gpu_backend()
         if query.stride(3) != 1 or query.data_ptr() % 16 or any(s % 8 for s in query.stride()[:3]):
@@ -422,9 +423,12 @@ class PagePool:
                 "paged decode attention takes bf16/fp16 pools with head_dim 128 and at most 16 "
                 f"query rows per kv head (got {self.dtype}, head_dim {self.head_dim}, "
                 f"{q_heads // self.kv_heads} x {tokens} rows)")
-        backend.pool_decode_attention(self.tensors, query, out, scale, max(int(max_seq), 1),
-                                      int(split_tokens), self.attention_workspace(need))
+        self._attention_call(backend, query, out, scale, max(int(max_seq), 1), int(split_tokens),
+                             self.attention_workspace(need))
         return out
+
+    def _attention_call(self, backend, query, out, scale, max_seq, split_tokens, ws):
+        backend.pool_decode_attention(self.tensors, query, out, scale, max_seq, split_tokens, ws)
 
     def attention_workspace(self, nbytes: int) -> torch.Tensor:
         """The pool's decode-attention workspace (split records), at least `nbytes`; grown, never
@@ -626,8 +630,11 @@ class QuantPagePool(PagePool):
     def copy_rows(self, src_rows: Sequence[int], num_pages: Optional[int] = None) -> "PagePool":
         raise NotImplementedError("beam selection is not available on a pool with quantised (fp8) pages")
 
-    def attend(self, *args, **kwargs):
-        raise NotImplementedError("decode attention reads full-precision pages; gather this pool instead")
+    def _attention_call(self, backend, query, out, scale, max_seq, split_tokens, ws):
+        if self.page_size % 16:
+            raise NotImplementedError("decode attention over quantised pages needs page_size a multiple of 16")
+        backend.pool_decode_attention_cold(self.tensors, self.cold_tensors, self.window, query, out, scale,
+                                           max_seq, split_tokens, ws)
 
     def to(self, device) -> "QuantPagePool":
         super().to(device)
@@ -803,13 +810,19 @@ class _HostOps:
     def pool_decode_attention(t, query, out, scale, batch):
         """Decode attention for a pool in host memory: the gathered rows, float32 arithmetic."""
         kp, vp, bt, lens, hw, free, ctrl, shares = t
-        _, q_heads, tokens, D = query.shape
-        group = q_heads // kp.shape[2]
         seq = int(lens[:batch].max())
-        shape = (batch, kp.shape[2], seq, D)
+        shape = (batch, kp.shape[2], seq, query.shape[3])
         ko = torch.empty(shape, dtype=kp.dtype)
         vo = torch.empty(shape, dtype=kp.dtype)
         _HostOps.pool_gather(t, ko, vo, batch, seq)
+        _HostOps.attention_over(ko, vo, lens, query, out, scale, batch)
+
+    @staticmethod
+    def attention_over(ko, vo, lens, query, out, scale, batch):
+        """Attention of `query` over gathered rows ko / vo ``[batch, kv_heads, seq, D]`` (row b
+        has lens[b] positions; query token i sees [0, lens[b] - tokens + i]), float32."""
+        _, q_heads, tokens, D = query.shape
+        group = q_heads // ko.shape[1]
         for b in range(batch):
             n = int(lens[b])
             k = ko[b, :, :n].float().repeat_interleave(group, dim=0)  # [q_heads, n, D]

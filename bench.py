@@ -270,8 +270,10 @@ class Workload:
                     pool.append(k, v)
 
 
-def attention_leg(cfg, pools, B, dev, reps=20):
-    """Decode attention over the pools' current rows: one launch per layer, graph-replayed."""
+def attention_leg(cfg, pools, B, dev, reps=20, kv_bytes=None):
+    """Decode attention over the pools' current rows: one launch per layer, graph-replayed.
+    kv_bytes(pool, lens): the K/V bytes one call reads (default: every visible element in the
+    cache dtype)."""
     import numpy as np
     import torch
 
@@ -293,7 +295,7 @@ def attention_leg(cfg, pools, B, dev, reps=20):
 
     def step():
         for layer, pool in enumerate(pools):
-            backend.pool_decode_attention(pool.tensors, q, outs[layer], scale, max_seq, 0, wss[layer])
+            pool._attention_call(backend, q, outs[layer], scale, max_seq, 0, wss[layer])
 
     step()
     torch.cuda.synchronize()
@@ -314,7 +316,10 @@ def attention_leg(cfg, pools, B, dev, reps=20):
         ms = start.elapsed_time(end) / reps
         best = ms if best is None else min(best, ms)
     io = 2 * B * G * H * D * esize  # query read + output written
-    call_bytes = [int(x.sum()) * H * D * 2 * esize + io for x in lens]
+    if kv_bytes is None:
+        call_bytes = [int(x.sum()) * H * D * 2 * esize + io for x in lens]
+    else:
+        call_bytes = [kv_bytes(p, x) + io for p, x in zip(pools, lens)]
     per_call_us = best * 1e3 / L
     gbs = sum(call_bytes) / (best / 1e3) / 1e9
     # layer 0 against an fp32 attention over the gathered K/V (rows 0 and B - 1)
@@ -334,8 +339,10 @@ def attention_leg(cfg, pools, B, dev, reps=20):
     if any(p.errors() for p in pools):
         raise SystemExit("device error bits set by the attention leg")
     gathered = 3 * (sum(call_bytes) - L * io) / L  # gather reads + writes K/V, attention re-reads
+    kname = "attention_flat_kernel" + ("<..., COLD> (fp8 pages read as codes)" if getattr(pools[0], "quantized", False)
+                                       else "")
     return {
-        "kernel": "attention_flat_kernel + attention_merge_kernel (one launch pair per layer)",
+        "kernel": kname + " + attention_merge_kernel (one launch pair per layer)",
         "query_heads_per_kv_head": G,
         "us_per_layer_call": round(per_call_us, 2),
         "us_per_step_all_layers": round(best * 1e3, 1),
@@ -567,6 +574,12 @@ def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10):
             d = (g.float() - x.float())
             err[name] = {"rms_rel": round(float(d.pow(2).mean().sqrt() / x.float().pow(2).mean().sqrt()), 5),
                          "max_abs": round(float(d.abs().max()), 4)}
+    def kv_bytes(pool, lens_b):
+        c = np.minimum(pool.cold_blocks[:B] * P, lens_b)
+        return int((lens_b - c).sum() * H * D * 2 * esize + c.sum() * H * D * 2
+                   + (c // P).sum() * (H * D + P * H))
+
+    attn = attention_leg(cfg, pools, B, dev, kv_bytes=kv_bytes) if D == 128 and P % 16 == 0 else None
     mem = pools[0].memory_bytes()
     full = 2 * B * mb * P * H * D * esize
     return {
@@ -583,6 +596,7 @@ def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10):
         "context": f"{int(lens.min())}..{int(lens.max())}, quantised blocks per row {int(cold.min())}..{int(cold.max())}",
         "parity": {"layer0_bit_exact_vs_oracle": bit_exact, "after_decode_steps": steps},
         "error_vs_full_precision": err,
+        "paged_attention_fp8": attn,
     }
 
 

@@ -332,6 +332,20 @@ int barq_kv_update_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, cons
                         int64_t seq_out, int64_t out_stride_b, int64_t out_stride_h,
                         int64_t out_stride_s, int64_t flags, void* stream);
 
+/*
+ * barq_kv_decode_attention for a pool with a cold store: quantised blocks are read as their fp8
+ * codes and scales (half the bytes of a bf16 page) and dequantised in registers to exactly the
+ * values barq_kv_gather_cold returns, so the result equals attention over the dequantising
+ * gather.  Needs page_size a multiple of 16 and the cold store's element type matching flags
+ * (bf16, or fp16 with BARQ_KV_ATTN_FP16); workspace as for barq_kv_decode_attention.
+ */
+int barq_kv_decode_attention_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, const void* query,
+                                  int64_t batch, int64_t q_heads, int64_t tokens, int64_t q_stride_b,
+                                  int64_t q_stride_h, int64_t q_stride_t, void* out, int64_t out_stride_b,
+                                  int64_t out_stride_h, int64_t out_stride_t, float scale, int64_t max_seq,
+                                  int64_t split_tokens, int64_t flags, void* workspace, int64_t workspace_bytes,
+                                  void* stream);
+
 /* barq_kv_free_rows for a pool with a cold store: cold pages return to free_cold. */
 int barq_kv_free_rows_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, const int32_t* rows,
                            int64_t num_rows, void* stream);

@@ -238,3 +238,20 @@ class CColdPool(CPool):
         assert not free & set(hot) and not free_c & set(cold)
         assert len(free) == int(ctrl[0]) and len(free_c) == int(ctrl[2])
         assert len(hot) + len(free) == self.num_pages and len(cold) + len(free_c) == self.num_cold
+
+
+def attend_cold(pool: "CColdPool", q, *, scale=None, out_f32=True, max_seq=0, split_tokens=0):
+    """barq_kv_decode_attention_cold over a CColdPool; returns out [B, Hq, T, D]."""
+    B, Hq, T, D = q.shape
+    need = pool.lib.barq_kv_attention_workspace_bytes(pool.ref, B, Hq, T, max_seq, split_tokens)
+    assert need >= 0
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=pool.kp.device)
+    dt = torch.float32 if out_f32 else pool.dtype
+    out = torch.full((B, T, Hq, D), float("nan"), dtype=dt, device=pool.kp.device).transpose(1, 2)
+    flags = (1 if pool.dtype == torch.float16 else 0) | (2 if out_f32 else 0)
+    scale = D ** -0.5 if scale is None else scale
+    _capi.check(pool.lib.barq_kv_decode_attention_cold(
+        pool.ref, pool.cref, q.data_ptr(), B, Hq, T, q.stride(0), q.stride(1), q.stride(2), out.data_ptr(),
+        out.stride(0), out.stride(1), out.stride(2), scale, max_seq, split_tokens, flags, ws.data_ptr(),
+        ws.numel(), pool._stream()))
+    return out

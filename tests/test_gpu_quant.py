@@ -235,3 +235,106 @@ def test_model_on_gpu_with_fp8_pages_tracks_full_precision(hip):
     out = model.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=new, do_sample=False,
                          past_key_values=cache)
     assert out.shape == (2, prompt + new) and cache.get_seq_length() == prompt + new - 1
+
+
+ATT_F32 = dict(rtol=2e-5, atol=2e-5)
+ATT_OUT = {torch.bfloat16: dict(rtol=2.0 ** -8, atol=2e-5), torch.float16: dict(rtol=2.0 ** -11, atol=2e-5)}
+
+
+@pytest.mark.parametrize("dtype,page,window", [(torch.bfloat16, 16, 0), (torch.bfloat16, 16, 48),
+                                               (torch.float16, 32, 32), (torch.bfloat16, 32, 128)])
+def test_decode_attention_reads_quantised_pages(hip, dtype, page, window):
+    """Attention over a quantised pool (barq_kv_decode_attention_cold: cold blocks read as codes
+    and scales, dequantised in registers) against the float64 reference over the dequantising
+    gather's K/V -- the values the cold store holds -- on ragged rows mixing cold and hot blocks,
+    G = 1, 4, 8 and two query tokens; fp32 and cache-dtype outputs."""
+    from attn_ref import decode_attention_reference, within_tolerance
+    from barqtrain_amd.paged import QuantPagePool
+
+    H, D = 4, 128
+    lens = [700, 333, 129, 64, 17, 1]
+    B, cap = len(lens), 768
+    pool = QuantPagePool(max_batch=B, max_blocks=cap // page, page_size=page, kv_heads=H, head_dim=D, dtype=dtype,
+                         device="cuda", window=window)
+    gen = torch.Generator().manual_seed(page + window)
+    done = 0
+    for b in range(B, 0, -1):           # rows [0, b) grow to the next length, longest first
+        n = lens[b - 1] - done
+        if n > 0:
+            k, v = hf_layout(b, H, n, D, dtype, gen) * 3, hf_layout(b, H, n, D, dtype, gen)
+            pool.append(k.cuda(), v.cuda())
+            done += n
+    assert int(pool.cold_blocks.max()) > 0
+    kd, vd = (t.double().cpu().numpy() for t in pool.gather(B))
+    for G, T in ((1, 1), (4, 1), (8, 1), (4, 2)):
+        q = hf_layout(B, G * H, T, D, dtype, gen).cuda()
+        want = decode_attention_reference(q.double().cpu().numpy(), kd, vd, lens, D ** -0.5)
+        got = pool.attend(q, out_dtype=torch.float32)
+        ok, ratio = within_tolerance(got.double().cpu().numpy(), want, **ATT_F32)
+        assert ok, f"G={G} T={T}: {ratio:.3g} x tolerance"
+        got = pool.attend(q)
+        ok, ratio = within_tolerance(got.double().cpu().numpy(), want, **ATT_OUT[dtype])
+        assert ok, f"G={G} T={T} {dtype}: {ratio:.3g} x tolerance"
+    assert pool.errors() == 0
+
+
+def test_decode_attention_cold_through_capi(capi):
+    """The C entry point on a CColdPool with a crafted cold page (zero, subnormal and NaN-free
+    boundary codes take the exact per-element decode) next to hot pages."""
+    from attn_ref import decode_attention_reference, within_tolerance
+    from capi_pool import attend_cold
+
+    B, H, D, P, W = 2, 2, 128, 16, 16
+    pool = CColdPool(window=W, max_batch=B, max_blocks=8, page_size=P, heads=H, dim=D, dtype=torch.bfloat16)
+    gen = torch.Generator().manual_seed(21)
+    k, v = hf_layout(B, H, 70, D, torch.bfloat16, gen), hf_layout(B, H, 70, D, torch.bfloat16, gen)
+    k[0, :, 3] = 0.0                     # a zero key: zero codes in a cold page
+    v[1, 1, 5, :7] = 1e-30               # tiny values: subnormal codes
+    pool.append(k.cuda(), v.cuda())
+    pool.compress(B)
+    assert pool.errors() == 0 and int((pool.bt[:, :3] <= -2).sum()) == 6
+    kd, vd = (t.double().cpu().numpy() for t in pool.gather(B, 70))
+    q = hf_layout(B, 4 * H, 1, D, torch.bfloat16, gen).cuda()
+    out = attend_cold(pool, q)
+    torch.cuda.synchronize()
+    want = decode_attention_reference(q.double().cpu().numpy(), kd, vd, [70, 70], D ** -0.5)
+    ok, ratio = within_tolerance(out.double().cpu().numpy(), want, **ATT_F32)
+    assert ok, ratio
+    assert pool.errors() == 0
+
+
+def test_fused_paged_attention_on_fp8_pages_in_a_model(hip):
+    """A bf16 Llama whose decode attention reads the quantised pages directly (fused "barq_paged"
+    attention + kv_quant), teacher-forced against the same model on DynamicCache: logits within
+    5 % relative (L2), argmax agreeing on at least 75 % of steps."""
+    pytest.importorskip("transformers")
+    from transformers.cache_utils import DynamicCache
+
+    from barqtrain import create_paged_kv_cache
+    from barqtrain_amd import attention
+    from test_gpu_layer import bf16_llama
+
+    model, cfg = bf16_llama()
+    model = model.to("cuda")
+    prompt, new = 64, 32
+    seq = torch.randint(1, 512, (2, prompt + new), generator=torch.Generator().manual_seed(8)).to("cuda")
+
+    @torch.no_grad()
+    def forced(cache):
+        out = model(seq[:, :prompt], past_key_values=cache, use_cache=True)
+        logits = [out.logits[:, -1].float()]
+        for i in range(prompt, prompt + new - 1):
+            out = model(seq[:, i:i + 1], past_key_values=cache, use_cache=True)
+            logits.append(out.logits[:, -1].float())
+        return torch.stack(logits, 1)
+
+    model.config._attn_implementation = "sdpa"
+    ref = forced(DynamicCache(config=cfg))
+    attention.enable_paged_attention(model)
+    cache = create_paged_kv_cache(model, max_batch_size=2, max_cache_len=prompt + new, page_size=16,
+                                  kv_quant="fp8_e4m3", residual_window=16)
+    got = forced(cache)
+    assert all(layer.fused_attention and int(layer.pool.cold_blocks.min()) >= 3 for layer in cache.layers)
+    assert all(layer.pool.errors() == 0 for layer in cache.layers)
+    assert ((got - ref).norm() / ref.norm()) < 0.05
+    assert (got.argmax(-1) == ref.argmax(-1)).float().mean() >= 0.75
