@@ -61,6 +61,14 @@ struct VecT<1> { using T = uint8_t; };
 template <typename T>
 __device__ __forceinline__ T zero_vec() { return T(0); }
 
+// s_waitcnt with vmcnt = K (K < 16) and no wait on the other counters (gfx9 encoding: vmcnt
+// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int K>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(K >= 0 && K < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(K | (0x7 << 4) | (0xF << 8));
+}
+
 // Streaming accesses (page reads, input reads, output writes): every byte is touched once per
 // launch, so they carry the nontemporal hint and do not displace other data from the caches.
 template <typename T>
@@ -81,27 +89,39 @@ __device__ __forceinline__ int checked_page(int page, int64_t num_pages) {
   return (page >= 0 && (int64_t)page < num_pages) ? page : -1;
 }
 
-__device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+// Wave-wide inclusive scan on DPP: row shifts by 1, 2, 4, 8 scan each 16-lane row, then the
+// row broadcasts of lanes 15 and 31 carry row totals into rows 1, 3 and 2, 3.  Each step is a
+// VALU operation on register data; the ds_bpermute that a shuffle compiles to costs an LDS
+// round trip per step, and the control wave runs these on every launch's critical path.
+// Lanes a shift or broadcast does not reach keep `identity`.  The whole wave must be active.
+struct AddOp {
+  __device__ int operator()(int a, int b) const { return a + b; }
+};
+struct MaxOp {
+  __device__ int operator()(int a, int b) const { return max(a, b); }
+};
+
+template <typename Op>
+__device__ __forceinline__ int wave_scan_dpp(int v, int identity, Op op) {
+  v = op(v, __builtin_amdgcn_update_dpp(identity, v, 0x111, 0xf, 0xf, false));  // row_shr:1
+  v = op(v, __builtin_amdgcn_update_dpp(identity, v, 0x112, 0xf, 0xf, false));  // row_shr:2
+  v = op(v, __builtin_amdgcn_update_dpp(identity, v, 0x114, 0xf, 0xf, false));  // row_shr:4
+  v = op(v, __builtin_amdgcn_update_dpp(identity, v, 0x118, 0xf, 0xf, false));  // row_shr:8
+  v = op(v, __builtin_amdgcn_update_dpp(identity, v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  v = op(v, __builtin_amdgcn_update_dpp(identity, v, 0x143, 0xc, 0xf, false));  // row_bcast:31
   return v;
+}
+
+// Sum / maximum over the wave, uniform (returned in a scalar register).
+__device__ __forceinline__ int wave_sum(int v) {
+  return __builtin_amdgcn_readlane(wave_scan_dpp(v, 0, AddOp()), kWave - 1);
 }
 
 __device__ __forceinline__ int wave_max(int v) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, kWave));
-  return v;
+  return __builtin_amdgcn_readlane(wave_scan_dpp(v, INT_MIN, MaxOp()), kWave - 1);
 }
 
-__device__ __forceinline__ int wave_incl_scan(int v) {
-  const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int up = __shfl_up(v, o, kWave);
-    if (lane >= o) v += up;
-  }
-  return v;
-}
+__device__ __forceinline__ int wave_incl_scan(int v) { return wave_scan_dpp(v, 0, AddOp()); }
 
 // Exclusive prefix sum of v over the workgroup's NW waves; *total gets the sum of all.
 // Uses lds[0 .. NW).  Every thread of the workgroup must call it.
@@ -212,7 +232,7 @@ __device__ void commit_from_lanes(const barq_kv_pool& p, int batch, int tokens, 
   }
   const int incl = wave_incl_scan(nb.count);
   const int excl = incl - nb.count;
-  const int total = __shfl(incl, kWave - 1, kWave);
+  const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
   const int most = wave_max(nb.count);
   for (int j = 0; j < most; ++j) {
     const int k = excl + j;
@@ -265,7 +285,6 @@ struct StreamArgs {
   int32_t seq_from_device;
   int32_t commit_in_kernel;  // the launch commits its own append
   int32_t hv;        // vectors per token (kv_heads * vr)
-  int32_t rstep;     // kThreads / hv, fast mapping only
   int32_t nsub;      // arrival sub-counters in use
   FastDiv div_hv;    // by hv
   FastDiv div_vr;    // by vectors per head row
@@ -273,11 +292,12 @@ struct StreamArgs {
   FastDiv div_chunks;
 };
 
-// FAST: hv is 64, 128 or 256 and every lane offset fits 32 bits.  A copy wave then covers whole
-// runs of 64 vectors of one token position at a time, so position, block, page and output row
-// are wave-uniform (scalar registers) and a lane's addresses differ only by its column offset.
-template <int VB, bool FAST>
-__global__ void __launch_bounds__(kStreamThreads) stream_kernel(const StreamArgs a) {
+// LPP > 0: hv = 64 * LPP (LPP = 1, 2 or 4) and offsets within a page, a row's output and a row's
+// input fit 32 bits.  A copy wave then moves whole positions, 64 vectors per load, so position,
+// block, page and output row are wave-uniform (scalar registers) and a lane's addresses differ
+// only by its column offset.  LPP = 0: any geometry.
+template <int VB, int LPP>
+__device__ __forceinline__ void stream_body(const StreamArgs& a) {
   using V = typename VecT<VB>::T;
   __shared__ int64_t s_pbase[kMaxTilePages + 1];  // byte offset of each block's page, or -1
   __shared__ int s_meta[6];                       // len, hw, lo, hi, blk_lo, last
@@ -395,7 +415,7 @@ __global__ void __launch_bounds__(kStreamThreads) stream_kernel(const StreamArgs
         last = atomicAdd(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 1) == nsub - 1;
       }
     }
-    if (__shfl(last, 0, kWave)) {
+    if (__builtin_amdgcn_readfirstlane(last)) {
       commit_from_lanes(p, a.batch, T, a.gather ? a.seq_out : INT_MAX, a.div_page, c_len, c_hw, c_top, c_free);
       if (lane == 0) atomicExch(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 0);
     }
@@ -414,47 +434,91 @@ __global__ void __launch_bounds__(kStreamThreads) stream_kernel(const StreamArgs
   char* out = kv ? a.out_v : a.out_k;
   const int wave = (int)(threadIdx.x / kWave);
 
-  if (FAST) {
+  if constexpr (LPP > 0) {
+    // hv = 64 * LPP vectors per position, 32-bit offsets.  The four copy waves split a step of
+    // RSTEP = 4 / LPP positions: wave w takes position (w - 1) / LPP of the step and column
+    // block (w - 1) % LPP (vectors block * 64 + lane), so at every step the workgroup reads and
+    // writes RSTEP whole adjacent rows; a wave's kUnroll loads cover positions r0, r0 + RSTEP, ...
+    constexpr int RSTEP = 4 / LPP;
+    constexpr int kSpan = RSTEP * kUnroll;  // positions one iteration of the workgroup covers
     if (wave > 0) {
       const int lane = (int)(threadIdx.x & (kWave - 1));
-      const int ct0 = (wave - 1) * kWave;
-      const int r0 = __builtin_amdgcn_readfirstlane((int)a.div_hv.div((uint32_t)ct0));
-      const int col = ct0 - r0 * a.hv + lane;
+      const int r0 = (wave - 1) / LPP;
+      const int col = ((wave - 1) % LPP) * kWave + lane;
       const int h = (int)a.div_vr.div((uint32_t)col);
       const int v = col - h * (int)a.div_vr.d;
       const uint32_t page_lane = (uint32_t)(col * VB);
       const uint32_t out_lane = (uint32_t)((int64_t)h * a.out_sh + (int64_t)v * VB);
       const uint32_t in_lane = (uint32_t)((int64_t)h * a.in_sh + (int64_t)v * VB);
+      const uint32_t tokb = (uint32_t)a.tok_bytes;
+      const uint32_t oss = (uint32_t)a.out_ss;
+      const uint32_t ist = (uint32_t)a.in_st;
       const char* in_row = in + (int64_t)b * a.in_sb;
       char* out_row = out + (int64_t)b * a.out_sb;
-      const int rstep = a.rstep;
-      for (int j0 = r0; j0 < npos; j0 += rstep * kUnroll) {
+      const int ulen = __builtin_amdgcn_readfirstlane(len);
+      const int uhw = __builtin_amdgcn_readfirstlane(hw);
+      const int ulo = __builtin_amdgcn_readfirstlane(lo);
+      const int unpos = __builtin_amdgcn_readfirstlane(npos);
+      const int ublk_lo = __builtin_amdgcn_readfirstlane(blk_lo);
+      for (int j0 = r0; j0 < unpos; j0 += kSpan) {
+        const int sf = ulo + j0;                     // first position of this wave's iteration
+        const int sl = sf + (kUnroll - 1) * RSTEP;   // last
+        const int bf = (int)a.div_page.div((uint32_t)sf);
         V val[kUnroll];
+        if (j0 + (kUnroll - 1) * RSTEP < unpos && sl < ulen && (int)a.div_page.div((uint32_t)sl) <= bf + 1) {
+          // Interior iteration: every position inside the tile and written before this launch
+          // (s < seq_lens <= high_water), at most two pages.  Loads back to back, stores one at
+          // a time (a single-round launch drains HBM fastest with one store in flight per wave).
+          const int64_t pb0 = __hip_readfirstlane(s_pbase[bf - ublk_lo]);
+          const int64_t pb1 = __hip_readfirstlane(s_pbase[min(bf + 1 - ublk_lo, kMaxTilePages)]);
+          const int split = (bf + 1) * P;            // first position of the second page
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const int j = j0 + u * rstep;
-          const int s = lo + j;
-          val[u] = zero_vec<V>();
-          if (j < npos) {
-            if ((unsigned)(s - len) < (unsigned)T) {
-              val[u] = ld_stream<V>(in_row + (int64_t)(s - len) * a.in_st + in_lane);
-            } else if (s < hw) {
-              const int blk = (int)a.div_page.div((uint32_t)s);
-              const int64_t pb = __hip_readfirstlane(s_pbase[blk - blk_lo]);
-              if (pb >= 0) val[u] = ld_stream<V>(pages + pb + (int64_t)(s - blk * P) * a.tok_bytes + page_lane);
+          for (int u = 0; u < kUnroll; ++u) {
+            const int s = sf + u * RSTEP;
+            const bool second = s >= split;
+            const int64_t pb = second ? pb1 : pb0;
+            const uint32_t off = (uint32_t)(s - (second ? split : split - P)) * tokb;
+            val[u] = pb >= 0 ? ld_stream<V>((pages + pb + off) + page_lane) : zero_vec<V>();
+          }
+#pragma unroll
+          for (int u = 0; u < kUnroll; ++u) {
+            wait_vm<0>();
+            st_stream<V>((out_row + (uint32_t)(sf + u * RSTEP) * oss) + out_lane, val[u]);
+          }
+          continue;
+        }
+        // Boundary iteration: the tile's last positions, new tokens, positions never written
+        // (zero), stale positions past seq_lens, or more than two pages (small page sizes).
+        // Taken in halves of kUnroll / 2 loads, which keeps the register footprint small.
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          constexpr int kHalf = kUnroll / 2;
+#pragma unroll
+          for (int k = 0; k < kHalf; ++k) {
+            const int j = j0 + (half * kHalf + k) * RSTEP;
+            const int s = ulo + j;
+            val[k] = zero_vec<V>();
+            if (j < unpos) {
+              if ((unsigned)(s - ulen) < (unsigned)T) {
+                val[k] = ld_stream<V>((in_row + (uint32_t)(s - ulen) * ist) + in_lane);
+              } else if (s < uhw) {
+                const int blk = (int)a.div_page.div((uint32_t)s);
+                const int64_t pb = __hip_readfirstlane(s_pbase[blk - ublk_lo]);
+                if (pb >= 0) val[k] = ld_stream<V>((pages + pb + (uint32_t)(s - blk * P) * tokb) + page_lane);
+              }
             }
           }
-        }
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const int j = j0 + u * rstep;
-          const int s = lo + j;
-          if (j < npos) {
-            if (a.gather) st_stream<V>(out_row + (int64_t)s * a.out_ss + out_lane, val[u]);
-            if ((unsigned)(s - len) < (unsigned)T) {
-              const int blk = (int)a.div_page.div((uint32_t)s);
-              const int64_t pb = __hip_readfirstlane(s_pbase[blk - blk_lo]);
-              if (pb >= 0) *(V*)(pages + pb + (int64_t)(s - blk * P) * a.tok_bytes + page_lane) = val[u];
+          for (int k = 0; k < kHalf; ++k) {
+            const int j = j0 + (half * kHalf + k) * RSTEP;
+            const int s = ulo + j;
+            if (j < unpos) {
+              if (a.gather) st_stream<V>((out_row + (uint32_t)s * oss) + out_lane, val[k]);
+              if ((unsigned)(s - ulen) < (unsigned)T) {
+                const int blk = (int)a.div_page.div((uint32_t)s);
+                const int64_t pb = __hip_readfirstlane(s_pbase[blk - ublk_lo]);
+                if (pb >= 0) *(V*)((pages + pb + (uint32_t)(s - blk * P) * tokb) + page_lane) = val[k];
+              }
             }
           }
         }
@@ -520,6 +584,20 @@ __global__ void __launch_bounds__(kStreamThreads) stream_kernel(const StreamArgs
       if (threadIdx.x == 0) atomicExch(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 0);
     }
   }
+}
+
+// The unit-mapped kernels hold 16 vectors per copy thread; five waves per SIMD keep four tiles
+// resident per CU (their few spills sit on the new-token path).  The generic kernel keeps the
+// compiler's register allocation.
+template <int VB, int LPP>
+__global__ void __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(5)))
+stream_kernel(const StreamArgs a) {
+  stream_body<VB, LPP>(a);
+}
+
+template <int VB>
+__global__ void __launch_bounds__(kStreamThreads) stream_kernel_any(const StreamArgs a) {
+  stream_body<VB, 0>(a);
 }
 
 __global__ void __launch_bounds__(kThreads) commit_kernel(const barq_kv_pool p, int batch,
@@ -1088,11 +1166,15 @@ int launch(const void* fn, dim3 grid, void* arg, hipStream_t stream, int threads
     }                                                                                           \
   }
 
-int launch_stream_kernel(int vb, bool fast, dim3 grid, StreamArgs* arg, hipStream_t stream) {
-#define BARQ_STREAM_CASE(VB)                                                                       \
-  case VB:                                                                                         \
-    return fast ? launch((const void*)&stream_kernel<VB, true>, grid, arg, stream, kStreamThreads) \
-                : launch((const void*)&stream_kernel<VB, false>, grid, arg, stream, kStreamThreads);
+int launch_stream_kernel(int vb, int lpp, dim3 grid, StreamArgs* arg, hipStream_t stream) {
+#define BARQ_STREAM_CASE(VB)                                                                      \
+  case VB:                                                                                        \
+    switch (lpp) {                                                                                \
+      case 1: return launch((const void*)&stream_kernel<VB, 1>, grid, arg, stream, kStreamThreads); \
+      case 2: return launch((const void*)&stream_kernel<VB, 2>, grid, arg, stream, kStreamThreads); \
+      case 4: return launch((const void*)&stream_kernel<VB, 4>, grid, arg, stream, kStreamThreads); \
+      default: return launch((const void*)&stream_kernel_any<VB>, grid, arg, stream, kStreamThreads); \
+    }
   switch (vb) {
     BARQ_STREAM_CASE(16)
     BARQ_STREAM_CASE(8)
@@ -1154,10 +1236,16 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   const int64_t chunks = (span + chunk - 1) / chunk;
   const int64_t tiles = 2 * batch * chunks;
   if (tiles > kI32Max) return BARQ_KV_ERR_INVALID;
-  // The wave-uniform mapping needs whole 64-vector runs per wave and 32-bit lane offsets.
-  const bool fast = (hv == 64 || hv == 128 || hv == 256) &&
-                    (!gather || (pool->kv_heads - 1) * osh * eb + row_bytes <= (int64_t)UINT32_MAX) &&
-                    (tokens == 0 || (pool->kv_heads - 1) * sh * eb + row_bytes <= (int64_t)UINT32_MAX);
+  // The wave-uniform mapping needs whole 64-vector runs per wave and 32-bit offsets within a
+  // page, within a row's output ([seq_out, H, D] span) and within a row's input.
+  const auto span32 = [](int64_t n, int64_t stride, int64_t inner) {
+    return stride >= 0 && stride <= (int64_t)UINT32_MAX && (n - 1) * stride + inner <= (int64_t)UINT32_MAX;
+  };
+  const int64_t head_span_out = (pool->kv_heads - 1) * osh * eb + row_bytes;
+  const int64_t head_span_in = (pool->kv_heads - 1) * sh * eb + row_bytes;
+  const bool fast = (hv == 64 || hv == 128 || hv == 256) && P * tok_bytes <= (int64_t)UINT32_MAX &&
+                    (!gather || (osh * eb <= (int64_t)UINT32_MAX && span32(seq_out, oss * eb, head_span_out))) &&
+                    (tokens == 0 || (sh * eb <= (int64_t)UINT32_MAX && span32(tokens, st * eb, head_span_in)));
 
   StreamArgs a;
   a.pool = *pool;
@@ -1182,7 +1270,6 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   a.seq_from_device = (gather && (flags & BARQ_KV_SEQ_FROM_DEVICE)) ? 1 : 0;
   a.commit_in_kernel = (flags & BARQ_KV_SEPARATE_FINALIZE) ? 0 : 1;
   a.hv = (int32_t)hv;
-  a.rstep = fast ? (int32_t)(kThreads / hv) : 0;
   a.nsub = (int32_t)std::min<int64_t>(tiles, BARQ_KV_CTRL_SUBCOUNTERS);
   a.div_hv = FastDiv::make((uint32_t)hv);
   a.div_vr = FastDiv::make((uint32_t)vr);
@@ -1190,7 +1277,7 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   a.div_chunks = FastDiv::make((uint32_t)chunks);
 
   hipStream_t s = (hipStream_t)stream;
-  int rc = launch_stream_kernel(vb, fast, dim3((uint32_t)tiles), &a, s);
+  int rc = launch_stream_kernel(vb, fast ? (int)(hv / 64) : 0, dim3((uint32_t)tiles), &a, s);
   if (rc != BARQ_KV_OK) return rc;
   if (tokens > 0 && !a.commit_in_kernel) {
     barq_kv_pool pc = *pool;
