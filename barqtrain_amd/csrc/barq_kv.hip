@@ -44,6 +44,8 @@ constexpr int kTileTargetBytes = 64 * 1024;
 // 268 MB 53.4 -> 50.9 us), while a launch that is resident at once streams best from the
 // larger tiles (84 MB: 16.6 us at 64 KiB, 18.4 us at 32 KiB; ~1000 tiles: even).
 constexpr int64_t kLargeLaunchTiles = 1536;
+// Stream-kernel tiles (five-wave workgroups) resident on one CU at once.
+constexpr int64_t kResidentTilesPerCU = 4;
 
 template <int VB>
 struct VecT;
@@ -286,10 +288,14 @@ struct StreamArgs {
   int32_t commit_in_kernel;  // the launch commits its own append
   int32_t hv;        // vectors per token (kv_heads * vr)
   int32_t nsub;      // arrival sub-counters in use
+  int32_t full_tiles;  // tiles of `chunk` positions; the blocks after them are tail pieces
+  int32_t tail_lo;     // gather: first position of the tail
+  int32_t piece_len;   // gather: positions per tail piece
   FastDiv div_hv;    // by hv
   FastDiv div_vr;    // by vectors per head row
   FastDiv div_page;  // by page_size
   FastDiv div_chunks;
+  FastDiv div_pieces;  // by tail pieces per (row, K or V)
 };
 
 // LPP > 0: hv = 64 * LPP (LPP = 1, 2 or 4) and offsets within a page, a row's output and a row's
@@ -303,10 +309,27 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
   __shared__ int s_meta[6];                       // len, hw, lo, hi, blk_lo, last
 
   const barq_kv_pool& p = a.pool;
-  const int kv = blockIdx.x & 1;
-  const int rest = blockIdx.x >> 1;
-  const int b = (int)a.div_chunks.div((uint32_t)rest);
-  const int c = rest - b * (int)a.div_chunks.d;
+  // Block -> tile.  Blocks [0, full_tiles) are (K or V, row, chunk) tiles of `chunk` positions;
+  // a gather launch may follow them with tail pieces, (K or V, row, piece) of piece_len
+  // positions from tail_lo on, sized so that every CU receives the same work.
+  const int bid = (int)blockIdx.x;
+  const bool tail = bid >= a.full_tiles;
+  int kv, b, c;
+  if (!tail) {
+    kv = bid & 1;
+    const int rest = bid >> 1;
+    b = (int)a.div_chunks.div((uint32_t)rest);
+    c = rest - b * (int)a.div_chunks.d;
+  } else {
+    // Piece j of the tail: stream j / n, piece j mod n (n pieces per stream).
+    const int j = bid - a.full_tiles;
+    const int sid = (int)a.div_pieces.div((uint32_t)j);
+    c = j - sid * (int)a.div_pieces.d;
+    kv = sid & 1;
+    b = sid >> 1;
+  }
+  const int tlo = tail ? a.tail_lo + c * a.piece_len : c * a.chunk;
+  const int tlen = tail ? a.piece_len : a.chunk;
   const int T = a.tokens;
   const int P = (int)p.page_size;
   const int mb = (int)p.max_blocks;
@@ -325,8 +348,8 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
     const int len = p.seq_lens[b];
     const int hw = p.high_water[b];
     int pre = -1;
-    const int gb0 = c * a.ppt;
-    if (a.gather && lane < a.ppt && gb0 + lane < mb) pre = p.block_table[(int64_t)b * mb + gb0 + lane];
+    const int gb0 = (int)a.div_page.div((uint32_t)tlo);  // first block of a gather tile
+    if (a.gather && lane <= a.ppt && gb0 + lane < mb) pre = p.block_table[(int64_t)b * mb + gb0 + lane];
     int rl = 0, rh = 0;
     if (rows_in_lanes && lane < a.batch && (T > 0 || a.seq_from_device)) {
       rl = p.seq_lens[lane];
@@ -346,8 +369,8 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
     }
     int lo, hi;
     if (a.gather) {
-      lo = c * a.chunk;
-      hi = min(lo + a.chunk, smax);
+      lo = tlo;
+      hi = min(lo + tlen, smax);
     } else {
       lo = len + c * a.chunk;
       hi = min(lo + a.chunk, len + T);
@@ -443,7 +466,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
     constexpr int kSpan = RSTEP * kUnroll;  // positions one iteration of the workgroup covers
     if (wave > 0) {
       const int lane = (int)(threadIdx.x & (kWave - 1));
-      const int r0 = (wave - 1) / LPP;
+      const int r0 = __builtin_amdgcn_readfirstlane((wave - 1) / LPP);  // wave-uniform
       const int col = ((wave - 1) % LPP) * kWave + lane;
       const int h = (int)a.div_vr.div((uint32_t)col);
       const int v = col - h * (int)a.div_vr.d;
@@ -461,29 +484,45 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
       const int unpos = __builtin_amdgcn_readfirstlane(npos);
       const int ublk_lo = __builtin_amdgcn_readfirstlane(blk_lo);
       for (int j0 = r0; j0 < unpos; j0 += kSpan) {
+        const int nu = min(kUnroll, (unpos - j0 + RSTEP - 1) / RSTEP);  // positions in the tile
         const int sf = ulo + j0;                     // first position of this wave's iteration
-        const int sl = sf + (kUnroll - 1) * RSTEP;   // last
+        const int sl = sf + (nu - 1) * RSTEP;        // last
         const int bf = (int)a.div_page.div((uint32_t)sf);
+        const int bl = (int)a.div_page.div((uint32_t)sl);
+        const int64_t pb0 = __hip_readfirstlane(s_pbase[bf - ublk_lo]);
+        const int64_t pb1 = __hip_readfirstlane(s_pbase[min(bf + 1 - ublk_lo, kMaxTilePages)]);
+        const int64_t pb2 = __hip_readfirstlane(s_pbase[min(bf + 2 - ublk_lo, kMaxTilePages)]);
         V val[kUnroll];
-        if (j0 + (kUnroll - 1) * RSTEP < unpos && sl < ulen && (int)a.div_page.div((uint32_t)sl) <= bf + 1) {
-          // Interior iteration: every position inside the tile and written before this launch
-          // (s < seq_lens <= high_water), at most two pages.  Loads back to back, stores one at
-          // a time (a single-round launch drains HBM fastest with one store in flight per wave).
-          const int64_t pb0 = __hip_readfirstlane(s_pbase[bf - ublk_lo]);
-          const int64_t pb1 = __hip_readfirstlane(s_pbase[min(bf + 1 - ublk_lo, kMaxTilePages)]);
-          const int split = (bf + 1) * P;            // first position of the second page
+        if (bl <= bf + 2 && sl < max(uhw, ulen + T) && pb0 >= 0 && (bl < bf + 1 || pb1 >= 0) &&
+            (bl < bf + 2 || pb2 >= 0)) {
+          // Every position holds data (an earlier append, or a new token of this launch), on at
+          // most three mapped pages.  Branch-free loads, back to back: positions past the tile
+          // repeat the wave's last position (a cache hit) instead of branching, which would make
+          // the compiler wait for each load.  Stores go one at a time (a single-round launch
+          // drains HBM fastest with one store in flight per wave).
+          const int split1 = (bf + 1) * P;           // first position of the second page
+          const int split2 = split1 + P;             // and of the third
 #pragma unroll
           for (int u = 0; u < kUnroll; ++u) {
-            const int s = sf + u * RSTEP;
-            const bool second = s >= split;
-            const int64_t pb = second ? pb1 : pb0;
-            const uint32_t off = (uint32_t)(s - (second ? split : split - P)) * tokb;
-            val[u] = pb >= 0 ? ld_stream<V>((pages + pb + off) + page_lane) : zero_vec<V>();
+            const int s = sf + min(u, nu - 1) * RSTEP;
+            const int64_t pb = s >= split2 ? pb2 : (s >= split1 ? pb1 : pb0);
+            const int pstart = s >= split2 ? split2 : (s >= split1 ? split1 : split1 - P);
+            const bool fresh = (unsigned)(s - ulen) < (unsigned)T;
+            const char* base = fresh ? in_row + (uint32_t)(s - ulen) * ist : pages + pb + (uint32_t)(s - pstart) * tokb;
+            val[u] = ld_stream<V>(base + (fresh ? in_lane : page_lane));
           }
 #pragma unroll
           for (int u = 0; u < kUnroll; ++u) {
-            wait_vm<0>();
-            st_stream<V>((out_row + (uint32_t)(sf + u * RSTEP) * oss) + out_lane, val[u]);
+            if (u < nu) {
+              const int s = sf + u * RSTEP;
+              wait_vm<0>();
+              if (a.gather) st_stream<V>((out_row + (uint32_t)s * oss) + out_lane, val[u]);
+              if ((unsigned)(s - ulen) < (unsigned)T) {
+                const int64_t pb = s >= split2 ? pb2 : (s >= split1 ? pb1 : pb0);
+                const int pstart = s >= split2 ? split2 : (s >= split1 ? split1 : split1 - P);
+                *(V*)((pages + pb + (uint32_t)(s - pstart) * tokb) + page_lane) = val[u];
+              }
+            }
           }
           continue;
         }
@@ -1149,6 +1188,21 @@ bool pool_ok(const barq_kv_pool* p) {
   return true;
 }
 
+// Compute units of the current device (cached per device; 0 if the query fails).  Workgroups
+// are handed to CUs round-robin, so a launch of k * CUs equal tiles gives every CU k of them.
+int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static int cached[kMaxDevices];  // 0 = not queried yet
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 int launch(const void* fn, dim3 grid, void* arg, hipStream_t stream, int threads = kThreads) {
   void* args[] = {arg};
   return hipLaunchKernel(fn, grid, dim3(threads), args, 0, stream) == hipSuccess ? BARQ_KV_OK
@@ -1247,6 +1301,24 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
                     (!gather || (osh * eb <= (int64_t)UINT32_MAX && span32(seq_out, oss * eb, head_span_out))) &&
                     (tokens == 0 || (sh * eb <= (int64_t)UINT32_MAX && span32(tokens, st * eb, head_span_in)));
 
+  // A gather launch whose tiles are all resident at once ends when the CUs holding the most
+  // tiles finish (a CU streams at a roughly fixed rate).  When the tile count is not a multiple
+  // of the CU count, whole rounds of tiles are kept and the remaining positions of every
+  // (row, K or V) are cut into pieces, one per CU in total: every CU then gets the same work.
+  const int64_t rk = 2 * batch;  // (row, K or V) streams
+  int64_t full_tiles = tiles, tail_lo = 0, piece_len = 1, per_rk = 1, grid = tiles;
+  if (gather && fast) {
+    const int64_t ncu = device_cu_count();
+    if (ncu > 0 && ncu % rk == 0 && tiles > ncu && tiles % ncu != 0 && tiles <= kResidentTilesPerCU * ncu) {
+      per_rk = ncu / rk;
+      const int64_t full_chunks = (tiles / ncu) * per_rk;  // whole rounds of tiles
+      tail_lo = full_chunks * chunk;
+      piece_len = (span - tail_lo + per_rk - 1) / per_rk;  // <= chunk
+      full_tiles = rk * full_chunks;
+      grid = full_tiles + ncu;
+    }
+  }
+
   StreamArgs a;
   a.pool = *pool;
   a.in_k = (const char*)ks;
@@ -1270,14 +1342,18 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   a.seq_from_device = (gather && (flags & BARQ_KV_SEQ_FROM_DEVICE)) ? 1 : 0;
   a.commit_in_kernel = (flags & BARQ_KV_SEPARATE_FINALIZE) ? 0 : 1;
   a.hv = (int32_t)hv;
-  a.nsub = (int32_t)std::min<int64_t>(tiles, BARQ_KV_CTRL_SUBCOUNTERS);
+  a.nsub = (int32_t)std::min<int64_t>(grid, BARQ_KV_CTRL_SUBCOUNTERS);
   a.div_hv = FastDiv::make((uint32_t)hv);
   a.div_vr = FastDiv::make((uint32_t)vr);
   a.div_page = FastDiv::make((uint32_t)P);
-  a.div_chunks = FastDiv::make((uint32_t)chunks);
+  a.div_chunks = FastDiv::make((uint32_t)(full_tiles / rk));  // chunks per (row, K or V) in full tiles
+  a.full_tiles = (int32_t)full_tiles;
+  a.tail_lo = (int32_t)tail_lo;
+  a.piece_len = (int32_t)piece_len;
+  a.div_pieces = FastDiv::make((uint32_t)per_rk);
 
   hipStream_t s = (hipStream_t)stream;
-  int rc = launch_stream_kernel(vb, fast ? (int)(hv / 64) : 0, dim3((uint32_t)tiles), &a, s);
+  int rc = launch_stream_kernel(vb, fast ? (int)(hv / 64) : 0, dim3((uint32_t)grid), &a, s);
   if (rc != BARQ_KV_OK) return rc;
   if (tokens > 0 && !a.commit_in_kernel) {
     barq_kv_pool pc = *pool;
