@@ -302,7 +302,7 @@ struct StreamArgs {
 // input fit 32 bits.  A copy wave then moves whole positions, 64 vectors per load, so position,
 // block, page and output row are wave-uniform (scalar registers) and a lane's addresses differ
 // only by its column offset.  LPP = 0: any geometry.
-template <int VB, int LPP, int UNR, bool ROUNDS>
+template <int VB, int LPP, bool ROUNDS>
 __device__ __forceinline__ void stream_body(const StreamArgs& a) {
   using V = typename VecT<VB>::T;
   __shared__ int64_t s_pbase[kMaxTilePages + 1];  // byte offset of each block's page, or -1
@@ -510,10 +510,9 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
     // hv = 64 * LPP vectors per position, 32-bit offsets.  The four copy waves split a step of
     // RSTEP = 4 / LPP positions: wave w takes position (w - 1) / LPP of the step and column
     // block (w - 1) % LPP (vectors block * 64 + lane), so at every step the workgroup reads and
-    // writes RSTEP whole adjacent rows; a wave's UNR loads cover positions r0, r0 + RSTEP, ...
-    // (UNR = 16, or 8 for tiles of at most 8 * RSTEP positions).
+    // writes RSTEP whole adjacent rows; a wave's kUnroll loads cover positions r0, r0 + RSTEP, ...
     constexpr int RSTEP = 4 / LPP;
-    constexpr int kSpan = RSTEP * UNR;  // positions one iteration of the workgroup covers
+    constexpr int kSpan = RSTEP * kUnroll;  // positions one iteration of the workgroup covers
     if (wave > 0) {
       const int lane = (int)(threadIdx.x & (kWave - 1));
       const int r0 = __builtin_amdgcn_readfirstlane((wave - 1) / LPP);  // wave-uniform
@@ -534,7 +533,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
       const int unpos = __builtin_amdgcn_readfirstlane(npos);
       const int ublk_lo = __builtin_amdgcn_readfirstlane(blk_lo);
       for (int j0 = r0; j0 < unpos; j0 += kSpan) {
-        const int nu = min(UNR, (unpos - j0 + RSTEP - 1) / RSTEP);  // positions in the tile
+        const int nu = min(kUnroll, (unpos - j0 + RSTEP - 1) / RSTEP);  // positions in the tile
         const int sf = ulo + j0;                     // first position of this wave's iteration
         const int sl = sf + (nu - 1) * RSTEP;        // last
         const int bf = (int)a.div_page.div((uint32_t)sf);
@@ -551,9 +550,9 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
           // drains HBM fastest with one store in flight per wave).
           const int split1 = (bf + 1) * P;           // first position of the second page
           const int split2 = split1 + P;             // and of the third
-          V val[UNR];
+          V val[kUnroll];
 #pragma unroll
-          for (int u = 0; u < UNR; ++u) {
+          for (int u = 0; u < kUnroll; ++u) {
             const int s = sf + min(u, nu - 1) * RSTEP;
             const int64_t pb = s >= split2 ? pb2 : (s >= split1 ? pb1 : pb0);
             const int pstart = s >= split2 ? split2 : (s >= split1 ? split1 : split1 - P);
@@ -563,7 +562,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
           }
           wait_vm<0>();
 #pragma unroll
-          for (int u = 0; u < UNR; ++u) {
+          for (int u = 0; u < kUnroll; ++u) {
             if (u < nu) {
               const int s = sf + u * RSTEP;
               wait_vm<0>();
@@ -577,13 +576,13 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
           }
           continue;
         }
-        V val[UNR];
+        V val[kUnroll];
         // Boundary iteration: the tile's last positions, new tokens, positions never written
         // (zero), stale positions past seq_lens, or more than two pages (small page sizes).
-        // Taken in halves of UNR / 2 loads, which keeps the register footprint small.
+        // Taken in halves of kUnroll / 2 loads, which keeps the register footprint small.
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-          constexpr int kHalf = UNR / 2;
+          constexpr int kHalf = kUnroll / 2;
 #pragma unroll
           for (int k = 0; k < kHalf; ++k) {
             const int j = j0 + (half * kHalf + k) * RSTEP;
@@ -680,20 +679,20 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
 // The unit-mapped kernels hold 16 vectors per copy thread; five waves per SIMD keep four tiles
 // resident per CU (their few spills sit on the new-token path).  The generic kernel keeps the
 // compiler's register allocation.
-template <int VB, int LPP, int UNR>
+template <int VB, int LPP>
 __global__ void __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(5)))
 stream_kernel(const StreamArgs a) {
-  stream_body<VB, LPP, UNR, false>(a);
+  stream_body<VB, LPP, false>(a);
 }
 
 template <int VB, int LPP>
 __global__ void __launch_bounds__(kStreamThreads) stream_kernel_rounds(const StreamArgs a) {
-  stream_body<VB, LPP, kUnroll, true>(a);
+  stream_body<VB, LPP, true>(a);
 }
 
 template <int VB>
 __global__ void __launch_bounds__(kStreamThreads) stream_kernel_any(const StreamArgs a) {
-  stream_body<VB, 0, kUnroll, false>(a);
+  stream_body<VB, 0, false>(a);
 }
 
 __global__ void __launch_bounds__(kThreads) commit_kernel(const barq_kv_pool p, int batch,
@@ -1277,11 +1276,9 @@ int launch(const void* fn, dim3 grid, void* arg, hipStream_t stream, int threads
     }                                                                                           \
   }
 
-// `narrow`: 8 loads per copy thread and iteration (tiles of at most 8 * RSTEP positions);
-// `rounds`: the launch's tiles run in several rounds.  Both are built for 16-byte vectors only;
-// other widths take the 16-load single-round kernels.
-int launch_stream_kernel(int vb, int lpp, bool narrow, bool rounds, dim3 grid, StreamArgs* arg,
-                         hipStream_t stream) {
+// `rounds`: the launch's tiles run in several rounds (built for 16-byte vectors only; other
+// widths take the single-round kernels).
+int launch_stream_kernel(int vb, int lpp, bool rounds, dim3 grid, StreamArgs* arg, hipStream_t stream) {
 #define BARQ_STREAM_CASE(VB, KERNEL, ...)                                                                 \
     switch (lpp) {                                                                                        \
       case 1: return launch((const void*)&KERNEL<VB, 1, ##__VA_ARGS__>, grid, arg, stream, kStreamThreads); \
@@ -1293,15 +1290,13 @@ int launch_stream_kernel(int vb, int lpp, bool narrow, bool rounds, dim3 grid, S
     case 16:
       if (rounds) {
         BARQ_STREAM_CASE(16, stream_kernel_rounds)
-      } else if (narrow) {
-        BARQ_STREAM_CASE(16, stream_kernel, kUnroll / 2)
       } else {
-        BARQ_STREAM_CASE(16, stream_kernel, kUnroll)
+        BARQ_STREAM_CASE(16, stream_kernel)
       }
-    case 8: BARQ_STREAM_CASE(8, stream_kernel, kUnroll)
-    case 4: BARQ_STREAM_CASE(4, stream_kernel, kUnroll)
-    case 2: BARQ_STREAM_CASE(2, stream_kernel, kUnroll)
-    default: BARQ_STREAM_CASE(1, stream_kernel, kUnroll)
+    case 8: BARQ_STREAM_CASE(8, stream_kernel)
+    case 4: BARQ_STREAM_CASE(4, stream_kernel)
+    case 2: BARQ_STREAM_CASE(2, stream_kernel)
+    default: BARQ_STREAM_CASE(1, stream_kernel)
   }
 #undef BARQ_STREAM_CASE
 }
@@ -1419,12 +1414,10 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   a.div_pieces = FastDiv::make((uint32_t)per_rk);
 
   hipStream_t s = (hipStream_t)stream;
-  // Tiles of at most 8 steps of 4 / LPP positions take the narrow (8-load) kernel; launches
-  // with more tiles than the CUs hold at once take the kernel built for several rounds.
+  // Launches with more tiles than the CUs hold at once take the kernel built for several rounds.
   const int64_t ncu = device_cu_count();
   const bool rounds = fast && ncu > 0 && grid > kResidentTilesPerCU * ncu;
-  const bool narrow = fast && chunk * hv <= (int64_t)(kUnroll / 2) * 256;
-  int rc = launch_stream_kernel(vb, fast ? (int)(hv / 64) : 0, narrow, rounds, dim3((uint32_t)grid), &a, s);
+  int rc = launch_stream_kernel(vb, fast ? (int)(hv / 64) : 0, rounds, dim3((uint32_t)grid), &a, s);
   if (rc != BARQ_KV_OK) return rc;
   if (tokens > 0 && !a.commit_in_kernel) {
     barq_kv_pool pc = *pool;
