@@ -151,6 +151,49 @@ def staircase(lengths_desc):
     return calls
 
 
+@pytest.mark.parametrize("B,S", [(2, 2100), (8, 700), (16, 600), (32, 300)])
+def test_cu_balanced_tail_pieces(capi, B, S):
+    """Single-round gather launches whose tile count (2 * B * ceil(S / 32) at 8 KV heads x 128,
+    bf16, page 16) is not a multiple of the CU count cut their tail into one piece per CU.
+    Ragged rows (stale and zero-padded positions in the pieces), updates of 1 and 3 tokens, exact
+    extents and device-side extents over a larger output; positions past the longest row are
+    never written."""
+    H, D, P = 8, 128, 16
+    rng = np.random.default_rng(5000 + B)
+    lengths = sorted(rng.integers(S // 2, S + 1, size=B).tolist(), reverse=True)
+    lengths[0] = S
+    cap = S + 40
+    pool = make_pool(cap, B, H, D, P, torch.bfloat16)
+    oracle = DenseLayerOracle(B, cap, P)
+    gen = torch.Generator().manual_seed(B)
+    for b, t in staircase(lengths):
+        k = hf_layout(b, H, t, D, torch.bfloat16, gen)
+        v = hf_layout(b, H, t, D, torch.bfloat16, gen)
+        pool.append(k.cuda(), v.cuda())
+        oracle.append(to_bits(k), to_bits(v))
+    compare_layer(pool, oracle, None, f"B{B} prefill")
+    sentinel = torch.full((B, H, cap, D), -7.0, dtype=torch.bfloat16, device="cuda")
+    for step, t in enumerate([1, 3, 1, 1, 3]):
+        k = hf_layout(B, H, t, D, torch.bfloat16, gen)
+        v = hf_layout(B, H, t, D, torch.bfloat16, gen)
+        oracle.append(to_bits(k), to_bits(v))
+        seq = oracle.get_seq_length()
+        if step % 2:
+            ko, vo = sentinel.clone(), sentinel.clone()
+            pool.update(k.cuda(), v.cuda(), cap, SEQ_FROM_DEVICE, out=(ko, vo))
+            compare_layer(pool, oracle, (ko[:, :, :seq], vo[:, :, :seq]), f"B{B} step {step} device extent")
+            untouched = to_bits(sentinel[:, :, seq:])
+            assert_bits_equal(ko[:, :, seq:], untouched, f"B{B} step {step} K past the longest row")
+            assert_bits_equal(vo[:, :, seq:], untouched, f"B{B} step {step} V past the longest row")
+        else:
+            got = pool.update(k.cuda(), v.cuda(), seq)
+            compare_layer(pool, oracle, got, f"B{B} step {step}")
+    got = pool.gather(B, oracle.get_seq_length())
+    compare_layer(pool, oracle, got, f"B{B} gather")
+    pool.check_invariants()
+    assert pool.errors() == 0
+
+
 def test_config3_ragged_random_pages(capi):
     """B=64, context lengths U{128..4096}, pages handed out in a seeded random permutation:
     a non-contiguous block table; 1-token append + gather steps."""
