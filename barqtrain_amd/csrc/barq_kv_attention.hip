@@ -48,7 +48,9 @@ constexpr int kHeadDim = 128;              // the one head size this kernel is b
 constexpr int kSteps = kHeadDim / 32;      // k-steps of the score MFMA
 constexpr int kBlock = 16;                 // positions per chunk: one score MFMA's columns
 constexpr int kMaxRows = 16;               // query rows (G * T) one wave serves
-constexpr int kThreads = 256;              // workgroup of the merge kernel
+constexpr int kThreads = 256;              // workgroup of the merge kernel ...
+constexpr int kMergeWide = 1024;           // ... or this, for grids of fewer workgroups than
+constexpr int kMergeWideBelow = 256;       // this (the CUs of an MI355X)
 constexpr int kTableRegs = 4;              // block-table window: lanes x registers
 constexpr int kTableEntries = kTableRegs * 64;
 constexpr int kMaxBatch = 1024;            // rows whose lengths the schedule stages in LDS
@@ -246,22 +248,34 @@ __device__ __forceinline__ int table_lane(const int (&pt)[kTableRegs], int idx) 
 }
 
 // Block-table window of row b: lane j of pt[k] holds block blk0 + 64k + j, for the blocks
-// [blk0, blk_end) the piece reads.  An entry that names no page of the pool is recorded and read
-// as page 0, so no access leaves the pool.
+// [blk0, blk_end) the piece reads.  issue_table starts the loads; check_table, where the entries
+// are first needed, records an entry that names no page of the pool and reads it as page 0, so
+// no access leaves the pool.
+__device__ __forceinline__ void issue_table(const AttnArgs& a, int b, int blk0, int blk_end, int lane,
+                                            int (&pt)[kTableRegs]) {
+  const int n = min(kTableEntries, min(blk_end, a.max_blocks) - blk0);
+  const int32_t* row = a.block_table + (int64_t)b * a.max_blocks + blk0 + lane;
+#pragma unroll
+  for (int k = 0; k < kTableRegs; ++k) pt[k] = 64 * k + lane < n ? row[64 * k] : 0;
+}
+template <bool COLD>
+__device__ __forceinline__ void check_table(const AttnArgs& a, int (&pt)[kTableRegs]) {
+  bool bad = false;
+#pragma unroll
+  for (int k = 0; k < kTableRegs; ++k) {
+    const int page = pt[k];
+    const bool cold_ok = COLD && page <= -2 && -2 - page < a.num_cold;
+    const bool bad_k = (uint32_t)page >= (uint32_t)a.num_pages && !cold_ok;
+    pt[k] = bad_k ? 0 : page;
+    bad |= bad_k;
+  }
+  if (bad) atomicOr(a.errors, BARQ_KV_ERRBIT_BAD_INDEX);
+}
 template <bool COLD>
 __device__ __forceinline__ void load_table(const AttnArgs& a, int b, int blk0, int blk_end, int lane,
                                            int (&pt)[kTableRegs]) {
-  const int n = min(kTableEntries, min(blk_end, a.max_blocks) - blk0);
-#pragma unroll
-  for (int k = 0; k < kTableRegs; ++k) {
-    int page = 64 * k + lane < n ? a.block_table[(int64_t)b * a.max_blocks + blk0 + 64 * k + lane] : 0;
-    const bool cold_ok = COLD && page <= -2 && -2 - page < a.num_cold;
-    if ((uint32_t)page >= (uint32_t)a.num_pages && !cold_ok) {
-      atomicOr(a.errors, BARQ_KV_ERRBIT_BAD_INDEX);
-      page = 0;
-    }
-    pt[k] = page;
-  }
+  issue_table(a, b, blk0, blk_end, lane, pt);
+  check_table<COLD>(a, pt);
 }
 
 // K and V of one 16-position chunk for this lane.  K: lane (g, n16) holds dims 32 * step + 8 * g
@@ -480,26 +494,24 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
   const int M = a.rows;
   const int T = a.tokens;
 
-  // Query rows in the A layout of the score MFMA: lane (row n16, k-group g) holds dims
-  // 32 * step + 8 * g .. +7 of row n16 (zero for padding rows); kept in LDS.
-  {
-    u32x4 qv[kSteps];
-    if (n16 < M) {
-      const char* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(kvh * a.group + n16 / T) * a.q_sh +
-                       (int64_t)(n16 % T) * a.q_st + 16 * g;
-#pragma unroll
-      for (int st = 0; st < kSteps; ++st) qv[st] = *(const u32x4*)(qp + 64 * st);
-    } else {
-#pragma unroll
-      for (int st = 0; st < kSteps; ++st) qv[st] = u32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int st = 0; st < kSteps; ++st) lq[st][lane] = qv[st];
-  }
+  // The block-table window and the query rows load together: one round trip before the first
+  // chunk's loads.  Query rows in the A layout of the score MFMA: lane (row n16, k-group g) holds
+  // dims 32 * step + 8 * g .. +7 of row n16 (zero for padding rows); kept in LDS.
   int blk0 = (int)a.page_div.div((uint32_t)t_begin);
   const int blk_end = t_end > t_begin ? (int)a.page_div.div((uint32_t)(t_end - 1)) + 1 : blk0;
   int pt[kTableRegs];
-  load_table<COLD>(a, b, blk0, blk_end, lane, pt);
+  issue_table(a, b, blk0, blk_end, lane, pt);
+  {
+    u32x4 qv[kSteps];
+    const bool qrow = n16 < M;
+    const char* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(kvh * a.group + n16 / T) * a.q_sh +
+                     (int64_t)(n16 % T) * a.q_st + 16 * g;
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) qv[st] = qrow ? *(const u32x4*)(qp + 64 * st) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) lq[st][lane] = qv[st];
+  }
+  check_table<COLD>(a, pt);
 
   const char* kbase = a.kpages + (int64_t)kvh * a.head_bytes;
   const char* vbase = a.vpages + (int64_t)kvh * a.head_bytes;
@@ -593,32 +605,38 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
     }
   };
 
-  // Two register buffers: the next chunk's loads are in flight while this one is computed.
-  u32x4 ka[kSteps], va[4], kb[kSteps], vb[4];
-  bool cold_a = false, cold_b = false;  // the buffer holds codes and scales (wave-uniform)
+  // A ring of D register buffers: the next D - 1 chunks' loads are in flight while one is
+  // computed.  Two buffers: a third spills (or, for 4 query rows, runs slower) with the
+  // accumulators in registers.
+  constexpr int D = 2;
+  u32x4 kr[D][kSteps], vr[D][4];
+  bool cr[D];  // the buffer holds codes and scales (wave-uniform)
   int tc = t_begin;
-  if (tc < t_end) load(tc, ka, va, cold_a);
-  while (tc < t_end) {
-    if (tc + kBlock < t_end) load(tc + kBlock, kb, vb, cold_b);
-    __builtin_amdgcn_sched_barrier(0);
-    bool codes_a = false;
-    if (COLD && cold_a) {
-      codes_a = __builtin_amdgcn_ballot_w64(!chunk_scales_moderate(ka, va)) == 0;
-      if (!codes_a) dequant_chunk<E>(ka, va);
-    }
-    compute(tc, ka, va, codes_a);
-    tc += kBlock;
-    if (tc >= t_end) break;
-    if (tc + kBlock < t_end) load(tc + kBlock, ka, va, cold_a);
-    __builtin_amdgcn_sched_barrier(0);
-    bool codes_b = false;
-    if (COLD && cold_b) {
-      codes_b = __builtin_amdgcn_ballot_w64(!chunk_scales_moderate(kb, vb)) == 0;
-      if (!codes_b) dequant_chunk<E>(kb, vb);
-    }
-    compute(tc, kb, vb, codes_b);
-    tc += kBlock;
+#pragma unroll
+  for (int i = 0; i < D - 1; ++i) {
+    cr[i] = false;
+    if (tc + i * kBlock < t_end) load(tc + i * kBlock, kr[i], vr[i], cr[i]);
   }
+  cr[D - 1] = false;
+  if (tc < t_end) {
+    for (;;) {
+#pragma unroll
+      for (int i = 0; i < D; ++i) {
+        const int j = (i + D - 1) % D;
+        if (tc + (D - 1) * kBlock < t_end) load(tc + (D - 1) * kBlock, kr[j], vr[j], cr[j]);
+        __builtin_amdgcn_sched_barrier(0);
+        bool codes = false;
+        if (COLD && cr[i]) {
+          codes = __builtin_amdgcn_ballot_w64(!chunk_scales_moderate(kr[i], vr[i])) == 0;
+          if (!codes) dequant_chunk<E>(kr[i], vr[i]);
+        }
+        compute(tc, kr[i], vr[i], codes);
+        tc += kBlock;
+        if (tc >= t_end) goto chunks_done;
+      }
+    }
+  }
+chunks_done:
 
   // Row sums across the 16 lanes of each row group; P.V partials across the 4 position slots.
 #pragma unroll
@@ -702,20 +720,20 @@ void attention_flat_kernel(const AttnArgs a) {
   }
 }
 
-// Merge of one query row's records: one workgroup per (row, kv head, batch row).  Thread
-// (quad, class) folds the records class, class + 8, ... into a running (max, sum, 4 dims) --
-// every record load is independent -- and the 8 classes are folded through LDS.  Rows of
-// length 0 get zeros here; pairs inside one range were written by their wave.
-template <int E, typename OutT>
-__global__ __launch_bounds__(kThreads) void attention_merge_kernel(const AttnArgs a) {
+// Merge of one query row's records: one workgroup of NT threads per (row, kv head, batch row).
+// Thread (quad, class) folds the records class, class + NT / 32, ... into a running (max, sum,
+// 4 dims) -- every record load is independent -- and the classes are folded through LDS.  Rows
+// of length 0 get zeros here; pairs inside one range were written by their wave.
+template <int E, typename OutT, int NT>
+__global__ __launch_bounds__(NT) void attention_merge_kernel(const AttnArgs a) {
   constexpr int kQuads = kHeadDim / 4;
-  constexpr int kClasses = kThreads / kQuads;
+  constexpr int kClasses = NT / kQuads;
   __shared__ int s_len[kMaxBatch];
   __shared__ int s_incl[kMaxBatch];
   __shared__ int s_total;
-  __shared__ f32x4 po[kThreads];
-  __shared__ float pm[kThreads];
-  __shared__ float pl[kThreads];
+  __shared__ f32x4 po[NT];
+  __shared__ float pm[NT];
+  __shared__ float pl[NT];
 
   const int tid = threadIdx.x;
   const int row = blockIdx.x;
@@ -803,8 +821,13 @@ hipError_t launch_typed(AttnArgs a, bool merge, hipStream_t stream) {
   hipLaunchKernelGGL(k, dim3((unsigned)a.waves), dim3(kWave), 0, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || !merge) return err;
-  hipLaunchKernelGGL((attention_merge_kernel<E, OutT>), dim3((unsigned)a.rows, (unsigned)a.kv_heads, (unsigned)a.batch),
-                     dim3(kThreads), 0, stream, a);
+  // Fewer merge workgroups than CUs (few long pairs, many records each): 1024 threads each.
+  if ((int64_t)a.rows * a.kv_heads * a.batch < kMergeWideBelow)
+    hipLaunchKernelGGL((attention_merge_kernel<E, OutT, kMergeWide>),
+                       dim3((unsigned)a.rows, (unsigned)a.kv_heads, (unsigned)a.batch), dim3(kMergeWide), 0, stream, a);
+  else
+    hipLaunchKernelGGL((attention_merge_kernel<E, OutT, kThreads>), dim3((unsigned)a.rows, (unsigned)a.kv_heads, (unsigned)a.batch),
+                       dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 

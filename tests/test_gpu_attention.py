@@ -109,6 +109,15 @@ def test_llama3_8b_decode_shape():
     check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=4, out_f32=False)
 
 
+def test_long_row_many_records():
+    """One long row over 2 kv heads: the automatic schedule cuts each pair into ~1000 ranges, whose
+    records the merge launch folds with its wide workgroups (fewer merge workgroups than CUs)."""
+    lens = [12001]
+    pool, kd, vd, lens = make_rows(1, 2, 16, lens, torch.bfloat16, seed=77, order_seed=8)
+    check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=5)
+    check(pool, kd, vd, lens, 2, 3, torch.bfloat16, seed=6, out_f32=False)
+
+
 def test_empty_rows_and_closed_forms():
     """A row of length 0 (and one shorter than T) gives zeros; equal V rows give that row; a zero
     query gives the mean of V."""
