@@ -22,6 +22,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <atomic>
 #include <climits>
 
 #include "barq_kv.h"
@@ -1248,15 +1249,15 @@ bool pool_ok(const barq_kv_pool* p) {
 // are handed to CUs round-robin, so a launch of k * CUs equal tiles gives every CU k of them.
 int device_cu_count() {
   constexpr int kMaxDevices = 64;
-  static int cached[kMaxDevices];  // 0 = not queried yet
+  static std::atomic<int> cached[kMaxDevices];  // 0 = not queried yet; host threads may race here
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
-  if (cached[dev] == 0) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 int launch(const void* fn, dim3 grid, void* arg, hipStream_t stream, int threads = kThreads) {

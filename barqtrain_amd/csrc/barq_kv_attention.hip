@@ -30,6 +30,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 
 #include "barq_kv.h"
@@ -799,17 +800,22 @@ __global__ __launch_bounds__(NT) void attention_merge_kernel(const AttnArgs a) {
   }
 }
 
-// Resident waves of a kernel on the current device (cached per instantiation).
+// Resident waves of a kernel on the current device (cached per instantiation and device; host
+// threads may race on the cache, which only ever stores the one value a device gives).
 template <typename K>
 int resident_waves(K kernel) {
-  static int waves = 0;
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];  // 0 = not queried yet
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return kMaxWaves;
+  int waves = dev >= 0 && dev < kMaxDevices ? cached[dev].load(std::memory_order_relaxed) : 0;
   if (waves == 0) {
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kWave, 0) != hipSuccess)
       return kMaxWaves;
     waves = std::min(std::max(cus * per_cu, 1), kMaxWaves);
+    if (dev >= 0 && dev < kMaxDevices) cached[dev].store(waves, std::memory_order_relaxed);
   }
   return waves;
 }
