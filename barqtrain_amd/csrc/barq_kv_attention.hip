@@ -562,29 +562,28 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
         if (tc + n16 > len - T + row % T) x[r] = -INFINITY;
       }
     }
-    bool rescale = false;
     float alpha[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float mnew = fmaxf(m_run[r], row16_max(x[r]));
       const float mu = mnew == -INFINITY ? 0.f : mnew;
       alpha[r] = __builtin_amdgcn_exp2f(m_run[r] - mu);
-      rescale |= mnew != m_run[r];
       x[r] = __builtin_amdgcn_exp2f(x[r] - mu);
       l_part[r] = l_part[r] * alpha[r] + x[r];
       m_run[r] = mnew;
     }
     if (g < R) *(f32x4*)&lp[n16][4 * g] = f32x4{x[0], x[1], x[2], x[3]};
-    if (__builtin_amdgcn_ballot_w64(rescale)) {
+    // Every chunk rescales every row's accumulators (alpha is exactly 1 where a row's maximum did
+    // not move, so the values are those of rescaling only on change): with the multiply under a
+    // branch the compiler kept two copies of the accumulators live (8 and 16 query rows spilled).
 #pragma unroll
-      for (int r2 = 0; r2 < R; ++r2)
+    for (int r2 = 0; r2 < R; ++r2)
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const float al = lane_value(alpha[m], 16 * r2);
+      for (int m = 0; m < 4; ++m) {
+        const float al = lane_value(alpha[m], 16 * r2);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[r2][e][m] *= al;
-        }
-    }
+        for (int e = 0; e < 8; ++e) acc[r2][e][m] *= al;
+      }
     // P.V: lane 4b' + n of the 4x4x1 MFMA block b' takes position 4s + g of the chunk.
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
