@@ -155,19 +155,32 @@ class PagePool:
     def check_append(self, batch: int, tokens: int, max_length: Optional[int] = None) -> int:
         """Raise if appending would pass `max_length` (default: the block capacity) or drain the
         pool; return the number of pages the append takes."""
+        return self._plan_append(batch, tokens, max_length)[0]
+
+    def _plan_append(self, batch: int, tokens: int, max_length: Optional[int]) -> tuple[int, int]:
+        """check_append's work, returning (pages taken, longest row after the append).  Every
+        update passes here, so the arithmetic on the rows' shadow is kept to a few array ops
+        (each costs about a microsecond on a decode batch)."""
         limit = self.capacity if max_length is None else int(max_length)
         if batch > self.max_batch:
             raise ValueError("batch size exceeds the configured paged KV cache capacity")
-        if batch > 0 and tokens > 0:
-            ends = self.lens[:batch] + tokens
-            worst = int(ends.max())
-            if worst > limit or worst > self.capacity:
-                raise PagedKVCapacityError(
-                    f"paged KV cache capacity exceeded: requested {worst}, max_cache_len={limit}"
-                )
-        need = int(self.new_block_counts(batch, tokens).sum())
+        if batch <= 0 or tokens <= 0:
+            return 0, self.max_len(batch)
+        lens = self.lens[:batch]
+        worst = int(lens.max()) + tokens
+        if worst > limit or worst > self.capacity:
+            raise PagedKVCapacityError(
+                f"paged KV cache capacity exceeded: requested {worst}, max_cache_len={limit}"
+            )
+        # blocks mapped for the first time: min(ceil((len + T) / P), max_blocks) - ceil(hw / P)
+        P = self.page_size
+        end = lens + (tokens + P - 1)
+        end //= P
+        np.minimum(end, self.max_blocks, out=end)
+        end -= (self.hw[:batch] + (P - 1)) // P
+        need = int(np.maximum(end, 0, out=end).sum())
         self.ensure_free(need, "append")
-        return need
+        return need, worst
 
     def ensure_free(self, need: int, what: str) -> None:
         """Raise PagedKVPoolExhausted unless `need` pages are free.  After shared-page operations
@@ -184,8 +197,9 @@ class PagePool:
     def _advance(self, batch: int, tokens: int, need: int) -> None:
         if batch <= 0 or tokens <= 0:
             return
-        self.lens[:batch] += tokens
-        np.maximum(self.hw[:batch], self.lens[:batch], out=self.hw[:batch])
+        lens, hw = self.lens[:batch], self.hw[:batch]
+        lens += tokens
+        np.maximum(hw, lens, out=hw)
         self.free_count -= need
 
     def max_len(self, batch: int) -> int:
@@ -259,11 +273,10 @@ class PagePool:
         """Append, then materialise rows [0, batch) up to the longest row, in one pass."""
         self._check_states(key_states, value_states)
         batch, _, tokens, _ = key_states.shape
-        need = self.check_append(batch, tokens, max_length)
+        need, worst = self._plan_append(batch, tokens, max_length)
         if tokens == 0:
             return self.gather(batch, seq_out, out, flags)
-        ends = self.lens[:batch] + tokens
-        seq = int(ends.max()) if seq_out is None else int(seq_out)
+        seq = worst if seq_out is None else int(seq_out)
         ko, vo = out if out is not None else self._new_out(batch, seq)
         k, v = self._compatible_pair(key_states, value_states)
         self._ops().pool_update_(self.tensors, k, v, ko, vo, seq, flags)
