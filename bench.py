@@ -7,7 +7,7 @@ one decode step of the cache: for every layer, append 1 token per row and materi
 contiguous [B, H, seq, D] K and V (ctx 513 -> 768 over the 256 steps).  Inputs are N(0, 1) in
 fp32 rounded to the cache dtype from a seeded generator and already resident in HBM.
 
-`--config 1..5` selects the five configurations of BASELINE.json (C1 tiny plumbing, C2
+`--config 1..5` selects the five benchmark configurations (C1 tiny plumbing, C2
 Llama-3-8B decode, C3 fragmented ragged batch with a random page permutation, C4 32k chunked
 prefill, C5 80-layer 70B-class share with the pool at 90 % occupancy and seeded row churn).
 
@@ -604,7 +604,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1. The cache path "
-                                   "shards by sequence, KV head or layer with no collective (see DESIGN.md)."}))
+                                   "would shard by sequence, KV head or layer, with no collective on it."}))
         sys.exit(2)
     import torch
 
