@@ -116,6 +116,8 @@ def test_long_row_many_records():
     pool, kd, vd, lens = make_rows(1, 2, 16, lens, torch.bfloat16, seed=77, order_seed=8)
     check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=5)
     check(pool, kd, vd, lens, 2, 3, torch.bfloat16, seed=6, out_f32=False)
+    check(pool, kd, vd, lens, 16, 1, torch.bfloat16, seed=7)    # 16 query rows per kv head
+    check(pool, kd, vd, lens, 8, 2, torch.bfloat16, seed=8, split_tokens=48)  # fixed short ranges
 
 
 def test_empty_rows_and_closed_forms():
