@@ -172,11 +172,11 @@ class PagePool:
             raise PagedKVCapacityError(
                 f"paged KV cache capacity exceeded: requested {worst}, max_cache_len={limit}"
             )
-        # blocks mapped for the first time: min(ceil((len + T) / P), max_blocks) - ceil(hw / P)
+        # blocks mapped for the first time: ceil((len + T) / P) - ceil(hw / P) where positive (no
+        # row passes max_blocks: worst <= capacity was checked above)
         P = self.page_size
         end = lens + (tokens + P - 1)
         end //= P
-        np.minimum(end, self.max_blocks, out=end)
         end -= (self.hw[:batch] + (P - 1)) // P
         need = int(np.maximum(end, 0, out=end).sum())
         self.ensure_free(need, "append")
