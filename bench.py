@@ -69,7 +69,8 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "paged KV append+gather GB/s (% HBM peak); µs per decode-step cache update"
-KERNEL = "stream_kernel<16, 2> (fused append + gather, one launch per layer)"
+KERNEL = ("stream_kernel<16, 2> (fused append + gather, one launch per layer; launches of more than 4 tiles "
+          "per CU, as at C3-C5, run its stream_kernel_rounds<16, 2> instantiation)")
 
 # prefill: ("uniform", n) | ("ragged", lo, hi, seed) | ("chunks", count, size)
 CONFIGS = {
