@@ -340,29 +340,31 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
   // control wave's lanes, one row per lane.
   const bool early = committing && rows_in_lanes;
 
-  int c_len = 0, c_hw = 0, c_top = 0;
-
   if (threadIdx.x < kWave) {
     const int lane = threadIdx.x;
-    // One round of independent loads: this row, the tile's block-table slice (gather tiles are
-    // block aligned), every row's metadata (batch <= kWave) and the stack top.
+    // One round of independent loads: this row's length and mark (uniform: scalar cache) and the
+    // tile's block-table slice (gather tiles are block aligned).  Batch-wide values -- the longest
+    // row, the rank of this row's new blocks -- are read only by the tiles that need them: every
+    // tile reading the same lines of seq_lens / high_water at once serialises those reads on one
+    // L2 channel (at C2 about 1.5 us of a 15 us launch).
     const int len = p.seq_lens[b];
     const int hw = p.high_water[b];
     int pre = -1;
     const int gb0 = (int)a.div_page.div((uint32_t)tlo);  // first block of a gather tile
     if (a.gather && lane <= a.ppt && gb0 + lane < mb) pre = p.block_table[(int64_t)b * mb + gb0 + lane];
-    int rl = 0, rh = 0;
-    if (rows_in_lanes && lane < a.batch && (T > 0 || a.seq_from_device)) {
-      rl = p.seq_lens[lane];
-      rh = p.high_water[lane];
-    }
-    const int top = T > 0 ? p.ctrl[BARQ_KV_CTRL_FREE_TOP] : 0;
-
+    int rl = 0, rh = 0;  // lane r < batch: row r's length and mark, once loaded
+    bool rows_loaded = false;
     int smax = a.seq_out;
-    if (a.seq_from_device) {
+    // A gather tile reaching past its own row's end (capped by the buffer) needs the longest row.
+    if (a.gather && a.seq_from_device && tlo + tlen > min(len + T, a.seq_out)) {
       int m = 0;
       if (rows_in_lanes) {
-        if (lane < a.batch) m = rl + T;
+        if (lane < a.batch) {
+          rl = p.seq_lens[lane];
+          rh = p.high_water[lane];
+          m = rl + T;
+        }
+        rows_loaded = true;
       } else {
         for (int r = lane; r < a.batch; r += kWave) m = max(m, p.seq_lens[r] + T);
       }
@@ -383,9 +385,14 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
     }
     const NewBlocks nb = new_blocks(len, hw, T, mb, a.div_page);
     const bool touches_new = nb.count > 0 && blk_lo < nb.first + nb.count && blk_lo + nblk > nb.first;
-    int base = 0;
+    int base = 0, top = 0;
     if (touches_new) {
+      top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
       if (rows_in_lanes) {
+        if (!rows_loaded && lane < a.batch) {
+          rl = p.seq_lens[lane];
+          rh = p.high_water[lane];
+        }
         base = wave_sum(lane < b ? new_blocks(rl, rh, T, mb, a.div_page).count : 0);
       } else {
         base = wave_rank_base(p, b, T, a.div_page);
@@ -416,9 +423,6 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
       s_meta[3] = hi;
       s_meta[4] = blk_lo;
     }
-    c_len = rl;
-    c_hw = rh;
-    c_top = top;
   }
   __syncthreads();
 
@@ -426,8 +430,6 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
     // Control wave.  Every metadata value this tile uses was read before the barrier, so the
     // tile arrives now, and the copy waves never wait for the arrival or the commit.
     const int lane = threadIdx.x;
-    const int fidx = c_top - 1 - lane;  // the page that the lane-th new block takes
-    const int c_free = fidx >= 0 ? p.free_pages[fidx] : -1;
     int last = 0;
     if (lane == 0) {
       const int nsub = a.nsub;
@@ -440,6 +442,17 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
       }
     }
     if (__builtin_amdgcn_readfirstlane(last)) {
+      // Every tile has read the metadata it uses and only this wave writes it in this launch, so
+      // the commit inputs read now are the launch's starting state: lane r holds row r's length
+      // and mark, lane k the page the k-th new block takes.
+      int c_len = 0, c_hw = 0;
+      if (lane < a.batch) {
+        c_len = p.seq_lens[lane];
+        c_hw = p.high_water[lane];
+      }
+      const int c_top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
+      const int fidx = c_top - 1 - lane;
+      const int c_free = fidx >= 0 ? p.free_pages[fidx] : -1;
       commit_from_lanes(p, a.batch, T, a.gather ? a.seq_out : INT_MAX, a.div_page, c_len, c_hw, c_top, c_free);
       if (lane == 0) atomicExch(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 0);
     }
@@ -694,6 +707,183 @@ __global__ void __launch_bounds__(kStreamThreads) stream_kernel_rounds(const Str
 template <int VB>
 __global__ void __launch_bounds__(kStreamThreads) stream_kernel_any(const StreamArgs a) {
   stream_body<VB, 0, false>(a);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Lean gather / update: launches whose tiles of one or two pages are all resident at once
+// (batch <= 64, whole-row geometry, 16-byte vectors).  Every copy wave reads its own tile's
+// metadata -- the row's length and mark, the block-table entries of the tile's blocks -- with
+// uniform loads, served by the scalar cache, and starts streaming without LDS staging; batch-wide
+// values (the longest row, the rank of a row's new blocks) are read only by the tiles that need
+// them.  Wave 0 only counts the tile as arrived, after a barrier that follows every copy wave's
+// metadata loads, and in the last tile to arrive commits the append.  Measured at the C2 shape
+// against the control-wave kernel above (gather at context 520..760): 1-page tiles 13.2-14.9 us
+// against 14.8-16.3 us while at most five tiles per CU exist, 2-page tiles 14.6-17.0 us against
+// 16.0-18.0 us beyond.
+// ---------------------------------------------------------------------------------------------
+
+// Lean tiles resident on one CU: five at up to 8 vectors per copy thread (<= 64 VGPRs), four at
+// 16 (75 VGPRs: six waves per SIMD).
+constexpr int64_t kLeanResidentTilesPerCU = 5;
+constexpr int64_t kLeanResidentTilesPerCU16 = 4;
+
+// NU: vectors per copy thread (positions per tile / (4 / LPP)); tiles are whole pages, at most two.
+template <int NU, int LPP>
+__global__ void __launch_bounds__(kStreamThreads) lean_stream_kernel(const StreamArgs a) {
+  using V = typename VecT<16>::T;
+  constexpr int RSTEP = 4 / LPP;
+  const barq_kv_pool& p = a.pool;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+  const int lane = (int)(threadIdx.x & (kWave - 1));
+  const int bid = (int)blockIdx.x;
+  const int kv = bid & 1;
+  const int rest = bid >> 1;
+  const int b = (int)a.div_chunks.div((uint32_t)rest);
+  const int c = rest - b * (int)a.div_chunks.d;
+  const int T = a.tokens;
+  const int P = (int)p.page_size;
+  const int mb = (int)p.max_blocks;
+  const bool committing = T > 0 && a.commit_in_kernel;
+
+  if (wave == 0) {
+    if (!committing) return;
+    __syncthreads();  // every copy wave of the tile holds the metadata it uses
+    int last = 0;
+    if (lane == 0) {
+      const int nsub = a.nsub;
+      const int sub = bid % nsub;
+      const int expect = ((int)gridDim.x - sub + nsub - 1) / nsub;
+      int* counter = &p.ctrl[BARQ_KV_CTRL_SUBCOUNTER0 + sub * BARQ_KV_CTRL_SUBCOUNTER_STRIDE];
+      if (atomicAdd(counter, 1) == expect - 1) {
+        atomicExch(counter, 0);
+        last = atomicAdd(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 1) == nsub - 1;
+      }
+    }
+    if (__builtin_amdgcn_readfirstlane(last)) {
+      // Every tile has read its metadata and only this wave writes metadata in this launch, so
+      // what it reads now is the launch's starting state.
+      int c_len = 0, c_hw = 0;
+      if (lane < a.batch) {
+        c_len = p.seq_lens[lane];
+        c_hw = p.high_water[lane];
+      }
+      const int c_top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
+      const int fidx = c_top - 1 - lane;
+      const int c_free = fidx >= 0 ? p.free_pages[fidx] : -1;
+      commit_from_lanes(p, a.batch, T, a.seq_out, a.div_page, c_len, c_hw, c_top, c_free);
+      if (lane == 0) atomicExch(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 0);
+    }
+    return;
+  }
+
+  // Copy waves.  Tile (K or V, row b, chunk c): positions [c * chunk, + chunk), blocks blk0 and,
+  // for two-page tiles, blk0 + 1 (< max_blocks: the grid covers seq_out <= capacity).
+  const int len = p.seq_lens[b];
+  const int hw = p.high_water[b];
+  const int blk0 = c * a.ppt;
+  const int e0 = p.block_table[(int64_t)b * mb + blk0];
+  int e1 = -1;
+  if (a.ppt > 1 && blk0 + 1 < mb) e1 = p.block_table[(int64_t)b * mb + blk0 + 1];
+  const int lo = c * a.chunk;
+  int hi = lo + a.chunk;
+  if (hi > min(len + T, a.seq_out)) {
+    // Positions past this row's end: the output extent is the longest row (or seq_out).
+    int smax = a.seq_out;
+    if (a.seq_from_device) smax = min(wave_max(lane < a.batch ? p.seq_lens[lane] + T : 0), a.seq_out);
+    hi = min(hi, smax);
+  }
+  const NewBlocks nb = new_blocks(len, hw, T, mb, a.div_page);
+  const int nbl = a.ppt > 1 ? 2 : 1;
+  int base = 0, top = 0;
+  if (nb.count > 0 && blk0 < nb.first + nb.count && blk0 + nbl > nb.first) {
+    // The tile holds new blocks: their pages are ranked after the new blocks of rows [0, b).
+    top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
+    base = wave_sum(lane < b ? new_blocks(p.seq_lens[lane], p.high_water[lane], T, mb, a.div_page).count : 0);
+  }
+  int64_t pbs[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int blk = blk0 + k;
+    int page = -1;
+    if (k < nbl && blk < mb) {
+      if (blk < nb.first) {
+        page = checked_page(k == 0 ? e0 : e1, p.num_pages);
+      } else if (blk < nb.first + nb.count) {
+        const int idx = top - 1 - (base + blk - nb.first);
+        page = idx >= 0 ? checked_page(p.free_pages[idx], p.num_pages) : -1;
+      }
+    }
+    pbs[k] = page >= 0 ? (int64_t)page * a.page_bytes : (int64_t)-1;
+  }
+  const int64_t pb0 = pbs[0], pb1 = pbs[1];
+  if (committing) {
+    __builtin_amdgcn_s_waitcnt(0);  // the metadata loads have returned before the tile arrives
+    __syncthreads();
+  }
+  if (hi <= lo) return;
+
+  const int cw = wave - 1;
+  const int r0 = cw / LPP;
+  const int col = (cw % LPP) * kWave + lane;
+  const int h = (int)a.div_vr.div((uint32_t)col);
+  const int v = col - h * (int)a.div_vr.d;
+  const uint32_t page_lane = (uint32_t)(col * 16);
+  const uint32_t out_lane = (uint32_t)((int64_t)h * a.out_sh + (int64_t)v * 16);
+  const uint32_t in_lane = (uint32_t)((int64_t)h * a.in_sh + (int64_t)v * 16);
+  const uint32_t tokb = (uint32_t)a.tok_bytes;
+  const uint32_t oss = (uint32_t)a.out_ss;
+  const uint32_t ist = (uint32_t)a.in_st;
+  const char* in_row = (kv ? a.in_v : a.in_k) + (int64_t)b * a.in_sb;
+  char* out_row = (kv ? a.out_v : a.out_k) + (int64_t)b * a.out_sb;
+  char* pages = (char*)(kv ? p.value_pages : p.key_pages);
+  const int nval = hi - lo;
+  V val[NU];
+  if (hi <= max(hw, len + T) && pb0 >= 0 && (nval <= P || pb1 >= 0)) {
+    // Every position holds data on mapped pages: branch-free loads, back to back (positions past
+    // the tile repeat its last one, a cache hit).
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int j = min(r0 + u * RSTEP, nval - 1);
+      const int s = lo + j;
+      const bool second = j >= P;
+      const char* page_pos = pages + (second ? pb1 : pb0) + (uint32_t)(second ? j - P : j) * tokb;
+      const bool fresh = (unsigned)(s - len) < (unsigned)T;
+      val[u] = ld_stream<V>(fresh ? in_row + (uint32_t)(s - len) * ist + in_lane : page_pos + page_lane);
+    }
+  } else {
+    // Zero padding, unmapped blocks (an exhausted pool) or positions never written.
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int j = r0 + u * RSTEP;
+      const int s = lo + j;
+      val[u] = zero_vec<V>();
+      if (j < nval) {
+        const bool second = j >= P;
+        const int64_t pb = second ? pb1 : pb0;
+        if ((unsigned)(s - len) < (unsigned)T) {
+          val[u] = ld_stream<V>(in_row + (uint32_t)(s - len) * ist + in_lane);
+        } else if (s < hw && pb >= 0) {
+          val[u] = ld_stream<V>(pages + pb + (uint32_t)(second ? j - P : j) * tokb + page_lane);
+        }
+      }
+    }
+  }
+  wait_vm<0>();
+  // One store in flight per wave: a single-round launch drains HBM fastest that way.
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int j = r0 + u * RSTEP;
+    if (j < nval) {
+      const int s = lo + j;
+      wait_vm<0>();
+      st_stream<V>(out_row + (uint32_t)s * oss + out_lane, val[u]);
+      if ((unsigned)(s - len) < (unsigned)T) {
+        const bool second = j >= P;
+        const int64_t pb = second ? pb1 : pb0;
+        if (pb >= 0) *(V*)(pages + pb + (uint32_t)(second ? j - P : j) * tokb + page_lane) = val[u];
+      }
+    }
+  }
 }
 
 __global__ void __launch_bounds__(kThreads) commit_kernel(const barq_kv_pool p, int batch,
@@ -1302,6 +1492,21 @@ int launch_stream_kernel(int vb, int lpp, bool rounds, dim3 grid, StreamArgs* ar
 #undef BARQ_STREAM_CASE
 }
 
+int launch_lean_kernel(int nu, int lpp, dim3 grid, StreamArgs* arg, hipStream_t stream) {
+#define BARQ_LEAN_CASE(NU)                                                                               \
+    switch (lpp) {                                                                                        \
+      case 1: return launch((const void*)&lean_stream_kernel<NU, 1>, grid, arg, stream, kStreamThreads);  \
+      case 2: return launch((const void*)&lean_stream_kernel<NU, 2>, grid, arg, stream, kStreamThreads);  \
+      default: return launch((const void*)&lean_stream_kernel<NU, 4>, grid, arg, stream, kStreamThreads); \
+    }
+  switch (nu) {
+    case 4: BARQ_LEAN_CASE(4)
+    case 8: BARQ_LEAN_CASE(8)
+    default: BARQ_LEAN_CASE(16)
+  }
+#undef BARQ_LEAN_CASE
+}
+
 BARQ_DEFINE_VB_LAUNCH(dense_append_kernel, DenseArgs)
 BARQ_DEFINE_VB_LAUNCH(copy_rows_kernel, CopyArgs)
 BARQ_DEFINE_VB_LAUNCH(select_build_kernel, SelectArgs)
@@ -1337,21 +1542,8 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   const int64_t vr = row_bytes / vb;
   const int64_t hv = pool->kv_heads * vr;
 
-  // Positions per tile: whole pages, about kTileTargetBytes of each of K and V.
   const int64_t P = pool->page_size;
-  int64_t pages_per_tile = kTileTargetBytes / (P * tok_bytes);
-  if (pages_per_tile < 1) pages_per_tile = 1;
-  if (pages_per_tile > kMaxTilePages) pages_per_tile = kMaxTilePages;
-  // An append tile starts at an arbitrary slot, so its `chunk` positions touch at most
-  // pages_per_tile + 1 blocks: s_pbase holds kMaxTilePages + 1.
   const int64_t span = gather ? seq_out : tokens;
-  if (pages_per_tile > 1 && 2 * batch * ((span + pages_per_tile * P - 1) / (pages_per_tile * P)) > kLargeLaunchTiles)
-    pages_per_tile /= 2;
-  const int64_t chunk = pages_per_tile * P;
-  if (chunk * hv > kI32Max - (int64_t)kThreads * kUnroll) return BARQ_KV_ERR_INVALID;
-  const int64_t chunks = (span + chunk - 1) / chunk;
-  const int64_t tiles = 2 * batch * chunks;
-  if (tiles > kI32Max) return BARQ_KV_ERR_INVALID;
   // The wave-uniform mapping needs whole 64-vector runs per wave and 32-bit offsets within a
   // page, within a row's output ([seq_out, H, D] span) and within a row's input.
   const auto span32 = [](int64_t n, int64_t stride, int64_t inner) {
@@ -1362,15 +1554,47 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   const bool fast = (hv == 64 || hv == 128 || hv == 256) && P * tok_bytes <= (int64_t)UINT32_MAX &&
                     (!gather || (osh * eb <= (int64_t)UINT32_MAX && span32(seq_out, oss * eb, head_span_out))) &&
                     (tokens == 0 || (sh * eb <= (int64_t)UINT32_MAX && span32(tokens, st * eb, head_span_in)));
+  const int64_t ncu = device_cu_count();
 
-  // A gather launch whose tiles are all resident at once ends when the CUs holding the most
-  // tiles finish (a CU streams at a roughly fixed rate).  When the tile count is not a multiple
-  // of the CU count, whole rounds of tiles are kept and the remaining positions of every
-  // (row, K or V) are cut into pieces, one per CU in total: every CU then gets the same work.
+  // Lean kernel: a gather launch whose tiles of one page -- else two -- are all resident at once.
+  const int64_t lpp = hv / 64;
+  int64_t lean_ppt = 0, lean_nu = 0;
+  if (gather && fast && vb == 16 && batch <= kWave && ncu > 0) {
+    for (int64_t q = 1; q <= 2 && lean_ppt == 0; ++q) {
+      if ((q * P * lpp) % 4 != 0) continue;  // whole steps of 4 / LPP positions
+      const int64_t nu = q * P * lpp / 4;
+      if (nu != 4 && nu != 8 && nu != 16) continue;
+      const int64_t resident = nu == 16 ? kLeanResidentTilesPerCU16 : kLeanResidentTilesPerCU;
+      if (2 * batch * ((span + q * P - 1) / (q * P)) <= resident * ncu) {
+        lean_ppt = q;
+        lean_nu = nu;
+      }
+    }
+  }
+
+  // Positions per tile: whole pages, about kTileTargetBytes of each of K and V.
+  int64_t pages_per_tile = kTileTargetBytes / (P * tok_bytes);
+  if (pages_per_tile < 1) pages_per_tile = 1;
+  if (pages_per_tile > kMaxTilePages) pages_per_tile = kMaxTilePages;
+  // An append tile starts at an arbitrary slot, so its `chunk` positions touch at most
+  // pages_per_tile + 1 blocks: s_pbase holds kMaxTilePages + 1.
+  if (pages_per_tile > 1 && 2 * batch * ((span + pages_per_tile * P - 1) / (pages_per_tile * P)) > kLargeLaunchTiles)
+    pages_per_tile /= 2;
+  if (lean_ppt > 0) pages_per_tile = lean_ppt;
+  const int64_t chunk = pages_per_tile * P;
+  if (chunk * hv > kI32Max - (int64_t)kThreads * kUnroll) return BARQ_KV_ERR_INVALID;
+  const int64_t chunks = (span + chunk - 1) / chunk;
+  const int64_t tiles = 2 * batch * chunks;
+  if (tiles > kI32Max) return BARQ_KV_ERR_INVALID;
+
+  // A gather launch of the control-wave kernel whose tiles are all resident at once ends when the
+  // CUs holding the most tiles finish (a CU streams at a roughly fixed rate).  When the tile
+  // count is not a multiple of the CU count, whole rounds of tiles are kept and the remaining
+  // positions of every (row, K or V) are cut into pieces, one per CU in total: every CU then
+  // gets the same work.
   const int64_t rk = 2 * batch;  // (row, K or V) streams
   int64_t full_tiles = tiles, tail_lo = 0, piece_len = 1, per_rk = 1, grid = tiles;
-  if (gather && fast) {
-    const int64_t ncu = device_cu_count();
+  if (gather && fast && lean_ppt == 0) {
     if (ncu > 0 && ncu % rk == 0 && tiles > ncu && tiles % ncu != 0 && tiles <= kResidentTilesPerCU * ncu) {
       per_rk = ncu / rk;
       const int64_t full_chunks = (tiles / ncu) * per_rk;  // whole rounds of tiles
@@ -1416,9 +1640,9 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
 
   hipStream_t s = (hipStream_t)stream;
   // Launches with more tiles than the CUs hold at once take the kernel built for several rounds.
-  const int64_t ncu = device_cu_count();
   const bool rounds = fast && ncu > 0 && grid > kResidentTilesPerCU * ncu;
-  int rc = launch_stream_kernel(vb, fast ? (int)(hv / 64) : 0, rounds, dim3((uint32_t)grid), &a, s);
+  int rc = lean_ppt > 0 ? launch_lean_kernel((int)lean_nu, (int)lpp, dim3((uint32_t)grid), &a, s)
+                        : launch_stream_kernel(vb, fast ? (int)(hv / 64) : 0, rounds, dim3((uint32_t)grid), &a, s);
   if (rc != BARQ_KV_OK) return rc;
   if (tokens > 0 && !a.commit_in_kernel) {
     barq_kv_pool pc = *pool;
