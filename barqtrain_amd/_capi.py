@@ -79,6 +79,8 @@ _SIGNATURES = {
     "barq_kv_attention_workspace_bytes": (c_i64, [ctypes.POINTER(BarqKVPool)] + [c_i64] * 5),
     "barq_kv_decode_attention": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_ptr] + [c_i64] * 6 + [c_ptr]
                                  + [c_i64] * 3 + [ctypes.c_float] + [c_i64] * 3 + [c_ptr, c_i64, c_ptr]),
+    "barq_kv_decode_attention_noalloc": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_ptr] + [c_i64] * 6 + [c_ptr]
+                                         + [c_i64] * 3 + [ctypes.c_float] + [c_i64] * 3 + [c_ptr]),
     "barq_kv_cold_reset": (ctypes.c_int, [_POOL, _COLD, c_ptr]),
     "barq_kv_compress": (ctypes.c_int, [_POOL, _COLD, c_i64, c_ptr]),
     "barq_kv_gather_cold": (ctypes.c_int, [_POOL, _COLD, c_ptr, c_ptr] + [c_i64] * 6 + [c_ptr]),

@@ -1667,6 +1667,7 @@ const char* barq_kv_status_string(int status) {
     case BARQ_KV_OK: return "ok";
     case BARQ_KV_ERR_INVALID: return "invalid argument (pointer, size, stride or alignment)";
     case BARQ_KV_ERR_LAUNCH: return "HIP kernel launch failed";
+    case BARQ_KV_ERR_SCRATCH: return "request exceeds the static scratch (BARQ_KV_SCRATCH_BYTES per GPU)";
     default: return "unknown status";
   }
 }

@@ -1014,6 +1014,36 @@ int barq_kv_decode_attention(const barq_kv_pool* pool, const void* query, int64_
                           workspace_bytes, stream);
 }
 
+// Workspace of barq_kv_decode_attention_noalloc: one static array per GPU.  Host code never
+// passes `scratch` itself (in host code the name is a stand-in, not a device address); the
+// kernels get the address hipGetSymbolAddress resolves on each device.
+static __device__ __align__(256) unsigned char scratch[BARQ_KV_SCRATCH_BYTES];
+
+int barq_kv_decode_attention_noalloc(const barq_kv_pool* pool, const void* query, int64_t batch,
+                                     int64_t q_heads, int64_t tokens, int64_t q_stride_b,
+                                     int64_t q_stride_h, int64_t q_stride_t, void* out,
+                                     int64_t out_stride_b, int64_t out_stride_h,
+                                     int64_t out_stride_t, float scale, int64_t max_seq,
+                                     int64_t split_tokens, int64_t flags, void* stream) {
+  AttnPlan plan;
+  const int rc = plan_attention(pool, batch, q_heads, tokens, max_seq, split_tokens, &plan);
+  if (rc != BARQ_KV_OK) return rc;
+  if (plan.bytes > BARQ_KV_SCRATCH_BYTES) return BARQ_KV_ERR_SCRATCH;
+  // The array's address on the current device, resolved on the first call there.
+  constexpr int kMaxDevices = 64;
+  static std::atomic<void*> addr[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return BARQ_KV_ERR_LAUNCH;
+  void* ptr = addr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return BARQ_KV_ERR_LAUNCH;
+    addr[dev].store(ptr, std::memory_order_release);
+  }
+  return decode_attention(pool, nullptr, query, batch, q_heads, tokens, q_stride_b, q_stride_h, q_stride_t, out,
+                          out_stride_b, out_stride_h, out_stride_t, scale, max_seq, split_tokens, flags, ptr,
+                          BARQ_KV_SCRATCH_BYTES, stream);
+}
+
 int barq_kv_decode_attention_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, const void* query,
                                   int64_t batch, int64_t q_heads, int64_t tokens, int64_t q_stride_b,
                                   int64_t q_stride_h, int64_t q_stride_t, void* out, int64_t out_stride_b,

@@ -54,6 +54,8 @@ extern "C" {
 #define BARQ_KV_OK 0
 #define BARQ_KV_ERR_INVALID 1 /* a pointer, size, stride or alignment the kernels cannot take */
 #define BARQ_KV_ERR_LAUNCH 2  /* the HIP runtime refused a launch */
+#define BARQ_KV_ERR_SCRATCH 3 /* the request needs more than the library's static scratch
+                                 (BARQ_KV_SCRATCH_BYTES per GPU); use the workspace variant */
 
 /* Words of barq_kv_pool.ctrl.  Counters sit on lines of their own; all counters are 0 between
    launches. */
@@ -269,6 +271,29 @@ int barq_kv_decode_attention(const barq_kv_pool* pool, const void* query, int64_
                              int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_t,
                              float scale, int64_t max_seq, int64_t split_tokens, int64_t flags,
                              void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Bytes of the static device scratch behind barq_kv_decode_attention_noalloc (per GPU). */
+#define BARQ_KV_SCRATCH_BYTES (16 * 1024 * 1024)
+
+/*
+ * No counterpart in the reference.  For callers that cannot allocate device memory -- code under
+ * HIP graph capture, a serving loop that forbids hipMalloc, harnesses that count allocations --:
+ * barq_kv_decode_attention with the workspace taken from a static device array of the library
+ * (BARQ_KV_SCRATCH_BYTES on each GPU it runs on, held until the process ends) instead of an
+ * argument.  Arguments, results and errors as barq_kv_decode_attention; a launch whose workspace
+ * (barq_kv_attention_workspace_bytes) exceeds BARQ_KV_SCRATCH_BYTES returns BARQ_KV_ERR_SCRATCH
+ * and enqueues nothing (16 MiB holds every batch <= 64 with 8 KV heads, G * tokens <= 16 and the
+ * automatic split).  The workspace needs no initialisation, so calls clear nothing.  Every call on
+ * a GPU uses that GPU's one array: calls that overlap on one GPU (other streams, other host
+ * threads) race on it; order them on one stream.  The first call on a device resolves the array's
+ * address there; the call allocates nothing.
+ */
+int barq_kv_decode_attention_noalloc(const barq_kv_pool* pool, const void* query, int64_t batch,
+                                     int64_t q_heads, int64_t tokens, int64_t q_stride_b,
+                                     int64_t q_stride_h, int64_t q_stride_t, void* out,
+                                     int64_t out_stride_b, int64_t out_stride_h,
+                                     int64_t out_stride_t, float scale, int64_t max_seq,
+                                     int64_t split_tokens, int64_t flags, void* stream);
 
 /*
  * ---- Quantised KV pages (fp8), no reference counterpart: the reference plans "quantized KV-cache
