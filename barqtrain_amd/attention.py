@@ -4,10 +4,14 @@ implementation (``"barq_paged"``).
 A ``BarqPagedKVCache`` built with ``fused_attention=True`` appends in ``update`` and returns, in
 place of materialised K/V, zero-stride views that name their cache layer.  The attention
 function registered here finds the layer on the key view and, for decode (``G * T <= 16`` query
-rows per kv head, no padding mask), runs the pool's decode-attention kernel: softmax(Q K^T) V
-is computed from the pages through the block table, so the per-step gather of the whole history
-(and its write and re-read) disappears.  Prefill and padded batches take the gathered K/V and an
-fp32 attention; calls without a paged cache go to transformers' SDPA path.
+rows per kv head, no padding mask, head_dim 128), runs the pool's decode-attention kernel:
+softmax(Q K^T) V is computed from the pages through the block table, so the per-step gather of
+the whole history (and its write and re-read) disappears.  Prefill, padded batches and other
+head sizes take the gathered K/V through torch's fused SDPA kernels (flash or memory-efficient,
+grouped-query heads without copies, bottom-right causal); host tensors, and shapes no fused
+kernel takes, an fp32 attention.  Calls without a paged cache go to transformers' SDPA path.
+Options the paged path does not implement (logit soft-capping, attention sinks, sliding
+windows, dropout) raise instead of being ignored.
 
 The kernel's numbers are fp32 throughout (scores from exact bf16/fp16 products, fp32 softmax and
 P.V), so logits track an fp32 reference more closely than the default bf16 attention does.
@@ -19,6 +23,7 @@ import math
 from typing import Optional
 
 import torch
+import torch.nn.functional as F
 
 ATTN_IMPLEMENTATION = "barq_paged"
 _KERNEL_MAX_ROWS = 16
@@ -57,6 +62,46 @@ def _fp32_attention(query, key, value, attention_mask, scale):
     return torch.matmul(probs, v).transpose(1, 2).contiguous().to(query.dtype)
 
 
+def _sdpa_attention(query, key, value, attention_mask, scale):
+    """Fused SDPA over gathered K/V (q [B, Hq, T, D], k/v [B, Hkv, S, D]) with the same masking
+    as _fp32_attention; returns [B, T, Hq, D], or None when no fused kernel takes the shapes.
+    Only the flash and memory-efficient kernels are allowed: the math fallback runs batched
+    bf16 products over transposed views."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    from torch.nn.attention.bias import causal_lower_right
+
+    T, S = query.shape[2], key.shape[2]
+    if attention_mask is None:
+        mask = causal_lower_right(T, S) if T > 1 else None
+    elif attention_mask.dtype == torch.bool:
+        mask = attention_mask[..., :S]
+    else:
+        mask = attention_mask[..., :S].to(query.dtype)
+    group = query.shape[1] // key.shape[1]
+    # Grouped heads natively where a kernel takes them (ROCm's fused kernels do not with a mask),
+    # else K/V expanded to the query heads.
+    attempts = (True, False) if attention_mask is None else (False,)
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        for gqa in attempts:
+            k, v = (key, value) if gqa or group == 1 else (key.repeat_interleave(group, 1),
+                                                         value.repeat_interleave(group, 1))
+            try:
+                out = F.scaled_dot_product_attention(query, k, v, attn_mask=mask, scale=scale,
+                                                     enable_gqa=gqa and group > 1)
+            except RuntimeError:
+                continue
+            return out.transpose(1, 2).contiguous()
+    return None
+
+
+def _gathered_attention(query, key, value, attention_mask, scale):
+    if query.is_cuda and query.dtype in (torch.bfloat16, torch.float16):
+        out = _sdpa_attention(query, key, value, attention_mask, scale)
+        if out is not None:
+            return out
+    return _fp32_attention(query, key, value, attention_mask, scale)
+
+
 def paged_attention_forward(module: torch.nn.Module, query: torch.Tensor, key: torch.Tensor,
                             value: torch.Tensor, attention_mask: Optional[torch.Tensor],
                             scaling: Optional[float] = None, dropout: float = 0.0, **kwargs):
@@ -67,6 +112,13 @@ def paged_attention_forward(module: torch.nn.Module, query: torch.Tensor, key: t
 
         return sdpa_attention_forward(module, query, key, value, attention_mask, scaling=scaling,
                                       dropout=dropout, **kwargs)
+    unsupported = [name for name in ("softcap", "s_aux", "sliding_window") if kwargs.get(name) is not None]
+    if dropout:
+        unsupported.append("dropout")
+    if unsupported:
+        raise NotImplementedError(
+            f"barq_paged attention does not implement {', '.join(unsupported)}; use another attention "
+            "implementation (the paged cache works with any: create_paged_kv_cache(..., fused_attention=False))")
     pool = layer.pool
     _, q_heads, tokens, head_dim = query.shape
     scale = scaling if scaling is not None else 1.0 / math.sqrt(head_dim)
@@ -77,7 +129,7 @@ def paged_attention_forward(module: torch.nn.Module, query: torch.Tensor, key: t
     if kernel_ok:
         return pool.attend(query, scale).transpose(1, 2), None
     k, v = layer.current_tensors()
-    return _fp32_attention(query, k, v, attention_mask, scale), None
+    return _gathered_attention(query, k, v, attention_mask, scale), None
 
 
 def register() -> str:

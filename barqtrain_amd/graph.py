@@ -71,6 +71,10 @@ class CapturedDecodeStep:
             bucket = max(64, -(-self.capacity // 16))
         self.bucket = int(bucket) if bucket else self.capacity
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        # Captured launches hold the pools' device pointers: a pool whose tensors are replaced
+        # (PagePool.to) bumps its generation, and the graphs are captured again.
+        self._generations = [p.generation for p in self.pools]
+        self._device = p0.key_pages.device
 
     def _graph(self, extent: int, compress: bool = False) -> torch.cuda.CUDAGraph:
         """The graph whose launches cover output positions [0, extent), captured on first use
@@ -99,6 +103,12 @@ class CapturedDecodeStep:
         Raises, before anything runs, if any layer would pass its capacity or run out of pages."""
         B, T = self.batch, self.tokens
         p0 = self.pools[0]
+        generations = [p.generation for p in self.pools]
+        if generations != self._generations:
+            if any(p.key_pages.device != self._device for p in self.pools):
+                raise ValueError("a pool of this captured step left its device; capture a new step")
+            self.graphs.clear()
+            self._generations = generations
         lens = self._lens[:, :B]
         hw = self._hw[:, :B]
         ends = lens + T

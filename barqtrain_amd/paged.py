@@ -289,6 +289,13 @@ class PagePool:
         max_length = max(int(max_length), 0)
         if batch <= 0:
             return
+        if self.shared:
+            # Room for the identity selection below, from the lengths after the crop, before
+            # anything changes: every tail block (re-opened for writing) may need a copy.
+            lens = self.lens.copy()
+            np.minimum(lens[:batch], max_length, out=lens[:batch])
+            nb = np.minimum(-(-self.hw // self.page_size), self.max_blocks)
+            self.ensure_free(int((nb - np.minimum(lens // self.page_size, nb)).sum()), "crop")
         self._ops().pool_crop_(self.tensors, batch, max_length)
         np.minimum(self.lens[:batch], max_length, out=self.lens[:batch])
         if self.shared:
@@ -346,8 +353,10 @@ class PagePool:
         return rows
 
     def _selected(self, lens: np.ndarray, hw: np.ndarray, need: int) -> None:
-        """Host shadow after a selection: the new rows' lengths and marks (other rows empty)."""
-        self.lens, self.hw = lens, hw
+        """Host shadow after a selection: the new rows' lengths and marks (other rows empty).
+        Written in place: a captured decode step keeps views of these arrays."""
+        self.lens[:] = lens
+        self.hw[:] = hw
         self.free_count -= need
         self.free_exact = False   # moves, copies and released pages are settled on the device
         self.shared = True
@@ -555,6 +564,9 @@ class QuantPagePool(PagePool):
         self._check_states(key_states, value_states)
         batch, _, tokens, _ = key_states.shape
         if tokens > self.chunk:
+            # Every chunk's capacity, hot-page and cold-page needs are checked up front, so an
+            # append that cannot finish raises before its first chunk changes anything.
+            self._check_chunked(batch, tokens, max_length)
             for s0 in range(0, tokens, self.chunk):
                 self.append(key_states[:, :, s0:s0 + self.chunk], value_states[:, :, s0:s0 + self.chunk],
                             max_length)
@@ -569,6 +581,45 @@ class QuantPagePool(PagePool):
         ops.pool_compress_(self.tensors, self.cold_tensors, self.window, batch)
         self._advance(batch, tokens, need)
         self._quantised(batch, frontier, moved)
+
+    def _check_chunked(self, batch: int, tokens: int, max_length: Optional[int]) -> None:
+        """Raise, changing nothing, unless appending `tokens` to rows [0, batch) in chunks of
+        `chunk` fits: the same capacity rule, hot-page and cold-page arithmetic each chunk's
+        append and quantisation apply, run on a copy of the host shadow."""
+        limit = self.capacity if max_length is None else int(max_length)
+        if batch > self.max_batch:
+            raise ValueError("batch size exceeds the configured paged KV cache capacity")
+        if batch <= 0 or tokens <= 0:
+            return
+        lens = self.lens[:batch].copy()
+        hw = self.hw[:batch].copy()
+        cold = self.cold_blocks[:batch].copy()
+        worst = int(lens.max()) + tokens
+        if worst > limit or worst > self.capacity:
+            raise PagedKVCapacityError(
+                f"paged KV cache capacity exceeded: requested {worst}, max_cache_len={limit}")
+        if not self.free_exact:  # a lower bound: read the device's count once
+            self.free_count = int(self.ctrl[CTRL_FREE_TOP].item())
+            self.free_exact = True
+        free, cold_free, P = self.free_count, self.cold_free, self.page_size
+        for s0 in range(0, tokens, self.chunk):
+            t = min(self.chunk, tokens - s0)
+            end = np.minimum(-(-(lens + t) // P), self.max_blocks)
+            need = int(np.maximum(end - (-(-hw // P)), 0).sum())
+            if need > free:
+                raise PagedKVPoolExhausted(
+                    f"paged KV page pool exhausted: append needs {need} pages at token {s0}, {free} free")
+            free -= need
+            lens += t
+            np.maximum(hw, lens, out=hw)
+            frontier = np.maximum(lens - self.window, 0) // P
+            moved = int(np.maximum(frontier - cold, 0).sum())
+            if moved > cold_free:
+                raise PagedKVPoolExhausted(
+                    f"paged KV cold store exhausted: quantising needs {moved} pages, {cold_free} free")
+            np.maximum(cold, frontier, out=cold)
+            cold_free -= moved
+            free += moved
 
     def gather(self, batch: int, seq_out: Optional[int] = None,
                out: Optional[tuple[torch.Tensor, torch.Tensor]] = None,

@@ -116,3 +116,19 @@ def test_generate_on_fp8_quantised_pages_tracks_full_precision():
     assert all(int(layer.pool.cold_blocks.min()) >= 14 for layer in cache.layers)
     assert (seq[:, 40:] == ref_seq[:, 40:]).float().mean() >= 0.9
     assert ((logits - ref_logits).norm() / ref_logits.norm()) < 0.05
+
+
+def test_paged_route_rejects_options_it_does_not_implement():
+    """Logit soft-capping, attention sinks, sliding windows and dropout raise on the paged route
+    instead of being dropped (a model with them would otherwise change its logits silently)."""
+    import types
+
+    from barqtrain_amd import attention
+
+    layer = types.SimpleNamespace(pool=None)
+    q = torch.zeros(1, 4, 1, 8)
+    k = torch.zeros(1, 2, 3, 8)
+    k._barq_paged_layer = layer
+    for kw in ({"softcap": 30.0}, {"s_aux": torch.zeros(4)}, {"sliding_window": 4096}, {"dropout": 0.1}):
+        with pytest.raises(NotImplementedError):
+            attention.paged_attention_forward(None, q, k, k, None, **kw)

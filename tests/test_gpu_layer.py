@@ -204,6 +204,8 @@ def test_paged_attention_decode_in_a_model(hip, monkeypatch):
 
     def run(kernel: bool):
         monkeypatch.setattr(attention, "_KERNEL_MAX_ROWS", 16 if kernel else 0)
+        # the reference attention is the fp32 one, not the fused bf16 SDPA the route takes
+        monkeypatch.setattr(attention, "_sdpa_attention", lambda *a: None)
         cache = create_paged_kv_cache(model, max_batch_size=3, max_cache_len=prompt + new, page_size=16)
         steps = []
         with torch.no_grad():
@@ -224,10 +226,129 @@ def test_paged_attention_decode_in_a_model(hip, monkeypatch):
     assert err <= 0.02 * scale, f"logits differ by {err} (scale {scale})"
     assert (fused.argmax(-1) == reference.argmax(-1)).float().mean().item() >= 0.9
 
-    monkeypatch.setattr(attention, "_KERNEL_MAX_ROWS", 16)
+    monkeypatch.undo()
     monkeypatch.setenv("BARQTRAIN_PAGED_KV_MIN_CACHE_LEN", "0")
     patch_inference(model, paged_attention=True)
     out = model.generate(seq[:, :prompt], attention_mask=torch.ones_like(seq[:, :prompt]), max_new_tokens=8,
                          do_sample=False)
     assert model._barqtrain_last_generate_used_paged_kv is True
     assert out.shape == (3, prompt + 8)
+
+
+def test_graph_recaptured_after_pool_tensors_move(hip):
+    """A captured step whose pool is moved off the GPU and back (PagePool.to: new device
+    tensors) captures its graphs again instead of replaying launches on the freed memory."""
+    from barqtrain_amd.graph import CapturedDecodeStep
+    from barqtrain_amd.paged import PagePool
+
+    L, B, H, D, P, prefill, steps = 2, 3, 8, 128, 16, 20, 8
+    cap = prefill + steps
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator().manual_seed(9)
+    pools = [PagePool(max_batch=B, max_blocks=-(-cap // P), page_size=P, kv_heads=H, head_dim=D,
+                      dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    oracles = [DenseLayerOracle(B, cap, P) for _ in range(L)]
+    for pool, oracle in zip(pools, oracles):
+        k = hf_layout(B, H, prefill, D, torch.bfloat16, gen)
+        pool.update(k.to(dev), k.to(dev))
+        oracle.update(to_bits(k), to_bits(k))
+    kin = torch.zeros((L, B, H, 1, D), dtype=torch.bfloat16, device=dev)
+    step = CapturedDecodeStep(pools, B, 1, inputs=(kin, kin))
+    for s in range(steps):
+        if s == steps // 2:
+            torch.cuda.synchronize()
+            pools[1].to("cpu")
+            torch.cuda.synchronize()
+            pools[1].to(dev)
+            torch.cuda.synchronize()
+        ks = [hf_layout(B, H, 1, D, torch.bfloat16, gen) for _ in range(L)]
+        for layer in range(L):
+            kin[layer].copy_(ks[layer].to(dev))
+        outs = step.replay()
+        torch.cuda.synchronize()
+        for layer in range(L):
+            ok, ov = oracles[layer].update(to_bits(ks[layer]), to_bits(ks[layer]))
+            assert_bits(outs[layer][0], ok, f"replay {s} layer {layer} K")
+            assert_bits(pools[layer].gather(B)[1], ov, f"replay {s} layer {layer} V (eager gather)")
+    assert all(p.errors() == 0 for p in pools)
+
+
+def small_head_llama(seed=0):
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    torch.manual_seed(seed)
+    # head_dim 64 with 4 query heads over 2 kv heads: the reference's benchmark model
+    # (Qwen2-0.5B) has head_dim 64, which the decode kernel does not take
+    cfg = LlamaConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=1024,
+                      pad_token_id=0, eos_token_id=None)
+    return LlamaForCausalLM(cfg).to(torch.bfloat16).eval(), cfg
+
+
+def test_paged_route_head_dim_64_and_padded_batch(hip, monkeypatch):
+    """The "barq_paged" route for shapes the decode kernel does not take -- head_dim 64, and a
+    left-padded batch (a mask) -- runs torch's fused SDPA over the gathered K/V.  Against the same
+    route with the fp32 attention (a reference free of bf16 batched products): prefill logits
+    agree to bf16 rounding and greedy tokens agree."""
+    pytest.importorskip("transformers")
+    from barqtrain import create_paged_kv_cache
+    from barqtrain_amd import attention
+
+    model, cfg = small_head_llama()
+    model = model.to("cuda")
+    attention.enable_paged_attention(model)
+    ids = torch.randint(1, 512, (3, 29), generator=torch.Generator().manual_seed(6)).to("cuda")
+    mask = torch.ones_like(ids)
+    mask[1, :5] = 0  # row 1 left-padded
+    mask[2, :11] = 0
+    new = 16
+    sdpa = attention._sdpa_attention
+    fused = []
+
+    def decode(use_sdpa: bool):
+        monkeypatch.setattr(attention, "_sdpa_attention",
+                            (lambda *a: fused.append(1) or sdpa(*a)) if use_sdpa else (lambda *a: None))
+        cache = create_paged_kv_cache(model, max_batch_size=3, max_cache_len=29 + new, page_size=16)
+        out = model.generate(ids, attention_mask=mask, max_new_tokens=new, do_sample=False, past_key_values=cache,
+                             return_dict_in_generate=True, output_logits=True)
+        assert all(layer.pool.errors() == 0 for layer in cache.layers)
+        return out.sequences, torch.stack(out.logits).float()
+
+    seq, logits = decode(True)
+    assert len(fused) >= cfg.num_hidden_layers * new, "every attention call ran fused SDPA"
+    ref_seq, ref_logits = decode(False)
+    scale = ref_logits[0].abs().max().item()
+    assert (logits[0] - ref_logits[0]).abs().max().item() <= 0.02 * scale
+    assert (seq == ref_seq).float().mean().item() >= 0.9
+
+
+def test_long_prefill_stays_within_memory(hip):
+    """A 16k-token prefill of one row through the paged route: attention over the gathered K/V
+    runs in fused SDPA (no [heads, T, S] score tensor: that would be 32 GiB in fp32); the last
+    query rows match an fp32 attention computed for those rows alone."""
+    from barqtrain_amd import attention
+    from barqtrain_amd.kv_cache import BarqPagedKVCacheLayer
+
+    T, Hkv, G, D = 16384, 8, 4, 128
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(4)
+    layer = BarqPagedKVCacheLayer(max_batch_size=1, max_cache_len=T, page_size=32)
+    k = torch.randn((1, T, Hkv, D), generator=gen, device=dev).to(torch.bfloat16).transpose(1, 2)
+    v = torch.randn((1, T, Hkv, D), generator=gen, device=dev).to(torch.bfloat16).transpose(1, 2)
+    q = torch.randn((1, T, G * Hkv, D), generator=gen, device=dev).to(torch.bfloat16).transpose(1, 2)
+    kk, vv = layer.update(k, v)
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    out = attention._gathered_attention(q, kk, vv, None, D ** -0.5)  # [1, T, Hq, D]
+    torch.cuda.synchronize()
+    assert torch.cuda.max_memory_allocated() - base < 2 * 2**30
+    rows = 16
+    qs = q[:, :, -rows:].float()
+    sc = torch.matmul(qs, kk.float().repeat_interleave(G, 1).transpose(-1, -2).contiguous()) * D ** -0.5
+    pos = torch.arange(T, device=dev)
+    limit = T - rows + torch.arange(rows, device=dev)
+    sc = sc.masked_fill(pos[None, :] > limit[:, None], float("-inf"))
+    ref = torch.matmul(torch.softmax(sc, -1), vv.float().repeat_interleave(G, 1)).transpose(1, 2)
+    err = (out[:, -rows:].float() - ref).abs().max().item()
+    assert err <= 2.0 ** -7 * ref.abs().max().item() + 1e-3, err
