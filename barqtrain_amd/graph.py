@@ -98,6 +98,15 @@ class CapturedDecodeStep:
             self.graphs[(extent, compress)] = graph
         return graph
 
+    def prepare(self, longest_rows) -> None:
+        """Capture now the graphs of the steps whose longest row (after the append) takes the
+        given values, so that no replay of them captures (capture costs milliseconds)."""
+        for worst in longest_rows:
+            extent = min(self.capacity, -(-int(worst) // self.bucket) * self.bucket)
+            self._graph(extent, False)
+            if any(self.quantized):
+                self._graph(extent, True)
+
     def replay(self) -> list[tuple[torch.Tensor, torch.Tensor]]:
         """Run one captured step; returns each layer's (K, V) views ``[batch, H, seq, D]``.
         Raises, before anything runs, if any layer would pass its capacity or run out of pages."""

@@ -249,6 +249,42 @@ class PagePool:
         self._ops().pool_append_(self.tensors, k, v)
         self._advance(batch, tokens, need)
 
+    def append_rows(self, rows: Sequence[int], key_states: torch.Tensor, value_states: torch.Tensor,
+                    max_length: Optional[int] = None) -> None:
+        """Append ``key_states[i]`` / ``value_states[i]`` to row ``rows[i]`` (distinct rows, not
+        necessarily [0, batch)): a freed row takes a new sequence's prefill while the others keep
+        decoding.  Checked in full first (capacity, free pages), then one append launch per row
+        over the one-row view of the row metadata -- the same kernels, sharing the free stack,
+        so pages come off it in the order of `rows`."""
+        self._check_states(key_states, value_states)
+        rows = [int(r) for r in rows]
+        if len(rows) != key_states.shape[0]:
+            raise ValueError("append_rows: one row index per batch entry of the states")
+        if len(set(rows)) != len(rows):
+            raise ValueError("append_rows: rows must be distinct")
+        if any(r < 0 or r >= self.max_batch for r in rows):
+            raise IndexError("append_rows: row out of range")
+        tokens = key_states.shape[2]
+        if not rows or tokens == 0:
+            return
+        r = np.asarray(rows)
+        limit = self.capacity if max_length is None else int(max_length)
+        worst = int(self.lens[r].max()) + tokens
+        if worst > limit or worst > self.capacity:
+            raise PagedKVCapacityError(f"paged KV cache capacity exceeded: requested {worst}, max_cache_len={limit}")
+        P = self.page_size
+        need = int(np.maximum(-(-(self.lens[r] + tokens) // P) - (-(-self.hw[r] // P)), 0).sum())
+        self.ensure_free(need, "append_rows")
+        k, v = self._compatible_pair(key_states, value_states)
+        t = self.tensors
+        ops = self._ops()
+        for i, row in enumerate(rows):
+            one = t[:2] + [t[2][row:row + 1], t[3][row:row + 1], t[4][row:row + 1]] + t[5:]
+            ops.pool_append_(one, k[i:i + 1], v[i:i + 1])
+        self.lens[r] += tokens
+        self.hw[r] = np.maximum(self.hw[r], self.lens[r])
+        self.free_count -= need
+
     def _new_out(self, batch: int, seq: int) -> tuple[torch.Tensor, torch.Tensor]:
         shape = (batch, self.kv_heads, seq, self.head_dim)
         return (torch.empty(shape, dtype=self.dtype, device=self.device),
@@ -687,6 +723,9 @@ class QuantPagePool(PagePool):
 
         return {"hot_pages": size(self.tensors[:2]), "cold_store": size(self.cold_tensors[:4]),
                 "metadata": size(self.tensors[2:]) + size(self.cold_tensors[4:])}
+
+    def append_rows(self, rows, key_states, value_states, max_length=None) -> None:
+        raise NotImplementedError("append_rows is not available on a pool with quantised (fp8) pages")
 
     def select_rows(self, src_rows: Sequence[int]) -> None:
         raise NotImplementedError("beam selection is not available on a pool with quantised (fp8) pages")

@@ -2,33 +2,44 @@
 """Benchmark of the paged KV-cache hot path on one MI355X.
 
 Workload (default, configuration 2 -- the Llama-3-8B KV shape): 32 layers, batch 16, 8 KV heads x
-128, bf16, page 16.  Every row is prefilled with 512 tokens (untimed), then each timed step is
-one decode step of the cache: for every layer, append 1 token per row and materialise the whole
-contiguous [B, H, seq, D] K and V (ctx 513 -> 768 over the 256 steps).  Inputs are N(0, 1) in
-fp32 rounded to the cache dtype from a seeded generator and already resident in HBM.
+128, bf16, page 16.  Every row is prefilled with 512 tokens (untimed), then the configuration's
+trajectory is 256 decode steps of the cache: for every layer, append 1 token per row and
+materialise the whole contiguous [B, H, seq, D] K and V (ctx 513 -> 768).  `--steps K` times K
+consecutive steps of that trajectory: all of it for K >= 256 (the default), else the K steps
+centred in it -- reached by running the steps before them untimed after the prefill -- so that
+the timed steps move the trajectory's mean bytes per step; the first K steps are reported beside
+them (`first_steps`).  Inputs are N(0, 1) in fp32 rounded to the cache dtype from a seeded
+generator and already resident in HBM.
 
-`--config 1..5` selects the five benchmark configurations (C1 tiny plumbing, C2
-Llama-3-8B decode, C3 fragmented ragged batch with a random page permutation, C4 32k chunked
-prefill, C5 80-layer 70B-class share with the pool at 90 % occupancy and seeded row churn).
+`--config 1..5` selects the five benchmark configurations (C1 tiny plumbing, C2 Llama-3-8B
+decode, C3 fragmented ragged batch with a random page permutation, C4 32k chunked prefill, C5
+80-layer 70B-class share with the pool at 90 % occupancy: before every decode step two seeded
+rows are freed and re-prefilled with 8192 new tokens, which take the pages released rows left).
 
 A step runs as one replay of a captured HIP graph of the per-layer fused append+gather launches
 (graph mode, C1-C4; the step's new K/V are first copied into the graph's static input buffers,
-as a model's K/V projection would write them), or as host-launched layer updates (eager mode, the
-per-call path HF attention takes; C5, whose launches move gigabytes each).  Throughput counts
-algorithmic bytes per step, summed over layers: append 2*B*T*tb (read new, write page) + gather
-sum_b(ctx_b)*tb (read) + B*S_max*tb (write, zero padding of short rows included), tb =
-2*H*D*esize; metadata is not counted.  Per-step bytes come from the same length arithmetic the
-kernels apply, run on the host.
+as a model's K/V projection would write them; every graph the window uses is captured before
+timing), or as host-launched layer calls (eager mode, the per-call path HF attention takes; C5).
+Throughput counts algorithmic bytes per step, summed over layers: append 2*B*T*tb (read new,
+write page) + gather sum_b(ctx_b)*tb (read) + B*S_max*tb (write, zero padding of short rows
+included), tb = 2*H*D*esize; metadata is not counted.  Per-step bytes come from the same length
+arithmetic the kernels apply, run on the host.  C5's re-prefill (2*2*8192*tb per layer: read
+new, write pages) is timed and reported on its own (`refill`); its decode updates are bracketed
+with HIP events per launch and `value` counts them alone.
 
-`roofline` is the dominant kernel alone: in graph mode the same graph replayed without the input
-copies, timed with HIP events on the stream it runs on; `achieved` = algorithmic bytes per
-launch / average launch duration.  `traffic` (measured HBM bytes per launch) is read from the
-committed rocprof counter summary profiles/stream_kernel_c<N>_decode_traffic.json when present.
+`roofline` is the dominant kernel alone: in graph mode the same graphs replayed without the
+input copies, timed with HIP events on the stream they run on; in eager mode the event-bracketed
+update launches; `achieved` = algorithmic bytes per launch / average launch duration.
+`traffic` (measured HBM bytes per launch) is read from the committed rocprof counter summary
+profiles/stream_kernel_c<N>_traffic.json when it holds this run's window; otherwise it is null
+and `traffic_measured` gives the counter ratio and the window it was measured at.
 
-`cpu_baseline` is the oracle's numpy restatement of the reference path (per-token
-_python_append + materialised current_tensors) on one host core over the same input bits (C1/C2:
-all layers and steps; larger configs: the first decode steps of layer 0).  The same run checks
-the GPU's layer-0 K/V after those steps bit for bit against it (`parity`).
+`cpu_baseline` is the reference CPU path -- the reference layer's per-(row, token) append and its
+view + .contiguous() gather, restated in torch (oracle/kv_oracle_torch.py, checked against the
+numpy oracle) -- on the host's cores (torch.set_num_threads), over the same input bits and the
+same window (C1/C2: 8 of the layers; larger configs: layer 0), timing the decode updates only;
+`numpy_one_thread` beside it (C1/C2) is the numpy oracle on one core.  The same run checks the
+GPU's layer-0 K/V after the window bit for bit against it (`parity`).
 
 `paged_attention` (bf16/fp16 configurations) times the decode-attention kernel that reads K/V
 from the pages through the block table (the step the gathered K/V feed), over the pools as the
@@ -50,8 +61,9 @@ graph-replayed, and times the dequantising gather alone for its roofline; layer 
 bit for bit with the quantisation oracle and, for the error quantisation introduces, with the
 full-precision K/V.
 
-Prints ONE JSON line.  `--pmc-probe` instead runs the eager workload the rocprof counter runs
-profile: a 64 MiB elementwise pass (calibration), the prefill, then the decode steps.
+Prints ONE JSON line.  `--pmc-probe` instead runs, eagerly, the window the counter runs profile:
+the prefill and the steps before the window, then a 64 MiB elementwise pass (calibration, and the
+marker after which the window's launches follow), then the window.
 """
 
 from __future__ import annotations
@@ -69,8 +81,9 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "paged KV append+gather GB/s (% HBM peak); µs per decode-step cache update"
-KERNEL = ("stream_kernel<16, 2> (fused append + gather, one launch per layer; launches of more than 4 tiles "
-          "per CU, as at C3-C5, run its stream_kernel_rounds<16, 2> instantiation)")
+KERNEL = ("stream kernel, fused append + gather, one launch per layer: lean_stream_kernel<8, 2> (1-page tiles) "
+          "while every 1-page tile fits on the CUs at once, lean_stream_kernel16<2> (2-page tiles) while those do, "
+          "else stream_kernel_rounds<16, 2> (several dispatch rounds, as at C3-C5)")
 
 # prefill: ("uniform", n) | ("ragged", lo, hi, seed) | ("chunks", count, size)
 CONFIGS = {
@@ -85,7 +98,7 @@ CONFIGS = {
             prefill=("chunks", 16, 2048), decode=64, seed=1004, mode="graph", cpu_steps=16),
     5: dict(name="C5 70B-class single-GPU share", layers=80, batch=32, heads=8, dim=128, page=16, dtype="bfloat16",
             prefill=("uniform", 8192), decode=64, seed=1005, mode="eager", occupancy=0.9,
-            churn=(2, 4005), cpu_steps=4, group=8),
+            churn=(2, 4005), refill=True, cpu_steps=4, group=8),
 }
 
 
@@ -150,7 +163,7 @@ def prefill_calls(cfg):
 
 
 def churn_rows(cfg, steps):
-    """Rows freed (and restarted empty) before each decode step."""
+    """Rows freed (and, with `refill`, re-prefilled) before each decode step."""
     import numpy as np
 
     if "churn" not in cfg:
@@ -161,60 +174,122 @@ def churn_rows(cfg, steps):
 
 
 def step_bytes_all(cfg, steps, churn):
-    """Algorithmic bytes of each decode step (all layers), from the host length arithmetic."""
-    lens = list(prefill_lengths(cfg))
+    """Algorithmic bytes of each decode step's updates (all layers), from the host length
+    arithmetic; churned rows restart empty, or at their prefill length when re-prefilled."""
+    start = prefill_lengths(cfg)
+    lens = list(start)
     tb, B, L = tok_bytes(cfg), cfg["batch"], cfg["layers"]
     out = []
     for s in range(steps):
         for r in churn[s]:
-            lens[r] = 0
+            lens[r] = start[r] if cfg.get("refill") else 0
         lens = [x + 1 for x in lens]
         out.append(L * (2 * B * tb + sum(lens) * tb + B * max(lens) * tb))
     return out
 
 
-def cpu_baseline(cfg, wl, steps, layers):
-    """The oracle (reference CPU path + contiguous materialisation) on `layers` layers x `steps`
-    decode steps, timing the decode steps only; returns (result, layer-0 K/V after the steps)."""
-    from kvgen import to_bits
-    from oracle.kv_oracle import DenseLayerOracle
+def longest_rows(cfg, steps, churn):
+    """Longest row after each decode step's append (the extent its graph covers)."""
+    start = prefill_lengths(cfg)
+    lens = list(start)
+    out = []
+    for s in range(steps):
+        for r in churn[s]:
+            lens[r] = start[r] if cfg.get("refill") else 0
+        lens = [x + 1 for x in lens]
+        out.append(max(lens))
+    return out
 
-    cap = max(prefill_lengths(cfg)) + wl.steps_cap
-    total = 0.0
-    final = None
-    for layer in range(layers):
-        oracle = DenseLayerOracle(cfg["batch"], cap, cfg["page"])
+
+def window_start(cfg, steps):
+    """First decode step of the timed window: the `steps` steps centred in the configuration's
+    trajectory when they are fewer (their bytes per step are then its mean), else step 0."""
+    total = cfg["decode"]
+    return (total - steps) // 2 if steps < total else 0
+
+
+def host_threads():
+    """Threads of the CPU baseline: the cores this process may run on, capped by
+    OMP_NUM_THREADS when it is set (the GPU box sets it to its CPU share)."""
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_baseline(cfg, wl, start, steps, layers):
+    """The reference CPU path (oracle/kv_oracle_torch.py) on the host's cores: `layers` layers,
+    each prefilled and advanced to the window untimed, then the window's decode updates timed
+    (churned rows are freed and re-prefilled between them, untimed).  Returns (result, layer-0
+    K/V after the window, as torch tensors).  For C1/C2 the numpy oracle on one core times layer 0
+    beside it."""
+    import torch
+
+    from oracle.kv_oracle import DenseLayerOracle
+    from oracle.kv_oracle_torch import DenseLayerTorch
+
+    B, P, L = cfg["batch"], cfg["page"], cfg["layers"]
+    cap = max(prefill_lengths(cfg)) + wl.n_steps
+    refill = tuple(t.cpu() for t in wl.refill) if wl.refill is not None else None
+    threads = host_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+
+    def timed_layer(ref, layer, to_input):
         for k, v in wl.prefill_inputs(layer):
-            oracle.append(to_bits(k), to_bits(v))
-        kd = to_bits(wl.k_dec[:steps, layer])  # [steps, B, H, 1, D]
-        vd = to_bits(wl.v_dec[:steps, layer])
-        t0 = time.perf_counter()
-        for s in range(steps):
-            if wl.churn[s]:
-                oracle.release_rows(wl.churn[s])
-            ok, ov = oracle.update(kd[s], vd[s])
-        total += time.perf_counter() - t0
-        if layer == 0:
-            final = (ok, ov)
-    nbytes = sum(wl.step_bytes[:steps]) * layers / cfg["layers"]
+            ref.append(to_input(k), to_input(v))
+        kd = [to_input(wl.k_dec[s, layer]) for s in range(start + steps)]
+        vd = [to_input(wl.v_dec[s, layer]) for s in range(start + steps)]
+        spent, out = 0.0, None
+        for s in range(start + steps):
+            rows = wl.churn[s]
+            if rows:
+                ref.release_rows(rows)
+                if refill is not None:
+                    ref.append_rows(rows, to_input(refill[0]), to_input(refill[1]))
+            t0 = time.perf_counter()
+            out = ref.update(kd[s], vd[s])
+            if s >= start:
+                spent += time.perf_counter() - t0
+        return spent, out
+
+    try:
+        total, final = 0.0, None
+        for layer in range(layers):
+            spent, out = timed_layer(DenseLayerTorch(B, cap, P), layer, lambda t: t.cpu())
+            total += spent
+            if layer == 0:
+                final = out
+    finally:
+        torch.set_num_threads(prev)
+    nbytes = sum(wl.step_bytes[start:start + steps]) * layers / L
     result = {
         "value": round(nbytes / total / 1e9, 3),
         "unit": "GB/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": f"{layers} of {cfg['layers']} layers x the first {steps} decode steps (append 1 token x "
-                  f"{cfg['batch']} rows + materialised gather), numpy restatement of the reference "
-                  f"kv_cache.py _python_append + current_tensors, one thread; same input bits",
-        "ms_per_step": round(total / steps * cfg["layers"] / layers * 1e3, 3),
+        "sample": f"{layers} of {L} layers x the {steps} timed decode steps (append 1 token x {B} rows + "
+                  f"materialised gather), torch restatement of the reference kv_cache.py _python_append + "
+                  f"current_tensors (view + .contiguous()) on {threads} threads; same input bits",
+        "ms_per_step": round(total / steps * L / layers * 1e3, 3),
         "seconds": round(total, 2),
     }
+    if cfg["cpu_steps"] is None:  # C1/C2: the numpy oracle on one core, layer 0
+        from kvgen import to_bits
+
+        spent, _ = timed_layer(DenseLayerOracle(B, cap, P), 0, to_bits)
+        result["numpy_one_thread"] = {"value": round(nbytes / layers / spent / 1e9, 3), "cores": 1,
+                                      "ms_per_step": round(spent / steps * L * 1e3, 3),
+                                      "sample": "layer 0 x the timed steps, numpy oracle"}
     return result, final
 
 
 class Workload:
-    """Pools, prefill, per-step inputs and churn of one configuration on cuda:0."""
+    """Pools, prefill, per-step inputs and churn of one configuration on cuda:0, for decode steps
+    [0, n_steps) of its trajectory."""
 
-    def __init__(self, cfg, steps, warmup, dev):
+    def __init__(self, cfg, n_steps, dev):
         import numpy as np
         import torch
 
@@ -223,14 +298,15 @@ class Workload:
         self.cfg, self.dev = cfg, dev
         self.dtype = getattr(torch, cfg["dtype"])
         L, B, H, D, P = cfg["layers"], cfg["batch"], cfg["heads"], cfg["dim"], cfg["page"]
-        self.steps_cap = max(steps, warmup)
+        self.n_steps = n_steps
+        self.steps_cap = n_steps
         lens = prefill_lengths(cfg)
-        cap = max(lens) + self.steps_cap
+        cap = max(lens) + n_steps
         mb = math.ceil(cap / P)
         num_pages = B * mb
         if "occupancy" in cfg:  # the prefill's pages fill `occupancy` of the pool
             live = sum(math.ceil(x / P) for x in lens)
-            num_pages = max(math.ceil(live / cfg["occupancy"]), live + B * math.ceil(self.steps_cap / P) + B)
+            num_pages = max(math.ceil(live / cfg["occupancy"]), live + B * math.ceil(n_steps / P) + B)
         order = None
         if "perm_seed" in cfg:
             perm = np.random.default_rng(cfg["perm_seed"]).permutation(num_pages).astype(np.int32)
@@ -239,11 +315,18 @@ class Workload:
         self.pools = [PagePool(max_batch=B, max_blocks=mb, page_size=P, kv_heads=H, head_dim=D, dtype=self.dtype,
                                device=dev, num_pages=num_pages, page_order=order) for _ in range(L)]
         gen = torch.Generator(device=dev).manual_seed(cfg["seed"])
-        n_in = self.steps_cap
-        self.k_dec = self._normal(gen, (n_in, L, B, 1, H, D)).transpose(3, 4)
-        self.v_dec = self._normal(gen, (n_in, L, B, 1, H, D)).transpose(3, 4)
-        self.churn = churn_rows(cfg, n_in)
-        self.step_bytes = step_bytes_all(cfg, n_in, self.churn)
+        self.k_dec = self._normal(gen, (n_steps, L, B, 1, H, D)).transpose(3, 4)
+        self.v_dec = self._normal(gen, (n_steps, L, B, 1, H, D)).transpose(3, 4)
+        self.churn = churn_rows(cfg, n_steps)
+        self.step_bytes = step_bytes_all(cfg, n_steps, self.churn)
+        self.longest = longest_rows(cfg, n_steps, self.churn)
+        self.refill = None
+        if cfg.get("refill"):  # one seeded prefill that every re-prefilled row takes
+            n, ctx = cfg["churn"][0], lens[0]
+            g = torch.Generator(device=dev).manual_seed(cfg["seed"] + 7)
+            self.refill = (self._normal(g, (n, ctx, H, D)).transpose(1, 2),
+                           self._normal(g, (n, ctx, H, D)).transpose(1, 2))
+            self.refill_bytes = L * 2 * n * ctx * tok_bytes(cfg)  # per step: read new + write pages
 
     def _normal(self, gen, shape):
         import torch
@@ -269,6 +352,14 @@ class Workload:
                     pool.update(k, v)
                 else:
                     pool.append(k, v)
+
+    def churn_layer(self, s, pool):
+        """Step s's churn on one layer: its rows freed and, with `refill`, re-prefilled."""
+        rows = self.churn[s]
+        if rows:
+            pool.free_rows(rows)
+            if self.refill is not None:
+                pool.append_rows(rows, *self.refill)
 
 
 def attention_leg(cfg, pools, B, dev, reps=20, kv_bytes=None):
@@ -623,115 +714,143 @@ def main():
     warmup = args.warmup if args.warmup is not None else (2 if big else 16)
     repeat = args.repeat if args.repeat is not None else (1 if big else 3)
     mode = args.mode or cfg["mode"]
-    if args.pmc_probe:
-        warmup, mode = 0, "eager"
+    start = window_start(cfg, steps)
     L, B, H, D, P = cfg["layers"], cfg["batch"], cfg["heads"], cfg["dim"], cfg["page"]
     dev = torch.device("cuda", 0)
-    wl = Workload(cfg, steps, warmup, dev)
+    wl = Workload(cfg, start + max(steps, warmup), dev)
     pools = wl.pools
     flags = SEPARATE_FINALIZE if args.separate_commit else 0
 
-    if args.pmc_probe:
-        src = torch.zeros(64 * 2**20, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            torch.bitwise_not(src, out=dst)  # calibration: one elementwise kernel, 64 MiB in + 64 MiB out
+    if args.pmc_probe:  # prefill + steps before the window, calibration pass (the marker), the window
         wl.prefill()
-        for s in range(steps):
+        for s in range(start + steps):
+            if s == start:
+                torch.cuda.synchronize()
+                src = torch.zeros(64 * 2**20, dtype=torch.uint8, device=dev)
+                dst = torch.empty_like(src)
+                for _ in range(3):
+                    torch.bitwise_not(src, out=dst)  # calibration: 64 MiB in + 64 MiB out
+                torch.cuda.synchronize()
             for layer, pool in enumerate(pools):
-                if wl.churn[s]:
-                    pool.free_rows(wl.churn[s])
+                wl.churn_layer(s, pool)
                 pool.update(wl.k_dec[s, layer], wl.v_dec[s, layer], flags=flags)
         torch.cuda.synchronize()
-        total = sum(wl.step_bytes[:steps])
-        print(json.dumps({"pmc_probe": True, "config": cfg["name"], "steps": steps, "launches": steps * L,
-                          "algorithmic_bytes_per_launch": total / (steps * L)}), flush=True)
+        total = sum(wl.step_bytes[start:start + steps])
+        print(json.dumps({"pmc_probe": True, "config": cfg["name"], "window_start": start, "steps": steps,
+                          "launches": steps * L, "algorithmic_bytes_per_launch": total / (steps * L)}), flush=True)
         return
 
     graph = None
     last = {}
+    marks = []  # eager mode: (start, end) events around every update launch of the window
     if mode == "graph":
-        if any(wl.churn[:wl.steps_cap]):
+        if any(wl.churn):
             raise SystemExit("graph mode replays a fixed step; configurations with row churn run eager")
         kin = torch.empty((L, B, H, 1, D), dtype=wl.dtype, device=dev)
         vin = torch.empty_like(kin)
         graph = CapturedDecodeStep(pools, B, 1, separate_commit=args.separate_commit, inputs=(kin, vin),
                                    bucket=args.bucket)
+        graph.prepare(wl.longest)  # no capture inside a timed region
 
-        def run_step(s):
+        def run_step(s, record=False):
             kin.copy_(wl.k_dec[s])
             vin.copy_(wl.v_dec[s])
             graph.replay()
     else:
-        def run_step(s):
+        def run_step(s, record=False):
             for layer, pool in enumerate(pools):
-                if wl.churn[s]:
-                    pool.free_rows(wl.churn[s])
+                wl.churn_layer(s, pool)
+                if record:
+                    e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                    e[0].record()
                 out = pool.update(wl.k_dec[s, layer], wl.v_dec[s, layer], flags=flags)
+                if record:
+                    e[1].record()
+                    marks.append(e)
                 if layer == 0:
                     last["out"] = out
 
-    # The prefill (untimed for the decode metric; reported on its own for chunked prefill).
+    # The prefill (untimed for the decode metric; reported on its own for chunked prefill), then
+    # warm-up steps at the window.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     wl.prefill()
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
-    for s in range(warmup):
+    for s in range(start + warmup):
         run_step(s)
     torch.cuda.synchronize()
 
-    def timed(fn):
+    def timed(fn, lo, n):
+        """Best of `repeat`: prefill, steps [0, lo) untimed, then steps [lo, lo + n) bracketed by
+        synchronisations and timed with events.  Returns (ms, event-bracketed update ms)."""
         best = None
         for _ in range(max(1, repeat)):
             wl.prefill()
-            torch.cuda.synchronize()
-            start = torch.cuda.Event(enable_timing=True)
-            end = torch.cuda.Event(enable_timing=True)
-            start.record()
-            for s in range(steps):
+            for s in range(lo):
                 fn(s)
-            end.record()
             torch.cuda.synchronize()
-            ms = start.elapsed_time(end)
-            best = ms if best is None else min(best, ms)
+            marks.clear()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for s in range(lo, lo + n):
+                fn(s, record=True) if fn is run_step else fn(s)
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1)
+            upd = sum(a.elapsed_time(b) for a, b in marks) if marks else None
+            if best is None or ms < best[0]:
+                best = (ms, upd)
         return best
 
-    # The dominant kernel alone: the per-layer launches without the input copies (graph mode),
-    # timed on the stream they run on.  (The inputs are not refreshed here, so the state this
-    # leaves is overwritten by the full timed run below.)
-    kernel_ms = timed(lambda s: graph.replay()) if graph is not None else None
-
-    best = timed(run_step)
+    # The dominant kernel alone: in graph mode the per-layer launches without the input copies,
+    # timed on the stream they run on (the inputs are not refreshed, so the state this leaves is
+    # overwritten by the full timed run below); in eager mode the event-bracketed updates.
+    kernel_ms = timed(lambda s: graph.replay(), start, steps)[0] if graph is not None else None
+    best, upd_ms = timed(run_step, start, steps)
     errors = [p.errors() for p in pools]
     if any(errors):
         raise SystemExit(f"device error bits set: {errors}")
     if kernel_ms is None:
-        kernel_ms = best
+        kernel_ms = upd_ms
+    decode_ms = upd_ms if wl.refill is not None else best  # C5: the updates alone
 
-    total_bytes = sum(wl.step_bytes[:steps])
-    gbs = total_bytes / (best / 1e3) / 1e9
+    total_bytes = sum(wl.step_bytes[start:start + steps])
+    gbs = total_bytes / (decode_ms / 1e3) / 1e9
     launches = steps * L
     avg_launch_us = kernel_ms * 1e3 / launches
     bytes_per_launch = total_bytes / launches
     achieved = bytes_per_launch / (avg_launch_us * 1e-6) / 1e9
 
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"stream_kernel_c{args.config}_decode_traffic.json")
+    traffic, traffic_measured = None, None
+    tpath = os.path.join(ROOT, "profiles", f"stream_kernel_c{args.config}_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            windows = json.load(f)["windows"]
+        for w in windows:
+            if w["window_start"] == start and w["steps"] == steps:
+                traffic = w["hbm_bytes_per_launch"]
+        if traffic is None and windows:
+            w = min(windows, key=lambda w: abs(w["algorithmic_bytes_per_launch"] - bytes_per_launch))
+            traffic_measured = {"traffic_over_algorithmic": w["traffic_over_algorithmic"],
+                                "window_start": w["window_start"], "steps": w["steps"],
+                                "context": w["context"]}
 
     lens = prefill_lengths(cfg)
     kind = cfg["prefill"]
+    ctx_lo = min(lens) + start + 1
     workload = (f"{cfg['name']}: {L} layers, batch {B}, {H} KV heads x {D}, {cfg['dtype']}, page {P}; "
-                f"prefill ({kind[0]}, context {min(lens)}..{max(lens)}, untimed), then {steps} decode steps of "
-                f"1-token append + full contiguous gather per layer")
+                f"prefill ({kind[0]}, context {min(lens)}..{max(lens)}, untimed), then decode steps "
+                f"{start}..{start + steps - 1} of the {cfg['decode']}-step trajectory timed (1-token append + "
+                f"full contiguous gather per layer; context {ctx_lo}..{max(lens) + start + steps} on the longest "
+                f"rows{'; the steps before them run untimed' if start else ''})")
     if "perm_seed" in cfg:
         workload += f"; pages handed out in a seeded random permutation (seed {cfg['perm_seed']})"
     if "occupancy" in cfg:
         workload += (f"; pool of {pools[0].num_pages} pages per layer ({cfg['occupancy']:.0%} occupied after the "
-                     f"prefill), {cfg['churn'][0]} seeded rows freed and restarted before every step")
+                     f"prefill), {cfg['churn'][0]} seeded rows freed before every step"
+                     + (f" and re-prefilled with {lens[0]} tokens (timed apart)" if wl.refill is not None else ""))
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -739,8 +858,8 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
-        "ms_per_step": round(best / steps, 4),
-        "us_per_step": round(best * 1e3 / steps, 2),
+        "ms_per_step": round(decode_ms / steps, 4),
+        "us_per_step": round(decode_ms * 1e3 / steps, 2),
         "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -751,7 +870,8 @@ def main():
             "workload": workload,
             "mode": mode + (" + separate commit" if args.separate_commit else ""),
             "layers": L, "batch": B, "kv_heads": H, "head_dim": D, "page_size": P,
-            "prefill": kind[0], "decode_steps": steps, "parallelism": "single GPU",
+            "prefill": kind[0], "decode_steps": steps, "window_start": start, "trajectory_steps": cfg["decode"],
+            "parallelism": "single GPU",
         },
         "roofline": {
             "bound": "hbm",
@@ -765,6 +885,27 @@ def main():
             "avg_launch_us": round(avg_launch_us, 3),
         },
     }
+    if traffic_measured is not None:
+        result["roofline"]["traffic_measured"] = traffic_measured
+    if wl.refill is not None:
+        refill_ms = best - upd_ms
+        result["refill"] = {"rows_per_step": cfg["churn"][0], "tokens_per_row": lens[0],
+                            "ms_per_step": round(refill_ms / steps, 3),
+                            "gbs": round(wl.refill_bytes * steps / (refill_ms / 1e3) / 1e9, 1),
+                            "bytes_per_step": wl.refill_bytes,
+                            "step_with_refill_ms": round(best / steps, 3),
+                            "note": "free_rows + append_rows of the churned rows, every layer, host-launched"}
+    if start > 0:  # the first `steps` steps of the trajectory, for comparison
+        first_kernel = timed(lambda s: graph.replay(), 0, steps)[0] if graph is not None else None
+        first, first_upd = timed(run_step, 0, steps)
+        first_decode = first_upd if wl.refill is not None else first
+        fb = sum(wl.step_bytes[:steps])
+        fk = first_kernel if first_kernel is not None else first_upd
+        result["first_steps"] = {
+            "decode_steps": f"0..{steps - 1}", "value": round(fb / (first_decode / 1e3) / 1e9, 2),
+            "us_per_step": round(first_decode * 1e3 / steps, 2),
+            "avg_launch_us": round(fk * 1e3 / launches, 3), "bytes_per_launch": int(fb / launches),
+            "frac": round(fb / launches / (fk * 1e3 / launches * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     if kind[0] == "chunks":
         chunk_bytes = sum(L * (2 * B * kind[2] + 2 * B * (c + 1) * kind[2]) * tok_bytes(cfg) for c in range(kind[1]))
         result["chunked_prefill"] = {"calls_per_layer": kind[1], "seconds_eager": round(prefill_s, 4),
@@ -777,12 +918,12 @@ def main():
 
         from kvgen import to_bits
 
-        cpu_steps = cfg["cpu_steps"] or steps
-        layers = 1 if cfg["cpu_steps"] else min(args.cpu_layers or L, L)
-        result["cpu_baseline"], want = cpu_baseline(cfg, wl, cpu_steps, layers)
+        cpu_steps = min(cfg["cpu_steps"] or steps, steps)
+        layers = 1 if cfg["cpu_steps"] else min(args.cpu_layers or 8, L)
+        result["cpu_baseline"], want = cpu_baseline(cfg, wl, start, cpu_steps, layers)
         # the GPU's layer 0 after the same steps, from a fresh prefill
         wl.prefill()
-        for s in range(cpu_steps):
+        for s in range(start + cpu_steps):
             run_step(s)
         torch.cuda.synchronize()
         if graph is not None:
@@ -790,13 +931,13 @@ def main():
             got = (graph.key_out[0][:, :, :seq], graph.value_out[0][:, :, :seq])
         else:
             got = last["out"]
-        result["parity"] = {"layer0_kv_bit_exact_vs_oracle": bool(
-            np.array_equal(to_bits(got[0]), want[0]) and np.array_equal(to_bits(got[1]), want[1])),
-            "after_decode_steps": cpu_steps}
+        result["parity"] = {"layer0_kv_bit_exact_vs_cpu_reference": bool(
+            np.array_equal(to_bits(got[0]), to_bits(want[0])) and np.array_equal(to_bits(got[1]), to_bits(want[1]))),
+            "after_decode_steps": start + cpu_steps}
     if not args.no_attention and cfg["dtype"] in ("bfloat16", "float16") and D == 128:
         result["paged_attention"] = attention_leg(cfg, pools, B, dev)
     if args.quant and cfg["dtype"] in ("bfloat16", "float16"):
-        result["quantized_kv"] = quant_leg(cfg, wl, steps, dev, best / steps)
+        result["quantized_kv"] = quant_leg(cfg, wl, steps, dev, decode_ms / steps)
     if not args.no_beam:
         result["beam_select"] = beam_leg(cfg, wl, dev)
     print(json.dumps(result), flush=True)

@@ -197,6 +197,26 @@ class DenseLayerOracle:
         self.seq_lens[...] = 0
         self.current_batch_size = 0
 
+    # Appending to chosen rows (the page pool's append_rows, no reference counterpart): for each
+    # row, the per-row body of _python_append (kv_cache.py:77-90) -- the reference appends to
+    # rows [0, batch) one row at a time, so this is the same loop over a chosen set of rows.
+    def append_rows(self, rows: Sequence[int], key_states: np.ndarray, value_states: np.ndarray) -> None:
+        if not self.is_initialized:
+            self.lazy_initialization(key_states)
+        token_count = key_states.shape[2]
+        for i, r in enumerate(rows):
+            start = int(self.seq_lens[r])
+            end = start + token_count
+            if end > self.max_cache_len:
+                raise CapacityError(
+                    f"paged KV cache capacity exceeded: requested {end}, max_cache_len={self.max_cache_len}"
+                )
+            for token_idx in range(token_count):
+                pos = start + token_idx
+                self.keys[r, :, pos // self.page_size, pos % self.page_size, :] = key_states[i, :, token_idx, :]
+                self.values[r, :, pos // self.page_size, pos % self.page_size, :] = value_states[i, :, token_idx, :]
+            self.seq_lens[r] = end
+
     # Free-and-reallocate of one row (the page pool's free_rows, no reference counterpart):
     # the row returns to the state lazy_initialization gives it -- zero data, zero length.
     def release_rows(self, rows: Sequence[int]) -> None:

@@ -56,6 +56,19 @@ class CPool:
         _capi.check(self.lib.barq_kv_append(self.ref, k.data_ptr(), v.data_ptr(), k.shape[0], k.shape[2],
                                             k.stride(0), k.stride(1), k.stride(2), self._stream()))
 
+    def append_rows(self, rows, k, v):
+        """k[i], v[i] appended to row rows[i]: barq_kv_append over the one-row view of each row's
+        metadata (block-table row, length, mark), the free stack shared."""
+        for i, r in enumerate(rows):
+            one = _capi.BarqKVPool(*[getattr(self.s, f) for f, _ in _capi.BarqKVPool._fields_])
+            one.block_table = self.bt[r:r + 1].data_ptr()
+            one.seq_lens = self.lens[r:r + 1].data_ptr()
+            one.high_water = self.hw[r:r + 1].data_ptr()
+            one.max_batch = 1
+            ki, vi = k[i:i + 1], v[i:i + 1]
+            _capi.check(self.lib.barq_kv_append(ctypes.byref(one), ki.data_ptr(), vi.data_ptr(), 1, ki.shape[2],
+                                                ki.stride(0), ki.stride(1), ki.stride(2), self._stream()))
+
     def gather(self, batch, seq, flags=0, out=None):
         ko, vo = out or self.new_out(batch, seq)
         _capi.check(self.lib.barq_kv_gather(self.ref, ko.data_ptr(), vo.data_ptr(), batch, seq,
@@ -196,6 +209,19 @@ class CColdPool(CPool):
 
     def compress(self, batch):
         _capi.check(self.lib.barq_kv_compress(self.ref, self.cref, batch, self._stream()))
+
+    def append_rows(self, rows, k, v):
+        """k[i], v[i] appended to row rows[i]: barq_kv_append over the one-row view of each row's
+        metadata (block-table row, length, mark), the free stack shared."""
+        for i, r in enumerate(rows):
+            one = _capi.BarqKVPool(*[getattr(self.s, f) for f, _ in _capi.BarqKVPool._fields_])
+            one.block_table = self.bt[r:r + 1].data_ptr()
+            one.seq_lens = self.lens[r:r + 1].data_ptr()
+            one.high_water = self.hw[r:r + 1].data_ptr()
+            one.max_batch = 1
+            ki, vi = k[i:i + 1], v[i:i + 1]
+            _capi.check(self.lib.barq_kv_append(ctypes.byref(one), ki.data_ptr(), vi.data_ptr(), 1, ki.shape[2],
+                                                ki.stride(0), ki.stride(1), ki.stride(2), self._stream()))
 
     def gather(self, batch, seq, flags=0, out=None):
         ko, vo = out or self.new_out(batch, seq)

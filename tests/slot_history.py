@@ -32,6 +32,16 @@ class SlotHistory:
             self.lens[b] += tokens
         self.current = batch
 
+    def append_rows(self, rows, keys: np.ndarray, values: np.ndarray) -> None:
+        """Entry i of the call goes to row rows[i] (the current batch is unchanged)."""
+        call = len(self.inputs)
+        self.inputs.append((keys, values))
+        tokens = keys.shape[2]
+        for i, r in enumerate(rows):
+            for t in range(tokens):
+                self.rows[r][self.lens[r] + t] = (call, i, t)
+            self.lens[r] += tokens
+
     def crop(self, max_length: int) -> None:
         for b in range(self.current):
             self.lens[b] = min(self.lens[b], max_length)

@@ -348,3 +348,103 @@ def test_planted_mistake_fails_dynamic_layer_check():
 def test_planted_mistake_fails_golden_digests():
     with pytest.raises(AssertionError):
         check_config1_digests(_OffByOnePage)
+
+
+# ----------------------------------------------------------------------------- torch restatement
+# oracle/kv_oracle_torch.py is the CPU baseline bench.py times on the host's cores; it must give
+# the numpy oracle's bits.  It is fed the same raw bits as signed-integer tensors (its operations
+# are copies, so the element type does not matter).
+_SIGNED_NP = {np.dtype(np.uint16): np.int16, np.dtype(np.uint32): np.int32, np.dtype(np.uint64): np.int64}
+
+
+class TorchBits:
+    """DenseLayerTorch behind the numpy oracle's bits interface."""
+
+    def __init__(self, max_batch_size, max_cache_len, page_size=16):
+        from oracle.kv_oracle_torch import DenseLayerTorch
+
+        self.layer = DenseLayerTorch(max_batch_size, max_cache_len, page_size)
+
+    def update(self, k, v):
+        u = k.dtype
+        gk, gv = self.layer.update(torch.from_numpy(np.ascontiguousarray(k).view(_SIGNED_NP[u])),
+                                   torch.from_numpy(np.ascontiguousarray(v).view(_SIGNED_NP[u])))
+        return gk.numpy().view(u), gv.numpy().view(u)
+
+    def release_rows(self, rows):
+        self.layer.release_rows(rows)
+
+    def get_seq_length(self):
+        return self.layer.get_seq_length()
+
+
+def test_torch_restatement_known_answer_and_golden_digests():
+    check_known_answer(TorchBits)
+    check_config1_digests(TorchBits)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_torch_restatement_matches_numpy_oracle(seed):
+    rng = np.random.default_rng(500 + seed)
+    Bmax, H, D, cap, P = 5, 2, 8, 40, 4
+    a, b = DenseLayerOracle(Bmax, cap, P), TorchBits(Bmax, cap, P)
+    for _ in range(40):
+        if rng.random() < 0.15 and a.is_initialized:
+            rows = sorted(rng.choice(Bmax, size=int(rng.integers(1, 3)), replace=False).tolist())
+            a.release_rows(rows)
+            b.release_rows(rows)
+            continue
+        n = int(rng.integers(1, Bmax + 1))
+        t = int(rng.integers(1, 6))
+        if a.is_initialized and int(a.seq_lens[:n].max()) + t > cap:
+            continue
+        k = rng.integers(0, 2**16, size=(n, H, t, D), dtype=np.uint16)
+        v = rng.integers(0, 2**16, size=(n, H, t, D), dtype=np.uint16)
+        ak, av = a.update(k, v)
+        bk, bv = b.update(k, v)
+        assert np.array_equal(ak, bk) and np.array_equal(av, bv)
+        assert a.get_seq_length() == b.get_seq_length()
+
+
+def test_torch_restatement_capacity_error():
+    b = TorchBits(2, 6, 4)
+    b.update(np.zeros((2, 1, 5, 2), np.uint16), np.zeros((2, 1, 5, 2), np.uint16))
+    with pytest.raises(ValueError, match="capacity exceeded"):
+        b.update(np.zeros((1, 1, 2, 2), np.uint16), np.zeros((1, 1, 2, 2), np.uint16))
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_append_rows_matches_slot_history_in_both_oracles(seed):
+    """append_rows (a new sequence's prefill into freed rows while others decode) in the numpy
+    and torch restatements, against the slot-history model (no pages, no dense layout)."""
+    rng = np.random.default_rng(700 + seed)
+    Bmax, H, D, cap, P = 6, 2, 4, 48, 4
+    a, b = DenseLayerOracle(Bmax, cap, P), TorchBits(Bmax, cap, P)
+    hist = SlotHistory(Bmax)
+    k = rng.integers(0, 2**16, size=(Bmax, H, 5, D), dtype=np.uint16)
+    for layer in (a, b):
+        layer.update(k, k)
+    hist.append(k, k)
+    for _ in range(25):
+        if rng.random() < 0.4:
+            rows = sorted(rng.choice(Bmax, size=int(rng.integers(1, 3)), replace=False).tolist())
+            for layer in (a, b):
+                layer.release_rows(rows)
+            hist.release(rows)
+            t = int(rng.integers(1, 9))
+            kr = rng.integers(0, 2**16, size=(len(rows), H, t, D), dtype=np.uint16)
+            vr = rng.integers(0, 2**16, size=(len(rows), H, t, D), dtype=np.uint16)
+            if max(hist.lens[r] for r in rows) + t > cap:
+                continue
+            a.append_rows(rows, kr, vr)
+            b.layer.append_rows(rows, torch.from_numpy(kr.view(np.int16)), torch.from_numpy(vr.view(np.int16)))
+            hist.append_rows(rows, kr, vr)
+        if max(hist.lens) + 1 > cap:
+            break
+        k = rng.integers(0, 2**16, size=(Bmax, H, 1, D), dtype=np.uint16)
+        ak, av = a.update(k, k)
+        bk, bv = b.update(k, k)
+        hist.append(k, k)
+        hk, hv = hist.gather(H, D, np.uint16)
+        assert np.array_equal(ak, hk) and np.array_equal(av, hv)
+        assert np.array_equal(bk, hk) and np.array_equal(bv, hv)
