@@ -26,14 +26,14 @@ from pathlib import Path
 from types import ModuleType
 from typing import Optional
 
-_PKG_DIR = Path(__file__).resolve().parent
-_REPO_ROOT = _PKG_DIR.parent
-_HIP_SOURCES = (
-    _PKG_DIR / "csrc" / "barq_kv.hip",
-    _PKG_DIR / "csrc" / "fastdiv.h",
-    _PKG_DIR / "csrc" / "barq_kv_torch.cpp",
-    _REPO_ROOT / "include" / "barq_kv.h",
-)
+
+def _hip_sources() -> tuple[Path, ...]:
+    """The files the in-tree build compiles (its own list, so the two cannot drift apart)."""
+    from barqtrain_amd.build import source_files
+
+    return source_files()
+
+
 _CUDA_BACKEND: Optional[ModuleType] = None
 _CUDA_BUILD_FAILED = False
 
@@ -103,7 +103,7 @@ def load_cuda_backend() -> Optional[ModuleType]:
     if not _env_enabled("BARQTRAIN_AUTO_BUILD", "1"):
         return None
 
-    missing = [src for src in _HIP_SOURCES if not src.exists()]
+    missing = [src for src in _hip_sources() if not src.exists()]
     if missing:
         warnings.warn(
             "BarqTrain HIP sources missing, skipping the GPU backend: "

@@ -26,6 +26,13 @@ LIB_NAME = "libbarq_kv.so"
 EXT_NAME = "barqtrain_cuda"
 OFFLOAD_ARCH = "gfx950"
 HIP_SOURCES = ("barq_kv.hip", "barq_kv_attention.hip", "barq_kv_quant.hip")
+HIP_HEADERS = ("fastdiv.h", "barq_kv_fp8.h")
+HOST_SOURCES = ("barq_kv_torch.cpp",)
+
+
+def source_files() -> tuple[Path, ...]:
+    """Every file the build reads: the HIP sources and headers, the binding, the C ABI header."""
+    return tuple(CSRC / f for f in HIP_SOURCES + HIP_HEADERS + HOST_SOURCES) + (INCLUDE / "barq_kv.h",)
 
 # Packed fp32 instructions stay off in every HIP compile (none are needed: the kernels only
 # move bits, but the flag keeps the compiler from forming them).
@@ -98,7 +105,7 @@ def build_extension(verbose: bool = False) -> Path:
         f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
         *[f"-I{p}" for p in cpp_extension.include_paths(device_type="cuda")],
         f"-I{rocm}/include", f"-I{sysconfig.get_paths()['include']}", f"-I{INCLUDE}",
-        str(CSRC / "barq_kv_torch.cpp"),
+        *(str(CSRC / f) for f in HOST_SOURCES),
         f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-ltorch_hip",
         f"-L{PKG_DIR}", "-lbarq_kv", "-Wl,-rpath,$ORIGIN",
         "-o", str(tmp),

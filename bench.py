@@ -61,9 +61,11 @@ graph-replayed, and times the dequantising gather alone for its roofline; layer 
 bit for bit with the quantisation oracle and, for the error quantisation introduces, with the
 full-precision K/V.
 
-Prints ONE JSON line.  `--pmc-probe` instead runs, eagerly, the window the counter runs profile:
-the prefill and the steps before the window, then a 64 MiB elementwise pass (calibration, and the
-marker after which the window's launches follow), then the window.
+Prints ONE JSON line.  `--pmc-probe` instead makes, once, the launches the counter and trace runs
+profile, as the timed run makes them (graphs in graph mode): the prefill and the steps before the
+window, a 64 MiB elementwise pass (the counters' calibration, and the marker after which the
+window's launches follow), the window, then one decode-attention call per layer; with `--quant`,
+the fp8 leg's prefill, the marker, its decode steps and one dequantising gather per layer.
 """
 
 from __future__ import annotations
@@ -82,7 +84,7 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 HBM_PEAK_GBS = 8000.0
 METRIC = "paged KV append+gather GB/s (% HBM peak); µs per decode-step cache update"
 KERNEL = ("stream kernel, fused append + gather, one launch per layer: lean_stream_kernel<8, 2> (1-page tiles) "
-          "while every 1-page tile fits on the CUs at once, lean_stream_kernel16<2> (2-page tiles) while those do, "
+          "while every 1-page tile fits on the CUs at once, lean_stream_kernel<16, 2> (2-page tiles) while those do, "
           "else stream_kernel_rounds<16, 2> (several dispatch rounds, as at C3-C5)")
 
 # prefill: ("uniform", n) | ("ragged", lo, hi, seed) | ("chunks", count, size)
@@ -114,7 +116,9 @@ def parse():
     ap.add_argument("--cpu-layers", type=int, default=None,
                     help="layers the CPU baseline runs (C1/C2 default: all)")
     ap.add_argument("--repeat", type=int, default=None, help="timed repetitions; the best is reported")
-    ap.add_argument("--pmc-probe", action="store_true", help="eager run for rocprof counter passes")
+    ap.add_argument("--window-start", type=int, default=None,
+                    help="first timed decode step (default: the timed steps centred in the trajectory)")
+    ap.add_argument("--pmc-probe", action="store_true", help="the profiled launches, once, for rocprof runs")
     ap.add_argument("--no-attention", action="store_true", help="skip the paged decode-attention leg")
     ap.add_argument("--no-beam", action="store_true", help="skip the beam-reorder (select_rows) leg")
     ap.add_argument("--quant", action="store_true", help="add the fp8 quantised-KV leg (not run by default)")
@@ -362,10 +366,10 @@ class Workload:
                 pool.append_rows(rows, *self.refill)
 
 
-def attention_leg(cfg, pools, B, dev, reps=20, kv_bytes=None):
+def attention_leg(cfg, pools, B, dev, reps=20, kv_bytes=None, probe=False):
     """Decode attention over the pools' current rows: one launch per layer, graph-replayed.
     kv_bytes(pool, lens): the K/V bytes one call reads (default: every visible element in the
-    cache dtype)."""
+    cache dtype).  `probe`: one eager call per layer, nothing timed (for counter runs)."""
     import numpy as np
     import torch
 
@@ -391,6 +395,8 @@ def attention_leg(cfg, pools, B, dev, reps=20, kv_bytes=None):
 
     step()
     torch.cuda.synchronize()
+    if probe:
+        return None
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         step()
@@ -562,7 +568,7 @@ def beam_leg(cfg, wl, dev, reps=20):
     }
 
 
-def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10):
+def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10, probe=None):
     """fp8 quantised pages (QuantPagePool): every layer prefilled as the configuration does (long
     appends in 256-token chunks, each followed by quantisation), then `steps` decode steps of
     append + quantise-what-left-the-window + dequantising gather, graph-replayed; no row churn.
@@ -598,6 +604,18 @@ def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10):
         vin.copy_(wl.v_dec[s])
         step.replay()
 
+    if probe is not None:  # counter runs: prefill, marker, the decode steps, one gather per layer
+        prefill()
+        step.prepare([max(prefill_lengths(cfg)) + s + 1 for s in range(steps)])
+        probe()
+        for s in range(steps):
+            run(s)
+        seq = pools[0].max_len(B)
+        ko, vo = pools[0]._new_out(B, seq)
+        for pool in pools:
+            backend.pool_gather_cold(pool.tensors, pool.cold_tensors, pool.window, ko, vo, B, seq, 0)
+        torch.cuda.synchronize()
+        return None
     prefill()
     for s in range(min(4, steps)):
         run(s)
@@ -692,6 +710,48 @@ def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10):
     }
 
 
+def calibration_pass(dev):
+    """64 MiB read + 64 MiB written by one elementwise kernel, three times: the counters' scale,
+    and the marker after which a probe's window follows."""
+    import torch
+
+    torch.cuda.synchronize()
+    src = torch.zeros(64 * 2**20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.bitwise_not(src, out=dst)
+    torch.cuda.synchronize()
+
+
+def pmc_probe(cfg, wl, start, steps, run_step, dev, quant):
+    """The launches the counter runs profile, as the timed run makes them: the prefill and the
+    steps before the window, the calibration pass, the window's steps, then one decode-attention
+    call per layer over the state they leave (bf16/fp16, head_dim 128).  With `quant`, the fp8
+    leg's prefill, the calibration pass, then its decode steps and one dequantising gather and
+    attention call per layer."""
+    import torch
+
+    L = cfg["layers"]
+    if quant:
+        quant_leg(cfg, wl, steps, dev, 0.0, probe=lambda: calibration_pass(dev))
+        print(json.dumps({"pmc_probe": "quant", "config": cfg["name"], "steps": steps}), flush=True)
+        return
+    wl.prefill()
+    for s in range(start):
+        run_step(s)
+    calibration_pass(dev)
+    for s in range(start, start + steps):
+        run_step(s)
+    torch.cuda.synchronize()
+    attn = cfg["dtype"] in ("bfloat16", "float16") and cfg["dim"] == 128
+    if attn:
+        attention_leg(cfg, wl.pools, cfg["batch"], dev, reps=1, probe=True)
+    total = sum(wl.step_bytes[start:start + steps])
+    print(json.dumps({"pmc_probe": True, "config": cfg["name"], "window_start": start, "steps": steps,
+                      "launches": steps * L, "algorithmic_bytes_per_launch": total / (steps * L),
+                      "attention_calls": L if attn else 0}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -714,31 +774,14 @@ def main():
     warmup = args.warmup if args.warmup is not None else (2 if big else 16)
     repeat = args.repeat if args.repeat is not None else (1 if big else 3)
     mode = args.mode or cfg["mode"]
-    start = window_start(cfg, steps)
+    start = window_start(cfg, steps) if args.window_start is None else args.window_start
+    if args.window_start is not None and (start < 0 or start + steps > cfg["decode"]):
+        raise SystemExit(f"window {start}..{start + steps - 1} is outside the {cfg['decode']}-step trajectory")
     L, B, H, D, P = cfg["layers"], cfg["batch"], cfg["heads"], cfg["dim"], cfg["page"]
     dev = torch.device("cuda", 0)
     wl = Workload(cfg, start + max(steps, warmup), dev)
     pools = wl.pools
     flags = SEPARATE_FINALIZE if args.separate_commit else 0
-
-    if args.pmc_probe:  # prefill + steps before the window, calibration pass (the marker), the window
-        wl.prefill()
-        for s in range(start + steps):
-            if s == start:
-                torch.cuda.synchronize()
-                src = torch.zeros(64 * 2**20, dtype=torch.uint8, device=dev)
-                dst = torch.empty_like(src)
-                for _ in range(3):
-                    torch.bitwise_not(src, out=dst)  # calibration: 64 MiB in + 64 MiB out
-                torch.cuda.synchronize()
-            for layer, pool in enumerate(pools):
-                wl.churn_layer(s, pool)
-                pool.update(wl.k_dec[s, layer], wl.v_dec[s, layer], flags=flags)
-        torch.cuda.synchronize()
-        total = sum(wl.step_bytes[start:start + steps])
-        print(json.dumps({"pmc_probe": True, "config": cfg["name"], "window_start": start, "steps": steps,
-                          "launches": steps * L, "algorithmic_bytes_per_launch": total / (steps * L)}), flush=True)
-        return
 
     graph = None
     last = {}
@@ -769,6 +812,10 @@ def main():
                     marks.append(e)
                 if layer == 0:
                     last["out"] = out
+
+    if args.pmc_probe:
+        pmc_probe(cfg, wl, start, steps, run_step, dev, args.quant)
+        return
 
     # The prefill (untimed for the decode metric; reported on its own for chunked prefill), then
     # warm-up steps at the window.

@@ -118,6 +118,16 @@ def test_torch_binding_module_surface(built):
     assert mod.CTRL_WORDS == paged.CTRL_WORDS == header_define("BARQ_KV_CTRL_WORDS")
 
 
+def test_loader_lists_every_native_source():
+    """The loader's missing-source check names exactly the files the build reads."""
+    from barqtrain_amd import _ffi
+
+    listed = {p.resolve() for p in _ffi._hip_sources()}
+    on_disk = {p.resolve() for p in build.CSRC.iterdir() if p.suffix in (".hip", ".h", ".cpp")}
+    on_disk |= {p.resolve() for p in build.INCLUDE.glob("*.h")}
+    assert listed == on_disk
+
+
 def test_library_is_gfx950_only(built, tmp_path):
     """The fatbin embedded in the library holds one device code object, for gfx950."""
     fatbin = tmp_path / "fatbin.bin"
