@@ -186,12 +186,15 @@ template <int NTHREADS>
 __device__ void commit_append(const barq_kv_pool& p, int batch, int tokens, int limit,
                               const FastDiv& div_page) {
   __shared__ int lds_scan[NTHREADS / kWave];
+  __shared__ int s_incl[NTHREADS];   // rank end of each row of the chunk
+  __shared__ int s_first[NTHREADS];  // first new block of each row of the chunk
   const int top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
   const int mb = (int)p.max_blocks;
+  const int tid = (int)threadIdx.x;
   int used = 0;
   int err = 0;
   for (int r0 = 0; r0 < batch; r0 += NTHREADS) {
-    const int r = r0 + (int)threadIdx.x;
+    const int r = r0 + tid;
     int len = 0, hw = 0;
     NewBlocks nb{0, 0};
     if (r < batch) {
@@ -203,25 +206,42 @@ __device__ void commit_append(const barq_kv_pool& p, int batch, int tokens, int 
     }
     int chunk_total = 0;
     const int excl = block_exclusive_scan<NTHREADS / kWave>(nb.count, lds_scan, &chunk_total);
-    if (r < batch) {
-      for (int j = 0; j < nb.count; ++j) {
-        const int idx = top - 1 - (used + excl + j);
+    s_incl[tid] = excl + nb.count;
+    s_first[tid] = nb.first;
+    __syncthreads();
+    // The chunk's new blocks in rank order, one per thread: rank k belongs to the first row whose
+    // rank end passes k, and takes free_pages[top - 1 - (used + k)].
+    for (int k0 = 0; k0 < chunk_total; k0 += NTHREADS) {
+      const int k = k0 + tid;
+      if (k < chunk_total) {
+        int lo = 0, hi = NTHREADS - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (s_incl[mid] > k) hi = mid;
+          else lo = mid + 1;
+        }
+        const int row_excl = lo > 0 ? s_incl[lo - 1] : 0;
+        const int idx = top - 1 - (used + k);
         const int page = idx >= 0 ? checked_page(p.free_pages[idx], p.num_pages) : -1;
         if (page < 0) err |= BARQ_KV_ERRBIT_POOL_EXHAUSTED;
-        p.block_table[(int64_t)r * mb + nb.first + j] = page;
+        p.block_table[(int64_t)(r0 + lo) * mb + s_first[lo] + (k - row_excl)] = page;
       }
+    }
+    if (r < batch) {
       p.seq_lens[r] = len + tokens;
       p.high_water[r] = max(hw, len + tokens);
     }
     used += chunk_total;
+    __syncthreads();  // s_incl / s_first are rewritten by the next chunk of rows
   }
-  if (threadIdx.x == 0) p.ctrl[BARQ_KV_CTRL_FREE_TOP] = max(0, top - used);
+  if (tid == 0) p.ctrl[BARQ_KV_CTRL_FREE_TOP] = max(0, top - used);
   if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
 }
 
 // The same commit by one wave, from metadata its lanes already hold (batch <= kWave): lane r
 // holds row r's length and high-water mark, lane k holds free_pages[top - 1 - k], the page the
-// k-th new block takes (ranks past the wave are read from the stack).
+// k-th new block takes.  The new blocks are mapped one rank per lane, 64 ranks a round; ranks
+// past the first 64 read their page from the stack, eight rounds' reads in flight at once.
 __device__ void commit_from_lanes(const barq_kv_pool& p, int batch, int tokens, int limit,
                                   const FastDiv& div_page, int len, int hw, int top, int free_k) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -234,18 +254,33 @@ __device__ void commit_from_lanes(const barq_kv_pool& p, int batch, int tokens, 
     if (len + tokens > limit) err |= BARQ_KV_ERRBIT_OUT_SHORT;
   }
   const int incl = wave_incl_scan(nb.count);
-  const int excl = incl - nb.count;
   const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
-  const int most = wave_max(nb.count);
-  for (int j = 0; j < most; ++j) {
-    const int k = excl + j;
-    const int from_lane = __shfl(free_k, k & (kWave - 1), kWave);
-    if (j < nb.count) {
+  constexpr int kGroup = 8;  // 64-rank rounds whose stack reads are in flight together
+  for (int g0 = 0; g0 < total; g0 += kGroup * kWave) {
+    int pg[kGroup];
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      const int k = g0 + u * kWave + lane;
       const int idx = top - 1 - k;
-      int page = -1;
-      if (idx >= 0) page = checked_page(k < kWave ? from_lane : p.free_pages[idx], p.num_pages);
-      if (page < 0) err |= BARQ_KV_ERRBIT_POOL_EXHAUSTED;
-      p.block_table[(int64_t)lane * mb + nb.first + j] = page;
+      pg[u] = -1;
+      if (k < total && idx >= 0) pg[u] = (g0 == 0 && u == 0) ? free_k : p.free_pages[idx];
+    }
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      const int k0 = g0 + u * kWave;
+      if (k0 >= total) break;
+      const int k = k0 + lane;
+      // Rank k belongs to row `row`: the number of rows whose rank end is at most k.
+      int row = 0;
+      for (int r = 0; r < batch; ++r) row += k >= __builtin_amdgcn_readlane(incl, r) ? 1 : 0;
+      const int src = row & (kWave - 1);
+      const int row_first = __shfl(nb.first, src, kWave);
+      const int row_excl = __shfl(incl - nb.count, src, kWave);
+      if (k < total) {
+        const int page = top - 1 - k >= 0 ? checked_page(pg[u], p.num_pages) : -1;
+        if (page < 0) err |= BARQ_KV_ERRBIT_POOL_EXHAUSTED;
+        p.block_table[(int64_t)row * mb + row_first + (k - row_excl)] = page;
+      }
     }
   }
   if (lane < batch) {
@@ -1003,26 +1038,38 @@ __global__ void __launch_bounds__(kThreads) free_rows_kernel(const barq_kv_pool 
     }
     const int cnt = min(ceil_div_fd(p.high_water[r], div_page), mb);
     int32_t* row = p.block_table + (int64_t)r * mb;
-    for (int j0 = 0; j0 < cnt; j0 += kThreads) {
-      const int j = j0 + (int)threadIdx.x;
-      int page = -1, freed = 0;
-      if (j < cnt) {
-        page = checked_page(row[j], p.num_pages);
-        freed = page >= 0;
-        if (freed && p.page_shares) {
-          freed = atomicSub(&p.page_shares[page], 1) == 0;
-          if (freed) p.page_shares[page] = 0;
+    constexpr int kGroup = 4;  // chunks of kThreads blocks whose entries are read together
+    for (int g0 = 0; g0 < cnt; g0 += kGroup * kThreads) {
+      int entry[kGroup];
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        const int j = g0 + u * kThreads + (int)threadIdx.x;
+        entry[u] = j < cnt ? row[j] : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        const int j0 = g0 + u * kThreads;
+        if (j0 >= cnt) break;
+        const int j = j0 + (int)threadIdx.x;
+        int page = -1, freed = 0;
+        if (j < cnt) {
+          page = checked_page(entry[u], p.num_pages);
+          freed = page >= 0;
+          if (freed && p.page_shares) {
+            freed = atomicSub(&p.page_shares[page], 1) == 0;
+            if (freed) p.page_shares[page] = 0;
+          }
+          row[j] = -1;
         }
-        row[j] = -1;
+        int chunk_total = 0;
+        const int excl = block_exclusive_scan<kWaves>(freed, lds_scan, &chunk_total);
+        if (freed) {
+          const int64_t slot = (int64_t)top + pushed + excl;
+          if (slot < p.num_pages) p.free_pages[slot] = page;
+          else err |= BARQ_KV_ERRBIT_BAD_INDEX;
+        }
+        pushed += chunk_total;
       }
-      int chunk_total = 0;
-      const int excl = block_exclusive_scan<kWaves>(freed, lds_scan, &chunk_total);
-      if (freed) {
-        const int64_t slot = (int64_t)top + pushed + excl;
-        if (slot < p.num_pages) p.free_pages[slot] = page;
-        else err |= BARQ_KV_ERRBIT_BAD_INDEX;
-      }
-      pushed += chunk_total;
     }
     __syncthreads();  // every thread has read the row's mark before it is cleared
     if (threadIdx.x == 0) {

@@ -408,6 +408,47 @@ def test_misaligned_inputs_use_narrow_vectors(capi):
     compare_layer(pool, oracle, got, "misaligned")
 
 
+@pytest.mark.parametrize("flags", [0, SEPARATE_FINALIZE])
+def test_commits_that_map_thousands_of_blocks(capi, flags):
+    """Commits that map many new blocks at once: 600 rows (wider than a wave: the workgroup
+    commit, several chunks of rows and of ranks), then one 5000-token row (the one-wave commit,
+    1250 ranks: several rounds of 64 and of the grouped stack reads), which is freed again
+    (1250 block-table entries read back in groups)."""
+    H, D, P = 2, 8, 4
+    gen = torch.Generator().manual_seed(77)
+    B, T = 600, 37
+    cap = 2 * T + 1
+    pool = make_pool(cap, B, H, D, P, torch.float32)
+    oracle = DenseLayerOracle(B, cap, P)
+    for t in (T, 1, T):
+        k = hf_layout(B, H, t, D, torch.float32, gen)
+        v = hf_layout(B, H, t, D, torch.float32, gen)
+        got = pool.update(k.cuda(), v.cuda(), oracle.get_seq_length() + t, flags)
+        oracle.append(to_bits(k), to_bits(v))
+        compare_layer(pool, oracle, got, f"600 rows after {t}")
+    pool.check_invariants()
+    assert pool.errors() == 0
+
+    T1 = 5000
+    pool = make_pool(T1 + 1, 2, H, D, P, torch.float32)
+    oracle = DenseLayerOracle(2, T1 + 1, P)
+    k = hf_layout(1, H, T1, D, torch.float32, gen)
+    v = hf_layout(1, H, T1, D, torch.float32, gen)
+    pool.append(k.cuda(), v.cuda())
+    oracle.append(to_bits(k), to_bits(v))
+    k = hf_layout(2, H, 1, D, torch.float32, gen)
+    got = pool.update(k.cuda(), k.cuda(), T1 + 1, flags)
+    oracle.append(to_bits(k), to_bits(k))
+    compare_layer(pool, oracle, got, "one long row")
+    pool.check_invariants()
+    pool.free_rows([0])
+    oracle.release_rows([0])
+    assert pool.free_top() == pool.num_pages - 1  # row 1 keeps its one page
+    compare_layer(pool, oracle, None, "after freeing the long row")
+    pool.check_invariants()
+    assert pool.errors() == 0
+
+
 def test_empty_batch_and_zero_tokens(capi):
     H, D, P = 2, 8, 4
     pool = make_pool(16, 2, H, D, P, torch.float32)
