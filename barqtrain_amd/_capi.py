@@ -51,6 +51,7 @@ class BarqKVCold(ctypes.Structure):
         ("key_scales", c_ptr),
         ("value_scales", c_ptr),
         ("free_cold", c_ptr),
+        ("cold_shares", c_ptr),
         ("num_cold", c_i64),
         ("window", c_i64),
         ("element_type", c_i64),
@@ -87,6 +88,8 @@ _SIGNATURES = {
     "barq_kv_update_cold": (ctypes.c_int, [_POOL, _COLD, c_ptr, c_ptr] + [c_i64] * 5 + [c_ptr, c_ptr]
                             + [c_i64] * 5 + [c_ptr]),
     "barq_kv_free_rows_cold": (ctypes.c_int, [_POOL, _COLD, c_ptr, c_i64, c_ptr]),
+    "barq_kv_select_rows_cold_layers": (ctypes.c_int, [_POOL, _COLD, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_ptr]),
+    "barq_kv_crop_cold": (ctypes.c_int, [_POOL, _COLD, c_i64, c_i64, c_ptr]),
     "barq_kv_decode_attention_cold": (ctypes.c_int, [_POOL, _COLD, c_ptr] + [c_i64] * 6 + [c_ptr] + [c_i64] * 3
                                       + [ctypes.c_float] + [c_i64] * 3 + [c_ptr, c_i64, c_ptr]),
 }

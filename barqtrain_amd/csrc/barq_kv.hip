@@ -1239,6 +1239,12 @@ struct SelectPool {  // the per-pool pointers of a barq_kv_pool
 struct SelectArgs {
   SelectPool pools[kSelectPools];
   int32_t num_pages[kSelectPools];
+  // Pools with fp8 cold stores (cold != 0): quantised blocks are shared by reference, counted in
+  // cold_shares and released to free_cold; every hot block is tail (moved or copied).
+  int32_t* cold_shares[kSelectPools];
+  int32_t* free_cold[kSelectPools];
+  int32_t num_cold[kSelectPools];
+  int32_t cold;
   const int32_t* rows;
   int32_t* ws;            // per pool, ws_pool_words: see SelectWs
   int64_t ws_pool_words;
@@ -1285,6 +1291,20 @@ __device__ __forceinline__ void tail_blocks(const SelectPool& p, int r, int mb, 
   *count = nb - f;
 }
 
+// A block-table entry naming cold page -2 - e of a store of num_cold pages.
+__device__ __forceinline__ bool cold_entry(int e, int num_cold) { return e <= -2 && -2 - e < num_cold; }
+
+// The blocks a selection moves or copies: the tail, or, in a pool with a cold store, every block
+// below the high-water mark (the cold ones among them are shared instead).
+__device__ __forceinline__ void select_blocks(const SelectArgs& a, const SelectPool& p, int r, int* first,
+                                              int* count) {
+  tail_blocks(p, r, a.max_blocks, a.div_page, first, count);
+  if (a.cold) {
+    *count += *first;
+    *first = 0;
+  }
+}
+
 __global__ void __launch_bounds__(kThreads) select_plan_kernel(const SelectArgs a) {
   __shared__ int s_first[kSelectMaxBatch];
   __shared__ int lds_scan[kWaves];
@@ -1309,13 +1329,16 @@ __global__ void __launch_bounds__(kThreads) select_plan_kernel(const SelectArgs 
       const int r = a.rows[q];
       if (r >= 0 && r < a.max_batch) {
         int f, cnt;
-        tail_blocks(p, r, mb, a.div_page, &f, &cnt);
-        if (s_first[r] != q) {
+        select_blocks(a, p, r, &f, &cnt);
+        if (s_first[r] != q && !a.cold) {
           c = cnt;
         } else {
+          const int ncold = a.num_cold[blockIdx.x];
           for (int t = 0; t < cnt; ++t) {
-            const int page = checked_page(p.block_table[(int64_t)r * mb + f + t], num_pages);
-            c += page < 0 || p.page_shares[page] != 0;
+            const int e = p.block_table[(int64_t)r * mb + f + t];
+            if (a.cold && cold_entry(e, ncold)) continue;  // shared
+            const int page = checked_page(e, num_pages);
+            c += s_first[r] != q || page < 0 || p.page_shares[page] != 0;
           }
         }
       }
@@ -1350,7 +1373,7 @@ __global__ void __launch_bounds__(kThreads) select_build_kernel(const SelectArgs
     const int r = a.rows[i];
     const bool valid = r >= 0 && r < a.max_batch;
     int f = 0, cnt = 0;
-    if (valid) tail_blocks(p, r, mb, a.div_page, &f, &cnt);
+    if (valid) select_blocks(a, p, r, &f, &cnt);
     else atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], BARQ_KV_ERRBIT_BAD_INDEX);
     w.lens[i] = valid ? p.seq_lens[r] : 0;
     w.marks[i] = valid ? p.high_water[r] : 0;
@@ -1379,14 +1402,21 @@ __global__ void __launch_bounds__(kThreads) select_build_kernel(const SelectArgs
   // The tail, in chunks of one block per thread: moved blocks keep their page, the others take
   // the next pages of the row's range on the stack and are copied by the whole workgroup.
   const int nvec = (int)(a.page_bytes / VB);
+  const int ncold = a.num_cold[blockIdx.y];
   int done = 0;
   for (int t0 = 0; t0 < cnt; t0 += kThreads) {
     const int t = t0 + (int)threadIdx.x;
-    int page = -1, copy = 0;
+    int page = -1, copy = 0;  // page: the entry kept when nothing is copied
     if (t < cnt) {
-      page = checked_page(src_row[f + t], num_pages);
-      if (page < 0) err |= BARQ_KV_ERRBIT_BAD_INDEX;
-      copy = !(taker && page >= 0 && p.page_shares[page] == 0);
+      const int e = src_row[f + t];
+      if (a.cold && cold_entry(e, ncold)) {  // a quantised block never changes: shared
+        page = e;
+        atomicAdd(&a.cold_shares[blockIdx.y][-2 - e], 1);
+      } else {
+        page = checked_page(e, num_pages);
+        if (page < 0) err |= BARQ_KV_ERRBIT_BAD_INDEX;
+        copy = !(taker && page >= 0 && p.page_shares[page] == 0);
+      }
     }
     int chunk_copies = 0;
     const int k = block_exclusive_scan<kWaves>(copy, lds_scan, &chunk_copies);
@@ -1426,13 +1456,26 @@ __global__ void __launch_bounds__(kThreads) select_settle_kernel(const SelectArg
   if (!*w.go) return;  // uniform
   int32_t* row = p.block_table + (int64_t)r * mb;
   int f, nb;
-  tail_blocks(p, r, mb, a.div_page, &f, &nb);
+  select_blocks(a, p, r, &f, &nb);
   nb += f;
   const int taker = w.first[r];
   const int32_t* kept = taker >= 0 ? w.table + (int64_t)taker * mb : nullptr;
+  const int ncold = a.num_cold[blockIdx.y];
   int err = 0;
   for (int j = threadIdx.x; j < nb; j += kThreads) {
-    const int page = checked_page(row[j], num_pages);
+    const int e = row[j];
+    if (a.cold && cold_entry(e, ncold)) {  // the old row's reference to a quantised block
+      const int c = -2 - e;
+      int32_t* shares = a.cold_shares[blockIdx.y];
+      if (atomicSub(&shares[c], 1) == 0) {
+        shares[c] = 0;
+        const int slot = atomicAdd(&p.ctrl[BARQ_KV_CTRL_COLD_TOP], 1);
+        if (slot < ncold) a.free_cold[blockIdx.y][slot] = c;
+        else err |= BARQ_KV_ERRBIT_BAD_INDEX;
+      }
+      continue;
+    }
+    const int page = checked_page(e, num_pages);
     if (page < 0) continue;
     if (kept && j >= f && kept[j] == page) continue;  // moved to its first taker
     if (atomicSub(&p.page_shares[page], 1) == 0) {
@@ -1703,6 +1746,69 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   return BARQ_KV_OK;
 }
 
+// barq_kv_select_rows_layers, and with `colds` (one per pool) its cold-store form.
+int select_rows_impl(const barq_kv_pool* pools, const barq_kv_cold* colds, int64_t num_pools,
+                     const int32_t* src_rows, int64_t num_rows, int32_t* workspace, int64_t workspace_words,
+                     void* stream) {
+  if (!pools || num_pools < 1) return BARQ_KV_ERR_INVALID;
+  const barq_kv_pool& g = pools[0];
+  for (int64_t l = 0; l < num_pools; ++l) {
+    const barq_kv_pool& p = pools[l];
+    if (!pool_ok(&p) || !p.page_shares || p.num_pages > kI32Max) return BARQ_KV_ERR_INVALID;
+    if (p.max_batch != g.max_batch || p.max_blocks != g.max_blocks || p.page_size != g.page_size ||
+        p.kv_heads != g.kv_heads || p.head_dim != g.head_dim || p.elem_bytes != g.elem_bytes)
+      return BARQ_KV_ERR_INVALID;
+    for (int64_t m = 0; m < l; ++m)  // a pool named twice would release its rows twice
+      if (pools[m].block_table == p.block_table || pools[m].ctrl == p.ctrl || pools[m].page_shares == p.page_shares)
+        return BARQ_KV_ERR_INVALID;
+    if (colds) {
+      const barq_kv_cold& c = colds[l];
+      if (!c.cold_shares || !c.free_cold || c.num_cold < 1 || c.num_cold >= kI32Max - 2) return BARQ_KV_ERR_INVALID;
+      for (int64_t m = 0; m < l; ++m)
+        if (colds[m].cold_shares == c.cold_shares || colds[m].free_cold == c.free_cold) return BARQ_KV_ERR_INVALID;
+    }
+  }
+  if (num_rows < 0 || num_rows > g.max_batch || g.max_batch > kSelectMaxBatch || g.max_blocks > kI32Max)
+    return BARQ_KV_ERR_INVALID;
+  const int64_t ws_pool_words = select_ws_pool_words(num_rows, g.max_blocks, g.max_batch);
+  if ((num_rows > 0 && !src_rows) || !workspace ||
+      workspace_words < std::min<int64_t>(num_pools, kSelectPools) * ws_pool_words)
+    return BARQ_KV_ERR_INVALID;
+  SelectArgs a;
+  a.rows = src_rows;
+  a.ws = workspace;
+  a.ws_pool_words = ws_pool_words;
+  a.page_bytes = g.page_size * g.kv_heads * g.head_dim * g.elem_bytes;
+  a.n = (int32_t)num_rows;
+  a.max_batch = (int32_t)g.max_batch;
+  a.max_blocks = (int32_t)g.max_blocks;
+  a.div_page = FastDiv::make((uint32_t)g.page_size);
+  a.cold = colds ? 1 : 0;
+  hipStream_t s = (hipStream_t)stream;
+  int rc = BARQ_KV_OK;
+  for (int64_t l0 = 0; l0 < num_pools && rc == BARQ_KV_OK; l0 += kSelectPools) {
+    const int set = (int)std::min<int64_t>(kSelectPools, num_pools - l0);
+    uint64_t bits = (uint64_t)a.page_bytes;
+    for (int k = 0; k < kSelectPools; ++k) {
+      const barq_kv_pool& p = pools[l0 + std::min(k, set - 1)];
+      a.pools[k] = SelectPool{(const char*)p.key_pages, (const char*)p.value_pages, p.block_table, p.seq_lens,
+                              p.high_water, p.free_pages, p.ctrl, p.page_shares};
+      a.num_pages[k] = (int32_t)p.num_pages;
+      const barq_kv_cold* c = colds ? &colds[l0 + std::min(k, set - 1)] : nullptr;
+      a.cold_shares[k] = c ? c->cold_shares : nullptr;
+      a.free_cold[k] = c ? c->free_cold : nullptr;
+      a.num_cold[k] = c ? (int32_t)c->num_cold : 0;
+      bits |= (uint64_t)(uintptr_t)p.key_pages | (uint64_t)(uintptr_t)p.value_pages;
+    }
+    rc = launch((const void*)&select_plan_kernel, dim3((uint32_t)set), &a, s);
+    if (rc == BARQ_KV_OK && num_rows > 0)
+      rc = launch_select_build_kernel(vector_bytes(bits), dim3((uint32_t)num_rows, (uint32_t)set), &a, s);
+    if (rc == BARQ_KV_OK)
+      rc = launch((const void*)&select_settle_kernel, dim3((uint32_t)g.max_batch, (uint32_t)set), &a, s);
+  }
+  return rc;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1852,52 +1958,14 @@ int64_t barq_kv_select_workspace_words(const barq_kv_pool* pool, int64_t num_poo
 int barq_kv_select_rows_layers(const barq_kv_pool* pools, int64_t num_pools, const int32_t* src_rows,
                                int64_t num_rows, int32_t* workspace, int64_t workspace_words,
                                void* stream) {
-  if (!pools || num_pools < 1) return BARQ_KV_ERR_INVALID;
-  const barq_kv_pool& g = pools[0];
-  for (int64_t l = 0; l < num_pools; ++l) {
-    const barq_kv_pool& p = pools[l];
-    if (!pool_ok(&p) || !p.page_shares || p.num_pages > kI32Max) return BARQ_KV_ERR_INVALID;
-    if (p.max_batch != g.max_batch || p.max_blocks != g.max_blocks || p.page_size != g.page_size ||
-        p.kv_heads != g.kv_heads || p.head_dim != g.head_dim || p.elem_bytes != g.elem_bytes)
-      return BARQ_KV_ERR_INVALID;
-    for (int64_t m = 0; m < l; ++m)  // a pool named twice would release its rows twice
-      if (pools[m].block_table == p.block_table || pools[m].ctrl == p.ctrl || pools[m].page_shares == p.page_shares)
-        return BARQ_KV_ERR_INVALID;
-  }
-  if (num_rows < 0 || num_rows > g.max_batch || g.max_batch > kSelectMaxBatch || g.max_blocks > kI32Max)
-    return BARQ_KV_ERR_INVALID;
-  const int64_t ws_pool_words = select_ws_pool_words(num_rows, g.max_blocks, g.max_batch);
-  if ((num_rows > 0 && !src_rows) || !workspace ||
-      workspace_words < std::min<int64_t>(num_pools, kSelectPools) * ws_pool_words)
-    return BARQ_KV_ERR_INVALID;
-  SelectArgs a;
-  a.rows = src_rows;
-  a.ws = workspace;
-  a.ws_pool_words = ws_pool_words;
-  a.page_bytes = g.page_size * g.kv_heads * g.head_dim * g.elem_bytes;
-  a.n = (int32_t)num_rows;
-  a.max_batch = (int32_t)g.max_batch;
-  a.max_blocks = (int32_t)g.max_blocks;
-  a.div_page = FastDiv::make((uint32_t)g.page_size);
-  hipStream_t s = (hipStream_t)stream;
-  int rc = BARQ_KV_OK;
-  for (int64_t l0 = 0; l0 < num_pools && rc == BARQ_KV_OK; l0 += kSelectPools) {
-    const int set = (int)std::min<int64_t>(kSelectPools, num_pools - l0);
-    uint64_t bits = (uint64_t)a.page_bytes;
-    for (int k = 0; k < kSelectPools; ++k) {
-      const barq_kv_pool& p = pools[l0 + std::min(k, set - 1)];
-      a.pools[k] = SelectPool{(const char*)p.key_pages, (const char*)p.value_pages, p.block_table, p.seq_lens,
-                              p.high_water, p.free_pages, p.ctrl, p.page_shares};
-      a.num_pages[k] = (int32_t)p.num_pages;
-      bits |= (uint64_t)(uintptr_t)p.key_pages | (uint64_t)(uintptr_t)p.value_pages;
-    }
-    rc = launch((const void*)&select_plan_kernel, dim3((uint32_t)set), &a, s);
-    if (rc == BARQ_KV_OK && num_rows > 0)
-      rc = launch_select_build_kernel(vector_bytes(bits), dim3((uint32_t)num_rows, (uint32_t)set), &a, s);
-    if (rc == BARQ_KV_OK)
-      rc = launch((const void*)&select_settle_kernel, dim3((uint32_t)g.max_batch, (uint32_t)set), &a, s);
-  }
-  return rc;
+  return select_rows_impl(pools, nullptr, num_pools, src_rows, num_rows, workspace, workspace_words, stream);
+}
+
+int barq_kv_select_rows_cold_layers(const barq_kv_pool* pools, const barq_kv_cold* colds, int64_t num_pools,
+                                    const int32_t* src_rows, int64_t num_rows, int32_t* workspace,
+                                    int64_t workspace_words, void* stream) {
+  if (!colds) return BARQ_KV_ERR_INVALID;
+  return select_rows_impl(pools, colds, num_pools, src_rows, num_rows, workspace, workspace_words, stream);
 }
 
 int barq_kv_select_rows(const barq_kv_pool* pool, const int32_t* src_rows, int64_t num_rows,

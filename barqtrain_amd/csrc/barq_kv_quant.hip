@@ -80,6 +80,7 @@ struct ColdPtrs {
   uint8_t* key_scales;
   uint8_t* value_scales;
   int32_t* free_cold;
+  int32_t* shares;     // references beyond the first, or null
   int64_t num_cold;
   int32_t window;
 };
@@ -501,6 +502,8 @@ __global__ void __launch_bounds__(kThreads) free_rows_cold_kernel(const FreeArgs
         if (e <= -2) cold = checked_id(-2 - e, a.c.num_cold);
         if (hot >= 0 && p.page_shares && atomicSub(&p.page_shares[hot], 1) != 0) hot = -1;
         else if (hot >= 0 && p.page_shares) p.page_shares[hot] = 0;
+        if (cold >= 0 && a.c.shares && atomicSub(&a.c.shares[cold], 1) != 0) cold = -1;
+        else if (cold >= 0 && a.c.shares) a.c.shares[cold] = 0;
         row[j] = -1;
       }
       int hot_n = 0, cold_n = 0;
@@ -535,7 +538,103 @@ __global__ void __launch_bounds__(kThreads) free_rows_cold_kernel(const FreeArgs
 __global__ void cold_reset_kernel(ColdPtrs c, int32_t* ctrl) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < c.num_cold) c.free_cold[i] = (int32_t)(c.num_cold - 1 - i);
+  if (i < c.num_cold && c.shares) c.shares[i] = 0;
   if (i == 0) ctrl[BARQ_KV_CTRL_COLD_TOP] = (int32_t)c.num_cold;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Crop with a cold store: workgroup per row.  The row's quantised blocks from the one holding its
+// new length on are re-opened: a page popped from free_pages receives the block's dequantised K
+// and V (code * 2^e rounded to the element type, as the gather reads it), the block maps it, and
+// the cold page loses the reference.
+// ---------------------------------------------------------------------------------------------
+
+struct CropArgs {
+  barq_kv_pool p;
+  ColdPtrs c;
+  int32_t batch;
+  int32_t max_length;
+  FastDiv div_page;
+};
+
+template <int KIND>
+__global__ void __launch_bounds__(kThreads) crop_cold_kernel(const CropArgs a) {
+  using E = Elem<KIND>;
+  using Bits = typename E::Bits;
+  __shared__ int lds_scan[kWaves];
+  __shared__ int s_block[kThreads];  // the chunk's re-opened blocks ...
+  __shared__ int s_hot[kThreads];    // ... and the pages they take (-1: none left)
+  __shared__ int s_base;
+  const barq_kv_pool& p = a.p;
+  const int r = blockIdx.x;
+  const int mb = (int)p.max_blocks;
+  const int P = (int)p.page_size, H = (int)p.kv_heads, D = (int)p.head_dim;
+  const int HD = H * D;
+  const int len = min(p.seq_lens[r], a.max_length);
+  const int first = (int)a.div_page.div((uint32_t)len);
+  const int nb = min(ceil_div_fd(p.high_water[r], a.div_page), mb);
+  int32_t* row = p.block_table + (int64_t)r * mb;
+  int err = 0;
+  for (int j0 = first; j0 < nb; j0 += kThreads) {
+    const int j = j0 + (int)threadIdx.x;
+    int c = -1;
+    if (j < nb) {
+      const int e = row[j];
+      if (e <= -2) c = checked_id(-2 - e, a.c.num_cold);
+    }
+    int count = 0;
+    const int k = block_exclusive_scan(c >= 0, lds_scan, &count);
+    if (threadIdx.x == 0 && count > 0) {
+      const int before = atomicSub(&p.ctrl[BARQ_KV_CTRL_FREE_TOP], count);
+      const int got = max(0, min(before, count));
+      if (got < count) {
+        atomicAdd(&p.ctrl[BARQ_KV_CTRL_FREE_TOP], count - got);
+        err |= BARQ_KV_ERRBIT_POOL_EXHAUSTED;
+      }
+      s_base = before - got;  // pages [s_base, s_base + got) of the stack, the top one first
+      s_hot[0] = got;         // read before the per-block entries below are written
+    }
+    __syncthreads();
+    const int got = s_hot[0], base = s_base;
+    __syncthreads();
+    if (c >= 0) {
+      s_block[k] = j;
+      s_hot[k] = k < got ? checked_id(p.free_pages[base + got - 1 - k], p.num_pages) : -1;
+      if (k < got && s_hot[k] < 0) err |= BARQ_KV_ERRBIT_BAD_INDEX;
+    }
+    __syncthreads();
+    for (int q = 0; q < min(count, got); ++q) {
+      const int jb = s_block[q], hp = s_hot[q];
+      const int cp = -2 - row[jb];  // every thread reads the entry before thread 0 rewrites it
+      __syncthreads();
+      if (hp < 0) continue;  // uniform
+      Bits* kp = (Bits*)p.key_pages + (int64_t)hp * P * HD;
+      Bits* vp = (Bits*)p.value_pages + (int64_t)hp * P * HD;
+      const uint8_t* kc = a.c.codes[0] + (int64_t)cp * P * HD;
+      const uint8_t* vc = a.c.codes[1] + (int64_t)cp * P * HD;
+      for (int i = threadIdx.x; i < P * HD; i += kThreads) {
+        const int t = i / HD, hd = i - t * HD, h = hd / D;
+        const int ek = (int)a.c.key_scales[(int64_t)cp * HD + hd] - 127;
+        const int ev = (int)a.c.value_scales[((int64_t)cp * P + t) * H + h] - 127;
+        kp[i] = E::from_float(ldexpf(e4m3_decode(kc[i]), ek));
+        vp[i] = E::from_float(ldexpf(e4m3_decode(vc[i]), ev));
+      }
+      __syncthreads();  // the cold page is read in full before it can return to the stack
+      if (threadIdx.x == 0) {
+        row[jb] = hp;
+        if (!a.c.shares || atomicSub(&a.c.shares[cp], 1) == 0) {
+          if (a.c.shares) a.c.shares[cp] = 0;
+          const int slot = atomicAdd(&p.ctrl[BARQ_KV_CTRL_COLD_TOP], 1);
+          if (slot < a.c.num_cold) a.c.free_cold[slot] = cp;
+          else err |= BARQ_KV_ERRBIT_BAD_INDEX;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  __syncthreads();  // every thread has read the row's length before it is lowered
+  if (threadIdx.x == 0 && r < a.batch) p.seq_lens[r] = len;
+  if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -570,6 +669,7 @@ ColdPtrs cold_ptrs(const barq_kv_cold* c) {
   r.key_scales = (uint8_t*)c->key_scales;
   r.value_scales = (uint8_t*)c->value_scales;
   r.free_cold = c->free_cold;
+  r.shares = c->cold_shares;
   r.num_cold = c->num_cold;
   r.window = (int32_t)c->window;
   return r;
@@ -699,6 +799,22 @@ int barq_kv_update_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, cons
     rc = barq_kv_gather_cold(pool, cold, key_out, value_out, batch, seq_out, osb, osh, oss,
                              flags & BARQ_KV_SEQ_FROM_DEVICE, stream);
   return rc;
+}
+
+int barq_kv_crop_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, int64_t batch, int64_t max_length,
+                      void* stream) {
+  if (!cold_ok(pool, cold) || batch < 0 || batch > pool->max_batch) return BARQ_KV_ERR_INVALID;
+  if (batch == 0) return BARQ_KV_OK;
+  CropArgs a;
+  a.p = *pool;
+  a.c = cold_ptrs(cold);
+  a.batch = (int32_t)batch;
+  a.max_length = (int32_t)std::max<int64_t>(0, std::min<int64_t>(max_length, kI32Max));
+  a.div_page = FastDiv::make((uint32_t)pool->page_size);
+  const void* fn = cold->element_type == BARQ_KV_BF16   ? (const void*)&crop_cold_kernel<BARQ_KV_BF16>
+                   : cold->element_type == BARQ_KV_FP16 ? (const void*)&crop_cold_kernel<BARQ_KV_FP16>
+                                                        : (const void*)&crop_cold_kernel<BARQ_KV_FP32>;
+  return launch(fn, dim3((uint32_t)batch), &a, (hipStream_t)stream);
 }
 
 int barq_kv_free_rows_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, const int32_t* rows,

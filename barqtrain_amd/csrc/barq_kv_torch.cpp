@@ -248,28 +248,30 @@ void pool_select_rows_(std::vector<at::Tensor> pool, at::Tensor rows, at::Tensor
                "pool_select_rows_");
 }
 
-// A pool's fp8 cold store as (key_codes, value_codes, key_scales, value_scales, free_cold), the
-// tensors of barqtrain_amd.paged.ColdStore, and its residual window in tokens.
+// A pool's fp8 cold store as (key_codes, value_codes, key_scales, value_scales, free_cold,
+// cold_shares), the tensors of barqtrain_amd.paged.QuantPagePool, and its residual window.
 barq_kv_cold cold_from(const barq_kv_pool& p, const at::Tensor& pages, const std::vector<at::Tensor>& t,
                        int64_t window) {
-  TORCH_CHECK(t.size() == 5, "a cold store is 5 tensors");
-  for (size_t i = 0; i < 5; ++i)
+  TORCH_CHECK(t.size() == 6, "a cold store is 6 tensors");
+  for (size_t i = 0; i < 6; ++i)
     TORCH_CHECK(t[i].is_cuda() && t[i].is_contiguous() && t[i].get_device() == pages.get_device() &&
                     t[i].scalar_type() == (i < 4 ? at::kByte : at::kInt),
-                "cold-store tensors must be contiguous (uint8 codes and scales, int32 free list) on the pool's device");
+                "cold-store tensors must be contiguous (uint8 codes and scales, int32 free list and shares) on the "
+                "pool's device");
   const int64_t n = t[0].size(0);
   TORCH_CHECK(t[0].dim() == 4 && t[0].size(1) == p.page_size && t[0].size(2) == p.kv_heads &&
                   t[0].size(3) == p.head_dim && t[1].sizes() == t[0].sizes(),
               "codes must be [num_cold, page_size, kv_heads, head_dim]");
   TORCH_CHECK(t[2].numel() == n * p.kv_heads * p.head_dim && t[3].numel() == n * p.page_size * p.kv_heads &&
-                  t[4].numel() == n,
-              "cold-store scale / free-list sizes do not match num_cold");
+                  t[4].numel() == n && t[5].numel() == n,
+              "cold-store scale / free-list / shares sizes do not match num_cold");
   barq_kv_cold c;
   c.key_codes = t[0].data_ptr();
   c.value_codes = t[1].data_ptr();
   c.key_scales = t[2].data_ptr();
   c.value_scales = t[3].data_ptr();
   c.free_cold = t[4].data_ptr<int32_t>();
+  c.cold_shares = t[5].data_ptr<int32_t>();
   c.num_cold = n;
   c.window = window;
   const auto dt = pages.scalar_type();
@@ -332,6 +334,37 @@ void pool_free_rows_cold_(std::vector<at::Tensor> pool, std::vector<at::Tensor> 
   c10::DeviceGuard guard(pool[0].device());
   check_status(barq_kv_free_rows_cold(&p, &c, rows.data_ptr<int32_t>(), rows.numel(), current_stream(pool[0])),
                "pool_free_rows_cold_");
+}
+
+void pool_crop_cold_(std::vector<at::Tensor> pool, std::vector<at::Tensor> cold, int64_t window, int64_t batch,
+                     int64_t max_length) {
+  barq_kv_pool p = pool_from(pool);
+  barq_kv_cold c = cold_from(p, pool[0], cold, window);
+  c10::DeviceGuard guard(pool[0].device());
+  check_status(barq_kv_crop_cold(&p, &c, batch, max_length, current_stream(pool[0])), "pool_crop_cold_");
+}
+
+// One selection applied to pools with cold stores (a model's layers): pools[i] with colds[i].
+void pool_select_rows_cold_(std::vector<std::vector<at::Tensor>> pools, std::vector<std::vector<at::Tensor>> colds,
+                            int64_t window, at::Tensor rows, at::Tensor workspace) {
+  TORCH_CHECK(!pools.empty() && pools.size() == colds.size(), "one cold store per pool");
+  std::vector<barq_kv_pool> ps;
+  std::vector<barq_kv_cold> cs;
+  for (size_t i = 0; i < pools.size(); ++i) {
+    ps.push_back(pool_from(pools[i]));
+    cs.push_back(cold_from(ps.back(), pools[i][0], colds[i], window));
+    TORCH_CHECK(pools[i][0].get_device() == rows.get_device(), "the pools and rows must share a device");
+  }
+  TORCH_CHECK(rows.is_cuda() && rows.scalar_type() == at::kInt && rows.is_contiguous(),
+              "rows must be contiguous int32 on the pools' device");
+  TORCH_CHECK(workspace.is_cuda() && workspace.scalar_type() == at::kInt && workspace.is_contiguous() &&
+                  workspace.get_device() == rows.get_device(),
+              "workspace must be contiguous int32 on the pools' device");
+  c10::DeviceGuard guard(rows.device());
+  check_status(barq_kv_select_rows_cold_layers(ps.data(), cs.data(), (int64_t)ps.size(), rows.data_ptr<int32_t>(),
+                                               rows.numel(), workspace.data_ptr<int32_t>(), workspace.numel(),
+                                               current_stream(rows)),
+               "pool_select_rows_cold_");
 }
 
 // The pools of a model's layers packed as an array of barq_kv_pool (a CPU uint8 tensor), for
@@ -456,6 +489,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("pool_gather_cold", &pool_gather_cold, "Materialise rows of a pool with a cold store, dequantising");
   m.def("pool_update_cold_", &pool_update_cold_, "Append, compress, materialise (pool with a cold store)");
   m.def("pool_free_rows_cold_", &pool_free_rows_cold_, "Return rows' hot and cold pages");
+  m.def("pool_crop_cold_", &pool_crop_cold_, "Clamp row lengths, re-opening quantised blocks past them");
+  m.def("pool_select_rows_cold_", &pool_select_rows_cold_,
+        "One row selection applied to pools with cold stores, sharing quantised blocks");
   m.def("pool_group", &pool_group, "Pack the pools of a model's layers for the batched entry points");
   m.def("select_workspace_words", &select_workspace_words, "Workspace words of pool_group_select_rows_");
   m.def("pool_group_select_rows_", &pool_group_select_rows_,

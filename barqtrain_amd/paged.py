@@ -529,10 +529,16 @@ class QuantPagePool(PagePool):
     Full-precision ("hot") pages hold each row's last ``window`` tokens and its partial block: an
     append writes there, the blocks that left the window are quantised (``barq_kv_compress``)
     and reads dequantise (``barq_kv_gather_cold``).  Appends longer than ``chunk`` tokens
-    (prefill) run in chunks, so the hot pool needs ``max_batch * (ceil((window + chunk) / P) +
-    2)`` pages (the default); the cold store defaults to every block that can lie wholly before
-    the window, ``max_batch * (max_blocks - window // P)``.  A crop
-    must stay at or above the quantised blocks; beam selection is not available on this pool.
+    (prefill) run in chunks, so a row holds at most ``ceil((window + chunk) / P) + 2`` hot pages,
+    and ``ceil(window / P) + 1`` between appends.  The default pool is the sum of the two per row:
+    a beam selection copies hot blocks before the ones it drops return, which takes at most the
+    second term per row.  The cold store defaults to every block that can lie wholly before the
+    window, ``max_batch * (max_blocks - window // P)``.
+
+    Beam selection (``select_rows``) shares quantised blocks between rows by reference (they
+    never change) and moves or copies the hot ones, so a hot page always has one holder.  A crop
+    below a row's quantised blocks re-opens them: their dequantised contents become hot pages
+    again (lossy, as any read of them is) and are quantised anew when they leave the window.
     """
 
     quantized = True
@@ -549,8 +555,8 @@ class QuantPagePool(PagePool):
         self.chunk = int(chunk)
         P = int(page_size)
         if num_pages is None:
-            num_pages = min(int(max_batch) * (-(-(self.window + self.chunk) // P) + 2),
-                            int(max_batch) * (int(max_blocks) + 1))
+            per_row = (-(-(self.window + self.chunk) // P) + 2) + (-(-self.window // P) + 1)
+            num_pages = min(int(max_batch) * per_row, int(max_batch) * (int(max_blocks) + 1))
         # A row's quantised blocks lie wholly before its last `window` tokens.
         default_cold = int(max_batch) * max(int(max_blocks) - self.window // P, 1)
         self.num_cold = int(num_cold) if num_cold is not None else default_cold
@@ -565,29 +571,42 @@ class QuantPagePool(PagePool):
         self.key_scales = torch.empty((self.num_cold, int(kv_heads), int(head_dim)), **u8)
         self.value_scales = torch.empty((self.num_cold, P, int(kv_heads)), **u8)
         self.free_cold = torch.empty((self.num_cold,), dtype=torch.int32, device=dev)
+        self.cold_shares = torch.empty((self.num_cold,), dtype=torch.int32, device=dev)
         self.cold_blocks = np.zeros(int(max_batch), dtype=np.int64)  # leading quantised blocks per row
         self.cold_free = self.num_cold
+        self.cold_exact = True  # cold_free equals the device's cold stack (else a lower bound)
         super().__init__(max_batch=max_batch, max_blocks=max_blocks, page_size=page_size, kv_heads=kv_heads,
                          head_dim=head_dim, dtype=dtype, device=device, num_pages=num_pages,
                          page_order=page_order)
 
     @property
     def cold_tensors(self) -> list[torch.Tensor]:
-        return [self.key_codes, self.value_codes, self.key_scales, self.value_scales, self.free_cold]
+        return [self.key_codes, self.value_codes, self.key_scales, self.value_scales, self.free_cold,
+                self.cold_shares]
 
     def reset(self, page_order: Optional[torch.Tensor] = None) -> None:
         super().reset(page_order)
         self._ops().pool_cold_reset_(self.tensors, self.cold_tensors, self.window)
         self.cold_blocks[:] = 0
         self.cold_free = self.num_cold
+        self.cold_exact = True
+
+    def ensure_cold(self, need: int) -> None:
+        """Raise PagedKVPoolExhausted unless `need` cold pages are free.  After selections the host
+        count is a lower bound (a released cold page may still be shared); it is refreshed from
+        the device only when it would refuse."""
+        if need > self.cold_free and not self.cold_exact:
+            self.cold_free = int(self.ctrl[CTRL_COLD_TOP].item())
+            self.cold_exact = True
+        if need > self.cold_free:
+            raise PagedKVPoolExhausted(
+                f"paged KV cold store exhausted: quantising needs {need} pages, {self.cold_free} free")
 
     def _cold_after(self, batch: int, tokens: int) -> tuple[np.ndarray, int]:
         """(frontier after appending `tokens` to rows [0, batch), blocks it newly quantises)."""
         frontier = np.maximum(self.lens[:batch] + tokens - self.window, 0) // self.page_size
         moved = int(np.maximum(frontier - self.cold_blocks[:batch], 0).sum())
-        if moved > self.cold_free:
-            raise PagedKVPoolExhausted(
-                f"paged KV cold store exhausted: quantising needs {moved} pages, {self.cold_free} free")
+        self.ensure_cold(moved)
         return frontier, moved
 
     def _quantised(self, batch: int, frontier: np.ndarray, moved: int) -> None:
@@ -637,6 +656,9 @@ class QuantPagePool(PagePool):
         if not self.free_exact:  # a lower bound: read the device's count once
             self.free_count = int(self.ctrl[CTRL_FREE_TOP].item())
             self.free_exact = True
+        if not self.cold_exact:
+            self.cold_free = int(self.ctrl[CTRL_COLD_TOP].item())
+            self.cold_exact = True
         free, cold_free, P = self.free_count, self.cold_free, self.page_size
         for s0 in range(0, tokens, self.chunk):
             t = min(self.chunk, tokens - s0)
@@ -690,13 +712,24 @@ class QuantPagePool(PagePool):
         return ko, vo
 
     def crop(self, batch: int, max_length: int) -> None:
-        """As PagePool.crop; the new lengths must leave every quantised block behind them (an
-        append never writes a quantised page)."""
+        """seq_lens[:batch] = min(seq_lens, max_length).  Quantised blocks from the one holding a
+        row's new length on are re-opened as hot pages holding their dequantised contents
+        (barq_kv_crop_cold); the room for them is checked before anything changes."""
         m = max(int(max_length), 0)
-        if batch > 0 and ((np.minimum(self.lens[:batch], m) // self.page_size) < self.cold_blocks[:batch]).any():
-            raise ValueError("crop would reopen a quantised block for writing: crop within the residual window "
-                             f"({self.window} tokens) or use a larger window")
-        super().crop(batch, max_length)
+        if batch <= 0:
+            return
+        first = np.minimum(self.lens[:batch], m) // self.page_size
+        reopened = np.maximum(self.cold_blocks[:batch] - first, 0)
+        need = int(reopened.sum())
+        self.ensure_free(need, "crop")
+        self._ops().pool_crop_cold_(self.tensors, self.cold_tensors, self.window, batch, m)
+        np.minimum(self.lens[:batch], m, out=self.lens[:batch])
+        np.minimum(self.cold_blocks[:batch], first, out=self.cold_blocks[:batch])
+        self.free_count -= need
+        if self.shared:
+            self.cold_exact = False  # a re-opened block's cold page may stay held by another row
+        else:
+            self.cold_free += need
 
     def free_rows(self, rows: Sequence[int]) -> None:
         rows = [int(r) for r in rows]
@@ -710,8 +743,11 @@ class QuantPagePool(PagePool):
         r = np.asarray(rows)
         nb = np.minimum(-(-self.hw[r] // self.page_size), self.max_blocks)
         cold = np.minimum(self.cold_blocks[r], nb)
-        self.free_count += int((nb - cold).sum())
-        self.cold_free += int(cold.sum())
+        self.free_count += int((nb - cold).sum())  # hot pages have one holder
+        if self.shared:
+            self.cold_exact = False  # shared cold pages stay held
+        else:
+            self.cold_free += int(cold.sum())
         self.lens[r] = 0
         self.hw[r] = 0
         self.cold_blocks[r] = 0
@@ -727,11 +763,37 @@ class QuantPagePool(PagePool):
     def append_rows(self, rows, key_states, value_states, max_length=None) -> None:
         raise NotImplementedError("append_rows is not available on a pool with quantised (fp8) pages")
 
+    def hot_block_counts(self, rows: np.ndarray) -> np.ndarray:
+        """Hot blocks of each row: below the high-water mark and after the quantised ones (the
+        blocks a selection moves or copies)."""
+        nb = np.minimum(-(-self.hw[rows] // self.page_size), self.max_blocks)
+        return nb - np.minimum(self.cold_blocks[rows], nb)
+
+    def select_copy_bound(self, rows: np.ndarray) -> int:
+        """Pages a selection copies, at most: the hot blocks of repeated takers."""
+        return int(self.hot_block_counts(rows)[self.repeated_mask(rows)].sum())
+
     def select_rows(self, src_rows: Sequence[int]) -> None:
-        raise NotImplementedError("beam selection is not available on a pool with quantised (fp8) pages")
+        """In place: row i becomes row src_rows[i] (repeats allowed), every other row empty.
+        Quantised blocks are shared by reference; hot blocks move to the first taker of their
+        row and are copied for the others (barq_kv_select_rows_cold_layers)."""
+        select_rows_layers([self], src_rows)
+
+    def _selected_cold(self, r: np.ndarray, need: int) -> None:
+        n = len(r)
+        lens, hw, cold = np.zeros_like(self.lens), np.zeros_like(self.hw), np.zeros_like(self.cold_blocks)
+        lens[:n], hw[:n], cold[:n] = self.lens[r], self.hw[r], self.cold_blocks[r]
+        self.lens[:] = lens  # in place: a captured decode step keeps views of these arrays
+        self.hw[:] = hw
+        self.cold_blocks[:] = cold
+        self.free_count -= need
+        self.free_exact = False  # moved and released pages are settled on the device
+        self.cold_exact = False  # released cold pages return only when no row shares them
+        self.shared = True       # cold pages may have several holders (hot pages never do)
 
     def copy_rows(self, src_rows: Sequence[int], num_pages: Optional[int] = None) -> "PagePool":
-        raise NotImplementedError("beam selection is not available on a pool with quantised (fp8) pages")
+        raise NotImplementedError("a pool with quantised (fp8) pages selects rows in place only: "
+                                  "size max_batch_size for the selection (batch * num_beams)")
 
     def _attention_call(self, backend, query, out, scale, max_seq, split_tokens, ws):
         if self.page_size % 16:
@@ -741,12 +803,42 @@ class QuantPagePool(PagePool):
 
     def to(self, device) -> "QuantPagePool":
         super().to(device)
-        for name in ("key_codes", "value_codes", "key_scales", "value_scales", "free_cold"):
+        for name in ("key_codes", "value_codes", "key_scales", "value_scales", "free_cold", "cold_shares"):
             setattr(self, name, getattr(self, name).to(self.device, non_blocking=True))
         return self
 
 
 _GROUPS: dict = {}
+
+
+def _select_rows_cold(pools: list, src_rows: Sequence[int]) -> None:
+    """select_rows_layers for pools with quantised pages: one set of launches for pools of one
+    device, geometry and window (else one per pool), every pool checked for room first."""
+    if not all(getattr(p, "quantized", False) for p in pools):
+        raise ValueError("a selection over quantised pools needs every pool quantised")
+    if len({id(p) for p in pools}) != len(pools):
+        raise ValueError("select_rows_layers: a pool is named twice")
+    rows = [p._selection(src_rows) for p in pools]
+    need = [p.select_copy_bound(r) if len(r) else 0 for p, r in zip(pools, rows)]
+    for p, k in zip(pools, need):
+        p.ensure_free(k, "select_rows")
+    g = pools[0]
+    key = lambda p: (p.device, p.max_batch, p.max_blocks, p.page_size, p.kv_heads, p.head_dim, p.dtype, p.window)
+    groups = [pools] if all(key(p) == key(g) for p in pools) else [[p] for p in pools]
+    r = rows[0]
+    n = len(r)
+    for group in groups:
+        q = group[0]
+        words = n * (q.max_blocks + 3) + q.max_batch + 2
+        words *= min(len(group), 32)
+        ws = getattr(q, "_select_ws", None)
+        if ws is None or ws.numel() < words:
+            ws = torch.empty((words,), dtype=torch.int32, device=q.device)
+            q._select_ws = ws
+        q._ops().pool_select_rows_cold_([p.tensors for p in group], [p.cold_tensors for p in group], q.window,
+                                        q._index_tensor(r.tolist() or [0])[:n], ws)
+    for p, k in zip(pools, need):
+        p._selected_cold(r, k)
 
 
 def _pool_group(pools: list[PagePool]):
@@ -770,6 +862,9 @@ def select_rows_layers(pools: Sequence[PagePool], src_rows: Sequence[int]) -> No
     geometry; every pool is checked for room before any is changed."""
     pools = list(pools)
     if not pools:
+        return
+    if any(getattr(p, "quantized", False) for p in pools):
+        _select_rows_cold(pools, src_rows)
         return
     g = pools[0]
     geom = (g.device, g.max_batch, g.max_blocks, g.page_size, g.kv_heads, g.head_dim, g.dtype)
@@ -940,9 +1035,10 @@ class _HostOps:
     # -------------------------------------------------------------- fp8 cold store (host memory)
     @staticmethod
     def pool_cold_reset_(t, cold, window):
-        free = cold[4]
+        free, shares = cold[4], cold[5]
         n = free.numel()
         free.copy_(torch.arange(n - 1, -1, -1, dtype=torch.int32))
+        shares.zero_()
         t[6][CTRL_COLD_TOP] = n
 
     @staticmethod
@@ -976,7 +1072,7 @@ class _HostOps:
     @staticmethod
     def pool_compress_(t, cold, window, batch):
         kp, vp, bt, lens, hw, free, ctrl, shares = t
-        kc, vc, ks, vs, free_cold = cold
+        kc, vc, ks, vs, free_cold, _ = cold
         P, MB = _HostOps._geometry(t)
         for r in range(batch):
             jmax = min(max(int(lens[r]) - window, 0) // P, min(-(-int(hw[r]) // P), MB))
@@ -1001,7 +1097,7 @@ class _HostOps:
     @staticmethod
     def pool_gather_cold(t, cold, window, key_out, value_out, batch, seq_out, flags=0):
         kp, vp, bt, lens, hw, free, ctrl, shares = t
-        kc, vc, ks, vs, _ = cold
+        kc, vc, ks, vs, _, _ = cold
         P, MB = _HostOps._geometry(t)
         if flags & SEQ_FROM_DEVICE:
             seq_out = min(seq_out, int(lens[:batch].max())) if batch else 0
@@ -1033,12 +1129,21 @@ class _HostOps:
         _HostOps.pool_gather_cold(t, cold, window, key_out, value_out, key_states.shape[0], seq_out, flags)
 
     @staticmethod
+    def _release_cold(cold, ctrl, c):
+        """Drop one reference to cold page c; push it on free_cold when none is left."""
+        free_cold, cold_shares = cold[4], cold[5]
+        if int(cold_shares[c]) > 0:
+            cold_shares[c] -= 1
+            return
+        top = int(ctrl[CTRL_COLD_TOP])
+        free_cold[top] = c
+        ctrl[CTRL_COLD_TOP] = top + 1
+
+    @staticmethod
     def pool_free_rows_cold_(t, cold, window, rows):
         kp, vp, bt, lens, hw, free, ctrl, shares = t
-        free_cold = cold[4]
         P, MB = _HostOps._geometry(t)
         top = int(ctrl[CTRL_FREE_TOP])
-        ctop = int(ctrl[CTRL_COLD_TOP])
         for r in rows.tolist():
             n = min(-(-int(hw[r]) // P), MB)
             for j in range(n):
@@ -1046,13 +1151,99 @@ class _HostOps:
                 if e >= 0:
                     top = _HostOps._release(t, e, top)
                 elif e <= -2:
-                    free_cold[ctop] = -2 - e
-                    ctop += 1
+                    _HostOps._release_cold(cold, ctrl, -2 - e)
             bt[r, :n] = -1
             lens[r] = 0
             hw[r] = 0
         ctrl[CTRL_FREE_TOP] = top
-        ctrl[CTRL_COLD_TOP] = ctop
+
+    @staticmethod
+    def pool_crop_cold_(t, cold, window, batch, max_length):
+        """Lower lengths; re-open each row's quantised blocks from the one holding its new length
+        (barq_kv_crop_cold): their dequantised contents go to pages popped from the stack."""
+        kp, vp, bt, lens, hw, free, ctrl, shares = t
+        kc, vc, ks, vs = cold[:4]
+        P, MB = _HostOps._geometry(t)
+        for r in range(batch):
+            m = min(int(lens[r]), max_length)
+            for j in range(m // P, min(-(-int(hw[r]) // P), MB)):
+                e = int(bt[r, j])
+                if e > -2:
+                    continue
+                top = int(ctrl[CTRL_FREE_TOP])
+                if top <= 0:
+                    ctrl[CTRL_ERRORS] |= ERRBIT_POOL_EXHAUSTED
+                    continue
+                c, page = -2 - e, int(free[top - 1])
+                ctrl[CTRL_FREE_TOP] = top - 1
+                kp[page] = _HostOps._dequantise(kc[c], ks[c].long()[None] - 127, kp.dtype)
+                vp[page] = _HostOps._dequantise(vc[c], vs[c].long()[..., None] - 127, kp.dtype)
+                bt[r, j] = page
+                _HostOps._release_cold(cold, ctrl, c)
+            lens[r] = m
+
+    @staticmethod
+    def pool_select_rows_cold_(pools, colds, window, rows, workspace=None):
+        """Selection over pools with cold stores (barq_kv_select_rows_cold_layers): quantised
+        blocks shared by reference, every hot block moved to its row's first taker or copied."""
+        for t, cold in zip(pools, colds):
+            _HostOps._select_cold(t, cold, rows.tolist())
+
+    @staticmethod
+    def _select_cold(t, cold, rows):
+        kp, vp, bt, lens, hw, free, ctrl, shares = t
+        cold_shares = cold[5]
+        P, MB = _HostOps._geometry(t)
+        n, B = len(rows), bt.shape[0]
+        nb = lambda r: min(-(-int(hw[r]) // P), MB)
+        first = {}
+        for i, r in enumerate(rows):
+            first.setdefault(r, i)
+        copies = 0
+        for i, r in enumerate(rows):
+            for j in range(nb(r)):
+                e = int(bt[r, j])
+                if e > -2 and not (first[r] == i and e >= 0 and int(shares[e]) == 0):
+                    copies += 1
+        top = int(ctrl[CTRL_FREE_TOP])
+        if copies > top:
+            ctrl[CTRL_ERRORS] |= ERRBIT_POOL_EXHAUSTED
+            return
+        new_bt = torch.full((n, MB), -1, dtype=torch.int32)
+        used, moved = 0, set()
+        for i, r in enumerate(rows):
+            for j in range(nb(r)):
+                e = int(bt[r, j])
+                if e <= -2:
+                    cold_shares[-2 - e] += 1
+                    new_bt[i, j] = e
+                elif first[r] == i and e >= 0 and int(shares[e]) == 0:
+                    moved.add((r, j))
+                    new_bt[i, j] = e
+                else:
+                    page = int(free[top - 1 - used])
+                    used += 1
+                    if e >= 0:
+                        kp[page] = kp[e]
+                        vp[page] = vp[e]
+                    new_bt[i, j] = page
+        new_lens = lens[rows].clone() if n else torch.zeros(0, dtype=torch.int32)
+        new_hw = hw[rows].clone() if n else torch.zeros(0, dtype=torch.int32)
+        top -= used
+        ctrl[CTRL_FREE_TOP] = top
+        for r in range(B):
+            for j in range(nb(r)):
+                e = int(bt[r, j])
+                if e <= -2:
+                    _HostOps._release_cold(cold, ctrl, -2 - e)
+                elif e >= 0 and (r, j) not in moved:
+                    ctrl[CTRL_FREE_TOP] = _HostOps._release(t, e, int(ctrl[CTRL_FREE_TOP]))
+        bt.fill_(-1)
+        lens.zero_()
+        hw.zero_()
+        bt[:n] = new_bt
+        lens[:n] = new_lens
+        hw[:n] = new_hw
 
     @staticmethod
     def pool_crop_(t, batch, max_length):

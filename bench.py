@@ -587,8 +587,11 @@ def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10, probe=
     L, B, H, D, P = cfg["layers"], cfg["batch"], cfg["heads"], cfg["dim"], cfg["page"]
     cap = max(prefill_lengths(cfg)) + wl.steps_cap
     mb = math.ceil(cap / P)
+    # no beam selection here: the hot pool holds the window and a prefill chunk per row, without
+    # the default's room for selection copies
+    hot = B * (-(-(window + 64) // P) + 2)
     pools = [QuantPagePool(max_batch=B, max_blocks=mb, page_size=P, kv_heads=H, head_dim=D, dtype=wl.dtype,
-                           device=dev, window=window) for _ in range(L)]
+                           device=dev, window=window, num_pages=hot) for _ in range(L)]
     kin = torch.empty((L, B, H, 1, D), dtype=wl.dtype, device=dev)
     vin = torch.empty_like(kin)
     step = CapturedDecodeStep(pools, B, 1, inputs=(kin, vin))

@@ -321,6 +321,9 @@ typedef struct barq_kv_cold {
   void* key_scales;    /* uint8 [num_cold, kv_heads, head_dim]: E8M0, per channel */
   void* value_scales;  /* uint8 [num_cold, page_size, kv_heads]: E8M0, per token */
   int32_t* free_cold;  /* int32 [num_cold], a stack; entries [0, ctrl[BARQ_KV_CTRL_COLD_TOP]) free */
+  int32_t* cold_shares; /* int32 [num_cold], references to the cold page beyond the first (0 for a
+                           free page and for a page one block maps), or NULL for a store whose
+                           rows never share cold pages (barq_kv_select_rows_cold_layers needs it) */
   int64_t num_cold;
   int64_t window;      /* residual window in tokens, >= 0 */
   int64_t element_type; /* the pool's elements: BARQ_KV_BF16, BARQ_KV_FP16 or BARQ_KV_FP32 */
@@ -330,7 +333,7 @@ typedef struct barq_kv_cold {
 #define BARQ_KV_FP16 1
 #define BARQ_KV_FP32 2
 
-/* Every cold page free (after barq_kv_pool_reset, which clears ctrl). */
+/* Every cold page free and cold_shares zero (after barq_kv_pool_reset, which clears ctrl). */
 int barq_kv_cold_reset(const barq_kv_pool* pool, const barq_kv_cold* cold, void* stream);
 
 /*
@@ -371,9 +374,38 @@ int barq_kv_decode_attention_cold(const barq_kv_pool* pool, const barq_kv_cold* 
                                   int64_t split_tokens, int64_t flags, void* workspace, int64_t workspace_bytes,
                                   void* stream);
 
-/* barq_kv_free_rows for a pool with a cold store: cold pages return to free_cold. */
+/* barq_kv_free_rows for a pool with a cold store: a cold page returns to free_cold when no block
+ * holds it any more (cold_shares counts the others). */
 int barq_kv_free_rows_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, const int32_t* rows,
                            int64_t num_rows, void* stream);
+
+/*
+ * barq_kv_select_rows_layers for pools with cold stores (colds[i] is pools[i]'s), replacing
+ * batch_select_indices / batch_repeat_interleave / reorder_cache (python/barqtrain/kv_cache.py:
+ * 166-186) on quantised caches: a quantised block never changes, so the new rows share it
+ * (cold_shares counts the extra references); every hot block below the high-water mark -- the
+ * residual window and the partial block, which an append, a crop or barq_kv_compress may still
+ * rewrite -- moves to the first new row taking its source when no other block holds its page,
+ * and is copied into a page from the free stack otherwise, so hot pages are never shared.  All
+ * or nothing per pool, workspace and geometry rules as for barq_kv_select_rows_layers; needs
+ * page_shares and cold_shares.
+ */
+int barq_kv_select_rows_cold_layers(const barq_kv_pool* pools, const barq_kv_cold* colds, int64_t num_pools,
+                                    const int32_t* src_rows, int64_t num_rows, int32_t* workspace,
+                                    int64_t workspace_words, void* stream);
+
+/*
+ * barq_kv_crop for a pool with a cold store (python/barqtrain/kv_cache.py:158-164): seq_lens[b] =
+ * min(seq_lens[b], max_length) for rows [0, batch), and every quantised block of such a row from
+ * the one holding its new length up to the high-water mark is re-opened: its dequantised
+ * contents (the values barq_kv_gather_cold returns) are written into a page from the free stack,
+ * which the block maps from then on, and the cold page loses the block's reference.  barq_kv_compress
+ * quantises such a block again once it leaves the window.  A block finding no free page stays
+ * quantised and sets BARQ_KV_ERRBIT_POOL_EXHAUSTED.  Pages are taken in no fixed order.  Needs
+ * a pool whose hot pages are not shared (as barq_kv_select_rows_cold_layers leaves them).
+ */
+int barq_kv_crop_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, int64_t batch, int64_t max_length,
+                      void* stream);
 
 #ifdef __cplusplus
 }

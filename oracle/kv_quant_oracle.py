@@ -20,6 +20,12 @@ ships no implementation, so this module states the algorithm the product impleme
 * a row's block j is quantised once it lies wholly before the row's residual window,
   (j + 1) * P <= len - W, from its content at that time (a full block never changes again).
 * reads dequantise: decode(code) * 2^e, rounded to the cache dtype (ties to even).
+* a crop below a row's quantised blocks re-opens them: from the block holding the row's new
+  length on, a quantised block's stored content becomes its dequantised read (the bits a
+  gather returned before the crop), which is what the row then holds there -- quantised again,
+  from that content, once the block leaves the window anew.
+* a selection (beam reordering) copies rows whole, quantised blocks included: a shared
+  quantised block reads the same for every row holding it.
 
 Pinning (tests/test_quant_oracle.py): every finite float32 code point and rounding boundary of
 the encoder against torch's float8_e4m3fn conversion (an independent library routine); the
@@ -164,8 +170,9 @@ class QuantLayerOracle(DenseLayerOracle):
 
     ``window`` is the residual window W in tokens; ``dtype`` the cache dtype ('bf16', 'f16',
     'f32') of the bit arrays.  ``cold[r]`` counts row r's leading quantised blocks; it grows
-    after every append to floor((len - W) / P) and never shrinks except when the row is
-    released or the cache reset (a crop must stay at or above it).
+    after every append to floor((len - W) / P), and falls to floor(new len / P) when a crop
+    re-opens blocks (their content replaced by its dequantised read), or to 0 when the row is
+    released or the cache reset.
     """
 
     def __init__(self, max_batch_size: int, max_cache_len: int, page_size: int, window: int, dtype: str):
@@ -185,10 +192,20 @@ class QuantLayerOracle(DenseLayerOracle):
             return
         m = max_length if max_length >= 0 else self.get_seq_length() - abs(max_length)
         m = max(m, 0)
-        if (np.minimum(self.seq_lens[: self.current_batch_size], m) // self.page_size
-                < self.cold[: self.current_batch_size]).any():
-            raise ValueError("crop below a quantised block")
+        for r in range(self.current_batch_size):
+            first = min(int(self.seq_lens[r]), m) // self.page_size
+            for j in range(first, int(self.cold[r])):  # re-opened: the block now holds its read
+                for cache, key in ((self.keys, True), (self.values, False)):
+                    cache[r, :, j] = self._dequantised_block(cache[r, :, j], key)
+            self.cold[r] = min(int(self.cold[r]), first)
         super().crop(max_length)
+
+    def _dequantised_block(self, block: np.ndarray, key: bool) -> np.ndarray:
+        """A block's bits [H, P, D] as a read of it quantised returns them."""
+        page = np.ascontiguousarray(bits_to_float32(block, self.qdtype).transpose(1, 0, 2))  # [P, H, D]
+        codes, scales = quantize_key_page(page) if key else quantize_value_page(page)
+        deq = dequantize(codes, scales[None] if key else scales[..., None])
+        return float32_to_bits(deq.transpose(1, 0, 2), self.qdtype)
 
     def batch_select_indices(self, indices: Sequence[int]) -> None:
         if not self.is_initialized or self.current_batch_size == 0:
@@ -197,6 +214,11 @@ class QuantLayerOracle(DenseLayerOracle):
         super().batch_select_indices(indices)
         self.cold = np.zeros(self.max_batch_size, dtype=np.int64)
         self.cold[: len(cold)] = cold
+
+    def batch_repeat_interleave(self, repeats: int) -> None:
+        if not self.is_initialized or self.current_batch_size == 0:
+            return
+        self.batch_select_indices([b for b in range(self.current_batch_size) for _ in range(int(repeats))])
 
     def reset(self) -> None:
         super().reset()
@@ -213,11 +235,7 @@ class QuantLayerOracle(DenseLayerOracle):
         P = self.page_size
         for r in range(self.current_batch_size or cache.shape[0]):
             for j in range(int(self.cold[r])):
-                page = bits_to_float32(cache[r, :, j], self.qdtype)  # [H, P, D]
-                page = np.ascontiguousarray(page.transpose(1, 0, 2))  # [P, H, D]
-                codes, scales = quantize_key_page(page) if key else quantize_value_page(page)
-                deq = dequantize(codes, scales[None] if key else scales[..., None])
-                out[r, :, j] = float32_to_bits(deq.transpose(1, 0, 2), self.qdtype)
+                out[r, :, j] = self._dequantised_block(cache[r, :, j], key)
         return out
 
     def current_tensors(self) -> tuple[np.ndarray, np.ndarray]:

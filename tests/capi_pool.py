@@ -190,9 +190,11 @@ class CColdPool(CPool):
         self.ks = torch.empty((n, self.heads, self.dim), **u8)
         self.vs = torch.empty((n, self.page_size, self.heads), **u8)
         self.free_cold = torch.empty((n,), dtype=torch.int32, device=dev)
+        self.cold_shares = torch.empty((n,), dtype=torch.int32, device=dev)
         self.num_cold = n
         self.cs = _capi.BarqKVCold(self.kc.data_ptr(), self.vc.data_ptr(), self.ks.data_ptr(), self.vs.data_ptr(),
-                                   self.free_cold.data_ptr(), n, self.window, ELEMENT_TYPE[self.dtype])
+                                   self.free_cold.data_ptr(), self.cold_shares.data_ptr(), n, self.window,
+                                   ELEMENT_TYPE[self.dtype])
         self.cold_reset()
 
     @property
@@ -242,9 +244,22 @@ class CColdPool(CPool):
         _capi.check(self.lib.barq_kv_free_rows_cold(self.ref, self.cref, idx.data_ptr(), len(rows), self._stream()))
         torch.cuda.current_stream().synchronize()
 
+    def select_rows(self, rows):
+        idx = torch.tensor(rows or [0], dtype=torch.int32, device=self.kp.device)
+        words = self.lib.barq_kv_select_workspace_words(self.ref, 1, len(rows))
+        assert words > 0
+        ws = torch.empty(words, dtype=torch.int32, device=self.kp.device)
+        _capi.check(self.lib.barq_kv_select_rows_cold_layers(self.ref, self.cref, 1, idx.data_ptr(), len(rows),
+                                                             ws.data_ptr(), ws.numel(), self._stream()))
+        torch.cuda.current_stream().synchronize()
+
+    def crop(self, batch, max_length):
+        _capi.check(self.lib.barq_kv_crop_cold(self.ref, self.cref, batch, max_length, self._stream()))
+
     def check_invariants(self, window=None):
-        """Per row: blocks below the high-water mark hold a page (cold ones first, as a prefix);
-        hot and cold pages each held once and absent from their free stacks, which hold the rest."""
+        """Per row: blocks below the high-water mark hold a page (cold ones first, as a prefix).
+        Hot pages are held once; a cold page held by k blocks has cold_shares k - 1; each stack
+        holds exactly the pages no block holds."""
         P = self.page_size
         bt = self.bt.cpu().numpy()
         hw = self.hw.cpu().numpy()
@@ -260,10 +275,13 @@ class CColdPool(CPool):
             hot += row[c:].tolist()
         free = set(self.free.cpu().numpy()[: int(ctrl[0])].tolist())
         free_c = set(self.free_cold.cpu().numpy()[: int(ctrl[2])].tolist())
-        assert len(set(hot)) == len(hot) and len(set(cold)) == len(cold)
+        held_c = np.bincount(np.asarray(cold, dtype=np.int64), minlength=self.num_cold)
+        shares_c = self.cold_shares.cpu().numpy()
+        assert len(set(hot)) == len(hot)
+        assert (shares_c == np.maximum(held_c - 1, 0)).all()
         assert not free & set(hot) and not free_c & set(cold)
         assert len(free) == int(ctrl[0]) and len(free_c) == int(ctrl[2])
-        assert len(hot) + len(free) == self.num_pages and len(cold) + len(free_c) == self.num_cold
+        assert len(hot) + len(free) == self.num_pages and int((held_c > 0).sum()) + len(free_c) == self.num_cold
 
 
 def attend_cold(pool: "CColdPool", q, *, scale=None, out_f32=True, max_seq=0, split_tokens=0):

@@ -1,7 +1,8 @@
 """GPU parity of the fp8 cold store (barq_kv_compress / barq_kv_gather_cold / barq_kv_update_cold /
-barq_kv_free_rows_cold), through the C ABI and the layer API, against the oracle
-QuantLayerOracle: bit-exact (codes, scales and every dequantised element), with page accounting
-checked after every operation."""
+barq_kv_free_rows_cold / barq_kv_select_rows_cold_layers / barq_kv_crop_cold), through the C ABI
+and the layer API, against the oracle QuantLayerOracle: bit-exact (codes, scales and every
+dequantised element), with page accounting -- shared cold pages included -- checked after every
+operation."""
 
 from __future__ import annotations
 
@@ -46,10 +47,10 @@ def test_random_programs_through_capi(capi, case, seed):
     gen = torch.Generator().manual_seed(seed)
     pool = CColdPool(window=W, max_batch=Bmax, max_blocks=-(-cap // P), page_size=P, heads=H, dim=D, dtype=dtype)
     oracle = q.QuantLayerOracle(Bmax, cap, P, W, DT[dtype])
-    for it in range(40):
+    for it in range(60):
         r = rng.random()
-        if r < 0.6 or not oracle.is_initialized:
-            b = int(rng.integers(1, Bmax + 1))
+        if r < 0.55 or not oracle.is_initialized:
+            b = int(rng.integers(1, (oracle.max_batch_size if oracle.is_initialized else Bmax) + 1))
             t = int(rng.integers(1, 30)) if rng.random() < 0.3 else 1
             if oracle.is_initialized and int(oracle.seq_lens[:b].max()) + t > cap:
                 continue
@@ -62,13 +63,18 @@ def test_random_programs_through_capi(capi, case, seed):
                 got = pool.update(k.cuda(), v.cuda(), oracle.get_seq_length())
                 ok, ov = oracle.current_tensors()
                 assert np.array_equal(to_bits(got[0]), ok) and np.array_equal(to_bits(got[1]), ov), f"update it{it}"
-        elif r < 0.75 and oracle.current_batch_size:
+        elif r < 0.7 and oracle.current_batch_size:
             cur = oracle.current_batch_size
-            m = int(rng.integers(int(oracle.cold[:cur].max()) * P, cap))
+            m = int(rng.integers(0, cap))  # below quantised blocks too: barq_kv_crop_cold re-opens them
             pool.crop(cur, m)
             oracle.crop(m)
+        elif r < 0.85 and oracle.current_batch_size:
+            rows = rng.integers(0, oracle.current_batch_size, size=int(rng.integers(1, Bmax + 1))).tolist()
+            pool.select_rows(rows)  # repeats share quantised blocks; hot blocks move or are copied
+            oracle.batch_select_indices(rows)
         elif oracle.current_batch_size:
-            rows = sorted(rng.choice(Bmax, size=int(rng.integers(1, 3)), replace=False).tolist())
+            n = oracle.max_batch_size
+            rows = sorted(rng.choice(n, size=min(int(rng.integers(1, 3)), n), replace=False).tolist())
             pool.free_rows(rows)
             oracle.release_rows(rows)
         if oracle.current_batch_size:
@@ -193,6 +199,34 @@ def test_layer_api_with_graph_replays(hip):
         assert pool.errors() == 0
         assert int(pool.ctrl[0]) == pool.free_count and int(pool.ctrl[2]) == pool.cold_free
         assert pool.cold_blocks.tolist() == [(100 - W) // P] * B
+
+
+def test_beam_search_on_fp8_pages_matches_the_oracle_beam_by_beam(hip, monkeypatch):
+    """generate(num_beams=4, kv_quant="fp8_e4m3") on GPU pools: every layer's every update returns
+    the oracle's K/V bit for bit, every beam reordering (one barq_kv_select_rows_cold_layers
+    launch set for all layers) applied to the oracle too; the beams share quantised blocks."""
+    pytest.importorskip("transformers")
+    from barqtrain import create_paged_kv_cache
+    from quant_shadow import shadow
+    from test_gpu_layer import tiny_llama
+
+    model, cfg = tiny_llama()
+    model = model.to("cuda")
+    model.config._attn_implementation = "eager"
+    prompt, new = 40, 24
+    ids = torch.randint(1, 512, (2, prompt), generator=torch.Generator().manual_seed(9)).to("cuda")
+    cache = create_paged_kv_cache(model, max_batch_size=8, max_cache_len=prompt + new, page_size=4,
+                                  kv_quant="fp8_e4m3", residual_window=8)
+    stats = shadow(cache, monkeypatch)
+    out = model.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=new, do_sample=False,
+                         num_beams=4, num_return_sequences=2, past_key_values=cache,
+                         return_dict_in_generate=True, output_scores=True)
+    assert out.sequences.shape == (4, prompt + new)
+    assert all(s["updates"] >= new - 1 and s["selections"] >= new - 2 for s in stats), stats
+    for layer in cache.layers:
+        pool = layer.pool
+        assert pool.on_gpu and pool.errors() == 0 and pool.shared
+        assert int(pool.cold_shares.max()) > 0  # beams hold quantised blocks in common
 
 
 def test_model_on_gpu_with_fp8_pages_tracks_full_precision(hip):

@@ -19,7 +19,7 @@ def built():
 def test_library_exports_every_header_function(built):
     lib = ctypes.CDLL(str(build.lib_path()))
     declared = _capi.header_functions()
-    assert len(declared) == 22
+    assert len(declared) == 24
     for name in declared:
         assert hasattr(lib, name), name
     out = subprocess.run(["nm", "-D", "--defined-only", str(build.lib_path())], capture_output=True, text=True).stdout

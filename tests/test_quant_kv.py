@@ -1,7 +1,8 @@
 """Quantised (fp8) KV pages through the layer API on host-memory tensors, against the oracle
-QuantLayerOracle bit for bit: random programs of ragged and long (chunked) appends, crops within
-the residual window, row releases and resets; page accounting of the hot pool and the cold store;
-the flag plumbing of create_paged_kv_cache.  CPU only."""
+QuantLayerOracle bit for bit: random programs of ragged and long (chunked) appends, crops (also
+below quantised blocks, which re-opens them), beam selections (quantised blocks shared, hot
+blocks moved or copied), row releases and resets; page accounting of the hot pool and the cold
+store; beam search in generate(); the flag plumbing of create_paged_kv_cache.  CPU only."""
 
 from __future__ import annotations
 
@@ -16,22 +17,29 @@ DT = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
 
 
 def check_accounting(pool):
-    """Host shadow = device state: stack tops, frontiers, and every page held exactly once."""
+    """Host shadow against the device state: stack tops (exact, or lower bounds after a
+    selection), frontiers; every hot page held once; a cold page held by k blocks has
+    cold_shares k - 1; each stack holds exactly the pages no block holds."""
     P = pool.page_size
     bt = pool.block_table.numpy()
-    assert int(pool.ctrl[0]) == pool.free_count and int(pool.ctrl[2]) == pool.cold_free
+    top, ctop = int(pool.ctrl[0]), int(pool.ctrl[2])
+    assert top == pool.free_count if pool.free_exact else top >= pool.free_count
+    assert ctop == pool.cold_free if pool.cold_exact else ctop >= pool.cold_free
     hot, cold = [], []
     for r in range(pool.max_batch):
         n = -(-int(pool.high_water[r]) // P)
         row = bt[r, :n]
         c = int(pool.cold_blocks[r])
         assert (row[:c] <= -2).all() and (row[c:] >= 0).all(), (r, row, c)
+        assert (bt[r, n:] == -1).all()
         cold += (-2 - row[:c]).tolist()
         hot += row[c:].tolist()
-    assert len(set(hot)) == len(hot) and len(set(cold)) == len(cold)
-    assert not set(hot) & set(pool.free_pages[: pool.free_count].tolist())
-    assert not set(cold) & set(pool.free_cold[: pool.cold_free].tolist())
-    assert len(hot) + pool.free_count == pool.num_pages and len(cold) + pool.cold_free == pool.num_cold
+    held = np.bincount(np.asarray(cold, dtype=np.int64), minlength=pool.num_cold)
+    assert len(set(hot)) == len(hot)
+    assert (pool.cold_shares.numpy() == np.maximum(held - 1, 0)).all()
+    assert not set(hot) & set(pool.free_pages[:top].tolist())
+    assert not set(cold) & set(pool.free_cold[:ctop].tolist())
+    assert len(hot) + top == pool.num_pages and int((held > 0).sum()) + ctop == pool.num_cold
 
 
 @pytest.mark.parametrize("dtype,page,window,seed", [(torch.bfloat16, 4, 8, 0), (torch.float16, 16, 16, 1),
@@ -49,7 +57,7 @@ def test_random_programs_match_the_oracle(dtype, page, window, seed):
     for it in range(50):
         r = rng.random()
         if r < 0.6 or not oracle.is_initialized:
-            b = int(rng.integers(1, Bmax + 1))
+            b = int(rng.integers(1, (oracle.max_batch_size if oracle.is_initialized else Bmax) + 1))
             t = int(rng.integers(1, 40)) if rng.random() < 0.3 else 1
             if oracle.is_initialized and int(oracle.seq_lens[:b].max()) + t > cap:
                 continue
@@ -58,14 +66,19 @@ def test_random_programs_match_the_oracle(dtype, page, window, seed):
             gk, gv = layer.update(k, v)
             ok, ov = oracle.update(to_bits(k), to_bits(v))
             assert np.array_equal(to_bits(gk), ok) and np.array_equal(to_bits(gv), ov), it
-        elif r < 0.75:
-            cur = oracle.current_batch_size
-            lo = int(max((oracle.cold[:cur].max() if cur else 0) * page, 0))
-            m = int(rng.integers(lo, cap))
+        elif r < 0.7:
+            m = int(rng.integers(0, cap))  # below quantised blocks too: they are re-opened
             layer.crop(m)
             oracle.crop(m)
+        elif r < 0.8 and oracle.current_batch_size:
+            cur = oracle.current_batch_size
+            n = int(rng.integers(1, Bmax + 1))
+            rows = rng.integers(0, cur, size=n).tolist()  # repeats, drops and reorders
+            layer.batch_select_indices(torch.tensor(rows))
+            oracle.batch_select_indices(rows)
         elif r < 0.9 and oracle.current_batch_size:
-            rows = sorted(rng.choice(Bmax, size=int(rng.integers(1, 3)), replace=False).tolist())
+            rows = sorted(rng.choice(oracle.max_batch_size, size=min(int(rng.integers(1, 3)), oracle.max_batch_size),
+                                     replace=False).tolist())
             layer.free_rows(rows)
             oracle.release_rows(rows)
         else:
@@ -113,7 +126,7 @@ def test_long_prefill_runs_in_chunks_within_a_small_hot_pool():
 
     pool = QuantPagePool(max_batch=2, max_blocks=64, page_size=16, kv_heads=1, head_dim=8, dtype=torch.float16,
                          device="cpu", window=32, chunk=64)
-    assert pool.num_pages == 2 * (6 + 2)  # ceil((32 + 64) / 16) + 2 pages per row
+    assert pool.num_pages == 2 * ((6 + 2) + (2 + 1))  # ceil((32 + 64) / 16) + 2, ceil(32 / 16) + 1 per row
     gen = torch.Generator().manual_seed(5)
     k, v = hf_layout(2, 1, 1000, 8, torch.float16, gen), hf_layout(2, 1, 1000, 8, torch.float16, gen)
     gk, _ = pool.update(k, v)
@@ -123,21 +136,84 @@ def test_long_prefill_runs_in_chunks_within_a_small_hot_pool():
     assert mem["hot_pages"] < mem["cold_store"]
 
 
-def test_crop_into_quantised_blocks_is_refused_and_changes_nothing():
-    from barqtrain_amd.paged import QuantPagePool
+def test_crop_below_quantised_blocks_reopens_them():
+    """Crop to 5 tokens of a row with blocks 0-1 quantised: block 1 (holding position 5) becomes
+    a hot page holding its dequantised read -- the gather reads the same bits as before -- and
+    the next append writes into it; without room for the page the crop raises, changing nothing."""
+    from barqtrain_amd.paged import PagedKVPoolExhausted, QuantPagePool
 
     pool = QuantPagePool(max_batch=1, max_blocks=8, page_size=4, kv_heads=1, head_dim=4, dtype=torch.float32,
                          device="cpu", window=4)
+    oracle = QuantLayerOracle(1, 32, 4, 4, "f32")
     gen = torch.Generator().manual_seed(6)
-    pool.append(hf_layout(1, 1, 14, 4, torch.float32, gen), hf_layout(1, 1, 14, 4, torch.float32, gen))
+    k, v = hf_layout(1, 1, 14, 4, torch.float32, gen), hf_layout(1, 1, 14, 4, torch.float32, gen)
+    pool.append(k, v)
+    oracle.append(to_bits(k), to_bits(v))
     assert pool.cold_blocks.tolist() == [2]
-    with pytest.raises(ValueError):
-        pool.crop(1, 7)
-    assert pool.lens.tolist() == [14] and int(pool.seq_lens[0]) == 14
-    pool.crop(1, 8)
-    assert pool.lens.tolist() == [8]
+    before = to_bits(pool.gather(1)[0])
+    free, cold_free = pool.free_count, pool.cold_free
+    pool.crop(1, 5)
+    oracle.crop(5)
+    assert pool.lens.tolist() == [5] and pool.cold_blocks.tolist() == [1]
+    assert pool.free_count == free - 1 and pool.cold_free == cold_free + 1
+    assert int(pool.block_table[0, 1]) >= 0 and int(pool.block_table[0, 0]) <= -2
+    assert np.array_equal(to_bits(pool.gather(1, 14)[0]), before)
+    k, v = hf_layout(1, 1, 3, 4, torch.float32, gen), hf_layout(1, 1, 3, 4, torch.float32, gen)
+    gk, gv = pool.update(k, v)
+    ok, ov = oracle.update(to_bits(k), to_bits(v))
+    assert np.array_equal(to_bits(gk), ok) and np.array_equal(to_bits(gv), ov)
+    check_accounting(pool)
+
+    full = QuantPagePool(max_batch=1, max_blocks=8, page_size=4, kv_heads=1, head_dim=4, dtype=torch.float32,
+                         device="cpu", window=4, chunk=4, num_pages=3)
+    full.append(hf_layout(1, 1, 14, 4, torch.float32, gen), hf_layout(1, 1, 14, 4, torch.float32, gen))
+    assert full.free_count == 1 and full.cold_blocks.tolist() == [2]  # re-opening 2 blocks needs 2
+    state = (full.lens.copy(), full.block_table.clone(), full.seq_lens.clone())
+    with pytest.raises(PagedKVPoolExhausted):
+        full.crop(1, 2)
+    assert np.array_equal(state[0], full.lens) and torch.equal(state[1], full.block_table)
+    assert torch.equal(state[2], full.seq_lens)
+
+
+def test_beam_selection_shares_quantised_blocks_and_moves_hot_ones():
+    """Rows [0, 0, 1]: both takers of row 0 share its quantised blocks (cold_shares 1); the first
+    takes its hot pages, the second copies them; row 1's pages move.  Then a crop re-opens a
+    shared block for one row only, and releasing rows returns cold pages when unshared."""
+    from barqtrain_amd.paged import QuantPagePool
+
+    P, H, D, W = 4, 2, 8, 4
+    pool = QuantPagePool(max_batch=3, max_blocks=8, page_size=P, kv_heads=H, head_dim=D, dtype=torch.bfloat16,
+                         device="cpu", window=W)
+    oracle = QuantLayerOracle(3, 32, P, W, "bf16")
+    gen = torch.Generator().manual_seed(7)
+    k, v = hf_layout(2, H, 18, D, torch.bfloat16, gen), hf_layout(2, H, 18, D, torch.bfloat16, gen)
+    pool.append(k, v)
+    oracle.append(to_bits(k), to_bits(v))
+    hot0 = pool.block_table[0, 3:5].clone()
+    pool.select_rows([0, 0, 1])
+    oracle.batch_select_indices([0, 0, 1])
+    bt = pool.block_table
+    assert torch.equal(bt[0, :3], bt[1, :3]) and (bt[0, :3] <= -2).all()
+    assert (pool.cold_shares[(-2 - bt[0, :3]).long()] == 1).all()
+    assert torch.equal(bt[0, 3:5], hot0) and not set(bt[1, 3:5].tolist()) & set(hot0.tolist())
+    check_accounting(pool)
+    gk, gv = pool.gather(3)
+    ok, ov = oracle.current_tensors()
+    assert np.array_equal(to_bits(gk), ok) and np.array_equal(to_bits(gv), ov)
+    pool.crop(3, 6)
+    oracle.crop(6)
+    check_accounting(pool)
+    k, v = hf_layout(3, H, 5, D, torch.bfloat16, gen), hf_layout(3, H, 5, D, torch.bfloat16, gen)
+    gk, gv = pool.update(k, v)
+    ok, ov = oracle.update(to_bits(k), to_bits(v))
+    assert np.array_equal(to_bits(gk), ok) and np.array_equal(to_bits(gv), ov)
+    pool.free_rows([1])
+    oracle.release_rows([1])
+    check_accounting(pool)
+    pool.free_rows([0, 2])
+    assert int(pool.ctrl[2]) == pool.num_cold and int(pool.ctrl[0]) == pool.num_pages
     with pytest.raises(NotImplementedError):
-        pool.select_rows([0])
+        pool.copy_rows([0])
 
 
 def test_factory_flag_and_environment(monkeypatch):
@@ -162,3 +238,29 @@ def test_factory_flag_and_environment(monkeypatch):
     assert create_paged_kv_cache(Config(), max_batch_size=1, max_cache_len=64).layers[0].kv_quant is None
     with pytest.raises(ValueError):
         create_paged_kv_cache(Config(), max_batch_size=1, max_cache_len=64, kv_quant="int4")
+
+
+def test_beam_search_on_fp8_pages_matches_the_oracle_beam_by_beam(monkeypatch):
+    """generate(num_beams=4) on a quantised cache: every layer's every update returns the oracle's
+    K/V bit for bit, with every beam reordering applied to the oracle too (quant_shadow); the
+    beams share quantised blocks."""
+    pytest.importorskip("transformers")
+    from barqtrain.kv_cache import create_paged_kv_cache
+    from quant_shadow import shadow
+    from test_generate import tiny_llama
+
+    model, cfg = tiny_llama()
+    model.config._attn_implementation = "eager"
+    prompt, new = 21, 16
+    ids = torch.randint(1, 512, (2, prompt), generator=torch.Generator().manual_seed(8))
+    cache = create_paged_kv_cache(model, max_batch_size=8, max_cache_len=prompt + new, page_size=4,
+                                  kv_quant="fp8_e4m3", residual_window=8)
+    stats = shadow(cache, monkeypatch)
+    out = model.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=new, do_sample=False,
+                         num_beams=4, num_return_sequences=2, past_key_values=cache,
+                         return_dict_in_generate=True, output_scores=True)
+    assert out.sequences.shape[0] == 4
+    assert all(s["updates"] >= new - 1 and s["selections"] >= new - 2 for s in stats), stats
+    assert all(layer.pool.shared and int(layer.pool.cold_shares.max()) > 0 for layer in cache.layers)
+    for layer in cache.layers:
+        check_accounting(layer.pool)

@@ -176,8 +176,34 @@ def test_layer_oracle_quantises_blocks_behind_the_window():
     kc, ks = o.quantized_page(0, 1, True)
     want = q.float32_to_bits(q.dequantize(kc, ks[None]).transpose(1, 0, 2), "bf16")
     assert np.array_equal(gk[0, :, 4:8], want)
-    with pytest.raises(ValueError):
-        o.crop(10)                                   # block 2 is quantised
     o.crop(13)
+    assert o.cold.tolist() == [3, 3]
     o.release_rows([1])
     assert o.cold.tolist() == [3, 0]
+
+
+def test_crop_reopens_quantised_blocks_with_their_read():
+    """A crop to 10 tokens re-opens block 2 (positions 8..11): afterwards every position reads
+    the bits it read before the crop (the re-opened block holds its dequantised read), and
+    quantising that content again when the block leaves the window anew reads the same bits
+    once more (power-of-two scales put a dequantised group on its own grid, and bf16 holds
+    every code * 2^e exactly)."""
+    from kvgen import hf_layout, to_bits
+
+    P, W = 4, 8
+    o = q.QuantLayerOracle(1, 64, P, W, "bf16")
+    gen = torch.Generator().manual_seed(1)
+    k, v = hf_layout(1, 2, 21, 16, torch.bfloat16, gen), hf_layout(1, 2, 21, 16, torch.bfloat16, gen)
+    o.append(to_bits(k), to_bits(v))
+    before = o.current_tensors()
+    stored = o.keys[0, :, 2].copy()
+    o.crop(10)
+    assert o.cold.tolist() == [2]
+    assert not np.array_equal(o.keys[0, :, 2], stored)  # the content itself changed ...
+    got = o._read(o.keys[:1], True).reshape(1, 2, -1, 16)[..., :21, :]
+    assert np.array_equal(got, before[0])               # ... to what was read
+    o.append(to_bits(k[:, :, :12]), to_bits(v[:, :, :12]))  # to 22: blocks 0..2 quantised again
+    assert o.cold.tolist() == [3]
+    after = o.current_tensors()
+    assert np.array_equal(after[0][..., :10, :], before[0][..., :10, :])
+    assert np.array_equal(after[1][..., :10, :], before[1][..., :10, :])
