@@ -28,6 +28,7 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxTokenHeads = 4096;  // page_size * kv_heads: a compress workgroup's value maxima
 constexpr int kMaxChannels = 16384;   // kv_heads * head_dim: a compress workgroup's key exponents
 constexpr int kUnroll = 4;            // vectors in flight per gather thread
+constexpr int kGatherThreads = 256;   // a gather workgroup: 4 waves
 constexpr int64_t kI32Max = 0x7fffffffLL;
 
 __device__ __forceinline__ int checked_id(int id, int64_t n) { return (id >= 0 && (int64_t)id < n) ? id : -1; }
@@ -318,8 +319,86 @@ struct Vec {
   };
 };
 
+// VE elements from their E4M3 codes and scales: keys with VE per-channel scale bytes (ksc),
+// values with one per-token scale byte (vsc).  Exact: code * 2^(s - 127) rounded once to the
+// element type.
 template <int KIND, int VE>
-__global__ void __launch_bounds__(kThreads) gather_cold_kernel(const GatherArgs a) {
+__device__ __forceinline__ typename Vec<KIND, VE>::Out dequant_vec(typename Vec<KIND, VE>::CodeU codes,
+                                                                  typename Vec<KIND, VE>::CodeU ksc, uint32_t vsc,
+                                                                  int kv) {
+  using V = Vec<KIND, VE>;
+  using E = Elem<KIND>;
+  using Bits = typename E::Bits;
+  typename V::OutU val;
+  if constexpr (VE == 8 && KIND != BARQ_KV_FP32) {
+    const uint32_t w0 = codes.v.x, w1 = codes.v.y;
+    // Hardware decode (gfx950: OCP E4M3, exact for every finite code) times 2^(s - 127), exact in
+    // fp32 while the scale bytes stay in [64, 191]; rounded to the output type as from_float
+    // does.  NaN codes (the hardware drops their sign) and other scales take the paths below.
+    const uint32_t sk0 = kv == 0 ? ksc.v.x : vsc * 0x01010101u;
+    const uint32_t sk1 = kv == 0 ? ksc.v.y : vsc * 0x01010101u;
+    const uint32_t mid = ((sk0 >> 1) ^ sk0) & ((sk1 >> 1) ^ sk1) & 0x40404040u;
+    const uint32_t n0 = (w0 & 0x7F7F7F7Fu) ^ 0x7F7F7F7Fu, n1 = (w1 & 0x7F7F7F7Fu) ^ 0x7F7F7F7Fu;
+    const uint32_t nan = (((n0 - 0x01010101u) & ~n0) | ((n1 - 0x01010101u) & ~n1)) & 0x80808080u;
+    if (mid == 0x40404040u && nan == 0) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const uint32_t w = j ? w1 : w0, sw = j ? sk1 : sk0;
+        const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+        const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+        const float f[4] = {lo[0] * __uint_as_float((sw & 0xFFu) << 23),
+                            lo[1] * __uint_as_float(((sw >> 8) & 0xFFu) << 23),
+                            hi[0] * __uint_as_float(((sw >> 16) & 0xFFu) << 23),
+                            hi[1] * __uint_as_float((sw >> 24) << 23)};
+        // The hardware reads code 0x80 as +0: every code's sign bit goes back on its value.
+        if constexpr (KIND == BARQ_KV_BF16) {  // exact values: the top halves
+          const uint32_t p0 = __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u) |
+                              ((w << 8) & 0x8000u) | ((w << 16) & 0x80000000u);
+          const uint32_t p1 = __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u) |
+                              ((w >> 8) & 0x8000u) | (w & 0x80000000u);
+          val.e[4 * j] = (Bits)p0;
+          val.e[4 * j + 1] = (Bits)(p0 >> 16);
+          val.e[4 * j + 2] = (Bits)p1;
+          val.e[4 * j + 3] = (Bits)(p1 >> 16);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            val.e[4 * j + e] = (Bits)(E::from_float(f[e]) | (((w >> (8 * e + 7)) & 1u) << 15));
+        }
+      }
+      return val.v;
+    }
+    uint32_t s0, s1, s2, s3;  // scale pairs, spread like the code pairs
+    bool fast = codes_normal(w0) && codes_normal(w1);
+    if (kv == 0) {
+#pragma unroll
+      for (int e = 0; e < VE; ++e) fast = fast && scale_fast<KIND>(ksc.b[e]);
+      s0 = spread_lo(ksc.v.x);
+      s1 = spread_hi(ksc.v.x);
+      s2 = spread_lo(ksc.v.y);
+      s3 = spread_hi(ksc.v.y);
+    } else {
+      fast = fast && scale_fast<KIND>(vsc);
+      s0 = s1 = s2 = s3 = vsc | (vsc << 16);
+    }
+    if (fast) {
+      uint32_t r[4] = {fast_pair<KIND>(spread_lo(w0), s0), fast_pair<KIND>(spread_hi(w0), s1),
+                       fast_pair<KIND>(spread_lo(w1), s2), fast_pair<KIND>(spread_hi(w1), s3)};
+      return *(typename V::Out*)r;
+    }
+  }
+  if (kv == 0) {
+#pragma unroll
+    for (int e = 0; e < VE; ++e) val.e[e] = E::from_float(ldexpf(e4m3_decode(codes.b[e]), (int)ksc.b[e] - 127));
+  } else {
+#pragma unroll
+    for (int e = 0; e < VE; ++e) val.e[e] = E::from_float(ldexpf(e4m3_decode(codes.b[e]), (int)vsc - 127));
+  }
+  return val.v;
+}
+
+template <int KIND, int VE>
+__global__ void __launch_bounds__(kGatherThreads) gather_cold_kernel(const GatherArgs a) {
   using V = Vec<KIND, VE>;
   using E = Elem<KIND>;
   using Bits = typename E::Bits;
@@ -330,6 +409,10 @@ __global__ void __launch_bounds__(kThreads) gather_cold_kernel(const GatherArgs 
   const int b = (int)a.div_nblk.div((uint32_t)bj);
   const int j = bj - b * a.nblk;
   const int P = (int)p.page_size, H = (int)p.kv_heads, D = (int)p.head_dim;
+  const int pos0 = j * P;
+  // The row's mark and the block's entry are read together with the lengths (one round trip).
+  const int hw = p.high_water[b];
+  const int stored = p.block_table[(int64_t)b * p.max_blocks + j];
   if (a.from_device) {
     if (threadIdx.x < kWave) {
       int m = 0;
@@ -341,10 +424,8 @@ __global__ void __launch_bounds__(kThreads) gather_cold_kernel(const GatherArgs 
     __syncthreads();
   }
   const int S = a.from_device ? s_seq : a.seq_out;
-  const int pos0 = j * P;
   if (pos0 >= S) return;  // uniform
-  const int hw = p.high_water[b];
-  const int entry = pos0 < hw ? p.block_table[(int64_t)b * p.max_blocks + j] : -1;
+  const int entry = pos0 < hw ? stored : -1;
   const int hot = checked_id(entry, p.num_pages);
   const int cold = entry <= -2 ? checked_id(-2 - entry, a.c.num_cold) : -1;
   if (entry <= -2 && cold < 0 && threadIdx.x == 0) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], BARQ_KV_ERRBIT_BAD_INDEX);
@@ -353,115 +434,170 @@ __global__ void __launch_bounds__(kThreads) gather_cold_kernel(const GatherArgs 
   Bits* out = (Bits*)a.out[kv] + (int64_t)b * a.osb;
   const int live = min(S, hw) - pos0;  // positions of this block with data
   const int end = min(S - pos0, P);    // positions of this block in the output
-  for (int v0 = threadIdx.x; v0 < nvec; v0 += kThreads * kUnroll) {
+  const int slot = hot >= 0 ? hot : cold;
+  // Every load of a round is issued before any value is used (one round trip per round).
+  for (int v0 = threadIdx.x; v0 < nvec; v0 += kGatherThreads * kUnroll) {
     typename V::OutU val[kUnroll];
-    int64_t at[kUnroll];
-    bool in[kUnroll];
+    int64_t at[kUnroll], el[kUnroll];
+    int tok[kUnroll], head[kUnroll], col[kUnroll];
+    bool in[kUnroll], has[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int v = v0 + u * kThreads;
+      const int v = v0 + u * kGatherThreads;
       const int h = (int)a.div_head.div((uint32_t)v);
       const int rem = v - h * (int)a.div_head.d;
       const int t = (int)a.div_dv.div((uint32_t)rem);
       const int dv = rem - t * dv_n;
       in[u] = v < nvec && t < end;
+      has[u] = in[u] && t < live && slot >= 0;
       at[u] = (int64_t)h * a.osh + (int64_t)(pos0 + t) * a.oss + (int64_t)dv * VE;
+      el[u] = (((int64_t)slot * P + t) * H + h) * D + (int64_t)dv * VE;
+      tok[u] = t;
+      head[u] = h;
+      col[u] = dv * VE;
       val[u].v = typename V::Out(0);
-      if (!in[u] || t >= live) continue;
-      const int64_t el = (((int64_t)(hot >= 0 ? hot : cold) * P + t) * H + h) * D + (int64_t)dv * VE;
-      if (hot >= 0) {
-        const char* base = kv ? (const char*)p.value_pages : (const char*)p.key_pages;
-        val[u].v = __builtin_nontemporal_load((const typename V::Out*)(base + el * (int64_t)sizeof(Bits)));
-      } else if (cold >= 0) {
-        typename V::CodeU codes;
-        codes.v = __builtin_nontemporal_load((const typename V::Codes*)(a.c.codes[kv] + el));
-        if constexpr (VE == 8 && KIND != BARQ_KV_FP32) {
-          const uint32_t w0 = codes.v.x, w1 = codes.v.y;
-          {
-            // Hardware decode (gfx950: OCP E4M3, exact for every finite code) times 2^(s - 127),
-            // exact in fp32 while the scale bytes stay in [64, 191]; rounded to the output type
-            // as from_float does.  NaN codes (the hardware drops their sign) and other scales
-            // take the paths below.
-            uint32_t sk0, sk1;
-            if (kv == 0) {
-              typename V::CodeU sc;
-              sc.v = *(const typename V::Codes*)(a.c.key_scales + ((int64_t)cold * H + h) * D + (int64_t)dv * VE);
-              sk0 = sc.v.x;
-              sk1 = sc.v.y;
-            } else {
-              sk0 = sk1 = (uint32_t)a.c.value_scales[((int64_t)cold * P + t) * H + h] * 0x01010101u;
-            }
-            const uint32_t mid = ((sk0 >> 1) ^ sk0) & ((sk1 >> 1) ^ sk1) & 0x40404040u;
-            const uint32_t n0 = (w0 & 0x7F7F7F7Fu) ^ 0x7F7F7F7Fu, n1 = (w1 & 0x7F7F7F7Fu) ^ 0x7F7F7F7Fu;
-            const uint32_t nan = (((n0 - 0x01010101u) & ~n0) | ((n1 - 0x01010101u) & ~n1)) & 0x80808080u;
-            if (mid == 0x40404040u && nan == 0) {
+    }
+    if (hot >= 0) {  // uniform
+      const char* base = kv ? (const char*)p.value_pages : (const char*)p.key_pages;
 #pragma unroll
-              for (int j = 0; j < 2; ++j) {
-                const uint32_t w = j ? w1 : w0, sw = j ? sk1 : sk0;
-                const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
-                const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
-                const float f[4] = {lo[0] * __uint_as_float((sw & 0xFFu) << 23),
-                                    lo[1] * __uint_as_float(((sw >> 8) & 0xFFu) << 23),
-                                    hi[0] * __uint_as_float(((sw >> 16) & 0xFFu) << 23),
-                                    hi[1] * __uint_as_float((sw >> 24) << 23)};
-                // The hardware reads code 0x80 as +0: every code's sign bit goes back on its value.
-                if constexpr (KIND == BARQ_KV_BF16) {  // exact values: the top halves
-                  const uint32_t p0 = __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u) |
-                                      ((w << 8) & 0x8000u) | ((w << 16) & 0x80000000u);
-                  const uint32_t p1 = __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u) |
-                                      ((w >> 8) & 0x8000u) | (w & 0x80000000u);
-                  val[u].e[4 * j] = (Bits)p0;
-                  val[u].e[4 * j + 1] = (Bits)(p0 >> 16);
-                  val[u].e[4 * j + 2] = (Bits)p1;
-                  val[u].e[4 * j + 3] = (Bits)(p1 >> 16);
-                } else {
+      for (int u = 0; u < kUnroll; ++u)
+        if (has[u]) val[u].v = __builtin_nontemporal_load((const typename V::Out*)(base + el[u] * (int64_t)sizeof(Bits)));
+    } else if (cold >= 0) {  // uniform
+      typename V::CodeU codes[kUnroll], ksc[kUnroll];
+      uint32_t vsc[kUnroll];
 #pragma unroll
-                  for (int e = 0; e < 4; ++e)
-                    val[u].e[4 * j + e] = (Bits)(E::from_float(f[e]) | (((w >> (8 * e + 7)) & 1u) << 15));
-                }
-              }
-              continue;
-            }
-          }
-          uint32_t s0, s1, s2, s3;  // scale pairs, spread like the code pairs
-          bool fast = codes_normal(w0) && codes_normal(w1);
-          if (kv == 0) {
-            typename V::CodeU sc;
-            sc.v = *(const typename V::Codes*)(a.c.key_scales + ((int64_t)cold * H + h) * D + (int64_t)dv * VE);
-#pragma unroll
-            for (int e = 0; e < VE; ++e) fast = fast && scale_fast<KIND>(sc.b[e]);
-            s0 = spread_lo(sc.v.x);
-            s1 = spread_hi(sc.v.x);
-            s2 = spread_lo(sc.v.y);
-            s3 = spread_hi(sc.v.y);
-          } else {
-            const uint32_t sv = a.c.value_scales[((int64_t)cold * P + t) * H + h];
-            fast = fast && scale_fast<KIND>(sv);
-            s0 = s1 = s2 = s3 = sv | (sv << 16);
-          }
-          if (fast) {
-            uint32_t r[4] = {fast_pair<KIND>(spread_lo(w0), s0), fast_pair<KIND>(spread_hi(w0), s1),
-                             fast_pair<KIND>(spread_lo(w1), s2), fast_pair<KIND>(spread_hi(w1), s3)};
-            val[u].v = *(typename V::Out*)r;
-            continue;
-          }
-        }
-        if (kv == 0) {
-          typename V::CodeU sc;
-          sc.v = *(const typename V::Codes*)(a.c.key_scales + ((int64_t)cold * H + h) * D + (int64_t)dv * VE);
-#pragma unroll
-          for (int e = 0; e < VE; ++e)
-            val[u].e[e] = E::from_float(ldexpf(e4m3_decode(codes.b[e]), (int)sc.b[e] - 127));
-        } else {
-          const int ve = (int)a.c.value_scales[((int64_t)cold * P + t) * H + h] - 127;
-#pragma unroll
-          for (int e = 0; e < VE; ++e) val[u].e[e] = E::from_float(ldexpf(e4m3_decode(codes.b[e]), ve));
-        }
+      for (int u = 0; u < kUnroll; ++u) {
+        codes[u].v = typename V::Codes(0);
+        ksc[u].v = typename V::Codes(0);
+        vsc[u] = 0;
+        if (!has[u]) continue;
+        codes[u].v = __builtin_nontemporal_load((const typename V::Codes*)(a.c.codes[kv] + el[u]));
+        if (kv == 0)
+          ksc[u].v = *(const typename V::Codes*)(a.c.key_scales + ((int64_t)cold * H + head[u]) * D + col[u]);
+        else
+          vsc[u] = a.c.value_scales[((int64_t)cold * P + tok[u]) * H + head[u]];
       }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u)
+        if (has[u]) val[u].v = dequant_vec<KIND, VE>(codes[u], ksc[u], vsc[u], kv);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)
       if (in[u]) __builtin_nontemporal_store(val[u].v, (typename V::Out*)(out + at[u]));
+  }
+}
+
+// The gather for 8-element vectors (2-byte elements) when a token's kv_heads * head_dim
+// elements are 64 * LPP vectors: a wave moves whole positions, lane l taking vectors l, l + 64,
+// ... of each, so a lane's columns -- and its key scales -- are fixed for the tile and only the
+// position varies (wave-uniform).  Each wave holds 8 vectors per lane in flight (8 / LPP
+// positions a round); per-channel key scales are read once per tile.
+template <int KIND, int LPP>
+__global__ void __launch_bounds__(kGatherThreads) gather_cold_lanes_kernel(const GatherArgs a) {
+  using V = Vec<KIND, 8>;
+  using E = Elem<KIND>;
+  using Bits = typename E::Bits;
+  constexpr int kNPos = 8 / LPP;  // positions a wave moves per round
+  constexpr int kWavesPerTile = kGatherThreads / kWave;
+  __shared__ int s_seq;
+  const barq_kv_pool& p = a.p;
+  const int kv = blockIdx.x & 1;
+  const int bj = blockIdx.x >> 1;
+  const int b = (int)a.div_nblk.div((uint32_t)bj);
+  const int j = bj - b * a.nblk;
+  const int P = (int)p.page_size, H = (int)p.kv_heads, D = (int)p.head_dim;
+  const int pos0 = j * P;
+  const int hw = p.high_water[b];
+  const int stored = p.block_table[(int64_t)b * p.max_blocks + j];
+  if (a.from_device) {
+    if (threadIdx.x < kWave) {
+      int m = 0;
+      for (int i = threadIdx.x; i < a.batch; i += kWave) m = max(m, p.seq_lens[i]);
+#pragma unroll
+      for (int o = kWave / 2; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, kWave));
+      if (threadIdx.x == 0) s_seq = min(m, a.seq_out);
+    }
+    __syncthreads();
+  }
+  const int S = a.from_device ? s_seq : a.seq_out;
+  if (pos0 >= S) return;  // uniform
+  const int entry = pos0 < hw ? stored : -1;
+  const int hot = checked_id(entry, p.num_pages);
+  const int cold = entry <= -2 ? checked_id(-2 - entry, a.c.num_cold) : -1;
+  if (entry <= -2 && cold < 0 && threadIdx.x == 0) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], BARQ_KV_ERRBIT_BAD_INDEX);
+  const int live = min(S, hw) - pos0;
+  const int end = min(S - pos0, P);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int HD = H * D;
+  const int dvn = D / 8;
+  // this lane's columns: element offsets within a token row and within an output position
+  int col[LPP];
+  int64_t ocol[LPP];
+#pragma unroll
+  for (int c = 0; c < LPP; ++c) {
+    const int vi = c * kWave + lane;
+    const int h = vi / dvn;
+    col[c] = vi * 8;
+    ocol[c] = (int64_t)h * a.osh + (int64_t)(vi - h * dvn) * 8;
+  }
+  Bits* out = (Bits*)a.out[kv] + (int64_t)b * a.osb + (int64_t)pos0 * a.oss;
+  typename V::CodeU ksc[LPP];
+  if (cold >= 0 && kv == 0) {
+#pragma unroll
+    for (int c = 0; c < LPP; ++c) ksc[c].v = *(const typename V::Codes*)(a.c.key_scales + (int64_t)cold * HD + col[c]);
+  }
+  for (int t0 = wave * kNPos; t0 < end; t0 += kWavesPerTile * kNPos) {
+    Bits* o = out + (int64_t)t0 * a.oss;
+    if (hot >= 0) {  // uniform: a copy, every load of the round in flight before the stores
+      const char* base = (kv ? (const char*)p.value_pages : (const char*)p.key_pages) +
+                         ((int64_t)hot * P + t0) * HD * (int64_t)sizeof(Bits);
+      typename V::OutU val[kNPos][LPP];
+#pragma unroll
+      for (int i = 0; i < kNPos; ++i)
+#pragma unroll
+        for (int c = 0; c < LPP; ++c) {
+          val[i][c].v = typename V::Out(0);
+          if (t0 + i < live)
+            val[i][c].v = __builtin_nontemporal_load(
+                (const typename V::Out*)(base + ((int64_t)i * HD + col[c]) * (int64_t)sizeof(Bits)));
+        }
+#pragma unroll
+      for (int i = 0; i < kNPos; ++i)
+#pragma unroll
+        for (int c = 0; c < LPP; ++c)
+          if (t0 + i < end) __builtin_nontemporal_store(val[i][c].v, (typename V::Out*)(o + (int64_t)i * a.oss + ocol[c]));
+    } else if (cold >= 0) {  // uniform: codes and scales of the round in flight, then decode + store
+      const uint8_t* codes = a.c.codes[kv] + ((int64_t)cold * P + t0) * HD;
+      typename V::CodeU cv[kNPos][LPP];
+      uint32_t vsc[kNPos][LPP];
+#pragma unroll
+      for (int i = 0; i < kNPos; ++i)
+#pragma unroll
+        for (int c = 0; c < LPP; ++c) {
+          cv[i][c].v = typename V::Codes(0);
+          vsc[i][c] = 0;
+          if (t0 + i < live) {
+            cv[i][c].v = __builtin_nontemporal_load((const typename V::Codes*)(codes + (int64_t)i * HD + col[c]));
+            if (kv) vsc[i][c] = a.c.value_scales[((int64_t)cold * P + t0 + i) * H + (c * kWave + lane) / dvn];
+          }
+        }
+#pragma unroll
+      for (int i = 0; i < kNPos; ++i)
+#pragma unroll
+        for (int c = 0; c < LPP; ++c) {
+          if (t0 + i >= end) continue;
+          const typename V::Out v =
+              t0 + i < live ? dequant_vec<KIND, 8>(cv[i][c], ksc[c], vsc[i][c], kv) : typename V::Out(0);
+          __builtin_nontemporal_store(v, (typename V::Out*)(o + (int64_t)i * a.oss + ocol[c]));
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kNPos; ++i)
+#pragma unroll
+        for (int c = 0; c < LPP; ++c)
+          if (t0 + i < end) __builtin_nontemporal_store(typename V::Out(0), (typename V::Out*)(o + (int64_t)i * a.oss + ocol[c]));
+    }
   }
 }
 
@@ -700,15 +836,18 @@ const void* compress_fn(int64_t kind, int ve) {
 }
 
 template <int KIND>
-int launch_gather(int ve, dim3 grid, GatherArgs* a, hipStream_t s) {
+int launch_gather(int ve, int lpp, dim3 grid, GatherArgs* a, hipStream_t s) {
+  const void* fn = (const void*)&gather_cold_kernel<KIND, 1>;
   if constexpr (KIND != BARQ_KV_FP32) {  // 8 two-byte elements: a 16-byte vector
-    if (ve == 8) return launch((const void*)&gather_cold_kernel<KIND, 8>, grid, a, s);
+    if (ve == 8) fn = (const void*)&gather_cold_kernel<KIND, 8>;
+    if (ve == 8 && lpp == 1) fn = (const void*)&gather_cold_lanes_kernel<KIND, 1>;
+    if (ve == 8 && lpp == 2) fn = (const void*)&gather_cold_lanes_kernel<KIND, 2>;
+    if (ve == 8 && lpp == 4) fn = (const void*)&gather_cold_lanes_kernel<KIND, 4>;
   }
-  switch (ve) {
-    case 4: return launch((const void*)&gather_cold_kernel<KIND, 4>, grid, a, s);
-    case 2: return launch((const void*)&gather_cold_kernel<KIND, 2>, grid, a, s);
-    default: return launch((const void*)&gather_cold_kernel<KIND, 1>, grid, a, s);
-  }
+  if (ve == 4) fn = (const void*)&gather_cold_kernel<KIND, 4>;
+  if (ve == 2) fn = (const void*)&gather_cold_kernel<KIND, 2>;
+  void* args[] = {a};
+  return hipLaunchKernel(fn, grid, dim3(kGatherThreads), args, 0, s) == hipSuccess ? BARQ_KV_OK : BARQ_KV_ERR_LAUNCH;
 }
 
 }  // namespace
@@ -778,11 +917,17 @@ int barq_kv_gather_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, void
   a.div_nblk = FastDiv::make((uint32_t)a.nblk);
   const int64_t tiles = batch * a.nblk * 2;
   if (tiles > kI32Max) return BARQ_KV_ERR_INVALID;
+  // Whole positions per wave: a token row of 64 * lpp vectors, and 32-bit offsets within a page
+  const int64_t hd8 = pool->kv_heads * D / 8;
+  const int lpp = (ve == 8 && D % 8 == 0 && hd8 % kWave == 0 &&
+                   (hd8 / kWave == 1 || hd8 / kWave == 2 || hd8 / kWave == 4) &&
+                   pool->page_size * pool->kv_heads * D <= kI32Max)
+                      ? (int)(hd8 / kWave) : 0;
   hipStream_t s = (hipStream_t)stream;
   switch (cold->element_type) {
-    case BARQ_KV_BF16: return launch_gather<BARQ_KV_BF16>(ve, dim3((uint32_t)tiles), &a, s);
-    case BARQ_KV_FP16: return launch_gather<BARQ_KV_FP16>(ve, dim3((uint32_t)tiles), &a, s);
-    default: return launch_gather<BARQ_KV_FP32>(ve, dim3((uint32_t)tiles), &a, s);
+    case BARQ_KV_BF16: return launch_gather<BARQ_KV_BF16>(ve, lpp, dim3((uint32_t)tiles), &a, s);
+    case BARQ_KV_FP16: return launch_gather<BARQ_KV_FP16>(ve, lpp, dim3((uint32_t)tiles), &a, s);
+    default: return launch_gather<BARQ_KV_FP32>(ve, lpp, dim3((uint32_t)tiles), &a, s);
   }
 }
 
