@@ -8,7 +8,9 @@
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 
+#include <algorithm>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "barq_kv.h"
@@ -367,6 +369,72 @@ void pool_select_rows_cold_(std::vector<std::vector<at::Tensor>> pools, std::vec
                "pool_select_rows_cold_");
 }
 
+// One decode-step call of PagePool.update / append with its host planning in C++: the capacity
+// and free-page checks of the host shadow (int64 arrays lens / hw, updated in place on success),
+// output allocation and the launch.  handle: pool_group of this one pool; pages: its key_pages
+// (device, dtype).  Returns (key_out, value_out, pages taken); pages taken < 0 when the call must
+// take the checked Python path instead, which raises the exact error (-1: capacity exceeded, -2:
+// not enough free pages by the host count, -3: nothing to append, -4: states the pool cannot
+// take as they are).
+std::tuple<at::Tensor, at::Tensor, int64_t> pool_step_(at::Tensor handle, at::Tensor pages, at::Tensor key_states,
+                                                       at::Tensor value_states, py::buffer lens, py::buffer hw,
+                                                       int64_t free_count, int64_t limit, int64_t flags, bool gather) {
+  TORCH_CHECK(handle.device().is_cpu() && handle.scalar_type() == at::kByte &&
+                  handle.numel() == (int64_t)sizeof(barq_kv_pool),
+              "not a one-pool group (see pool_group)");
+  const barq_kv_pool p = *reinterpret_cast<const barq_kv_pool*>(handle.data_ptr<uint8_t>());
+  TORCH_CHECK(pages.is_cuda() && pages.data_ptr() == p.key_pages, "pages do not belong to the handle");
+  at::Tensor none;
+  if (key_states.dim() != 4 || value_states.sizes() != key_states.sizes() || key_states.size(1) != p.kv_heads ||
+      key_states.size(3) != p.head_dim || !key_states.is_cuda() || !value_states.is_cuda() ||
+      key_states.get_device() != pages.get_device() || value_states.get_device() != pages.get_device() ||
+      key_states.scalar_type() != pages.scalar_type() || value_states.scalar_type() != pages.scalar_type() ||
+      key_states.size(0) > p.max_batch)
+    return {none, none, -4};
+  const int64_t batch = key_states.size(0), tokens = key_states.size(2);
+  const py::buffer_info li = lens.request(true), hi = hw.request(true);
+  TORCH_CHECK(li.itemsize == 8 && hi.itemsize == 8 && li.ndim == 1 && hi.ndim == 1 && li.shape[0] >= batch &&
+                  hi.shape[0] >= batch && li.strides[0] == 8 && hi.strides[0] == 8,
+              "lens / hw must be contiguous int64 arrays of at least batch entries");
+  int64_t* L = static_cast<int64_t*>(li.ptr);
+  int64_t* W = static_cast<int64_t*>(hi.ptr);
+  if (batch == 0 || tokens == 0) return {none, none, -3};
+  const int64_t P = p.page_size;
+  int64_t worst = 0, need = 0;
+  for (int64_t r = 0; r < batch; ++r) {
+    const int64_t end = L[r] + tokens;
+    worst = std::max(worst, end);
+    need += std::max<int64_t>(std::min((end + P - 1) / P, p.max_blocks) - (W[r] + P - 1) / P, 0);
+  }
+  if (worst > limit || worst > p.max_blocks * P) return {none, none, -1};
+  if (need > free_count) return {none, none, -2};
+  at::Tensor k = key_states, v = value_states;
+  if (k.stride(3) != 1 || v.stride(3) != 1 || !same_layout(k, v)) {
+    k = k.contiguous();
+    v = v.contiguous();
+  }
+  c10::DeviceGuard guard(pages.device());
+  at::Tensor ko, vo;
+  int rc;
+  if (gather) {
+    at::Tensor both = at::empty({2, batch, p.kv_heads, worst, p.head_dim}, pages.options());
+    ko = both[0];
+    vo = both[1];
+    rc = barq_kv_update(&p, k.data_ptr(), v.data_ptr(), batch, tokens, k.stride(0), k.stride(1), k.stride(2),
+                        ko.data_ptr(), vo.data_ptr(), worst, ko.stride(0), ko.stride(1), ko.stride(2), flags,
+                        current_stream(pages));
+  } else {
+    rc = barq_kv_append(&p, k.data_ptr(), v.data_ptr(), batch, tokens, k.stride(0), k.stride(1), k.stride(2),
+                        current_stream(pages));
+  }
+  check_status(rc, gather ? "pool_update_" : "pool_append_");
+  for (int64_t r = 0; r < batch; ++r) {
+    L[r] += tokens;
+    W[r] = std::max(W[r], L[r]);
+  }
+  return {ko, vo, need};
+}
+
 // The pools of a model's layers packed as an array of barq_kv_pool (a CPU uint8 tensor), for
 // the batched entry points.  The array holds raw device pointers: the caller keeps the pools'
 // tensors alive and unmoved while it uses it.
@@ -493,6 +561,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("pool_select_rows_cold_", &pool_select_rows_cold_,
         "One row selection applied to pools with cold stores, sharing quantised blocks");
   m.def("pool_group", &pool_group, "Pack the pools of a model's layers for the batched entry points");
+  m.def("pool_step_", &pool_step_, "One update / append with its host planning (see PagePool.update)");
   m.def("select_workspace_words", &select_workspace_words, "Workspace words of pool_group_select_rows_");
   m.def("pool_group_select_rows_", &pool_group_select_rows_,
         "One row selection applied to every pool of a group, sharing full pages");

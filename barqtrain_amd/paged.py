@@ -238,8 +238,26 @@ class PagePool:
             return key_states.contiguous(), value_states.contiguous()
         return key_states, value_states
 
+    def _step(self, key_states, value_states, max_length, flags, gather):
+        """One update (gather) or append with the host planning done in the binding (pool_step_):
+        returns (key_out, value_out, pages taken), or pages taken < 0 when the call must take the
+        checked path (which raises the exact error, or handles an empty call)."""
+        backend = _gpu_backend()
+        handle = self.__dict__.get("_handle")
+        if handle is None or handle[0] != self.generation:
+            handle = (self.generation, backend.pool_group([self.tensors]))
+            self._handle = handle
+        limit = self.capacity if max_length is None else int(max_length)
+        ko, vo, need = backend.pool_step_(handle[1], self.key_pages, key_states, value_states, self.lens, self.hw,
+                                          self.free_count, limit, flags, gather)
+        if need >= 0:
+            self.free_count -= need
+        return ko, vo, need
+
     def append(self, key_states: torch.Tensor, value_states: torch.Tensor,
                max_length: Optional[int] = None) -> None:
+        if self.on_gpu and self._step(key_states, value_states, max_length, 0, False)[2] >= 0:
+            return
         self._check_states(key_states, value_states)
         batch, _, tokens, _ = key_states.shape
         need = self.check_append(batch, tokens, max_length)
@@ -307,6 +325,10 @@ class PagePool:
                max_length: Optional[int] = None, out=None, seq_out: Optional[int] = None,
                flags: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
         """Append, then materialise rows [0, batch) up to the longest row, in one pass."""
+        if self.on_gpu and out is None and seq_out is None:
+            ko, vo, need = self._step(key_states, value_states, max_length, flags, True)
+            if need >= 0:
+                return ko, vo
         self._check_states(key_states, value_states)
         batch, _, tokens, _ = key_states.shape
         need, worst = self._plan_append(batch, tokens, max_length)

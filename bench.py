@@ -122,6 +122,8 @@ def parse():
     ap.add_argument("--no-attention", action="store_true", help="skip the paged decode-attention leg")
     ap.add_argument("--no-beam", action="store_true", help="skip the beam-reorder (select_rows) leg")
     ap.add_argument("--quant", action="store_true", help="add the fp8 quantised-KV leg (not run by default)")
+    ap.add_argument("--batch", type=int, default=None,
+                    help="rows per layer instead of the config's (small-launch characterisation, e.g. --batch 1)")
     ap.add_argument("--bucket", type=int, default=None,
                     help="graph extent bucket in positions (default: the step's own; 0: one graph over the capacity)")
     return ap.parse_args()
@@ -772,6 +774,10 @@ def main():
         raise SystemExit("barqtrain_cuda HIP backend not built (python -m barqtrain_amd.build)")
     torch.cuda.set_device(0)
     cfg = CONFIGS[args.config]
+    if args.batch is not None:
+        if args.batch < 1 or "churn" in cfg or cfg["prefill"][0] != "uniform":
+            raise SystemExit("--batch takes a positive row count, for configurations with a uniform prefill")
+        cfg = dict(cfg, batch=args.batch, name=f"{cfg['name']} (batch {args.batch})")
     steps = args.steps if args.steps is not None else cfg["decode"]
     big = args.config >= 3
     warmup = args.warmup if args.warmup is not None else (2 if big else 16)

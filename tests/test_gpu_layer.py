@@ -352,3 +352,48 @@ def test_long_prefill_stays_within_memory(hip):
     ref = torch.matmul(torch.softmax(sc, -1), vv.float().repeat_interleave(G, 1)).transpose(1, 2)
     err = (out[:, -rows:].float() - ref).abs().max().item()
     assert err <= 2.0 ** -7 * ref.abs().max().item() + 1e-3, err
+
+
+def test_eager_step_planned_in_the_binding(hip):
+    """PagePool.update / append on GPU pools plan in the binding (pool_step_): the same outputs
+    and host shadow as the checked path, and every refusal raises what the checked path raises,
+    changing nothing (free pages, capacity, dtype, batch); empty calls still gather."""
+    from barqtrain_amd.paged import PagedKVCapacityError, PagedKVPoolExhausted, PagePool
+
+    H, D, P = 2, 64, 16
+    pool = PagePool(max_batch=3, max_blocks=4, page_size=P, kv_heads=H, head_dim=D, dtype=torch.bfloat16,
+                    device="cuda", num_pages=9)
+    oracle = DenseLayerOracle(3, 64, P)
+    gen = torch.Generator().manual_seed(11)
+    for t in (20, 1, 13):
+        k, v = hf_layout(3, H, t, D, torch.bfloat16, gen), hf_layout(3, H, t, D, torch.bfloat16, gen)
+        gk, gv = pool.update(k.cuda(), v.cuda())
+        ok, ov = oracle.update(to_bits(k), to_bits(v))
+        assert_bits(gk, ok, f"K after {t}")
+        assert_bits(gv, ov, f"V after {t}")
+    k = hf_layout(2, H, 3, D, torch.bfloat16, gen)
+    pool.append(k.cuda(), k.cuda())
+    oracle.append(to_bits(k), to_bits(k))
+    assert pool.lens.tolist() == [37, 37, 34] and pool.hw.tolist() == [37, 37, 34]
+    assert pool.free_count == int(pool.ctrl[0].item()) == 9 - 9
+    gk, _ = pool.gather(2)
+    assert_bits(gk, oracle.current_tensors()[0], "K after append")
+    state = (pool.lens.copy(), pool.hw.copy(), pool.free_count)
+    one = torch.zeros((1, H, 1, D), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(PagedKVPoolExhausted):  # row 2 at 34 + 15 crosses into a fourth block
+        pool.update(torch.zeros((3, H, 15, D), dtype=torch.bfloat16, device="cuda"),
+                    torch.zeros((3, H, 15, D), dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(PagedKVCapacityError):
+        pool.update(one, one, max_length=37)
+    with pytest.raises(RuntimeError):  # the binding's dtype check, as before the fast path
+        pool.update(one.float(), one.float())
+    with pytest.raises(ValueError):
+        big = torch.zeros((4, H, 1, D), dtype=torch.bfloat16, device="cuda")
+        pool.append(big, big)
+    assert (pool.lens.copy(), pool.hw.copy(), pool.free_count)[2] == state[2]
+    assert np.array_equal(pool.lens, state[0]) and np.array_equal(pool.hw, state[1])
+    empty = torch.zeros((3, H, 0, D), dtype=torch.bfloat16, device="cuda")
+    gk, gv = pool.update(empty, empty)
+    ok, _ = oracle.update(to_bits(empty.cpu()), to_bits(empty.cpu()))
+    assert gk.shape == (3, H, 37, D)
+    assert_bits(gk, ok, "K of an empty update")
