@@ -291,6 +291,41 @@ __device__ void commit_from_lanes(const barq_kv_pool& p, int batch, int tokens, 
   if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
 }
 
+// The tile arrives -- on one of BARQ_KV_CTRL_SUBCOUNTERS sub-counters, whose last arrivals count
+// on the main counter -- and the last tile to arrive commits the launch's append.  A
+// sub-counter's last arrival reads the commit inputs (every row's length and mark, the stack
+// top) together with its main arrival: until the last arrival commits nothing writes them, so
+// they are the launch's starting state.  The stack entries new blocks take are read only when
+// there are new blocks.  Run by a whole wave (the control wave), after every wave of the tile
+// holds the metadata it uses.
+__device__ void arrive_and_commit(const barq_kv_pool& p, int nsub, int batch, int tokens, int limit,
+                                  const FastDiv& div_page) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int sublast = 0;
+  if (lane == 0) {
+    const int sub = (int)blockIdx.x % nsub;
+    const int expect = ((int)gridDim.x - sub + nsub - 1) / nsub;
+    int* counter = &p.ctrl[BARQ_KV_CTRL_SUBCOUNTER0 + sub * BARQ_KV_CTRL_SUBCOUNTER_STRIDE];
+    sublast = atomicAdd(counter, 1) == expect - 1;
+    if (sublast) atomicExch(counter, 0);
+  }
+  if (!__builtin_amdgcn_readfirstlane(sublast)) return;
+  int last = 0;
+  if (lane == 0) last = atomicAdd(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 1) == nsub - 1;
+  int c_len = 0, c_hw = 0;
+  if (lane < batch) {
+    c_len = p.seq_lens[lane];
+    c_hw = p.high_water[lane];
+  }
+  const int c_top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
+  if (!__builtin_amdgcn_readfirstlane(last)) return;
+  const int news = wave_sum(lane < batch ? new_blocks(c_len, c_hw, tokens, (int)p.max_blocks, div_page).count : 0);
+  const int fidx = c_top - 1 - lane;
+  const int c_free = news > 0 && fidx >= 0 ? p.free_pages[fidx] : -1;
+  commit_from_lanes(p, batch, tokens, limit, div_page, c_len, c_hw, c_top, c_free);
+  if (lane == 0) atomicExch(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 0);
+}
+
 // ---------------------------------------------------------------------------------------------
 // Append / gather / update.
 //
@@ -464,33 +499,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a) {
   if (early && threadIdx.x < kWave) {
     // Control wave.  Every metadata value this tile uses was read before the barrier, so the
     // tile arrives now, and the copy waves never wait for the arrival or the commit.
-    const int lane = threadIdx.x;
-    int last = 0;
-    if (lane == 0) {
-      const int nsub = a.nsub;
-      const int sub = (int)blockIdx.x % nsub;
-      const int expect = ((int)gridDim.x - sub + nsub - 1) / nsub;
-      int* counter = &p.ctrl[BARQ_KV_CTRL_SUBCOUNTER0 + sub * BARQ_KV_CTRL_SUBCOUNTER_STRIDE];
-      if (atomicAdd(counter, 1) == expect - 1) {
-        atomicExch(counter, 0);
-        last = atomicAdd(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 1) == nsub - 1;
-      }
-    }
-    if (__builtin_amdgcn_readfirstlane(last)) {
-      // Every tile has read the metadata it uses and only this wave writes it in this launch, so
-      // the commit inputs read now are the launch's starting state: lane r holds row r's length
-      // and mark, lane k the page the k-th new block takes.
-      int c_len = 0, c_hw = 0;
-      if (lane < a.batch) {
-        c_len = p.seq_lens[lane];
-        c_hw = p.high_water[lane];
-      }
-      const int c_top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
-      const int fidx = c_top - 1 - lane;
-      const int c_free = fidx >= 0 ? p.free_pages[fidx] : -1;
-      commit_from_lanes(p, a.batch, T, a.gather ? a.seq_out : INT_MAX, a.div_page, c_len, c_hw, c_top, c_free);
-      if (lane == 0) atomicExch(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 0);
-    }
+    arrive_and_commit(p, a.nsub, a.batch, T, a.gather ? a.seq_out : INT_MAX, a.div_page);
     return;
   }
 
@@ -783,31 +792,7 @@ __global__ void __launch_bounds__(kStreamThreads) lean_stream_kernel(const Strea
   if (wave == 0) {
     if (!committing) return;
     __syncthreads();  // every copy wave of the tile holds the metadata it uses
-    int last = 0;
-    if (lane == 0) {
-      const int nsub = a.nsub;
-      const int sub = bid % nsub;
-      const int expect = ((int)gridDim.x - sub + nsub - 1) / nsub;
-      int* counter = &p.ctrl[BARQ_KV_CTRL_SUBCOUNTER0 + sub * BARQ_KV_CTRL_SUBCOUNTER_STRIDE];
-      if (atomicAdd(counter, 1) == expect - 1) {
-        atomicExch(counter, 0);
-        last = atomicAdd(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 1) == nsub - 1;
-      }
-    }
-    if (__builtin_amdgcn_readfirstlane(last)) {
-      // Every tile has read its metadata and only this wave writes metadata in this launch, so
-      // what it reads now is the launch's starting state.
-      int c_len = 0, c_hw = 0;
-      if (lane < a.batch) {
-        c_len = p.seq_lens[lane];
-        c_hw = p.high_water[lane];
-      }
-      const int c_top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
-      const int fidx = c_top - 1 - lane;
-      const int c_free = fidx >= 0 ? p.free_pages[fidx] : -1;
-      commit_from_lanes(p, a.batch, T, a.seq_out, a.div_page, c_len, c_hw, c_top, c_free);
-      if (lane == 0) atomicExch(&p.ctrl[BARQ_KV_CTRL_ARRIVED], 0);
-    }
+    arrive_and_commit(p, a.nsub, a.batch, T, a.seq_out, a.div_page);
     return;
   }
 

@@ -107,8 +107,10 @@ class CapturedDecodeStep:
             if any(self.quantized):
                 self._graph(extent, True)
 
-    def replay(self) -> list[tuple[torch.Tensor, torch.Tensor]]:
-        """Run one captured step; returns each layer's (K, V) views ``[batch, H, seq, D]``.
+    def replay(self, views: bool = True) -> Optional[list[tuple[torch.Tensor, torch.Tensor]]]:
+        """Run one captured step; returns each layer's (K, V) views ``[batch, H, seq, D]`` of the
+        persistent outputs (None with ``views=False``, for callers that read ``key_out`` /
+        ``value_out`` themselves: two views per layer cost more host time than the replay).
         Raises, before anything runs, if any layer would pass its capacity or run out of pages."""
         B, T = self.batch, self.tokens
         p0 = self.pools[0]
@@ -138,5 +140,7 @@ class CapturedDecodeStep:
             p.free_count -= int(n)
             if c is not None:
                 p._quantised(B, *c)
+        if not views:
+            return None
         seqs = ends.max(axis=1).tolist()
         return [(k[:, :, :n], v[:, :, :n]) for k, v, n in zip(self.key_out, self.value_out, seqs)]

