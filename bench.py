@@ -227,10 +227,11 @@ def host_threads():
 
 def cpu_baseline(cfg, wl, start, steps, layers):
     """The reference CPU path (oracle/kv_oracle_torch.py) on the host's cores: `layers` layers,
-    each prefilled and advanced to the window untimed, then the window's decode updates timed
-    (churned rows are freed and re-prefilled between them, untimed).  Returns (result, layer-0
-    K/V after the window, as torch tensors).  For C1/C2 the numpy oracle on one core times layer 0
-    beside it."""
+    each prefilled untimed, then decode steps [first, start + steps) timed, where first is 0 for
+    C1/C2 (the steps before the window and the window: about ten seconds at C2) and the window's
+    start for the larger configurations (churned rows are freed and re-prefilled between steps,
+    untimed).  Returns (result, layer-0 K/V after the window, as torch tensors).  For C1/C2 the
+    numpy oracle on one core times layer 0 beside it."""
     import torch
 
     from oracle.kv_oracle import DenseLayerOracle
@@ -239,6 +240,7 @@ def cpu_baseline(cfg, wl, start, steps, layers):
     B, P, L = cfg["batch"], cfg["page"], cfg["layers"]
     cap = max(prefill_lengths(cfg)) + wl.n_steps
     refill = tuple(t.cpu() for t in wl.refill) if wl.refill is not None else None
+    first = 0 if cfg["cpu_steps"] is None else start
     threads = host_threads()
     prev = torch.get_num_threads()
     torch.set_num_threads(threads)
@@ -257,7 +259,7 @@ def cpu_baseline(cfg, wl, start, steps, layers):
                     ref.append_rows(rows, to_input(refill[0]), to_input(refill[1]))
             t0 = time.perf_counter()
             out = ref.update(kd[s], vd[s])
-            if s >= start:
+            if s >= first:
                 spent += time.perf_counter() - t0
         return spent, out
 
@@ -270,16 +272,18 @@ def cpu_baseline(cfg, wl, start, steps, layers):
                 final = out
     finally:
         torch.set_num_threads(prev)
-    nbytes = sum(wl.step_bytes[start:start + steps]) * layers / L
+    n = start + steps
+    nbytes = sum(wl.step_bytes[first:n]) * layers / L
     result = {
         "value": round(nbytes / total / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{layers} of {L} layers x the {steps} timed decode steps (append 1 token x {B} rows + "
-                  f"materialised gather), torch restatement of the reference kv_cache.py _python_append + "
-                  f"current_tensors (view + .contiguous()) on {threads} threads; same input bits",
-        "ms_per_step": round(total / steps * L / layers * 1e3, 3),
+        "sample": f"{layers} of {L} layers x decode steps {first}..{n - 1} (the GPU's timed window is steps "
+                  f"{start}..{n - 1}; append 1 token x {B} rows + materialised gather), torch restatement of "
+                  f"the reference kv_cache.py _python_append + current_tensors (view + .contiguous()) on "
+                  f"{threads} threads; same input bits",
+        "ms_per_step": round(total / (n - first) * L / layers * 1e3, 3),
         "seconds": round(total, 2),
     }
     if cfg["cpu_steps"] is None:  # C1/C2: the numpy oracle on one core, layer 0
@@ -287,8 +291,8 @@ def cpu_baseline(cfg, wl, start, steps, layers):
 
         spent, _ = timed_layer(DenseLayerOracle(B, cap, P), 0, to_bits)
         result["numpy_one_thread"] = {"value": round(nbytes / layers / spent / 1e9, 3), "cores": 1,
-                                      "ms_per_step": round(spent / steps * L * 1e3, 3),
-                                      "sample": "layer 0 x the timed steps, numpy oracle"}
+                                      "ms_per_step": round(spent / (n - first) * L * 1e3, 3),
+                                      "sample": f"layer 0 x decode steps {first}..{n - 1}, numpy oracle"}
     return result, final
 
 
@@ -987,7 +991,7 @@ def main():
         from kvgen import to_bits
 
         cpu_steps = min(cfg["cpu_steps"] or steps, steps)
-        layers = 1 if cfg["cpu_steps"] else min(args.cpu_layers or 8, L)
+        layers = 1 if cfg["cpu_steps"] else min(args.cpu_layers or L, L)
         result["cpu_baseline"], want = cpu_baseline(cfg, wl, start, cpu_steps, layers)
         # the GPU's layer 0 after the same steps, from a fresh prefill
         wl.prefill()
