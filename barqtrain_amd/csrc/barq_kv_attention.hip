@@ -45,8 +45,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
-constexpr int kHeadDim = 128;              // the one head size this kernel is built for
-constexpr int kSteps = kHeadDim / 32;      // k-steps of the score MFMA
 constexpr int kBlock = 16;                 // positions per chunk: one score MFMA's columns
 constexpr int kMaxRows = 16;               // query rows (G * T) one wave serves
 constexpr int kThreads = 256;              // workgroup of the merge kernel ...
@@ -60,6 +58,19 @@ constexpr int kMinRangeChunks = 4;         // the automatic range never goes bel
 
 enum : int { kBF16 = 0, kF16 = 1 };
 
+// Head sizes the kernels are built for (HD = 64 or 128) and the lane layout each gives.  Scores:
+// lane (g, n16) of the 16x16x32 MFMA holds dims 32 * step + 8 * g .. +7 of one position, HD / 32
+// steps.  V: a position's HD dims are HD / 8 lanes of 8 dims, so one 16-byte load per lane covers
+// 64 / (HD / 8) positions and a chunk takes 16 / that many loads.
+template <int HD>
+struct Head {
+  static_assert(HD == 64 || HD == 128, "head sizes 64 and 128");
+  static constexpr int kSteps = HD / 32;              // k-steps of the score MFMA
+  static constexpr int kVLanes = HD / 8;              // lanes of one position's V
+  static constexpr int kVPos = kWave / kVLanes;       // positions of one V load
+  static constexpr int kVLoads = kBlock / kVPos;      // V loads of one chunk
+};
+
 struct AttnArgs {
   const char* kpages;
   const char* vpages;
@@ -71,7 +82,7 @@ struct AttnArgs {
   int64_t o_sb, o_sh, o_st;  // output strides, bytes
   const char* q;
   char* out;
-  float* part;          // records of record_floats(rows), indexed range + pair
+  float* part;          // records of record_floats(rows, head_dim), indexed range + pair
   FastDiv page_div;
   int32_t row_bytes;    // bytes between positions of a page
   int32_t head_bytes;   // bytes of one head's run (head_dim elements)
@@ -98,8 +109,8 @@ struct AttnArgs {
 
 // A piece's partial: rows x head_dim unnormalised sums, then the rows' running maxima and sums,
 // padded to whole 16-byte vectors.
-__host__ __device__ constexpr int64_t record_floats(int64_t rows) {
-  return rows * kHeadDim + (2 * rows + 3) / 4 * 4;
+__host__ __device__ constexpr int64_t record_floats(int64_t rows, int64_t head_dim) {
+  return rows * head_dim + (2 * rows + 3) / 4 * 4;
 }
 
 template <int E>
@@ -280,13 +291,18 @@ __device__ __forceinline__ void load_table(const AttnArgs& a, int b, int blk0, i
 }
 
 // K and V of one 16-position chunk for this lane.  K: lane (g, n16) holds dims 32 * step + 8 * g
-// .. +7 of position tc + n16; V: dims 8 * n16 .. +7 of position tc + 4s + g.  Positions >= end
-// load nothing and read as zero.
-template <bool UNIFORM, bool PRED, bool COLD>
+// .. +7 of position tc + n16; V: lane (vpos, vdim) = (lane / (HD / 8), lane % (HD / 8)) holds
+// dims 8 * vdim .. +7 of position tc + kVPos * s + vpos.  Positions >= end load nothing and read
+// as zero.
+template <int HD, bool UNIFORM, bool PRED, bool COLD>
 __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kTableRegs], int blk0,
                                            const char* kbase, const char* vbase, int tc, int end,
-                                           int klane, int vlane, int n16, int g, int kvh, u32x4 (&kv)[kSteps],
-                                           u32x4 (&vv)[4], bool& cold) {
+                                           int klane, int vlane, int n16, int g, int vpos, int vdim, int kvh,
+                                           u32x4 (&kv)[Head<HD>::kSteps], u32x4 (&vv)[Head<HD>::kVLoads],
+                                           bool& cold) {
+  constexpr int kSteps = Head<HD>::kSteps;
+  constexpr int kVPos = Head<HD>::kVPos;
+  constexpr int kVLoads = Head<HD>::kVLoads;
   cold = false;
   if constexpr (UNIFORM) {
     // page_size is a multiple of 16: the chunk lies in one page, its base a scalar.
@@ -297,14 +313,14 @@ __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kT
         // Quantised page: raw codes and scales into the chunk registers, decoded just before the
         // chunk is computed (so the loads stay in flight meanwhile).  K: lane (g, n16) takes 8
         // codes of dims 32 st + 8 g of position tc + n16, and their 8 per-channel scales; V: 8
-        // codes of dims 8 n16 of position tc + 4 s + g, and that position's scale.
+        // codes of dims 8 vdim of position tc + kVPos s + vpos, and that position's scale.
         cold = true;
         const int c = -2 - page;
         const int t0 = tc - (int)(blk * (uint32_t)a.page_size);
-        const int64_t head = (int64_t)kvh * kHeadDim;
-        const int64_t code_page = (int64_t)c * a.page_size * a.kv_heads * kHeadDim;
-        const uint8_t* kc = a.kcodes + code_page + (int64_t)(t0 + n16) * a.kv_heads * kHeadDim + head + 8 * g;
-        const uint8_t* ks = a.kscales + ((int64_t)c * a.kv_heads) * kHeadDim + head + 8 * g;
+        const int64_t head = (int64_t)kvh * HD;
+        const int64_t code_page = (int64_t)c * a.page_size * a.kv_heads * HD;
+        const uint8_t* kc = a.kcodes + code_page + (int64_t)(t0 + n16) * a.kv_heads * HD + head + 8 * g;
+        const uint8_t* ks = a.kscales + ((int64_t)c * a.kv_heads) * HD + head + 8 * g;
 #pragma unroll
         for (int st = 0; st < kSteps; ++st) {
           const bool in = !PRED || tc + n16 < end;
@@ -313,10 +329,10 @@ __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kT
           kv[st] = u32x4{cw.x, cw.y, sw.x, sw.y};
         }
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int t = t0 + 4 * s + g;
-          const bool in = !PRED || tc + 4 * s + g < end;
-          const uint2 cw = in ? *(const uint2*)(a.vcodes + code_page + (int64_t)t * a.kv_heads * kHeadDim + head + 8 * n16)
+        for (int s = 0; s < kVLoads; ++s) {
+          const int t = t0 + kVPos * s + vpos;
+          const bool in = !PRED || tc + kVPos * s + vpos < end;
+          const uint2 cw = in ? *(const uint2*)(a.vcodes + code_page + (int64_t)t * a.kv_heads * HD + head + 8 * vdim)
                               : uint2{0, 0};
           const uint32_t sv = in ? a.vscales[((int64_t)c * a.page_size + t) * a.kv_heads + kvh] : 127u;
           vv[s] = u32x4{cw.x, cw.y, sv, 0};
@@ -332,8 +348,8 @@ __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kT
     for (int st = 0; st < kSteps; ++st)
       kv[st] = (!PRED || tc + n16 < end) ? ld_page(kp + 64 * st) : u32x4{0, 0, 0, 0};
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      vv[s] = (!PRED || tc + 4 * s + g < end) ? ld_page(vp + 4 * s * a.row_bytes) : u32x4{0, 0, 0, 0};
+    for (int s = 0; s < kVLoads; ++s)
+      vv[s] = (!PRED || tc + kVPos * s + vpos < end) ? ld_page(vp + kVPos * s * a.row_bytes) : u32x4{0, 0, 0, 0};
   } else {
     const int tk = min(tc + n16, end - 1);
     const uint32_t bk = a.page_div.div((uint32_t)tk);
@@ -344,13 +360,13 @@ __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kT
     for (int st = 0; st < kSteps; ++st)
       kv[st] = tc + n16 < end ? ld_page(kp + 64 * st) : u32x4{0, 0, 0, 0};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int tv = min(tc + 4 * s + g, end - 1);
+    for (int s = 0; s < kVLoads; ++s) {
+      const int tv = min(tc + kVPos * s + vpos, end - 1);
       const uint32_t bv = a.page_div.div((uint32_t)tv);
       const int pv = table_lane(pt, (int)bv - blk0);
       const char* vp = vbase + (int64_t)pv * a.page_bytes +
-                       (int64_t)(tv - (int)(bv * (uint32_t)a.page_size)) * a.row_bytes + 16 * n16;
-      vv[s] = tc + 4 * s + g < end ? ld_page(vp) : u32x4{0, 0, 0, 0};
+                       (int64_t)(tv - (int)(bv * (uint32_t)a.page_size)) * a.row_bytes + 16 * vdim;
+      vv[s] = tc + kVPos * s + vpos < end ? ld_page(vp) : u32x4{0, 0, 0, 0};
     }
   }
 }
@@ -379,47 +395,34 @@ __device__ __forceinline__ u32x4 dequant_vector(const u32x4 x, bool value) {
   return u32x4{o[0], o[1], o[2], o[3]};
 }
 
-template <int E>
-__device__ __forceinline__ void dequant_chunk(u32x4 (&kv)[kSteps], u32x4 (&vv)[4]) {
-  static_assert(kSteps == 4, "vectors 0-3 are K steps, 4-7 V position slots");
-  bool fast = true;
-#pragma unroll
-  for (int st = 0; st < kSteps; ++st) fast = fast && barq_fp8::dequant8_fast_ok<E>(kv[st][0], kv[st][1], kv[st][2], kv[st][3]);
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const uint32_t sv = vv[s][2] * 0x01010101u;
-    fast = fast && barq_fp8::dequant8_fast_ok<E>(vv[s][0], vv[s][1], sv, sv);
-  }
-  if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
-#pragma unroll
-    for (int st = 0; st < kSteps; ++st) {
-      uint32_t o[4];
-      barq_fp8::dequant8_fast<E>(kv[st][0], kv[st][1], kv[st][2], kv[st][3], o);
-      kv[st] = u32x4{o[0], o[1], o[2], o[3]};
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const uint32_t sv = vv[s][2] * 0x01010101u;
-      uint32_t o[4];
-      barq_fp8::dequant8_fast<E>(vv[s][0], vv[s][1], sv, sv, o);
-      vv[s] = u32x4{o[0], o[1], o[2], o[3]};
-    }
-    return;
-  }
-#pragma unroll 1
-  for (int i = 0; i < 8; ++i) {
-    u32x4 x;
+// Vector i of a chunk's registers -- K step i (i < NK), else V load i - NK -- for a wave-uniform
+// runtime i, through constant-index switches (a dynamic index would move the chunk to scratch).
+template <int NK, int NV>
+__device__ __forceinline__ u32x4 chunk_vector(const u32x4 (&kv)[NK], const u32x4 (&vv)[NV], int i) {
+  static_assert((NK == 4 && NV == 4) || (NK == 2 && NV == 2), "chunk layouts of head sizes 128 and 64");
+  if constexpr (NK == 4) {
     switch (i) {
-      case 0: x = kv[0]; break;
-      case 1: x = kv[1]; break;
-      case 2: x = kv[2]; break;
-      case 3: x = kv[3]; break;
-      case 4: x = vv[0]; break;
-      case 5: x = vv[1]; break;
-      case 6: x = vv[2]; break;
-      default: x = vv[3]; break;
+      case 0: return kv[0];
+      case 1: return kv[1];
+      case 2: return kv[2];
+      case 3: return kv[3];
+      case 4: return vv[0];
+      case 5: return vv[1];
+      case 6: return vv[2];
+      default: return vv[3];
     }
-    const u32x4 y = dequant_vector<E>(x, i >= 4);
+  } else {
+    switch (i) {
+      case 0: return kv[0];
+      case 1: return kv[1];
+      case 2: return vv[0];
+      default: return vv[1];
+    }
+  }
+}
+template <int NK, int NV>
+__device__ __forceinline__ void set_chunk_vector(u32x4 (&kv)[NK], u32x4 (&vv)[NV], int i, const u32x4 y) {
+  if constexpr (NK == 4) {
     switch (i) {
       case 0: kv[0] = y; break;
       case 1: kv[1] = y; break;
@@ -430,6 +433,47 @@ __device__ __forceinline__ void dequant_chunk(u32x4 (&kv)[kSteps], u32x4 (&vv)[4
       case 6: vv[2] = y; break;
       default: vv[3] = y; break;
     }
+  } else {
+    switch (i) {
+      case 0: kv[0] = y; break;
+      case 1: kv[1] = y; break;
+      case 2: vv[0] = y; break;
+      default: vv[1] = y; break;
+    }
+  }
+}
+
+template <int E, int NK, int NV>
+__device__ __forceinline__ void dequant_chunk(u32x4 (&kv)[NK], u32x4 (&vv)[NV]) {
+  bool fast = true;
+#pragma unroll
+  for (int st = 0; st < NK; ++st) fast = fast && barq_fp8::dequant8_fast_ok<E>(kv[st][0], kv[st][1], kv[st][2], kv[st][3]);
+#pragma unroll
+  for (int s = 0; s < NV; ++s) {
+    const uint32_t sv = vv[s][2] * 0x01010101u;
+    fast = fast && barq_fp8::dequant8_fast_ok<E>(vv[s][0], vv[s][1], sv, sv);
+  }
+  if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
+#pragma unroll
+    for (int st = 0; st < NK; ++st) {
+      uint32_t o[4];
+      barq_fp8::dequant8_fast<E>(kv[st][0], kv[st][1], kv[st][2], kv[st][3], o);
+      kv[st] = u32x4{o[0], o[1], o[2], o[3]};
+    }
+#pragma unroll
+    for (int s = 0; s < NV; ++s) {
+      const uint32_t sv = vv[s][2] * 0x01010101u;
+      uint32_t o[4];
+      barq_fp8::dequant8_fast<E>(vv[s][0], vv[s][1], sv, sv, o);
+      vv[s] = u32x4{o[0], o[1], o[2], o[3]};
+    }
+    return;
+  }
+  // Vector i: K step i (i < NK) or V load i - NK, picked and put back by constant indices.
+#pragma unroll 1
+  for (int i = 0; i < NK + NV; ++i) {
+    const u32x4 y = dequant_vector<E>(chunk_vector(kv, vv, i), i >= NK);
+    set_chunk_vector(kv, vv, i, y);
   }
 }
 
@@ -440,12 +484,13 @@ __device__ __forceinline__ void dequant_chunk(u32x4 (&kv)[kSteps], u32x4 (&vv)[4
 // operand holds exactly the dequantised value.  V needs no scale here: its per-position scale
 // multiplies the probability (exact: a power of two).  A NaN code reads as NaN either way, and
 // the hardware's +0 for code 0x80 (-0) changes no product or sum.
-__device__ __forceinline__ bool chunk_scales_moderate(const u32x4 (&kv)[kSteps], const u32x4 (&vv)[4]) {
+template <int NK, int NV>
+__device__ __forceinline__ bool chunk_scales_moderate(const u32x4 (&kv)[NK], const u32x4 (&vv)[NV]) {
   uint32_t ok = 0x40404040u;
 #pragma unroll
-  for (int st = 0; st < kSteps; ++st) ok &= ((kv[st][2] >> 1) ^ kv[st][2]) & ((kv[st][3] >> 1) ^ kv[st][3]);
+  for (int st = 0; st < NK; ++st) ok &= ((kv[st][2] >> 1) ^ kv[st][2]) & ((kv[st][3] >> 1) ^ kv[st][3]);
 #pragma unroll
-  for (int s = 0; s < 4; ++s) ok &= ((vv[s][2] >> 1) ^ vv[s][2]) | 0x40404000u;
+  for (int s = 0; s < NV; ++s) ok &= ((vv[s][2] >> 1) ^ vv[s][2]) | 0x40404000u;
   return (ok & 0x40404040u) == 0x40404040u;  // every byte's top two bits are 01 or 10: 64..191
 }
 
@@ -486,12 +531,19 @@ __device__ __forceinline__ void v_operand(const u32x4 x, float (&f)[8]) {
   }
 }
 
-template <int E, int R, bool UNIFORM, typename OutT, bool COLD>
-__device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u32x4 (&lq)[kSteps][kWave],
-                             int b, int kvh, int len, int t_begin, int t_end, bool whole, int64_t rec_id) {
+template <int HD, int E, int R, bool UNIFORM, typename OutT, bool COLD>
+__device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
+                             u32x4 (&lq)[Head<HD>::kSteps][kWave], int b, int kvh, int len, int t_begin,
+                             int t_end, bool whole, int64_t rec_id) {
+  constexpr int kSteps = Head<HD>::kSteps;
+  constexpr int kVLanes = Head<HD>::kVLanes;
+  constexpr int kVPos = Head<HD>::kVPos;
+  constexpr int kVLoads = Head<HD>::kVLoads;
   const int lane = threadIdx.x;
   const int n16 = lane & 15;
   const int g = lane >> 4;
+  const int vpos = lane / kVLanes;  // V: position slot and 8-dim group of this lane
+  const int vdim = lane % kVLanes;
   const int M = a.rows;
   const int T = a.tokens;
 
@@ -517,7 +569,7 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
   const char* kbase = a.kpages + (int64_t)kvh * a.head_bytes;
   const char* vbase = a.vpages + (int64_t)kvh * a.head_bytes;
   const int klane = n16 * a.row_bytes + 16 * g;
-  const int vlane = g * a.row_bytes + 16 * n16;
+  const int vlane = vpos * a.row_bytes + 16 * vdim;
 
   float m_run[4], l_part[4];
 #pragma unroll
@@ -531,7 +583,7 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[r2][e] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto load = [&](int tc, u32x4 (&kv)[kSteps], u32x4 (&vv)[4], bool& cold) {
+  auto load = [&](int tc, u32x4 (&kv)[kSteps], u32x4 (&vv)[kVLoads], bool& cold) {
     // Slide the table window when the chunk's last block leaves it (every 254+ blocks).
     const int last = (int)a.page_div.div((uint32_t)min(tc + kBlock, t_end) - 1u);
     if (last - blk0 >= kTableEntries) {
@@ -539,13 +591,15 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
       load_table<COLD>(a, b, blk0, blk_end, lane, pt);
     }
     if (tc + kBlock <= t_end)
-      load_chunk<UNIFORM, false, COLD>(a, pt, blk0, kbase, vbase, tc, t_end, klane, vlane, n16, g, kvh, kv, vv, cold);
+      load_chunk<HD, UNIFORM, false, COLD>(a, pt, blk0, kbase, vbase, tc, t_end, klane, vlane, n16, g, vpos, vdim,
+                                           kvh, kv, vv, cold);
     else
-      load_chunk<UNIFORM, true, COLD>(a, pt, blk0, kbase, vbase, tc, t_end, klane, vlane, n16, g, kvh, kv, vv, cold);
+      load_chunk<HD, UNIFORM, true, COLD>(a, pt, blk0, kbase, vbase, tc, t_end, klane, vlane, n16, g, vpos, vdim,
+                                          kvh, kv, vv, cold);
   };
 
   // codes: the chunk registers hold a quantised chunk with moderate scales (see k_operand).
-  auto compute = [&](int tc, const u32x4 (&kv)[kSteps], const u32x4 (&vv)[4], bool codes) {
+  auto compute = [&](int tc, const u32x4 (&kv)[kSteps], const u32x4 (&vv)[kVLoads], bool codes) {
     // Scores: lane (g, n16), register r = row 4g + r, position tc + n16; log2 units.
     f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -584,9 +638,10 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[r2][e][m] *= al;
       }
-    // P.V: lane 4b' + n of the 4x4x1 MFMA block b' takes position 4s + g of the chunk.
+    // P.V: lane 4b' + n of the 4x4x1 MFMA block b' takes position kVPos * s + vpos of the chunk
+    // (the four lanes of a block share it) and dims 8 * vdim + e.
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < kVLoads; ++s) {
       float vf[8];
       float vs = 1.0f;  // a quantised position's scale, moved onto its probability
       if (COLD && codes) {
@@ -597,7 +652,7 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
       }
 #pragma unroll
       for (int r2 = 0; r2 < R; ++r2) {
-        const float pa = lp[4 * s + g][4 * r2 + (lane & 3)] * vs;
+        const float pa = lp[kVPos * s + vpos][4 * r2 + (lane & 3)] * vs;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           acc[r2][e] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vf[e], acc[r2][e], 0, 0, 0);
@@ -609,7 +664,7 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
   // computed.  Two buffers: a third spills (or, for 4 query rows, runs slower) with the
   // accumulators in registers.
   constexpr int D = 2;
-  u32x4 kr[D][kSteps], vr[D][4];
+  u32x4 kr[D][kSteps], vr[D][kVLoads];
   bool cr[D];  // the buffer holds codes and scales (wave-uniform)
   int tc = t_begin;
 #pragma unroll
@@ -628,7 +683,7 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
         bool codes = false;
         if (COLD && cr[i]) {
           codes = __builtin_amdgcn_ballot_w64(!chunk_scales_moderate(kr[i], vr[i])) == 0;
-          if (!codes) dequant_chunk<E>(kr[i], vr[i]);
+          if (!codes) dequant_chunk<E, kSteps, kVLoads>(kr[i], vr[i]);
         }
         compute(tc, kr[i], vr[i], codes);
         tc += kBlock;
@@ -638,7 +693,7 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows], u
   }
 chunks_done:
 
-  // Row sums across the 16 lanes of each row group; P.V partials across the 4 position slots.
+  // Row sums across the 16 lanes of each row group; P.V partials across the position slots.
 #pragma unroll
   for (int r = 0; r < 4; ++r) l_part[r] = row16_sum(l_part[r]);
 #pragma unroll
@@ -648,13 +703,13 @@ chunks_done:
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         float v = acc[r2][e][m];
-        v += __shfl_xor(v, 16, kWave);
-        v += __shfl_xor(v, 32, kWave);
+#pragma unroll
+        for (int o = kVLanes; o < kWave; o <<= 1) v += __shfl_xor(v, o, kWave);
         acc[r2][e][m] = v;
       }
-  // Lanes 0..15 now hold dims 8 * lane .. +7 of every row; lanes 16g .. 16g+15 hold the
-  // maxima and sums of rows 4g .. 4g+3.
-  const int64_t rec = record_floats(M);
+  // Lanes 0 .. HD / 8 - 1 now hold dims 8 * lane .. +7 of every row; lanes 16g .. 16g+15 hold
+  // the maxima and sums of rows 4g .. 4g+3.
+  const int64_t rec = record_floats(M, HD);
   float* pr = a.part + rec_id * rec;
 #pragma unroll
   for (int r2 = 0; r2 < R; ++r2)
@@ -665,7 +720,7 @@ chunks_done:
       const float mr = lane_value(m_run[m], 16 * r2);
       const float lr = lane_value(l_part[m], 16 * r2);
       if (whole) {
-        if (lane < 16) {
+        if (lane < kVLanes) {
           const float inv = lr > 0.f ? 1.f / lr : 0.f;
           char* o = out_row(a, b, kvh, row) + (int64_t)(8 * lane) * sizeof(OutT);
           store_out4<OutT, E>(o, f32x4{acc[r2][0][m], acc[r2][1][m], acc[r2][2][m], acc[r2][3][m]} * inv);
@@ -673,13 +728,13 @@ chunks_done:
                               f32x4{acc[r2][4][m], acc[r2][5][m], acc[r2][6][m], acc[r2][7][m]} * inv);
         }
       } else {
-        if (lane < 16) {
-          float* dst = pr + (int64_t)row * kHeadDim + 8 * lane;
+        if (lane < kVLanes) {
+          float* dst = pr + (int64_t)row * HD + 8 * lane;
           *(f32x4*)dst = f32x4{acc[r2][0][m], acc[r2][1][m], acc[r2][2][m], acc[r2][3][m]};
           *(f32x4*)(dst + 4) = f32x4{acc[r2][4][m], acc[r2][5][m], acc[r2][6][m], acc[r2][7][m]};
-        } else if (lane == 16) {
-          pr[(int64_t)M * kHeadDim + row] = mr;
-          pr[(int64_t)M * kHeadDim + M + row] = lr;
+        } else if (lane == kVLanes) {
+          pr[(int64_t)M * HD + row] = mr;
+          pr[(int64_t)M * HD + M + row] = lr;
         }
       }
     }
@@ -687,12 +742,12 @@ chunks_done:
 
 // One wave per workgroup, one workgroup per resident slot: ranges r = blockIdx.x, + gridDim.x,
 // ... of the flat chunk list.  UNIFORM: page_size is a multiple of 16.  R: groups of 4 query
-// rows (rows <= 4 * R).
-template <int E, int R, bool UNIFORM, typename OutT, bool COLD>
+// rows (rows <= 4 * R).  HD: the head size.
+template <int HD, int E, int R, bool UNIFORM, typename OutT, bool COLD>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(R <= 2 ? 2 : 1, R <= 2 ? 2 : 1)))
 void attention_flat_kernel(const AttnArgs a) {
-  __shared__ float lp[kBlock][kMaxRows];   // probabilities, staged for the P.V operand layout
-  __shared__ u32x4 lq[kSteps][kWave];      // the piece's query fragments
+  __shared__ float lp[kBlock][kMaxRows];             // probabilities, staged for the P.V operand layout
+  __shared__ u32x4 lq[Head<HD>::kSteps][kWave];      // the piece's query fragments
   __shared__ int s_len[kMaxBatch];
   __shared__ int s_incl[kMaxBatch];
 
@@ -712,21 +767,21 @@ void attention_flat_kernel(const AttnArgs a) {
       const int k0 = c - pair_first;
       const int piece_end = min(c_end, pair_first + nch);
       const bool whole = k0 == 0 && piece_end == pair_first + nch;
-      attend_piece<E, R, UNIFORM, OutT, COLD>(a, lp, lq, b, kvh, len, kBlock * k0,
-                                        min(len, kBlock * (k0 + piece_end - c)), whole,
-                                        (int64_t)r + (int64_t)b * a.kv_heads + kvh);
+      attend_piece<HD, E, R, UNIFORM, OutT, COLD>(a, lp, lq, b, kvh, len, kBlock * k0,
+                                                  min(len, kBlock * (k0 + piece_end - c)), whole,
+                                                  (int64_t)r + (int64_t)b * a.kv_heads + kvh);
       c = piece_end;
     }
   }
 }
 
 // Merge of one query row's records: one workgroup of NT threads per (row, kv head, batch row).
-// Thread (quad, class) folds the records class, class + NT / 32, ... into a running (max, sum,
-// 4 dims) -- every record load is independent -- and the classes are folded through LDS.  Rows
-// of length 0 get zeros here; pairs inside one range were written by their wave.
-template <int E, typename OutT, int NT>
+// Thread (quad, class) folds the records class, class + NT / (HD / 4), ... into a running (max,
+// sum, 4 dims) -- every record load is independent -- and the classes are folded through LDS.
+// Rows of length 0 get zeros here; pairs inside one range were written by their wave.
+template <int HD, int E, typename OutT, int NT>
 __global__ __launch_bounds__(NT) void attention_merge_kernel(const AttnArgs a) {
-  constexpr int kQuads = kHeadDim / 4;
+  constexpr int kQuads = HD / 4;
   constexpr int kClasses = NT / kQuads;
   __shared__ int s_len[kMaxBatch];
   __shared__ int s_incl[kMaxBatch];
@@ -757,7 +812,7 @@ __global__ __launch_bounds__(NT) void attention_merge_kernel(const AttnArgs a) {
   if (r_first == r_last) return;
 
   const int M = a.rows;
-  const int64_t rec = record_floats(M);
+  const int64_t rec = record_floats(M, HD);
   const int64_t p = (int64_t)b * a.kv_heads + kvh;
   const int quad = tid % kQuads;
   const int cls = tid / kQuads;
@@ -766,9 +821,9 @@ __global__ __launch_bounds__(NT) void attention_merge_kernel(const AttnArgs a) {
 #pragma unroll 4
   for (int r = r_first + cls; r <= r_last; r += kClasses) {
     const float* rp = a.part + (r + p) * rec;
-    const float ms = rp[(int64_t)M * kHeadDim + row];
-    const float ls = rp[(int64_t)M * kHeadDim + M + row];
-    const f32x4 os = *(const f32x4*)(rp + (int64_t)row * kHeadDim + 4 * quad);
+    const float ms = rp[(int64_t)M * HD + row];
+    const float ls = rp[(int64_t)M * HD + M + row];
+    const f32x4 os = *(const f32x4*)(rp + (int64_t)row * HD + 4 * quad);
     const float mn = fmaxf(mt, ms);
     const float mu = mn == -INFINITY ? 0.f : mn;
     const float wo = __builtin_amdgcn_exp2f(mt - mu);
@@ -819,45 +874,50 @@ int resident_waves(K kernel) {
   return waves;
 }
 
-template <int E, int R, bool U, typename OutT, bool COLD>
+template <int HD, int E, int R, bool U, typename OutT, bool COLD>
 hipError_t launch_typed(AttnArgs a, bool merge, hipStream_t stream) {
-  auto* k = attention_flat_kernel<E, R, U, OutT, COLD>;
+  auto* k = attention_flat_kernel<HD, E, R, U, OutT, COLD>;
   a.waves = resident_waves(k);
   hipLaunchKernelGGL(k, dim3((unsigned)a.waves), dim3(kWave), 0, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || !merge) return err;
   // Fewer merge workgroups than CUs (few long pairs, many records each): 1024 threads each.
   if ((int64_t)a.rows * a.kv_heads * a.batch < kMergeWideBelow)
-    hipLaunchKernelGGL((attention_merge_kernel<E, OutT, kMergeWide>),
+    hipLaunchKernelGGL((attention_merge_kernel<HD, E, OutT, kMergeWide>),
                        dim3((unsigned)a.rows, (unsigned)a.kv_heads, (unsigned)a.batch), dim3(kMergeWide), 0, stream, a);
   else
-    hipLaunchKernelGGL((attention_merge_kernel<E, OutT, kThreads>), dim3((unsigned)a.rows, (unsigned)a.kv_heads, (unsigned)a.batch),
-                       dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((attention_merge_kernel<HD, E, OutT, kThreads>),
+                       dim3((unsigned)a.rows, (unsigned)a.kv_heads, (unsigned)a.batch), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 
-template <int E, int R, bool U, bool COLD = false>
+template <int HD, int E, int R, bool U, bool COLD>
 hipError_t launch_out(const AttnArgs& a, bool out_f32, bool merge, hipStream_t stream) {
-  return out_f32 ? launch_typed<E, R, U, float, COLD>(a, merge, stream)
-                 : launch_typed<E, R, U, uint16_t, COLD>(a, merge, stream);
+  return out_f32 ? launch_typed<HD, E, R, U, float, COLD>(a, merge, stream)
+                 : launch_typed<HD, E, R, U, uint16_t, COLD>(a, merge, stream);
+}
+
+template <int HD, int E, bool U, bool COLD>
+hipError_t launch_rows(const AttnArgs& a, bool out_f32, bool merge, hipStream_t stream) {
+  const int groups = (a.rows + 3) / 4;
+  return groups == 1   ? launch_out<HD, E, 1, U, COLD>(a, out_f32, merge, stream)
+         : groups == 2 ? launch_out<HD, E, 2, U, COLD>(a, out_f32, merge, stream)
+                       : launch_out<HD, E, 4, U, COLD>(a, out_f32, merge, stream);
+}
+
+template <int HD, int E>
+hipError_t launch_pages(const AttnArgs& a, bool uniform, bool cold, bool out_f32, bool merge, hipStream_t stream) {
+  if (cold)  // quantised pools: page_size a multiple of 16 (checked by the caller)
+    return launch_rows<HD, E, true, true>(a, out_f32, merge, stream);
+  return uniform ? launch_rows<HD, E, true, false>(a, out_f32, merge, stream)
+                 : launch_rows<HD, E, false, false>(a, out_f32, merge, stream);
 }
 
 template <int E>
-hipError_t launch_dtype(const AttnArgs& a, bool uniform, bool cold, bool out_f32, bool merge, hipStream_t stream) {
-  const int groups = (a.rows + 3) / 4;
-  if (cold) {  // quantised pools: page_size a multiple of 16 (checked by the caller)
-    return groups == 1   ? launch_out<E, 1, true, true>(a, out_f32, merge, stream)
-           : groups == 2 ? launch_out<E, 2, true, true>(a, out_f32, merge, stream)
-                         : launch_out<E, 4, true, true>(a, out_f32, merge, stream);
-  }
-  if (uniform) {
-    return groups == 1   ? launch_out<E, 1, true>(a, out_f32, merge, stream)
-           : groups == 2 ? launch_out<E, 2, true>(a, out_f32, merge, stream)
-                         : launch_out<E, 4, true>(a, out_f32, merge, stream);
-  }
-  return groups == 1   ? launch_out<E, 1, false>(a, out_f32, merge, stream)
-         : groups == 2 ? launch_out<E, 2, false>(a, out_f32, merge, stream)
-                       : launch_out<E, 4, false>(a, out_f32, merge, stream);
+hipError_t launch_dtype(const AttnArgs& a, int head_dim, bool uniform, bool cold, bool out_f32, bool merge,
+                        hipStream_t stream) {
+  return head_dim == 64 ? launch_pages<64, E>(a, uniform, cold, out_f32, merge, stream)
+                        : launch_pages<128, E>(a, uniform, cold, out_f32, merge, stream);
 }
 
 struct AttnPlan {
@@ -873,7 +933,7 @@ struct AttnPlan {
 // schedule's own, total / resident waves).
 int plan_attention(const barq_kv_pool* pool, int64_t batch, int64_t q_heads, int64_t tokens,
                    int64_t max_seq, int64_t split_tokens, AttnPlan* plan) {
-  if (!pool || pool->elem_bytes != 2 || pool->head_dim != kHeadDim || pool->kv_heads <= 0 ||
+  if (!pool || pool->elem_bytes != 2 || (pool->head_dim != 64 && pool->head_dim != 128) || pool->kv_heads <= 0 ||
       pool->page_size <= 0 || pool->max_blocks <= 0 || pool->num_pages <= 0 ||
       pool->num_pages > INT32_MAX || pool->max_batch <= 0)
     return BARQ_KV_ERR_INVALID;
@@ -883,7 +943,7 @@ int plan_attention(const barq_kv_pool* pool, int64_t batch, int64_t q_heads, int
   const int64_t rows = (q_heads / pool->kv_heads) * tokens;
   if (rows > kMaxRows) return BARQ_KV_ERR_INVALID;
   const int64_t capacity = pool->max_blocks * pool->page_size;
-  const int64_t row_bytes = pool->kv_heads * kHeadDim * 2;
+  const int64_t row_bytes = pool->kv_heads * pool->head_dim * 2;
   if (max_seq <= 0 || max_seq > capacity) max_seq = capacity;
   // Lane offsets within a page are 32-bit; chunk indices of the whole schedule fit 31 bits.
   const int64_t pairs = batch * pool->kv_heads;
@@ -899,7 +959,7 @@ int plan_attention(const barq_kv_pool* pool, int64_t batch, int64_t q_heads, int
   plan->max_seq = max_seq;
   plan->range_chunks = chunks;
   plan->records = ranges + pairs;
-  plan->bytes = plan->records * record_floats(rows) * 4;
+  plan->bytes = plan->records * record_floats(rows, pool->head_dim) * 4;
   return BARQ_KV_OK;
 }
 
@@ -994,8 +1054,8 @@ int decode_attention(const barq_kv_pool* pool, const barq_kv_cold* cold, const v
   const bool out_f32 = (flags & BARQ_KV_ATTN_OUT_F32) != 0;
   const hipError_t err =
       (flags & BARQ_KV_ATTN_FP16)
-          ? launch_dtype<kF16>(a, uniform, cold != nullptr, out_f32, true, (hipStream_t)stream)
-          : launch_dtype<kBF16>(a, uniform, cold != nullptr, out_f32, true, (hipStream_t)stream);
+          ? launch_dtype<kF16>(a, (int)pool->head_dim, uniform, cold != nullptr, out_f32, true, (hipStream_t)stream)
+          : launch_dtype<kBF16>(a, (int)pool->head_dim, uniform, cold != nullptr, out_f32, true, (hipStream_t)stream);
   return err == hipSuccess ? BARQ_KV_OK : BARQ_KV_ERR_LAUNCH;
 }
 

@@ -500,7 +500,7 @@ class PagePool:
                                                  max(int(max_seq), 1), int(split_tokens))
         if need < 0:
             raise ValueError(
-                "paged decode attention takes bf16/fp16 pools with head_dim 128 and at most 16 "
+                "paged decode attention takes bf16/fp16 pools with head_dim 64 or 128 and at most 16 "
                 f"query rows per kv head (got {self.dtype}, head_dim {self.head_dim}, "
                 f"{q_heads // self.kv_heads} x {tokens} rows)")
         self._attention_call(backend, query, out, scale, max(int(max_seq), 1), int(split_tokens),

@@ -248,13 +248,13 @@ int64_t barq_kv_attention_workspace_bytes(const barq_kv_pool* pool, int64_t batc
                                           int64_t split_tokens);
 
 /*
- * Decode attention over rows [0, batch) of a 2-byte (bf16 / fp16) pool with head_dim 128,
- * reading K and V from the pages:
+ * Decode attention over rows [0, batch) of a 2-byte (bf16 / fp16) pool with head_dim 64 or
+ * 128 (D below), reading K and V from the pages:
  *   out[b, h, i, :] = sum_t softmax_t(scale * q[b, h, i, :] . K[b, h / G, t, :]) V[b, h / G, t, :]
  * over positions t <= seq_lens[b] - tokens + i (the query tokens are the row's last `tokens`
  * positions, already appended), G = q_heads / kv_heads.  A row with no visible position gets
- * zeros.  query: [batch, q_heads, tokens, 128] of the pool's type, element strides (q_stride_b,
- * q_stride_h, q_stride_t), 16-byte aligned rows; out: [batch, q_heads, tokens, 128] of the
+ * zeros.  query: [batch, q_heads, tokens, D] of the pool's type, element strides (q_stride_b,
+ * q_stride_h, q_stride_t), 16-byte aligned rows; out: [batch, q_heads, tokens, D] of the
  * pool's type or float32 (BARQ_KV_ATTN_OUT_F32), element strides (out_stride_*), each a
  * multiple of 8.  G * tokens <= 16, batch <= 1024.  max_seq bounds every row's length (0 = the pool's
  * capacity; longer rows attend their first max_seq positions and are flagged).  The work is

@@ -41,7 +41,7 @@ def fill_pool(pool, kd, vd, lens, dtype):
         cur = nxt
 
 
-def make_rows(B, Hkv, page, lens, dtype, seed, order_seed=None, cap=None):
+def make_rows(B, Hkv, page, lens, dtype, seed, order_seed=None, cap=None, D=128):
     lens = sorted((int(x) for x in lens), reverse=True)
     cap = cap or max(max(lens), 1)
     gen = torch.Generator().manual_seed(seed)
@@ -50,10 +50,10 @@ def make_rows(B, Hkv, page, lens, dtype, seed, order_seed=None, cap=None):
     n_pages = B * max_blocks
     if order_seed is not None:
         order = torch.from_numpy(np.random.default_rng(order_seed).permutation(n_pages).astype(np.int32))
-    pool = CPool(max_batch=B, max_blocks=max_blocks, page_size=page, heads=Hkv, dim=128, dtype=dtype,
+    pool = CPool(max_batch=B, max_blocks=max_blocks, page_size=page, heads=Hkv, dim=D, dtype=dtype,
                  num_pages=n_pages, order=order)
-    kd = torch.randn(B, Hkv, cap, 128, generator=gen).to(dtype).double().numpy()
-    vd = torch.randn(B, Hkv, cap, 128, generator=gen).to(dtype).double().numpy()
+    kd = torch.randn(B, Hkv, cap, D, generator=gen).to(dtype).double().numpy()
+    vd = torch.randn(B, Hkv, cap, D, generator=gen).to(dtype).double().numpy()
     fill_pool(pool, kd, vd, lens, dtype)
     torch.cuda.synchronize()
     assert pool.errors() == 0
@@ -62,10 +62,10 @@ def make_rows(B, Hkv, page, lens, dtype, seed, order_seed=None, cap=None):
 
 def check(pool, kd, vd, lens, G, T, dtype, seed, out_f32=True, split_tokens=0, max_seq=0, ws=None,
           scale=None):
-    B, Hkv = kd.shape[0], kd.shape[1]
+    B, Hkv, D = kd.shape[0], kd.shape[1], kd.shape[3]
     gen = torch.Generator().manual_seed(seed)
-    q = hf_layout(B, G * Hkv, T, 128, dtype, gen).cuda()
-    scale = 128 ** -0.5 if scale is None else scale
+    q = hf_layout(B, G * Hkv, T, D, dtype, gen).cuda()
+    scale = D ** -0.5 if scale is None else scale
     out, ws = pool.attend(q, scale=scale, out_f32=out_f32, split_tokens=split_tokens, max_seq=max_seq,
                           workspace=ws)
     torch.cuda.synchronize()
@@ -99,6 +99,25 @@ def test_multi_token_queries_causal(G, T):
     pool, kd, vd, lens = make_rows(len(lens), 2, 16, lens, torch.bfloat16, seed=G * T, order_seed=3)
     check(pool, kd, vd, lens, G, T, torch.bfloat16, seed=1, split_tokens=256)
     check(pool, kd, vd, lens, G, T, torch.bfloat16, seed=2)
+
+
+@pytest.mark.parametrize("dtype,page", [(torch.bfloat16, 16), (torch.float16, 32), (torch.bfloat16, 5),
+                                        (torch.float16, 1)])
+def test_head_dim_64(dtype, page):
+    """Head size 64 (Qwen2-0.5B: 14 query heads over 2 kv heads, G = 7): ragged rows with a random
+    page order, G = 7 / 1 / 4 / 16, multi-token queries, fixed and automatic splits, both output
+    types, and one long row whose pairs the merge launch folds from hundreds of records."""
+    lens = [1100, 769, 513, 257, 256, 255, 64, 17, 16, 1, 0]
+    pool, kd, vd, lens = make_rows(len(lens), 2, page, lens, dtype, seed=page + 64, order_seed=page + 65, D=64)
+    ws = None
+    for i, (G, T, split) in enumerate([(7, 1, 0), (1, 1, 256), (4, 1, 48), (16, 1, 0), (7, 2, 512), (2, 8, 0)]):
+        ws = check(pool, kd, vd, lens, G, T, dtype, seed=300 + i, split_tokens=split, ws=ws)
+    check(pool, kd, vd, lens, 7, 1, dtype, seed=9, out_f32=False)
+    assert pool.errors() == 0
+    pool, kd, vd, lens = make_rows(1, 2, page, [9001], dtype, seed=page + 66, order_seed=page + 67, D=64)
+    check(pool, kd, vd, lens, 7, 1, dtype, seed=10)
+    check(pool, kd, vd, lens, 7, 1, dtype, seed=11, out_f32=False)
+    assert pool.errors() == 0
 
 
 def test_llama3_8b_decode_shape():

@@ -181,15 +181,29 @@ def bf16_llama(seed=0):
     return LlamaForCausalLM(cfg).to(torch.bfloat16).eval(), cfg
 
 
-def test_paged_attention_decode_in_a_model(hip, monkeypatch):
+def qwen2_small_head(seed=0):
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    torch.manual_seed(seed)
+    # Qwen2-0.5B's attention geometry (the reference's benchmark model): 14 query heads over 2 kv
+    # heads (G = 7), head_dim 64, q/k/v biases; fewer layers and a small vocabulary
+    cfg = Qwen2Config(vocab_size=512, hidden_size=896, intermediate_size=1024, num_hidden_layers=2,
+                      num_attention_heads=14, num_key_value_heads=2, max_position_embeddings=1024,
+                      pad_token_id=0, eos_token_id=None)
+    return Qwen2ForCausalLM(cfg).to(torch.bfloat16).eval(), cfg
+
+
+@pytest.mark.parametrize("factory", [bf16_llama, qwen2_small_head], ids=["llama_d128_g4", "qwen2_d64_g7"])
+def test_paged_attention_decode_in_a_model(hip, monkeypatch, factory):
     """A bf16 model whose decode steps read K/V from the pages (the kernel) against the same
     model on the gather + fp32 attention path, token by token on one sequence: logits agree to
-    bf16 rounding.  Then generate() through patch_inference(paged_attention=True)."""
+    bf16 rounding.  Then generate() through patch_inference(paged_attention=True).  Head sizes 128
+    (Llama-3 ratio) and 64 (Qwen2-0.5B geometry)."""
     pytest.importorskip("transformers")
     from barqtrain import create_paged_kv_cache, patch_inference
     from barqtrain_amd import attention
 
-    model, cfg = bf16_llama()
+    model, cfg = factory()
     model = model.to("cuda")
     attention.enable_paged_attention(model)
     gen = torch.Generator().manual_seed(5)
@@ -277,8 +291,7 @@ def small_head_llama(seed=0):
     from transformers import LlamaConfig, LlamaForCausalLM
 
     torch.manual_seed(seed)
-    # head_dim 64 with 4 query heads over 2 kv heads: the reference's benchmark model
-    # (Qwen2-0.5B) has head_dim 64, which the decode kernel does not take
+    # head_dim 64 with 4 query heads over 2 kv heads
     cfg = LlamaConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
                       num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=1024,
                       pad_token_id=0, eos_token_id=None)
@@ -286,8 +299,8 @@ def small_head_llama(seed=0):
 
 
 def test_paged_route_head_dim_64_and_padded_batch(hip, monkeypatch):
-    """The "barq_paged" route for shapes the decode kernel does not take -- head_dim 64, and a
-    left-padded batch (a mask) -- runs torch's fused SDPA over the gathered K/V.  Against the same
+    """The "barq_paged" route for calls the decode kernel does not take -- a left-padded batch (a
+    mask), here with head_dim 64 -- runs torch's fused SDPA over the gathered K/V.  Against the same
     route with the fp32 attention (a reference free of bf16 batched products): prefill logits
     agree to bf16 rounding and greedy tokens agree."""
     pytest.importorskip("transformers")

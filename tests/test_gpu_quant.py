@@ -275,17 +275,18 @@ ATT_F32 = dict(rtol=2e-5, atol=2e-5)
 ATT_OUT = {torch.bfloat16: dict(rtol=2.0 ** -8, atol=2e-5), torch.float16: dict(rtol=2.0 ** -11, atol=2e-5)}
 
 
-@pytest.mark.parametrize("dtype,page,window", [(torch.bfloat16, 16, 0), (torch.bfloat16, 16, 48),
-                                               (torch.float16, 32, 32), (torch.bfloat16, 32, 128)])
-def test_decode_attention_reads_quantised_pages(hip, dtype, page, window):
+@pytest.mark.parametrize("dtype,page,window,D", [(torch.bfloat16, 16, 0, 128), (torch.bfloat16, 16, 48, 128),
+                                                 (torch.float16, 32, 32, 128), (torch.bfloat16, 32, 128, 128),
+                                                 (torch.bfloat16, 16, 48, 64), (torch.float16, 32, 0, 64)])
+def test_decode_attention_reads_quantised_pages(hip, dtype, page, window, D):
     """Attention over a quantised pool (barq_kv_decode_attention_cold: cold blocks read as codes
     and scales, dequantised in registers) against the float64 reference over the dequantising
     gather's K/V -- the values the cold store holds -- on ragged rows mixing cold and hot blocks,
-    G = 1, 4, 8 and two query tokens; fp32 and cache-dtype outputs."""
+    G = 1, 4, 8 and two query tokens; fp32 and cache-dtype outputs; head sizes 128 and 64."""
     from attn_ref import decode_attention_reference, within_tolerance
     from barqtrain_amd.paged import QuantPagePool
 
-    H, D = 4, 128
+    H = 4
     lens = [700, 333, 129, 64, 17, 1]
     B, cap = len(lens), 768
     pool = QuantPagePool(max_batch=B, max_blocks=cap // page, page_size=page, kv_heads=H, head_dim=D, dtype=dtype,
@@ -312,13 +313,14 @@ def test_decode_attention_reads_quantised_pages(hip, dtype, page, window):
     assert pool.errors() == 0
 
 
-def test_decode_attention_cold_through_capi(capi):
+@pytest.mark.parametrize("D", [128, 64])
+def test_decode_attention_cold_through_capi(capi, D):
     """The C entry point on a CColdPool with a crafted cold page (zero, subnormal and NaN-free
     boundary codes take the exact per-element decode) next to hot pages."""
     from attn_ref import decode_attention_reference, within_tolerance
     from capi_pool import attend_cold
 
-    B, H, D, P, W = 2, 2, 128, 16, 16
+    B, H, P, W = 2, 2, 16, 16
     pool = CColdPool(window=W, max_batch=B, max_blocks=8, page_size=P, heads=H, dim=D, dtype=torch.bfloat16)
     gen = torch.Generator().manual_seed(21)
     k, v = hf_layout(B, H, 70, D, torch.bfloat16, gen), hf_layout(B, H, 70, D, torch.bfloat16, gen)
