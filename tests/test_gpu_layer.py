@@ -16,6 +16,7 @@ import pytest
 import torch
 
 from kvgen import hf_layout, to_bits
+from mirror import DeviceMirror
 from oracle.kv_oracle import DenseLayerOracle
 
 pytestmark = pytest.mark.gpu
@@ -125,6 +126,53 @@ def test_graph_replays_match_oracle(hip):
             assert_bits(gk, ok, f"eager gather after replay {s}")
     assert all(p.errors() == 0 for p in pools)
     assert [int(x) for x in pools[0].seq_lens.cpu()] == [cap] * B
+
+
+def test_config2_all_layers_captured_every_step(hip):
+    """The benchmark's C2 step as it runs there: 32 layers of 16 rows x 8 KV heads x 128, bf16,
+    page 16, prefill 512, then 256 replays of one captured decode step.  Every replay's K/V of
+    every layer against the device mirror; every layer against the oracle after the last replay
+    (and the mirror with it)."""
+    from barqtrain_amd.graph import CapturedDecodeStep
+    from barqtrain_amd.paged import PagePool
+
+    L, B, H, D, P, prefill, steps = 32, 16, 8, 128, 16, 512, 256
+    cap = prefill + steps
+    dev = torch.device("cuda", 0)
+    bf16 = torch.bfloat16
+    gen = torch.Generator(device=dev).manual_seed(2002)
+
+    def tokens(T):  # [B, H, T, D] view of [B, T, H, D], as HF hands K/V to the cache
+        return torch.randn((B, T, H, D), generator=gen, device=dev).to(bf16).transpose(1, 2)
+
+    pools = [PagePool(max_batch=B, max_blocks=cap // P, page_size=P, kv_heads=H, head_dim=D, dtype=bf16,
+                      device=dev) for _ in range(L)]
+    mirrors = [DeviceMirror(B, H, cap, D, bf16) for _ in range(L)]
+    oracles = [DenseLayerOracle(B, cap, P) for _ in range(L)]
+    for pool, mirror, oracle in zip(pools, mirrors, oracles):
+        k, v = tokens(prefill), tokens(prefill)
+        mirror.append(k, v)
+        mirror.check(pool.update(k, v), "prefill")
+        oracle.append(to_bits(k), to_bits(v))
+    kin = torch.zeros((L, B, H, 1, D), dtype=bf16, device=dev)
+    vin = torch.zeros_like(kin)
+    step = CapturedDecodeStep(pools, B, 1, inputs=(kin, vin))
+    step.prepare(range(prefill + 1, cap + 1))
+    outs = None
+    for s in range(steps):
+        kin.copy_(torch.randn(kin.shape, generator=gen, device=dev).to(bf16))
+        vin.copy_(torch.randn(vin.shape, generator=gen, device=dev).to(bf16))
+        outs = step.replay()
+        kh, vh = to_bits(kin), to_bits(vin)
+        for layer in range(L):
+            mirrors[layer].append(kin[layer], vin[layer])
+            mirrors[layer].check(outs[layer], f"replay {s} layer {layer}")
+            oracles[layer].append(kh[layer], vh[layer])
+    for layer in range(L):
+        ok, ov = oracles[layer].current_tensors()
+        assert_bits(outs[layer][0], ok, f"layer {layer} K after {steps} replays")
+        assert_bits(outs[layer][1], ov, f"layer {layer} V after {steps} replays")
+    assert all(p.errors() == 0 for p in pools)
 
 
 def tiny_llama(seed=0):

@@ -17,6 +17,7 @@ import torch
 
 from capi_pool import SEPARATE_FINALIZE, SEQ_FROM_DEVICE, CPool
 from kvgen import C1, config1_steps, hf_layout, normal, to_bits
+from mirror import DeviceMirror
 from oracle.kv_oracle import DenseLayerOracle, dense_append_reference
 
 pytestmark = pytest.mark.gpu
@@ -114,23 +115,29 @@ def test_config1_update_every_step(capi, flags):
 
 def test_config2_llama8b_shape(capi):
     """B=16, 8 KV heads x 128, bf16, page 16: prefill 512, then 256 decode steps of fused
-    append+gather; two layers, every 32nd step and the last compared in full."""
+    append+gather; two layers, every step against the device mirror, every 32nd step and the
+    last against the oracle."""
     B, H, D, P, prefill, decode = 16, 8, 128, 16, 512, 256
     cap = prefill + decode
     gen = torch.Generator().manual_seed(1002)
     for layer in range(2):
         pool = make_pool(cap, B, H, D, P, torch.bfloat16)
         oracle = DenseLayerOracle(B, cap, P)
+        mirror = DeviceMirror(B, H, cap, D, torch.bfloat16)
         k = hf_layout(B, H, prefill, D, torch.bfloat16, gen)
         v = hf_layout(B, H, prefill, D, torch.bfloat16, gen)
         got = pool.update(k.cuda(), v.cuda(), prefill)
         oracle.append(to_bits(k), to_bits(v))
+        mirror.append(k.cuda(), v.cuda())
         compare_layer(pool, oracle, got, f"C2 layer {layer} prefill")
+        mirror.check(got, f"C2 layer {layer} prefill")
         for step in range(decode):
             k = hf_layout(B, H, 1, D, torch.bfloat16, gen)
             v = hf_layout(B, H, 1, D, torch.bfloat16, gen)
             got = pool.update(k.cuda(), v.cuda(), prefill + step + 1)
             oracle.append(to_bits(k), to_bits(v))
+            mirror.append(k.cuda(), v.cuda())
+            mirror.check(got, f"C2 layer {layer} step {step}")
             if step % 32 == 31 or step == decode - 1:
                 compare_layer(pool, oracle, got, f"C2 layer {layer} step {step}")
         pool.check_invariants()
@@ -196,7 +203,8 @@ def test_cu_balanced_tail_pieces(capi, B, S):
 
 def test_config3_ragged_random_pages(capi):
     """B=64, context lengths U{128..4096}, pages handed out in a seeded random permutation:
-    a non-contiguous block table; 1-token append + gather steps."""
+    a non-contiguous block table; 128 1-token append + gather steps, every one against the device
+    mirror, the first and the last against the oracle."""
     B, H, D, P = 64, 8, 128, 16
     rng = np.random.default_rng(2003)
     lengths = sorted(rng.integers(128, 4097, size=B).tolist(), reverse=True)
@@ -206,12 +214,14 @@ def test_config3_ragged_random_pages(capi):
     perm = torch.from_numpy(np.random.default_rng(3003).permutation(B * mb).astype(np.int32))
     pool = make_pool(cap, B, H, D, P, torch.bfloat16, order=perm)
     oracle = DenseLayerOracle(B, cap, P)
+    mirror = DeviceMirror(B, H, cap, D, torch.bfloat16)
     gen = torch.Generator().manual_seed(1003)
     for b, t in staircase(lengths):
         k = hf_layout(b, H, t, D, torch.bfloat16, gen)
         v = hf_layout(b, H, t, D, torch.bfloat16, gen)
         pool.append(k.cuda(), v.cuda())
         oracle.append(to_bits(k), to_bits(v))
+        mirror.append(k.cuda(), v.cuda())
     bt = pool.bt.cpu().numpy()
     assert (np.diff(bt[0, : lengths[0] // P]) != 1).any(), "block table should be non-contiguous"
     for step in range(steps):
@@ -220,6 +230,8 @@ def test_config3_ragged_random_pages(capi):
         seq = lengths[0] + step + 1
         got = pool.update(k.cuda(), v.cuda(), seq)
         oracle.append(to_bits(k), to_bits(v))
+        mirror.append(k.cuda(), v.cuda())
+        mirror.check(got, f"C3 step {step}")
         if step in (0, steps - 1):
             compare_layer(pool, oracle, got, f"C3 step {step}")
     pool.check_invariants()
@@ -250,18 +262,21 @@ def test_config5_pool_at_90_percent_with_churn(capi):
     """70B-class layer shape: B=32, context 8192, pool sized for 90% occupancy; before each 1-token
     append + gather of all rows, two seeded rows are freed and re-prefilled with 8192 new tokens
     (barq_kv_append over the row's one-row metadata view), which takes the pages those rows and
-    earlier ones released: the pool stays near 90% for every step."""
-    B, H, D, P, ctx, steps = 32, 8, 128, 16, 8192, 16
+    earlier ones released: the pool stays near 90% for every step.  All 64 steps of the
+    configuration, every one against the device mirror, steps 0, 31 and 63 against the oracle."""
+    B, H, D, P, ctx, steps = 32, 8, 128, 16, 8192, 64
     cap = ctx + steps
     live = B * (ctx // P)
     num_pages = int(np.ceil(live / 0.9))
     pool = make_pool(cap, B, H, D, P, torch.bfloat16, num_pages=num_pages)
     oracle = DenseLayerOracle(B, cap, P)
+    mirror = DeviceMirror(B, H, cap, D, torch.bfloat16)
     gen = torch.Generator().manual_seed(1005)
     k = hf_layout(B, H, ctx, D, torch.bfloat16, gen)
     v = hf_layout(B, H, ctx, D, torch.bfloat16, gen)
     pool.append(k.cuda(), v.cuda())
     oracle.append(to_bits(k), to_bits(v))
+    mirror.append(k.cuda(), v.cuda())
     del k, v
     assert pool.free_top() == num_pages - live
     churn = np.random.default_rng(4005)
@@ -270,10 +285,12 @@ def test_config5_pool_at_90_percent_with_churn(capi):
         rows = sorted(churn.choice(B, size=2, replace=False).tolist())
         pool.free_rows(rows)
         oracle.release_rows(rows)
+        mirror.release_rows(rows)
         kr = hf_layout(2, H, ctx, D, torch.bfloat16, gen)
         vr = hf_layout(2, H, ctx, D, torch.bfloat16, gen)
         pool.append_rows(rows, kr.cuda(), vr.cuda())
         oracle.append_rows(rows, to_bits(kr), to_bits(vr))
+        mirror.append_rows(rows, kr.cuda(), vr.cuda())
         del kr, vr
         most_free = max(most_free, pool.free_top())
         k = hf_layout(B, H, 1, D, torch.bfloat16, gen)
@@ -281,7 +298,9 @@ def test_config5_pool_at_90_percent_with_churn(capi):
         seq = oracle.get_seq_length() + 1
         got = pool.update(k.cuda(), v.cuda(), seq)
         oracle.append(to_bits(k), to_bits(v))
-        if step in (0, 7, steps - 1):
+        mirror.append(k.cuda(), v.cuda())
+        mirror.check(got, f"C5 step {step}")
+        if step in (0, 31, steps - 1):
             compare_layer(pool, oracle, got, f"C5 step {step}")
     # every decode step ran with >= 88% of the pool holding live tokens
     assert most_free <= 0.12 * num_pages, most_free
