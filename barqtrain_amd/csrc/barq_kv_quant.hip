@@ -87,7 +87,8 @@ struct ColdPtrs {
 };
 
 // ---------------------------------------------------------------------------------------------
-// Compress: workgroup per row.
+// Compress: workgroup per row.  quantise_page serves any geometry; quantise_regs below (one
+// round trip of loads per page) the common two-byte ones.
 // ---------------------------------------------------------------------------------------------
 
 struct CompressArgs {
@@ -265,6 +266,183 @@ __global__ void __launch_bounds__(kThreads) compress_kernel(const CompressArgs a
       }
       __syncthreads();
     }
+  }
+  if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
+}
+
+// Register-resident compress for 16-byte vectors of 2-byte elements, when a token's G = C / 8
+// vectors divide the workgroup (G | 256), a page holds NV * 256 vectors and D / 8 is a power of
+// two: thread t holds vectors t + 256 i (i < NV) of a page's K and V -- channel group t % G of
+// tokens t / G + i * 256 / G -- so a page costs one round trip of loads, issued (for a row's first
+// block) while the cold pages are popped.  Key maxima over the page's tokens combine the 256 / G
+// threads of a channel group through LDS; value maxima over a (token, head) combine the head's
+// D / 8 adjacent lanes with shuffles.  The codes and scales are quantise_page's: maxima of finite
+// magnitudes, group_exponent, e4m3_encode of x * 2^-e.  A row's blocks take the cold pages its one
+// pop reserves in block order (free_cold[top - 1], [top - 2], ...), and their hot pages go back
+// with one push, in block order.
+constexpr int kRegsMaxChannels = 2048;  // C = G * 8 with G | 256
+
+template <int KIND, int NV>
+struct PageRegs {
+  using Raw = typename RawC<16>::T;
+  Raw k[NV], v[NV];
+
+  __device__ void load(const barq_kv_pool& p, int hp, int C) {
+    const Raw* kp = (const Raw*)((const char*)p.key_pages + (int64_t)hp * p.page_size * C * 2);
+    const Raw* vp = (const Raw*)((const char*)p.value_pages + (int64_t)hp * p.page_size * C * 2);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) k[i] = kp[threadIdx.x + kThreads * i];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = vp[threadIdx.x + kThreads * i];
+  }
+  __device__ static float elem(const Raw& w, int e) {
+    return Elem<KIND>::to_float((uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+  }
+};
+
+template <int KIND, int NV>
+__device__ void quantise_regs(const CompressArgs& a, const PageRegs<KIND, NV>& pg, int cp, float* s_red,
+                              int8_t* s_kexp) {
+  using Regs = PageRegs<KIND, NV>;
+  const barq_kv_pool& p = a.p;
+  const int t = threadIdx.x;
+  const int P = (int)p.page_size, H = (int)p.kv_heads, D = (int)p.head_dim, C = H * D;
+  const int G = C / 8, VD = D / 8, R = kThreads / G;  // R threads share a channel group
+  const int g = t % G;
+  // key maxima over the page's tokens, per channel
+  float mk[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) mk[e] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mk[e] = fmaxf(mk[e], finite_abs(Regs::elem(pg.k[i], e)));
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s_red[t * 8 + e] = mk[e];
+  __syncthreads();
+  if (t < G) {
+    typename CodeVec<8>::U sc;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float m = s_red[t * 8 + e];
+      for (int q = 1; q < R; ++q) m = fmaxf(m, s_red[(t + q * G) * 8 + e]);
+      const int ex = group_exponent(m);
+      s_kexp[t * 8 + e] = (int8_t)ex;
+      sc.b[e] = (uint8_t)(ex + 127);
+    }
+    *(typename CodeVec<8>::Raw*)(a.c.key_scales + (int64_t)cp * C + t * 8) = sc.v;
+  }
+  __syncthreads();
+  int kex[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) kex[e] = s_kexp[g * 8 + e];
+  uint8_t* __restrict__ kc = a.c.codes[0] + (int64_t)cp * P * C;
+  uint8_t* __restrict__ vc = a.c.codes[1] + (int64_t)cp * P * C;
+  const int h = g / VD;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int tok = t / G + i * R;
+    // value maxima over (token, head): the head's VD adjacent lanes
+    float mv = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mv = fmaxf(mv, finite_abs(Regs::elem(pg.v[i], e)));
+    for (int o = 1; o < VD; o <<= 1) mv = fmaxf(mv, __shfl_xor(mv, o, kWave));
+    const int ve = group_exponent(mv);
+    if (g % VD == 0) a.c.value_scales[((int64_t)cp * P + tok) * H + h] = (uint8_t)(ve + 127);
+    typename CodeVec<8>::U ck, cv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ck.b[e] = (uint8_t)e4m3_encode(ldexpf(Regs::elem(pg.k[i], e), -kex[e]));
+      cv.b[e] = (uint8_t)e4m3_encode(ldexpf(Regs::elem(pg.v[i], e), -ve));
+    }
+    const int64_t at = (int64_t)tok * C + g * 8;
+    *(typename CodeVec<8>::Raw*)(kc + at) = ck.v;
+    *(typename CodeVec<8>::Raw*)(vc + at) = cv.v;
+  }
+}
+
+template <int KIND, int NV>
+__global__ void __launch_bounds__(kThreads) compress_regs_kernel(const CompressArgs a) {
+  __shared__ int lds_scan[kWaves];
+  __shared__ int s_blocks[kThreads];
+  __shared__ int s_pages[kThreads];
+  __shared__ int s_cold[kThreads];
+  __shared__ int s_avail, s_top, s_slot;
+  __shared__ float s_red[kThreads * 8];
+  __shared__ int8_t s_kexp[kRegsMaxChannels];
+  const barq_kv_pool& p = a.p;
+  const int tid = threadIdx.x;
+  const int r = blockIdx.x;
+  const int mb = (int)p.max_blocks;
+  const int C = (int)(p.kv_heads * p.head_dim);
+  const int len = p.seq_lens[r];
+  const int old_len = len - a.c.window;
+  const int jmax = min(old_len > 0 ? (int)a.div_page.div((uint32_t)old_len) : 0,
+                       min(ceil_div_fd(p.high_water[r], a.div_page), mb));
+  int32_t* row = p.block_table + (int64_t)r * mb;
+  int err = 0;
+  for (int j0 = 0; j0 < jmax; j0 += kThreads) {
+    const int j = j0 + tid;
+    int hot = 0, page = -1;
+    if (j < jmax) {
+      page = checked_id(row[j], p.num_pages);
+      hot = page >= 0 && (!p.page_shares || p.page_shares[page] == 0);
+    }
+    int count = 0;
+    const int k = block_exclusive_scan(hot, lds_scan, &count);
+    if (hot) {
+      s_blocks[k] = j;
+      s_pages[k] = page;
+    }
+    __syncthreads();
+    if (count == 0) continue;  // uniform
+    PageRegs<KIND, NV> pg;
+    pg.load(p, s_pages[0], C);  // in flight while the cold pages are reserved
+    if (tid == 0) {
+      const int before = atomicSub(&p.ctrl[BARQ_KV_CTRL_COLD_TOP], count);
+      int avail = 0;
+      if ((int64_t)before > a.c.num_cold) {
+        atomicAdd(&p.ctrl[BARQ_KV_CTRL_COLD_TOP], count);
+        err |= BARQ_KV_ERRBIT_BAD_INDEX;
+      } else {
+        avail = min(max(before, 0), count);
+        if (avail < count) {
+          atomicAdd(&p.ctrl[BARQ_KV_CTRL_COLD_TOP], count - avail);
+          err |= BARQ_KV_ERRBIT_POOL_EXHAUSTED;
+        }
+      }
+      s_avail = avail;
+      s_top = before;
+    }
+    __syncthreads();
+    const int avail = s_avail;
+    if (tid < avail) {
+      const int cp = checked_id(a.c.free_cold[s_top - 1 - tid], a.c.num_cold);
+      if (cp < 0) err |= BARQ_KV_ERRBIT_BAD_INDEX;
+      s_cold[tid] = cp;
+    }
+    __syncthreads();
+    for (int q = 0; q < avail; ++q) {
+      if (q > 0) pg.load(p, s_pages[q], C);
+      const int cp = s_cold[q];
+      if (cp >= 0) quantise_regs<KIND, NV>(a, pg, cp, s_red, s_kexp);  // uniform
+      __syncthreads();  // s_red / s_kexp reused by the next block
+    }
+    // Every thread has read every quantised hot page: map the cold pages, push the hot pages.
+    const int done = tid < avail && s_cold[tid] >= 0;
+    int n_done = 0;
+    const int pos = block_exclusive_scan(done, lds_scan, &n_done);
+    if (n_done > 0) {  // uniform
+      if (tid == 0) s_slot = atomicAdd(&p.ctrl[BARQ_KV_CTRL_FREE_TOP], n_done);
+      __syncthreads();
+      if (done) {
+        row[s_blocks[tid]] = BARQ_KV_COLD_ENTRY(s_cold[tid]);
+        const int slot = s_slot + pos;
+        if (slot < p.num_pages) p.free_pages[slot] = s_pages[tid];
+        else err |= BARQ_KV_ERRBIT_BAD_INDEX;
+      }
+    }
+    __syncthreads();  // s_blocks / s_pages / s_cold reused by the next round
   }
   if (err) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], err);
 }
@@ -836,6 +1014,31 @@ const void* compress_fn(int64_t kind, int ve) {
 }
 
 template <int KIND>
+const void* compress_regs_fn_t(int nv) {
+  switch (nv) {
+    case 1: return (const void*)&compress_regs_kernel<KIND, 1>;
+    case 2: return (const void*)&compress_regs_kernel<KIND, 2>;
+    case 4: return (const void*)&compress_regs_kernel<KIND, 4>;
+    default: return (const void*)&compress_regs_kernel<KIND, 8>;
+  }
+}
+
+// The register-resident compress when the geometry admits it (2-byte elements in 16-byte
+// vectors, G = kv_heads * head_dim / 8 dividing the workgroup, page_size * G / 256 vectors per
+// thread in {1, 2, 4, 8} -- 16 would not stay in registers --, head_dim / 8 a power of two up
+// to a wave), else null.
+const void* compress_regs_fn(const barq_kv_pool* p, int64_t kind, int ve) {
+  if (kind == BARQ_KV_FP32 || ve != 8) return nullptr;
+  const int64_t C = p->kv_heads * p->head_dim, G = C / 8, vd = p->head_dim / 8;
+  if (G < 1 || kThreads % G != 0 || vd > kWave || (vd & (vd - 1)) != 0 || (p->page_size * G) % kThreads != 0)
+    return nullptr;
+  const int64_t nv = p->page_size * G / kThreads;
+  if (nv != 1 && nv != 2 && nv != 4 && nv != 8) return nullptr;
+  return kind == BARQ_KV_BF16 ? compress_regs_fn_t<BARQ_KV_BF16>((int)nv)
+                              : compress_regs_fn_t<BARQ_KV_FP16>((int)nv);
+}
+
+template <int KIND>
 int launch_gather(int ve, int lpp, dim3 grid, GatherArgs* a, hipStream_t s) {
   const void* fn = (const void*)&gather_cold_kernel<KIND, 1>;
   if constexpr (KIND != BARQ_KV_FP32) {  // 8 two-byte elements: a 16-byte vector
@@ -879,7 +1082,8 @@ int barq_kv_compress(const barq_kv_pool* pool, const barq_kv_cold* cold, int64_t
   int ve = eb == 2 ? 8 : 4;
   while (ve > 1 && (D % ve || (bits & (uint64_t)(ve * eb - 1)) || (cbits & (uint64_t)(ve - 1)))) ve >>= 1;
   a.div_groups = FastDiv::make((uint32_t)(pool->kv_heads * D / ve));
-  return launch(compress_fn(cold->element_type, ve), dim3((uint32_t)batch), &a, (hipStream_t)stream);
+  const void* fn = compress_regs_fn(pool, cold->element_type, ve);
+  return launch(fn ? fn : compress_fn(cold->element_type, ve), dim3((uint32_t)batch), &a, (hipStream_t)stream);
 }
 
 int barq_kv_gather_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, void* key_out,
