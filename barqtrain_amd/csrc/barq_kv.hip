@@ -771,8 +771,22 @@ __global__ void __launch_bounds__(kStreamThreads) stream_kernel_any(const Stream
 constexpr int64_t kLeanResidentTilesPerCU = 5;
 constexpr int64_t kLeanResidentTilesPerCU16 = 4;
 
-// NU: vectors per copy thread (positions per tile / (4 / LPP)); tiles are whole pages, at most two.
-template <int NU, int LPP>
+// Page of block `blk`, the k-th block a lean tile touches (touched = nbl - k > 0): its table
+// entry for an old block, the stack entry of its rank for a new one; -1 when unmapped.
+__device__ __forceinline__ int lean_page(const barq_kv_pool& p, const NewBlocks& nb, int blk, int touched, int mb,
+                                         int top, int base, int entry) {
+  if (touched <= 0 || blk >= mb) return -1;
+  if (blk < nb.first) return checked_page(entry, p.num_pages);
+  if (blk < nb.first + nb.count) {
+    const int idx = top - 1 - (base + blk - nb.first);
+    return idx >= 0 ? checked_page(p.free_pages[idx], p.num_pages) : -1;
+  }
+  return -1;
+}
+
+// NU: vectors per copy thread (positions per tile / (4 / LPP)); tiles of one or two whole pages,
+// or (BAL) balanced chunks of at most one page.
+template <int NU, int LPP, bool BAL>
 __global__ void __launch_bounds__(kStreamThreads) lean_stream_kernel(const StreamArgs a) {
   using V = typename VecT<16>::T;
   constexpr int RSTEP = 4 / LPP;
@@ -796,51 +810,69 @@ __global__ void __launch_bounds__(kStreamThreads) lean_stream_kernel(const Strea
     return;
   }
 
-  // Copy waves.  Tile (K or V, row b, chunk c): positions [c * chunk, + chunk), blocks blk0 and,
-  // for two-page tiles, blk0 + 1 (< max_blocks: the grid covers seq_out <= capacity).
+  // Copy waves.  Tile (K or V, row b, chunk c).  Page-aligned tiles: positions [c * chunk,
+  // + chunk), whole pages.  Balanced tiles: the row's positions up to its new end, [0, L) with
+  // L = min(len + T, seq_out), cut into m = div_chunks.d equal chunks (ceil(L / m) positions,
+  // at most a tile's NU * 4 / LPP), so that every tile of the launch -- and every CU, the grid
+  // being a multiple of the CU count -- moves the same bytes whatever the context.  The output
+  // positions past the row's end, [L, E) up to the extent E (stale data below the mark, else
+  // zeros), are cut the same way when E = seq_out is known here, else (extent on the device)
+  // written by the row's last chunk.  Balanced tiles hold at most one page of positions, so a
+  // chunk at page offset `off` touches at most two blocks, as a two-page tile does.
   const int len = p.seq_lens[b];
   const int hw = p.high_water[b];
-  const int blk0 = c * a.ppt;
-  const int e0 = p.block_table[(int64_t)b * mb + blk0];
-  int e1 = -1;
-  if (a.ppt > 1 && blk0 + 1 < mb) e1 = p.block_table[(int64_t)b * mb + blk0 + 1];
-  const int lo = c * a.chunk;
-  int hi = lo + a.chunk;
-  if (hi > min(len + T, a.seq_out)) {
-    // Positions past this row's end: the output extent is the longest row (or seq_out).
-    int smax = a.seq_out;
-    if (a.seq_from_device) smax = min(wave_max(lane < a.batch ? p.seq_lens[lane] + T : 0), a.seq_out);
-    hi = min(hi, smax);
+  const int64_t trow = (int64_t)b * mb;
+  int lo, hi, xlo = 0, xhi = 0, blk0, off = 0, nbl, e0 = -1, e1 = -1;
+  if constexpr (!BAL) {
+    // the block-table entries load with the row's length
+    blk0 = c * a.ppt;
+    nbl = a.ppt > 1 ? 2 : 1;
+    e0 = p.block_table[trow + blk0];
+    if (nbl > 1 && blk0 + 1 < mb) e1 = p.block_table[trow + blk0 + 1];
+    lo = c * a.chunk;
+    hi = lo + a.chunk;
+    if (hi > min(len + T, a.seq_out)) {
+      // Positions past this row's end: the output extent is the longest row (or seq_out).
+      int smax = a.seq_out;
+      if (a.seq_from_device) smax = min(wave_max(lane < a.batch ? p.seq_lens[lane] + T : 0), a.seq_out);
+      hi = min(hi, smax);
+    }
+  } else {
+    const int m = (int)a.div_chunks.d;
+    const int L = min(len + T, a.seq_out);
+    const int q = (int)a.div_chunks.div((uint32_t)(L + m - 1));
+    lo = min(c * q, L);
+    hi = min(lo + q, L);
+    if (!a.seq_from_device) {
+      const int z = (int)a.div_chunks.div((uint32_t)(a.seq_out - L + m - 1));
+      xlo = min(L + c * z, a.seq_out);
+      xhi = min(xlo + z, a.seq_out);
+    } else if (c == m - 1) {
+      xlo = L;
+      xhi = min(wave_max(lane < a.batch ? p.seq_lens[lane] + T : 0), a.seq_out);
+    }
+    blk0 = (int)a.div_page.div((uint32_t)lo);
+    off = lo - blk0 * P;
+    nbl = hi > lo ? (int)a.div_page.div((uint32_t)(off + hi - lo - 1)) + 1 : 0;  // blocks touched
+    if (nbl > 0) e0 = p.block_table[trow + blk0];
+    if (nbl > 1 && blk0 + 1 < mb) e1 = p.block_table[trow + blk0 + 1];
   }
   const NewBlocks nb = new_blocks(len, hw, T, mb, a.div_page);
-  const int nbl = a.ppt > 1 ? 2 : 1;
   int base = 0, top = 0;
   if (nb.count > 0 && blk0 < nb.first + nb.count && blk0 + nbl > nb.first) {
     // The tile holds new blocks: their pages are ranked after the new blocks of rows [0, b).
     top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
     base = wave_sum(lane < b ? new_blocks(p.seq_lens[lane], p.high_water[lane], T, mb, a.div_page).count : 0);
   }
-  int64_t pbs[2];
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int blk = blk0 + k;
-    int page = -1;
-    if (k < nbl && blk < mb) {
-      if (blk < nb.first) {
-        page = checked_page(k == 0 ? e0 : e1, p.num_pages);
-      } else if (blk < nb.first + nb.count) {
-        const int idx = top - 1 - (base + blk - nb.first);
-        page = idx >= 0 ? checked_page(p.free_pages[idx], p.num_pages) : -1;
-      }
-    }
-    pbs[k] = page >= 0 ? (int64_t)page * a.page_bytes : (int64_t)-1;
-  }
-  const int64_t pb0 = pbs[0], pb1 = pbs[1];
+  const int pg0 = lean_page(p, nb, blk0, nbl, mb, top, base, e0);
+  const int pg1 = lean_page(p, nb, blk0 + 1, nbl - 1, mb, top, base, e1);
+  const int64_t pb0 = pg0 >= 0 ? (int64_t)pg0 * a.page_bytes : (int64_t)-1;
+  const int64_t pb1 = pg1 >= 0 ? (int64_t)pg1 * a.page_bytes : (int64_t)-1;
   if (committing) {
     __builtin_amdgcn_s_waitcnt(0);  // the metadata loads have returned before the tile arrives
     __syncthreads();
   }
-  if (hi <= lo) return;
+  if (hi <= lo && xhi <= xlo) return;
 
   const int cw = wave - 1;
   const int r0 = cw / LPP;
@@ -858,49 +890,80 @@ __global__ void __launch_bounds__(kStreamThreads) lean_stream_kernel(const Strea
   char* pages = (char*)(kv ? p.value_pages : p.key_pages);
   const int nval = hi - lo;
   V val[NU];
-  if (hi <= max(hw, len + T) && pb0 >= 0 && (nval <= P || pb1 >= 0)) {
-    // Every position holds data on mapped pages: branch-free loads, back to back (positions past
-    // the tile repeat its last one, a cache hit).
+  if (nval > 0) {
+    if (hi <= max(hw, len + T) && pb0 >= 0 && (nbl < 2 || pb1 >= 0)) {
+      // Every position holds data on mapped pages: branch-free loads, back to back (positions
+      // past the tile repeat its last one, a cache hit).
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      const int j = min(r0 + u * RSTEP, nval - 1);
-      const int s = lo + j;
-      const bool second = j >= P;
-      const char* page_pos = pages + (second ? pb1 : pb0) + (uint32_t)(second ? j - P : j) * tokb;
-      const bool fresh = (unsigned)(s - len) < (unsigned)T;
-      val[u] = ld_stream<V>(fresh ? in_row + (uint32_t)(s - len) * ist + in_lane : page_pos + page_lane);
+      for (int u = 0; u < NU; ++u) {
+        const int j = min(r0 + u * RSTEP, nval - 1);
+        const int s = lo + j;
+        const bool fresh = (unsigned)(s - len) < (unsigned)T;
+        const int w = off + j;
+        const bool second = w >= P;
+        const char* page_at = pages + (second ? pb1 : pb0) + (uint32_t)(second ? w - P : w) * tokb;
+        val[u] = ld_stream<V>(fresh ? in_row + (uint32_t)(s - len) * ist + in_lane : page_at + page_lane);
+      }
+    } else {
+      // Zero padding, unmapped blocks (an exhausted pool) or positions never written.
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const int j = r0 + u * RSTEP;
+        const int s = lo + j;
+        val[u] = zero_vec<V>();
+        if (j < nval) {
+          const int w = off + j;
+          const bool second = w >= P;
+          const int64_t pb = second ? pb1 : pb0;
+          if ((unsigned)(s - len) < (unsigned)T) {
+            val[u] = ld_stream<V>(in_row + (uint32_t)(s - len) * ist + in_lane);
+          } else if (s < hw && pb >= 0) {
+            val[u] = ld_stream<V>(pages + pb + (uint32_t)(second ? w - P : w) * tokb + page_lane);
+          }
+        }
+      }
     }
-  } else {
-    // Zero padding, unmapped blocks (an exhausted pool) or positions never written.
+    wait_vm<0>();
+    // One store in flight per wave: a single-round launch drains HBM fastest that way.
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
       const int j = r0 + u * RSTEP;
-      const int s = lo + j;
-      val[u] = zero_vec<V>();
       if (j < nval) {
-        const bool second = j >= P;
-        const int64_t pb = second ? pb1 : pb0;
+        const int s = lo + j;
+        wait_vm<0>();
+        st_stream<V>(out_row + (uint32_t)s * oss + out_lane, val[u]);
         if ((unsigned)(s - len) < (unsigned)T) {
-          val[u] = ld_stream<V>(in_row + (uint32_t)(s - len) * ist + in_lane);
-        } else if (s < hw && pb >= 0) {
-          val[u] = ld_stream<V>(pages + pb + (uint32_t)(second ? j - P : j) * tokb + page_lane);
+          const int w = off + j;
+          const bool second = w >= P;
+          const int64_t pb = second ? pb1 : pb0;
+          if (pb >= 0) *(V*)(pages + pb + (uint32_t)(second ? w - P : w) * tokb + page_lane) = val[u];
         }
       }
     }
   }
-  wait_vm<0>();
-  // One store in flight per wave: a single-round launch drains HBM fastest that way.
+  // Balanced tiles: output positions [xlo, xhi) past the row's new end (no new tokens there):
+  // stale data below the mark on the pages the table maps (blocks below the mark are old ones,
+  // which the commit does not remap), else zeros.
+  if constexpr (!BAL) return;
+  for (int s0 = xlo; s0 < xhi; s0 += NU * RSTEP) {
 #pragma unroll
-  for (int u = 0; u < NU; ++u) {
-    const int j = r0 + u * RSTEP;
-    if (j < nval) {
-      const int s = lo + j;
-      wait_vm<0>();
-      st_stream<V>(out_row + (uint32_t)s * oss + out_lane, val[u]);
-      if ((unsigned)(s - len) < (unsigned)T) {
-        const bool second = j >= P;
-        const int64_t pb = second ? pb1 : pb0;
-        if (pb >= 0) *(V*)(pages + pb + (uint32_t)(second ? j - P : j) * tokb + page_lane) = val[u];
+    for (int u = 0; u < NU; ++u) {
+      const int s = s0 + r0 + u * RSTEP;
+      val[u] = zero_vec<V>();
+      if (s < xhi && s < hw) {
+        const int blk = (int)a.div_page.div((uint32_t)s);
+        const int page = checked_page(p.block_table[trow + blk], p.num_pages);
+        if (page >= 0)
+          val[u] = ld_stream<V>(pages + (int64_t)page * a.page_bytes + (uint32_t)(s - blk * P) * tokb + page_lane);
+      }
+    }
+    wait_vm<0>();
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int s = s0 + r0 + u * RSTEP;
+      if (s < xhi) {
+        wait_vm<0>();
+        st_stream<V>(out_row + (uint32_t)s * oss + out_lane, val[u]);
       }
     }
   }
@@ -1567,12 +1630,13 @@ int launch_stream_kernel(int vb, int lpp, bool rounds, dim3 grid, StreamArgs* ar
 #undef BARQ_STREAM_CASE
 }
 
+template <bool BAL>
 int launch_lean_kernel(int nu, int lpp, dim3 grid, StreamArgs* arg, hipStream_t stream) {
-#define BARQ_LEAN_CASE(NU)                                                                               \
-    switch (lpp) {                                                                                        \
-      case 1: return launch((const void*)&lean_stream_kernel<NU, 1>, grid, arg, stream, kStreamThreads);  \
-      case 2: return launch((const void*)&lean_stream_kernel<NU, 2>, grid, arg, stream, kStreamThreads);  \
-      default: return launch((const void*)&lean_stream_kernel<NU, 4>, grid, arg, stream, kStreamThreads); \
+#define BARQ_LEAN_CASE(NU)                                                                                    \
+    switch (lpp) {                                                                                             \
+      case 1: return launch((const void*)&lean_stream_kernel<NU, 1, BAL>, grid, arg, stream, kStreamThreads);  \
+      case 2: return launch((const void*)&lean_stream_kernel<NU, 2, BAL>, grid, arg, stream, kStreamThreads);  \
+      default: return launch((const void*)&lean_stream_kernel<NU, 4, BAL>, grid, arg, stream, kStreamThreads); \
     }
   switch (nu) {
     case 4: BARQ_LEAN_CASE(4)
@@ -1633,16 +1697,31 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
 
   // Lean kernel: a gather launch whose tiles of one page -- else two -- are all resident at once.
   const int64_t lpp = hv / 64;
-  int64_t lean_ppt = 0, lean_nu = 0;
+  // Balanced lean tiles: every (row, K or V) cut into m equal chunks of at most a page's
+  // positions, 2 * batch * m the smallest multiple of the CU count, up to per_cu tiles per CU,
+  // that holds the one-page tiles' chunks; 0 if none does.
+  // (C2, context 513-576: 15.2 -> 14.1 us per launch.)  Two-page tiles stay page-aligned: cut
+  // the same way (up to three blocks a tile) they ran 1-2 % slower; six balanced one-page tiles
+  // per CU instead of two-page ones, 20 % slower.
+  const auto balanced_chunks = [&](int64_t aligned, int64_t per_cu) -> int64_t {
+    for (int64_t k = 1; k <= per_cu; ++k)
+      if ((k * ncu) % (2 * batch) == 0 && k * ncu / (2 * batch) >= aligned) return k * ncu / (2 * batch);
+    return 0;
+  };
+  int64_t lean_ppt = 0, lean_nu = 0, lean_m = 0;
   if (gather && fast && vb == 16 && batch <= kWave && ncu > 0) {
     for (int64_t q = 1; q <= 2 && lean_ppt == 0; ++q) {
       if ((q * P * lpp) % 4 != 0) continue;  // whole steps of 4 / LPP positions
       const int64_t nu = q * P * lpp / 4;
       if (nu != 4 && nu != 8 && nu != 16) continue;
       const int64_t resident = nu == 16 ? kLeanResidentTilesPerCU16 : kLeanResidentTilesPerCU;
-      if (2 * batch * ((span + q * P - 1) / (q * P)) <= resident * ncu) {
+      const int64_t aligned = (span + q * P - 1) / (q * P);
+      if (2 * batch * aligned <= resident * ncu) {
         lean_ppt = q;
         lean_nu = nu;
+        // one-page tiles, at least one per CU, not a multiple of the CU count: balance them
+        if (q == 1 && 2 * batch * aligned >= ncu && (2 * batch * aligned) % ncu != 0)
+          lean_m = balanced_chunks(aligned, resident);
       }
     }
   }
@@ -1658,7 +1737,8 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   if (lean_ppt > 0) pages_per_tile = lean_ppt;
   const int64_t chunk = pages_per_tile * P;
   if (chunk * hv > kI32Max - (int64_t)kThreads * kUnroll) return BARQ_KV_ERR_INVALID;
-  const int64_t chunks = (span + chunk - 1) / chunk;
+  int64_t chunks = (span + chunk - 1) / chunk;
+  if (lean_m > 0) chunks = lean_m;
   const int64_t tiles = 2 * batch * chunks;
   if (tiles > kI32Max) return BARQ_KV_ERR_INVALID;
 
@@ -1716,7 +1796,8 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   hipStream_t s = (hipStream_t)stream;
   // Launches with more tiles than the CUs hold at once take the kernel built for several rounds.
   const bool rounds = fast && ncu > 0 && grid > kResidentTilesPerCU * ncu;
-  int rc = lean_ppt > 0 ? launch_lean_kernel((int)lean_nu, (int)lpp, dim3((uint32_t)grid), &a, s)
+  int rc = lean_ppt > 0 ? (lean_m > 0 ? launch_lean_kernel<true>((int)lean_nu, (int)lpp, dim3((uint32_t)grid), &a, s)
+                                      : launch_lean_kernel<false>((int)lean_nu, (int)lpp, dim3((uint32_t)grid), &a, s))
                         : launch_stream_kernel(vb, fast ? (int)(hv / 64) : 0, rounds, dim3((uint32_t)grid), &a, s);
   if (rc != BARQ_KV_OK) return rc;
   if (tokens > 0 && !a.commit_in_kernel) {

@@ -201,6 +201,62 @@ def test_cu_balanced_tail_pieces(capi, B, S):
     assert pool.errors() == 0
 
 
+@pytest.mark.parametrize("B,P,S", [(8, 16, 700), (8, 32, 700), (16, 16, 560), (16, 16, 700), (32, 16, 300),
+                                   (2, 16, 2100)])
+def test_balanced_lean_tiles_with_stale_rows(capi, B, P, S):
+    """Single-round gather launches whose one-page tile count is not a multiple of the CU count
+    cut each (row, K or V) into equal chunks that start anywhere in a page (touching up to two
+    blocks); (16, 16, 700) takes page-aligned two-page tiles.  Ragged rows, a crop whose slots stay visible below the mark once a longer row sets
+    the extent, appends of 1 and 3 tokens that map new blocks, exact extents (the positions past
+    a row's end spread over its chunks) and device-side extents (written by the row's last chunk;
+    nothing past the longest row written)."""
+    H, D = 8, 128
+    rng = np.random.default_rng(7000 + B + P)
+    lengths = sorted(rng.integers(S // 2, S + 1, size=B).tolist(), reverse=True)
+    lengths[0] = S
+    cap = S + 40
+    pool = make_pool(cap, B, H, D, P, torch.bfloat16, order=torch.from_numpy(
+        np.random.default_rng(B).permutation(B * (-(-cap // P))).astype(np.int32)))
+    oracle = DenseLayerOracle(B, cap, P)
+    gen = torch.Generator().manual_seed(B * P)
+
+    def tokens(b, t):
+        return hf_layout(b, H, t, D, torch.bfloat16, gen), hf_layout(b, H, t, D, torch.bfloat16, gen)
+
+    for b, t in staircase(lengths):
+        k, v = tokens(b, t)
+        pool.append(k.cuda(), v.cuda())
+        oracle.append(to_bits(k), to_bits(v))
+    k, v = tokens(B, 1)  # every row: the crop below applies to the whole batch
+    pool.append(k.cuda(), v.cuda())
+    oracle.append(to_bits(k), to_bits(v))
+    compare_layer(pool, oracle, None, f"B{B} P{P} prefill")
+    cut = S // 2 + 7
+    pool.crop(B, cut)
+    oracle.crop(cut)
+    k, v = tokens(2, 150)  # rows 0 and 1 grow past the others again: their stale slots show
+    pool.append(k.cuda(), v.cuda())
+    oracle.append(to_bits(k), to_bits(v))
+    sentinel = torch.full((B, H, cap, D), -7.0, dtype=torch.bfloat16, device="cuda")
+    for step, t in enumerate([1, 3, 1, 3, 1, 1]):
+        k, v = tokens(B, t)
+        oracle.append(to_bits(k), to_bits(v))
+        seq = oracle.get_seq_length()
+        if step % 2:
+            ko, vo = sentinel.clone(), sentinel.clone()
+            pool.update(k.cuda(), v.cuda(), cap, SEQ_FROM_DEVICE, out=(ko, vo))
+            compare_layer(pool, oracle, (ko[:, :, :seq], vo[:, :, :seq]), f"B{B} P{P} step {step} device extent")
+            untouched = to_bits(sentinel[:, :, seq:])
+            assert_bits_equal(ko[:, :, seq:], untouched, f"B{B} P{P} step {step} K past the longest row")
+            assert_bits_equal(vo[:, :, seq:], untouched, f"B{B} P{P} step {step} V past the longest row")
+        else:
+            got = pool.update(k.cuda(), v.cuda(), seq)
+            compare_layer(pool, oracle, got, f"B{B} P{P} step {step}")
+    compare_layer(pool, oracle, pool.gather(B, oracle.get_seq_length()), f"B{B} P{P} gather")
+    pool.check_invariants()
+    assert pool.errors() == 0
+
+
 def test_config3_ragged_random_pages(capi):
     """B=64, context lengths U{128..4096}, pages handed out in a seeded random permutation:
     a non-contiguous block table; 128 1-token append + gather steps, every one against the device
