@@ -784,9 +784,9 @@ __device__ __forceinline__ int lean_page(const barq_kv_pool& p, const NewBlocks&
   return -1;
 }
 
-// NU: vectors per copy thread (positions per tile / (4 / LPP)); tiles of one or two whole pages,
-// or (BAL) balanced chunks of at most one page.
-template <int NU, int LPP, bool BAL>
+// NU: vectors per copy thread (positions per tile / (4 / LPP)); tiles are whole pages, at most two.
+// (lean_balanced_kernel below takes launches whose one-page tiles are cut into equal chunks.)
+template <int NU, int LPP>
 __global__ void __launch_bounds__(kStreamThreads) lean_stream_kernel(const StreamArgs a) {
   using V = typename VecT<16>::T;
   constexpr int RSTEP = 4 / LPP;
@@ -810,8 +810,143 @@ __global__ void __launch_bounds__(kStreamThreads) lean_stream_kernel(const Strea
     return;
   }
 
-  // Copy waves.  Tile (K or V, row b, chunk c).  Page-aligned tiles: positions [c * chunk,
-  // + chunk), whole pages.  Balanced tiles: the row's positions up to its new end, [0, L) with
+  // Copy waves.  Tile (K or V, row b, chunk c): positions [c * chunk, + chunk), blocks blk0 and,
+  // for two-page tiles, blk0 + 1 (< max_blocks: the grid covers seq_out <= capacity).
+  const int len = p.seq_lens[b];
+  const int hw = p.high_water[b];
+  const int blk0 = c * a.ppt;
+  const int e0 = p.block_table[(int64_t)b * mb + blk0];
+  int e1 = -1;
+  if (a.ppt > 1 && blk0 + 1 < mb) e1 = p.block_table[(int64_t)b * mb + blk0 + 1];
+  const int lo = c * a.chunk;
+  int hi = lo + a.chunk;
+  if (hi > min(len + T, a.seq_out)) {
+    // Positions past this row's end: the output extent is the longest row (or seq_out).
+    int smax = a.seq_out;
+    if (a.seq_from_device) smax = min(wave_max(lane < a.batch ? p.seq_lens[lane] + T : 0), a.seq_out);
+    hi = min(hi, smax);
+  }
+  const NewBlocks nb = new_blocks(len, hw, T, mb, a.div_page);
+  const int nbl = a.ppt > 1 ? 2 : 1;
+  int base = 0, top = 0;
+  if (nb.count > 0 && blk0 < nb.first + nb.count && blk0 + nbl > nb.first) {
+    // The tile holds new blocks: their pages are ranked after the new blocks of rows [0, b).
+    top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
+    base = wave_sum(lane < b ? new_blocks(p.seq_lens[lane], p.high_water[lane], T, mb, a.div_page).count : 0);
+  }
+  int64_t pbs[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int blk = blk0 + k;
+    int page = -1;
+    if (k < nbl && blk < mb) {
+      if (blk < nb.first) {
+        page = checked_page(k == 0 ? e0 : e1, p.num_pages);
+      } else if (blk < nb.first + nb.count) {
+        const int idx = top - 1 - (base + blk - nb.first);
+        page = idx >= 0 ? checked_page(p.free_pages[idx], p.num_pages) : -1;
+      }
+    }
+    pbs[k] = page >= 0 ? (int64_t)page * a.page_bytes : (int64_t)-1;
+  }
+  const int64_t pb0 = pbs[0], pb1 = pbs[1];
+  if (committing) {
+    __builtin_amdgcn_s_waitcnt(0);  // the metadata loads have returned before the tile arrives
+    __syncthreads();
+  }
+  if (hi <= lo) return;
+
+  const int cw = wave - 1;
+  const int r0 = cw / LPP;
+  const int col = (cw % LPP) * kWave + lane;
+  const int h = (int)a.div_vr.div((uint32_t)col);
+  const int v = col - h * (int)a.div_vr.d;
+  const uint32_t page_lane = (uint32_t)(col * 16);
+  const uint32_t out_lane = (uint32_t)((int64_t)h * a.out_sh + (int64_t)v * 16);
+  const uint32_t in_lane = (uint32_t)((int64_t)h * a.in_sh + (int64_t)v * 16);
+  const uint32_t tokb = (uint32_t)a.tok_bytes;
+  const uint32_t oss = (uint32_t)a.out_ss;
+  const uint32_t ist = (uint32_t)a.in_st;
+  const char* in_row = (kv ? a.in_v : a.in_k) + (int64_t)b * a.in_sb;
+  char* out_row = (kv ? a.out_v : a.out_k) + (int64_t)b * a.out_sb;
+  char* pages = (char*)(kv ? p.value_pages : p.key_pages);
+  const int nval = hi - lo;
+  V val[NU];
+  if (hi <= max(hw, len + T) && pb0 >= 0 && (nval <= P || pb1 >= 0)) {
+    // Every position holds data on mapped pages: branch-free loads, back to back (positions past
+    // the tile repeat its last one, a cache hit).
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int j = min(r0 + u * RSTEP, nval - 1);
+      const int s = lo + j;
+      const bool second = j >= P;
+      const char* page_pos = pages + (second ? pb1 : pb0) + (uint32_t)(second ? j - P : j) * tokb;
+      const bool fresh = (unsigned)(s - len) < (unsigned)T;
+      val[u] = ld_stream<V>(fresh ? in_row + (uint32_t)(s - len) * ist + in_lane : page_pos + page_lane);
+    }
+  } else {
+    // Zero padding, unmapped blocks (an exhausted pool) or positions never written.
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int j = r0 + u * RSTEP;
+      const int s = lo + j;
+      val[u] = zero_vec<V>();
+      if (j < nval) {
+        const bool second = j >= P;
+        const int64_t pb = second ? pb1 : pb0;
+        if ((unsigned)(s - len) < (unsigned)T) {
+          val[u] = ld_stream<V>(in_row + (uint32_t)(s - len) * ist + in_lane);
+        } else if (s < hw && pb >= 0) {
+          val[u] = ld_stream<V>(pages + pb + (uint32_t)(second ? j - P : j) * tokb + page_lane);
+        }
+      }
+    }
+  }
+  wait_vm<0>();
+  // One store in flight per wave: a single-round launch drains HBM fastest that way.
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int j = r0 + u * RSTEP;
+    if (j < nval) {
+      const int s = lo + j;
+      wait_vm<0>();
+      st_stream<V>(out_row + (uint32_t)s * oss + out_lane, val[u]);
+      if ((unsigned)(s - len) < (unsigned)T) {
+        const bool second = j >= P;
+        const int64_t pb = second ? pb1 : pb0;
+        if (pb >= 0) *(V*)(pages + pb + (uint32_t)(second ? j - P : j) * tokb + page_lane) = val[u];
+      }
+    }
+  }
+}
+
+// Balanced lean tiles: lean_stream_kernel's work for chunks that start anywhere in a page.
+// NU: vectors per copy thread; a chunk holds at most one page of positions (NU * 4 / LPP).
+template <int NU, int LPP>
+__global__ void __launch_bounds__(kStreamThreads) lean_balanced_kernel(const StreamArgs a) {
+  using V = typename VecT<16>::T;
+  constexpr int RSTEP = 4 / LPP;
+  const barq_kv_pool& p = a.pool;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+  const int lane = (int)(threadIdx.x & (kWave - 1));
+  const int bid = (int)blockIdx.x;
+  const int kv = bid & 1;
+  const int rest = bid >> 1;
+  const int b = (int)a.div_chunks.div((uint32_t)rest);
+  const int c = rest - b * (int)a.div_chunks.d;
+  const int T = a.tokens;
+  const int P = (int)p.page_size;
+  const int mb = (int)p.max_blocks;
+  const bool committing = T > 0 && a.commit_in_kernel;
+
+  if (wave == 0) {
+    if (!committing) return;
+    __syncthreads();  // every copy wave of the tile holds the metadata it uses
+    arrive_and_commit(p, a.nsub, a.batch, T, a.seq_out, a.div_page);
+    return;
+  }
+
+  // Copy waves.  Tile (K or V, row b, chunk c): the row's positions up to its new end, [0, L) with
   // L = min(len + T, seq_out), cut into m = div_chunks.d equal chunks (ceil(L / m) positions,
   // at most a tile's NU * 4 / LPP), so that every tile of the launch -- and every CU, the grid
   // being a multiple of the CU count -- moves the same bytes whatever the context.  The output
@@ -823,21 +958,7 @@ __global__ void __launch_bounds__(kStreamThreads) lean_stream_kernel(const Strea
   const int hw = p.high_water[b];
   const int64_t trow = (int64_t)b * mb;
   int lo, hi, xlo = 0, xhi = 0, blk0, off = 0, nbl, e0 = -1, e1 = -1;
-  if constexpr (!BAL) {
-    // the block-table entries load with the row's length
-    blk0 = c * a.ppt;
-    nbl = a.ppt > 1 ? 2 : 1;
-    e0 = p.block_table[trow + blk0];
-    if (nbl > 1 && blk0 + 1 < mb) e1 = p.block_table[trow + blk0 + 1];
-    lo = c * a.chunk;
-    hi = lo + a.chunk;
-    if (hi > min(len + T, a.seq_out)) {
-      // Positions past this row's end: the output extent is the longest row (or seq_out).
-      int smax = a.seq_out;
-      if (a.seq_from_device) smax = min(wave_max(lane < a.batch ? p.seq_lens[lane] + T : 0), a.seq_out);
-      hi = min(hi, smax);
-    }
-  } else {
+  {
     const int m = (int)a.div_chunks.d;
     const int L = min(len + T, a.seq_out);
     const int q = (int)a.div_chunks.div((uint32_t)(L + m - 1));
@@ -944,7 +1065,6 @@ __global__ void __launch_bounds__(kStreamThreads) lean_stream_kernel(const Strea
   // Balanced tiles: output positions [xlo, xhi) past the row's new end (no new tokens there):
   // stale data below the mark on the pages the table maps (blocks below the mark are old ones,
   // which the commit does not remap), else zeros.
-  if constexpr (!BAL) return;
   for (int s0 = xlo; s0 < xhi; s0 += NU * RSTEP) {
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
@@ -1632,11 +1752,12 @@ int launch_stream_kernel(int vb, int lpp, bool rounds, dim3 grid, StreamArgs* ar
 
 template <bool BAL>
 int launch_lean_kernel(int nu, int lpp, dim3 grid, StreamArgs* arg, hipStream_t stream) {
-#define BARQ_LEAN_CASE(NU)                                                                                    \
-    switch (lpp) {                                                                                             \
-      case 1: return launch((const void*)&lean_stream_kernel<NU, 1, BAL>, grid, arg, stream, kStreamThreads);  \
-      case 2: return launch((const void*)&lean_stream_kernel<NU, 2, BAL>, grid, arg, stream, kStreamThreads);  \
-      default: return launch((const void*)&lean_stream_kernel<NU, 4, BAL>, grid, arg, stream, kStreamThreads); \
+#define BARQ_LEAN_FN(NU, L) (BAL ? (const void*)&lean_balanced_kernel<NU, L> : (const void*)&lean_stream_kernel<NU, L>)
+#define BARQ_LEAN_CASE(NU)                                                                 \
+    switch (lpp) {                                                                          \
+      case 1: return launch(BARQ_LEAN_FN(NU, 1), grid, arg, stream, kStreamThreads);        \
+      case 2: return launch(BARQ_LEAN_FN(NU, 2), grid, arg, stream, kStreamThreads);        \
+      default: return launch(BARQ_LEAN_FN(NU, 4), grid, arg, stream, kStreamThreads);       \
     }
   switch (nu) {
     case 4: BARQ_LEAN_CASE(4)
@@ -1644,6 +1765,7 @@ int launch_lean_kernel(int nu, int lpp, dim3 grid, StreamArgs* arg, hipStream_t 
     default: BARQ_LEAN_CASE(16)
   }
 #undef BARQ_LEAN_CASE
+#undef BARQ_LEAN_FN
 }
 
 BARQ_DEFINE_VB_LAUNCH(dense_append_kernel, DenseArgs)

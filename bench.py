@@ -83,9 +83,10 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "paged KV append+gather GB/s (% HBM peak); µs per decode-step cache update"
-KERNEL = ("stream kernel, fused append + gather, one launch per layer: lean_stream_kernel<8, 2> (1-page tiles) "
-          "while every 1-page tile fits on the CUs at once, lean_stream_kernel<16, 2> (2-page tiles) while those do, "
-          "else stream_kernel_rounds<16, 2> (several dispatch rounds, as at C3-C5)")
+KERNEL = ("stream kernel, fused append + gather, one launch per layer: lean_stream_kernel<8, 2> (1-page tiles; "
+          "lean_balanced_kernel<8, 2>, equal unaligned chunks, when their count is not a multiple of the CUs) while "
+          "every 1-page tile fits on the CUs at once, lean_stream_kernel<16, 2> (2-page tiles) while those do, else "
+          "stream_kernel_rounds<16, 2> (several dispatch rounds, as at C3-C5)")
 
 # prefill: ("uniform", n) | ("ragged", lo, hi, seed) | ("chunks", count, size)
 CONFIGS = {
