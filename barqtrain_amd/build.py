@@ -26,7 +26,7 @@ LIB_NAME = "libbarq_kv.so"
 EXT_NAME = "barqtrain_cuda"
 OFFLOAD_ARCH = "gfx950"
 HIP_SOURCES = ("barq_kv.hip", "barq_kv_attention.hip", "barq_kv_quant.hip")
-HIP_HEADERS = ("fastdiv.h", "barq_kv_fp8.h")
+HIP_HEADERS = ("fastdiv.h", "barq_kv_fp8.h", "barq_kv_commit.h")
 HOST_SOURCES = ("barq_kv_torch.cpp",)
 
 

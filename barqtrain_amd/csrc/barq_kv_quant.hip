@@ -17,6 +17,7 @@
 #include <climits>
 
 #include "barq_kv.h"
+#include "barq_kv_commit.h"
 #include "barq_kv_fp8.h"
 #include "fastdiv.h"
 
@@ -95,6 +96,7 @@ struct CompressArgs {
   barq_kv_pool p;
   ColdPtrs c;
   int32_t batch;
+  int32_t ahead;       // tokens the rows are about to receive: quantise for lengths + ahead
   FastDiv div_page;
   FastDiv div_dim;     // head_dim
   FastDiv div_groups;  // kv_heads * head_dim / VE vectors per token
@@ -220,10 +222,10 @@ __global__ void __launch_bounds__(kThreads) compress_kernel(const CompressArgs a
   const barq_kv_pool& p = a.p;
   const int r = blockIdx.x;
   const int mb = (int)p.max_blocks;
-  const int len = p.seq_lens[r];
+  const int len = p.seq_lens[r] + a.ahead;
   const int old_len = len - a.c.window;
   const int jmax = min(old_len > 0 ? (int)a.div_page.div((uint32_t)old_len) : 0,
-                       min(ceil_div_fd(p.high_water[r], a.div_page), mb));
+                       min(ceil_div_fd(max(p.high_water[r], len), a.div_page), mb));
   int32_t* row = p.block_table + (int64_t)r * mb;
   int err = 0;
   for (int j0 = 0; j0 < jmax; j0 += kThreads) {
@@ -375,10 +377,10 @@ __global__ void __launch_bounds__(kThreads) compress_regs_kernel(const CompressA
   const int r = blockIdx.x;
   const int mb = (int)p.max_blocks;
   const int C = (int)(p.kv_heads * p.head_dim);
-  const int len = p.seq_lens[r];
+  const int len = p.seq_lens[r] + a.ahead;
   const int old_len = len - a.c.window;
   const int jmax = min(old_len > 0 ? (int)a.div_page.div((uint32_t)old_len) : 0,
-                       min(ceil_div_fd(p.high_water[r], a.div_page), mb));
+                       min(ceil_div_fd(max(p.high_water[r], len), a.div_page), mb));
   int32_t* row = p.block_table + (int64_t)r * mb;
   int err = 0;
   for (int j0 = 0; j0 < jmax; j0 += kThreads) {
@@ -779,6 +781,183 @@ __global__ void __launch_bounds__(kGatherThreads) gather_cold_lanes_kernel(const
   }
 }
 
+// The dequantising update in one launch, for tokens <= window (the blocks that leave the window
+// were quantised just before, from the lengths the rows are about to reach): the tiles of
+// gather_cold_lanes_kernel, whose rows also receive `tokens` new positions.  Every tile reads
+// the launch's starting state -- the row's length and mark, its block's entry, the output extent
+// (longest row + tokens), and for a block the append maps first the page its rank takes from the
+// stack -- then arrives; the last tile to arrive commits the append (barq_commit, as the stream
+// kernels do).  New positions are taken from the input, written to the output and to their hot
+// page; a tile holding none runs gather_cold_lanes_kernel's copy or decode unchanged.
+struct UpdateArgs {
+  GatherArgs g;
+  const char* in[2];      // key, value states
+  int64_t isb, ish, ist;  // input strides, elements
+  int32_t tokens;
+  int32_t nsub;           // arrival sub-counters in use
+  FastDiv div_page;
+};
+
+template <int KIND, int LPP>
+__global__ void __launch_bounds__(kGatherThreads) update_cold_lanes_kernel(const UpdateArgs u) {
+  using V = Vec<KIND, 8>;
+  using E = Elem<KIND>;
+  using Bits = typename E::Bits;
+  constexpr int kNPos = 8 / LPP;  // positions a wave moves per round
+  constexpr int kWavesPerTile = kGatherThreads / kWave;
+  const GatherArgs& a = u.g;
+  const barq_kv_pool& p = a.p;
+  const int kv = blockIdx.x & 1;
+  const int bj = blockIdx.x >> 1;
+  const int b = (int)a.div_nblk.div((uint32_t)bj);
+  const int j = bj - b * a.nblk;
+  const int P = (int)p.page_size, H = (int)p.kv_heads, D = (int)p.head_dim;
+  const int T = u.tokens;
+  const int mb = (int)p.max_blocks;
+  const int pos0 = j * P;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+
+  // The launch's starting state (batch <= 64: one row per lane).
+  const int len = p.seq_lens[b];
+  const int hw = p.high_water[b];
+  const int stored = p.block_table[(int64_t)b * mb + j];
+  int S = a.seq_out;
+  if (a.from_device) S = min(barq_commit::wave_max(lane < a.batch ? p.seq_lens[lane] + T : 0), a.seq_out);
+  const barq_commit::NewBlocks nb = barq_commit::new_blocks(len, hw, T, mb, u.div_page);
+  const bool fresh_block = j >= nb.first && j < nb.first + nb.count;
+  int newpage = -1;
+  if (fresh_block) {
+    const int top = p.ctrl[BARQ_KV_CTRL_FREE_TOP];
+    const int base = barq_commit::wave_sum(
+        lane < b ? barq_commit::new_blocks(p.seq_lens[lane], p.high_water[lane], T, mb, u.div_page).count : 0);
+    const int idx = top - 1 - (base + j - nb.first);
+    newpage = idx >= 0 ? checked_id(p.free_pages[idx], p.num_pages) : -1;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // every wave holds its metadata before the tile arrives
+  __syncthreads();
+  if (wave == 0) barq_commit::arrive_and_commit(p, u.nsub, a.batch, T, a.seq_out, u.div_page);
+  if (pos0 >= S) return;  // uniform
+
+  const bool old_block = pos0 < hw;  // mapped before this append
+  const int entry = old_block ? stored : -1;
+  const int hot = old_block ? checked_id(entry, p.num_pages) : newpage;
+  const int cold = entry <= -2 ? checked_id(-2 - entry, a.c.num_cold) : -1;
+  if (entry <= -2 && cold < 0 && threadIdx.x == 0) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], BARQ_KV_ERRBIT_BAD_INDEX);
+  const int live = min(S, hw) - pos0;  // old data: positions below the mark
+  const int end = min(S - pos0, P);
+  const int f_lo = len - pos0;         // new positions of the tile: [f_lo, f_lo + T) within [0, end)
+  const bool fresh_tile = f_lo < end && f_lo + T > 0;
+  const int HD = H * D;
+  const int dvn = D / 8;
+  int col[LPP];
+  int64_t ocol[LPP], icol[LPP];
+#pragma unroll
+  for (int c = 0; c < LPP; ++c) {
+    const int vi = c * kWave + lane;
+    const int h = vi / dvn;
+    col[c] = vi * 8;
+    ocol[c] = (int64_t)h * a.osh + (int64_t)(vi - h * dvn) * 8;
+    icol[c] = (int64_t)h * u.ish + (int64_t)(vi - h * dvn) * 8;
+  }
+  Bits* out = (Bits*)a.out[kv] + (int64_t)b * a.osb + (int64_t)pos0 * a.oss;
+  char* page_base = hot >= 0 ? (kv ? (char*)p.value_pages : (char*)p.key_pages) +
+                                   (int64_t)hot * P * HD * (int64_t)sizeof(Bits)
+                             : nullptr;
+  if (fresh_tile) {
+    // New positions from the input (to the output and their page), old ones from the hot page.
+    const Bits* in = (const Bits*)u.in[kv] + (int64_t)b * u.isb;
+    if (cold >= 0 && threadIdx.x == 0) atomicOr(&p.ctrl[BARQ_KV_CTRL_ERRORS], BARQ_KV_ERRBIT_BAD_INDEX);
+    for (int t0 = wave * kNPos; t0 < end; t0 += kWavesPerTile * kNPos) {
+      typename V::OutU val[kNPos][LPP];
+#pragma unroll
+      for (int i = 0; i < kNPos; ++i) {
+        const int t = t0 + i;
+        const bool fresh = (unsigned)(t - f_lo) < (unsigned)T;
+#pragma unroll
+        for (int c = 0; c < LPP; ++c) {
+          val[i][c].v = typename V::Out(0);
+          if (t < end && fresh)
+            val[i][c].v = __builtin_nontemporal_load(
+                (const typename V::Out*)(in + (int64_t)(t - f_lo) * u.ist + icol[c]));
+          else if (t < live && hot >= 0)
+            val[i][c].v = __builtin_nontemporal_load(
+                (const typename V::Out*)(page_base + ((int64_t)t * HD + col[c]) * (int64_t)sizeof(Bits)));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kNPos; ++i) {
+        const int t = t0 + i;
+        if (t >= end) continue;
+        const bool fresh = (unsigned)(t - f_lo) < (unsigned)T;
+#pragma unroll
+        for (int c = 0; c < LPP; ++c) {
+          __builtin_nontemporal_store(val[i][c].v, (typename V::Out*)(out + (int64_t)t * a.oss + ocol[c]));
+          if (fresh && hot >= 0)
+            *(typename V::Out*)(page_base + ((int64_t)t * HD + col[c]) * (int64_t)sizeof(Bits)) = val[i][c].v;
+        }
+      }
+    }
+    return;
+  }
+  typename V::CodeU ksc[LPP];
+  if (cold >= 0 && kv == 0) {
+#pragma unroll
+    for (int c = 0; c < LPP; ++c) ksc[c].v = *(const typename V::Codes*)(a.c.key_scales + (int64_t)cold * HD + col[c]);
+  }
+  for (int t0 = wave * kNPos; t0 < end; t0 += kWavesPerTile * kNPos) {
+    Bits* o = out + (int64_t)t0 * a.oss;
+    if (hot >= 0) {  // uniform: a copy, every load of the round in flight before the stores
+      const char* base = page_base + (int64_t)t0 * HD * (int64_t)sizeof(Bits);
+      typename V::OutU val[kNPos][LPP];
+#pragma unroll
+      for (int i = 0; i < kNPos; ++i)
+#pragma unroll
+        for (int c = 0; c < LPP; ++c) {
+          val[i][c].v = typename V::Out(0);
+          if (t0 + i < live)
+            val[i][c].v = __builtin_nontemporal_load(
+                (const typename V::Out*)(base + ((int64_t)i * HD + col[c]) * (int64_t)sizeof(Bits)));
+        }
+#pragma unroll
+      for (int i = 0; i < kNPos; ++i)
+#pragma unroll
+        for (int c = 0; c < LPP; ++c)
+          if (t0 + i < end) __builtin_nontemporal_store(val[i][c].v, (typename V::Out*)(o + (int64_t)i * a.oss + ocol[c]));
+    } else if (cold >= 0) {  // uniform: codes and scales of the round in flight, then decode + store
+      const uint8_t* codes = a.c.codes[kv] + ((int64_t)cold * P + t0) * HD;
+      typename V::CodeU cv[kNPos][LPP];
+      uint32_t vsc[kNPos][LPP];
+#pragma unroll
+      for (int i = 0; i < kNPos; ++i)
+#pragma unroll
+        for (int c = 0; c < LPP; ++c) {
+          cv[i][c].v = typename V::Codes(0);
+          vsc[i][c] = 0;
+          if (t0 + i < live) {
+            cv[i][c].v = __builtin_nontemporal_load((const typename V::Codes*)(codes + (int64_t)i * HD + col[c]));
+            if (kv) vsc[i][c] = a.c.value_scales[((int64_t)cold * P + t0 + i) * H + (c * kWave + lane) / dvn];
+          }
+        }
+#pragma unroll
+      for (int i = 0; i < kNPos; ++i)
+#pragma unroll
+        for (int c = 0; c < LPP; ++c) {
+          if (t0 + i >= end) continue;
+          const typename V::Out v =
+              t0 + i < live ? dequant_vec<KIND, 8>(cv[i][c], ksc[c], vsc[i][c], kv) : typename V::Out(0);
+          __builtin_nontemporal_store(v, (typename V::Out*)(o + (int64_t)i * a.oss + ocol[c]));
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kNPos; ++i)
+#pragma unroll
+        for (int c = 0; c < LPP; ++c)
+          if (t0 + i < end) __builtin_nontemporal_store(typename V::Out(0), (typename V::Out*)(o + (int64_t)i * a.oss + ocol[c]));
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Row release with a cold store: one workgroup, a row at a time; hot pages (shares-aware) go back
 // to free_pages, cold pages to free_cold, each in (row, block) order.
@@ -1065,13 +1244,20 @@ int barq_kv_cold_reset(const barq_kv_pool* pool, const barq_kv_cold* cold, void*
   return hipGetLastError() == hipSuccess ? BARQ_KV_OK : BARQ_KV_ERR_LAUNCH;
 }
 
-int barq_kv_compress(const barq_kv_pool* pool, const barq_kv_cold* cold, int64_t batch, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// barq_kv_compress for the lengths the rows [0, batch) will have after `ahead` more tokens.
+int compress_launch(const barq_kv_pool* pool, const barq_kv_cold* cold, int64_t batch, int64_t ahead,
+                    void* stream) {
   if (!cold_ok(pool, cold) || batch < 0 || batch > pool->max_batch) return BARQ_KV_ERR_INVALID;
   if (batch == 0) return BARQ_KV_OK;
   CompressArgs a;
   a.p = *pool;
   a.c = cold_ptrs(cold);
   a.batch = (int32_t)batch;
+  a.ahead = (int32_t)ahead;
   a.div_page = FastDiv::make((uint32_t)pool->page_size);
   a.div_dim = FastDiv::make((uint32_t)pool->head_dim);
   // widest vector along head_dim that every page row, code row and scale row admits
@@ -1084,6 +1270,83 @@ int barq_kv_compress(const barq_kv_pool* pool, const barq_kv_cold* cold, int64_t
   a.div_groups = FastDiv::make((uint32_t)(pool->kv_heads * D / ve));
   const void* fn = compress_regs_fn(pool, cold->element_type, ve);
   return launch(fn ? fn : compress_fn(cold->element_type, ve), dim3((uint32_t)batch), &a, (hipStream_t)stream);
+}
+
+// The update in two launches -- compress for the lengths the rows reach, then
+// update_cold_lanes_kernel -- when it applies: tokens in [1, window], batch <= 64, two-byte
+// elements whose token rows are 64, 128 or 256 vectors of 16 bytes, every address and stride
+// 16-byte aligned (codes and key scales 8-byte), the output reaching the new tokens.  Returns -1
+// (nothing launched) when it does not.
+int update_cold_fused(const barq_kv_pool* pool, const barq_kv_cold* cold, const void* ks, const void* vs,
+                      int64_t batch, int64_t tokens, int64_t sb, int64_t sh, int64_t st, void* ko, void* vo,
+                      int64_t seq_out, int64_t osb, int64_t osh, int64_t oss, int64_t flags, void* stream) {
+  if (!cold_ok(pool, cold) || pool->elem_bytes != 2 || cold->element_type == BARQ_KV_FP32) return -1;
+  if (batch < 1 || batch > kWave || batch > pool->max_batch || tokens < 1 || tokens > cold->window) return -1;
+  const int64_t P = pool->page_size, H = pool->kv_heads, D = pool->head_dim;
+  const int64_t cap = pool->max_blocks * P;
+  if (seq_out < tokens || seq_out > cap) return -1;
+  if (!ks || !vs || !ko || !vo || sb < 0 || sh < 0 || st < 0 || osb < 0 || osh < 0 || oss < 0) return -1;
+  const uint64_t bits = (uint64_t)(uintptr_t)ko | (uint64_t)(uintptr_t)vo | (uint64_t)(osb * 2) |
+                        (uint64_t)(osh * 2) | (uint64_t)(oss * 2) | (uint64_t)(D * 2) |
+                        (uint64_t)(uintptr_t)pool->key_pages | (uint64_t)(uintptr_t)pool->value_pages |
+                        (uint64_t)(uintptr_t)ks | (uint64_t)(uintptr_t)vs | (uint64_t)(sb * 2) |
+                        (uint64_t)(sh * 2) | (uint64_t)(st * 2);
+  const uint64_t code_bits = (uint64_t)(uintptr_t)cold->key_codes | (uint64_t)(uintptr_t)cold->value_codes |
+                             (uint64_t)(uintptr_t)cold->key_scales | (uint64_t)D;
+  if ((bits & 15) || (code_bits & 7)) return -1;
+  const int64_t hd8 = H * D / 8;
+  if (D % 8 != 0 || hd8 % kWave != 0 || (hd8 / kWave != 1 && hd8 / kWave != 2 && hd8 / kWave != 4) ||
+      P * H * D > kI32Max)
+    return -1;
+  const int lpp = (int)(hd8 / kWave);
+  if (!(flags & BARQ_KV_NO_COMPRESS)) {
+    const int rc = compress_launch(pool, cold, batch, tokens, stream);
+    if (rc != BARQ_KV_OK) return rc;
+  }
+  UpdateArgs u;
+  GatherArgs& a = u.g;
+  a.p = *pool;
+  a.c = cold_ptrs(cold);
+  a.out[0] = (char*)ko;
+  a.out[1] = (char*)vo;
+  a.osb = osb;
+  a.osh = osh;
+  a.oss = oss;
+  a.batch = (int32_t)batch;
+  a.seq_out = (int32_t)seq_out;
+  a.nblk = (int32_t)((seq_out + P - 1) / P);
+  a.from_device = (flags & BARQ_KV_SEQ_FROM_DEVICE) ? 1 : 0;
+  a.div_head = FastDiv::make((uint32_t)(P * (D / 8)));
+  a.div_dv = FastDiv::make((uint32_t)(D / 8));
+  a.div_nblk = FastDiv::make((uint32_t)a.nblk);
+  u.in[0] = (const char*)ks;
+  u.in[1] = (const char*)vs;
+  u.isb = sb;
+  u.ish = sh;
+  u.ist = st;
+  u.tokens = (int32_t)tokens;
+  const int64_t tiles = batch * a.nblk * 2;
+  u.nsub = (int32_t)std::min<int64_t>(tiles, BARQ_KV_CTRL_SUBCOUNTERS);
+  u.div_page = FastDiv::make((uint32_t)P);
+  const bool f16 = cold->element_type == BARQ_KV_FP16;
+  const void* fn = lpp == 1   ? (f16 ? (const void*)&update_cold_lanes_kernel<BARQ_KV_FP16, 1>
+                                     : (const void*)&update_cold_lanes_kernel<BARQ_KV_BF16, 1>)
+                   : lpp == 2 ? (f16 ? (const void*)&update_cold_lanes_kernel<BARQ_KV_FP16, 2>
+                                     : (const void*)&update_cold_lanes_kernel<BARQ_KV_BF16, 2>)
+                              : (f16 ? (const void*)&update_cold_lanes_kernel<BARQ_KV_FP16, 4>
+                                     : (const void*)&update_cold_lanes_kernel<BARQ_KV_BF16, 4>);
+  void* args[] = {&u};
+  return hipLaunchKernel(fn, dim3((uint32_t)tiles), dim3(kGatherThreads), args, 0, (hipStream_t)stream) == hipSuccess
+             ? BARQ_KV_OK
+             : BARQ_KV_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" {
+
+int barq_kv_compress(const barq_kv_pool* pool, const barq_kv_cold* cold, int64_t batch, void* stream) {
+  return compress_launch(pool, cold, batch, 0, stream);
 }
 
 int barq_kv_gather_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, void* key_out,
@@ -1142,6 +1405,9 @@ int barq_kv_update_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, cons
                         void* stream) {
   if (!cold_ok(pool, cold)) return BARQ_KV_ERR_INVALID;
   if (flags & ~(int64_t)(BARQ_KV_SEQ_FROM_DEVICE | BARQ_KV_NO_COMPRESS)) return BARQ_KV_ERR_INVALID;
+  const int fused = update_cold_fused(pool, cold, key_states, value_states, batch, tokens, stride_b, stride_h,
+                                      stride_t, key_out, value_out, seq_out, osb, osh, oss, flags, stream);
+  if (fused >= 0) return fused;
   int rc = barq_kv_append(pool, key_states, value_states, batch, tokens, stride_b, stride_h, stride_t, stream);
   if (rc == BARQ_KV_OK && !(flags & BARQ_KV_NO_COMPRESS)) rc = barq_kv_compress(pool, cold, batch, stream);
   if (rc == BARQ_KV_OK)

@@ -350,9 +350,15 @@ int barq_kv_gather_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, void
                         void* value_out, int64_t batch, int64_t seq_out, int64_t out_stride_b,
                         int64_t out_stride_h, int64_t out_stride_s, int64_t flags, void* stream);
 
-/* barq_kv_append + barq_kv_compress + barq_kv_gather_cold (three launches).  flags:
- * BARQ_KV_SEQ_FROM_DEVICE as for the gather; BARQ_KV_NO_COMPRESS skips the compress launch -- for
- * a caller that knows no row's block leaves the window in this call (every page_size-th token). */
+/* barq_kv_append + barq_kv_compress + barq_kv_gather_cold.  When tokens <= window, batch <= 64
+ * and the pool holds two-byte elements whose token rows are 64, 128 or 256 vectors of 16 bytes
+ * (every address and stride 16-byte aligned, codes and key scales 8-byte), in two launches: the
+ * compress for the lengths the rows reach, then one launch that appends and gathers -- as for
+ * barq_kv_update, a row whose new end passes seq_out loses the tokens past it and raises
+ * BARQ_KV_ERRBIT_OUT_SHORT; else in three launches.  The results are the same either way.
+ * flags: BARQ_KV_SEQ_FROM_DEVICE as for the gather; BARQ_KV_NO_COMPRESS skips the compress launch
+ * -- for a caller that knows no row's block leaves the window in this call (every page_size-th
+ * token). */
 #define BARQ_KV_NO_COMPRESS 4
 int barq_kv_update_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, const void* key_states,
                         const void* value_states, int64_t batch, int64_t tokens, int64_t stride_b,

@@ -35,6 +35,9 @@ CASES = [
     (torch.float32, 1, 12, 5, 0),
     (torch.bfloat16, 8, 128, 16, 32),
     (torch.bfloat16, 2, 6, 1, 3),   # 2-element vectors, one-token pages
+    # the one-launch update (tokens <= window, token rows of 64 / 128 16-byte vectors)
+    (torch.float16, 8, 128, 32, 48),
+    (torch.bfloat16, 4, 128, 16, 16),
 ]
 
 
