@@ -69,6 +69,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* lds, int* total)
 using barq_fp8::codes_normal;
 using barq_fp8::e4m3_decode;
 using barq_fp8::e4m3_encode;
+using barq_fp8::e4m3_encode4;
 using barq_fp8::Elem;
 using barq_fp8::fast_pair;
 using barq_fp8::finite_abs;
@@ -202,10 +203,23 @@ __device__ void quantise_page(const CompressArgs& a, int hp, int cp, int8_t* s_k
     Lanes<KIND, VE>::load(vp + at, xv);
     const int ve = s_vexp[th];
     typename CodeVec<VE>::U ck, cv;
+    if constexpr (VE % 4 == 0) {
+      uint32_t wk[VE / 4], wv[VE / 4];
 #pragma unroll
-    for (int e = 0; e < VE; ++e) {
-      ck.b[e] = (uint8_t)e4m3_encode(ldexpf(xk[e], -(int)s_kexp[ch + e]));
-      cv.b[e] = (uint8_t)e4m3_encode(ldexpf(xv[e], -ve));
+      for (int q = 0; q < VE / 4; ++q) {
+        const int e = 4 * q;
+        wk[q] = e4m3_encode4(ldexpf(xk[e], -(int)s_kexp[ch + e]), ldexpf(xk[e + 1], -(int)s_kexp[ch + e + 1]),
+                             ldexpf(xk[e + 2], -(int)s_kexp[ch + e + 2]), ldexpf(xk[e + 3], -(int)s_kexp[ch + e + 3]));
+        wv[q] = e4m3_encode4(ldexpf(xv[e], -ve), ldexpf(xv[e + 1], -ve), ldexpf(xv[e + 2], -ve), ldexpf(xv[e + 3], -ve));
+      }
+      __builtin_memcpy(ck.b, wk, VE);
+      __builtin_memcpy(cv.b, wv, VE);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VE; ++e) {
+        ck.b[e] = (uint8_t)e4m3_encode(ldexpf(xk[e], -(int)s_kexp[ch + e]));
+        cv.b[e] = (uint8_t)e4m3_encode(ldexpf(xv[e], -ve));
+      }
     }
     *(typename CodeVec<VE>::Raw*)(kc + at) = ck.v;
     *(typename CodeVec<VE>::Raw*)(vc + at) = cv.v;
@@ -352,11 +366,18 @@ __device__ void quantise_regs(const CompressArgs& a, const PageRegs<KIND, NV>& p
     const int ve = group_exponent(mv);
     if (g % VD == 0) a.c.value_scales[((int64_t)cp * P + tok) * H + h] = (uint8_t)(ve + 127);
     typename CodeVec<8>::U ck, cv;
+    uint32_t wk[2], wv[2];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      ck.b[e] = (uint8_t)e4m3_encode(ldexpf(Regs::elem(pg.k[i], e), -kex[e]));
-      cv.b[e] = (uint8_t)e4m3_encode(ldexpf(Regs::elem(pg.v[i], e), -ve));
+    for (int q = 0; q < 2; ++q) {
+      const int e = 4 * q;
+      wk[q] = e4m3_encode4(ldexpf(Regs::elem(pg.k[i], e), -kex[e]), ldexpf(Regs::elem(pg.k[i], e + 1), -kex[e + 1]),
+                           ldexpf(Regs::elem(pg.k[i], e + 2), -kex[e + 2]),
+                           ldexpf(Regs::elem(pg.k[i], e + 3), -kex[e + 3]));
+      wv[q] = e4m3_encode4(ldexpf(Regs::elem(pg.v[i], e), -ve), ldexpf(Regs::elem(pg.v[i], e + 1), -ve),
+                           ldexpf(Regs::elem(pg.v[i], e + 2), -ve), ldexpf(Regs::elem(pg.v[i], e + 3), -ve));
     }
+    __builtin_memcpy(ck.b, wk, 8);
+    __builtin_memcpy(cv.b, wv, 8);
     const int64_t at = (int64_t)tok * C + g * 8;
     *(typename CodeVec<8>::Raw*)(kc + at) = ck.v;
     *(typename CodeVec<8>::Raw*)(vc + at) = cv.v;
