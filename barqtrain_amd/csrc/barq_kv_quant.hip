@@ -843,8 +843,12 @@ __global__ void __launch_bounds__(kGatherThreads) update_cold_lanes_kernel(const
   const int len = p.seq_lens[b];
   const int hw = p.high_water[b];
   const int stored = p.block_table[(int64_t)b * mb + j];
+  // The extent (longest row + tokens) matters only to a block reaching past its row's new end:
+  // the others hold data at every position and skip the batch-wide read (every tile reading the
+  // same lengths serialises on one L2 channel).
   int S = a.seq_out;
-  if (a.from_device) S = min(barq_commit::wave_max(lane < a.batch ? p.seq_lens[lane] + T : 0), a.seq_out);
+  if (a.from_device && pos0 + P > len + T)
+    S = min(barq_commit::wave_max(lane < a.batch ? p.seq_lens[lane] + T : 0), a.seq_out);
   const barq_commit::NewBlocks nb = barq_commit::new_blocks(len, hw, T, mb, u.div_page);
   const bool fresh_block = j >= nb.first && j < nb.first + nb.count;
   int newpage = -1;
