@@ -614,7 +614,10 @@ __global__ void __launch_bounds__(kGatherThreads) gather_cold_kernel(const Gathe
   // The row's mark and the block's entry are read together with the lengths (one round trip).
   const int hw = p.high_water[b];
   const int stored = p.block_table[(int64_t)b * p.max_blocks + j];
-  if (a.from_device) {
+  // The extent (longest row) matters only to a block reaching past its row's length: the others
+  // hold data at every position and skip the batch-wide read.
+  const bool need_extent = a.from_device && pos0 + P > p.seq_lens[b];
+  if (need_extent) {  // uniform
     if (threadIdx.x < kWave) {
       int m = 0;
       for (int i = threadIdx.x; i < a.batch; i += kWave) m = max(m, p.seq_lens[i]);
@@ -624,7 +627,7 @@ __global__ void __launch_bounds__(kGatherThreads) gather_cold_kernel(const Gathe
     }
     __syncthreads();
   }
-  const int S = a.from_device ? s_seq : a.seq_out;
+  const int S = need_extent ? s_seq : a.seq_out;
   if (pos0 >= S) return;  // uniform
   const int entry = pos0 < hw ? stored : -1;
   const int hot = checked_id(entry, p.num_pages);
@@ -710,7 +713,10 @@ __global__ void __launch_bounds__(kGatherThreads) gather_cold_lanes_kernel(const
   const int pos0 = j * P;
   const int hw = p.high_water[b];
   const int stored = p.block_table[(int64_t)b * p.max_blocks + j];
-  if (a.from_device) {
+  // The extent (longest row) matters only to a block reaching past its row's length: the others
+  // hold data at every position and skip the batch-wide read.
+  const bool need_extent = a.from_device && pos0 + P > p.seq_lens[b];
+  if (need_extent) {  // uniform
     if (threadIdx.x < kWave) {
       int m = 0;
       for (int i = threadIdx.x; i < a.batch; i += kWave) m = max(m, p.seq_lens[i]);
@@ -720,7 +726,7 @@ __global__ void __launch_bounds__(kGatherThreads) gather_cold_lanes_kernel(const
     }
     __syncthreads();
   }
-  const int S = a.from_device ? s_seq : a.seq_out;
+  const int S = need_extent ? s_seq : a.seq_out;
   if (pos0 >= S) return;  // uniform
   const int entry = pos0 < hw ? stored : -1;
   const int hot = checked_id(entry, p.num_pages);
