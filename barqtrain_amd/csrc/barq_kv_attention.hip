@@ -55,6 +55,9 @@ constexpr int kTableEntries = kTableRegs * 64;
 constexpr int kMaxBatch = 1024;            // rows whose lengths the schedule stages in LDS
 constexpr int kMaxWaves = 2048;            // resident waves of an MI355X: 256 CUs x 4 SIMDs x 2
 constexpr int kMinRangeChunks = 4;         // the automatic range never goes below 64 positions
+constexpr int kPairWaves = 8;              // waves of a pair-kernel workgroup
+constexpr int64_t kPairMinPairs = 128;     // the pair kernel from this many (row, kv head) pairs ...
+constexpr int64_t kPairMaxChunks = 64;     // ... of at most this many 16-position chunks (max_seq)
 
 enum : int { kBF16 = 0, kF16 = 1 };
 
@@ -534,12 +537,12 @@ __device__ __forceinline__ void v_operand(const u32x4 x, float (&f)[8]) {
 template <int HD, int E, int R, bool UNIFORM, typename OutT, bool COLD>
 __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
                              u32x4 (&lq)[Head<HD>::kSteps][kWave], int b, int kvh, int len, int t_begin,
-                             int t_end, bool whole, int64_t rec_id) {
+                             int t_end, bool whole, float* pr) {
   constexpr int kSteps = Head<HD>::kSteps;
   constexpr int kVLanes = Head<HD>::kVLanes;
   constexpr int kVPos = Head<HD>::kVPos;
   constexpr int kVLoads = Head<HD>::kVLoads;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
   const int n16 = lane & 15;
   const int g = lane >> 4;
   const int vpos = lane / kVLanes;  // V: position slot and 8-dim group of this lane
@@ -708,9 +711,7 @@ chunks_done:
         acc[r2][e][m] = v;
       }
   // Lanes 0 .. HD / 8 - 1 now hold dims 8 * lane .. +7 of every row; lanes 16g .. 16g+15 hold
-  // the maxima and sums of rows 4g .. 4g+3.
-  const int64_t rec = record_floats(M, HD);
-  float* pr = a.part + rec_id * rec;
+  // the maxima and sums of rows 4g .. 4g+3.  A partial goes to the record at pr.
 #pragma unroll
   for (int r2 = 0; r2 < R; ++r2)
 #pragma unroll
@@ -767,11 +768,63 @@ void attention_flat_kernel(const AttnArgs a) {
       const int k0 = c - pair_first;
       const int piece_end = min(c_end, pair_first + nch);
       const bool whole = k0 == 0 && piece_end == pair_first + nch;
-      attend_piece<HD, E, R, UNIFORM, OutT, COLD>(a, lp, lq, b, kvh, len, kBlock * k0,
-                                                  min(len, kBlock * (k0 + piece_end - c)), whole,
-                                                  (int64_t)r + (int64_t)b * a.kv_heads + kvh);
+      attend_piece<HD, E, R, UNIFORM, OutT, COLD>(
+          a, lp, lq, b, kvh, len, kBlock * k0, min(len, kBlock * (k0 + piece_end - c)), whole,
+          a.part + ((int64_t)r + (int64_t)b * a.kv_heads + kvh) * record_floats(a.rows, HD));
       c = piece_end;
     }
+  }
+}
+
+// Many short pairs (C2: 16 rows x 8 kv heads, ~650 positions): one workgroup of W waves per
+// (row, kv head).  Wave w streams chunks [w * nch / W, (w + 1) * nch / W) of its pair, leaves its
+// partial record in LDS, and the workgroup folds the W records into the output (same base-2
+// online-softmax fold as the merge kernel): one launch, no global workspace, each pair's bytes
+// read once.  A wave with no chunks leaves a neutral record (maximum -inf, sum 0).
+template <int HD, int E, int R, typename OutT, bool COLD, int W>
+__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(R <= 2 ? 2 : 1, R <= 2 ? 2 : 1)))
+void attention_pair_kernel(const AttnArgs a) {
+  constexpr int kRecMax = (int)record_floats(4 * R, HD);
+  __shared__ float lp[W][kBlock][kMaxRows];
+  __shared__ u32x4 lq[W][Head<HD>::kSteps][kWave];
+  __shared__ float s_rec[W * kRecMax];
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+  const int pair = blockIdx.x;
+  const int b = pair / a.kv_heads;
+  const int kvh = pair - b * a.kv_heads;
+  int len = a.seq_lens[b];
+  if (len > a.max_seq) {
+    if (threadIdx.x == 0 && kvh == 0) atomicOr(a.errors, BARQ_KV_ERRBIT_ATTN_SHORT);
+    len = a.max_seq;
+  }
+  len = max(len, 0);
+  const int nch = (len + kBlock - 1) / kBlock;
+  const int c0 = (int)((int64_t)w * nch / W);
+  const int c1 = (int)((int64_t)(w + 1) * nch / W);
+  const int M = a.rows;
+  const int rec = (int)record_floats(M, HD);
+  attend_piece<HD, E, R, true, OutT, COLD>(a, lp[w], lq[w], b, kvh, len, kBlock * c0, min(len, kBlock * c1), false,
+                                           s_rec + w * rec);
+  __syncthreads();
+  constexpr int kQuads = HD / 4;
+  for (int t = threadIdx.x; t < M * kQuads; t += W * kWave) {
+    const int row = t / kQuads;
+    const int quad = t - row * kQuads;
+    float mstar = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < W; ++k) mstar = fmaxf(mstar, s_rec[k * rec + M * HD + row]);
+    const float mu = mstar == -INFINITY ? 0.f : mstar;
+    float l = 0.f;
+    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      const float* rk = s_rec + k * rec;
+      const float wk = __builtin_amdgcn_exp2f(rk[M * HD + row] - mu);
+      l += wk * rk[M * HD + M + row];
+      o += wk * *(const f32x4*)(rk + row * HD + 4 * quad);
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    store_out4<OutT, E>(out_row(a, b, kvh, row) + (int64_t)(4 * quad) * sizeof(OutT), o * inv);
   }
 }
 
@@ -876,6 +929,16 @@ int resident_waves(K kernel) {
 
 template <int HD, int E, int R, bool U, typename OutT, bool COLD>
 hipError_t launch_typed(AttnArgs a, bool merge, hipStream_t stream) {
+  // Many short pairs, the automatic split, whole-chunk pages, up to 8 query rows (two waves per
+  // SIMD keep the accumulators in registers): one workgroup per pair.
+  if constexpr (U && R <= 2) {
+    const int64_t pairs = (int64_t)a.batch * a.kv_heads;
+    if (a.range_chunks == 0 && pairs >= kPairMinPairs && (a.max_seq + kBlock - 1) / kBlock <= kPairMaxChunks) {
+      hipLaunchKernelGGL((attention_pair_kernel<HD, E, R, OutT, COLD, kPairWaves>), dim3((unsigned)pairs),
+                         dim3(kPairWaves * kWave), 0, stream, a);
+      return hipGetLastError();
+    }
+  }
   auto* k = attention_flat_kernel<HD, E, R, U, OutT, COLD>;
   a.waves = resident_waves(k);
   hipLaunchKernelGGL(k, dim3((unsigned)a.waves), dim3(kWave), 0, stream, a);

@@ -120,6 +120,23 @@ def test_head_dim_64(dtype, page):
     assert pool.errors() == 0
 
 
+@pytest.mark.parametrize("dtype,page,D", [(torch.bfloat16, 16, 128), (torch.float16, 32, 128), (torch.bfloat16, 16, 64)])
+def test_many_short_pairs_one_launch(dtype, page, D):
+    """128+ (row, kv head) pairs of at most 1024 positions with the automatic split take one
+    workgroup per pair that merges its waves' partials in LDS (one launch): ragged rows with
+    empty, one-position and chunk-boundary lengths, G = 1 / 2 / 4 / 8, two query tokens, both
+    output types; the flat schedule (a fixed split) over the same pool agrees."""
+    rng = np.random.default_rng(page + D)
+    lens = [700, 0, 1, 15, 16, 17, 31, 33] + rng.integers(0, 700, size=32).tolist()
+    pool, kd, vd, lens = make_rows(len(lens), 4, page, lens, dtype, seed=page * 3 + D, order_seed=page + D, D=D)
+    ws = None
+    for i, (G, T) in enumerate([(4, 1), (1, 1), (8, 1), (2, 2), (4, 2)]):
+        ws = check(pool, kd, vd, lens, G, T, dtype, seed=400 + i, ws=ws)
+    check(pool, kd, vd, lens, 4, 1, dtype, seed=9, out_f32=False)
+    check(pool, kd, vd, lens, 4, 1, dtype, seed=9, split_tokens=64)  # the flat schedule
+    assert pool.errors() == 0
+
+
 def test_llama3_8b_decode_shape():
     """The benchmark's C2 shape: 16 rows x 8 kv heads x 32 q heads, 513 positions, page 16."""
     lens = [513] * 16

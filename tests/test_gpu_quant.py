@@ -316,6 +316,37 @@ def test_decode_attention_reads_quantised_pages(hip, dtype, page, window, D):
     assert pool.errors() == 0
 
 
+def test_decode_attention_on_quantised_pages_many_pairs(hip):
+    """Attention over a quantised pool with 128 (row, kv head) pairs of short ragged rows (the
+    one-launch pair kernel): against the float64 reference over the dequantising gather's K/V."""
+    from attn_ref import decode_attention_reference, within_tolerance
+    from barqtrain_amd.paged import QuantPagePool
+
+    H, D, P, W = 4, 128, 16, 32
+    rng = np.random.default_rng(77)
+    lens = sorted([600, 1, 16, 33] + rng.integers(40, 600, size=28).tolist(), reverse=True)
+    B, cap = len(lens), 640
+    pool = QuantPagePool(max_batch=B, max_blocks=cap // P, page_size=P, kv_heads=H, head_dim=D,
+                         dtype=torch.bfloat16, device="cuda", window=W)
+    gen = torch.Generator().manual_seed(78)
+    done = 0
+    for b in range(B, 0, -1):
+        n = lens[b - 1] - done
+        if n > 0:
+            k, v = hf_layout(b, H, n, D, torch.bfloat16, gen) * 3, hf_layout(b, H, n, D, torch.bfloat16, gen)
+            pool.append(k.cuda(), v.cuda())
+            done += n
+    assert int(pool.cold_blocks.max()) > 0
+    kd, vd = (t.double().cpu().numpy() for t in pool.gather(B))
+    for G in (4, 2):
+        q = hf_layout(B, G * H, 1, D, torch.bfloat16, gen).cuda()
+        want = decode_attention_reference(q.double().cpu().numpy(), kd, vd, lens, D ** -0.5)
+        got = pool.attend(q, out_dtype=torch.float32)
+        ok, ratio = within_tolerance(got.double().cpu().numpy(), want, **ATT_F32)
+        assert ok, f"G={G}: {ratio:.3g} x tolerance"
+    assert pool.errors() == 0
+
+
 @pytest.mark.parametrize("D", [128, 64])
 def test_decode_attention_cold_through_capi(capi, D):
     """The C entry point on a CColdPool with a crafted cold page (zero, subnormal and NaN-free
