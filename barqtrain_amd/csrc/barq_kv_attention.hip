@@ -57,7 +57,7 @@ constexpr int kMaxWaves = 2048;            // resident waves of an MI355X: 256 C
 constexpr int kMinRangeChunks = 4;         // the automatic range never goes below 64 positions
 constexpr int kPairWaves = 8;              // waves of a pair-kernel workgroup
 constexpr int64_t kPairMinPairs = 128;     // the pair kernel from this many (row, kv head) pairs ...
-constexpr int64_t kPairMaxChunks = 64;     // ... of at most this many 16-position chunks (max_seq)
+constexpr int64_t kPairMaxChunks = 40;     // ... of at most this many 16-position chunks (max_seq)
 
 enum : int { kBF16 = 0, kF16 = 1 };
 

@@ -450,10 +450,13 @@ def attention_leg(cfg, pools, B, dev, reps=20, kv_bytes=None, probe=False):
     if any(p.errors() for p in pools):
         raise SystemExit("device error bits set by the attention leg")
     gathered = 3 * (sum(call_bytes) - L * io) / L  # gather reads + writes K/V, attention re-reads
-    kname = "attention_flat_kernel" + ("<..., COLD> (fp8 pages read as codes)" if getattr(pools[0], "quantized", False)
-                                       else "")
+    cold = "<..., COLD> (fp8 pages read as codes)" if getattr(pools[0], "quantized", False) else ""
+    if B * H >= 128 and max_seq <= 640 and G <= 8:  # the library's one-launch bounds
+        kname = "attention_pair_kernel" + cold + " (one launch per layer)"
+    else:
+        kname = "attention_flat_kernel" + cold + " + attention_merge_kernel (one launch pair per layer)"
     return {
-        "kernel": kname + " + attention_merge_kernel (one launch pair per layer)",
+        "kernel": kname,
         "query_heads_per_kv_head": G,
         "us_per_layer_call": round(per_call_us, 2),
         "us_per_step_all_layers": round(best * 1e3, 1),
