@@ -58,6 +58,7 @@ constexpr int kMinRangeChunks = 4;         // the automatic range never goes bel
 constexpr int kPairWaves = 8;              // waves of a pair-kernel workgroup
 constexpr int64_t kPairMinPairs = 128;     // the pair kernel from this many (row, kv head) pairs ...
 constexpr int64_t kPairMaxChunks = 40;     // ... of at most this many 16-position chunks (max_seq)
+static_assert(kPairMaxChunks <= kTableEntries, "a pair's blocks fit one table window");
 
 enum : int { kBF16 = 0, kF16 = 1 };
 
@@ -292,6 +293,28 @@ __device__ __forceinline__ void load_table(const AttnArgs& a, int b, int blk0, i
   issue_table(a, b, blk0, blk_end, lane, pt);
   check_table<COLD>(a, pt);
 }
+
+// Query rows of (row b, kv head kvh) in the A layout of the score MFMA: lane (row n16, k-group g)
+// holds dims 32 * step + 8 * g .. +7 of query row n16 (zero for padding rows).
+template <int HD>
+__device__ __forceinline__ void issue_query(const AttnArgs& a, int b, int kvh, int lane,
+                                            u32x4 (&qv)[Head<HD>::kSteps]) {
+  const int n16 = lane & 15;
+  const int g = lane >> 4;
+  const bool qrow = n16 < a.rows;
+  const char* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(kvh * a.group + n16 / a.tokens) * a.q_sh +
+                   (int64_t)(n16 % a.tokens) * a.q_st + 16 * g;
+#pragma unroll
+  for (int st = 0; st < Head<HD>::kSteps; ++st) qv[st] = qrow ? *(const u32x4*)(qp + 64 * st) : u32x4{0, 0, 0, 0};
+}
+
+// A piece's first round trip, started by its caller before the row's length is known: the
+// block-table window from block 0 (entries the caller's bound allows) and the query rows.
+template <int HD>
+struct PieceStart {
+  int pt[kTableRegs];
+  u32x4 qv[Head<HD>::kSteps];
+};
 
 // K and V of one 16-position chunk for this lane.  K: lane (g, n16) holds dims 32 * step + 8 * g
 // .. +7 of position tc + n16; V: lane (vpos, vdim) = (lane / (HD / 8), lane % (HD / 8)) holds
@@ -534,10 +557,10 @@ __device__ __forceinline__ void v_operand(const u32x4 x, float (&f)[8]) {
   }
 }
 
-template <int HD, int E, int R, bool UNIFORM, typename OutT, bool COLD>
+template <int HD, int E, int R, bool UNIFORM, typename OutT, bool COLD, bool PRE = false>
 __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
                              u32x4 (&lq)[Head<HD>::kSteps][kWave], int b, int kvh, int len, int t_begin,
-                             int t_end, bool whole, float* pr) {
+                             int t_end, bool whole, float* pr, const PieceStart<HD>* pre = nullptr) {
   constexpr int kSteps = Head<HD>::kSteps;
   constexpr int kVLanes = Head<HD>::kVLanes;
   constexpr int kVPos = Head<HD>::kVPos;
@@ -551,19 +574,23 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
   const int T = a.tokens;
 
   // The block-table window and the query rows load together: one round trip before the first
-  // chunk's loads.  Query rows in the A layout of the score MFMA: lane (row n16, k-group g) holds
-  // dims 32 * step + 8 * g .. +7 of row n16 (zero for padding rows); kept in LDS.
-  int blk0 = (int)a.page_div.div((uint32_t)t_begin);
+  // chunk's loads (PRE: the caller started both, the window from block 0, before it knew the
+  // row's length; entries past the piece's blocks are dropped unchecked).  The query rows are
+  // kept in LDS.
+  int blk0 = PRE ? 0 : (int)a.page_div.div((uint32_t)t_begin);
   const int blk_end = t_end > t_begin ? (int)a.page_div.div((uint32_t)(t_end - 1)) + 1 : blk0;
   int pt[kTableRegs];
-  issue_table(a, b, blk0, blk_end, lane, pt);
   {
     u32x4 qv[kSteps];
-    const bool qrow = n16 < M;
-    const char* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(kvh * a.group + n16 / T) * a.q_sh +
-                     (int64_t)(n16 % T) * a.q_st + 16 * g;
+    if constexpr (PRE) {
 #pragma unroll
-    for (int st = 0; st < kSteps; ++st) qv[st] = qrow ? *(const u32x4*)(qp + 64 * st) : u32x4{0, 0, 0, 0};
+      for (int k = 0; k < kTableRegs; ++k) pt[k] = 64 * k + lane < blk_end ? pre->pt[k] : 0;
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st) qv[st] = pre->qv[st];
+    } else {
+      issue_table(a, b, blk0, blk_end, lane, pt);
+      issue_query<HD>(a, b, kvh, lane, qv);
+    }
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) lq[st][lane] = qv[st];
   }
@@ -792,7 +819,12 @@ void attention_pair_kernel(const AttnArgs a) {
   const int pair = blockIdx.x;
   const int b = pair / a.kv_heads;
   const int kvh = pair - b * a.kv_heads;
+  // The row's length, the table window (every block max_seq allows) and the query rows load
+  // together.
   int len = a.seq_lens[b];
+  PieceStart<HD> ps;
+  issue_table(a, b, 0, (int)a.page_div.div((uint32_t)a.max_seq + a.page_size - 1), threadIdx.x & (kWave - 1), ps.pt);
+  issue_query<HD>(a, b, kvh, threadIdx.x & (kWave - 1), ps.qv);
   if (len > a.max_seq) {
     if (threadIdx.x == 0 && kvh == 0) atomicOr(a.errors, BARQ_KV_ERRBIT_ATTN_SHORT);
     len = a.max_seq;
@@ -803,8 +835,8 @@ void attention_pair_kernel(const AttnArgs a) {
   const int c1 = (int)((int64_t)(w + 1) * nch / W);
   const int M = a.rows;
   const int rec = (int)record_floats(M, HD);
-  attend_piece<HD, E, R, true, OutT, COLD>(a, lp[w], lq[w], b, kvh, len, kBlock * c0, min(len, kBlock * c1), false,
-                                           s_rec + w * rec);
+  attend_piece<HD, E, R, true, OutT, COLD, true>(a, lp[w], lq[w], b, kvh, len, kBlock * c0, min(len, kBlock * c1),
+                                                 false, s_rec + w * rec, &ps);
   __syncthreads();
   constexpr int kQuads = HD / 4;
   for (int t = threadIdx.x; t < M * kQuads; t += W * kWave) {
