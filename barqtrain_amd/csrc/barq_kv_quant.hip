@@ -520,6 +520,52 @@ struct Vec {
   };
 };
 
+// Hardware decode of 8 codes (words w0, w1) with their 8 scale bytes (sk0, sk1): gfx950's OCP
+// E4M3 conversion (exact for every finite code) times 2^(s - 127), exact in fp32 while the scale
+// bytes stay in [64, 191], rounded to the output type as from_float does.  hw_decodable tells
+// when it applies: NaN codes (the hardware drops their sign) and other scales take
+// dequant_vec's other paths.
+__device__ __forceinline__ bool hw_decodable(uint32_t w0, uint32_t w1, uint32_t sk0, uint32_t sk1) {
+  const uint32_t mid = ((sk0 >> 1) ^ sk0) & ((sk1 >> 1) ^ sk1) & 0x40404040u;
+  const uint32_t n0 = (w0 & 0x7F7F7F7Fu) ^ 0x7F7F7F7Fu, n1 = (w1 & 0x7F7F7F7Fu) ^ 0x7F7F7F7Fu;
+  const uint32_t nan = (((n0 - 0x01010101u) & ~n0) | ((n1 - 0x01010101u) & ~n1)) & 0x80808080u;
+  return mid == 0x40404040u && nan == 0;
+}
+
+template <int KIND>
+__device__ __forceinline__ typename Vec<KIND, 8>::Out hw_decode(uint32_t w0, uint32_t w1, uint32_t sk0, uint32_t sk1) {
+  using V = Vec<KIND, 8>;
+  using E = Elem<KIND>;
+  using Bits = typename E::Bits;
+  typename V::OutU val;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t w = j ? w1 : w0, sw = j ? sk1 : sk0;
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+    const float f[4] = {lo[0] * __uint_as_float((sw & 0xFFu) << 23),
+                        lo[1] * __uint_as_float(((sw >> 8) & 0xFFu) << 23),
+                        hi[0] * __uint_as_float(((sw >> 16) & 0xFFu) << 23),
+                        hi[1] * __uint_as_float((sw >> 24) << 23)};
+    // The hardware reads code 0x80 as +0: every code's sign bit goes back on its value.
+    if constexpr (KIND == BARQ_KV_BF16) {  // exact values: the top halves
+      const uint32_t p0 = __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u) |
+                          ((w << 8) & 0x8000u) | ((w << 16) & 0x80000000u);
+      const uint32_t p1 = __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u) |
+                          ((w >> 8) & 0x8000u) | (w & 0x80000000u);
+      val.e[4 * j] = (Bits)p0;
+      val.e[4 * j + 1] = (Bits)(p0 >> 16);
+      val.e[4 * j + 2] = (Bits)p1;
+      val.e[4 * j + 3] = (Bits)(p1 >> 16);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        val.e[4 * j + e] = (Bits)(E::from_float(f[e]) | (((w >> (8 * e + 7)) & 1u) << 15));
+    }
+  }
+  return val.v;
+}
+
 // VE elements from their E4M3 codes and scales: keys with VE per-channel scale bytes (ksc),
 // values with one per-token scale byte (vsc).  Exact: code * 2^(s - 127) rounded once to the
 // element type.
@@ -529,46 +575,12 @@ __device__ __forceinline__ typename Vec<KIND, VE>::Out dequant_vec(typename Vec<
                                                                   int kv) {
   using V = Vec<KIND, VE>;
   using E = Elem<KIND>;
-  using Bits = typename E::Bits;
   typename V::OutU val;
   if constexpr (VE == 8 && KIND != BARQ_KV_FP32) {
     const uint32_t w0 = codes.v.x, w1 = codes.v.y;
-    // Hardware decode (gfx950: OCP E4M3, exact for every finite code) times 2^(s - 127), exact in
-    // fp32 while the scale bytes stay in [64, 191]; rounded to the output type as from_float
-    // does.  NaN codes (the hardware drops their sign) and other scales take the paths below.
     const uint32_t sk0 = kv == 0 ? ksc.v.x : vsc * 0x01010101u;
     const uint32_t sk1 = kv == 0 ? ksc.v.y : vsc * 0x01010101u;
-    const uint32_t mid = ((sk0 >> 1) ^ sk0) & ((sk1 >> 1) ^ sk1) & 0x40404040u;
-    const uint32_t n0 = (w0 & 0x7F7F7F7Fu) ^ 0x7F7F7F7Fu, n1 = (w1 & 0x7F7F7F7Fu) ^ 0x7F7F7F7Fu;
-    const uint32_t nan = (((n0 - 0x01010101u) & ~n0) | ((n1 - 0x01010101u) & ~n1)) & 0x80808080u;
-    if (mid == 0x40404040u && nan == 0) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const uint32_t w = j ? w1 : w0, sw = j ? sk1 : sk0;
-        const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
-        const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
-        const float f[4] = {lo[0] * __uint_as_float((sw & 0xFFu) << 23),
-                            lo[1] * __uint_as_float(((sw >> 8) & 0xFFu) << 23),
-                            hi[0] * __uint_as_float(((sw >> 16) & 0xFFu) << 23),
-                            hi[1] * __uint_as_float((sw >> 24) << 23)};
-        // The hardware reads code 0x80 as +0: every code's sign bit goes back on its value.
-        if constexpr (KIND == BARQ_KV_BF16) {  // exact values: the top halves
-          const uint32_t p0 = __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u) |
-                              ((w << 8) & 0x8000u) | ((w << 16) & 0x80000000u);
-          const uint32_t p1 = __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u) |
-                              ((w >> 8) & 0x8000u) | (w & 0x80000000u);
-          val.e[4 * j] = (Bits)p0;
-          val.e[4 * j + 1] = (Bits)(p0 >> 16);
-          val.e[4 * j + 2] = (Bits)p1;
-          val.e[4 * j + 3] = (Bits)(p1 >> 16);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            val.e[4 * j + e] = (Bits)(E::from_float(f[e]) | (((w >> (8 * e + 7)) & 1u) << 15));
-        }
-      }
-      return val.v;
-    }
+    if (hw_decodable(w0, w1, sk0, sk1)) return hw_decode<KIND>(w0, w1, sk0, sk1);
     uint32_t s0, s1, s2, s3;  // scale pairs, spread like the code pairs
     bool fast = codes_normal(w0) && codes_normal(w1);
     if (kv == 0) {
@@ -691,6 +703,79 @@ __global__ void __launch_bounds__(kGatherThreads) gather_cold_kernel(const Gathe
   }
 }
 
+// dequant_vec's exact path for 8 codes (words w0, w1) and their scale bytes (sk0, sk1), one
+// element at a time: the rare path of the lanes kernels, holding one element's registers.
+template <int KIND>
+__device__ __forceinline__ typename Vec<KIND, 8>::Out exact8(uint32_t w0, uint32_t w1, uint32_t sk0, uint32_t sk1) {
+  uint32_t r0 = 0, r1 = 0, r2 = 0, r3 = 0;
+#pragma unroll 1
+  for (int e = 0; e < 8; ++e) {
+    const int sh = 8 * (e & 3);
+    const uint32_t code = ((e < 4 ? w0 : w1) >> sh) & 0xFFu;
+    const int sc = (int)(((e < 4 ? sk0 : sk1) >> sh) & 0xFFu);
+    const uint32_t bits = (uint32_t)Elem<KIND>::from_float(ldexpf(e4m3_decode(code), sc - 127)) << (16 * (e & 1));
+    const int word = e >> 1;
+    r0 |= word == 0 ? bits : 0u;
+    r1 |= word == 1 ? bits : 0u;
+    r2 |= word == 2 ? bits : 0u;
+    r3 |= word == 3 ? bits : 0u;
+  }
+  return typename Vec<KIND, 8>::Out{r0, r1, r2, r3};
+}
+
+// One wave's round of a cold tile in the lanes kernels (VALUES: the V page, whose scales are
+// per position and head; else K, per-channel scales ksc): positions t0 .. t0 + 8 / LPP - 1 of
+// the page, decoded below `live`, zeros up to `end`; the lane's columns col[c] (element offsets
+// in a token row) go to ocol[c] of the output rows at o.  The round's codes and scales load
+// together and unconditionally (positions clamped into the page): a load under a condition
+// leaves a phi of zero and the loaded value, into whose block the compiler moves the scale
+// arithmetic, waiting there for each load before the next is issued.  A vector decodes on the
+// hardware path when every lane's does (scales in [64, 191], no NaN code: the usual case), else
+// element by element; with dequant_vec inlined for the whole round the kernels held 4 waves per
+// SIMD instead of 5.
+template <int KIND, int LPP, bool VALUES>
+__device__ __forceinline__ void cold_round(const GatherArgs& a, int cold, int t0, int live, int end, int lane,
+                                           const int (&col)[LPP], const int64_t (&ocol)[LPP],
+                                           const typename Vec<KIND, 8>::CodeU (&ksc)[LPP],
+                                           typename Elem<KIND>::Bits* o) {
+  using V = Vec<KIND, 8>;
+  constexpr int kNPos = 8 / LPP;
+  const barq_kv_pool& p = a.p;
+  const int P = (int)p.page_size, H = (int)p.kv_heads, D = (int)p.head_dim;
+  const int HD = H * D;
+  const int dvn = D / 8;
+  const uint8_t* codes = a.c.codes[VALUES ? 1 : 0] + (int64_t)cold * P * HD;
+  const uint8_t* vscales = a.c.value_scales + (int64_t)cold * P * H;
+  typename V::CodeU cv[kNPos][LPP];
+  uint32_t vsc[kNPos][LPP];
+#pragma unroll
+  for (int i = 0; i < kNPos; ++i) {
+    const int t = min(t0 + i, P - 1);
+#pragma unroll
+    for (int c = 0; c < LPP; ++c) {
+      cv[i][c].v = __builtin_nontemporal_load((const typename V::Codes*)(codes + (int64_t)t * HD + col[c]));
+      vsc[i][c] = VALUES ? vscales[t * H + (c * kWave + lane) / dvn] : 0u;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kNPos; ++i)
+#pragma unroll
+    for (int c = 0; c < LPP; ++c) {
+      if (t0 + i >= end) continue;
+      const uint32_t w0 = cv[i][c].v.x, w1 = cv[i][c].v.y;
+      const uint32_t sk0 = VALUES ? vsc[i][c] * 0x01010101u : ksc[c].v.x;
+      const uint32_t sk1 = VALUES ? vsc[i][c] * 0x01010101u : ksc[c].v.y;
+      const bool dead = t0 + i >= live;
+      typename V::Out v;
+      if (__builtin_amdgcn_ballot_w64(!(dead || hw_decodable(w0, w1, sk0, sk1))) == 0)  // uniform
+        v = hw_decode<KIND>(w0, w1, sk0, sk1);
+      else
+        v = exact8<KIND>(w0, w1, sk0, sk1);
+      if (dead) v = typename V::Out(0);
+      __builtin_nontemporal_store(v, (typename V::Out*)(o + (int64_t)i * a.oss + ocol[c]));
+    }
+}
+
 // The gather for 8-element vectors (2-byte elements) when a token's kv_heads * head_dim
 // elements are 64 * LPP vectors: a wave moves whole positions, lane l taking vectors l, l + 64,
 // ... of each, so a lane's columns -- and its key scales -- are fixed for the tile and only the
@@ -774,30 +859,11 @@ __global__ void __launch_bounds__(kGatherThreads) gather_cold_lanes_kernel(const
 #pragma unroll
         for (int c = 0; c < LPP; ++c)
           if (t0 + i < end) __builtin_nontemporal_store(val[i][c].v, (typename V::Out*)(o + (int64_t)i * a.oss + ocol[c]));
-    } else if (cold >= 0) {  // uniform: codes and scales of the round in flight, then decode + store
-      const uint8_t* codes = a.c.codes[kv] + ((int64_t)cold * P + t0) * HD;
-      typename V::CodeU cv[kNPos][LPP];
-      uint32_t vsc[kNPos][LPP];
-#pragma unroll
-      for (int i = 0; i < kNPos; ++i)
-#pragma unroll
-        for (int c = 0; c < LPP; ++c) {
-          cv[i][c].v = typename V::Codes(0);
-          vsc[i][c] = 0;
-          if (t0 + i < live) {
-            cv[i][c].v = __builtin_nontemporal_load((const typename V::Codes*)(codes + (int64_t)i * HD + col[c]));
-            if (kv) vsc[i][c] = a.c.value_scales[((int64_t)cold * P + t0 + i) * H + (c * kWave + lane) / dvn];
-          }
-        }
-#pragma unroll
-      for (int i = 0; i < kNPos; ++i)
-#pragma unroll
-        for (int c = 0; c < LPP; ++c) {
-          if (t0 + i >= end) continue;
-          const typename V::Out v =
-              t0 + i < live ? dequant_vec<KIND, 8>(cv[i][c], ksc[c], vsc[i][c], kv) : typename V::Out(0);
-          __builtin_nontemporal_store(v, (typename V::Out*)(o + (int64_t)i * a.oss + ocol[c]));
-        }
+    } else if (cold >= 0) {  // uniform
+      if (kv)
+        cold_round<KIND, LPP, true>(a, cold, t0, live, end, lane, col, ocol, ksc, o);
+      else
+        cold_round<KIND, LPP, false>(a, cold, t0, live, end, lane, col, ocol, ksc, o);
     } else {
 #pragma unroll
       for (int i = 0; i < kNPos; ++i)
@@ -826,7 +892,7 @@ struct UpdateArgs {
 };
 
 template <int KIND, int LPP>
-__global__ void __launch_bounds__(kGatherThreads) update_cold_lanes_kernel(const UpdateArgs u) {
+__global__ void __launch_bounds__(kGatherThreads) __attribute__((amdgpu_waves_per_eu(LPP <= 2 ? 5 : 3))) update_cold_lanes_kernel(const UpdateArgs u) {
   using V = Vec<KIND, 8>;
   using E = Elem<KIND>;
   using Bits = typename E::Bits;
@@ -955,30 +1021,11 @@ __global__ void __launch_bounds__(kGatherThreads) update_cold_lanes_kernel(const
 #pragma unroll
         for (int c = 0; c < LPP; ++c)
           if (t0 + i < end) __builtin_nontemporal_store(val[i][c].v, (typename V::Out*)(o + (int64_t)i * a.oss + ocol[c]));
-    } else if (cold >= 0) {  // uniform: codes and scales of the round in flight, then decode + store
-      const uint8_t* codes = a.c.codes[kv] + ((int64_t)cold * P + t0) * HD;
-      typename V::CodeU cv[kNPos][LPP];
-      uint32_t vsc[kNPos][LPP];
-#pragma unroll
-      for (int i = 0; i < kNPos; ++i)
-#pragma unroll
-        for (int c = 0; c < LPP; ++c) {
-          cv[i][c].v = typename V::Codes(0);
-          vsc[i][c] = 0;
-          if (t0 + i < live) {
-            cv[i][c].v = __builtin_nontemporal_load((const typename V::Codes*)(codes + (int64_t)i * HD + col[c]));
-            if (kv) vsc[i][c] = a.c.value_scales[((int64_t)cold * P + t0 + i) * H + (c * kWave + lane) / dvn];
-          }
-        }
-#pragma unroll
-      for (int i = 0; i < kNPos; ++i)
-#pragma unroll
-        for (int c = 0; c < LPP; ++c) {
-          if (t0 + i >= end) continue;
-          const typename V::Out v =
-              t0 + i < live ? dequant_vec<KIND, 8>(cv[i][c], ksc[c], vsc[i][c], kv) : typename V::Out(0);
-          __builtin_nontemporal_store(v, (typename V::Out*)(o + (int64_t)i * a.oss + ocol[c]));
-        }
+    } else if (cold >= 0) {  // uniform
+      if (kv)
+        cold_round<KIND, LPP, true>(a, cold, t0, live, end, lane, col, ocol, ksc, o);
+      else
+        cold_round<KIND, LPP, false>(a, cold, t0, live, end, lane, col, ocol, ksc, o);
     } else {
 #pragma unroll
       for (int i = 0; i < kNPos; ++i)
