@@ -86,6 +86,43 @@ def test_random_programs_through_capi(capi, case, seed):
     assert pool.errors() == 0
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("H", [4, 8, 16])
+def test_lanes_kernels_decode_extreme_pages_like_the_oracle(capi, dtype, H):
+    """The gather and the one-launch update over cold pages whose token rows are 64, 128 or 256
+    16-byte vectors (H x 128): NaN and infinite values, signed zeros and (bf16) heads scaled by
+    2^-100 and 2^100, whose scale bytes leave [64, 191], so that vectors the hardware decode does
+    not cover take the element-wise path; bit-exact against the oracle."""
+    D, P, W = 128, 16, 16
+    rng = np.random.default_rng(H)
+    x = rng.standard_normal((2, 3 * P, H, D)).astype(np.float32)
+    x[0, 3, 1, 5] = np.nan
+    x[1, 20, 1, 3] = np.nan
+    x[1, 4, 0, 7] = np.inf
+    x[1, 5, 2, 9] = -np.inf
+    x[0, 6, 3, :] = -0.0
+    if dtype == torch.bfloat16:
+        x[0, :, 2, :] *= np.float32(2.0 ** -100)
+        x[1, 17:, 3, :64] *= np.float32(2.0 ** 100)
+    t = torch.from_numpy(x).to(dtype)
+    k = t[0][None].permute(0, 2, 1, 3).contiguous()
+    v = t[1][None].permute(0, 2, 1, 3).contiguous()
+    pool = CColdPool(window=W, max_batch=1, max_blocks=4, page_size=P, heads=H, dim=D, dtype=dtype)
+    oracle = q.QuantLayerOracle(1, 4 * P, P, W, DT[dtype])
+    pool.append(k.cuda(), v.cuda())
+    pool.compress(1)
+    oracle.append(to_bits(k), to_bits(v))
+    assert oracle.cold.tolist() == [2]
+    assert_same(pool, oracle, "gather")
+    gen = torch.Generator().manual_seed(H)
+    k1, v1 = hf_layout(1, H, 1, D, dtype, gen), hf_layout(1, H, 1, D, dtype, gen)
+    oracle.append(to_bits(k1), to_bits(v1))
+    got = pool.update(k1.cuda(), v1.cuda(), oracle.get_seq_length())
+    ok, ov = oracle.current_tensors()
+    assert np.array_equal(to_bits(got[0]), ok) and np.array_equal(to_bits(got[1]), ov), "update"
+    assert pool.errors() == 0
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
 def test_boundary_values_quantise_like_the_oracle(capi, dtype):
     """Groups whose values sit on E4M3 codes, on the midpoints between them (ties to even) and
