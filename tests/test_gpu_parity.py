@@ -158,10 +158,11 @@ def staircase(lengths_desc):
     return calls
 
 
-@pytest.mark.parametrize("B,S", [(2, 2100), (8, 700), (16, 600), (32, 300)])
+@pytest.mark.parametrize("B,S", [(2, 2100), (8, 700), (16, 600), (32, 300), (1, 32900), (4, 8300)])
 def test_cu_balanced_tail_pieces(capi, B, S):
     """Single-round gather launches whose tile count (2 * B * ceil(S / 32) at 8 KV heads x 128,
-    bf16, page 16) is not a multiple of the CU count cut their tail into one piece per CU.
+    bf16, page 16) is not a multiple of the CU count cut their tail into one piece per CU; (B = 1
+    and 4) launches of several dispatch rounds with such tile counts keep whole tiles.
     Ragged rows (stale and zero-padded positions in the pieces), updates of 1 and 3 tokens, exact
     extents and device-side extents over a larger output; positions past the longest row are
     never written."""
