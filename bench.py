@@ -636,6 +636,9 @@ def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10, probe=
         torch.cuda.synchronize()
         return None
     prefill()
+    # every graph the steps replay (each extent bucket, with and without the compress launch)
+    # captured before the timed region
+    step.prepare([max(prefill_lengths(cfg)) + s + 1 for s in range(steps)])
     for s in range(min(4, steps)):
         run(s)
     torch.cuda.synchronize()
