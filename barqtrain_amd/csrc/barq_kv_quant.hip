@@ -17,11 +17,20 @@
 #include <climits>
 
 #include "barq_kv.h"
+#include <atomic>
+
 #include "barq_kv_commit.h"
 #include "barq_kv_fp8.h"
 #include "fastdiv.h"
 
 namespace {
+
+// s_waitcnt vmcnt(K), the other counters left alone (vmcnt bits 3:0, expcnt 6:4, lgkmcnt 11:8).
+template <int K>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(K >= 0 && K < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(K | (0x7 << 4) | (0xF << 8));
+}
 
 constexpr int kThreads = 256;
 constexpr int kWave = 64;
@@ -732,12 +741,13 @@ __device__ __forceinline__ typename Vec<KIND, 8>::Out exact8(uint32_t w0, uint32
 // arithmetic, waiting there for each load before the next is issued.  A vector decodes on the
 // hardware path when every lane's does (scales in [64, 191], no NaN code: the usual case), else
 // element by element; with dequant_vec inlined for the whole round the kernels held 4 waves per
-// SIMD instead of 5.
+// SIMD instead of 5.  `spaced` (uniform): each store waits for the previous one, one store in
+// flight per wave.
 template <int KIND, int LPP, bool VALUES>
 __device__ __forceinline__ void cold_round(const GatherArgs& a, int cold, int t0, int live, int end, int lane,
                                            const int (&col)[LPP], const int64_t (&ocol)[LPP],
                                            const typename Vec<KIND, 8>::CodeU (&ksc)[LPP],
-                                           typename Elem<KIND>::Bits* o) {
+                                           typename Elem<KIND>::Bits* o, bool spaced) {
   using V = Vec<KIND, 8>;
   constexpr int kNPos = 8 / LPP;
   const barq_kv_pool& p = a.p;
@@ -772,6 +782,7 @@ __device__ __forceinline__ void cold_round(const GatherArgs& a, int cold, int t0
       else
         v = exact8<KIND>(w0, w1, sk0, sk1);
       if (dead) v = typename V::Out(0);
+      if (spaced) wait_vm<0>();
       __builtin_nontemporal_store(v, (typename V::Out*)(o + (int64_t)i * a.oss + ocol[c]));
     }
 }
@@ -861,9 +872,9 @@ __global__ void __launch_bounds__(kGatherThreads) gather_cold_lanes_kernel(const
           if (t0 + i < end) __builtin_nontemporal_store(val[i][c].v, (typename V::Out*)(o + (int64_t)i * a.oss + ocol[c]));
     } else if (cold >= 0) {  // uniform
       if (kv)
-        cold_round<KIND, LPP, true>(a, cold, t0, live, end, lane, col, ocol, ksc, o);
+        cold_round<KIND, LPP, true>(a, cold, t0, live, end, lane, col, ocol, ksc, o, false);
       else
-        cold_round<KIND, LPP, false>(a, cold, t0, live, end, lane, col, ocol, ksc, o);
+        cold_round<KIND, LPP, false>(a, cold, t0, live, end, lane, col, ocol, ksc, o, false);
     } else {
 #pragma unroll
       for (int i = 0; i < kNPos; ++i)
@@ -888,6 +899,8 @@ struct UpdateArgs {
   int64_t isb, ish, ist;  // input strides, elements
   int32_t tokens;
   int32_t nsub;           // arrival sub-counters in use
+  int32_t spaced;         // every tile resident at once: one store in flight per wave (3 % faster
+                          // at C2); launches of several rounds keep their stores back to back
   FastDiv div_page;
 };
 
@@ -1020,12 +1033,15 @@ __global__ void __launch_bounds__(kGatherThreads) __attribute__((amdgpu_waves_pe
       for (int i = 0; i < kNPos; ++i)
 #pragma unroll
         for (int c = 0; c < LPP; ++c)
-          if (t0 + i < end) __builtin_nontemporal_store(val[i][c].v, (typename V::Out*)(o + (int64_t)i * a.oss + ocol[c]));
+          if (t0 + i < end) {
+            if (u.spaced) wait_vm<0>();
+            __builtin_nontemporal_store(val[i][c].v, (typename V::Out*)(o + (int64_t)i * a.oss + ocol[c]));
+          }
     } else if (cold >= 0) {  // uniform
       if (kv)
-        cold_round<KIND, LPP, true>(a, cold, t0, live, end, lane, col, ocol, ksc, o);
+        cold_round<KIND, LPP, true>(a, cold, t0, live, end, lane, col, ocol, ksc, o, u.spaced);
       else
-        cold_round<KIND, LPP, false>(a, cold, t0, live, end, lane, col, ocol, ksc, o);
+        cold_round<KIND, LPP, false>(a, cold, t0, live, end, lane, col, ocol, ksc, o, u.spaced);
     } else {
 #pragma unroll
       for (int i = 0; i < kNPos; ++i)
@@ -1355,6 +1371,28 @@ int compress_launch(const barq_kv_pool* pool, const barq_kv_cold* cold, int64_t 
 // elements whose token rows are 64, 128 or 256 vectors of 16 bytes, every address and stride
 // 16-byte aligned (codes and key scales 8-byte), the output reaching the new tokens.  Returns -1
 // (nothing launched) when it does not.
+// Workgroups of a kGatherThreads-thread kernel resident at once on the current device (cached per
+// slot and device; 0 when the runtime does not say).  Host threads may race on the cache, which
+// only ever stores the one value a device gives.
+int resident_tiles(const void* fn, int slot) {
+  constexpr int kMaxDevices = 64;
+  constexpr int kSlots = 6;
+  static std::atomic<int> cached[kSlots][kMaxDevices];  // 0 = not queried yet
+  int dev = 0;
+  if (slot < 0 || slot >= kSlots || hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int v = cached[slot][dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kGatherThreads, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 ||
+        cus <= 0)
+      return 0;
+    v = per_cu * cus;
+    cached[slot][dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 int update_cold_fused(const barq_kv_pool* pool, const barq_kv_cold* cold, const void* ks, const void* vs,
                       int64_t batch, int64_t tokens, int64_t sb, int64_t sh, int64_t st, void* ko, void* vo,
                       int64_t seq_out, int64_t osb, int64_t osh, int64_t oss, int64_t flags, void* stream) {
@@ -1413,6 +1451,8 @@ int update_cold_fused(const barq_kv_pool* pool, const barq_kv_cold* cold, const 
                                      : (const void*)&update_cold_lanes_kernel<BARQ_KV_BF16, 2>)
                               : (f16 ? (const void*)&update_cold_lanes_kernel<BARQ_KV_FP16, 4>
                                      : (const void*)&update_cold_lanes_kernel<BARQ_KV_BF16, 4>);
+  const int64_t resident = resident_tiles(fn, (lpp == 1 ? 0 : lpp == 2 ? 1 : 2) * 2 + (f16 ? 1 : 0));
+  u.spaced = resident > 0 && tiles <= resident ? 1 : 0;
   void* args[] = {&u};
   return hipLaunchKernel(fn, dim3((uint32_t)tiles), dim3(kGatherThreads), args, 0, (hipStream_t)stream) == hipSuccess
              ? BARQ_KV_OK
