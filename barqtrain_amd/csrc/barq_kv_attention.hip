@@ -397,14 +397,9 @@ __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kT
   }
 }
 
-// One piece: positions [t_begin, t_end) of (row b, kv head kvh), row length len.  whole: the
-// piece is the whole pair (write the output), else write record `rec_id`.
-// Quantised chunk registers (codes and scales, as load_chunk left them) -> two-byte K and V.
-// When every vector of every lane qualifies, the exponent arithmetic decodes the chunk unrolled;
-// otherwise (a zero, subnormal or NaN code, or an extreme scale somewhere in the wave) one rolled
-// loop takes the vectors one by one -- exponent arithmetic where it applies, the exact element
-// path where not -- picking and putting back each vector with constant-index switches, so the
-// rare path adds no register pressure to the common one.
+// One register of a quantised chunk (8 codes and their scale bytes: K's per channel, V's -- value
+// -- the position's one) -> 8 two-byte values: exponent arithmetic where it applies, else the
+// exact element path.
 template <int E>
 __device__ __forceinline__ u32x4 dequant_vector(const u32x4 x, bool value) {
   const uint32_t s0 = value ? x[2] * 0x01010101u : x[2];
@@ -421,86 +416,62 @@ __device__ __forceinline__ u32x4 dequant_vector(const u32x4 x, bool value) {
   return u32x4{o[0], o[1], o[2], o[3]};
 }
 
-// Vector i of a chunk's registers -- K step i (i < NK), else V load i - NK -- for a wave-uniform
-// runtime i, through constant-index switches (a dynamic index would move the chunk to scratch).
-template <int NK, int NV>
-__device__ __forceinline__ u32x4 chunk_vector(const u32x4 (&kv)[NK], const u32x4 (&vv)[NV], int i) {
-  static_assert((NK == 4 && NV == 4) || (NK == 2 && NV == 2), "chunk layouts of head sizes 128 and 64");
-  if constexpr (NK == 4) {
-    switch (i) {
-      case 0: return kv[0];
-      case 1: return kv[1];
-      case 2: return kv[2];
-      case 3: return kv[3];
-      case 4: return vv[0];
-      case 5: return vv[1];
-      case 6: return vv[2];
-      default: return vv[3];
+// A quantised chunk's K (VALUE false: codes and per-channel scales per register) or V (VALUE
+// true: codes and the position's scale) -> two-byte values.  When every vector of every lane
+// qualifies, exponent arithmetic decodes the registers unrolled; otherwise (a zero, subnormal or
+// NaN code, or an extreme scale somewhere in the wave) one rolled loop takes the registers one by
+// one, picked and put back through constant-index switches (a dynamic index would move the chunk
+// to scratch), so the rare path adds no register pressure to the common one.
+template <int N>
+__device__ __forceinline__ u32x4 chunk_reg(const u32x4 (&r)[N], int n) {
+  static_assert(N == 2 || N == 4, "chunk layouts of head sizes 64 and 128");
+  if constexpr (N == 4) {
+    switch (n) {
+      case 0: return r[0];
+      case 1: return r[1];
+      case 2: return r[2];
+      default: return r[3];
     }
   } else {
-    switch (i) {
-      case 0: return kv[0];
-      case 1: return kv[1];
-      case 2: return vv[0];
-      default: return vv[1];
-    }
+    return n == 0 ? r[0] : r[1];
   }
 }
-template <int NK, int NV>
-__device__ __forceinline__ void set_chunk_vector(u32x4 (&kv)[NK], u32x4 (&vv)[NV], int i, const u32x4 y) {
-  if constexpr (NK == 4) {
-    switch (i) {
-      case 0: kv[0] = y; break;
-      case 1: kv[1] = y; break;
-      case 2: kv[2] = y; break;
-      case 3: kv[3] = y; break;
-      case 4: vv[0] = y; break;
-      case 5: vv[1] = y; break;
-      case 6: vv[2] = y; break;
-      default: vv[3] = y; break;
+template <int N>
+__device__ __forceinline__ void set_chunk_reg(u32x4 (&r)[N], int n, const u32x4 y) {
+  if constexpr (N == 4) {
+    switch (n) {
+      case 0: r[0] = y; break;
+      case 1: r[1] = y; break;
+      case 2: r[2] = y; break;
+      default: r[3] = y; break;
     }
   } else {
-    switch (i) {
-      case 0: kv[0] = y; break;
-      case 1: kv[1] = y; break;
-      case 2: vv[0] = y; break;
-      default: vv[1] = y; break;
-    }
+    if (n == 0) r[0] = y; else r[1] = y;
   }
 }
 
-template <int E, int NK, int NV>
-__device__ __forceinline__ void dequant_chunk(u32x4 (&kv)[NK], u32x4 (&vv)[NV]) {
+template <int E, bool VALUE, int N>
+__device__ __forceinline__ void dequant_regs(u32x4 (&r)[N]) {
   bool fast = true;
 #pragma unroll
-  for (int st = 0; st < NK; ++st) fast = fast && barq_fp8::dequant8_fast_ok<E>(kv[st][0], kv[st][1], kv[st][2], kv[st][3]);
-#pragma unroll
-  for (int s = 0; s < NV; ++s) {
-    const uint32_t sv = vv[s][2] * 0x01010101u;
-    fast = fast && barq_fp8::dequant8_fast_ok<E>(vv[s][0], vv[s][1], sv, sv);
+  for (int n = 0; n < N; ++n) {
+    const uint32_t s0 = VALUE ? r[n][2] * 0x01010101u : r[n][2];
+    const uint32_t s1 = VALUE ? r[n][2] * 0x01010101u : r[n][3];
+    fast = fast && barq_fp8::dequant8_fast_ok<E>(r[n][0], r[n][1], s0, s1);
   }
   if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
 #pragma unroll
-    for (int st = 0; st < NK; ++st) {
+    for (int n = 0; n < N; ++n) {
+      const uint32_t s0 = VALUE ? r[n][2] * 0x01010101u : r[n][2];
+      const uint32_t s1 = VALUE ? r[n][2] * 0x01010101u : r[n][3];
       uint32_t o[4];
-      barq_fp8::dequant8_fast<E>(kv[st][0], kv[st][1], kv[st][2], kv[st][3], o);
-      kv[st] = u32x4{o[0], o[1], o[2], o[3]};
-    }
-#pragma unroll
-    for (int s = 0; s < NV; ++s) {
-      const uint32_t sv = vv[s][2] * 0x01010101u;
-      uint32_t o[4];
-      barq_fp8::dequant8_fast<E>(vv[s][0], vv[s][1], sv, sv, o);
-      vv[s] = u32x4{o[0], o[1], o[2], o[3]};
+      barq_fp8::dequant8_fast<E>(r[n][0], r[n][1], s0, s1, o);
+      r[n] = u32x4{o[0], o[1], o[2], o[3]};
     }
     return;
   }
-  // Vector i: K step i (i < NK) or V load i - NK, picked and put back by constant indices.
 #pragma unroll 1
-  for (int i = 0; i < NK + NV; ++i) {
-    const u32x4 y = dequant_vector<E>(chunk_vector(kv, vv, i), i >= NK);
-    set_chunk_vector(kv, vv, i, y);
-  }
+  for (int n = 0; n < N; ++n) set_chunk_reg(r, n, dequant_vector<E>(chunk_reg(r, n), VALUE));
 }
 
 // Fast operands from a quantised chunk (scale bytes in [64, 191], checked per chunk): the codes
@@ -510,14 +481,16 @@ __device__ __forceinline__ void dequant_chunk(u32x4 (&kv)[NK], u32x4 (&vv)[NV]) 
 // operand holds exactly the dequantised value.  V needs no scale here: its per-position scale
 // multiplies the probability (exact: a power of two).  A NaN code reads as NaN either way, and
 // the hardware's +0 for code 0x80 (-0) changes no product or sum.
-template <int NK, int NV>
-__device__ __forceinline__ bool chunk_scales_moderate(const u32x4 (&kv)[NK], const u32x4 (&vv)[NV]) {
+// Every scale byte of a chunk's K registers (VALUE false: 8 per register) or V registers (the
+// position's byte) in 64..191: its top two bits are 01 or 10.  K is checked before the scores and
+// V before P.V, so neither waits for the other's loads.
+template <bool VALUE, int N>
+__device__ __forceinline__ bool scales_moderate(const u32x4 (&r)[N]) {
   uint32_t ok = 0x40404040u;
 #pragma unroll
-  for (int st = 0; st < NK; ++st) ok &= ((kv[st][2] >> 1) ^ kv[st][2]) & ((kv[st][3] >> 1) ^ kv[st][3]);
-#pragma unroll
-  for (int s = 0; s < NV; ++s) ok &= ((vv[s][2] >> 1) ^ vv[s][2]) | 0x40404000u;
-  return (ok & 0x40404040u) == 0x40404040u;  // every byte's top two bits are 01 or 10: 64..191
+  for (int n = 0; n < N; ++n)
+    ok &= VALUE ? (((r[n][2] >> 1) ^ r[n][2]) | 0x40404000u) : (((r[n][2] >> 1) ^ r[n][2]) & ((r[n][3] >> 1) ^ r[n][3]));
+  return (ok & 0x40404040u) == 0x40404040u;
 }
 
 __device__ __forceinline__ float e8m0_float(uint32_t s) { return __uint_as_float(s << 23); }
@@ -629,12 +602,14 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
   };
 
   // codes: the chunk registers hold a quantised chunk with moderate scales (see k_operand).
-  auto compute = [&](int tc, const u32x4 (&kv)[kSteps], const u32x4 (&vv)[kVLoads], bool codes) {
+  // kcodes: the K registers hold a quantised chunk's codes with moderate scales (k_operand);
+  // vcold: the V registers hold a quantised chunk's codes, checked here before P.V.
+  auto compute = [&](int tc, const u32x4 (&kv)[kSteps], u32x4 (&vv)[kVLoads], bool kcodes, bool vcold) {
     // Scores: lane (g, n16), register r = row 4g + r, position tc + n16; log2 units.
     f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < kSteps; ++st)
-      sc = mfma_qk<E>(lq[st][lane], (COLD && codes) ? k_operand<E>(kv[st]) : kv[st], sc);
+      sc = mfma_qk<E>(lq[st][lane], (COLD && kcodes) ? k_operand<E>(kv[st]) : kv[st], sc);
     float x[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) x[r] = sc[r] * a.scale_log2;
@@ -668,13 +643,18 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[r2][e][m] *= al;
       }
+    bool vcodes = false;
+    if (COLD && vcold) {
+      vcodes = __builtin_amdgcn_ballot_w64(!scales_moderate<true>(vv)) == 0;
+      if (!vcodes) dequant_regs<E, true>(vv);
+    }
     // P.V: lane 4b' + n of the 4x4x1 MFMA block b' takes position kVPos * s + vpos of the chunk
     // (the four lanes of a block share it) and dims 8 * vdim + e.
 #pragma unroll
     for (int s = 0; s < kVLoads; ++s) {
       float vf[8];
       float vs = 1.0f;  // a quantised position's scale, moved onto its probability
-      if (COLD && codes) {
+      if (COLD && vcodes) {
         v_operand(vv[s], vf);
         vs = e8m0_float(vv[s][2]);
       } else {
@@ -710,12 +690,12 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
         const int j = (i + D - 1) % D;
         if (tc + (D - 1) * kBlock < t_end) load(tc + (D - 1) * kBlock, kr[j], vr[j], cr[j]);
         __builtin_amdgcn_sched_barrier(0);
-        bool codes = false;
+        bool kcodes = false;
         if (COLD && cr[i]) {
-          codes = __builtin_amdgcn_ballot_w64(!chunk_scales_moderate(kr[i], vr[i])) == 0;
-          if (!codes) dequant_chunk<E, kSteps, kVLoads>(kr[i], vr[i]);
+          kcodes = __builtin_amdgcn_ballot_w64(!scales_moderate<false>(kr[i])) == 0;
+          if (!kcodes) dequant_regs<E, false>(kr[i]);
         }
-        compute(tc, kr[i], vr[i], codes);
+        compute(tc, kr[i], vr[i], kcodes, COLD && cr[i]);
         tc += kBlock;
         if (tc >= t_end) goto chunks_done;
       }
