@@ -57,7 +57,7 @@ constexpr int kMaxWaves = 2048;            // resident waves of an MI355X: 256 C
 constexpr int kMinRangeChunks = 4;         // the automatic range never goes below 64 positions
 constexpr int kPairWaves = 8;              // waves of a pair-kernel workgroup
 constexpr int64_t kPairMinPairs = 128;     // the pair kernel from this many (row, kv head) pairs ...
-constexpr int64_t kPairMaxChunks = 40;     // ... of at most this many 16-position chunks (max_seq)
+constexpr int64_t kPairMaxChunks = 44;     // ... of at most this many 16-position chunks (max_seq)
 static_assert(kPairMaxChunks <= kTableEntries, "a pair's blocks fit one table window");
 
 enum : int { kBF16 = 0, kF16 = 1 };
@@ -811,8 +811,11 @@ void attention_pair_kernel(const AttnArgs a) {
   }
   len = max(len, 0);
   const int nch = (len + kBlock - 1) / kBlock;
-  const int c0 = (int)((int64_t)w * nch / W);
-  const int c1 = (int)((int64_t)(w + 1) * nch / W);
+  // The first waves take the remainder: waves 0 .. 3 are each SIMD's first, whose loads are
+  // served first (the second wave on a SIMD gets its first chunk ~1.5 us later).
+  const int base = nch / W, extra = nch - base * W;
+  const int c0 = w * base + min(w, extra);
+  const int c1 = c0 + base + (w < extra ? 1 : 0);
   const int M = a.rows;
   const int rec = (int)record_floats(M, HD);
   attend_piece<HD, E, R, true, OutT, COLD, true>(a, lp[w], lq[w], b, kvh, len, kBlock * c0, min(len, kBlock * c1),

@@ -451,7 +451,7 @@ def attention_leg(cfg, pools, B, dev, reps=20, kv_bytes=None, probe=False):
         raise SystemExit("device error bits set by the attention leg")
     gathered = 3 * (sum(call_bytes) - L * io) / L  # gather reads + writes K/V, attention re-reads
     cold = "<..., COLD> (fp8 pages read as codes)" if getattr(pools[0], "quantized", False) else ""
-    if B * H >= 128 and max_seq <= 640 and G <= 8:  # the library's one-launch bounds
+    if B * H >= 128 and max_seq <= 704 and G <= 8:  # the library's one-launch bounds
         kname = "attention_pair_kernel" + cold + " (one launch per layer)"
     else:
         kname = "attention_flat_kernel" + cold + " + attention_merge_kernel (one launch pair per layer)"

@@ -122,12 +122,12 @@ def test_head_dim_64(dtype, page):
 
 @pytest.mark.parametrize("dtype,page,D", [(torch.bfloat16, 16, 128), (torch.float16, 32, 128), (torch.bfloat16, 16, 64)])
 def test_many_short_pairs_one_launch(dtype, page, D):
-    """128+ (row, kv head) pairs of at most 640 positions with the automatic split take one
+    """128+ (row, kv head) pairs of at most 704 positions with the automatic split take one
     workgroup per pair that merges its waves' partials in LDS (one launch): ragged rows with
     empty, one-position and chunk-boundary lengths, G = 1 / 2 / 4 / 8, two query tokens, both
     output types; the flat schedule (a fixed split) over the same pool agrees."""
     rng = np.random.default_rng(page + D)
-    lens = [600, 0, 1, 15, 16, 17, 31, 33] + rng.integers(0, 600, size=32).tolist()
+    lens = [700, 0, 1, 15, 16, 17, 31, 33] + rng.integers(0, 700, size=32).tolist()
     pool, kd, vd, lens = make_rows(len(lens), 4, page, lens, dtype, seed=page * 3 + D, order_seed=page + D, D=D)
     ws = None
     for i, (G, T) in enumerate([(4, 1), (1, 1), (8, 1), (2, 2), (4, 2)]):
