@@ -234,6 +234,30 @@ __device__ __forceinline__ int range_chunks(const AttnArgs& a, int total) {
   return max(kMinRangeChunks, (total + a.waves - 1) / a.waves);
 }
 
+// Ranges of the flat schedule: [0, na) of pa chunks each, then ranges of pb.  The automatic
+// split at two waves per SIMD (up to 8 query rows) gives the first half of the launch's waves --
+// each SIMD's first, whose loads are served first -- pa = per + per / 16 chunks and the second
+// half pb = per - per / 16, once ranges hold 16 chunks or more (at C2 the second wave on a SIMD
+// got its first chunk ~1.4 us later and streamed ~9 % slower).  Otherwise every range holds per.
+struct RangeMap {
+  int pa, pb, na;
+  __device__ int start(int r) const { return r < na ? r * pa : na * pa + (r - na) * pb; }
+  __device__ int of(int c) const {
+    const int split = na * pa;
+    return c < split ? c / pa : na + (c - split) / pb;
+  }
+};
+__device__ __forceinline__ RangeMap range_map(const AttnArgs& a, int total) {
+  const int per = range_chunks(a, total);
+  RangeMap m{per, per, 0};
+  if (a.range_chunks == 0 && a.rows <= 8 && per >= 16) {
+    m.pa = per + per / 16;
+    m.pb = per - per / 16;
+    m.na = a.waves / 2;
+  }
+  return m;
+}
+
 // The row holding chunk c: the first b with s_incl[b] > c (c < total).
 __device__ __forceinline__ int find_row(const int* s_incl, int batch, int c) {
   int lo = 0, hi = batch - 1;
@@ -761,10 +785,10 @@ void attention_flat_kernel(const AttnArgs a) {
 
   const int lane = threadIdx.x;
   const int total = scan_rows(a, lane, s_len, s_incl, blockIdx.x == 0 && lane == 0);
-  const int per = range_chunks(a, total);
-  for (int r = blockIdx.x; (int64_t)r * per < total; r += gridDim.x) {
-    int c = r * per;
-    const int c_end = min(total, c + per);
+  const RangeMap rm = range_map(a, total);
+  for (int r = blockIdx.x; rm.start(r) < total; r += gridDim.x) {
+    int c = rm.start(r);
+    const int c_end = min(total, rm.start(r + 1));
     while (c < c_end) {
       const int b = find_row(s_incl, a.batch, c);
       const int row_first = b > 0 ? s_incl[b - 1] : 0;
@@ -784,8 +808,8 @@ void attention_flat_kernel(const AttnArgs a) {
 }
 
 // Many short pairs (C2: 16 rows x 8 kv heads, ~650 positions): one workgroup of W waves per
-// (row, kv head).  Wave w streams chunks [w * nch / W, (w + 1) * nch / W) of its pair, leaves its
-// partial record in LDS, and the workgroup folds the W records into the output (same base-2
+// (row, kv head).  Wave w streams nch / W chunks of its pair (one more for the first nch % W
+// waves), leaves its partial record in LDS, and the workgroup folds the W records into the output (same base-2
 // online-softmax fold as the merge kernel): one launch, no global workspace, each pair's bytes
 // read once.  A wave with no chunks leaves a neutral record (maximum -inf, sum 0).
 template <int HD, int E, int R, typename OutT, bool COLD, int W>
@@ -867,7 +891,7 @@ __global__ __launch_bounds__(NT) void attention_merge_kernel(const AttnArgs a) {
     if (tid == 0) s_total = total;
   }
   __syncthreads();
-  const int per = range_chunks(a, s_total);
+  const RangeMap rm = range_map(a, s_total);
   const int nch = (s_len[b] + kBlock - 1) / kBlock;
   const int pair_first = (b > 0 ? s_incl[b - 1] : 0) + kvh * nch;
   if (nch == 0) {
@@ -875,8 +899,8 @@ __global__ __launch_bounds__(NT) void attention_merge_kernel(const AttnArgs a) {
       store_out4<OutT, E>(out_row(a, b, kvh, row) + (int64_t)(4 * tid) * sizeof(OutT), f32x4{0.f, 0.f, 0.f, 0.f});
     return;
   }
-  const int r_first = pair_first / per;
-  const int r_last = (pair_first + nch - 1) / per;
+  const int r_first = rm.of(pair_first);
+  const int r_last = rm.of(pair_first + nch - 1);
   if (r_first == r_last) return;
 
   const int M = a.rows;
