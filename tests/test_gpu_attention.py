@@ -137,6 +137,20 @@ def test_many_short_pairs_one_launch(dtype, page, D):
     assert pool.errors() == 0
 
 
+def test_flat_schedule_with_ranges_of_two_sizes():
+    """16 ragged rows of ~4200 positions over 8 kv heads (over 32k chunks: the automatic split's
+    ranges hold 16+ chunks, so the first half of the waves take larger ones), G = 4 and 8; a
+    fixed split over the same pool agrees."""
+    rng = np.random.default_rng(4242)
+    lens = sorted(rng.integers(4100, 4300, size=16).tolist(), reverse=True)
+    assert sum(-(-x // 16) for x in lens) * 8 >= 16 * 2048
+    pool, kd, vd, lens = make_rows(16, 8, 16, lens, torch.bfloat16, seed=4243, order_seed=4244)
+    ws = check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=1)
+    ws = check(pool, kd, vd, lens, 8, 1, torch.bfloat16, seed=2, ws=ws)
+    check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=3, split_tokens=512)
+    assert pool.errors() == 0
+
+
 def test_llama3_8b_decode_shape():
     """The benchmark's C2 shape: 16 rows x 8 kv heads x 32 q heads, 513 positions, page 16."""
     lens = [513] * 16
