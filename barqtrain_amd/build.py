@@ -78,46 +78,97 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(out, flush=True)
 
 
-def build_library(verbose: bool = False) -> Path:
-    """Compile the HIP kernels and C ABI into barqtrain_amd/libbarq_kv.so."""
-    out = lib_path()
+def object_dir() -> Path:
+    return PKG_DIR / "_build"
+
+
+def build_library(verbose: bool = False, defines: tuple[str, ...] = (), out: Path | None = None) -> Path:
+    """Compile the HIP kernels and C ABI into barqtrain_amd/libbarq_kv.so: every source to an
+    object in parallel (the sources are independent), then one link.  `defines` (``NAME=VALUE``)
+    and `out` build an alternative library from the same sources."""
+    out = out or lib_path()
+    objs = object_dir()
+    objs.mkdir(exist_ok=True)
+    tag = "" if not defines else "-" + "-".join(d.replace("=", "_") for d in defines)
+    procs = []
+    for name in HIP_SOURCES:
+        obj = objs / (Path(name).stem + tag + ".o")
+        cmd = [_hipcc(), *HIP_FLAGS, "-c", f"-I{INCLUDE}", f"-I{CSRC}", *(f"-D{d}" for d in defines),
+               str(CSRC / name), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((cmd, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+    failed = []
+    for cmd, _, proc in procs:
+        text = proc.communicate()[0]
+        if proc.returncode != 0:
+            failed.append(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{text}")
+    if failed:
+        raise RuntimeError("\n".join(failed))
     tmp = out.with_suffix(".so.tmp")
-    cmd = [_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}",
-           *[str(CSRC / name) for name in HIP_SOURCES], "-o", str(tmp)]
-    _run(cmd, verbose)
+    _run([_hipcc(), *HIP_FLAGS, "-shared", *(str(o) for _, o, _ in procs), "-o", str(tmp)], verbose)
     os.replace(tmp, out)
     return out
 
 
-def build_extension(verbose: bool = False) -> Path:
-    """Compile the torch binding module barqtrain_cuda next to the library."""
+def _extension_commands(obj: Path, tmp: Path) -> tuple[list[str], list[str]]:
+    """(compile, link) commands of the torch binding module."""
     import torch
     from torch.utils import cpp_extension
 
-    out = ext_path()
-    tmp = out.with_name(out.name + ".tmp")
     torch_lib = Path(torch.__file__).resolve().parent / "lib"
     rocm = os.environ.get("ROCM_PATH") or "/opt/rocm"
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
-    cmd = [
-        os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared",
+    compile_cmd = [
+        os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-c",
         f"-DTORCH_EXTENSION_NAME={EXT_NAME}", "-DTORCH_API_INCLUDE_EXTENSION_H",
         f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
         *[f"-I{p}" for p in cpp_extension.include_paths(device_type="cuda")],
         f"-I{rocm}/include", f"-I{sysconfig.get_paths()['include']}", f"-I{INCLUDE}",
-        *(str(CSRC / f) for f in HOST_SOURCES),
+        *(str(CSRC / f) for f in HOST_SOURCES), "-o", str(obj),
+    ]
+    link_cmd = [
+        os.environ.get("CXX", "g++"), "-shared", str(obj),
         f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-ltorch_hip",
         f"-L{PKG_DIR}", "-lbarq_kv", "-Wl,-rpath,$ORIGIN",
         "-o", str(tmp),
     ]
-    _run(cmd, verbose)
+    return compile_cmd, link_cmd
+
+
+def build_extension(verbose: bool = False, compiled: subprocess.Popen | None = None) -> Path:
+    """Compile the torch binding module barqtrain_cuda next to the library (its object may
+    already be compiling: `compiled`, started by build())."""
+    out = ext_path()
+    tmp = out.with_name(out.name + ".tmp")
+    object_dir().mkdir(exist_ok=True)
+    obj = object_dir() / "barq_kv_torch.o"
+    compile_cmd, link_cmd = _extension_commands(obj, tmp)
+    if compiled is None:
+        _run(compile_cmd, verbose)
+    else:
+        text = compiled.communicate()[0]
+        if compiled.returncode != 0:
+            raise RuntimeError(f"build step failed ({compiled.returncode}): {' '.join(compile_cmd)}\n{text}")
+    _run(link_cmd, verbose)
     os.replace(tmp, out)
     return out
 
 
 def build(verbose: bool = False) -> None:
-    build_library(verbose)
-    build_extension(verbose)
+    """Both parts; the binding's object compiles while the HIP sources do."""
+    object_dir().mkdir(exist_ok=True)
+    compile_cmd, _ = _extension_commands(object_dir() / "barq_kv_torch.o", ext_path())
+    if verbose:
+        print(" ".join(compile_cmd), flush=True)
+    ext_proc = subprocess.Popen(compile_cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    try:
+        build_library(verbose)
+    except BaseException:
+        ext_proc.kill()
+        ext_proc.wait()
+        raise
+    build_extension(verbose, compiled=ext_proc)
 
 
 def is_built() -> bool:

@@ -273,7 +273,7 @@ int barq_kv_decode_attention(const barq_kv_pool* pool, const void* query, int64_
                              void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Bytes of the static device scratch behind barq_kv_decode_attention_noalloc (per GPU). */
-#define BARQ_KV_SCRATCH_BYTES (16 * 1024 * 1024)
+#define BARQ_KV_SCRATCH_BYTES (24 * 1024 * 1024)
 
 /*
  * No counterpart in the reference.  For callers that cannot allocate device memory -- code under
@@ -282,8 +282,10 @@ int barq_kv_decode_attention(const barq_kv_pool* pool, const void* query, int64_
  * (BARQ_KV_SCRATCH_BYTES on each GPU it runs on, held until the process ends) instead of an
  * argument.  Arguments, results and errors as barq_kv_decode_attention; a launch whose workspace
  * (barq_kv_attention_workspace_bytes) exceeds BARQ_KV_SCRATCH_BYTES returns BARQ_KV_ERR_SCRATCH
- * and enqueues nothing (16 MiB holds every batch <= 64 with 8 KV heads, G * tokens <= 16 and the
- * automatic split).  The workspace needs no initialisation, so calls clear nothing.  Every call on
+ * and enqueues nothing.  With the automatic split the workspace is (2048 + batch * kv_heads)
+ * records of (G * tokens) * (head_dim + 2) floats, so 24 MiB holds every batch <= 64 with 8 KV heads
+ * and head_dim 128 at G * tokens <= 16 (21.3 MB at the largest); batch 1024 at that shape needs
+ * 85 MB and is refused.  The workspace needs no initialisation, so calls clear nothing.  Every call on
  * a GPU uses that GPU's one array: calls that overlap on one GPU (other streams, other host
  * threads) race on it; order them on one stream.  The first call on a device resolves the array's
  * address there; the call allocates nothing.
@@ -353,9 +355,15 @@ int barq_kv_gather_cold(const barq_kv_pool* pool, const barq_kv_cold* cold, void
 /* barq_kv_append + barq_kv_compress + barq_kv_gather_cold.  When tokens <= window, batch <= 64
  * and the pool holds two-byte elements whose token rows are 64, 128 or 256 vectors of 16 bytes
  * (every address and stride 16-byte aligned, codes and key scales 8-byte), in two launches: the
- * compress for the lengths the rows reach, then one launch that appends and gathers -- as for
- * barq_kv_update, a row whose new end passes seq_out loses the tokens past it and raises
- * BARQ_KV_ERRBIT_OUT_SHORT; else in three launches.  The results are the same either way.
+ * compress for the lengths the rows reach, then one launch that appends and gathers; else in three
+ * launches (append, compress, gather).  The two forms return the same K/V and leave the same
+ * pool, with one exception: in the two-launch form, as for barq_kv_update, a row whose new end
+ * passes seq_out does not store the tokens past seq_out in its pages (BARQ_KV_ERRBIT_OUT_SHORT is
+ * raised), while the three-launch form stores them.  The compress of the two-launch form runs
+ * before the append: if the second launch then fails (BARQ_KV_ERR_LAUNCH), the blocks that leave
+ * the window at the lengths the rows would have reached are already quantised (they are whole
+ * blocks at the current lengths too, so the pool stays consistent and the lengths unchanged; a
+ * gather returns their dequantised values).
  * flags: BARQ_KV_SEQ_FROM_DEVICE as for the gather; BARQ_KV_NO_COMPRESS skips the compress launch
  * -- for a caller that knows no row's block leaves the window in this call (every page_size-th
  * token). */
