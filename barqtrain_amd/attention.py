@@ -10,8 +10,10 @@ the whole history (and its write and re-read) disappears.  Prefill, padded batch
 head sizes take the gathered K/V through torch's fused SDPA kernels (flash or memory-efficient,
 grouped-query heads without copies, bottom-right causal); host tensors, and shapes no fused
 kernel takes, an fp32 attention.  Calls without a paged cache go to transformers' SDPA path.
-Options the paged path does not implement (logit soft-capping, attention sinks, sliding
-windows, dropout) raise instead of being ignored.
+Layers with options the kernel does not implement -- logit soft-capping (Gemma 2), attention
+sinks (``s_aux``, gpt-oss), dropout, or a sliding window that cuts the row -- attend over the
+gathered K/V: a sliding window alone (whose mask transformers builds) through fused SDPA, the
+others through the fp32 attention, which applies each option as the models' own attention does.
 
 The kernel's numbers are fp32 throughout (scores from exact bf16/fp16 products, fp32 softmax and
 P.V), so logits track an fp32 reference more closely than the default bf16 attention does.
@@ -40,25 +42,41 @@ def paged_kv_view(layer, like: torch.Tensor, seq: int) -> torch.Tensor:
     return view
 
 
-def _fp32_attention(query, key, value, attention_mask, scale):
+def _fp32_attention(query, key, value, attention_mask, scale, softcap=None, sinks=None, sliding_window=None,
+                    dropout=0.0):
     """Reference-precision attention over gathered K/V: q [B, Hq, T, D], k/v [B, Hkv, S, D];
-    bottom-right causal when no mask is given; returns [B, T, Hq, D] in the query's dtype."""
+    bottom-right causal when no mask is given; returns [B, T, Hq, D] in the query's dtype.
+    Options as the models that use them apply them: `softcap` caps the scaled scores to
+    softcap * tanh(s / softcap) before the mask (Gemma 2); `sinks` [Hq] is one extra logit per
+    head that takes part in the softmax and is then dropped (gpt-oss); `sliding_window` W lets
+    query position q see key positions k with q - W < k <= q (transformers' sliding-window
+    overlay); `dropout` drops probabilities (training only)."""
     B, Hq, T, D = query.shape
     group = Hq // key.shape[1]
     q = query.float()
     k = key.float().repeat_interleave(group, dim=1)
     v = value.float().repeat_interleave(group, dim=1)
     scores = torch.matmul(q, k.transpose(-1, -2).contiguous()) * scale
+    if softcap is not None:
+        scores = torch.tanh(scores / softcap) * softcap
     S = k.shape[2]
+    pos = torch.arange(S, device=q.device)
+    qpos = S - T + torch.arange(T, device=q.device)
     if attention_mask is None:
-        pos = torch.arange(S, device=q.device)
-        limit = S - T + torch.arange(T, device=q.device)
-        scores = scores.masked_fill(pos[None, :] > limit[:, None], float("-inf"))
+        scores = scores.masked_fill(pos[None, :] > qpos[:, None], float("-inf"))
     elif attention_mask.dtype == torch.bool:
         scores = scores.masked_fill(~attention_mask[..., :S], float("-inf"))
     else:
         scores = scores + attention_mask[..., :S].float()
-    probs = torch.softmax(scores, dim=-1).nan_to_num(0.0)
+    if sliding_window is not None:
+        scores = scores.masked_fill(pos[None, :] <= qpos[:, None] - sliding_window, float("-inf"))
+    if sinks is not None:
+        sink = sinks.float().to(q.device).reshape(1, Hq, 1, 1).expand(B, Hq, T, 1)
+        probs = torch.softmax(torch.cat([scores, sink], dim=-1), dim=-1)[..., :-1]
+    else:
+        probs = torch.softmax(scores, dim=-1).nan_to_num(0.0)
+    if dropout:
+        probs = F.dropout(probs, p=dropout, training=True)
     return torch.matmul(probs, v).transpose(1, 2).contiguous().to(query.dtype)
 
 
@@ -112,24 +130,32 @@ def paged_attention_forward(module: torch.nn.Module, query: torch.Tensor, key: t
 
         return sdpa_attention_forward(module, query, key, value, attention_mask, scaling=scaling,
                                       dropout=dropout, **kwargs)
-    unsupported = [name for name in ("softcap", "s_aux", "sliding_window") if kwargs.get(name) is not None]
-    if dropout:
-        unsupported.append("dropout")
-    if unsupported:
-        raise NotImplementedError(
-            f"barq_paged attention does not implement {', '.join(unsupported)}; use another attention "
-            "implementation (the paged cache works with any: create_paged_kv_cache(..., fused_attention=False))")
+    softcap, sinks, window = kwargs.get("softcap"), kwargs.get("s_aux"), kwargs.get("sliding_window")
+    if not module_training(module):
+        dropout = 0.0
+    # A window cuts the row only when some query sees fewer positions than it holds.
+    window_cuts = window is not None and key.shape[2] > int(window)
+    options = softcap is not None or sinks is not None or bool(dropout)
     pool = layer.pool
     _, q_heads, tokens, head_dim = query.shape
     scale = scaling if scaling is not None else 1.0 / math.sqrt(head_dim)
     rows = (q_heads // pool.kv_heads) * tokens
-    kernel_ok = (attention_mask is None and rows <= _KERNEL_MAX_ROWS and pool.on_gpu
-                 and (not getattr(pool, "quantized", False) or pool.page_size % 16 == 0)
+    kernel_ok = (not options and not window_cuts and attention_mask is None and rows <= _KERNEL_MAX_ROWS
+                 and pool.on_gpu and (not getattr(pool, "quantized", False) or pool.page_size % 16 == 0)
                  and pool.dtype in (torch.bfloat16, torch.float16) and pool.head_dim in (64, 128))
     if kernel_ok:
         return pool.attend(query, scale).transpose(1, 2), None
     k, v = layer.current_tensors()
+    if options or (window_cuts and attention_mask is None):
+        return _fp32_attention(query, k, v, attention_mask, scale, softcap=softcap, sinks=sinks,
+                               sliding_window=window if window_cuts else None, dropout=dropout), None
+    # no option, or a window that the mask transformers built already applies
     return _gathered_attention(query, k, v, attention_mask, scale), None
+
+
+def module_training(module) -> bool:
+    """Dropout applies while the attention module trains (as in the models' own attention)."""
+    return bool(getattr(module, "training", False))
 
 
 def register() -> str:

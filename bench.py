@@ -37,8 +37,10 @@ and `traffic_measured` gives the counter ratio and the window it was measured at
 `cpu_baseline` is the reference CPU path -- the reference layer's per-(row, token) append and its
 view + .contiguous() gather, restated in torch (oracle/kv_oracle_torch.py, checked against the
 numpy oracle) -- on the host's cores (torch.set_num_threads), over the same input bits and the
-same window (C1/C2: 8 of the layers; larger configs: layer 0), timing the decode updates only;
-`numpy_one_thread` beside it (C1/C2) is the numpy oracle on one core.  The same run checks the
+GPU's own window (C1/C2: every layer; larger configs: layer 0 over the window's first steps, x L),
+timing the decode updates only, step by step: the median step after one warm-up step (`total`
+keeps the rate over the summed steps); `numpy_one_thread` beside it (C1/C2) is the numpy oracle on
+one core.  The same run checks the
 GPU's layer-0 K/V after the window bit for bit against it (`parity`).
 
 `paged_attention` (bf16/fp16 configurations) times the decode-attention kernel that reads K/V
@@ -82,7 +84,7 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 HBM_PEAK_GBS = 8000.0
-CPU_BASELINE_SECONDS = 10.0  # timed CPU work the baseline repeats its sample to reach (at most 8 passes)
+CPU_BASELINE_SECONDS = 10.0  # CPU work (timed window and the untimed steps before it) the baseline repeats passes to reach (at most 8)
 METRIC = "paged KV append+gather GB/s (% HBM peak); µs per decode-step cache update"
 KERNEL = ("stream kernel, fused append + gather, one launch per layer: lean_stream_kernel<8, 2> (1-page tiles; "
           "lean_balanced_kernel<8, 2>, equal unaligned chunks, when their count is not a multiple of the CUs) while "
@@ -228,13 +230,18 @@ def host_threads():
 
 
 def cpu_baseline(cfg, wl, start, steps, layers):
-    """The reference CPU path (oracle/kv_oracle_torch.py) on the host's cores: `layers` layers,
-    each prefilled untimed, then decode steps [first, start + steps) timed, where first is 0 for
-    C1/C2 (the steps before the window and the window) and the window's start for the larger
-    configurations (churned rows are freed and re-prefilled between steps, untimed); the layers
-    are run again until about CPU_BASELINE_SECONDS of timed work.  Returns (result, layer-0 K/V
-    after the window, as torch tensors).  For C1/C2 the numpy oracle on one core times layer 0
-    beside it."""
+    """The reference CPU path (oracle/kv_oracle_torch.py) on the host's cores, timed as the
+    measurement plan says: `layers` layers, each prefilled untimed and run through the steps
+    before the window untimed, then one warm-up step (the step before the window; when the window
+    starts at step 0, its first step, which the median then leaves out) and the GPU's own window
+    of decode steps [start, start + steps) timed one step at a time with the host clock (churned
+    rows are freed and re-prefilled between steps, untimed).  A step's time is the sum over the
+    layers (times L / layers when fewer layers run); `ms_per_step` is the median over the
+    window's steps, pooled over passes (passes repeat the layers until about CPU_BASELINE_SECONDS
+    of work, at most 8).  `total` keeps the rate over every timed step (bytes over summed time).
+    Returns (result, layer-0 K/V after the window, as torch tensors).  For C1/C2 the numpy oracle
+    on one core times layer 0 beside it the same way."""
+    import numpy as np
     import torch
 
     from oracle.kv_oracle import DenseLayerOracle
@@ -243,18 +250,20 @@ def cpu_baseline(cfg, wl, start, steps, layers):
     B, P, L = cfg["batch"], cfg["page"], cfg["layers"]
     cap = max(prefill_lengths(cfg)) + wl.n_steps
     refill = tuple(t.cpu() for t in wl.refill) if wl.refill is not None else None
-    first = 0 if cfg["cpu_steps"] is None else start
+    n = start + steps
+    warm = 1 if start == 0 else 0  # the window's first step is the warm-up when nothing precedes it
     threads = host_threads()
     prev = torch.get_num_threads()
     torch.set_num_threads(threads)
 
     def timed_layer(ref, layer, to_input):
+        """Per-step seconds of steps [start, n) of one layer, and its last output."""
         for k, v in wl.prefill_inputs(layer):
             ref.append(to_input(k), to_input(v))
-        kd = [to_input(wl.k_dec[s, layer]) for s in range(start + steps)]
-        vd = [to_input(wl.v_dec[s, layer]) for s in range(start + steps)]
-        spent, out = 0.0, None
-        for s in range(start + steps):
+        kd = [to_input(wl.k_dec[s, layer]) for s in range(n)]
+        vd = [to_input(wl.v_dec[s, layer]) for s in range(n)]
+        spent, out = np.zeros(steps), None
+        for s in range(n):
             rows = wl.churn[s]
             if rows:
                 ref.release_rows(rows)
@@ -262,43 +271,56 @@ def cpu_baseline(cfg, wl, start, steps, layers):
                     ref.append_rows(rows, to_input(refill[0]), to_input(refill[1]))
             t0 = time.perf_counter()
             out = ref.update(kd[s], vd[s])
-            if s >= first:
-                spent += time.perf_counter() - t0
+            if s >= start:
+                spent[s - start] = time.perf_counter() - t0
         return spent, out
 
+    def summarise(per_pass):
+        """(median seconds per step over the pooled window steps, summed seconds) for per-pass arrays
+        of per-step seconds over the layers run."""
+        pooled = np.concatenate([p[warm:] for p in per_pass]) * (L / layers)
+        return float(np.median(pooled)), float(sum(p.sum() for p in per_pass))
+
     try:
-        # Passes over the layers until about CPU_BASELINE_SECONDS of timed work (at most 8).
-        total, final, passes = 0.0, None, 0
-        while passes < 8 and (passes == 0 or total < CPU_BASELINE_SECONDS):
+        per_pass, final, passes, wall0 = [], None, 0, time.perf_counter()
+        while passes < 8 and (passes == 0 or time.perf_counter() - wall0 < CPU_BASELINE_SECONDS):
+            step_s = np.zeros(steps)
             for layer in range(layers):
                 spent, out = timed_layer(DenseLayerTorch(B, cap, P), layer, lambda t: t.cpu())
-                total += spent
+                step_s += spent
                 if layer == 0 and passes == 0:
                     final = out
+            per_pass.append(step_s)
             passes += 1
     finally:
         torch.set_num_threads(prev)
-    n = start + steps
-    nbytes = sum(wl.step_bytes[first:n]) * layers / L * passes
+    med, total = summarise(per_pass)
+    window_bytes = np.asarray(wl.step_bytes[start:n], dtype=np.float64)
+    step_bytes = float(window_bytes[warm:].mean()) if steps > warm else float(window_bytes.mean())
     result = {
-        "value": round(nbytes / total / 1e9, 3),
+        "value": round(step_bytes / med / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{passes} pass(es) of {layers} of {L} layers x decode steps {first}..{n - 1} (the GPU's timed window is steps "
-                  f"{start}..{n - 1}; append 1 token x {B} rows + materialised gather), torch restatement of "
-                  f"the reference kv_cache.py _python_append + current_tensors (view + .contiguous()) on "
-                  f"{threads} threads; same input bits",
-        "ms_per_step": round(total / passes / (n - first) * L / layers * 1e3, 3),
-        "seconds": round(total, 2),
+        "sample": f"decode steps {start}..{n - 1} (the GPU's timed window; append 1 token x {B} rows + materialised "
+                  f"gather), {layers} of {L} layers" + ("" if layers == L else f" (x{L // layers} extrapolated)")
+                  + f", median step of {passes} pass(es) after one warm-up step; torch restatement of the reference "
+                  f"kv_cache.py _python_append + current_tensors (view + .contiguous()) on {threads} threads; "
+                  f"same input bits",
+        "ms_per_step": round(med * 1e3, 3),
+        "total": {"value": round(float(window_bytes.sum()) * layers / L * passes / total / 1e9, 3),
+                  "seconds": round(total, 2),
+                  "note": "every timed step of every pass: window bytes over summed step time"},
     }
     if cfg["cpu_steps"] is None:  # C1/C2: the numpy oracle on one core, layer 0
         from kvgen import to_bits
 
         spent, _ = timed_layer(DenseLayerOracle(B, cap, P), 0, to_bits)
-        result["numpy_one_thread"] = {"value": round(nbytes / passes / layers / spent / 1e9, 3), "cores": 1,
-                                      "ms_per_step": round(spent / (n - first) * L * 1e3, 3),
-                                      "sample": f"layer 0 x decode steps {first}..{n - 1}, numpy oracle"}
+        med1 = float(np.median(spent[warm:] if steps > warm else spent)) * L
+        result["numpy_one_thread"] = {"value": round(step_bytes / med1 / 1e9, 3), "cores": 1,
+                                      "ms_per_step": round(med1 * 1e3, 3),
+                                      "sample": f"layer 0 x decode steps {start}..{n - 1} (x{L} layers), median step, "
+                                                f"numpy oracle"}
     return result, final
 
 
@@ -758,13 +780,25 @@ def pmc_probe(cfg, wl, start, steps, run_step, dev, quant):
         quant_leg(cfg, wl, steps, dev, 0.0, probe=lambda: calibration_pass(dev))
         print(json.dumps({"pmc_probe": "quant", "config": cfg["name"], "steps": steps}), flush=True)
         return
+    def progress(what, s):
+        # A counter run serialises every dispatch and reads the counters after each one, so a
+        # long probe is slow, not hung: a line every 16 steps (after the GPU has finished them)
+        # shows how far it got.
+        if s % 16 == 15:
+            torch.cuda.synchronize()
+            print(f"pmc-probe: {what} step {s} done", file=sys.stderr, flush=True)
+
     wl.prefill()
+    print("pmc-probe: prefill enqueued", file=sys.stderr, flush=True)
     for s in range(start):
         run_step(s)
+        progress("pre-window", s)
     calibration_pass(dev)
     for s in range(start, start + steps):
         run_step(s)
+        progress("window", s)
     torch.cuda.synchronize()
+    print("pmc-probe: window done", file=sys.stderr, flush=True)
     attn = cfg["dtype"] in ("bfloat16", "float16") and cfg["dim"] == 128
     if attn:
         attention_leg(cfg, wl.pools, cfg["batch"], dev, reps=1, probe=True)

@@ -383,6 +383,65 @@ def test_paged_route_head_dim_64_and_padded_batch(hip, monkeypatch):
     assert (seq == ref_seq).float().mean().item() >= 0.9
 
 
+def gemma2_bf16(softcap, seed=0):
+    from transformers import Gemma2Config, Gemma2ForCausalLM
+
+    torch.manual_seed(seed)
+    # Gemma 2's options: a sliding window (16 positions) on every other layer and, when given,
+    # logit soft-capping; head_dim 128 with 4 query heads over 2 kv heads
+    cfg = Gemma2Config(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                       num_attention_heads=4, num_key_value_heads=2, head_dim=128, max_position_embeddings=1024,
+                       sliding_window=16, attn_logit_softcapping=softcap, final_logit_softcapping=None,
+                       query_pre_attn_scalar=128, pad_token_id=0, eos_token_id=None, bos_token_id=1)
+    return Gemma2ForCausalLM(cfg).to(torch.bfloat16).eval(), cfg
+
+
+@pytest.mark.parametrize("softcap", [None, 20.0], ids=["window", "window_softcap"])
+def test_paged_route_sliding_window_and_softcap_on_gpu(hip, monkeypatch, softcap):
+    """The "barq_paged" route on a bf16 Gemma 2 on the GPU: full-attention layers decode through the
+    page kernel, sliding-window layers past their window attend over the gathered K/V under the
+    window mask transformers builds, soft-capped layers through the fp32 attention that applies
+    the cap -- token by token against the same route with every call on the fp32 attention (the
+    kernel and fused SDPA off): logits agree to bf16 rounding, greedy tokens agree."""
+    pytest.importorskip("transformers")
+    from barqtrain import create_paged_kv_cache
+    from barqtrain_amd import attention
+    from barqtrain_amd.paged import PagePool
+
+    model, cfg = gemma2_bf16(softcap)
+    model = model.to("cuda")
+    attention.enable_paged_attention(model)
+    prompt, new = 37, 20
+    seq = torch.randint(2, 512, (2, prompt + new), generator=torch.Generator().manual_seed(9)).to("cuda")
+    calls = []
+    attend = PagePool.attend
+    monkeypatch.setattr(PagePool, "attend", lambda self, *a, **k: calls.append(1) or attend(self, *a, **k))
+
+    def run(reference: bool):
+        if reference:
+            monkeypatch.setattr(attention, "_KERNEL_MAX_ROWS", 0)
+            monkeypatch.setattr(attention, "_sdpa_attention", lambda *a: None)
+        cache = create_paged_kv_cache(model, max_batch_size=2, max_cache_len=prompt + new, page_size=16)
+        steps = []
+        with torch.no_grad():
+            out = model(seq[:, :prompt], past_key_values=cache, use_cache=True)
+            steps.append(out.logits[:, -1].float())
+            for t in range(new - 1):
+                out = model(seq[:, prompt + t:prompt + t + 1], past_key_values=cache, use_cache=True)
+                steps.append(out.logits[:, -1].float())
+        assert all(layer.pool.errors() == 0 for layer in cache.layers)
+        return torch.stack(steps)
+
+    routed = run(False)
+    # the full-attention layer (every other one) runs the kernel when nothing caps its scores
+    assert len(calls) == (0 if softcap else (new - 1) * cfg.num_hidden_layers // 2), len(calls)
+    reference = run(True)
+    scale = reference.abs().max().item()
+    err = (routed - reference).abs().max().item()
+    assert err <= 0.02 * scale, f"logits differ by {err} (scale {scale})"
+    assert (routed.argmax(-1) == reference.argmax(-1)).float().mean().item() >= 0.9
+
+
 def test_long_prefill_stays_within_memory(hip):
     """A 16k-token prefill of one row through the paged route: attention over the gathered K/V
     runs in fused SDPA (no [heads, T, S] score tensor: that would be 32 GiB in fp32); the last
