@@ -88,8 +88,7 @@ def test_refill_freed_rows_on_gpu_pool(dtype, page, seed):
     assert torch.cuda.is_available(), "GPU test collected without a visible GPU"
     B, H, D, ctx, steps = 8, 8, 128, 64, 24
     cap = 2 * ctx + steps + 2
-    live = B * -(-ctx // page)
-    num_pages = int(np.ceil(live / 0.9)) + 2 * -(-ctx // page)
+    num_pages = B * -(-cap // page)  # every row can reach the capacity
     pool = PagePool(max_batch=B, max_blocks=-(-cap // page), page_size=page, kv_heads=H, head_dim=D,
                     dtype=dtype, device="cuda", num_pages=num_pages)
     oracle = DenseLayerOracle(B, cap, page)
