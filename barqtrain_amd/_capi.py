@@ -70,6 +70,8 @@ _SIGNATURES = {
     "barq_kv_gather": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_ptr, c_ptr] + [c_i64] * 6 + [c_ptr]),
     "barq_kv_update": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_ptr, c_ptr] + [c_i64] * 5
                        + [c_ptr, c_ptr] + [c_i64] * 5 + [c_ptr]),
+    "barq_kv_update_known": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_ptr, c_ptr] + [c_i64] * 5
+                             + [c_ptr, c_ptr] + [c_i64] * 4 + [c_ptr, c_ptr, c_i64, c_ptr]),
     "barq_kv_crop": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_i64, c_i64, c_ptr]),
     "barq_kv_free_rows": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), c_ptr, c_i64, c_ptr]),
     "barq_kv_copy_rows": (ctypes.c_int, [ctypes.POINTER(BarqKVPool), ctypes.POINTER(BarqKVPool), c_ptr, c_i64, c_ptr]),

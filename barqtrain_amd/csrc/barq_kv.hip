@@ -634,6 +634,9 @@ __global__ void __launch_bounds__(kStreamThreads) stream_kernel_any(const Stream
 // 16 (75 VGPRs: six waves per SIMD).
 constexpr int64_t kLeanResidentTilesPerCU = 5;
 constexpr int64_t kLeanResidentTilesPerCU16 = 4;
+// Known-state launches of at most this many tiles store back to back (batch 1 at the C2 shape,
+// context 650: 5.08 -> 4.97 us per launch); larger ones keep one store in flight per wave.
+constexpr unsigned kKnownBackToBackTiles = 256;
 
 // Page of block `blk`, the k-th block a lean tile touches (touched = nbl - k > 0): its table
 // entry for an old block, the stack entry of its rank for a new one; -1 when unmapped.
@@ -774,6 +777,131 @@ __global__ void __launch_bounds__(kStreamThreads) lean_stream_kernel(const Strea
     if (j < nval) {
       const int s = lo + j;
       wait_vm<0>();
+      st_stream<V>(out_row + (uint32_t)s * oss + out_lane, val[u]);
+      if ((unsigned)(s - len) < (unsigned)T) {
+        const bool second = j >= P;
+        const int64_t pb = second ? pb1 : pb0;
+        if (pb >= 0) *(V*)(pages + pb + (uint32_t)(second ? j - P : j) * tokb + page_lane) = val[u];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Lean update with the row state known to the caller (barq_kv_update_known: an eager caller whose
+// host shadow holds the rows' lengths and marks and the stack top exactly).  The state arrives
+// in the kernel arguments, so no tile reads seq_lens, high_water or the stack top, and the
+// commit cannot race a tile's read: the first tile's control wave commits at once, with no
+// arrival counters.  The block-table entries a tile reads (blocks mapped before the launch) and
+// the stack entries new blocks take are not written by the commit.  A launch of at most one
+// tile per CU (the memory system far from busy) issues its stores back to back.
+// ---------------------------------------------------------------------------------------------
+
+struct KnownState {
+  int32_t len[kWave];
+  int32_t hw[kWave];
+  int32_t top;
+};
+
+template <int NU, int LPP>
+__global__ void __launch_bounds__(kStreamThreads) lean_known_kernel(const StreamArgs a, const KnownState ks) {
+  using V = typename VecT<16>::T;
+  constexpr int RSTEP = 4 / LPP;
+  const barq_kv_pool& p = a.pool;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+  const int lane = (int)(threadIdx.x & (kWave - 1));
+  const int bid = (int)blockIdx.x;
+  const int T = a.tokens;
+  const int mb = (int)p.max_blocks;
+
+  if (wave == 0) {
+    if (bid != 0 || T <= 0) return;
+    const int clen = lane < a.batch ? ks.len[lane] : 0;
+    const int chw = lane < a.batch ? ks.hw[lane] : 0;
+    const int news = wave_sum(lane < a.batch ? new_blocks(clen, chw, T, mb, a.div_page).count : 0);
+    const int fidx = ks.top - 1 - lane;
+    const int cfree = news > 0 && fidx >= 0 ? p.free_pages[fidx] : -1;
+    commit_from_lanes(p, a.batch, T, a.seq_out, a.div_page, clen, chw, ks.top, cfree);
+    return;
+  }
+
+  const int kv = bid & 1;
+  const int rest = bid >> 1;
+  const int b = (int)a.div_chunks.div((uint32_t)rest);
+  const int c = rest - b * (int)a.div_chunks.d;
+  const int P = (int)p.page_size;
+  const int len = ks.len[b];
+  const int hw = ks.hw[b];
+  const int blk0 = c * a.ppt;
+  const int e0 = p.block_table[(int64_t)b * mb + blk0];
+  int e1 = -1;
+  if (a.ppt > 1 && blk0 + 1 < mb) e1 = p.block_table[(int64_t)b * mb + blk0 + 1];
+  const int lo = c * a.chunk;
+  const int hi = min(lo + a.chunk, a.seq_out);
+  if (hi <= lo) return;
+  const NewBlocks nb = new_blocks(len, hw, T, mb, a.div_page);
+  const int nbl = a.ppt > 1 ? 2 : 1;
+  int base = 0;
+  if (nb.count > 0 && blk0 < nb.first + nb.count && blk0 + nbl > nb.first)
+    base = wave_sum(lane < b ? new_blocks(ks.len[lane], ks.hw[lane], T, mb, a.div_page).count : 0);
+  const int pg0 = lean_page(p, nb, blk0, nbl, mb, ks.top, base, e0);
+  const int pg1 = lean_page(p, nb, blk0 + 1, nbl - 1, mb, ks.top, base, e1);
+  const int64_t pb0 = pg0 >= 0 ? (int64_t)pg0 * a.page_bytes : (int64_t)-1;
+  const int64_t pb1 = pg1 >= 0 ? (int64_t)pg1 * a.page_bytes : (int64_t)-1;
+
+  const int cw = wave - 1;
+  const int r0 = cw / LPP;
+  const int col = (cw % LPP) * kWave + lane;
+  const int h = (int)a.div_vr.div((uint32_t)col);
+  const int v = col - h * (int)a.div_vr.d;
+  const uint32_t page_lane = (uint32_t)(col * 16);
+  const uint32_t out_lane = (uint32_t)((int64_t)h * a.out_sh + (int64_t)v * 16);
+  const uint32_t in_lane = (uint32_t)((int64_t)h * a.in_sh + (int64_t)v * 16);
+  const uint32_t tokb = (uint32_t)a.tok_bytes;
+  const uint32_t oss = (uint32_t)a.out_ss;
+  const uint32_t ist = (uint32_t)a.in_st;
+  const char* in_row = (kv ? a.in_v : a.in_k) + (int64_t)b * a.in_sb;
+  char* out_row = (kv ? a.out_v : a.out_k) + (int64_t)b * a.out_sb;
+  char* pages = (char*)(kv ? p.value_pages : p.key_pages);
+  const int nval = hi - lo;
+  V val[NU];
+  if (hi <= max(hw, len + T) && pb0 >= 0 && (nval <= P || pb1 >= 0)) {
+    // Every position holds data on mapped pages: branch-free loads, back to back (positions past
+    // the tile repeat its last one, a cache hit).
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int j = min(r0 + u * RSTEP, nval - 1);
+      const int s = lo + j;
+      const bool second = j >= P;
+      const char* page_pos = pages + (second ? pb1 : pb0) + (uint32_t)(second ? j - P : j) * tokb;
+      const bool fresh = (unsigned)(s - len) < (unsigned)T;
+      val[u] = ld_stream<V>(fresh ? in_row + (uint32_t)(s - len) * ist + in_lane : page_pos + page_lane);
+    }
+  } else {
+    // Zero padding, unmapped blocks (an exhausted pool) or positions never written.
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int j = r0 + u * RSTEP;
+      const int s = lo + j;
+      val[u] = zero_vec<V>();
+      if (j < nval) {
+        const bool second = j >= P;
+        const int64_t pb = second ? pb1 : pb0;
+        if ((unsigned)(s - len) < (unsigned)T) {
+          val[u] = ld_stream<V>(in_row + (uint32_t)(s - len) * ist + in_lane);
+        } else if (s < hw && pb >= 0) {
+          val[u] = ld_stream<V>(pages + pb + (uint32_t)(second ? j - P : j) * tokb + page_lane);
+        }
+      }
+    }
+  }
+  const bool paced = gridDim.x > kKnownBackToBackTiles;
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int j = r0 + u * RSTEP;
+    if (j < nval) {
+      const int s = lo + j;
+      if (paced) wait_vm<0>();
       st_stream<V>(out_row + (uint32_t)s * oss + out_lane, val[u]);
       if ((unsigned)(s - len) < (unsigned)T) {
         const bool second = j >= P;
@@ -1632,6 +1760,26 @@ int launch_lean_kernel(int nu, int lpp, dim3 grid, StreamArgs* arg, hipStream_t 
 #undef BARQ_LEAN_FN
 }
 
+int launch_known_kernel(int nu, int lpp, dim3 grid, StreamArgs* arg, const KnownState* known, hipStream_t stream) {
+  const void* fn = nullptr;
+#define BARQ_KNOWN_CASE(NU)                                              \
+  switch (lpp) {                                                         \
+    case 1: fn = (const void*)&lean_known_kernel<NU, 1>; break;          \
+    case 2: fn = (const void*)&lean_known_kernel<NU, 2>; break;          \
+    default: fn = (const void*)&lean_known_kernel<NU, 4>; break;         \
+  }
+  switch (nu) {
+    case 4: BARQ_KNOWN_CASE(4) break;
+    case 8: BARQ_KNOWN_CASE(8) break;
+    default: BARQ_KNOWN_CASE(16) break;
+  }
+#undef BARQ_KNOWN_CASE
+  KnownState ks = *known;
+  void* args[] = {arg, &ks};
+  return hipLaunchKernel(fn, grid, dim3(kStreamThreads), args, 0, stream) == hipSuccess ? BARQ_KV_OK
+                                                                                      : BARQ_KV_ERR_LAUNCH;
+}
+
 BARQ_DEFINE_VB_LAUNCH(dense_append_kernel, DenseArgs)
 BARQ_DEFINE_VB_LAUNCH(copy_rows_kernel, CopyArgs)
 BARQ_DEFINE_VB_LAUNCH(select_build_kernel, SelectArgs)
@@ -1640,7 +1788,7 @@ BARQ_DEFINE_VB_LAUNCH(select_build_kernel, SelectArgs)
 int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t batch,
                int64_t tokens, int64_t sb, int64_t sh, int64_t st, void* ko, void* vo,
                int64_t seq_out, int64_t osb, int64_t osh, int64_t oss, int64_t flags,
-               bool gather, void* stream) {
+               bool gather, void* stream, const KnownState* known = nullptr) {
   if (!pool_ok(pool)) return BARQ_KV_ERR_INVALID;
   if (batch < 0 || batch > pool->max_batch || tokens < 0 || tokens > kI32Max) return BARQ_KV_ERR_INVALID;
   if (flags & ~(int64_t)(BARQ_KV_SEQ_FROM_DEVICE | BARQ_KV_SEPARATE_FINALIZE)) return BARQ_KV_ERR_INVALID;
@@ -1782,6 +1930,10 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   hipStream_t s = (hipStream_t)stream;
   // Launches with more tiles than the CUs hold at once take the kernel built for several rounds.
   const bool rounds = fast && ncu > 0 && grid > kResidentTilesPerCU * ncu;
+  // The caller's row state in the arguments: page-aligned lean launches of an append and gather
+  // whose extent is given (the per-call path of an eager caller).
+  if (known && lean_ppt > 0 && lean_m == 0 && tokens > 0 && a.commit_in_kernel && !a.seq_from_device)
+    return launch_known_kernel((int)lean_nu, (int)lpp, dim3((uint32_t)grid), &a, known, s);
   int rc = lean_ppt > 0 ? (lean_m > 0 ? launch_lean_kernel<true>((int)lean_nu, (int)lpp, dim3((uint32_t)grid), &a, s)
                                       : launch_lean_kernel<false>((int)lean_nu, (int)lpp, dim3((uint32_t)grid), &a, s))
                         : launch_stream_kernel(vb, fast ? (int)(hv / 64) : 0, rounds, dim3((uint32_t)grid), &a, s);
@@ -1969,6 +2121,30 @@ int barq_kv_update(const barq_kv_pool* pool, const void* key_states, const void*
   return run_stream(pool, key_states, value_states, batch, tokens, stride_b, stride_h, stride_t,
                     key_out, value_out, seq_out, out_stride_b, out_stride_h, out_stride_s, flags,
                     true, stream);
+}
+
+int barq_kv_update_known(const barq_kv_pool* pool, const void* key_states, const void* value_states,
+                         int64_t batch, int64_t tokens, int64_t stride_b, int64_t stride_h,
+                         int64_t stride_t, void* key_out, void* value_out, int64_t seq_out,
+                         int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_s,
+                         const int32_t* seq_lens, const int32_t* high_water, int64_t free_top,
+                         void* stream) {
+  if (batch < 0 || (batch > 0 && (!seq_lens || !high_water)) || free_top < 0 ||
+      (pool && free_top > pool->num_pages))
+    return BARQ_KV_ERR_INVALID;
+  if (batch > kWave)  // the kernel's commit holds one row per lane: the device-read path
+    return run_stream(pool, key_states, value_states, batch, tokens, stride_b, stride_h, stride_t,
+                      key_out, value_out, seq_out, out_stride_b, out_stride_h, out_stride_s, 0, true, stream);
+  KnownState known;
+  for (int64_t r = 0; r < kWave; ++r) {
+    known.len[r] = r < batch ? seq_lens[r] : 0;
+    known.hw[r] = r < batch ? high_water[r] : 0;
+    if (r < batch && (known.len[r] < 0 || known.hw[r] < known.len[r])) return BARQ_KV_ERR_INVALID;
+  }
+  known.top = (int32_t)free_top;
+  return run_stream(pool, key_states, value_states, batch, tokens, stride_b, stride_h, stride_t,
+                    key_out, value_out, seq_out, out_stride_b, out_stride_h, out_stride_s, 0,
+                    true, stream, &known);
 }
 
 int barq_kv_crop(const barq_kv_pool* pool, int64_t batch, int64_t max_length, void* stream) {

@@ -378,7 +378,8 @@ void pool_select_rows_cold_(std::vector<std::vector<at::Tensor>> pools, std::vec
 // take as they are).
 std::tuple<at::Tensor, at::Tensor, int64_t> pool_step_(at::Tensor handle, at::Tensor pages, at::Tensor key_states,
                                                        at::Tensor value_states, py::buffer lens, py::buffer hw,
-                                                       int64_t free_count, int64_t limit, int64_t flags, bool gather) {
+                                                       int64_t free_count, bool free_exact, int64_t limit,
+                                                       int64_t flags, bool gather) {
   TORCH_CHECK(handle.device().is_cpu() && handle.scalar_type() == at::kByte &&
                   handle.numel() == (int64_t)sizeof(barq_kv_pool),
               "not a one-pool group (see pool_group)");
@@ -420,9 +421,21 @@ std::tuple<at::Tensor, at::Tensor, int64_t> pool_step_(at::Tensor handle, at::Te
     at::Tensor both = at::empty({2, batch, p.kv_heads, worst, p.head_dim}, pages.options());
     ko = both[0];
     vo = both[1];
-    rc = barq_kv_update(&p, k.data_ptr(), v.data_ptr(), batch, tokens, k.stride(0), k.stride(1), k.stride(2),
-                        ko.data_ptr(), vo.data_ptr(), worst, ko.stride(0), ko.stride(1), ko.stride(2), flags,
-                        current_stream(pages));
+    if (flags == 0 && free_exact && batch <= 64) {
+      // The shadow is exact: the launch takes the row state in its arguments.
+      int32_t l32[64], w32[64];
+      for (int64_t r = 0; r < batch; ++r) {
+        l32[r] = (int32_t)L[r];
+        w32[r] = (int32_t)W[r];
+      }
+      rc = barq_kv_update_known(&p, k.data_ptr(), v.data_ptr(), batch, tokens, k.stride(0), k.stride(1),
+                                k.stride(2), ko.data_ptr(), vo.data_ptr(), worst, ko.stride(0), ko.stride(1),
+                                ko.stride(2), l32, w32, free_count, current_stream(pages));
+    } else {
+      rc = barq_kv_update(&p, k.data_ptr(), v.data_ptr(), batch, tokens, k.stride(0), k.stride(1), k.stride(2),
+                          ko.data_ptr(), vo.data_ptr(), worst, ko.stride(0), ko.stride(1), ko.stride(2), flags,
+                          current_stream(pages));
+    }
   } else {
     rc = barq_kv_append(&p, k.data_ptr(), v.data_ptr(), batch, tokens, k.stride(0), k.stride(1), k.stride(2),
                         current_stream(pages));

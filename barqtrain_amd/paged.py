@@ -249,7 +249,7 @@ class PagePool:
             self._handle = handle
         limit = self.capacity if max_length is None else int(max_length)
         ko, vo, need = backend.pool_step_(handle[1], self.key_pages, key_states, value_states, self.lens, self.hw,
-                                          self.free_count, limit, flags, gather)
+                                          self.free_count, self.free_exact, limit, flags, gather)
         if need >= 0:
             self.free_count -= need
         return ko, vo, need

@@ -177,6 +177,26 @@ int barq_kv_update(const barq_kv_pool* pool, const void* key_states, const void*
                    int64_t flags, void* stream);
 
 /*
+ * barq_kv_update (flags 0) for a caller that holds the pool's row state: seq_lens[0 .. batch),
+ * high_water[0 .. batch) (host arrays) and free_top must equal the pool's device values when the
+ * launch runs (an eager caller's exact shadow of its own stream-ordered calls; a wrong value
+ * gives wrong pages and lengths, as a wrong block table would).  The same results and pool state
+ * as barq_kv_update, from a launch that reads none of that state on the device and commits it
+ * without waiting for every tile (a small launch then ends with its copies, not after two
+ * dependent counter round trips).  Launches outside the kernel's shapes (more than 64 rows, tiles
+ * not all resident at once, other geometries) run barq_kv_update.  It replaces the same
+ * reference path as barq_kv_update, the per-call paged_kv_append_ + current_tensors of
+ * python/barqtrain/kv_cache.py:93-142, for callers that track their lengths on the host
+ * (BarqPagedKVCacheLayer's shadow, kv_cache.py:150-153 read without a sync).
+ */
+int barq_kv_update_known(const barq_kv_pool* pool, const void* key_states, const void* value_states,
+                         int64_t batch, int64_t tokens, int64_t stride_b, int64_t stride_h,
+                         int64_t stride_t, void* key_out, void* value_out, int64_t seq_out,
+                         int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_s,
+                         const int32_t* seq_lens, const int32_t* high_water, int64_t free_top,
+                         void* stream);
+
+/*
  * seq_lens[b] = min(seq_lens[b], max_length) for rows [0, batch).  Page data is kept.  On a pool
  * whose rows share pages a crop can leave a shared block at or above its row's new length, where
  * the next append would write it for every row holding it: call barq_kv_select_rows with

@@ -19,7 +19,7 @@ def built():
 def test_library_exports_every_header_function(built):
     lib = ctypes.CDLL(str(build.lib_path()))
     declared = _capi.header_functions()
-    assert len(declared) == 24
+    assert len(declared) == 25
     for name in declared:
         assert hasattr(lib, name), name
     out = subprocess.run(["nm", "-D", "--defined-only", str(build.lib_path())], capture_output=True, text=True).stdout
@@ -38,6 +38,9 @@ def test_invalid_arguments_rejected_without_gpu(built):
     """Argument validation happens on the host before any HIP call."""
     lib = _capi.load_library()
     assert lib.barq_kv_pool_reset(None, None, None) == 1
+    # the known-state update checks the caller's state before anything else
+    assert lib.barq_kv_update_known(None, None, None, 1, 1, 0, 0, 0, None, None, 1, 0, 0, 0, None, None, 0, None) == 1
+    assert lib.barq_kv_update_known(None, None, None, 0, 1, 0, 0, 0, None, None, 1, 0, 0, 0, None, None, -1, None) == 1
     pool = _capi.BarqKVPool()
     assert lib.barq_kv_append(ctypes.byref(pool), None, None, 1, 1, 0, 0, 0, None) == 1
     assert lib.barq_kv_append_dense(None, None, None, None, None, 1, 1, 1, 1, 1, 1, 1, 2, 0, 0, 0, None) == 1
