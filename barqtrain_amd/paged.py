@@ -659,18 +659,20 @@ class QuantPagePool(PagePool):
         self._advance(batch, tokens, need)
         self._quantised(batch, frontier, moved)
 
-    def _check_chunked(self, batch: int, tokens: int, max_length: Optional[int]) -> None:
-        """Raise, changing nothing, unless appending `tokens` to rows [0, batch) in chunks of
-        `chunk` fits: the same capacity rule, hot-page and cold-page arithmetic each chunk's
-        append and quantisation apply, run on a copy of the host shadow."""
+    def _check_chunked(self, batch: int, tokens: int, max_length: Optional[int],
+                       rows: Optional[np.ndarray] = None) -> None:
+        """Raise, changing nothing, unless appending `tokens` to rows [0, batch) (or to `rows`) in
+        chunks of `chunk` fits: the same capacity rule, hot-page and cold-page arithmetic each
+        chunk's append and quantisation apply, run on a copy of the host shadow."""
         limit = self.capacity if max_length is None else int(max_length)
         if batch > self.max_batch:
             raise ValueError("batch size exceeds the configured paged KV cache capacity")
         if batch <= 0 or tokens <= 0:
             return
-        lens = self.lens[:batch].copy()
-        hw = self.hw[:batch].copy()
-        cold = self.cold_blocks[:batch].copy()
+        r = np.arange(batch) if rows is None else rows
+        lens = self.lens[r].copy()
+        hw = self.hw[r].copy()
+        cold = self.cold_blocks[r].copy()
         worst = int(lens.max()) + tokens
         if worst > limit or worst > self.capacity:
             raise PagedKVCapacityError(
@@ -782,8 +784,45 @@ class QuantPagePool(PagePool):
         return {"hot_pages": size(self.tensors[:2]), "cold_store": size(self.cold_tensors[:4]),
                 "metadata": size(self.tensors[2:]) + size(self.cold_tensors[4:])}
 
-    def append_rows(self, rows, key_states, value_states, max_length=None) -> None:
-        raise NotImplementedError("append_rows is not available on a pool with quantised (fp8) pages")
+    def append_rows(self, rows: Sequence[int], key_states: torch.Tensor, value_states: torch.Tensor,
+                    max_length: Optional[int] = None) -> None:
+        """Append ``key_states[i]`` / ``value_states[i]`` to row ``rows[i]`` (distinct rows): a
+        freed row takes a new sequence's prefill while the others keep decoding.  Checked in full
+        first (capacity, hot pages, cold pages, every chunk), then per row and per chunk of
+        `chunk` tokens an append and a quantisation of what left the window, each over the
+        row's one-row view of the row metadata -- the same kernels, sharing the free stacks."""
+        self._check_states(key_states, value_states)
+        rows = [int(r) for r in rows]
+        if len(rows) != key_states.shape[0]:
+            raise ValueError("append_rows: one row index per batch entry of the states")
+        if len(set(rows)) != len(rows):
+            raise ValueError("append_rows: rows must be distinct")
+        if any(r < 0 or r >= self.max_batch for r in rows):
+            raise IndexError("append_rows: row out of range")
+        tokens = key_states.shape[2]
+        if not rows or tokens == 0:
+            return
+        r = np.asarray(rows)
+        self._check_chunked(len(rows), tokens, max_length, rows=r)
+        k, v = self._compatible_pair(key_states, value_states)
+        t = self.tensors
+        ops = self._ops()
+        P = self.page_size
+        for i, row in enumerate(rows):
+            one = t[:2] + [t[2][row:row + 1], t[3][row:row + 1], t[4][row:row + 1]] + t[5:]
+            for s0 in range(0, tokens, self.chunk):
+                n = min(self.chunk, tokens - s0)
+                start = int(self.lens[row])
+                need = max(min(-(-(start + n) // P), self.max_blocks) - (-(-int(self.hw[row]) // P)), 0)
+                ops.pool_append_(one, k[i:i + 1, :, s0:s0 + n], v[i:i + 1, :, s0:s0 + n])
+                ops.pool_compress_(one, self.cold_tensors, self.window, 1)
+                self.lens[row] = start + n
+                self.hw[row] = max(int(self.hw[row]), start + n)
+                frontier = max(start + n - self.window, 0) // P
+                moved = max(frontier - int(self.cold_blocks[row]), 0)
+                self.cold_blocks[row] = max(int(self.cold_blocks[row]), frontier)
+                self.free_count += moved - need
+                self.cold_free -= moved
 
     def hot_block_counts(self, rows: np.ndarray) -> np.ndarray:
         """Hot blocks of each row: below the high-water mark and after the quantised ones (the
@@ -813,15 +852,85 @@ class QuantPagePool(PagePool):
         self.cold_exact = False  # released cold pages return only when no row shares them
         self.shared = True       # cold pages may have several holders (hot pages never do)
 
-    def copy_rows(self, src_rows: Sequence[int], num_pages: Optional[int] = None) -> "PagePool":
-        raise NotImplementedError("a pool with quantised (fp8) pages selects rows in place only: "
-                                  "size max_batch_size for the selection (batch * num_beams)")
+    def copy_rows(self, src_rows: Sequence[int], num_pages: Optional[int] = None,
+                  num_cold: Optional[int] = None) -> "QuantPagePool":
+        """A new pool whose row i holds row src_rows[i] of this one (repeats allowed), for
+        selections with more rows than this pool has (kv_cache.py:166-173 grows the batch): this
+        pool's state is copied into a pool of max(len(src_rows), max_batch) rows -- page and cold
+        page ids kept, the added pages and cold pages pushed on the free stacks -- which then
+        selects in place (select_rows: quantised blocks shared by reference, hot blocks moved to
+        their row's first taker and copied for the others).  Reads the stack tops (a
+        synchronisation)."""
+        src_rows = [int(r) for r in src_rows]
+        if any(r < 0 or r >= self.max_batch for r in src_rows):
+            raise IndexError("copy_rows: row out of range")
+        n = len(src_rows)
+        B2 = max(n, self.max_batch)
+        P = self.page_size
+        copies = self.select_copy_bound(np.asarray(src_rows, dtype=np.int64)) if n else 0
+        if num_pages is None:
+            per_row = (-(-(self.window + self.chunk) // P) + 2) + (-(-self.window // P) + 1)
+            num_pages = max(math.ceil(self.num_pages * B2 / self.max_batch), min(B2 * per_row, B2 * (self.max_blocks + 1)))
+        num_pages = max(int(num_pages), self.num_pages + copies)
+        if num_cold is None:
+            num_cold = max(self.num_cold, B2 * max(self.max_blocks - self.window // P, 1))
+        num_cold = max(int(num_cold), self.num_cold)
+        dst = QuantPagePool(max_batch=B2, max_blocks=self.max_blocks, page_size=P, kv_heads=self.kv_heads,
+                            head_dim=self.head_dim, dtype=self.dtype, device=self.device, window=self.window,
+                            chunk=self.chunk, num_pages=num_pages, num_cold=num_cold)
+        N, C, B = self.num_pages, self.num_cold, self.max_batch
+        top = int(self.ctrl[CTRL_FREE_TOP].item())
+        ctop = int(self.ctrl[CTRL_COLD_TOP].item())
+        i32 = dict(dtype=torch.int32, device=self.device)
+        with torch.no_grad():
+            dst.key_pages[:N].copy_(self.key_pages)
+            dst.value_pages[:N].copy_(self.value_pages)
+            dst.block_table.fill_(-1)
+            dst.block_table[:B].copy_(self.block_table)
+            for a, b in ((dst.seq_lens, self.seq_lens), (dst.high_water, self.high_water),
+                         (dst.page_shares, self.page_shares), (dst.cold_shares, self.cold_shares)):
+                a.zero_()
+                a[:b.numel()].copy_(b)
+            dst.free_pages[:top].copy_(self.free_pages[:top])
+            dst.free_pages[top:top + num_pages - N].copy_(torch.arange(N, num_pages, **i32))
+            for name in ("key_codes", "value_codes", "key_scales", "value_scales"):
+                getattr(dst, name)[:C].copy_(getattr(self, name))
+            dst.free_cold[:ctop].copy_(self.free_cold[:ctop])
+            dst.free_cold[ctop:ctop + num_cold - C].copy_(torch.arange(C, num_cold, **i32))
+            dst.ctrl.copy_(self.ctrl)
+            dst.ctrl[CTRL_FREE_TOP] = top + num_pages - N
+            dst.ctrl[CTRL_COLD_TOP] = ctop + num_cold - C
+        dst.lens[:B] = self.lens
+        dst.hw[:B] = self.hw
+        dst.cold_blocks[:B] = self.cold_blocks
+        dst.free_count, dst.free_exact = top + num_pages - N, True
+        dst.cold_free, dst.cold_exact = ctop + num_cold - C, True
+        dst.shared, dst.tails_shared = self.shared, self.tails_shared
+        if n:
+            dst.select_rows(src_rows)
+        return dst
 
     def _attention_call(self, backend, query, out, scale, max_seq, split_tokens, ws):
-        if self.page_size % 16:
-            raise NotImplementedError("decode attention over quantised pages needs page_size a multiple of 16")
-        backend.pool_decode_attention_cold(self.tensors, self.cold_tensors, self.window, query, out, scale,
-                                           max_seq, split_tokens, ws)
+        if self.page_size % 16 == 0:
+            backend.pool_decode_attention_cold(self.tensors, self.cold_tensors, self.window, query, out, scale,
+                                               max_seq, split_tokens, ws)
+            return
+        # Pages of other sizes: the kernel reads a 16-position chunk in one format, which such pages
+        # do not give.  The dequantising gather instead (the values the kernel would decode),
+        # then attention over the gathered K/V on the device, in float32, with the row lengths read
+        # on the device (so a captured graph serves growing rows).
+        batch, q_heads, tokens, _ = query.shape
+        ko, vo = self.gather(batch, max_seq)
+        group = q_heads // self.kv_heads
+        k = ko.float().repeat_interleave(group, dim=1)
+        v = vo.float().repeat_interleave(group, dim=1)
+        s = torch.matmul(query.float(), k.transpose(-1, -2).contiguous()) * scale  # [B, Hq, T, S]
+        lens = self.seq_lens[:batch].clamp(max=max_seq).to(torch.int64)
+        pos = torch.arange(max_seq, device=query.device)
+        qpos = lens[:, None] - tokens + torch.arange(tokens, device=query.device)[None, :]  # [B, T]
+        s = s.masked_fill((pos[None, None, :] > qpos[:, :, None])[:, None], float("-inf"))
+        p = torch.softmax(s, dim=-1).nan_to_num(0.0)
+        out.copy_(torch.matmul(p, v).to(out.dtype))
 
     def to(self, device) -> "QuantPagePool":
         super().to(device)

@@ -187,6 +187,15 @@ class QuantLayerOracle(DenseLayerOracle):
         frontier = np.maximum((self.seq_lens[:b].astype(np.int64) - self.window) // self.page_size, 0)
         self.cold[:b] = np.maximum(self.cold[:b], np.minimum(frontier, self.max_blocks))
 
+    def append_rows(self, rows: Sequence[int], key_states: np.ndarray, value_states: np.ndarray) -> None:
+        """``DenseLayerOracle.append_rows`` (a new sequence's tokens into freed rows), then the same
+        frontier rule as ``append`` for those rows: every block wholly before a row's window is
+        quantised, whether its tokens came in one call or in chunks."""
+        super().append_rows(rows, key_states, value_states)
+        r = np.asarray(rows, dtype=np.int64)
+        frontier = np.maximum((self.seq_lens[r].astype(np.int64) - self.window) // self.page_size, 0)
+        self.cold[r] = np.maximum(self.cold[r], np.minimum(frontier, self.max_blocks))
+
     def crop(self, max_length: int) -> None:
         if not self.is_initialized:
             return

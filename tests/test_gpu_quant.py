@@ -317,7 +317,9 @@ ATT_OUT = {torch.bfloat16: dict(rtol=2.0 ** -8, atol=2e-5), torch.float16: dict(
 
 @pytest.mark.parametrize("dtype,page,window,D", [(torch.bfloat16, 16, 0, 128), (torch.bfloat16, 16, 48, 128),
                                                  (torch.float16, 32, 32, 128), (torch.bfloat16, 32, 128, 128),
-                                                 (torch.bfloat16, 16, 48, 64), (torch.float16, 32, 0, 64)])
+                                                 (torch.bfloat16, 16, 48, 64), (torch.float16, 32, 0, 64),
+                                                 # pages not a multiple of 16 (dequantising gather + attention)
+                                                 (torch.bfloat16, 5, 16, 128), (torch.float16, 8, 24, 64)])
 def test_decode_attention_reads_quantised_pages(hip, dtype, page, window, D):
     """Attention over a quantised pool (barq_kv_decode_attention_cold: cold blocks read as codes
     and scales, dequantised in registers) against the float64 reference over the dequantising
@@ -445,3 +447,68 @@ def test_fused_paged_attention_on_fp8_pages_in_a_model(hip):
     assert all(layer.pool.errors() == 0 for layer in cache.layers)
     assert ((got - ref).norm() / ref.norm()) < 0.05
     assert (got.argmax(-1) == ref.argmax(-1)).float().mean() >= 0.75
+
+
+def test_refill_freed_rows_on_fp8_pages_like_the_oracle(hip):
+    """The serving pattern of C5 on fp8 pages: each step frees two rows, re-prefills them with a new
+    sequence of 200..700 tokens (QuantPagePool.append_rows: per row, chunks of append + quantise on
+    the row's one-row metadata view, the free stacks shared) while every row decodes -- against
+    the oracle bit for bit, the stacks' tops against the host shadow."""
+    from barqtrain_amd.paged import CTRL_COLD_TOP, CTRL_FREE_TOP, QuantPagePool
+    from oracle.kv_quant_oracle import QuantLayerOracle
+
+    B, H, D, P, W, ctx, steps = 6, 8, 128, 16, 64, 400, 10
+    cap = 1200
+    pool = QuantPagePool(max_batch=B, max_blocks=cap // P, page_size=P, kv_heads=H, head_dim=D, dtype=torch.bfloat16,
+                         device="cuda", window=W)
+    oracle = QuantLayerOracle(B, cap, P, W, "bf16")
+    rng = np.random.default_rng(8)
+    gen = torch.Generator().manual_seed(8)
+    k, v = hf_layout(B, H, ctx, D, torch.bfloat16, gen) * 2, hf_layout(B, H, ctx, D, torch.bfloat16, gen)
+    pool.append(k.cuda(), v.cuda())
+    oracle.append(to_bits(k), to_bits(v))
+    for step in range(steps):
+        rows = sorted(rng.choice(B, size=2, replace=False).tolist())
+        pool.free_rows(rows)
+        oracle.release_rows(rows)
+        t = int(rng.integers(200, 700))
+        kr, vr = hf_layout(2, H, t, D, torch.bfloat16, gen) * 2, hf_layout(2, H, t, D, torch.bfloat16, gen)
+        pool.append_rows(rows, kr.cuda(), vr.cuda())
+        oracle.append_rows(rows, to_bits(kr), to_bits(vr))
+        k, v = hf_layout(B, H, 1, D, torch.bfloat16, gen), hf_layout(B, H, 1, D, torch.bfloat16, gen)
+        got = pool.update(k.cuda(), v.cuda())
+        oracle.append(to_bits(k), to_bits(v))
+        assert pool.free_count == int(pool.ctrl[CTRL_FREE_TOP].item())
+        assert pool.cold_free == int(pool.ctrl[CTRL_COLD_TOP].item())
+        if step % 3 == 2 or step == steps - 1:
+            ok, ov = oracle.current_tensors()
+            assert np.array_equal(to_bits(got[0]), ok) and np.array_equal(to_bits(got[1]), ov), step
+    assert np.array_equal(pool.cold_blocks, oracle.cold)
+    assert pool.errors() == 0
+
+
+def test_selection_larger_than_an_fp8_pool_on_gpu(hip):
+    """batch_repeat_interleave past an fp8 pool's rows on the GPU: the layer moves to a grown pool
+    that selects in place (quantised blocks shared, hot blocks copied) -- against the oracle, then
+    decoding on."""
+    from barqtrain_amd.kv_cache import BarqPagedKVCacheLayer
+    from oracle.kv_quant_oracle import QuantLayerOracle
+
+    H, D, P, W, cap = 8, 128, 16, 32, 320
+    gen = torch.Generator().manual_seed(9)
+    layer = BarqPagedKVCacheLayer(max_batch_size=2, max_cache_len=cap, page_size=P, kv_quant="fp8_e4m3",
+                                  residual_window=W)
+    oracle = QuantLayerOracle(2, cap, P, W, "bf16")
+    k, v = hf_layout(2, H, 150, D, torch.bfloat16, gen) * 2, hf_layout(2, H, 150, D, torch.bfloat16, gen)
+    layer.update(k.cuda(), v.cuda())
+    oracle.append(to_bits(k), to_bits(v))
+    layer.batch_repeat_interleave(4)
+    oracle.batch_repeat_interleave(4)
+    assert layer.pool.max_batch >= 8 and layer.current_batch_size == 8
+    for _ in range(20):
+        k, v = hf_layout(8, H, 1, D, torch.bfloat16, gen), hf_layout(8, H, 1, D, torch.bfloat16, gen)
+        gk, gv = layer.update(k.cuda(), v.cuda())
+        oracle.append(to_bits(k), to_bits(v))
+    ok, ov = oracle.current_tensors()
+    assert np.array_equal(to_bits(gk), ok) and np.array_equal(to_bits(gv), ov)
+    assert layer.pool.errors() == 0

@@ -212,8 +212,10 @@ def test_beam_selection_shares_quantised_blocks_and_moves_hot_ones():
     check_accounting(pool)
     pool.free_rows([0, 2])
     assert int(pool.ctrl[2]) == pool.num_cold and int(pool.ctrl[0]) == pool.num_pages
-    with pytest.raises(NotImplementedError):
-        pool.copy_rows([0])
+    # a copy of the emptied pool: every page and cold page free, stacks extended
+    grown = pool.copy_rows([0, 1, 2, 2])
+    assert grown.max_batch == 4 and grown.free_count == grown.num_pages and grown.cold_free == grown.num_cold
+    check_accounting(grown)
 
 
 def test_factory_flag_and_environment(monkeypatch):
@@ -263,4 +265,91 @@ def test_beam_search_on_fp8_pages_matches_the_oracle_beam_by_beam(monkeypatch):
     assert all(s["updates"] >= new - 1 and s["selections"] >= new - 2 for s in stats), stats
     assert all(layer.pool.shared and int(layer.pool.cold_shares.max()) > 0 for layer in cache.layers)
     for layer in cache.layers:
+        check_accounting(layer.pool)
+
+
+def test_quant_oracle_append_rows_equals_append_on_leading_rows():
+    """QuantLayerOracle.append_rows pinned against append (already pinned): appending to rows
+    0 .. b-1 through append_rows leaves the same bits, lengths and quantised frontiers."""
+    gen = torch.Generator().manual_seed(11)
+    a = QuantLayerOracle(3, 64, 4, 8, "bf16")
+    b = QuantLayerOracle(3, 64, 4, 8, "bf16")
+    for t in (13, 1, 9, 1, 20):
+        k, v = to_bits(hf_layout(2, 2, t, 8, torch.bfloat16, gen)), to_bits(hf_layout(2, 2, t, 8, torch.bfloat16, gen))
+        a.append(k, v)
+        b.append_rows([0, 1], k, v)
+        for x, y in zip(a.current_tensors(), b.current_tensors()):
+            assert np.array_equal(x, y)
+        assert np.array_equal(a.cold, b.cold) and np.array_equal(a.seq_lens, b.seq_lens)
+    assert int(a.cold.max()) > 0
+
+
+@pytest.mark.parametrize("dtype,page,window,seed", [(torch.bfloat16, 4, 8, 0), (torch.float32, 5, 0, 1),
+                                                    (torch.float16, 16, 16, 2)])
+def test_append_rows_refills_freed_rows_like_the_oracle(dtype, page, window, seed):
+    """QuantPagePool.append_rows on a host pool: each step frees two rows, re-prefills them with a
+    ragged number of tokens (several chunks, each quantising what leaves the window) while the
+    others keep decoding -- bit for bit against the oracle, with the page accounting checked."""
+    from barqtrain_amd.paged import QuantPagePool
+
+    B, H, D, ctx, steps, cap = 5, 2, 8, 20, 14, 96
+    pool = QuantPagePool(max_batch=B, max_blocks=-(-cap // page), page_size=page, kv_heads=H, head_dim=D,
+                         dtype=dtype, device="cpu", window=window, chunk=6)
+    oracle = QuantLayerOracle(B, cap, page, window, DT[dtype])
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator().manual_seed(seed)
+    k, v = hf_layout(B, H, ctx, D, dtype, gen) * 3, hf_layout(B, H, ctx, D, dtype, gen)
+    pool.append(k, v)
+    oracle.append(to_bits(k), to_bits(v))
+    for step in range(steps):
+        rows = sorted(rng.choice(B, size=2, replace=False).tolist())
+        pool.free_rows(rows)
+        oracle.release_rows(rows)
+        t = int(rng.integers(1, 2 * ctx))
+        kr, vr = hf_layout(2, H, t, D, dtype, gen) * 3, hf_layout(2, H, t, D, dtype, gen)
+        order = rows if step % 2 else rows[::-1]
+        pool.append_rows(order, kr if step % 2 else kr.flip(0), vr if step % 2 else vr.flip(0))
+        oracle.append_rows(rows, to_bits(kr), to_bits(vr))
+        check_accounting(pool)
+        k, v = hf_layout(B, H, 1, D, dtype, gen), hf_layout(B, H, 1, D, dtype, gen)
+        got = pool.update(k, v)
+        oracle.append(to_bits(k), to_bits(v))
+        ok, ov = oracle.current_tensors()
+        assert np.array_equal(to_bits(got[0]), ok) and np.array_equal(to_bits(got[1]), ov), step
+        assert np.array_equal(pool.cold_blocks[:B], oracle.cold[:B])
+        check_accounting(pool)
+
+
+@pytest.mark.parametrize("dtype,page,window", [(torch.bfloat16, 4, 8), (torch.float16, 5, 0)])
+def test_selection_larger_than_the_pool_grows_it(dtype, page, window):
+    """A selection with more rows than a quantised pool holds (batch_repeat_interleave, a beam
+    search's first expansion): the layer moves to a larger pool holding this one's state, which
+    selects in place -- bit for bit against the oracle, then decoding on, with the accounting of
+    shared quantised blocks checked."""
+    from barqtrain_amd.kv_cache import BarqPagedKVCacheLayer
+
+    H, D, cap = 2, 8, 64
+    gen = torch.Generator().manual_seed(5)
+    layer = BarqPagedKVCacheLayer(max_batch_size=2, max_cache_len=cap, page_size=page, kv_quant="fp8_e4m3",
+                                  residual_window=window)
+    oracle = QuantLayerOracle(2, cap, page, window, DT[dtype])
+    k, v = hf_layout(2, H, 23, D, dtype, gen) * 3, hf_layout(2, H, 23, D, dtype, gen)
+    layer.update(k, v)
+    oracle.append(to_bits(k), to_bits(v))
+    before = layer.pool
+    layer.batch_repeat_interleave(3)  # 6 rows from a 2-row pool
+    oracle.batch_repeat_interleave(3)
+    assert layer.pool is not before and layer.pool.max_batch >= 6 and layer.current_batch_size == 6
+    ok, ov = oracle.current_tensors()
+    gk, gv = layer.pool.gather(6, ok.shape[2])
+    assert np.array_equal(to_bits(gk), ok) and np.array_equal(to_bits(gv), ov)
+    check_accounting(layer.pool)
+    layer.batch_select_indices(torch.tensor([5, 5, 0, 2, 3, 1]))
+    oracle.batch_select_indices([5, 5, 0, 2, 3, 1])
+    for _ in range(12):
+        k, v = hf_layout(6, H, 1, D, dtype, gen), hf_layout(6, H, 1, D, dtype, gen)
+        gk, gv = layer.update(k, v)
+        oracle.append(to_bits(k), to_bits(v))
+        ok, ov = oracle.current_tensors()
+        assert np.array_equal(to_bits(gk), ok) and np.array_equal(to_bits(gv), ov)
         check_accounting(layer.pool)
