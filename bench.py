@@ -430,8 +430,14 @@ def attention_leg(cfg, pools, B, dev, reps=20, kv_bytes=None, probe=False):
 
     step()
     torch.cuda.synchronize()
+    io = 2 * B * G * H * D * esize  # query read + output written
+    if kv_bytes is None:
+        call_bytes = [int(x.sum()) * H * D * 2 * esize + io for x in lens]
+    else:
+        call_bytes = [kv_bytes(p, x) + io for p, x in zip(pools, lens)]
     if probe:
-        return None
+        return {"attention_calls": L, "attention_algorithmic_bytes_per_call": int(sum(call_bytes) / L),
+                "attention_context": f"{int(min(x.min() for x in lens))}..{max_seq}"}
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         step()
@@ -448,11 +454,6 @@ def attention_leg(cfg, pools, B, dev, reps=20, kv_bytes=None, probe=False):
         torch.cuda.synchronize()
         ms = start.elapsed_time(end) / reps
         best = ms if best is None else min(best, ms)
-    io = 2 * B * G * H * D * esize  # query read + output written
-    if kv_bytes is None:
-        call_bytes = [int(x.sum()) * H * D * 2 * esize + io for x in lens]
-    else:
-        call_bytes = [kv_bytes(p, x) + io for p, x in zip(pools, lens)]
     per_call_us = best * 1e3 / L
     gbs = sum(call_bytes) / (best / 1e3) / 1e9
     # layer 0 against an fp32 attention over the gathered K/V (rows 0 and B - 1)
@@ -645,17 +646,38 @@ def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10, probe=
         vin.copy_(wl.v_dec[s])
         step.replay(views=False)
 
+    tb, esize = tok_bytes(cfg), elem_size(cfg)
+
+    def cold_read_bytes(lens_b, cold_b):
+        """Bytes a dequantising read of rows with these lengths and quantised blocks fetches."""
+        c = np.minimum(cold_b * P, lens_b)
+        return int((lens_b - c).sum() * tb + c.sum() * 2 * H * D + (c // P).sum() * (H * D + P * H))
+
     if probe is not None:  # counter runs: prefill, marker, the decode steps, one gather per layer
         prefill()
         step.prepare([max(prefill_lengths(cfg)) + s + 1 for s in range(steps)])
+        lens0 = pools[0].lens[:B].astype(np.int64).copy()
         probe()
+        update_bytes = []
         for s in range(steps):
             run(s)
+            if s % 16 == 15:
+                torch.cuda.synchronize()
+                print(f"pmc-probe: fp8 step {s} done", file=sys.stderr, flush=True)
+            lens_s = lens0 + s + 1
+            cold_s = np.maximum(lens_s - window, 0) // P
+            update_bytes.append(2 * B * tb + cold_read_bytes(lens_s, cold_s) + B * int(lens_s.max()) * tb)
         seq = pools[0].max_len(B)
         ko, vo = pools[0]._new_out(B, seq)
         for pool in pools:
             backend.pool_gather_cold(pool.tensors, pool.cold_tensors, pool.window, ko, vo, B, seq, 0)
         torch.cuda.synchronize()
+        lens_e = pools[0].lens[:B].astype(np.int64)
+        gather_bytes = cold_read_bytes(lens_e, pools[0].cold_blocks[:B].astype(np.int64)) + B * seq * tb
+        print(json.dumps({"pmc_probe": "quant", "config": cfg["name"], "steps": steps, "launches": steps * L,
+                          "update_algorithmic_bytes_per_launch": float(np.mean(update_bytes)),
+                          "gather_calls": L, "gather_algorithmic_bytes_per_launch": gather_bytes,
+                          "context": f"{int(lens0.min()) + 1}..{int(lens_e.max())}"}), flush=True)
         return None
     prefill()
     # every graph the steps replay (each extent bucket, with and without the compress launch)
@@ -695,8 +717,6 @@ def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10, probe=
     gather_us = start.elapsed_time(end) * 1e3 / reps / L
     lens = pools[0].lens[:B].astype(np.int64)
     cold = pools[0].cold_blocks[:B].astype(np.int64)
-    tb = tok_bytes(cfg)
-    esize = elem_size(cfg)
     cold_tok = cold * P
     hot_tok = lens - cold_tok
     gather_bytes = int(hot_tok.sum() * tb + cold_tok.sum() * 2 * H * D       # hot pages, codes
@@ -778,7 +798,6 @@ def pmc_probe(cfg, wl, start, steps, run_step, dev, quant):
     L = cfg["layers"]
     if quant:
         quant_leg(cfg, wl, steps, dev, 0.0, probe=lambda: calibration_pass(dev))
-        print(json.dumps({"pmc_probe": "quant", "config": cfg["name"], "steps": steps}), flush=True)
         return
     def progress(what, s):
         # A counter run serialises every dispatch and reads the counters after each one, so a
@@ -800,12 +819,11 @@ def pmc_probe(cfg, wl, start, steps, run_step, dev, quant):
     torch.cuda.synchronize()
     print("pmc-probe: window done", file=sys.stderr, flush=True)
     attn = cfg["dtype"] in ("bfloat16", "float16") and cfg["dim"] == 128
-    if attn:
-        attention_leg(cfg, wl.pools, cfg["batch"], dev, reps=1, probe=True)
+    attn_info = attention_leg(cfg, wl.pools, cfg["batch"], dev, reps=1, probe=True) if attn else {}
     total = sum(wl.step_bytes[start:start + steps])
     print(json.dumps({"pmc_probe": True, "config": cfg["name"], "window_start": start, "steps": steps,
                       "launches": steps * L, "algorithmic_bytes_per_launch": total / (steps * L),
-                      "attention_calls": L if attn else 0}), flush=True)
+                      "attention_calls": L if attn else 0, **attn_info}), flush=True)
 
 
 def main():
