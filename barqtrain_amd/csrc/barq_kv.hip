@@ -45,6 +45,7 @@ constexpr int kThreads = 256;                     // workgroup of the bookkeepin
 constexpr int kWave = 64;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kStreamThreads = kThreads + kWave;  // stream kernel: control wave + 4 copy waves
+constexpr int kCopyWaves = kStreamThreads / kWave - 1;
 constexpr int kUnroll = 16;                       // vectors in flight per copy thread
 constexpr int kMaxTilePages = 64;                 // block-table slots a tile stages in LDS
 // Positions per tile: whole pages, about this many bytes of K (or V).  With kUnroll 16-byte
@@ -669,10 +670,18 @@ __global__ void __launch_bounds__(kStreamThreads) lean_stream_kernel(const Strea
   const int P = (int)p.page_size;
   const int mb = (int)p.max_blocks;
   const bool committing = T > 0 && a.commit_in_kernel;
+  __shared__ int s_ready;  // copy waves whose metadata loads have returned (committing tiles)
+  if (committing) {
+    if (wave == 0 && lane == 0) s_ready = 0;
+    __syncthreads();
+  }
 
   if (wave == 0) {
     if (!committing) return;
-    __syncthreads();  // every copy wave of the tile holds the metadata it uses
+    // The tile arrives once every copy wave holds the metadata it uses: the copy waves count
+    // themselves in LDS instead of waiting for each other at a barrier.
+    while (__hip_atomic_load(&s_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < kCopyWaves)
+      __builtin_amdgcn_s_sleep(1);
     arrive_and_commit(p, a.nsub, a.batch, T, a.seq_out, a.div_page);
     return;
   }
@@ -682,9 +691,15 @@ __global__ void __launch_bounds__(kStreamThreads) lean_stream_kernel(const Strea
   const int len = p.seq_lens[b];
   const int hw = p.high_water[b];
   const int blk0 = c * a.ppt;
-  const int e0 = p.block_table[(int64_t)b * mb + blk0];
-  int e1 = -1;
-  if (a.ppt > 1 && blk0 + 1 < mb) e1 = p.block_table[(int64_t)b * mb + blk0 + 1];
+  const int64_t trow = (int64_t)b * mb;
+  const int e0 = p.block_table[trow + blk0];
+  const int e1_read = p.block_table[trow + min(blk0 + 1, mb - 1)];
+  // The arguments the copies address with are requested in the metadata's round trip (left to
+  // itself the compiler asks for them only once the metadata has arrived: one more round trip
+  // before the first page load).  Loads after this point are vector loads.
+  asm volatile("" ::"s"(a.in_k), "s"(a.in_v), "s"(a.out_k), "s"(a.out_v), "s"(a.in_sb), "s"(a.in_sh), "s"(a.in_st),
+               "s"(a.out_sb), "s"(a.out_sh), "s"(a.out_ss), "s"(a.page_bytes), "s"(a.tok_bytes));
+  const int e1 = (a.ppt > 1 && blk0 + 1 < mb) ? e1_read : -1;
   const int lo = c * a.chunk;
   int hi = lo + a.chunk;
   if (hi > min(len + T, a.seq_out)) {
@@ -718,8 +733,10 @@ __global__ void __launch_bounds__(kStreamThreads) lean_stream_kernel(const Strea
   }
   const int64_t pb0 = pbs[0], pb1 = pbs[1];
   if (committing) {
-    __builtin_amdgcn_s_waitcnt(0);  // the metadata loads have returned before the tile arrives
-    __syncthreads();
+    // Counted once the values have returned: the asm consumes every metadata value the tile read
+    // (the compiler waits for them before it), and the count follows it.
+    asm volatile("" ::"s"(len), "s"(hw), "s"(e0), "s"(e1), "s"(top), "s"(base), "s"(hi), "s"(pb0), "s"(pb1));
+    if (lane == 0) __hip_atomic_fetch_add(&s_ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   if (hi <= lo) return;
 
@@ -931,6 +948,8 @@ __global__ void __launch_bounds__(kStreamThreads) lean_balanced_kernel(const Str
   const int mb = (int)p.max_blocks;
   const bool committing = T > 0 && a.commit_in_kernel;
 
+  // (The LDS count of lean_stream_kernel, in place of this barrier, cost the balanced tiles
+  // ~1 %: their copy waves get their metadata late, and the control waves poll meanwhile.)
   if (wave == 0) {
     if (!committing) return;
     __syncthreads();  // every copy wave of the tile holds the metadata it uses
@@ -970,6 +989,7 @@ __global__ void __launch_bounds__(kStreamThreads) lean_balanced_kernel(const Str
     if (nbl > 0) e0 = p.block_table[trow + blk0];
     if (nbl > 1 && blk0 + 1 < mb) e1 = p.block_table[trow + blk0 + 1];
   }
+
   const NewBlocks nb = new_blocks(len, hw, T, mb, a.div_page);
   int base = 0, top = 0;
   if (nb.count > 0 && blk0 < nb.first + nb.count && blk0 + nbl > nb.first) {
