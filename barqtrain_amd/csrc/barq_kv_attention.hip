@@ -32,6 +32,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <type_traits>
 
 #include "barq_kv.h"
 #include "barq_kv_fp8.h"
@@ -57,8 +58,13 @@ constexpr int kMaxWaves = 2048;            // resident waves of an MI355X: 256 C
 constexpr int kMinRangeChunks = 4;         // the automatic range never goes below 64 positions
 constexpr int kPairWaves = 8;              // waves of a pair-kernel workgroup
 constexpr int64_t kPairMinPairs = 128;     // the pair kernel from this many (row, kv head) pairs ...
-constexpr int64_t kPairMaxChunks = 44;     // ... of at most this many 16-position chunks (max_seq)
-static_assert(kPairMaxChunks <= kTableEntries, "a pair's blocks fit one table window");
+constexpr int64_t kPairMaxChunks = 44;     // ... of at most this many 16-position chunks (max_seq);
+// with up to 4 query rows (two-byte pages): this many, and from twice the pairs (every CU busy)
+// this many
+constexpr int64_t kPairMaxChunksR1 = 64;
+constexpr int64_t kPairMaxChunksR1Wide = 128;
+static_assert(kPairMaxChunks <= kTableEntries && kPairMaxChunksR1Wide <= kTableEntries,
+              "a pair's blocks fit one table window");
 
 enum : int { kBF16 = 0, kF16 = 1 };
 
@@ -408,7 +414,7 @@ __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kT
                      (int64_t)(tk - (int)(bk * (uint32_t)a.page_size)) * a.row_bytes + 16 * g;
 #pragma unroll
     for (int st = 0; st < kSteps; ++st)
-      kv[st] = tc + n16 < end ? ld_page(kp + 64 * st) : u32x4{0, 0, 0, 0};
+      kv[st] = (!PRED || tc + n16 < end) ? ld_page(kp + 64 * st) : u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < kVLoads; ++s) {
       const int tv = min(tc + kVPos * s + vpos, end - 1);
@@ -416,7 +422,7 @@ __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kT
       const int pv = table_lane(pt, (int)bv - blk0);
       const char* vp = vbase + (int64_t)pv * a.page_bytes +
                        (int64_t)(tv - (int)(bv * (uint32_t)a.page_size)) * a.row_bytes + 16 * vdim;
-      vv[s] = tc + kVPos * s + vpos < end ? ld_page(vp) : u32x4{0, 0, 0, 0};
+      vv[s] = (!PRED || tc + kVPos * s + vpos < end) ? ld_page(vp) : u32x4{0, 0, 0, 0};
     }
   }
 }
@@ -610,13 +616,23 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[r2][e] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto load = [&](int tc, u32x4 (&kv)[kSteps], u32x4 (&vv)[kVLoads], bool& cold) {
-    // Slide the table window when the chunk's last block leaves it (every 254+ blocks).
+  // Slide the table window when the chunk's last block leaves it (every 254+ blocks).
+  auto slide = [&](int tc) {
     const int last = (int)a.page_div.div((uint32_t)min(tc + kBlock, t_end) - 1u);
     if (last - blk0 >= kTableEntries) {
       blk0 = (int)a.page_div.div((uint32_t)tc);
       load_table<COLD>(a, b, blk0, blk_end, lane, pt);
     }
+  };
+  // A whole chunk (tc + kBlock <= t_end): every lane loads, no branch around the loads.
+  auto load_full = [&](int tc, u32x4 (&kv)[kSteps], u32x4 (&vv)[kVLoads], bool& cold) {
+    slide(tc);
+    load_chunk<HD, UNIFORM, false, COLD>(a, pt, blk0, kbase, vbase, tc, t_end, klane, vlane, n16, g, vpos, vdim,
+                                         kvh, kv, vv, cold);
+  };
+  // The piece's last chunk, possibly partial: lanes past t_end load nothing.
+  auto load_tail = [&](int tc, u32x4 (&kv)[kSteps], u32x4 (&vv)[kVLoads], bool& cold) {
+    slide(tc);
     if (tc + kBlock <= t_end)
       load_chunk<HD, UNIFORM, false, COLD>(a, pt, blk0, kbase, vbase, tc, t_end, klane, vlane, n16, g, vpos, vdim,
                                            kvh, kv, vv, cold);
@@ -694,38 +710,76 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
     }
   };
 
-  // A ring of D register buffers: the next D - 1 chunks' loads are in flight while one is
-  // computed.  Two buffers: a third spills (or, for 4 query rows, runs slower) with the
-  // accumulators in registers.
-  constexpr int D = 2;
-  u32x4 kr[D][kSteps], vr[D][kVLoads];
-  bool cr[D];  // the buffer holds codes and scales (wave-uniform)
+  // Two register buffers: the next chunk's loads are in flight while one is computed (a third
+  // spills, or for 4 query rows runs slower, with the accumulators in registers).
+  u32x4 kr[2][kSteps], vr[2][kVLoads];
+  bool cr[2] = {false, false};  // the buffer holds codes and scales (wave-uniform)
   int tc = t_begin;
-#pragma unroll
-  for (int i = 0; i < D - 1; ++i) {
-    cr[i] = false;
-    if (tc + i * kBlock < t_end) load(tc + i * kBlock, kr[i], vr[i], cr[i]);
-  }
-  cr[D - 1] = false;
-  if (tc < t_end) {
-    for (;;) {
-#pragma unroll
-      for (int i = 0; i < D; ++i) {
-        const int j = (i + D - 1) % D;
-        if (tc + (D - 1) * kBlock < t_end) load(tc + (D - 1) * kBlock, kr[j], vr[j], cr[j]);
+  auto step = [&](int i) {
+    bool kcodes = false;
+    if (COLD && cr[i]) {
+      kcodes = __builtin_amdgcn_ballot_w64(!scales_moderate<false>(kr[i])) == 0;
+      if (!kcodes) dequant_regs<E, false>(kr[i]);
+    }
+    compute(tc, kr[i], vr[i], kcodes, COLD && cr[i]);
+    tc += kBlock;
+  };
+  if constexpr (PRE && !COLD && R == 1) {
+    // The wait the compiler puts before a chunk's products counts the loads issued after that
+    // chunk's; where one path to the products skips the next chunk's loads (the last chunk), that
+    // count is the smaller one on every path, and each chunk also waits for part of the next
+    // chunk's data.  So this loop runs only while the next chunk is whole and loads it on every
+    // path; the last one or two chunks are finished after it.  (The extra copies of the chunk
+    // code cost registers: the one-wave kernels, whose accumulators and pieces loop already fill
+    // them, and the quantised pools keep the loop below.)
+    auto finish = [&](auto buffer) {
+      constexpr int c = decltype(buffer)::value;
+      if (tc + kBlock < t_end) {
+        load_tail(tc + kBlock, kr[1 - c], vr[1 - c], cr[1 - c]);
         __builtin_amdgcn_sched_barrier(0);
-        bool kcodes = false;
-        if (COLD && cr[i]) {
-          kcodes = __builtin_amdgcn_ballot_w64(!scales_moderate<false>(kr[i])) == 0;
-          if (!kcodes) dequant_regs<E, false>(kr[i]);
+        step(c);
+        step(1 - c);
+      } else {
+        step(c);
+      }
+    };
+    if (tc + kBlock <= t_end) {
+      load_full(tc, kr[0], vr[0], cr[0]);
+      for (;;) {
+        if (tc + 2 * kBlock > t_end) {
+          finish(std::integral_constant<int, 0>{});
+          break;
         }
-        compute(tc, kr[i], vr[i], kcodes, COLD && cr[i]);
-        tc += kBlock;
-        if (tc >= t_end) goto chunks_done;
+        load_full(tc + kBlock, kr[1], vr[1], cr[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        step(0);
+        if (tc + 2 * kBlock > t_end) {
+          finish(std::integral_constant<int, 1>{});
+          break;
+        }
+        load_full(tc + kBlock, kr[0], vr[0], cr[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        step(1);
+      }
+    } else if (tc < t_end) {
+      load_tail(tc, kr[0], vr[0], cr[0]);
+      step(0);
+    }
+  } else {
+    if (tc < t_end) {
+      load_tail(tc, kr[0], vr[0], cr[0]);
+      for (;;) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          if (tc + kBlock < t_end) load_tail(tc + kBlock, kr[1 - i], vr[1 - i], cr[1 - i]);
+          __builtin_amdgcn_sched_barrier(0);
+          step(i);
+          if (tc >= t_end) goto chunks_done;
+        }
       }
     }
+  chunks_done:;
   }
-chunks_done:
 
   // Row sums across the 16 lanes of each row group; P.V partials across the position slots.
 #pragma unroll
@@ -972,7 +1026,10 @@ hipError_t launch_typed(AttnArgs a, bool merge, hipStream_t stream) {
   // SIMD keep the accumulators in registers): one workgroup per pair.
   if constexpr (U && R <= 2) {
     const int64_t pairs = (int64_t)a.batch * a.kv_heads;
-    if (a.range_chunks == 0 && pairs >= kPairMinPairs && (a.max_seq + kBlock - 1) / kBlock <= kPairMaxChunks) {
+    const int64_t max_chunks = R > 1 || COLD                ? kPairMaxChunks
+                               : pairs >= 2 * kPairMinPairs ? kPairMaxChunksR1Wide
+                                                            : kPairMaxChunksR1;
+    if (a.range_chunks == 0 && pairs >= kPairMinPairs && (a.max_seq + kBlock - 1) / kBlock <= max_chunks) {
       hipLaunchKernelGGL((attention_pair_kernel<HD, E, R, OutT, COLD, kPairWaves>), dim3((unsigned)pairs),
                          dim3(kPairWaves * kWave), 0, stream, a);
       return hipGetLastError();

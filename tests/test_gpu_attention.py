@@ -137,6 +137,27 @@ def test_many_short_pairs_one_launch(dtype, page, D):
     assert pool.errors() == 0
 
 
+@pytest.mark.parametrize("rows,Hkv,cap,dtype,D", [(32, 4, 1024, torch.bfloat16, 128),
+                                                  (32, 8, 2048, torch.float16, 128),
+                                                  (16, 8, 1024, torch.bfloat16, 64)])
+def test_long_pairs_one_launch(rows, Hkv, cap, dtype, D):
+    """Up to 4 query rows take the one-launch pair kernel for longer rows: 128 pairs of up to 1024
+    positions, 256 pairs of up to 2048.  Its loop loads the next chunk unconditionally while that
+    chunk is whole and finishes the last one or two after it, so lengths sit on and next to chunk
+    boundaries (empty, 1, 15 .. 33, cap - 17 .. cap); G = 4 / 1 / 2, two tokens x 2 heads, the
+    2-byte output; the flat schedule (a fixed split) over the same pool agrees."""
+    rng = np.random.default_rng(cap + D)
+    edges = [cap, cap - 1, cap - 15, cap - 16, cap - 17, 0, 1, 15, 16, 17, 31, 32, 33]
+    lens = edges + rng.integers(0, cap + 1, size=rows - len(edges)).tolist()
+    pool, kd, vd, lens = make_rows(rows, Hkv, 16, lens, dtype, seed=cap + 7, order_seed=cap + 8, D=D)
+    ws = None
+    for i, (G, T) in enumerate([(4, 1), (1, 1), (2, 2), (2, 1)]):
+        ws = check(pool, kd, vd, lens, G, T, dtype, seed=500 + i, ws=ws)
+    check(pool, kd, vd, lens, 4, 1, dtype, seed=9, out_f32=False)
+    check(pool, kd, vd, lens, 4, 1, dtype, seed=9, split_tokens=256)  # the flat schedule
+    assert pool.errors() == 0
+
+
 def test_flat_schedule_with_ranges_of_two_sizes():
     """16 ragged rows of ~4200 positions over 8 kv heads (over 32k chunks: the automatic split's
     ranges hold 16+ chunks, so the first half of the waves take larger ones), G = 4 and 8; a
