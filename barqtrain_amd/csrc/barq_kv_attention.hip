@@ -32,7 +32,6 @@
 #include <algorithm>
 #include <atomic>
 #include <cmath>
-#include <type_traits>
 
 #include "barq_kv.h"
 #include "barq_kv_fp8.h"
@@ -182,9 +181,14 @@ __device__ __forceinline__ float lane_value(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// V rows: each load reads whole 128-byte lines (four positions x 256 bytes), read once.
 __device__ __forceinline__ u32x4 ld_page(const char* p) {
   return __builtin_nontemporal_load((const u32x4*)p);
 }
+// K rows: one load reads 64 bytes of each of 16 positions (half a line), the next load the other
+// half; a plain load keeps the line in L1 for it, a nontemporal one fetched it twice (C2 decode
+// attention -5 % at 650 positions, -8 % at 1024).
+__device__ __forceinline__ u32x4 ld_page_k(const char* p) { return *(const u32x4*)p; }
 
 template <typename OutT, int E>
 __device__ __forceinline__ void store_out4(char* p, const f32x4 v) {
@@ -402,7 +406,7 @@ __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kT
     const char* vp = vbase + base + vlane;
 #pragma unroll
     for (int st = 0; st < kSteps; ++st)
-      kv[st] = (!PRED || tc + n16 < end) ? ld_page(kp + 64 * st) : u32x4{0, 0, 0, 0};
+      kv[st] = (!PRED || tc + n16 < end) ? ld_page_k(kp + 64 * st) : u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < kVLoads; ++s)
       vv[s] = (!PRED || tc + kVPos * s + vpos < end) ? ld_page(vp + kVPos * s * a.row_bytes) : u32x4{0, 0, 0, 0};
@@ -414,7 +418,7 @@ __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kT
                      (int64_t)(tk - (int)(bk * (uint32_t)a.page_size)) * a.row_bytes + 16 * g;
 #pragma unroll
     for (int st = 0; st < kSteps; ++st)
-      kv[st] = (!PRED || tc + n16 < end) ? ld_page(kp + 64 * st) : u32x4{0, 0, 0, 0};
+      kv[st] = (!PRED || tc + n16 < end) ? ld_page_k(kp + 64 * st) : u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < kVLoads; ++s) {
       const int tv = min(tc + kVPos * s + vpos, end - 1);
@@ -425,6 +429,29 @@ __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kT
       vv[s] = (!PRED || tc + kVPos * s + vpos < end) ? ld_page(vp) : u32x4{0, 0, 0, 0};
     }
   }
+}
+
+// A chunk of a two-byte pool with whole-chunk pages whose positions past `end` read position
+// end - 1 (the causal mask gives them probability 0): every lane loads, no branch around the loads.
+template <int HD>
+__device__ __forceinline__ void load_chunk_clamped(const AttnArgs& a, const int (&pt)[kTableRegs], int blk0,
+                                                   const char* kbase, const char* vbase, int tc, int end, int n16,
+                                                   int g, int vpos, int vdim, u32x4 (&kv)[Head<HD>::kSteps],
+                                                   u32x4 (&vv)[Head<HD>::kVLoads]) {
+  constexpr int kSteps = Head<HD>::kSteps;
+  constexpr int kVPos = Head<HD>::kVPos;
+  constexpr int kVLoads = Head<HD>::kVLoads;
+  const uint32_t blk = a.page_div.div((uint32_t)tc);
+  const int page = table_scalar(pt, (int)blk - blk0);
+  const int64_t base =
+      (int64_t)page * a.page_bytes + (int64_t)(tc - (int)(blk * (uint32_t)a.page_size)) * a.row_bytes;
+  const int lastp = end - 1 - tc;  // >= 15 for a whole chunk
+  const char* kp = kbase + base + min(n16, lastp) * a.row_bytes + 16 * g;
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) kv[st] = ld_page_k(kp + 64 * st);
+#pragma unroll
+  for (int s = 0; s < kVLoads; ++s)
+    vv[s] = ld_page(vbase + base + min(kVPos * s + vpos, lastp) * a.row_bytes + 16 * vdim);
 }
 
 // One register of a quantised chunk (8 codes and their scale bytes: K's per channel, V's -- value
@@ -624,12 +651,6 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
       load_table<COLD>(a, b, blk0, blk_end, lane, pt);
     }
   };
-  // A whole chunk (tc + kBlock <= t_end): every lane loads, no branch around the loads.
-  auto load_full = [&](int tc, u32x4 (&kv)[kSteps], u32x4 (&vv)[kVLoads], bool& cold) {
-    slide(tc);
-    load_chunk<HD, UNIFORM, false, COLD>(a, pt, blk0, kbase, vbase, tc, t_end, klane, vlane, n16, g, vpos, vdim,
-                                         kvh, kv, vv, cold);
-  };
   // The piece's last chunk, possibly partial: lanes past t_end load nothing.
   auto load_tail = [&](int tc, u32x4 (&kv)[kSteps], u32x4 (&vv)[kVLoads], bool& cold) {
     slide(tc);
@@ -725,45 +746,34 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
     tc += kBlock;
   };
   if constexpr (PRE && !COLD && R == 1) {
-    // The wait the compiler puts before a chunk's products counts the loads issued after that
-    // chunk's; where one path to the products skips the next chunk's loads (the last chunk), that
-    // count is the smaller one on every path, and each chunk also waits for part of the next
-    // chunk's data.  So this loop runs only while the next chunk is whole and loads it on every
-    // path; the last one or two chunks are finished after it.  (The extra copies of the chunk
-    // code cost registers: the one-wave kernels, whose accumulators and pieces loop already fill
-    // them, and the quantised pools keep the loop below.)
-    auto finish = [&](auto buffer) {
-      constexpr int c = decltype(buffer)::value;
-      if (tc + kBlock < t_end) {
-        load_tail(tc + kBlock, kr[1 - c], vr[1 - c], cr[1 - c]);
-        __builtin_amdgcn_sched_barrier(0);
-        step(c);
-        step(1 - c);
-      } else {
-        step(c);
-      }
+    // Pair kernel, up to 4 query rows, two-byte pages (its table window holds every block of the
+    // pair: no slide).  The wait the compiler puts before a chunk's products counts the loads
+    // issued after that chunk's; where one path to the products skips the next chunk's loads, or
+    // loads it under a lane mask, that count is the smaller one on every path and each chunk also
+    // waits for part of the next chunk's data.  So the next chunk, whole or partial, is loaded on
+    // every path of the loop, clamped instead of masked, and the loop is left before a load.
+    // (The quantised and 8+ row variants keep the ring below: this form's registers spill there.)
+    auto load_clamped = [&](int t, u32x4 (&kv)[kSteps], u32x4 (&vv)[kVLoads]) {
+      load_chunk_clamped<HD>(a, pt, blk0, kbase, vbase, t, t_end, n16, g, vpos, vdim, kv, vv);
     };
-    if (tc + kBlock <= t_end) {
-      load_full(tc, kr[0], vr[0], cr[0]);
+    if (tc < t_end) {
+      load_clamped(tc, kr[0], vr[0]);
       for (;;) {
-        if (tc + 2 * kBlock > t_end) {
-          finish(std::integral_constant<int, 0>{});
+        if (tc + kBlock >= t_end) {
+          step(0);
           break;
         }
-        load_full(tc + kBlock, kr[1], vr[1], cr[1]);
+        load_clamped(tc + kBlock, kr[1], vr[1]);
         __builtin_amdgcn_sched_barrier(0);
         step(0);
-        if (tc + 2 * kBlock > t_end) {
-          finish(std::integral_constant<int, 1>{});
+        if (tc + kBlock >= t_end) {
+          step(1);
           break;
         }
-        load_full(tc + kBlock, kr[0], vr[0], cr[0]);
+        load_clamped(tc + kBlock, kr[0], vr[0]);
         __builtin_amdgcn_sched_barrier(0);
         step(1);
       }
-    } else if (tc < t_end) {
-      load_tail(tc, kr[0], vr[0], cr[0]);
-      step(0);
     }
   } else {
     if (tc < t_end) {

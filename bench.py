@@ -48,7 +48,8 @@ from the pages through the block table (the step the gathered K/V feed), over th
 timed run left them: one call per layer with G query heads per KV head (4, the Llama-3-8B ratio;
 8 for the 70B-class C5), captured in a graph and replayed; algorithmic bytes per call = every
 visible K and V element once + query + output.  Layer 0 is checked against an fp32 attention over
-the gathered K/V.
+the gathered K/V.  C2 also reports it at the trajectory's middle (`at_mid_context`: every row
+cropped to 650 positions after the first measurement).
 
 `beam_select` times a beam reorder (Cache.reorder_cache) of every layer one decode step past
 the prefill: one in-place selection for all layers that shares full pages, moves each taken
@@ -97,7 +98,8 @@ CONFIGS = {
     1: dict(name="C1 tiny plumbing", layers=2, batch=1, heads=4, dim=64, page=16, dtype="float32",
             prefill=("uniform", 32), decode=128, seed=1001, mode="eager", cpu_steps=None),
     2: dict(name="C2 Llama-3-8B KV shape", layers=32, batch=16, heads=8, dim=128, page=16, dtype="bfloat16",
-            prefill=("uniform", 512), decode=256, seed=1002, mode="graph", cpu_steps=None),
+            prefill=("uniform", 512), decode=256, seed=1002, mode="graph", cpu_steps=None,
+            attention_mid_context=650),
     3: dict(name="C3 fragmented ragged batch", layers=32, batch=64, heads=8, dim=128, page=16, dtype="bfloat16",
             prefill=("ragged", 128, 4096, 2003), perm_seed=3003, decode=128, seed=1003, mode="graph",
             cpu_steps=8),
@@ -401,6 +403,18 @@ class Workload:
                 pool.append_rows(rows, *self.refill)
 
 
+def pair_kernel_bounds(pairs, max_seq, rows, quantised):
+    """The library's one-launch (pair kernel) bounds for a one-token decode call: 128+ (row, kv
+    head) pairs, up to 8 query rows, and at most 44 16-position chunks, or, for up to 4 query rows
+    over two-byte pages, 64 chunks (128 from 256 pairs)."""
+    if pairs < 128 or rows > 8:
+        return False
+    chunks = -(-max_seq // 16)
+    if rows > 4 or quantised:
+        return chunks <= 44
+    return chunks <= (128 if pairs >= 256 else 64)
+
+
 def attention_leg(cfg, pools, B, dev, reps=20, kv_bytes=None, probe=False):
     """Decode attention over the pools' current rows: one launch per layer, graph-replayed.
     kv_bytes(pool, lens): the K/V bytes one call reads (default: every visible element in the
@@ -474,7 +488,7 @@ def attention_leg(cfg, pools, B, dev, reps=20, kv_bytes=None, probe=False):
         raise SystemExit("device error bits set by the attention leg")
     gathered = 3 * (sum(call_bytes) - L * io) / L  # gather reads + writes K/V, attention re-reads
     cold = "<..., COLD> (fp8 pages read as codes)" if getattr(pools[0], "quantized", False) else ""
-    if B * H >= 128 and max_seq <= 704 and G <= 8:  # the library's one-launch bounds
+    if pair_kernel_bounds(B * H, max_seq, G, bool(cold)):
         kname = "attention_pair_kernel" + cold + " (one launch per layer)"
     else:
         kname = "attention_flat_kernel" + cold + " + attention_merge_kernel (one launch pair per layer)"
@@ -1071,7 +1085,17 @@ def main():
             np.array_equal(to_bits(got[0]), to_bits(want[0])) and np.array_equal(to_bits(got[1]), to_bits(want[1]))),
             "after_decode_steps": start + cpu_steps}
     if not args.no_attention and cfg["dtype"] in ("bfloat16", "float16") and D == 128:
-        result["paged_attention"] = attention_leg(cfg, pools, B, dev)
+        attn = attention_leg(cfg, pools, B, dev)
+        mid = cfg.get("attention_mid_context")
+        if mid and all(int(p.lens[:B].min()) >= mid for p in pools):
+            # the trajectory's middle: every row cropped to `mid` positions (the legs after this
+            # one prefill again)
+            for p in pools:
+                p.crop(B, mid)
+            m = attention_leg(cfg, pools, B, dev)
+            attn["at_mid_context"] = {k: m[k] for k in ("kernel", "context", "us_per_layer_call", "achieved",
+                                                       "frac", "bytes_per_call", "parity")}
+        result["paged_attention"] = attn
     if args.quant and cfg["dtype"] in ("bfloat16", "float16"):
         result["quantized_kv"] = quant_leg(cfg, wl, steps, dev, decode_ms / steps)
     if not args.no_beam:
