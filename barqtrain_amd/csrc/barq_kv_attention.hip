@@ -610,6 +610,10 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
   int blk0 = PRE ? 0 : (int)a.page_div.div((uint32_t)t_begin);
   const int blk_end = t_end > t_begin ? (int)a.page_div.div((uint32_t)(t_end - 1)) + 1 : blk0;
   int pt[kTableRegs];
+  // The pair kernel keeps its query fragments in registers (it has them to spare), the others
+  // read them from LDS for every chunk.
+  constexpr bool kQReg = PRE && !COLD && R == 1;
+  u32x4 qreg[kSteps];
   {
     u32x4 qv[kSteps];
     if constexpr (PRE) {
@@ -622,7 +626,12 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
       issue_query<HD>(a, b, kvh, lane, qv);
     }
 #pragma unroll
-    for (int st = 0; st < kSteps; ++st) lq[st][lane] = qv[st];
+    for (int st = 0; st < kSteps; ++st) {
+      if constexpr (kQReg)
+        qreg[st] = qv[st];
+      else
+        lq[st][lane] = qv[st];
+    }
   }
   check_table<COLD>(a, pt);
 
@@ -665,12 +674,13 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
   // codes: the chunk registers hold a quantised chunk with moderate scales (see k_operand).
   // kcodes: the K registers hold a quantised chunk's codes with moderate scales (k_operand);
   // vcold: the V registers hold a quantised chunk's codes, checked here before P.V.
+  constexpr bool kLazyMax = !COLD && R == 1;
   auto compute = [&](int tc, const u32x4 (&kv)[kSteps], u32x4 (&vv)[kVLoads], bool kcodes, bool vcold) {
     // Scores: lane (g, n16), register r = row 4g + r, position tc + n16; log2 units.
     f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < kSteps; ++st)
-      sc = mfma_qk<E>(lq[st][lane], (COLD && kcodes) ? k_operand<E>(kv[st]) : kv[st], sc);
+      sc = mfma_qk<E>(kQReg ? qreg[st] : lq[st][lane], (COLD && kcodes) ? k_operand<E>(kv[st]) : kv[st], sc);
     float x[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) x[r] = sc[r] * a.scale_log2;
@@ -682,28 +692,64 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
         if (tc + n16 > len - T + row % T) x[r] = -INFINITY;
       }
     }
-    float alpha[4];
+    if constexpr (kLazyMax) {
+      // Up to 4 query rows over two-byte pages: the running maximum moves only when a score of
+      // the chunk exceeds it by more than 8 (log2 units), so most chunks skip the row reductions
+      // and the rescale.  Probabilities are then at most 2^8 against the row's reference maximum
+      // (sums stay far from the float range; the output is the same quotient, rounded apart).
+      bool up = false;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float mnew = fmaxf(m_run[r], row16_max(x[r]));
-      const float mu = mnew == -INFINITY ? 0.f : mnew;
-      alpha[r] = __builtin_amdgcn_exp2f(m_run[r] - mu);
-      x[r] = __builtin_amdgcn_exp2f(x[r] - mu);
-      l_part[r] = l_part[r] * alpha[r] + x[r];
-      m_run[r] = mnew;
-    }
-    if (g < R) *(f32x4*)&lp[n16][4 * g] = f32x4{x[0], x[1], x[2], x[3]};
-    // Every chunk rescales every row's accumulators (alpha is exactly 1 where a row's maximum did
-    // not move, so the values are those of rescaling only on change): with the multiply under a
-    // branch the compiler kept two copies of the accumulators live (8 and 16 query rows spilled).
+      for (int r = 0; r < 4; ++r) up = up || x[r] > m_run[r] + 8.0f;
+      if (__builtin_amdgcn_ballot_w64(up && g < R) != 0) {
+        float alpha[4];
 #pragma unroll
-    for (int r2 = 0; r2 < R; ++r2)
+        for (int r = 0; r < 4; ++r) {
+          const float mnew = fmaxf(m_run[r], row16_max(x[r]));
+          const float mu = mnew == -INFINITY ? 0.f : mnew;
+          alpha[r] = __builtin_amdgcn_exp2f(m_run[r] - mu);
+          l_part[r] *= alpha[r];
+          m_run[r] = mnew;
+        }
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const float al = lane_value(alpha[m], 16 * r2);
+        for (int r2 = 0; r2 < R; ++r2)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[r2][e][m] *= al;
+          for (int m = 0; m < 4; ++m) {
+            const float al = lane_value(alpha[m], 16 * r2);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[r2][e][m] *= al;
+          }
       }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float mu = m_run[r] == -INFINITY ? 0.f : m_run[r];
+        x[r] = __builtin_amdgcn_exp2f(x[r] - mu);
+        l_part[r] += x[r];
+      }
+      if (g < R) *(f32x4*)&lp[n16][4 * g] = f32x4{x[0], x[1], x[2], x[3]};
+    } else {
+      float alpha[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float mnew = fmaxf(m_run[r], row16_max(x[r]));
+        const float mu = mnew == -INFINITY ? 0.f : mnew;
+        alpha[r] = __builtin_amdgcn_exp2f(m_run[r] - mu);
+        x[r] = __builtin_amdgcn_exp2f(x[r] - mu);
+        l_part[r] = l_part[r] * alpha[r] + x[r];
+        m_run[r] = mnew;
+      }
+      if (g < R) *(f32x4*)&lp[n16][4 * g] = f32x4{x[0], x[1], x[2], x[3]};
+      // Every chunk rescales every row's accumulators (alpha is exactly 1 where a row's maximum
+      // did not move): with the multiply under a branch the compiler kept two copies of the
+      // accumulators live at 8 and 16 query rows (spills).
+#pragma unroll
+      for (int r2 = 0; r2 < R; ++r2)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const float al = lane_value(alpha[m], 16 * r2);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[r2][e][m] *= al;
+        }
+    }
     bool vcodes = false;
     if (COLD && vcold) {
       vcodes = __builtin_amdgcn_ballot_w64(!scales_moderate<true>(vv)) == 0;
