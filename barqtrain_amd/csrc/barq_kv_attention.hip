@@ -58,8 +58,8 @@ constexpr int kMinRangeChunks = 4;         // the automatic range never goes bel
 constexpr int kPairWaves = 8;              // waves of a pair-kernel workgroup
 constexpr int64_t kPairMinPairs = 128;     // the pair kernel from this many (row, kv head) pairs ...
 constexpr int64_t kPairMaxChunks = 44;     // ... of at most this many 16-position chunks (max_seq);
-// with up to 4 query rows (two-byte pages): this many, and from twice the pairs (every CU busy)
-// this many
+// with up to 4 query rows: this many, and over two-byte pages from twice the pairs (every CU
+// busy) this many
 constexpr int64_t kPairMaxChunksR1 = 64;
 constexpr int64_t kPairMaxChunksR1Wide = 128;
 static_assert(kPairMaxChunks <= kTableEntries && kPairMaxChunksR1Wide <= kTableEntries,
@@ -674,7 +674,7 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
   // codes: the chunk registers hold a quantised chunk with moderate scales (see k_operand).
   // kcodes: the K registers hold a quantised chunk's codes with moderate scales (k_operand);
   // vcold: the V registers hold a quantised chunk's codes, checked here before P.V.
-  constexpr bool kLazyMax = !COLD && R == 1;
+  constexpr bool kLazyMax = R == 1 && (!COLD || PRE);  // (the quantised flat kernel would spill)
   auto compute = [&](int tc, const u32x4 (&kv)[kSteps], u32x4 (&vv)[kVLoads], bool kcodes, bool vcold) {
     // Scores: lane (g, n16), register r = row 4g + r, position tc + n16; log2 units.
     f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -693,7 +693,7 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
       }
     }
     if constexpr (kLazyMax) {
-      // Up to 4 query rows over two-byte pages: the running maximum moves only when a score of
+      // Up to 4 query rows: the running maximum moves only when a score of
       // the chunk exceeds it by more than 8 (log2 units), so most chunks skip the row reductions
       // and the rescale.  Probabilities are then at most 2^8 against the row's reference maximum
       // (sums stay far from the float range; the output is the same quotient, rounded apart).
@@ -1082,9 +1082,9 @@ hipError_t launch_typed(AttnArgs a, bool merge, hipStream_t stream) {
   // SIMD keep the accumulators in registers): one workgroup per pair.
   if constexpr (U && R <= 2) {
     const int64_t pairs = (int64_t)a.batch * a.kv_heads;
-    const int64_t max_chunks = R > 1 || COLD                ? kPairMaxChunks
-                               : pairs >= 2 * kPairMinPairs ? kPairMaxChunksR1Wide
-                                                            : kPairMaxChunksR1;
+    const int64_t max_chunks = R > 1                        ? kPairMaxChunks
+                               : COLD || pairs < 2 * kPairMinPairs ? kPairMaxChunksR1
+                                                                   : kPairMaxChunksR1Wide;
     if (a.range_chunks == 0 && pairs >= kPairMinPairs && (a.max_seq + kBlock - 1) / kBlock <= max_chunks) {
       hipLaunchKernelGGL((attention_pair_kernel<HD, E, R, OutT, COLD, kPairWaves>), dim3((unsigned)pairs),
                          dim3(kPairWaves * kWave), 0, stream, a);
