@@ -541,12 +541,36 @@ __device__ __forceinline__ bool hw_decodable(uint32_t w0, uint32_t w1, uint32_t 
   return mid == 0x40404040u && nan == 0;
 }
 
+// gfx950's scaled conversion: the two E4M3 codes of half HI of w times the fp32 scale s, rounded
+// once to bf16.  Checked on the GPU for every code pair and every scale byte 1 .. 254 (s = 2^(b -
+// 127)): identical to rounding the exact product, signed zeros included.
+template <bool HI>
+__device__ __forceinline__ uint32_t cvt2_bf16(uint32_t w, float s) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, s, HI));
+}
+__device__ __forceinline__ float e8m0_scale(uint32_t b) { return __uint_as_float(b << 23); }
+
 template <int KIND>
 __device__ __forceinline__ typename Vec<KIND, 8>::Out hw_decode(uint32_t w0, uint32_t w1, uint32_t sk0, uint32_t sk1) {
   using V = Vec<KIND, 8>;
   using E = Elem<KIND>;
   using Bits = typename E::Bits;
   typename V::OutU val;
+  if constexpr (KIND == BARQ_KV_BF16) {
+    // two conversions per pair of codes, one with each code's scale, and a half of each kept
+    uint32_t r[4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t w = j ? w1 : w0, sw = j ? sk1 : sk0;
+      const uint32_t a0 = cvt2_bf16<false>(w, e8m0_scale(sw & 0xFFu));
+      const uint32_t b0 = cvt2_bf16<false>(w, e8m0_scale((sw >> 8) & 0xFFu));
+      const uint32_t a1 = cvt2_bf16<true>(w, e8m0_scale((sw >> 16) & 0xFFu));
+      const uint32_t b1 = cvt2_bf16<true>(w, e8m0_scale(sw >> 24));
+      r[2 * j] = (a0 & 0xFFFFu) | (b0 & 0xFFFF0000u);
+      r[2 * j + 1] = (a1 & 0xFFFFu) | (b1 & 0xFFFF0000u);
+    }
+    return typename V::Out{r[0], r[1], r[2], r[3]};
+  }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const uint32_t w = j ? w1 : w0, sw = j ? sk1 : sk0;
@@ -573,6 +597,18 @@ __device__ __forceinline__ typename Vec<KIND, 8>::Out hw_decode(uint32_t w0, uin
     }
   }
   return val.v;
+}
+
+// hw_decode for one scale byte over all 8 codes (a value vector: one scale per position and head).
+template <int KIND>
+__device__ __forceinline__ typename Vec<KIND, 8>::Out hw_decode_one(uint32_t w0, uint32_t w1, uint32_t sb) {
+  if constexpr (KIND == BARQ_KV_BF16) {
+    const float s = e8m0_scale(sb);
+    return typename Vec<KIND, 8>::Out{cvt2_bf16<false>(w0, s), cvt2_bf16<true>(w0, s), cvt2_bf16<false>(w1, s),
+                                      cvt2_bf16<true>(w1, s)};
+  } else {
+    return hw_decode<KIND>(w0, w1, sb * 0x01010101u, sb * 0x01010101u);
+  }
 }
 
 // VE elements from their E4M3 codes and scales: keys with VE per-channel scale bytes (ksc),
@@ -777,9 +813,12 @@ __device__ __forceinline__ void cold_round(const GatherArgs& a, int cold, int t0
       const uint32_t sk1 = VALUES ? vsc[i][c] * 0x01010101u : ksc[c].v.y;
       const bool dead = t0 + i >= live;
       typename V::Out v;
-      if (__builtin_amdgcn_ballot_w64(!(dead || hw_decodable(w0, w1, sk0, sk1))) == 0)  // uniform
-        v = hw_decode<KIND>(w0, w1, sk0, sk1);
-      else
+      if (__builtin_amdgcn_ballot_w64(!(dead || hw_decodable(w0, w1, sk0, sk1))) == 0) {  // uniform
+        if constexpr (VALUES)
+          v = hw_decode_one<KIND>(w0, w1, vsc[i][c]);
+        else
+          v = hw_decode<KIND>(w0, w1, sk0, sk1);
+      } else
         v = exact8<KIND>(w0, w1, sk0, sk1);
       if (dead) v = typename V::Out(0);
       if (spaced) wait_vm<0>();

@@ -67,6 +67,15 @@ class CapturedDecodeStep:
         for i, p in enumerate(self.pools):
             p.lens = self._lens[i]
             p.hw = self._hw[i]
+        # The quantised pools' leading-cold-block counts, stacked the same way.
+        self._qidx = np.flatnonzero(self.quantized)
+        if self._qidx.size:
+            if any(self.pools[i].cold_blocks.base is not None for i in self._qidx):
+                raise ValueError("a page pool can belong to one captured step only")
+            self._cold = np.stack([self.pools[i].cold_blocks for i in self._qidx])
+            for j, i in enumerate(self._qidx):
+                self.pools[i].cold_blocks = self._cold[j]
+            self._windows = np.array([self.pools[i].window for i in self._qidx], dtype=np.int64)
         if bucket is None:
             bucket = max(64, -(-self.capacity // 16))
         self.bucket = int(bucket) if bucket else self.capacity
@@ -129,17 +138,33 @@ class CapturedDecodeStep:
                 f"paged KV cache capacity exceeded: requested {worst}, max_cache_len={self.capacity}")
         P = p0.page_size
         need = np.maximum(np.minimum(-(-ends // P), p0.max_blocks) - (-(-hw // P)), 0).sum(axis=1)
-        for p, n in zip(self.pools, need):
-            p.ensure_free(int(n), "append")
-        cold = [p._cold_after(B, T) if q else None for p, q in zip(self.pools, self.quantized)]
-        compress = any(c is not None and c[1] > 0 for c in cold)
+        grows = bool(need.any())
+        if grows:
+            for p, n in zip(self.pools, need):
+                p.ensure_free(int(n), "append")
+        # Blocks leaving the residual window, for every quantised pool at once (the per-pool
+        # _cold_after / _quantised arithmetic on the stacked shadows).
+        moved = None
+        if self._qidx.size:
+            frontier = np.maximum(ends[self._qidx] - self._windows[:, None], 0) // P
+            cold_b = self._cold[:, :B]
+            moved = np.maximum(frontier - cold_b, 0).sum(axis=1)
+            movers = np.flatnonzero(moved)
+            for j in movers:
+                self.pools[self._qidx[j]].ensure_cold(int(moved[j]))
+        compress = moved is not None and movers.size > 0
         self._graph(min(self.capacity, -(-worst // self.bucket) * self.bucket), compress).replay()
         lens += T
         np.maximum(hw, lens, out=hw)
-        for p, n, c in zip(self.pools, need, cold):
-            p.free_count -= int(n)
-            if c is not None:
-                p._quantised(B, *c)
+        if grows:
+            for p, n in zip(self.pools, need):
+                p.free_count -= int(n)
+        if compress:
+            np.maximum(cold_b, frontier, out=cold_b)
+            for j in movers:
+                p = self.pools[self._qidx[j]]
+                p.cold_free -= int(moved[j])
+                p.free_count += int(moved[j])  # each quantised block returned its full-precision page
         if not views:
             return None
         seqs = ends.max(axis=1).tolist()
