@@ -330,16 +330,22 @@ __device__ __forceinline__ void load_table(const AttnArgs& a, int b, int blk0, i
 
 // Query rows of (row b, kv head kvh) in the A layout of the score MFMA: lane (row n16, k-group g)
 // holds dims 32 * step + 8 * g .. +7 of query row n16 (zero for padding rows).
-template <int HD>
+// Query fragments in the K layout of the kernel: lane (g, n16) holds, for step st, 8 dims of row
+// n16 -- dims 32 st + 8 g (two-byte pages), or 8 kSteps g + 8 st with QUANT (quantised pools: each
+// lane's K codes and scales of a position are then one contiguous run, loaded 16 bytes at a time).
+// Any assignment of dims to (step, g) gives the same dot products as long as Q and K share it.
+template <int HD, bool QUANT>
 __device__ __forceinline__ void issue_query(const AttnArgs& a, int b, int kvh, int lane,
                                             u32x4 (&qv)[Head<HD>::kSteps]) {
+  constexpr int kSteps = Head<HD>::kSteps;
   const int n16 = lane & 15;
   const int g = lane >> 4;
   const bool qrow = n16 < a.rows;
   const char* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(kvh * a.group + n16 / a.tokens) * a.q_sh +
-                   (int64_t)(n16 % a.tokens) * a.q_st + 16 * g;
+                   (int64_t)(n16 % a.tokens) * a.q_st + (QUANT ? 16 * kSteps * g : 16 * g);
 #pragma unroll
-  for (int st = 0; st < Head<HD>::kSteps; ++st) qv[st] = qrow ? *(const u32x4*)(qp + 64 * st) : u32x4{0, 0, 0, 0};
+  for (int st = 0; st < kSteps; ++st)
+    qv[st] = qrow ? *(const u32x4*)(qp + (QUANT ? 16 : 64) * st) : u32x4{0, 0, 0, 0};
 }
 
 // A piece's first round trip, started by its caller before the row's length is known: the
@@ -351,9 +357,9 @@ struct PieceStart {
 };
 
 // K and V of one 16-position chunk for this lane.  K: lane (g, n16) holds dims 32 * step + 8 * g
-// .. +7 of position tc + n16; V: lane (vpos, vdim) = (lane / (HD / 8), lane % (HD / 8)) holds
-// dims 8 * vdim .. +7 of position tc + kVPos * s + vpos.  Positions >= end load nothing and read
-// as zero.
+// .. +7 of position tc + n16 (quantised pools: dims 8 kSteps g + 8 step .. +7, see issue_query);
+// V: lane (vpos, vdim) = (lane / (HD / 8), lane % (HD / 8)) holds dims 8 * vdim .. +7 of position
+// tc + kVPos * s + vpos.  Positions >= end load nothing and read as zero.
 template <int HD, bool UNIFORM, bool PRED, bool COLD>
 __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kTableRegs], int blk0,
                                            const char* kbase, const char* vbase, int tc, int end,
@@ -379,14 +385,18 @@ __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kT
         const int t0 = tc - (int)(blk * (uint32_t)a.page_size);
         const int64_t head = (int64_t)kvh * HD;
         const int64_t code_page = (int64_t)c * a.page_size * a.kv_heads * HD;
-        const uint8_t* kc = a.kcodes + code_page + (int64_t)(t0 + n16) * a.kv_heads * HD + head + 8 * g;
-        const uint8_t* ks = a.kscales + ((int64_t)c * a.kv_heads) * HD + head + 8 * g;
+        // (the quantised kernels' K layout: lane g's codes and scales for every step are one run
+        // of 8 kSteps bytes, loaded 16 bytes at a time)
+        const uint8_t* kc =
+            a.kcodes + code_page + (int64_t)(t0 + n16) * a.kv_heads * HD + head + 8 * kSteps * g;
+        const uint8_t* ks = a.kscales + ((int64_t)c * a.kv_heads) * HD + head + 8 * kSteps * g;
+        const bool in = !PRED || tc + n16 < end;
 #pragma unroll
-        for (int st = 0; st < kSteps; ++st) {
-          const bool in = !PRED || tc + n16 < end;
-          const uint2 cw = in ? *(const uint2*)(kc + 32 * st) : uint2{0, 0};
-          const uint2 sw = *(const uint2*)(ks + 32 * st);
-          kv[st] = u32x4{cw.x, cw.y, sw.x, sw.y};
+        for (int st = 0; st < kSteps; st += 2) {
+          const u32x4 cw = in ? *(const u32x4*)(kc + 8 * st) : u32x4{0, 0, 0, 0};
+          const u32x4 sw = *(const u32x4*)(ks + 8 * st);
+          kv[st] = u32x4{cw[0], cw[1], sw[0], sw[1]};
+          kv[st + 1] = u32x4{cw[2], cw[3], sw[2], sw[3]};
         }
 #pragma unroll
         for (int s = 0; s < kVLoads; ++s) {
@@ -406,7 +416,7 @@ __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kT
     const char* vp = vbase + base + vlane;
 #pragma unroll
     for (int st = 0; st < kSteps; ++st)
-      kv[st] = (!PRED || tc + n16 < end) ? ld_page_k(kp + 64 * st) : u32x4{0, 0, 0, 0};
+      kv[st] = (!PRED || tc + n16 < end) ? ld_page_k(kp + (COLD ? 16 : 64) * st) : u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < kVLoads; ++s)
       vv[s] = (!PRED || tc + kVPos * s + vpos < end) ? ld_page(vp + kVPos * s * a.row_bytes) : u32x4{0, 0, 0, 0};
@@ -623,7 +633,7 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
       for (int st = 0; st < kSteps; ++st) qv[st] = pre->qv[st];
     } else {
       issue_table(a, b, blk0, blk_end, lane, pt);
-      issue_query<HD>(a, b, kvh, lane, qv);
+      issue_query<HD, COLD>(a, b, kvh, lane, qv);
     }
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) {
@@ -637,7 +647,7 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
 
   const char* kbase = a.kpages + (int64_t)kvh * a.head_bytes;
   const char* vbase = a.vpages + (int64_t)kvh * a.head_bytes;
-  const int klane = n16 * a.row_bytes + 16 * g;
+  const int klane = n16 * a.row_bytes + (COLD ? 16 * kSteps * g : 16 * g);  // the K layout (issue_query)
   const int vlane = vpos * a.row_bytes + 16 * vdim;
 
   float m_run[4], l_part[4];
@@ -938,7 +948,7 @@ void attention_pair_kernel(const AttnArgs a) {
   int len = a.seq_lens[b];
   PieceStart<HD> ps;
   issue_table(a, b, 0, (int)a.page_div.div((uint32_t)a.max_seq + a.page_size - 1), threadIdx.x & (kWave - 1), ps.pt);
-  issue_query<HD>(a, b, kvh, threadIdx.x & (kWave - 1), ps.qv);
+  issue_query<HD, COLD>(a, b, kvh, threadIdx.x & (kWave - 1), ps.qv);
   if (len > a.max_seq) {
     if (threadIdx.x == 0 && kvh == 0) atomicOr(a.errors, BARQ_KV_ERRBIT_ATTN_SHORT);
     len = a.max_seq;
