@@ -328,12 +328,11 @@ __device__ __forceinline__ void load_table(const AttnArgs& a, int b, int blk0, i
   check_table<COLD>(a, pt);
 }
 
-// Query rows of (row b, kv head kvh) in the A layout of the score MFMA: lane (row n16, k-group g)
-// holds dims 32 * step + 8 * g .. +7 of query row n16 (zero for padding rows).
-// Query fragments in the K layout of the kernel: lane (g, n16) holds, for step st, 8 dims of row
-// n16 -- dims 32 st + 8 g (two-byte pages), or 8 kSteps g + 8 st with QUANT (quantised pools: each
-// lane's K codes and scales of a position are then one contiguous run, loaded 16 bytes at a time).
-// Any assignment of dims to (step, g) gives the same dot products as long as Q and K share it.
+// Query rows of (row b, kv head kvh) in the A layout of the score MFMA, in the kernel's K order:
+// lane (row n16, k-group g) holds, for step st, 8 dims of query row n16 (zero for padding rows) --
+// dims 32 st + 8 g (two-byte pages), or 8 kSteps g + 8 st with QUANT (quantised pools: each lane's
+// K codes and scales of a position are then one contiguous run, loaded 16 bytes at a time).  Any
+// assignment of dims to (step, g) gives the same dot products as long as Q and K share it.
 template <int HD, bool QUANT>
 __device__ __forceinline__ void issue_query(const AttnArgs& a, int b, int kvh, int lane,
                                             u32x4 (&qv)[Head<HD>::kSteps]) {
