@@ -771,12 +771,14 @@ def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10, probe=
     mem = pools[0].memory_bytes()
     full = 2 * B * mb * P * H * D * esize
     return {
-        "kernels": "stream_kernel (append) + compress_kernel + gather_cold_kernel per layer, graph-replayed",
+        "kernels": ("update_cold_lanes_kernel (append + dequantising gather, one launch) per layer, and "
+                    "compress_regs_kernel when blocks leave the window; graph-replayed"),
         "format": f"fp8 E4M3 codes, E8M0 scales (keys per channel, values per token over a page), "
                   f"residual window {window} tokens",
         "us_per_step_all_layers": round(ms * 1e3, 1),
         "full_precision_us_per_step": round(bf16_ms_per_step * 1e3, 1),
-        "gather_cold_kernel": {"avg_launch_us": round(gather_us, 2), "bytes_per_launch": gather_bytes,
+        "gather_cold_kernel": {"kernel": "gather_cold_lanes_kernel (the dequantising gather alone)",
+                               "avg_launch_us": round(gather_us, 2), "bytes_per_launch": gather_bytes,
                                "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                "frac": round(gbs / HBM_PEAK_GBS, 4)},
         "memory_per_layer_bytes": {**mem, "full_precision_pool": full,
