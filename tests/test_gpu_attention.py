@@ -61,7 +61,7 @@ def make_rows(B, Hkv, page, lens, dtype, seed, order_seed=None, cap=None, D=128)
 
 
 def check(pool, kd, vd, lens, G, T, dtype, seed, out_f32=True, split_tokens=0, max_seq=0, ws=None,
-          scale=None):
+          scale=None, tol=None):
     B, Hkv, D = kd.shape[0], kd.shape[1], kd.shape[3]
     gen = torch.Generator().manual_seed(seed)
     q = hf_layout(B, G * Hkv, T, D, dtype, gen).cuda()
@@ -71,7 +71,7 @@ def check(pool, kd, vd, lens, G, T, dtype, seed, out_f32=True, split_tokens=0, m
     torch.cuda.synchronize()
     want = decode_attention_reference(q.double().cpu().numpy(), kd, vd, lens, scale)
     got = out.double().cpu().numpy()
-    tol = F32_TOL if out_f32 else OUT_TOL[dtype]
+    tol = tol or (F32_TOL if out_f32 else OUT_TOL[dtype])
     ok, ratio = within_tolerance(got, want, **tol)
     assert ok, f"G={G} T={T} lens={list(lens)[:8]} split={split_tokens}: error {ratio:.3g} x tolerance"
     return ws
@@ -156,6 +156,44 @@ def test_long_pairs_one_launch(rows, Hkv, cap, dtype, D):
     check(pool, kd, vd, lens, 4, 1, dtype, seed=9, out_f32=False)
     check(pool, kd, vd, lens, 4, 1, dtype, seed=9, split_tokens=256)  # the flat schedule
     assert pool.errors() == 0
+
+
+@pytest.mark.parametrize("pattern", ["rising", "falling", "spikes"])
+def test_running_maximum_moves_between_chunks(pattern):
+    """Score ranges that move between chunks (with up to 4 query rows the running maximum moves
+    only when a score exceeds it by 2^8): keys scaled per position so that the scores of each of
+    the first chunks pass the last maximum by more than that (a rescale at each), fall (none
+    after the first), or spike at a few positions; 128 pairs (the pair kernel) and 8 pairs (the
+    flat schedule), G = 4, one and two query tokens, both output types.  Scores reach ~25 here,
+    whose fp32 sums carry ~1e-5 absolute error into the weights, so the float32 check allows
+    1e-4 (a missed rescale is off by a factor of 2^8 or more)."""
+    D, cap, page = 128, 704, 16
+    for B, Hkv in ((32, 4), (4, 2)):
+        rng = np.random.default_rng(len(pattern) * 100 + B)
+        lens = sorted([cap, 1, 17, 255] + rng.integers(1, cap, size=B - 4).tolist(), reverse=True)
+        gen = torch.Generator().manual_seed(B + 5)
+        k = torch.randn(B, Hkv, cap, D, generator=gen)
+        v = torch.randn(B, Hkv, cap, D, generator=gen)
+        pos = torch.arange(cap, dtype=torch.float32)
+        if pattern == "rising":  # +2.2 a chunk on the scores' spread: > 8 (log2) on the maximum
+            f = 1 + 2.2 * torch.clamp(pos / 16, max=4.0)
+        elif pattern == "falling":
+            f = 1 + 2.2 * torch.clamp((cap - pos) / 16, max=4.0)
+        else:
+            f = torch.ones(cap)
+            f[torch.from_numpy(rng.choice(cap, size=12, replace=False))] = 10.0
+        k = k * f[None, None, :, None]
+        kd = k.to(torch.bfloat16).double().numpy()
+        vd = v.to(torch.bfloat16).double().numpy()
+        order = torch.from_numpy(rng.permutation(B * (cap // page)).astype(np.int32))
+        pool = CPool(max_batch=B, max_blocks=cap // page, page_size=page, heads=Hkv, dim=D, dtype=torch.bfloat16,
+                     num_pages=B * (cap // page), order=order)
+        fill_pool(pool, kd, vd, lens, torch.bfloat16)
+        torch.cuda.synchronize()
+        for i, (G, T) in enumerate([(4, 1), (2, 2)]):
+            check(pool, kd, vd, lens, G, T, torch.bfloat16, seed=700 + i, tol=dict(rtol=1e-4, atol=1e-4))
+        check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=9, out_f32=False)
+        assert pool.errors() == 0
 
 
 def test_flat_schedule_with_ranges_of_two_sizes():

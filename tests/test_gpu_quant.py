@@ -355,16 +355,19 @@ def test_decode_attention_reads_quantised_pages(hip, dtype, page, window, D):
     assert pool.errors() == 0
 
 
-def test_decode_attention_on_quantised_pages_many_pairs(hip):
-    """Attention over a quantised pool with 128 (row, kv head) pairs of short ragged rows (the
-    one-launch pair kernel): against the float64 reference over the dequantising gather's K/V."""
+@pytest.mark.parametrize("cap", [640, 1024])
+def test_decode_attention_on_quantised_pages_many_pairs(hip, cap):
+    """Attention over a quantised pool with 128 (row, kv head) pairs of ragged rows (the one-launch
+    pair kernel: up to 44 chunks, and with up to 4 query rows up to 64): against the float64
+    reference over the dequantising gather's K/V."""
     from attn_ref import decode_attention_reference, within_tolerance
     from barqtrain_amd.paged import QuantPagePool
 
     H, D, P, W = 4, 128, 16, 32
-    rng = np.random.default_rng(77)
-    lens = sorted([600, 1, 16, 33] + rng.integers(40, 600, size=28).tolist(), reverse=True)
-    B, cap = len(lens), 640
+    rng = np.random.default_rng(77 + cap)
+    top = cap - 40
+    lens = sorted([top, top - 15, 1, 16, 33] + rng.integers(40, top, size=27).tolist(), reverse=True)
+    B = len(lens)
     pool = QuantPagePool(max_batch=B, max_blocks=cap // P, page_size=P, kv_heads=H, head_dim=D,
                          dtype=torch.bfloat16, device="cuda", window=W)
     gen = torch.Generator().manual_seed(78)
