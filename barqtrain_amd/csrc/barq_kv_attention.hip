@@ -368,6 +368,7 @@ __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kT
   constexpr int kSteps = Head<HD>::kSteps;
   constexpr int kVPos = Head<HD>::kVPos;
   constexpr int kVLoads = Head<HD>::kVLoads;
+  static_assert(UNIFORM || !COLD, "quantised pools read whole-chunk pages (their K order assumes it)");
   cold = false;
   if constexpr (UNIFORM) {
     // page_size is a multiple of 16: the chunk lies in one page, its base a scalar.
