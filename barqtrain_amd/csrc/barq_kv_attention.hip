@@ -684,7 +684,9 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
   // codes: the chunk registers hold a quantised chunk with moderate scales (see k_operand).
   // kcodes: the K registers hold a quantised chunk's codes with moderate scales (k_operand);
   // vcold: the V registers hold a quantised chunk's codes, checked here before P.V.
-  constexpr bool kLazyMax = R == 1 && (!COLD || PRE);  // (the quantised flat kernel would spill)
+  // (with the rescale under a branch, the quantised flat kernel and 8+ rows on the flat schedule
+  // or over quantised pages spill)
+  constexpr bool kLazyMax = R == 1 ? !COLD || PRE : R == 2 && PRE && !COLD;
   auto compute = [&](int tc, const u32x4 (&kv)[kSteps], u32x4 (&vv)[kVLoads], bool kcodes, bool vcold) {
     // Scores: lane (g, n16), register r = row 4g + r, position tc + n16; log2 units.
     f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -703,9 +705,8 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
       }
     }
     if constexpr (kLazyMax) {
-      // Up to 4 query rows: the running maximum moves only when a score of
-      // the chunk exceeds it by more than 8 (log2 units), so most chunks skip the row reductions
-      // and the rescale.  Probabilities are then at most 2^8 against the row's reference maximum
+      // The running maximum moves only when a score of the chunk exceeds it by more than 8
+      // (log2 units), so most chunks skip the row reductions and the rescale.  Probabilities are then at most 2^8 against the row's reference maximum
       // (sums stay far from the float range; the output is the same quotient, rounded apart).
       bool up = false;
 #pragma unroll

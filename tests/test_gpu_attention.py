@@ -160,11 +160,11 @@ def test_long_pairs_one_launch(rows, Hkv, cap, dtype, D):
 
 @pytest.mark.parametrize("pattern", ["rising", "falling", "spikes"])
 def test_running_maximum_moves_between_chunks(pattern):
-    """Score ranges that move between chunks (with up to 4 query rows the running maximum moves
-    only when a score exceeds it by 2^8): keys scaled per position so that the scores of each of
+    """Score ranges that move between chunks (up to 4 query rows, and 8 in the pair kernel, move
+    the running maximum only when a score exceeds it by 2^8): keys scaled per position so that the scores of each of
     the first chunks pass the last maximum by more than that (a rescale at each), fall (none
     after the first), or spike at a few positions; 128 pairs (the pair kernel) and 8 pairs (the
-    flat schedule), G = 4, one and two query tokens, both output types.  Scores reach ~25 here,
+    flat schedule), G = 4 and 8, one and two query tokens, both output types.  Scores reach ~25 here,
     whose fp32 sums carry ~1e-5 absolute error into the weights, so the float32 check allows
     1e-4 (a missed rescale is off by a factor of 2^8 or more)."""
     D, cap, page = 128, 704, 16
@@ -190,7 +190,7 @@ def test_running_maximum_moves_between_chunks(pattern):
                      num_pages=B * (cap // page), order=order)
         fill_pool(pool, kd, vd, lens, torch.bfloat16)
         torch.cuda.synchronize()
-        for i, (G, T) in enumerate([(4, 1), (2, 2)]):
+        for i, (G, T) in enumerate([(4, 1), (2, 2), (8, 1)]):
             check(pool, kd, vd, lens, G, T, torch.bfloat16, seed=700 + i, tol=dict(rtol=1e-4, atol=1e-4))
         check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=9, out_f32=False)
         assert pool.errors() == 0
