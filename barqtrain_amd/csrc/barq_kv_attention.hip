@@ -56,10 +56,12 @@ constexpr int kMaxBatch = 1024;            // rows whose lengths the schedule st
 constexpr int kMaxWaves = 2048;            // resident waves of an MI355X: 256 CUs x 4 SIMDs x 2
 constexpr int kMinRangeChunks = 4;         // the automatic range never goes below 64 positions
 constexpr int kPairWaves = 8;              // waves of a pair-kernel workgroup
-constexpr int64_t kPairMinPairs = 128;     // the pair kernel from this many (row, kv head) pairs ...
-constexpr int64_t kPairMaxChunks = 44;     // ... of at most this many 16-position chunks (max_seq);
-// with up to 4 query rows: this many, and over two-byte pages from twice the pairs (every CU
-// busy) this many
+// The pair kernel (one workgroup per (row, kv head) pair) takes launches of at most kPairMaxChunks
+// 16-position chunks a pair (max_seq); from kPairMinPairs pairs with up to 4 query rows at most
+// kPairMaxChunksR1, and over two-byte pages from twice the pairs (every CU busy)
+// kPairMaxChunksR1Wide.
+constexpr int64_t kPairMinPairs = 128;
+constexpr int64_t kPairMaxChunks = 44;
 constexpr int64_t kPairMaxChunksR1 = 64;
 constexpr int64_t kPairMaxChunksR1Wide = 128;
 static_assert(kPairMaxChunks <= kTableEntries && kPairMaxChunksR1Wide <= kTableEntries,
@@ -1089,14 +1091,18 @@ int resident_waves(K kernel) {
 
 template <int HD, int E, int R, bool U, typename OutT, bool COLD>
 hipError_t launch_typed(AttnArgs a, bool merge, hipStream_t stream) {
-  // Many short pairs, the automatic split, whole-chunk pages, up to 8 query rows (two waves per
-  // SIMD keep the accumulators in registers): one workgroup per pair.
+  // Pairs of bounded length, the automatic split, whole-chunk pages, up to 8 query rows (two waves
+  // per SIMD keep the accumulators in registers): one workgroup per pair.
   if constexpr (U && R <= 2) {
     const int64_t pairs = (int64_t)a.batch * a.kv_heads;
-    const int64_t max_chunks = R > 1                        ? kPairMaxChunks
+    // Fewer pairs than kPairMinPairs leave CUs idle, but up to kPairMaxChunks a pair one launch
+    // still beats the flat pair of launches and its merge (C2 shape at batch 1: 650 positions
+    // 16.3 -> 12.6 us, 128 positions 12.8 -> 6.3 us; at 2048 the flat schedule wins, 14.8 against
+    // 28.4).
+    const int64_t max_chunks = R > 1 || pairs < kPairMinPairs        ? kPairMaxChunks
                                : COLD || pairs < 2 * kPairMinPairs ? kPairMaxChunksR1
                                                                    : kPairMaxChunksR1Wide;
-    if (a.range_chunks == 0 && pairs >= kPairMinPairs && (a.max_seq + kBlock - 1) / kBlock <= max_chunks) {
+    if (a.range_chunks == 0 && pairs > 0 && (a.max_seq + kBlock - 1) / kBlock <= max_chunks) {
       hipLaunchKernelGGL((attention_pair_kernel<HD, E, R, OutT, COLD, kPairWaves>), dim3((unsigned)pairs),
                          dim3(kPairWaves * kWave), 0, stream, a);
       return hipGetLastError();

@@ -404,13 +404,13 @@ class Workload:
 
 
 def pair_kernel_bounds(pairs, max_seq, rows, quantised):
-    """The library's one-launch (pair kernel) bounds for a one-token decode call: 128+ (row, kv
-    head) pairs, up to 8 query rows, and at most 44 16-position chunks, or, for up to 4 query rows,
-    64 chunks (over two-byte pages 128 from 256 pairs)."""
-    if pairs < 128 or rows > 8:
+    """The library's one-launch (pair kernel) bounds for a one-token decode call: up to 8 query
+    rows and at most 44 16-position chunks, or, from 128 (row, kv head) pairs with up to 4 query
+    rows, 64 chunks (over two-byte pages 128 from 256 pairs)."""
+    if pairs < 1 or rows > 8:
         return False
     chunks = -(-max_seq // 16)
-    if rows > 4:
+    if rows > 4 or pairs < 128:
         return chunks <= 44
     return chunks <= (128 if pairs >= 256 and not quantised else 64)
 

@@ -158,13 +158,33 @@ def test_long_pairs_one_launch(rows, Hkv, cap, dtype, D):
     assert pool.errors() == 0
 
 
+@pytest.mark.parametrize("B,Hkv,D", [(1, 8, 128), (3, 8, 128), (2, 2, 64)])
+def test_few_pairs_one_launch(B, Hkv, D):
+    """Fewer than 128 (row, kv head) pairs -- batch-1 decode -- take the one-launch pair kernel up
+    to 44 chunks a pair (704 positions): rows on and next to chunk boundaries, G = 4 / 8 / 1, two
+    query tokens, both output types; 705 positions take the flat schedule, which agrees."""
+    rng = np.random.default_rng(B * 10 + D)
+    lens = sorted([704, 17, 1][:B] + rng.integers(1, 705, size=max(B - 3, 0)).tolist(), reverse=True)
+    pool, kd, vd, lens = make_rows(B, Hkv, 16, lens, torch.bfloat16, seed=B + D, order_seed=B + D + 1, D=D,
+                                   cap=720)
+    ws = None
+    for i, (G, T) in enumerate([(4, 1), (8, 1), (1, 1), (2, 2)]):
+        ws = check(pool, kd, vd, lens, G, T, torch.bfloat16, seed=800 + i, ws=ws)
+    check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=9, out_f32=False)
+    assert pool.errors() == 0
+    pool, kd, vd, lens = make_rows(1, Hkv, 16, [705], torch.bfloat16, seed=B + D + 2, order_seed=B + D + 3, D=D)
+    check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=11)
+    assert pool.errors() == 0
+
+
 @pytest.mark.parametrize("pattern", ["rising", "falling", "spikes"])
 def test_running_maximum_moves_between_chunks(pattern):
     """Score ranges that move between chunks (up to 4 query rows, and 8 in the pair kernel, move
     the running maximum only when a score exceeds it by 2^8): keys scaled per position so that the scores of each of
     the first chunks pass the last maximum by more than that (a rescale at each), fall (none
-    after the first), or spike at a few positions; 128 pairs (the pair kernel) and 8 pairs (the
-    flat schedule), G = 4 and 8, one and two query tokens, both output types.  Scores reach ~25 here,
+    after the first), or spike at a few positions; 128 and 8 pairs (the pair kernel), and the
+    flat schedule (a fixed split) over the 8, G = 4 and 8, one and two query tokens, both output
+    types.  Scores reach ~25 here,
     whose fp32 sums carry ~1e-5 absolute error into the weights, so the float32 check allows
     1e-4 (a missed rescale is off by a factor of 2^8 or more)."""
     D, cap, page = 128, 704, 16
@@ -193,6 +213,8 @@ def test_running_maximum_moves_between_chunks(pattern):
         for i, (G, T) in enumerate([(4, 1), (2, 2), (8, 1)]):
             check(pool, kd, vd, lens, G, T, torch.bfloat16, seed=700 + i, tol=dict(rtol=1e-4, atol=1e-4))
         check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=9, out_f32=False)
+        if B * Hkv < 128:
+            check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=10, split_tokens=64, tol=dict(rtol=1e-4, atol=1e-4))
         assert pool.errors() == 0
 
 
