@@ -17,9 +17,10 @@ decode, C3 fragmented ragged batch with a random page permutation, C4 32k chunke
 rows are freed and re-prefilled with 8192 new tokens, which take the pages released rows left).
 
 A step runs as one replay of a captured HIP graph of the per-layer fused append+gather launches
-(graph mode, C1-C4; the step's new K/V are first copied into the graph's static input buffers,
-as a model's K/V projection would write them; every graph the window uses is captured before
-timing), or as host-launched layer calls (eager mode, the per-call path HF attention takes; C5).
+(graph mode, C1-C4; the step's new K/V are first copied into the graph's static input buffer,
+one copy for K and V, as a model's fused K/V projection would write them; every graph the window
+uses is captured before timing), or as host-launched layer calls (eager mode, the per-call path
+HF attention takes; C5).
 Throughput counts algorithmic bytes per step, summed over layers: append 2*B*T*tb (read new,
 write page) + gather sum_b(ctx_b)*tb (read) + B*S_max*tb (write, zero padding of short rows
 included), tb = 2*H*D*esize; metadata is not counted.  Per-step bytes come from the same length
@@ -356,8 +357,14 @@ class Workload:
         self.pools = [PagePool(max_batch=B, max_blocks=mb, page_size=P, kv_heads=H, head_dim=D, dtype=self.dtype,
                                device=dev, num_pages=num_pages, page_order=order) for _ in range(L)]
         gen = torch.Generator(device=dev).manual_seed(cfg["seed"])
-        self.k_dec = self._normal(gen, (n_steps, L, B, 1, H, D)).transpose(3, 4)
-        self.v_dec = self._normal(gen, (n_steps, L, B, 1, H, D)).transpose(3, 4)
+        # K and V of every decode step in one buffer, [step, K|V, L, B, H, 1, D] (a model's fused
+        # projection writes both): a step's inputs arrive with one copy
+        kv = torch.empty((n_steps, 2, L, B, 1, H, D), dtype=self.dtype, device=dev)
+        kv[:, 0] = self._normal(gen, (n_steps, L, B, 1, H, D))
+        kv[:, 1] = self._normal(gen, (n_steps, L, B, 1, H, D))
+        self.kv_dec = kv.transpose(4, 5)
+        self.k_dec = self.kv_dec[:, 0]
+        self.v_dec = self.kv_dec[:, 1]
         self.churn = churn_rows(cfg, n_steps)
         self.step_bytes = step_bytes_all(cfg, n_steps, self.churn)
         self.longest = longest_rows(cfg, n_steps, self.churn)
@@ -645,9 +652,8 @@ def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10, probe=
     hot = B * (-(-(window + 64) // P) + 2)
     pools = [QuantPagePool(max_batch=B, max_blocks=mb, page_size=P, kv_heads=H, head_dim=D, dtype=wl.dtype,
                            device=dev, window=window, num_pages=hot) for _ in range(L)]
-    kin = torch.empty((L, B, H, 1, D), dtype=wl.dtype, device=dev)
-    vin = torch.empty_like(kin)
-    step = CapturedDecodeStep(pools, B, 1, inputs=(kin, vin))
+    kvin = torch.empty((2, L, B, H, 1, D), dtype=wl.dtype, device=dev)
+    step = CapturedDecodeStep(pools, B, 1, inputs=(kvin[0], kvin[1]))
 
     def prefill():
         for layer, pool in enumerate(pools):
@@ -656,8 +662,7 @@ def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10, probe=
                 pool.append(k, v)
 
     def run(s):
-        kin.copy_(wl.k_dec[s])
-        vin.copy_(wl.v_dec[s])
+        kvin.copy_(wl.kv_dec[s])
         step.replay(views=False)
 
     tb, esize = tok_bytes(cfg), elem_size(cfg)
@@ -883,15 +888,13 @@ def main():
     if mode == "graph":
         if any(wl.churn):
             raise SystemExit("graph mode replays a fixed step; configurations with row churn run eager")
-        kin = torch.empty((L, B, H, 1, D), dtype=wl.dtype, device=dev)
-        vin = torch.empty_like(kin)
-        graph = CapturedDecodeStep(pools, B, 1, separate_commit=args.separate_commit, inputs=(kin, vin),
-                                   bucket=args.bucket)
+        kvin = torch.empty((2, L, B, H, 1, D), dtype=wl.dtype, device=dev)
+        graph = CapturedDecodeStep(pools, B, 1, separate_commit=args.separate_commit,
+                                   inputs=(kvin[0], kvin[1]), bucket=args.bucket)
         graph.prepare(wl.longest)  # no capture inside a timed region
 
         def run_step(s, record=False):
-            kin.copy_(wl.k_dec[s])
-            vin.copy_(wl.v_dec[s])
+            kvin.copy_(wl.kv_dec[s])
             graph.replay(views=False)
     else:
         # each step's per-layer input views, made before any timing (a model's projections
