@@ -672,8 +672,8 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
       load_table<COLD>(a, b, blk0, blk_end, lane, pt);
     }
   };
-  // The piece's last chunk, possibly partial: lanes past t_end load nothing.
-  auto load_tail = [&](int tc, u32x4 (&kv)[kSteps], u32x4 (&vv)[kVLoads], bool& cold) {
+  // A chunk of the piece, whole or its partial last one (lanes past t_end load nothing).
+  auto load_any = [&](int tc, u32x4 (&kv)[kSteps], u32x4 (&vv)[kVLoads], bool& cold) {
     slide(tc);
     if (tc + kBlock <= t_end)
       load_chunk<HD, UNIFORM, false, COLD>(a, pt, blk0, kbase, vbase, tc, t_end, klane, vlane, n16, g, vpos, vdim,
@@ -836,11 +836,11 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
     }
   } else {
     if (tc < t_end) {
-      load_tail(tc, kr[0], vr[0], cr[0]);
+      load_any(tc, kr[0], vr[0], cr[0]);
       for (;;) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-          if (tc + kBlock < t_end) load_tail(tc + kBlock, kr[1 - i], vr[1 - i], cr[1 - i]);
+          if (tc + kBlock < t_end) load_any(tc + kBlock, kr[1 - i], vr[1 - i], cr[1 - i]);
           __builtin_amdgcn_sched_barrier(0);
           step(i);
           if (tc >= t_end) goto chunks_done;
