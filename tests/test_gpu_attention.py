@@ -137,19 +137,22 @@ def test_many_short_pairs_one_launch(dtype, page, D):
     assert pool.errors() == 0
 
 
-@pytest.mark.parametrize("rows,Hkv,cap,dtype,D", [(32, 4, 1024, torch.bfloat16, 128),
-                                                  (32, 8, 2048, torch.float16, 128),
-                                                  (16, 8, 1024, torch.bfloat16, 64)])
-def test_long_pairs_one_launch(rows, Hkv, cap, dtype, D):
+@pytest.mark.parametrize("rows,Hkv,cap,dtype,D,page", [(32, 4, 1024, torch.bfloat16, 128, 16),
+                                                       (32, 8, 2048, torch.float16, 128, 16),
+                                                       (16, 8, 1024, torch.bfloat16, 64, 16),
+                                                       (32, 4, 1024, torch.float16, 128, 32),
+                                                       (16, 8, 1024, torch.bfloat16, 128, 64)])
+def test_long_pairs_one_launch(rows, Hkv, cap, dtype, D, page):
     """Up to 4 query rows take the one-launch pair kernel for longer rows: 128 pairs of up to 1024
-    positions, 256 pairs of up to 2048.  Its loop loads the next chunk unconditionally while that
-    chunk is whole and finishes the last one or two after it, so lengths sit on and next to chunk
-    boundaries (empty, 1, 15 .. 33, cap - 17 .. cap); G = 4 / 1 / 2, two tokens x 2 heads, the
-    2-byte output; the flat schedule (a fixed split) over the same pool agrees."""
+    positions, 256 pairs of up to 2048, pages of 16, 32 and 64 positions.  Its loop loads the next
+    chunk on every path, a partial last chunk with its positions past the row's end clamped to the
+    last one, so lengths sit on and next to chunk boundaries (empty, 1, 15 .. 33, cap - 17 ..
+    cap); G = 4 / 1 / 2, two tokens x 2 heads, the 2-byte output; the flat schedule (a fixed
+    split) over the same pool agrees."""
     rng = np.random.default_rng(cap + D)
     edges = [cap, cap - 1, cap - 15, cap - 16, cap - 17, 0, 1, 15, 16, 17, 31, 32, 33]
     lens = edges + rng.integers(0, cap + 1, size=rows - len(edges)).tolist()
-    pool, kd, vd, lens = make_rows(rows, Hkv, 16, lens, dtype, seed=cap + 7, order_seed=cap + 8, D=D)
+    pool, kd, vd, lens = make_rows(rows, Hkv, page, lens, dtype, seed=cap + 7, order_seed=cap + 8, D=D)
     ws = None
     for i, (G, T) in enumerate([(4, 1), (1, 1), (2, 2), (2, 1)]):
         ws = check(pool, kd, vd, lens, G, T, dtype, seed=500 + i, ws=ws)
