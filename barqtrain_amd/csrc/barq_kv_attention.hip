@@ -66,6 +66,10 @@ constexpr int64_t kPairMaxChunksR1 = 64;
 constexpr int64_t kPairMaxChunksR1Wide = 128;
 static_assert(kPairMaxChunks <= kTableEntries && kPairMaxChunksR1Wide <= kTableEntries,
               "a pair's blocks fit one table window");
+// When two workgroups a pair fit on the GPU at once (C2: 128 pairs, 256 CUs), a pair of at least
+// kPairSplitChunks chunks is cut over both (their exchange costs ~1.3 us; shorter rows lose more
+// than they gain).
+constexpr int kPairSplitChunks = 24;
 
 enum : int { kBF16 = 0, kF16 = 1 };
 
@@ -88,6 +92,7 @@ struct AttnArgs {
   const int32_t* block_table;
   const int32_t* seq_lens;
   int32_t* errors;
+  int32_t* ctrl;        // the pool's control words (arrival counts of split pairs)
   int64_t page_bytes;   // bytes between pages
   int64_t q_sb, q_sh, q_st;  // query strides, bytes
   int64_t o_sb, o_sh, o_st;  // output strides, bytes
@@ -935,15 +940,32 @@ void attention_flat_kernel(const AttnArgs a) {
 // waves), leaves its partial record in LDS, and the workgroup folds the W records into the output (same base-2
 // online-softmax fold as the merge kernel): one launch, no global workspace, each pair's bytes
 // read once.  A wave with no chunks leaves a neutral record (maximum -inf, sum 0).
-template <int HD, int E, int R, typename OutT, bool COLD, int W>
+//
+// S = 2 (launches whose 2 x pairs workgroups are resident at once): workgroups p and p + pairs
+// share pair p; a row of at least kPairSplitChunks chunks is cut over their 2W waves (ranges
+// dealt alternately), else the second workgroup leaves at once and the first takes the row alone.
+// A split pair's workgroups each fold their waves in LDS, publish the folded record in the
+// workspace and arrive on the pair's count in ctrl; the second to arrive folds both records into
+// the output and sets the count back to 0.  No workgroup waits for another, so the grid needs no
+// co-residency to finish.  The records are written with agent-scope atomic stores, which write
+// through to the device's coherence point (`global_store ... sc1`), every one of them complete
+// (s_waitcnt vmcnt(0), then the barrier) before the arrival; the second arrival reads them with
+// agent-scope atomic loads (`sc1`) issued after its count returned.  An agent-scope release fence
+// would write back the whole L2 (~1.7 us); this exchange costs ~1.3 us in all.
+template <int HD, int E, int R, typename OutT, bool COLD, int W, int S>
 __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(R <= 2 ? 2 : 1, R <= 2 ? 2 : 1)))
 void attention_pair_kernel(const AttnArgs a) {
+  static_assert(S == 1 || S == 2, "one or two workgroups a pair");
   constexpr int kRecMax = (int)record_floats(4 * R, HD);
+  constexpr int kQuads = HD / 4;
   __shared__ float lp[W][kBlock][kMaxRows];
   __shared__ u32x4 lq[W][Head<HD>::kSteps][kWave];
   __shared__ float s_rec[W * kRecMax];
+  __shared__ int s_arrived;
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
-  const int pair = blockIdx.x;
+  const int pairs = (int)gridDim.x / S;
+  const int half = S == 2 && (int)blockIdx.x >= pairs;
+  const int pair = (int)blockIdx.x - half * pairs;
   const int b = pair / a.kv_heads;
   const int kvh = pair - b * a.kv_heads;
   // The row's length, the table window (every block max_seq allows) and the query rows load
@@ -953,31 +975,34 @@ void attention_pair_kernel(const AttnArgs a) {
   issue_table(a, b, 0, (int)a.page_div.div((uint32_t)a.max_seq + a.page_size - 1), threadIdx.x & (kWave - 1), ps.pt);
   issue_query<HD, COLD>(a, b, kvh, threadIdx.x & (kWave - 1), ps.qv);
   if (len > a.max_seq) {
-    if (threadIdx.x == 0 && kvh == 0) atomicOr(a.errors, BARQ_KV_ERRBIT_ATTN_SHORT);
+    if (threadIdx.x == 0 && kvh == 0 && !half) atomicOr(a.errors, BARQ_KV_ERRBIT_ATTN_SHORT);
     len = a.max_seq;
   }
   len = max(len, 0);
   const int nch = (len + kBlock - 1) / kBlock;
+  const bool split = S == 2 && nch >= kPairSplitChunks;
+  if (S == 2 && half && !split) return;
   // The first waves take the remainder: waves 0 .. 3 are each SIMD's first, whose loads are
   // served first (the second wave on a SIMD gets its first chunk ~1.5 us later).
-  const int base = nch / W, extra = nch - base * W;
-  const int c0 = w * base + min(w, extra);
-  const int c1 = c0 + base + (w < extra ? 1 : 0);
+  const int parts = split ? 2 * W : W;
+  const int gw = split ? 2 * w + half : w;
+  const int base = nch / parts, extra = nch - base * parts;
+  const int c0 = gw * base + min(gw, extra);
+  const int c1 = c0 + base + (gw < extra ? 1 : 0);
   const int M = a.rows;
   const int rec = (int)record_floats(M, HD);
   attend_piece<HD, E, R, true, OutT, COLD, true>(a, lp[w], lq[w], b, kvh, len, kBlock * c0, min(len, kBlock * c1),
                                                  false, s_rec + w * rec, &ps);
   __syncthreads();
-  constexpr int kQuads = HD / 4;
-  for (int t = threadIdx.x; t < M * kQuads; t += W * kWave) {
-    const int row = t / kQuads;
-    const int quad = t - row * kQuads;
-    float mstar = -INFINITY;
+  // Thread t folds (row, quad) = (t / kQuads, t % kQuads) of the W records: unnormalised sums of
+  // 4 dims, the row's maximum and sum.
+  auto fold = [&](int row, int quad, float& mstar, float& l, f32x4& o) {
+    mstar = -INFINITY;
 #pragma unroll
     for (int k = 0; k < W; ++k) mstar = fmaxf(mstar, s_rec[k * rec + M * HD + row]);
     const float mu = mstar == -INFINITY ? 0.f : mstar;
-    float l = 0.f;
-    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+    l = 0.f;
+    o = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k = 0; k < W; ++k) {
       const float* rk = s_rec + k * rec;
@@ -985,8 +1010,73 @@ void attention_pair_kernel(const AttnArgs a) {
       l += wk * rk[M * HD + M + row];
       o += wk * *(const f32x4*)(rk + row * HD + 4 * quad);
     }
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    store_out4<OutT, E>(out_row(a, b, kvh, row) + (int64_t)(4 * quad) * sizeof(OutT), o * inv);
+  };
+  if (!split) {
+    for (int t = threadIdx.x; t < M * kQuads; t += W * kWave) {
+      const int row = t / kQuads;
+      const int quad = t - row * kQuads;
+      float mstar, l;
+      f32x4 o;
+      fold(row, quad, mstar, l, o);
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      store_out4<OutT, E>(out_row(a, b, kvh, row) + (int64_t)(4 * quad) * sizeof(OutT), o * inv);
+    }
+    return;
+  }
+  if constexpr (S == 2) {
+    static_assert(4 * R * kQuads <= W * kWave, "one (row, quad) of the record a thread");
+    const int t = threadIdx.x;
+    const bool item = t < M * kQuads;
+    const int row = t / kQuads;
+    const int quad = t - row * kQuads;
+    float mstar = -INFINITY, l = 0.f;
+    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Records 2p and 2p + 1 of the workspace hold the two halves of pair p.
+    float* mine = a.part + (int64_t)(2 * pair + half) * rec;
+    const float* theirs = a.part + (int64_t)(2 * pair + 1 - half) * rec;
+    if (item) {
+      fold(row, quad, mstar, l, o);
+      uint64_t* d = (uint64_t*)(mine + row * HD + 4 * quad);
+      __hip_atomic_store(d, __builtin_bit_cast(uint64_t, float2{o[0], o[1]}), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(d + 1, __builtin_bit_cast(uint64_t, float2{o[2], o[3]}), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      if (quad == 0) {
+        __hip_atomic_store((uint32_t*)(mine + M * HD + row), __builtin_bit_cast(uint32_t, mstar), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store((uint32_t*)(mine + M * HD + M + row), __builtin_bit_cast(uint32_t, l), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed
+    __syncthreads();
+    if (t == 0) {
+      int32_t* count = a.ctrl + BARQ_KV_CTRL_PAIR_WORD(pair);
+      const int before = __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (before == 1) __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_arrived = before;
+    }
+    __syncthreads();
+    if (s_arrived != 1 || !item) return;
+    const uint64_t* e = (const uint64_t*)(theirs + row * HD + 4 * quad);
+    const float2 o01 = __builtin_bit_cast(float2, __hip_atomic_load(e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const float2 o23 = __builtin_bit_cast(float2, __hip_atomic_load(e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const float mp = __builtin_bit_cast(
+        float, __hip_atomic_load((const uint32_t*)(theirs + M * HD + row), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const float lp2 = __builtin_bit_cast(
+        float, __hip_atomic_load((const uint32_t*)(theirs + M * HD + M + row), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    // Folded in the halves' order, whichever workgroup came second: the same bits every call.
+    const f32x4 op = f32x4{o01.x, o01.y, o23.x, o23.y};
+    const float m0 = half ? mp : mstar, m1 = half ? mstar : mp;
+    const float l0 = half ? lp2 : l, l1 = half ? l : lp2;
+    const f32x4 o0 = half ? op : o, o1 = half ? o : op;
+    const float mboth = fmaxf(m0, m1);
+    const float mu = mboth == -INFINITY ? 0.f : mboth;
+    const float w0 = __builtin_amdgcn_exp2f(m0 - mu), w1 = __builtin_amdgcn_exp2f(m1 - mu);
+    const float lsum = w0 * l0 + w1 * l1;
+    const f32x4 osum = w0 * o0 + w1 * o1;
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    store_out4<OutT, E>(out_row(a, b, kvh, row) + (int64_t)(4 * quad) * sizeof(OutT), osum * inv);
   }
 }
 
@@ -1069,24 +1159,31 @@ __global__ __launch_bounds__(NT) void attention_merge_kernel(const AttnArgs a) {
   }
 }
 
-// Resident waves of a kernel on the current device (cached per instantiation and device; host
-// threads may race on the cache, which only ever stores the one value a device gives).
-template <typename K>
-int resident_waves(K kernel) {
+// Resident workgroups of THREADS threads of a kernel on the current device, at most kMaxWaves
+// (cached per instantiation and device; host threads may race on the cache, which only ever
+// stores the one value a device gives); `fallback` when the runtime cannot tell.
+template <int THREADS, typename K>
+int resident_blocks(K kernel, int fallback) {
   constexpr int kMaxDevices = 64;
   static std::atomic<int> cached[kMaxDevices];  // 0 = not queried yet
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return kMaxWaves;
-  int waves = dev >= 0 && dev < kMaxDevices ? cached[dev].load(std::memory_order_relaxed) : 0;
-  if (waves == 0) {
+  if (hipGetDevice(&dev) != hipSuccess) return fallback;
+  int blocks = dev >= 0 && dev < kMaxDevices ? cached[dev].load(std::memory_order_relaxed) : 0;
+  if (blocks == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kWave, 0) != hipSuccess)
-      return kMaxWaves;
-    waves = std::min(std::max(cus * per_cu, 1), kMaxWaves);
-    if (dev >= 0 && dev < kMaxDevices) cached[dev].store(waves, std::memory_order_relaxed);
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, THREADS, 0) != hipSuccess)
+      return fallback;
+    blocks = std::min(std::max(cus * per_cu, 1), kMaxWaves);
+    if (dev >= 0 && dev < kMaxDevices) cached[dev].store(blocks, std::memory_order_relaxed);
   }
-  return waves;
+  return blocks;
+}
+
+// Resident waves of a one-wave-workgroup kernel.
+template <typename K>
+int resident_waves(K kernel) {
+  return resident_blocks<kWave>(kernel, kMaxWaves);
 }
 
 template <int HD, int E, int R, bool U, typename OutT, bool COLD>
@@ -1103,8 +1200,16 @@ hipError_t launch_typed(AttnArgs a, bool merge, hipStream_t stream) {
                                : COLD || pairs < 2 * kPairMinPairs ? kPairMaxChunksR1
                                                                    : kPairMaxChunksR1Wide;
     if (a.range_chunks == 0 && pairs > 0 && (a.max_seq + kBlock - 1) / kBlock <= max_chunks) {
-      hipLaunchKernelGGL((attention_pair_kernel<HD, E, R, OutT, COLD, kPairWaves>), dim3((unsigned)pairs),
-                         dim3(kPairWaves * kWave), 0, stream, a);
+      // Two workgroups a pair when every one of them is resident at once and rows may be long
+      // enough to split (the kernel decides per row); the pair counts in ctrl bound the pairs.
+      auto* split = attention_pair_kernel<HD, E, R, OutT, COLD, kPairWaves, 2>;
+      if ((a.max_seq + kBlock - 1) / kBlock >= kPairSplitChunks && pairs <= BARQ_KV_CTRL_PAIR_SLOTS &&
+          2 * pairs <= resident_blocks<kPairWaves * kWave>(split, 0)) {
+        hipLaunchKernelGGL(split, dim3((unsigned)(2 * pairs)), dim3(kPairWaves * kWave), 0, stream, a);
+      } else {
+        hipLaunchKernelGGL((attention_pair_kernel<HD, E, R, OutT, COLD, kPairWaves, 1>), dim3((unsigned)pairs),
+                           dim3(kPairWaves * kWave), 0, stream, a);
+      }
       return hipGetLastError();
     }
   }
@@ -1242,6 +1347,7 @@ int decode_attention(const barq_kv_pool* pool, const barq_kv_cold* cold, const v
   a.block_table = pool->block_table;
   a.seq_lens = pool->seq_lens;
   a.errors = pool->ctrl + BARQ_KV_CTRL_ERRORS;
+  a.ctrl = pool->ctrl;
   a.head_bytes = (int32_t)(pool->head_dim * 2);
   a.row_bytes = (int32_t)(pool->kv_heads * a.head_bytes);
   a.page_bytes = pool->page_size * (int64_t)a.row_bytes;

@@ -67,6 +67,11 @@ extern "C" {
 #define BARQ_KV_CTRL_SUBCOUNTER_STRIDE 64 /* ... one per 256 bytes ... */
 #define BARQ_KV_CTRL_SUBCOUNTERS 16       /* ... this many */
 #define BARQ_KV_CTRL_WORDS (BARQ_KV_CTRL_SUBCOUNTER0 + BARQ_KV_CTRL_SUBCOUNTERS * BARQ_KV_CTRL_SUBCOUNTER_STRIDE)
+/* Arrival counts of decode attention's split (row, kv head) pairs, one word per pair q <
+   BARQ_KV_CTRL_PAIR_SLOTS, in the second 128 bytes of each sub-counter's 256. */
+#define BARQ_KV_CTRL_PAIR_SLOTS (BARQ_KV_CTRL_SUBCOUNTERS * 32)
+#define BARQ_KV_CTRL_PAIR_WORD(q) \
+  (BARQ_KV_CTRL_SUBCOUNTER0 + ((q) / 32) * BARQ_KV_CTRL_SUBCOUNTER_STRIDE + 32 + (q) % 32)
 
 /* Sticky error bits in ctrl[BARQ_KV_CTRL_ERRORS]. */
 #define BARQ_KV_ERRBIT_POOL_EXHAUSTED 1 /* a new block found no free page; its tokens were dropped */

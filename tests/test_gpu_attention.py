@@ -161,6 +161,40 @@ def test_long_pairs_one_launch(rows, Hkv, cap, dtype, D, page):
     assert pool.errors() == 0
 
 
+def pair_words(pool, pairs):
+    """The split pairs' arrival counts (BARQ_KV_CTRL_PAIR_WORD of include/barq_kv.h)."""
+    idx = [64 + (q // 32) * 64 + 32 + q % 32 for q in range(pairs)]
+    return pool.ctrl.cpu().numpy()[idx]
+
+
+@pytest.mark.parametrize("dtype,D,G", [(torch.bfloat16, 128, 4), (torch.float16, 128, 8), (torch.bfloat16, 64, 2)])
+def test_split_pairs_same_bits_every_call(dtype, D, G):
+    """128 (row, kv head) pairs on 256 CUs: two workgroups a pair, each folding its waves in LDS;
+    the second to arrive folds both halves' records into the output.  Rows from 24 chunks (369
+    positions) are split, shorter ones taken by one workgroup, in the same launch (lengths on
+    both sides of that bound and of chunk boundaries).  Against the float64 reference; three
+    calls in a row give the same bits (the fold does not depend on which half arrives second)
+    and leave every pair's arrival count at 0; the flat schedule agrees."""
+    rng = np.random.default_rng(D + G)
+    lens = [704, 703, 369, 368, 385, 384, 383, 0, 1, 17] + rng.integers(0, 705, size=6).tolist()
+    pool, kd, vd, lens = make_rows(16, 8, 16, lens, dtype, seed=D + G, order_seed=D + G + 1, D=D, cap=704)
+    q = hf_layout(16, G * 8, 1, D, dtype, torch.Generator().manual_seed(G)).cuda()
+    outs = []
+    ws = None
+    for _ in range(3):
+        out, ws = pool.attend(q, out_f32=True, workspace=ws)
+        torch.cuda.synchronize()
+        outs.append(out.double().cpu().numpy())
+        assert not pair_words(pool, 128).any()
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
+    want = decode_attention_reference(q.double().cpu().numpy(), kd, vd, lens, D ** -0.5)
+    ok, ratio = within_tolerance(outs[0], want, **F32_TOL)
+    assert ok, f"{ratio:.3g} x tolerance"
+    check(pool, kd, vd, lens, G, 1, dtype, seed=5, out_f32=False)
+    check(pool, kd, vd, lens, G, 1, dtype, seed=6, split_tokens=64)  # the flat schedule
+    assert pool.errors() == 0
+
+
 @pytest.mark.parametrize("B,Hkv,D", [(1, 8, 128), (3, 8, 128), (2, 2, 64)])
 def test_few_pairs_one_launch(B, Hkv, D):
     """Fewer than 128 (row, kv head) pairs -- batch-1 decode -- take the one-launch pair kernel up
@@ -169,7 +203,7 @@ def test_few_pairs_one_launch(B, Hkv, D):
     rng = np.random.default_rng(B * 10 + D)
     lens = sorted([704, 17, 1][:B] + rng.integers(1, 705, size=max(B - 3, 0)).tolist(), reverse=True)
     pool, kd, vd, lens = make_rows(B, Hkv, 16, lens, torch.bfloat16, seed=B + D, order_seed=B + D + 1, D=D,
-                                   cap=720)
+                                   cap=704)
     ws = None
     for i, (G, T) in enumerate([(4, 1), (8, 1), (1, 1), (2, 2)]):
         ws = check(pool, kd, vd, lens, G, T, torch.bfloat16, seed=800 + i, ws=ws)
