@@ -32,6 +32,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <type_traits>
 
 #include "barq_kv.h"
 #include "barq_kv_fp8.h"
@@ -66,10 +67,14 @@ constexpr int64_t kPairMaxChunksR1 = 64;
 constexpr int64_t kPairMaxChunksR1Wide = 128;
 static_assert(kPairMaxChunks <= kTableEntries && kPairMaxChunksR1Wide <= kTableEntries,
               "a pair's blocks fit one table window");
-// When two workgroups a pair fit on the GPU at once (C2: 128 pairs, 256 CUs), a pair of at least
-// kPairSplitChunks chunks is cut over both (their exchange costs ~1.3 us; shorter rows lose more
-// than they gain).
-constexpr int kPairSplitChunks = 24;
+// When several workgroups a pair fit on the GPU at once (C2: 128 pairs, 256 CUs: two), a pair is
+// cut over as many of them as give each at least kPairPartChunks chunks, at most kMaxSplit (the
+// exchange costs ~1.3 us; shorter parts lose more than they gain).  With three or more a pair,
+// rows of up to kSplitChunksPerPart chunks a workgroup take the pair kernel.
+constexpr int kPairPartChunks = 12;
+constexpr int kMaxSplit = 8;
+constexpr int64_t kSplitChunksPerPart = 24;
+constexpr int kSplitAny = 0;  // attention_pair_kernel's S: the grid's count, 3 .. kMaxSplit
 
 enum : int { kBF16 = 0, kF16 = 1 };
 
@@ -941,21 +946,22 @@ void attention_flat_kernel(const AttnArgs a) {
 // online-softmax fold as the merge kernel): one launch, no global workspace, each pair's bytes
 // read once.  A wave with no chunks leaves a neutral record (maximum -inf, sum 0).
 //
-// S = 2 (launches whose 2 x pairs workgroups are resident at once): workgroups p and p + pairs
-// share pair p; a row of at least kPairSplitChunks chunks is cut over their 2W waves (ranges
-// dealt alternately), else the second workgroup leaves at once and the first takes the row alone.
-// A split pair's workgroups each fold their waves in LDS, publish the folded record in the
-// workspace and arrive on the pair's count in ctrl; the second to arrive folds both records into
-// the output and sets the count back to 0.  No workgroup waits for another, so the grid needs no
+// S = 2, or kSplitAny for the grid's count (launches whose S x pairs workgroups are resident at
+// once): workgroups p, p + pairs, ... share pair p; a row is cut over the first k of them, k the
+// most that give each at least kPairPartChunks chunks (ranges dealt to their k x W waves in turn),
+// and the others leave at once (k = 1: the first takes the row alone).  A split pair's workgroups
+// each fold their waves in LDS, publish the folded record in the workspace and arrive on the
+// pair's count in ctrl; the last to arrive folds the k records into the output and sets the count
+// back to 0.  No workgroup waits for another, so the grid needs no
 // co-residency to finish.  The records are written with agent-scope atomic stores, which write
 // through to the device's coherence point (`global_store ... sc1`), every one of them complete
 // (s_waitcnt vmcnt(0), then the barrier) before the arrival; the second arrival reads them with
-// agent-scope atomic loads (`sc1`) issued after its count returned.  An agent-scope release fence
+// agent-scope atomic loads (`sc1`) issued after its count returned, every record's loads at once.  An agent-scope release fence
 // would write back the whole L2 (~1.7 us); this exchange costs ~1.3 us in all.
 template <int HD, int E, int R, typename OutT, bool COLD, int W, int S>
 __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(R <= 2 ? 2 : 1, R <= 2 ? 2 : 1)))
 void attention_pair_kernel(const AttnArgs a) {
-  static_assert(S == 1 || S == 2, "one or two workgroups a pair");
+  static_assert(S == 1 || S == 2 || S == kSplitAny, "one, two or the grid's count of workgroups a pair");
   constexpr int kRecMax = (int)record_floats(4 * R, HD);
   constexpr int kQuads = HD / 4;
   __shared__ float lp[W][kBlock][kMaxRows];
@@ -963,8 +969,13 @@ void attention_pair_kernel(const AttnArgs a) {
   __shared__ float s_rec[W * kRecMax];
   __shared__ int s_arrived;
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
-  const int pairs = (int)gridDim.x / S;
-  const int half = S == 2 && (int)blockIdx.x >= pairs;
+  // (The first workgroups of a launch compute this before their first load: a compare where it
+  // can be one.)
+  const int pairs = S == kSplitAny ? a.batch * a.kv_heads : (int)gridDim.x / S;
+  const int nsplit = S == kSplitAny ? (int)gridDim.x / pairs : S;
+  const int half = S == 1   ? 0
+                   : S == 2 ? (int)((int)blockIdx.x >= pairs)
+                            : (int)blockIdx.x / pairs;  // this workgroup's part of the pair
   const int pair = (int)blockIdx.x - half * pairs;
   const int b = pair / a.kv_heads;
   const int kvh = pair - b * a.kv_heads;
@@ -980,12 +991,13 @@ void attention_pair_kernel(const AttnArgs a) {
   }
   len = max(len, 0);
   const int nch = (len + kBlock - 1) / kBlock;
-  const bool split = S == 2 && nch >= kPairSplitChunks;
-  if (S == 2 && half && !split) return;
+  const int kparts = S == 1 ? 1 : min(nsplit, max(1, nch / kPairPartChunks));
+  const bool split = kparts > 1;
+  if (half >= kparts) return;
   // The first waves take the remainder: waves 0 .. 3 are each SIMD's first, whose loads are
   // served first (the second wave on a SIMD gets its first chunk ~1.5 us later).
-  const int parts = split ? 2 * W : W;
-  const int gw = split ? 2 * w + half : w;
+  const int parts = kparts * W;
+  const int gw = w * kparts + half;
   const int base = nch / parts, extra = nch - base * parts;
   const int c0 = gw * base + min(gw, extra);
   const int c1 = c0 + base + (gw < extra ? 1 : 0);
@@ -1023,7 +1035,7 @@ void attention_pair_kernel(const AttnArgs a) {
     }
     return;
   }
-  if constexpr (S == 2) {
+  if constexpr (S != 1) {
     static_assert(4 * R * kQuads <= W * kWave, "one (row, quad) of the record a thread");
     const int t = threadIdx.x;
     const bool item = t < M * kQuads;
@@ -1031,9 +1043,9 @@ void attention_pair_kernel(const AttnArgs a) {
     const int quad = t - row * kQuads;
     float mstar = -INFINITY, l = 0.f;
     f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
-    // Records 2p and 2p + 1 of the workspace hold the two halves of pair p.
-    float* mine = a.part + (int64_t)(2 * pair + half) * rec;
-    const float* theirs = a.part + (int64_t)(2 * pair + 1 - half) * rec;
+    // Records nsplit * p + j of the workspace hold the parts of pair p.
+    const float* recs = a.part + (int64_t)nsplit * pair * rec;
+    float* mine = a.part + ((int64_t)nsplit * pair + half) * rec;
     if (item) {
       fold(row, quad, mstar, l, o);
       uint64_t* d = (uint64_t*)(mine + row * HD + 4 * quad);
@@ -1053,28 +1065,62 @@ void attention_pair_kernel(const AttnArgs a) {
     if (t == 0) {
       int32_t* count = a.ctrl + BARQ_KV_CTRL_PAIR_WORD(pair);
       const int before = __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (before == 1) __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (before == kparts - 1) __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       s_arrived = before;
     }
     __syncthreads();
-    if (s_arrived != 1 || !item) return;
-    const uint64_t* e = (const uint64_t*)(theirs + row * HD + 4 * quad);
-    const float2 o01 = __builtin_bit_cast(float2, __hip_atomic_load(e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    const float2 o23 = __builtin_bit_cast(float2, __hip_atomic_load(e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    const float mp = __builtin_bit_cast(
-        float, __hip_atomic_load((const uint32_t*)(theirs + M * HD + row), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    const float lp2 = __builtin_bit_cast(
-        float, __hip_atomic_load((const uint32_t*)(theirs + M * HD + M + row), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    // Folded in the halves' order, whichever workgroup came second: the same bits every call.
-    const f32x4 op = f32x4{o01.x, o01.y, o23.x, o23.y};
-    const float m0 = half ? mp : mstar, m1 = half ? mstar : mp;
-    const float l0 = half ? lp2 : l, l1 = half ? l : lp2;
-    const f32x4 o0 = half ? op : o, o1 = half ? o : op;
-    const float mboth = fmaxf(m0, m1);
-    const float mu = mboth == -INFINITY ? 0.f : mboth;
-    const float w0 = __builtin_amdgcn_exp2f(m0 - mu), w1 = __builtin_amdgcn_exp2f(m1 - mu);
-    const float lsum = w0 * l0 + w1 * l1;
-    const f32x4 osum = w0 * o0 + w1 * o1;
+    if (s_arrived != kparts - 1 || !item) return;
+    // The pair's records, folded in the parts' order whichever workgroup came last (the same bits
+    // every call): NS slots' loads issued at once, slots past the pair's parts re-reading its last.
+    auto gather_fold = [&](auto ns, float& lsum, f32x4& osum) {
+      constexpr int NS = decltype(ns)::value;
+      float mm[NS], ll[NS];
+      f32x4 oo[NS];
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        if (NS == 2 && j == half) continue;  // two parts: only the other one's record
+        const float* rj = recs + (int64_t)min(j, kparts - 1) * rec;
+        const uint64_t* e = (const uint64_t*)(rj + row * HD + 4 * quad);
+        const float2 o01 = __builtin_bit_cast(float2, __hip_atomic_load(e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        const float2 o23 =
+            __builtin_bit_cast(float2, __hip_atomic_load(e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        oo[j] = f32x4{o01.x, o01.y, o23.x, o23.y};
+        mm[j] = __builtin_bit_cast(
+            float, __hip_atomic_load((const uint32_t*)(rj + M * HD + row), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        ll[j] = __builtin_bit_cast(float, __hip_atomic_load((const uint32_t*)(rj + M * HD + M + row),
+                                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      }
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        if (j == half) {
+          mm[j] = mstar;
+          ll[j] = l;
+          oo[j] = o;
+        } else if (j >= kparts) {
+          mm[j] = -INFINITY;
+          ll[j] = 0.f;
+          oo[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+      float mboth = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < NS; ++j) mboth = fmaxf(mboth, mm[j]);
+      const float mu = mboth == -INFINITY ? 0.f : mboth;
+      lsum = 0.f;
+      osum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        const float wj = __builtin_amdgcn_exp2f(mm[j] - mu);
+        lsum += wj * ll[j];
+        osum += wj * oo[j];
+      }
+    };
+    float lsum;
+    f32x4 osum;
+    if (S == 2 || kparts == 2)
+      gather_fold(std::integral_constant<int, 2>{}, lsum, osum);
+    else
+      gather_fold(std::integral_constant<int, (S == 2 ? 2 : kMaxSplit)>{}, lsum, osum);
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
     store_out4<OutT, E>(out_row(a, b, kvh, row) + (int64_t)(4 * quad) * sizeof(OutT), osum * inv);
   }
@@ -1196,16 +1242,24 @@ hipError_t launch_typed(AttnArgs a, bool merge, hipStream_t stream) {
     // still beats the flat pair of launches and its merge (C2 shape at batch 1: 650 positions
     // 16.3 -> 12.6 us, 128 positions 12.8 -> 6.3 us; at 2048 the flat schedule wins, 14.8 against
     // 28.4).
-    const int64_t max_chunks = R > 1 || pairs < kPairMinPairs        ? kPairMaxChunks
-                               : COLD || pairs < 2 * kPairMinPairs ? kPairMaxChunksR1
-                                                                   : kPairMaxChunksR1Wide;
-    if (a.range_chunks == 0 && pairs > 0 && (a.max_seq + kBlock - 1) / kBlock <= max_chunks) {
-      // Two workgroups a pair when every one of them is resident at once and rows may be long
-      // enough to split (the kernel decides per row); the pair counts in ctrl bound the pairs.
-      auto* split = attention_pair_kernel<HD, E, R, OutT, COLD, kPairWaves, 2>;
-      if ((a.max_seq + kBlock - 1) / kBlock >= kPairSplitChunks && pairs <= BARQ_KV_CTRL_PAIR_SLOTS &&
-          2 * pairs <= resident_blocks<kPairWaves * kWave>(split, 0)) {
-        hipLaunchKernelGGL(split, dim3((unsigned)(2 * pairs)), dim3(kPairWaves * kWave), 0, stream, a);
+    // Workgroups a pair: as many as are resident at once with the others' (the kernel decides per
+    // row how many it uses), at most kMaxSplit; the pair counts in ctrl bound the pairs.
+    auto* split_any = attention_pair_kernel<HD, E, R, OutT, COLD, kPairWaves, kSplitAny>;
+    const int64_t chunks = (a.max_seq + kBlock - 1) / kBlock;
+    const int64_t nsplit =
+        pairs > 0 && pairs <= BARQ_KV_CTRL_PAIR_SLOTS && chunks >= 2 * kPairPartChunks
+            ? std::min<int64_t>(kMaxSplit, resident_blocks<kPairWaves * kWave>(split_any, 0) / pairs)
+            : 1;
+    int64_t max_chunks = R > 1 || pairs < kPairMinPairs        ? kPairMaxChunks
+                         : COLD || pairs < 2 * kPairMinPairs ? kPairMaxChunksR1
+                                                             : kPairMaxChunksR1Wide;
+    if (nsplit > 2) max_chunks = std::min<int64_t>(kTableEntries, std::max(max_chunks, nsplit * kSplitChunksPerPart));
+    if (a.range_chunks == 0 && pairs > 0 && chunks <= max_chunks) {
+      if (nsplit > 2) {
+        hipLaunchKernelGGL(split_any, dim3((unsigned)(nsplit * pairs)), dim3(kPairWaves * kWave), 0, stream, a);
+      } else if (nsplit == 2) {
+        hipLaunchKernelGGL((attention_pair_kernel<HD, E, R, OutT, COLD, kPairWaves, 2>), dim3((unsigned)(2 * pairs)),
+                           dim3(kPairWaves * kWave), 0, stream, a);
       } else {
         hipLaunchKernelGGL((attention_pair_kernel<HD, E, R, OutT, COLD, kPairWaves, 1>), dim3((unsigned)pairs),
                            dim3(kPairWaves * kWave), 0, stream, a);

@@ -197,9 +197,10 @@ def test_split_pairs_same_bits_every_call(dtype, D, G):
 
 @pytest.mark.parametrize("B,Hkv,D", [(1, 8, 128), (3, 8, 128), (2, 2, 64)])
 def test_few_pairs_one_launch(B, Hkv, D):
-    """Fewer than 128 (row, kv head) pairs -- batch-1 decode -- take the one-launch pair kernel up
-    to 44 chunks a pair (704 positions): rows on and next to chunk boundaries, G = 4 / 8 / 1, two
-    query tokens, both output types; 705 positions take the flat schedule, which agrees."""
+    """Fewer than 128 (row, kv head) pairs -- batch-1 decode -- take the one-launch pair kernel
+    with up to 8 workgroups a pair (each at least 12 chunks of the row): rows of up to 704
+    positions on and next to chunk boundaries, G = 4 / 8 / 1, two query tokens, both output
+    types; 3073 positions (past 8 x 24 chunks) take the flat schedule, which agrees."""
     rng = np.random.default_rng(B * 10 + D)
     lens = sorted([704, 17, 1][:B] + rng.integers(1, 705, size=max(B - 3, 0)).tolist(), reverse=True)
     pool, kd, vd, lens = make_rows(B, Hkv, 16, lens, torch.bfloat16, seed=B + D, order_seed=B + D + 1, D=D,
@@ -209,8 +210,34 @@ def test_few_pairs_one_launch(B, Hkv, D):
         ws = check(pool, kd, vd, lens, G, T, torch.bfloat16, seed=800 + i, ws=ws)
     check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=9, out_f32=False)
     assert pool.errors() == 0
-    pool, kd, vd, lens = make_rows(1, Hkv, 16, [705], torch.bfloat16, seed=B + D + 2, order_seed=B + D + 3, D=D)
+    pool, kd, vd, lens = make_rows(1, Hkv, 16, [3073], torch.bfloat16, seed=B + D + 2, order_seed=B + D + 3, D=D)
     check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=11)
+    assert pool.errors() == 0
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 64)])
+def test_small_batch_pairs_over_many_workgroups(dtype, D):
+    """8 (row, kv head) pairs on 256 CUs: up to 8 workgroups a pair (the grid's count), a row cut
+    over as many as give each 12 chunks -- 3072 positions over 8, 1537 over 8, 385 over 2, 191
+    alone -- and the last to arrive folding the parts' records in their order.  Rows up to 3072
+    positions take this one launch (the flat schedule before).  G = 4 / 8, two query tokens,
+    against the float64 reference; three calls give the same bits and leave every arrival count
+    at 0; the flat schedule agrees."""
+    pool, kd, vd, lens = make_rows(4, 2, 16, [3072, 1537, 385, 191], dtype, seed=D, order_seed=D + 1, D=D)
+    for i, (G, T) in enumerate([(4, 1), (8, 1), (2, 2)]):
+        q = hf_layout(4, G * 2, T, D, dtype, torch.Generator().manual_seed(30 + i)).cuda()
+        outs = []
+        for _ in range(3):
+            out, _ = pool.attend(q, out_f32=True)
+            torch.cuda.synchronize()
+            outs.append(out.double().cpu().numpy())
+            assert not pair_words(pool, 8).any()
+        assert all(np.array_equal(outs[0], o) for o in outs[1:])
+        want = decode_attention_reference(q.double().cpu().numpy(), kd, vd, lens, D ** -0.5)
+        ok, ratio = within_tolerance(outs[0], want, **F32_TOL)
+        assert ok, f"G={G} T={T}: {ratio:.3g} x tolerance"
+    check(pool, kd, vd, lens, 4, 1, dtype, seed=7, out_f32=False)
+    check(pool, kd, vd, lens, 4, 1, dtype, seed=8, split_tokens=256)  # the flat schedule
     assert pool.errors() == 0
 
 
