@@ -693,10 +693,17 @@ def quant_leg(cfg, wl, steps, dev, bf16_ms_per_step, window=128, reps=10, probe=
         torch.cuda.synchronize()
         lens_e = pools[0].lens[:B].astype(np.int64)
         gather_bytes = cold_read_bytes(lens_e, pools[0].cold_blocks[:B].astype(np.int64)) + B * seq * tb
+        attn_info = {}
+        if D == 128 and P % 16 == 0:  # one decode attention per layer over the quantised pages
+            def attn_bytes(pool, lens_b):
+                return cold_read_bytes(lens_b, pool.cold_blocks[:B].astype(np.int64))
+
+            attn_info = attention_leg(cfg, pools, B, dev, reps=1, kv_bytes=attn_bytes, probe=True)
+            print("pmc-probe: fp8 attention done", file=sys.stderr, flush=True)
         print(json.dumps({"pmc_probe": "quant", "config": cfg["name"], "steps": steps, "launches": steps * L,
                           "update_algorithmic_bytes_per_launch": float(np.mean(update_bytes)),
                           "gather_calls": L, "gather_algorithmic_bytes_per_launch": gather_bytes,
-                          "context": f"{int(lens0.min()) + 1}..{int(lens_e.max())}"}), flush=True)
+                          "context": f"{int(lens0.min()) + 1}..{int(lens_e.max())}", **attn_info}), flush=True)
         return None
     prefill()
     # every graph the steps replay (each extent bucket, with and without the compress launch)
