@@ -1856,7 +1856,9 @@ int run_stream(const barq_kv_pool* pool, const void* ks, const void* vs, int64_t
   // that holds the one-page tiles' chunks; 0 if none does.
   // (C2, context 513-576: 15.2 -> 14.1 us per launch.)  Two-page tiles stay page-aligned: cut
   // the same way (up to three blocks a tile) they ran 1-2 % slower; six balanced one-page tiles
-  // per CU instead of two-page ones, 20 % slower.
+  // per CU instead of two-page ones, 20 % slower; balanced chunks of up to two pages, three or
+  // four per CU, in place of the one-page tiles (C2 at extents 576 / 640): 14.84 / 16.02 ->
+  // 15.28 / 16.22 and 17.52 / 17.57 us.
   const auto balanced_chunks = [&](int64_t aligned, int64_t per_cu) -> int64_t {
     for (int64_t k = 1; k <= per_cu; ++k)
       if ((k * ncu) % (2 * batch) == 0 && k * ncu / (2 * batch) >= aligned) return k * ncu / (2 * batch);
