@@ -416,3 +416,59 @@ def test_page_pool_attend_and_graph_replays(hip):
             ok, ratio = within_tolerance(outs[li].double().cpu().numpy(), want, **F32_TOL)
             assert ok, f"replay {s} layer {li}: {ratio:.3g} x tolerance"
     assert all(p.errors() == 0 for p in pools)
+
+
+@pytest.mark.parametrize("B,Hkv,prefill", [(16, 8, 400), (2, 4, 700)])
+def test_split_pairs_in_graph_replays(hip, B, Hkv, prefill):
+    """Split pairs under graph capture: append + attend over 2 layers captured once (128 pairs:
+    two workgroups a pair; 8 pairs: up to 8), replayed while the rows grow, with eager work
+    between replays; every replay against the reference, and every pair's arrival count back at
+    0 after it (the last arrival resets it inside the launch: nothing in the graph clears it)."""
+    from barqtrain_amd.paged import PagePool
+
+    L, G, D, P, steps = 2, 4, 128, 16, 5
+    cap = prefill + steps
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator().manual_seed(B + prefill)
+    pools = [PagePool(max_batch=B, max_blocks=-(-cap // P), page_size=P, kv_heads=Hkv, head_dim=D,
+                      dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    dense_k = np.zeros((L, B, Hkv, cap, D))
+    dense_v = np.zeros((L, B, Hkv, cap, D))
+    for li, pool in enumerate(pools):
+        k = hf_layout(B, Hkv, prefill, D, torch.bfloat16, gen)
+        v = hf_layout(B, Hkv, prefill, D, torch.bfloat16, gen)
+        pool.append(k.to(dev), v.to(dev))
+        dense_k[li, :, :, :prefill] = k.double().numpy()
+        dense_v[li, :, :, :prefill] = v.double().numpy()
+    kin = torch.zeros((L, B, Hkv, 1, D), dtype=torch.bfloat16, device=dev)
+    vin = torch.zeros_like(kin)
+    qin = torch.zeros((L, B, G * Hkv, 1, D), dtype=torch.bfloat16, device=dev)
+    outs = [torch.zeros((B, 1, G * Hkv, D), dtype=torch.float32, device=dev).transpose(1, 2) for _ in range(L)]
+    for pool in pools:
+        pool.attention_workspace(hip.attention_workspace_bytes(pool.tensors, B, G * Hkv, 1, cap, 0))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for li, pool in enumerate(pools):
+            hip.pool_append_(pool.tensors, kin[li], vin[li])
+            hip.pool_decode_attention(pool.tensors, qin[li], outs[li], D ** -0.5, cap, 0,
+                                      pool.attention_workspace(0))
+    for s in range(steps):
+        ks = [hf_layout(B, Hkv, 1, D, torch.bfloat16, gen) for _ in range(L)]
+        vs = [hf_layout(B, Hkv, 1, D, torch.bfloat16, gen) for _ in range(L)]
+        qs = [hf_layout(B, G * Hkv, 1, D, torch.bfloat16, gen) for _ in range(L)]
+        for li in range(L):
+            kin[li].copy_(ks[li].to(dev))
+            vin[li].copy_(vs[li].to(dev))
+            qin[li].copy_(qs[li].to(dev))
+            dense_k[li, :, :, prefill + s] = ks[li][:, :, 0].double().numpy()
+            dense_v[li, :, :, prefill + s] = vs[li][:, :, 0].double().numpy()
+        _ = torch.randn(1 << 18, device=dev).sum().item()  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        n = prefill + s + 1
+        for li in range(L):
+            want = decode_attention_reference(qs[li].double().numpy(), dense_k[li], dense_v[li], [n] * B, D ** -0.5)
+            ok, ratio = within_tolerance(outs[li].double().cpu().numpy(), want, **F32_TOL)
+            assert ok, f"replay {s} layer {li}: {ratio:.3g} x tolerance"
+            assert not pair_words(pools[li], B * Hkv).any()
+    assert all(p.errors() == 0 for p in pools)
