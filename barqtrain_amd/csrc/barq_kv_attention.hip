@@ -942,22 +942,23 @@ void attention_flat_kernel(const AttnArgs a) {
 
 // Many short pairs (C2: 16 rows x 8 kv heads, ~650 positions): one workgroup of W waves per
 // (row, kv head).  Wave w streams nch / W chunks of its pair (one more for the first nch % W
-// waves), leaves its partial record in LDS, and the workgroup folds the W records into the output (same base-2
-// online-softmax fold as the merge kernel): one launch, no global workspace, each pair's bytes
-// read once.  A wave with no chunks leaves a neutral record (maximum -inf, sum 0).
+// waves), leaves its partial record in LDS, and the workgroup folds the W records into the
+// output (the merge kernel's base-2 online-softmax fold): one launch, each pair's bytes read
+// once.  A wave with no chunks leaves a neutral record (maximum -inf, sum 0).
 //
 // S = 2, or kSplitAny for the grid's count (launches whose S x pairs workgroups are resident at
-// once): workgroups p, p + pairs, ... share pair p; a row is cut over the first k of them, k the
-// most that give each at least kPairPartChunks chunks (ranges dealt to their k x W waves in turn),
-// and the others leave at once (k = 1: the first takes the row alone).  A split pair's workgroups
-// each fold their waves in LDS, publish the folded record in the workspace and arrive on the
-// pair's count in ctrl; the last to arrive folds the k records into the output and sets the count
-// back to 0.  No workgroup waits for another, so the grid needs no
-// co-residency to finish.  The records are written with agent-scope atomic stores, which write
-// through to the device's coherence point (`global_store ... sc1`), every one of them complete
-// (s_waitcnt vmcnt(0), then the barrier) before the arrival; the second arrival reads them with
-// agent-scope atomic loads (`sc1`) issued after its count returned, every record's loads at once.  An agent-scope release fence
-// would write back the whole L2 (~1.7 us); this exchange costs ~1.3 us in all.
+// once): workgroups p, p + pairs, ... share pair p.  A row is cut over the first k of them, k the
+// most that give each at least kPairPartChunks chunks (ranges dealt to their k x W waves in
+// turn), and the others leave at once (k = 1: the first takes the row alone).  A split pair's
+// workgroups each fold their waves in LDS, publish the folded record in the workspace and
+// arrive on the pair's count in ctrl; the last to arrive folds the k records into the output and
+// sets the count back to 0.  No workgroup waits for another, so the grid needs no co-residency
+// to finish.  The records are written with agent-scope atomic stores, which write through to
+// the device's coherence point (`global_store ... sc1`), every one of them complete
+// (s_waitcnt vmcnt(0), then the barrier) before the arrival; the last arrival reads them with
+// agent-scope atomic loads (`sc1`) issued after its count returned, every record's loads at
+// once.  An agent-scope release fence would write back the whole L2 (~1.7 us); this exchange
+// costs ~1.3 us in all.
 template <int HD, int E, int R, typename OutT, bool COLD, int W, int S>
 __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(R <= 2 ? 2 : 1, R <= 2 ? 2 : 1)))
 void attention_pair_kernel(const AttnArgs a) {
