@@ -68,10 +68,14 @@ constexpr int64_t kPairMaxChunksR1Wide = 128;
 static_assert(kPairMaxChunks <= kTableEntries && kPairMaxChunksR1Wide <= kTableEntries,
               "a pair's blocks fit one table window");
 // When several workgroups a pair fit on the GPU at once (C2: 128 pairs, 256 CUs: two), a pair is
-// cut over as many of them as give each at least kPairPartChunks chunks, at most kMaxSplit (the
-// exchange costs ~1.3 us; shorter parts lose more than they gain).  With three or more a pair,
-// rows of up to kSplitChunksPerPart chunks a workgroup take the pair kernel.
-constexpr int kPairPartChunks = 12;
+// cut over as many of them as give each at least pair_part_chunks<R>() chunks, at most kMaxSplit
+// (the exchange costs ~1.3 us; shorter parts lose more than they gain: at the C2 shape two
+// workgroups break even at ~18-22 chunks with 4 query rows, ~27 with 8).  With three or more a
+// pair, rows of up to kSplitChunksPerPart chunks a workgroup take the pair kernel.
+template <int R>
+__host__ __device__ constexpr int pair_part_chunks() {
+  return R == 1 ? 11 : 14;
+}
 constexpr int kMaxSplit = 8;
 constexpr int64_t kSplitChunksPerPart = 24;
 constexpr int kSplitAny = 0;  // attention_pair_kernel's S: the grid's count, 3 .. kMaxSplit
@@ -948,7 +952,7 @@ void attention_flat_kernel(const AttnArgs a) {
 //
 // S = 2, or kSplitAny for the grid's count (launches whose S x pairs workgroups are resident at
 // once): workgroups p, p + pairs, ... share pair p.  A row is cut over the first k of them, k the
-// most that give each at least kPairPartChunks chunks (ranges dealt to their k x W waves in
+// most that give each at least pair_part_chunks<R>() chunks (ranges dealt to their k x W waves in
 // turn), and the others leave at once (k = 1: the first takes the row alone).  A split pair's
 // workgroups each fold their waves in LDS, publish the folded record in the workspace and
 // arrive on the pair's count in ctrl; the last to arrive folds the k records into the output and
@@ -992,7 +996,7 @@ void attention_pair_kernel(const AttnArgs a) {
   }
   len = max(len, 0);
   const int nch = (len + kBlock - 1) / kBlock;
-  const int kparts = S == 1 ? 1 : min(nsplit, max(1, nch / kPairPartChunks));
+  const int kparts = S == 1 ? 1 : min(nsplit, max(1, nch / pair_part_chunks<R>()));
   const bool split = kparts > 1;
   if (half >= kparts) return;
   // The first waves take the remainder: waves 0 .. 3 are each SIMD's first, whose loads are
@@ -1248,7 +1252,7 @@ hipError_t launch_typed(AttnArgs a, bool merge, hipStream_t stream) {
     auto* split_any = attention_pair_kernel<HD, E, R, OutT, COLD, kPairWaves, kSplitAny>;
     const int64_t chunks = (a.max_seq + kBlock - 1) / kBlock;
     const int64_t nsplit =
-        pairs > 0 && pairs <= BARQ_KV_CTRL_PAIR_SLOTS && chunks >= 2 * kPairPartChunks
+        pairs > 0 && pairs <= BARQ_KV_CTRL_PAIR_SLOTS && chunks >= 2 * pair_part_chunks<R>()
             ? std::min<int64_t>(kMaxSplit, resident_blocks<kPairWaves * kWave>(split_any, 0) / pairs)
             : 1;
     int64_t max_chunks = R > 1 || pairs < kPairMinPairs        ? kPairMaxChunks

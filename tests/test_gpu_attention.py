@@ -170,13 +170,14 @@ def pair_words(pool, pairs):
 @pytest.mark.parametrize("dtype,D,G", [(torch.bfloat16, 128, 4), (torch.float16, 128, 8), (torch.bfloat16, 64, 2)])
 def test_split_pairs_same_bits_every_call(dtype, D, G):
     """128 (row, kv head) pairs on 256 CUs: two workgroups a pair, each folding its waves in LDS;
-    the second to arrive folds both halves' records into the output.  Rows from 24 chunks (369
-    positions) are split, shorter ones taken by one workgroup, in the same launch (lengths on
-    both sides of that bound and of chunk boundaries).  Against the float64 reference; three
+    the second to arrive folds both halves' records into the output.  Rows from 22 chunks (337
+    positions) are split with up to 4 query rows, from 28 (433) with 8, shorter ones taken by
+    one workgroup, in the same launch (lengths on both sides of those bounds and of chunk
+    boundaries).  Against the float64 reference; three
     calls in a row give the same bits (the fold does not depend on which half arrives second)
     and leave every pair's arrival count at 0; the flat schedule agrees."""
     rng = np.random.default_rng(D + G)
-    lens = [704, 703, 369, 368, 385, 384, 383, 0, 1, 17] + rng.integers(0, 705, size=6).tolist()
+    lens = [704, 703, 433, 432, 337, 336, 385, 0, 1, 17] + rng.integers(0, 705, size=6).tolist()
     pool, kd, vd, lens = make_rows(16, 8, 16, lens, dtype, seed=D + G, order_seed=D + G + 1, D=D, cap=704)
     q = hf_layout(16, G * 8, 1, D, dtype, torch.Generator().manual_seed(G)).cuda()
     outs = []
@@ -198,7 +199,7 @@ def test_split_pairs_same_bits_every_call(dtype, D, G):
 @pytest.mark.parametrize("B,Hkv,D", [(1, 8, 128), (3, 8, 128), (2, 2, 64)])
 def test_few_pairs_one_launch(B, Hkv, D):
     """Fewer than 128 (row, kv head) pairs -- batch-1 decode -- take the one-launch pair kernel
-    with up to 8 workgroups a pair (each at least 12 chunks of the row): rows of up to 704
+    with up to 8 workgroups a pair (each at least 11 chunks of the row, 14 with 8 query rows): rows of up to 704
     positions on and next to chunk boundaries, G = 4 / 8 / 1, two query tokens, both output
     types; 3073 positions (past 8 x 24 chunks) take the flat schedule, which agrees."""
     rng = np.random.default_rng(B * 10 + D)
@@ -218,8 +219,9 @@ def test_few_pairs_one_launch(B, Hkv, D):
 @pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 64)])
 def test_small_batch_pairs_over_many_workgroups(dtype, D):
     """8 (row, kv head) pairs on 256 CUs: up to 8 workgroups a pair (the grid's count), a row cut
-    over as many as give each 12 chunks -- 3072 positions over 8, 1537 over 8, 385 over 2, 191
-    alone -- and the last to arrive folding the parts' records in their order.  Rows up to 3072
+    over as many as give each 11 chunks (14 with 8 query rows) -- with 4 rows 3072 positions over
+    8, 1537 over 8, 385 over 2, 191 alone -- and the last to arrive folding the parts' records in
+    their order.  Rows up to 3072
     positions take this one launch (the flat schedule before).  G = 4 / 8, two query tokens,
     against the float64 reference; three calls give the same bits and leave every arrival count
     at 0; the flat schedule agrees."""
