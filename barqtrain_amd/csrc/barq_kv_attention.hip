@@ -79,6 +79,13 @@ __host__ __device__ constexpr int pair_part_chunks() {
 constexpr int kMaxSplit = 8;
 constexpr int64_t kSplitChunksPerPart = 24;
 constexpr int kSplitAny = 0;  // attention_pair_kernel's S: the grid's count, 3 .. kMaxSplit
+// Longer rows at small batches (C4: one row of 32k positions, 8 pairs): up to kMaxSplitLong
+// workgroups a pair, past 8 parts at least kLongPartChunks chunks each and at most
+// kLongChunksPerPart (a part's blocks fit one table window, loaded at the part's start).
+constexpr int kSplitLong = -1;  // attention_pair_kernel's S: the grid's count, 3 .. kMaxSplitLong
+constexpr int kMaxSplitLong = 32;
+constexpr int kLongPartChunks = 32;
+constexpr int64_t kLongChunksPerPart = 72;
 
 enum : int { kBF16 = 0, kF16 = 1 };
 
@@ -369,6 +376,7 @@ template <int HD>
 struct PieceStart {
   int pt[kTableRegs];
   u32x4 qv[Head<HD>::kSteps];
+  int blk0;  // the window's first block
 };
 
 // K and V of one 16-position chunk for this lane.  K: lane (g, n16) holds dims 32 * step + 8 * g
@@ -630,10 +638,10 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
   const int T = a.tokens;
 
   // The block-table window and the query rows load together: one round trip before the first
-  // chunk's loads (PRE: the caller started both, the window from block 0, before it knew the
-  // row's length; entries past the piece's blocks are dropped unchecked).  The query rows are
+  // chunk's loads (PRE: the caller started both, the window from block pre->blk0, mostly before
+  // it knew the row's length; entries past the piece's blocks are dropped unchecked).  The query rows are
   // kept in LDS.
-  int blk0 = PRE ? 0 : (int)a.page_div.div((uint32_t)t_begin);
+  int blk0 = PRE ? pre->blk0 : (int)a.page_div.div((uint32_t)t_begin);
   const int blk_end = t_end > t_begin ? (int)a.page_div.div((uint32_t)(t_end - 1)) + 1 : blk0;
   int pt[kTableRegs];
   // The pair kernel keeps its query fragments in registers (it has them to spare), the others
@@ -644,7 +652,7 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
     u32x4 qv[kSteps];
     if constexpr (PRE) {
 #pragma unroll
-      for (int k = 0; k < kTableRegs; ++k) pt[k] = 64 * k + lane < blk_end ? pre->pt[k] : 0;
+      for (int k = 0; k < kTableRegs; ++k) pt[k] = 64 * k + lane < blk_end - blk0 ? pre->pt[k] : 0;
 #pragma unroll
       for (int st = 0; st < kSteps; ++st) qv[st] = pre->qv[st];
     } else {
@@ -966,7 +974,9 @@ void attention_flat_kernel(const AttnArgs a) {
 template <int HD, int E, int R, typename OutT, bool COLD, int W, int S>
 __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(R <= 2 ? 2 : 1, R <= 2 ? 2 : 1)))
 void attention_pair_kernel(const AttnArgs a) {
-  static_assert(S == 1 || S == 2 || S == kSplitAny, "one, two or the grid's count of workgroups a pair");
+  static_assert(S == 1 || S == 2 || S == kSplitAny || S == kSplitLong,
+                "one, two or the grid's count of workgroups a pair");
+  constexpr bool kGrid = S == kSplitAny || S == kSplitLong;  // the workgroups a pair: the grid's count
   constexpr int kRecMax = (int)record_floats(4 * R, HD);
   constexpr int kQuads = HD / 4;
   __shared__ float lp[W][kBlock][kMaxRows];
@@ -976,8 +986,8 @@ void attention_pair_kernel(const AttnArgs a) {
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
   // (The first workgroups of a launch compute this before their first load: a compare where it
   // can be one.)
-  const int pairs = S == kSplitAny ? a.batch * a.kv_heads : (int)gridDim.x / S;
-  const int nsplit = S == kSplitAny ? (int)gridDim.x / pairs : S;
+  const int pairs = kGrid ? a.batch * a.kv_heads : (int)gridDim.x / S;
+  const int nsplit = kGrid ? (int)gridDim.x / pairs : S;
   const int half = S == 1   ? 0
                    : S == 2 ? (int)((int)blockIdx.x >= pairs)
                             : (int)blockIdx.x / pairs;  // this workgroup's part of the pair
@@ -988,6 +998,7 @@ void attention_pair_kernel(const AttnArgs a) {
   // together.
   int len = a.seq_lens[b];
   PieceStart<HD> ps;
+  ps.blk0 = 0;
   issue_table(a, b, 0, (int)a.page_div.div((uint32_t)a.max_seq + a.page_size - 1), threadIdx.x & (kWave - 1), ps.pt);
   issue_query<HD, COLD>(a, b, kvh, threadIdx.x & (kWave - 1), ps.qv);
   if (len > a.max_seq) {
@@ -996,16 +1007,35 @@ void attention_pair_kernel(const AttnArgs a) {
   }
   len = max(len, 0);
   const int nch = (len + kBlock - 1) / kBlock;
-  const int kparts = S == 1 ? 1 : min(nsplit, max(1, nch / pair_part_chunks<R>()));
+  int kparts = S == 1 ? 1 : min(nsplit, max(1, nch / pair_part_chunks<R>()));
+  if (S == kSplitLong && kparts > 8) kparts = min(nsplit, max(8, nch / kLongPartChunks));
   const bool split = kparts > 1;
   if (half >= kparts) return;
   // The first waves take the remainder: waves 0 .. 3 are each SIMD's first, whose loads are
-  // served first (the second wave on a SIMD gets its first chunk ~1.5 us later).
-  const int parts = kparts * W;
-  const int gw = w * kparts + half;
-  const int base = nch / parts, extra = nch - base * parts;
-  const int c0 = gw * base + min(gw, extra);
-  const int c1 = c0 + base + (gw < extra ? 1 : 0);
+  // served first (the second wave on a SIMD gets its first chunk ~1.5 us later).  Rows whose
+  // blocks all lie in the prologue's window deal their ranges to the workgroups in turn; longer
+  // ones (kSplitLong) give each workgroup a contiguous part, which loads its own window.
+  int c0, c1;
+  if (S != kSplitLong || (int)a.page_div.div((uint32_t)max(kBlock * nch - 1, 0)) < kTableEntries) {
+    const int parts = kparts * W;
+    const int gw = w * kparts + half;
+    const int base = nch / parts, extra = nch - base * parts;
+    c0 = gw * base + min(gw, extra);
+    c1 = c0 + base + (gw < extra ? 1 : 0);
+  } else {
+    const int hb = nch / kparts, hx = nch - hb * kparts;
+    const int h0 = half * hb + min(half, hx);
+    const int hn = hb + (half < hx ? 1 : 0);
+    const int base = hn / W, extra = hn - base * W;
+    c0 = h0 + w * base + min(w, extra);
+    c1 = c0 + base + (w < extra ? 1 : 0);
+    const int blo = (int)a.page_div.div((uint32_t)(kBlock * h0));
+    const int bhi = hn > 0 ? (int)a.page_div.div((uint32_t)(min(len, kBlock * (h0 + hn)) - 1)) + 1 : blo;
+    if (bhi > kTableEntries) {
+      issue_table(a, b, blo, bhi, threadIdx.x & (kWave - 1), ps.pt);
+      ps.blk0 = blo;
+    }
+  }
   const int M = a.rows;
   const int rec = (int)record_floats(M, HD);
   attend_piece<HD, E, R, true, OutT, COLD, true>(a, lp[w], lq[w], b, kvh, len, kBlock * c0, min(len, kBlock * c1),
@@ -1124,8 +1154,10 @@ void attention_pair_kernel(const AttnArgs a) {
     f32x4 osum;
     if (S == 2 || kparts == 2)
       gather_fold(std::integral_constant<int, 2>{}, lsum, osum);
-    else
+    else if (S != kSplitLong || kparts <= kMaxSplit)
       gather_fold(std::integral_constant<int, (S == 2 ? 2 : kMaxSplit)>{}, lsum, osum);
+    else
+      gather_fold(std::integral_constant<int, (S == kSplitLong ? kMaxSplitLong : 2)>{}, lsum, osum);
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
     store_out4<OutT, E>(out_row(a, b, kvh, row) + (int64_t)(4 * quad) * sizeof(OutT), osum * inv);
   }
@@ -1270,6 +1302,17 @@ hipError_t launch_typed(AttnArgs a, bool merge, hipStream_t stream) {
                            dim3(kPairWaves * kWave), 0, stream, a);
       }
       return hipGetLastError();
+    }
+    // Longer rows at small batches (C4 at 32k positions: 34.3 -> 31.1 us against the flat pair of
+    // launches): up to kMaxSplitLong workgroups a pair, each part's blocks in a window of its own.
+    if (a.range_chunks == 0 && pairs > 0 && pairs <= BARQ_KV_CTRL_PAIR_SLOTS) {
+      auto* split_long = attention_pair_kernel<HD, E, R, OutT, COLD, kPairWaves, kSplitLong>;
+      const int64_t nlong =
+          std::min<int64_t>(kMaxSplitLong, resident_blocks<kPairWaves * kWave>(split_long, 0) / pairs);
+      if (nlong > 2 && chunks <= nlong * kLongChunksPerPart) {
+        hipLaunchKernelGGL(split_long, dim3((unsigned)(nlong * pairs)), dim3(kPairWaves * kWave), 0, stream, a);
+        return hipGetLastError();
+      }
     }
   }
   auto* k = attention_flat_kernel<HD, E, R, U, OutT, COLD>;

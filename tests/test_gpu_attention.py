@@ -201,7 +201,8 @@ def test_few_pairs_one_launch(B, Hkv, D):
     """Fewer than 128 (row, kv head) pairs -- batch-1 decode -- take the one-launch pair kernel
     with up to 8 workgroups a pair (each at least 11 chunks of the row, 14 with 8 query rows): rows of up to 704
     positions on and next to chunk boundaries, G = 4 / 8 / 1, two query tokens, both output
-    types; 3073 positions (past 8 x 24 chunks) take the flat schedule, which agrees."""
+    types; a row past the pair kernels' reach (36,865 positions, over 32 x 72 chunks) takes the flat
+    schedule, which agrees."""
     rng = np.random.default_rng(B * 10 + D)
     lens = sorted([704, 17, 1][:B] + rng.integers(1, 705, size=max(B - 3, 0)).tolist(), reverse=True)
     pool, kd, vd, lens = make_rows(B, Hkv, 16, lens, torch.bfloat16, seed=B + D, order_seed=B + D + 1, D=D,
@@ -211,7 +212,7 @@ def test_few_pairs_one_launch(B, Hkv, D):
         ws = check(pool, kd, vd, lens, G, T, torch.bfloat16, seed=800 + i, ws=ws)
     check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=9, out_f32=False)
     assert pool.errors() == 0
-    pool, kd, vd, lens = make_rows(1, Hkv, 16, [3073], torch.bfloat16, seed=B + D + 2, order_seed=B + D + 3, D=D)
+    pool, kd, vd, lens = make_rows(1, 2, 16, [36865], torch.bfloat16, seed=B + D + 2, order_seed=B + D + 3, D=D)
     check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=11)
     assert pool.errors() == 0
 
@@ -307,8 +308,10 @@ def test_llama3_8b_decode_shape():
 
 
 def test_long_row_many_records():
-    """One long row over 2 kv heads: the automatic schedule cuts each pair into ~1000 ranges, whose
-    records the merge launch folds with its wide workgroups (fewer merge workgroups than CUs)."""
+    """One long row (12,001 positions) over 2 kv heads: up to 8 query rows take the long-row pair
+    kernel (16 workgroups a pair, each part's table window its own); 16 query rows and a fixed
+    split take the flat schedule, whose many records a pair the merge launch folds with its wide
+    workgroups (fewer merge workgroups than CUs)."""
     lens = [12001]
     pool, kd, vd, lens = make_rows(1, 2, 16, lens, torch.bfloat16, seed=77, order_seed=8)
     check(pool, kd, vd, lens, 4, 1, torch.bfloat16, seed=5)
@@ -474,3 +477,29 @@ def test_split_pairs_in_graph_replays(hip, B, Hkv, prefill):
             assert ok, f"replay {s} layer {li}: {ratio:.3g} x tolerance"
             assert not pair_words(pools[li], B * Hkv).any()
     assert all(p.errors() == 0 for p in pools)
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 64)])
+def test_long_rows_over_many_workgroups(dtype, D):
+    """Rows longer than one table window (256 blocks) at a small batch: the long-row pair kernel,
+    up to 32 workgroups a pair.  8,192 positions: 16 contiguous parts of 32 chunks, those past block
+    256 loading their own window; 3,001 positions in the same launch: 8 parts dealt in turn from
+    the prologue's window.  G = 4 / 8, two query tokens, both output types, against the float64
+    reference; three calls give the same bits and leave every arrival count at 0; the flat
+    schedule agrees."""
+    pool, kd, vd, lens = make_rows(2, 4, 16, [8192, 3001], dtype, seed=D + 3, order_seed=D + 4, D=D)
+    for i, (G, T) in enumerate([(4, 1), (8, 1), (2, 2)]):
+        q = hf_layout(2, G * 4, T, D, dtype, torch.Generator().manual_seed(60 + i)).cuda()
+        outs = []
+        for _ in range(3):
+            out, _ = pool.attend(q, out_f32=True)
+            torch.cuda.synchronize()
+            outs.append(out.double().cpu().numpy())
+            assert not pair_words(pool, 8).any()
+        assert all(np.array_equal(outs[0], o) for o in outs[1:])
+        want = decode_attention_reference(q.double().cpu().numpy(), kd, vd, lens, D ** -0.5)
+        ok, ratio = within_tolerance(outs[0], want, **F32_TOL)
+        assert ok, f"G={G} T={T}: {ratio:.3g} x tolerance"
+    check(pool, kd, vd, lens, 4, 1, dtype, seed=9, out_f32=False)
+    check(pool, kd, vd, lens, 4, 1, dtype, seed=10, split_tokens=256)  # the flat schedule
+    assert pool.errors() == 0

@@ -515,3 +515,36 @@ def test_selection_larger_than_an_fp8_pool_on_gpu(hip):
     ok, ov = oracle.current_tensors()
     assert np.array_equal(to_bits(gk), ok) and np.array_equal(to_bits(gv), ov)
     assert layer.pool.errors() == 0
+
+
+def test_decode_attention_on_quantised_pages_long_rows(hip):
+    """Attention over a quantised pool whose rows pass one table window (the long-row pair kernel
+    over cold blocks: 5,000 and 1,500 positions, 8 pairs), against the float64 reference over the
+    dequantising gather's K/V."""
+    from attn_ref import decode_attention_reference, within_tolerance
+    from barqtrain_amd.paged import QuantPagePool
+
+    H, D, P, W = 4, 128, 16, 64
+    lens = [5000, 1500]
+    B, cap = len(lens), 5008
+    pool = QuantPagePool(max_batch=B, max_blocks=cap // P, page_size=P, kv_heads=H, head_dim=D, dtype=torch.bfloat16,
+                         device="cuda", window=W)
+    gen = torch.Generator().manual_seed(91)
+    done = 0
+    for b in range(B, 0, -1):
+        n = lens[b - 1] - done
+        while n > 0:
+            t = min(n, 1024)
+            k, v = hf_layout(b, H, t, D, torch.bfloat16, gen) * 3, hf_layout(b, H, t, D, torch.bfloat16, gen)
+            pool.append(k.cuda(), v.cuda())
+            done += t
+            n -= t
+    assert int(pool.cold_blocks.max()) > 256
+    kd, vd = (t.double().cpu().numpy() for t in pool.gather(B))
+    for G in (4, 8):
+        q = hf_layout(B, G * H, 1, D, torch.bfloat16, gen).cuda()
+        want = decode_attention_reference(q.double().cpu().numpy(), kd, vd, lens, D ** -0.5)
+        got = pool.attend(q, out_dtype=torch.float32)
+        ok, ratio = within_tolerance(got.double().cpu().numpy(), want, **ATT_F32)
+        assert ok, f"G={G}: {ratio:.3g} x tolerance"
+    assert pool.errors() == 0
