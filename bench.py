@@ -410,16 +410,28 @@ class Workload:
                 pool.append_rows(rows, *self.refill)
 
 
-def pair_kernel_bounds(pairs, max_seq, rows, quantised):
-    """The library's one-launch (pair kernel) bounds for a one-token decode call: up to 8 query
-    rows and at most 44 16-position chunks, or, from 128 (row, kv head) pairs with up to 4 query
-    rows, 64 chunks (over two-byte pages 128 from 256 pairs)."""
+def pair_kernel_bounds(pairs, max_seq, rows, quantised, cus=256):
+    """Whether the library takes a one-token decode call in one launch (its pair kernel), as its
+    host code decides (barq_kv_attention.hip, launch_typed): up to 8 query rows; at most 44
+    16-position chunks, or, from 128 (row, kv head) pairs with up to 4 query rows, 64 (over
+    two-byte pages 128 from 256 pairs); with three or more 8-wave workgroups a pair resident (one a
+    CU), up to 24 chunks a workgroup (at most 8 of them, within one 256-block window), else up to
+    72 a workgroup over at most 32 of them."""
     if pairs < 1 or rows > 8:
         return False
     chunks = -(-max_seq // 16)
+    part = 11 if rows <= 4 else 14
+    nsplit = min(8, cus // pairs) if pairs <= 512 and chunks >= 2 * part else 1
     if rows > 4 or pairs < 128:
-        return chunks <= 44
-    return chunks <= (128 if pairs >= 256 and not quantised else 64)
+        bound = 44
+    else:
+        bound = 128 if pairs >= 256 and not quantised else 64
+    if nsplit > 2:
+        bound = min(256, max(bound, nsplit * 24))
+    if chunks <= bound:
+        return True
+    nlong = min(32, cus // pairs) if pairs <= 512 else 0
+    return nlong > 2 and chunks <= nlong * 72
 
 
 def attention_leg(cfg, pools, B, dev, reps=20, kv_bytes=None, probe=False):
@@ -495,7 +507,8 @@ def attention_leg(cfg, pools, B, dev, reps=20, kv_bytes=None, probe=False):
         raise SystemExit("device error bits set by the attention leg")
     gathered = 3 * (sum(call_bytes) - L * io) / L  # gather reads + writes K/V, attention re-reads
     cold = "<..., COLD> (fp8 pages read as codes)" if getattr(pools[0], "quantized", False) else ""
-    if pair_kernel_bounds(B * H, max_seq, G, bool(cold)):
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    if pair_kernel_bounds(B * H, max_seq, G, bool(cold), cus):
         kname = "attention_pair_kernel" + cold + " (one launch per layer)"
     else:
         kname = "attention_flat_kernel" + cold + " + attention_merge_kernel (one launch pair per layer)"

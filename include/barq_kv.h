@@ -288,8 +288,8 @@ int64_t barq_kv_attention_workspace_bytes(const barq_kv_pool* pool, int64_t batc
  * (rounded up to 16; 0 = automatic).  Ranges that end inside a (row, kv head) keep partial
  * results in workspace (device memory of barq_kv_attention_workspace_bytes(...) bytes, 16-byte
  * aligned, no initialisation needed), merged by a second launch on the same stream; launches
- * that share a workspace must not overlap.  Short rows (up to 44 to 192 chunks of 16 positions,
- * by batch and query rows) take one launch instead, one or more workgroups per (row, kv head); the
+ * that share a workspace must not overlap.  Rows of up to 44 to 2,304 chunks of 16 positions (by
+ * batch and query rows) take one launch instead, one or more workgroups per (row, kv head); the
  * workgroups of a split pair pass their partial results through the workspace and count their
  * arrivals on the pool's ctrl (BARQ_KV_CTRL_PAIR_WORD), which they leave at 0, so calls on one
  * pool are ordered on one stream like every call naming it.
