@@ -4,7 +4,7 @@ implementation (``"barq_paged"``).
 A ``BarqPagedKVCache`` built with ``fused_attention=True`` appends in ``update`` and returns, in
 place of materialised K/V, zero-stride views that name their cache layer.  The attention
 function registered here finds the layer on the key view and, for decode (``G * T <= 16`` query
-rows per kv head, no padding mask, head_dim 64 or 128), runs the pool's decode-attention kernel:
+rows per kv head, no padding mask, head_dim 64, 128 or 256), runs the pool's decode-attention kernel:
 softmax(Q K^T) V is computed from the pages through the block table, so the per-step gather of
 the whole history (and its write and re-read) disappears.  Prefill, padded batches and other
 head sizes take the gathered K/V through torch's fused SDPA kernels (flash or memory-efficient,
@@ -142,7 +142,7 @@ def paged_attention_forward(module: torch.nn.Module, query: torch.Tensor, key: t
     rows = (q_heads // pool.kv_heads) * tokens
     kernel_ok = (not options and not window_cuts and attention_mask is None and rows <= _KERNEL_MAX_ROWS
                  and pool.on_gpu and (not getattr(pool, "quantized", False) or pool.page_size % 16 == 0)
-                 and pool.dtype in (torch.bfloat16, torch.float16) and pool.head_dim in (64, 128))
+                 and pool.dtype in (torch.bfloat16, torch.float16) and pool.head_dim in (64, 128, 256))
     if kernel_ok:
         return pool.attend(query, scale).transpose(1, 2), None
     k, v = layer.current_tensors()

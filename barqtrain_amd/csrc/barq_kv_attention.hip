@@ -89,13 +89,14 @@ constexpr int64_t kLongChunksPerPart = 72;
 
 enum : int { kBF16 = 0, kF16 = 1 };
 
-// Head sizes the kernels are built for (HD = 64 or 128) and the lane layout each gives.  Scores:
+// Head sizes the kernels are built for (HD = 64, 128, and 256 on two-byte pages through the flat
+// schedule at one wave per SIMD) and the lane layout each gives.  Scores:
 // lane (g, n16) of the 16x16x32 MFMA holds dims 32 * step + 8 * g .. +7 of one position, HD / 32
 // steps.  V: a position's HD dims are HD / 8 lanes of 8 dims, so one 16-byte load per lane covers
 // 64 / (HD / 8) positions and a chunk takes 16 / that many loads.
 template <int HD>
 struct Head {
-  static_assert(HD == 64 || HD == 128, "head sizes 64 and 128");
+  static_assert(HD == 64 || HD == 128 || HD == 256, "head sizes 64, 128 and 256");
   static constexpr int kSteps = HD / 32;              // k-steps of the score MFMA
   static constexpr int kVLanes = HD / 8;              // lanes of one position's V
   static constexpr int kVPos = kWave / kVLanes;       // positions of one V load
@@ -515,8 +516,19 @@ __device__ __forceinline__ u32x4 dequant_vector(const u32x4 x, bool value) {
 // to scratch), so the rare path adds no register pressure to the common one.
 template <int N>
 __device__ __forceinline__ u32x4 chunk_reg(const u32x4 (&r)[N], int n) {
-  static_assert(N == 2 || N == 4, "chunk layouts of head sizes 64 and 128");
-  if constexpr (N == 4) {
+  static_assert(N == 2 || N == 4 || N == 8, "chunk layouts of head sizes 64, 128 and 256");
+  if constexpr (N == 8) {
+    switch (n) {
+      case 0: return r[0];
+      case 1: return r[1];
+      case 2: return r[2];
+      case 3: return r[3];
+      case 4: return r[4];
+      case 5: return r[5];
+      case 6: return r[6];
+      default: return r[7];
+    }
+  } else if constexpr (N == 4) {
     switch (n) {
       case 0: return r[0];
       case 1: return r[1];
@@ -529,7 +541,18 @@ __device__ __forceinline__ u32x4 chunk_reg(const u32x4 (&r)[N], int n) {
 }
 template <int N>
 __device__ __forceinline__ void set_chunk_reg(u32x4 (&r)[N], int n, const u32x4 y) {
-  if constexpr (N == 4) {
+  if constexpr (N == 8) {
+    switch (n) {
+      case 0: r[0] = y; break;
+      case 1: r[1] = y; break;
+      case 2: r[2] = y; break;
+      case 3: r[3] = y; break;
+      case 4: r[4] = y; break;
+      case 5: r[5] = y; break;
+      case 6: r[6] = y; break;
+      default: r[7] = y; break;
+    }
+  } else if constexpr (N == 4) {
     switch (n) {
       case 0: r[0] = y; break;
       case 1: r[1] = y; break;
@@ -921,7 +944,8 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
 // ... of the flat chunk list.  UNIFORM: page_size is a multiple of 16.  R: groups of 4 query
 // rows (rows <= 4 * R).  HD: the head size.
 template <int HD, int E, int R, bool UNIFORM, typename OutT, bool COLD>
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(R <= 2 ? 2 : 1, R <= 2 ? 2 : 1)))
+__global__ __launch_bounds__(kWave)
+__attribute__((amdgpu_waves_per_eu(R <= 2 && HD <= 128 ? 2 : 1, R <= 2 && HD <= 128 ? 2 : 1)))
 void attention_flat_kernel(const AttnArgs a) {
   __shared__ float lp[kBlock][kMaxRows];             // probabilities, staged for the P.V operand layout
   __shared__ u32x4 lq[Head<HD>::kSteps][kWave];      // the piece's query fragments
@@ -1273,7 +1297,7 @@ template <int HD, int E, int R, bool U, typename OutT, bool COLD>
 hipError_t launch_typed(AttnArgs a, bool merge, hipStream_t stream) {
   // Pairs of bounded length, the automatic split, whole-chunk pages, up to 8 query rows (two waves
   // per SIMD keep the accumulators in registers): one workgroup per pair.
-  if constexpr (U && R <= 2) {
+  if constexpr (U && R <= 2 && HD <= 128) {
     const int64_t pairs = (int64_t)a.batch * a.kv_heads;
     // Fewer pairs than kPairMinPairs leave CUs idle, but up to kPairMaxChunks a pair one launch
     // still beats the flat pair of launches and its merge (C2 shape at batch 1: 650 positions
@@ -1346,17 +1370,23 @@ hipError_t launch_rows(const AttnArgs& a, bool out_f32, bool merge, hipStream_t 
 
 template <int HD, int E>
 hipError_t launch_pages(const AttnArgs& a, bool uniform, bool cold, bool out_f32, bool merge, hipStream_t stream) {
-  if (cold)  // quantised pools: page_size a multiple of 16 (checked by the caller)
-    return launch_rows<HD, E, true, true>(a, out_f32, merge, stream);
-  return uniform ? launch_rows<HD, E, true, false>(a, out_f32, merge, stream)
-                 : launch_rows<HD, E, false, false>(a, out_f32, merge, stream);
+  if constexpr (HD == 256) {  // two-byte pages only (the caller refuses quantised pools)
+    return uniform ? launch_rows<HD, E, true, false>(a, out_f32, merge, stream)
+                   : launch_rows<HD, E, false, false>(a, out_f32, merge, stream);
+  } else {
+    if (cold)  // quantised pools: page_size a multiple of 16 (checked by the caller)
+      return launch_rows<HD, E, true, true>(a, out_f32, merge, stream);
+    return uniform ? launch_rows<HD, E, true, false>(a, out_f32, merge, stream)
+                   : launch_rows<HD, E, false, false>(a, out_f32, merge, stream);
+  }
 }
 
 template <int E>
 hipError_t launch_dtype(const AttnArgs& a, int head_dim, bool uniform, bool cold, bool out_f32, bool merge,
                         hipStream_t stream) {
-  return head_dim == 64 ? launch_pages<64, E>(a, uniform, cold, out_f32, merge, stream)
-                        : launch_pages<128, E>(a, uniform, cold, out_f32, merge, stream);
+  return head_dim == 64    ? launch_pages<64, E>(a, uniform, cold, out_f32, merge, stream)
+         : head_dim == 128 ? launch_pages<128, E>(a, uniform, cold, out_f32, merge, stream)
+                           : launch_pages<256, E>(a, uniform, cold, out_f32, merge, stream);
 }
 
 struct AttnPlan {
@@ -1372,7 +1402,7 @@ struct AttnPlan {
 // schedule's own, total / resident waves).
 int plan_attention(const barq_kv_pool* pool, int64_t batch, int64_t q_heads, int64_t tokens,
                    int64_t max_seq, int64_t split_tokens, AttnPlan* plan) {
-  if (!pool || pool->elem_bytes != 2 || (pool->head_dim != 64 && pool->head_dim != 128) || pool->kv_heads <= 0 ||
+  if (!pool || pool->elem_bytes != 2 || (pool->head_dim != 64 && pool->head_dim != 128 && pool->head_dim != 256) || pool->kv_heads <= 0 ||
       pool->page_size <= 0 || pool->max_blocks <= 0 || pool->num_pages <= 0 ||
       pool->num_pages > INT32_MAX || pool->max_batch <= 0)
     return BARQ_KV_ERR_INVALID;
@@ -1479,6 +1509,7 @@ int decode_attention(const barq_kv_pool* pool, const barq_kv_cold* cold, const v
   a.num_cold = 0;
 
   const bool uniform = pool->page_size % kBlock == 0;
+  if (cold && pool->head_dim == 256) return BARQ_KV_ERR_INVALID;  // quantised pools: head sizes 64, 128
   if (cold) {
     const int64_t want = (flags & BARQ_KV_ATTN_FP16) ? BARQ_KV_FP16 : BARQ_KV_BF16;
     if (!uniform || cold->element_type != want || !cold->key_codes || !cold->value_codes || !cold->key_scales ||

@@ -500,7 +500,7 @@ class PagePool:
                                                  max(int(max_seq), 1), int(split_tokens))
         if need < 0:
             raise ValueError(
-                "paged decode attention takes bf16/fp16 pools with head_dim 64 or 128 and at most 16 "
+                "paged decode attention takes bf16/fp16 pools with head_dim 64, 128 or 256 and at most 16 "
                 f"query rows per kv head (got {self.dtype}, head_dim {self.head_dim}, "
                 f"{q_heads // self.kv_heads} x {tokens} rows)")
         self._attention_call(backend, query, out, scale, max(int(max_seq), 1), int(split_tokens),
@@ -911,12 +911,12 @@ class QuantPagePool(PagePool):
         return dst
 
     def _attention_call(self, backend, query, out, scale, max_seq, split_tokens, ws):
-        if self.page_size % 16 == 0:
+        if self.page_size % 16 == 0 and self.head_dim in (64, 128):
             backend.pool_decode_attention_cold(self.tensors, self.cold_tensors, self.window, query, out, scale,
                                                max_seq, split_tokens, ws)
             return
         # Pages of other sizes: the kernel reads a 16-position chunk in one format, which such pages
-        # do not give.  The dequantising gather instead (the values the kernel would decode),
+        # do not give (nor does it decode codes at head size 256).  The dequantising gather instead (the values the kernel would decode),
         # then attention over the gathered K/V on the device, in float32, with the row lengths read
         # on the device (so a captured graph serves growing rows).
         batch, q_heads, tokens, _ = query.shape

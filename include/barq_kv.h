@@ -273,8 +273,8 @@ int64_t barq_kv_attention_workspace_bytes(const barq_kv_pool* pool, int64_t batc
                                           int64_t split_tokens);
 
 /*
- * Decode attention over rows [0, batch) of a 2-byte (bf16 / fp16) pool with head_dim 64 or
- * 128 (D below), reading K and V from the pages:
+ * Decode attention over rows [0, batch) of a 2-byte (bf16 / fp16) pool with head_dim 64, 128 or
+ * 256 (D below), reading K and V from the pages:
  *   out[b, h, i, :] = sum_t softmax_t(scale * q[b, h, i, :] . K[b, h / G, t, :]) V[b, h / G, t, :]
  * over positions t <= seq_lens[b] - tokens + i (the query tokens are the row's last `tokens`
  * positions, already appended), G = q_heads / kv_heads.  A row with no visible position gets

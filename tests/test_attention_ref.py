@@ -125,7 +125,8 @@ def test_workspace_bytes_and_rejections():
     assert ws(ctypes.byref(_fake_pool(elem=4)), 2, 32, 1, 100, 0) == -1   # fp32 pool
     assert ws(ctypes.byref(_fake_pool(dim=64)), 2, 32, 1, 100, 0) == (2048 + pairs) * (4 * 64 + 8) * 4  # head_dim 64
     assert ws(ctypes.byref(_fake_pool(dim=96)), 2, 32, 1, 100, 0) == -1   # head_dim 96
-    assert ws(ctypes.byref(_fake_pool(dim=256)), 2, 32, 1, 100, 0) == -1  # head_dim 256
+    assert ws(ctypes.byref(_fake_pool(dim=256)), 2, 32, 1, 100, 0) == (2048 + pairs) * (4 * 256 + 8) * 4  # head_dim 256
+    assert ws(ctypes.byref(_fake_pool(dim=512)), 2, 32, 1, 100, 0) == -1  # head_dim 512
 
     att = lib.barq_kv_decode_attention
     # Fake, aligned device addresses: every call below is rejected before any launch (batch 0

@@ -120,6 +120,25 @@ def test_head_dim_64(dtype, page):
     assert pool.errors() == 0
 
 
+@pytest.mark.parametrize("dtype,page", [(torch.bfloat16, 16), (torch.float16, 32), (torch.bfloat16, 5)])
+def test_head_dim_256(dtype, page):
+    """Head size 256 (Gemma: 8 query heads over 1 kv head, or 16 over 8 -- G = 8 / 2 here) on
+    two-byte pages, through the flat schedule at one wave per SIMD: ragged rows with a random page
+    order (16-position chunks, pages of 16, 32 and 5), G = 8 / 2 / 4 / 16, two query tokens,
+    fixed and automatic splits, both output types, and a long row folded from many records."""
+    lens = [1100, 513, 257, 256, 255, 64, 17, 16, 1, 0]
+    pool, kd, vd, lens = make_rows(len(lens), 2, page, lens, dtype, seed=page + 256, order_seed=page + 257, D=256)
+    ws = None
+    for i, (G, T, split) in enumerate([(8, 1, 0), (2, 1, 256), (4, 2, 48), (16, 1, 0), (8, 2, 0)]):
+        ws = check(pool, kd, vd, lens, G, T, dtype, seed=900 + i, split_tokens=split, ws=ws)
+    check(pool, kd, vd, lens, 8, 1, dtype, seed=9, out_f32=False)
+    assert pool.errors() == 0
+    pool, kd, vd, lens = make_rows(1, 2, page, [6001], dtype, seed=page + 258, order_seed=page + 259, D=256)
+    check(pool, kd, vd, lens, 8, 1, dtype, seed=10)
+    check(pool, kd, vd, lens, 2, 1, dtype, seed=11, out_f32=False)
+    assert pool.errors() == 0
+
+
 @pytest.mark.parametrize("dtype,page,D", [(torch.bfloat16, 16, 128), (torch.float16, 32, 128), (torch.bfloat16, 16, 64)])
 def test_many_short_pairs_one_launch(dtype, page, D):
     """128+ (row, kv head) pairs of at most 704 positions with the automatic split take one
