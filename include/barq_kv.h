@@ -314,7 +314,8 @@ int barq_kv_decode_attention(const barq_kv_pool* pool, const void* query, int64_
  * and enqueues nothing.  With the automatic split the workspace is (2048 + batch * kv_heads)
  * records of (G * tokens) * (head_dim + 2) floats, so 24 MiB holds every batch <= 64 with 8 KV heads
  * and head_dim 128 at G * tokens <= 16 (21.3 MB at the largest); batch 1024 at that shape needs
- * 85 MB and is refused.  The workspace needs no initialisation, so calls clear nothing.  Every call on
+ * 85 MB and is refused.  Head_dim 256 doubles the records: the same batches fit at
+ * G * tokens <= 9 (23.8 MB), and G * tokens = 16 is refused at any batch (33.9 MB at batch 1).  The workspace needs no initialisation, so calls clear nothing.  Every call on
  * a GPU uses that GPU's one array: calls that overlap on one GPU (other streams, other host
  * threads) race on it; order them on one stream.  The first call on a device resolves the array's
  * address there; the call allocates nothing.
