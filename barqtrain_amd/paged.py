@@ -916,9 +916,10 @@ class QuantPagePool(PagePool):
                                                max_seq, split_tokens, ws)
             return
         # Pages of other sizes: the kernel reads a 16-position chunk in one format, which such pages
-        # do not give (nor does it decode codes at head size 256).  The dequantising gather instead (the values the kernel would decode),
-        # then attention over the gathered K/V on the device, in float32, with the row lengths read
-        # on the device (so a captured graph serves growing rows).
+        # do not give (nor does it decode codes at head size 256).  The dequantising gather instead
+        # (the values the kernel would decode), then attention over the gathered K/V on the device,
+        # in float32, with the row lengths read on the device (so a captured graph serves growing
+        # rows).
         batch, q_heads, tokens, _ = query.shape
         ko, vo = self.gather(batch, max_seq)
         group = q_heads // self.kv_heads

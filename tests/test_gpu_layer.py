@@ -241,12 +241,24 @@ def qwen2_small_head(seed=0):
     return Qwen2ForCausalLM(cfg).to(torch.bfloat16).eval(), cfg
 
 
-@pytest.mark.parametrize("factory", [bf16_llama, qwen2_small_head], ids=["llama_d128_g4", "qwen2_d64_g7"])
+def wide_head(seed=0):
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    torch.manual_seed(seed)
+    # Gemma-2B's attention geometry: 8 query heads over 1 kv head (G = 8), head_dim 256
+    cfg = LlamaConfig(vocab_size=512, hidden_size=1024, intermediate_size=1024, num_hidden_layers=2,
+                      num_attention_heads=8, num_key_value_heads=1, head_dim=256, max_position_embeddings=1024,
+                      pad_token_id=0, eos_token_id=None)
+    return LlamaForCausalLM(cfg).to(torch.bfloat16).eval(), cfg
+
+
+@pytest.mark.parametrize("factory", [bf16_llama, qwen2_small_head, wide_head],
+                         ids=["llama_d128_g4", "qwen2_d64_g7", "llama_d256_g8"])
 def test_paged_attention_decode_in_a_model(hip, monkeypatch, factory):
     """A bf16 model whose decode steps read K/V from the pages (the kernel) against the same
     model on the gather + fp32 attention path, token by token on one sequence: logits agree to
     bf16 rounding.  Then generate() through patch_inference(paged_attention=True).  Head sizes 128
-    (Llama-3 ratio) and 64 (Qwen2-0.5B geometry)."""
+    (Llama-3 ratio), 64 (Qwen2-0.5B geometry) and 256 (Gemma-2B geometry)."""
     pytest.importorskip("transformers")
     from barqtrain import create_paged_kv_cache, patch_inference
     from barqtrain_amd import attention

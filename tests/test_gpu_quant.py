@@ -319,12 +319,14 @@ ATT_OUT = {torch.bfloat16: dict(rtol=2.0 ** -8, atol=2e-5), torch.float16: dict(
                                                  (torch.float16, 32, 32, 128), (torch.bfloat16, 32, 128, 128),
                                                  (torch.bfloat16, 16, 48, 64), (torch.float16, 32, 0, 64),
                                                  # pages not a multiple of 16 (dequantising gather + attention)
-                                                 (torch.bfloat16, 5, 16, 128), (torch.float16, 8, 24, 64)])
+                                                 (torch.bfloat16, 5, 16, 128), (torch.float16, 8, 24, 64),
+                                                 # head size 256 (dequantising gather + attention)
+                                                 (torch.bfloat16, 16, 48, 256)])
 def test_decode_attention_reads_quantised_pages(hip, dtype, page, window, D):
     """Attention over a quantised pool (barq_kv_decode_attention_cold: cold blocks read as codes
     and scales, dequantised in registers) against the float64 reference over the dequantising
     gather's K/V -- the values the cold store holds -- on ragged rows mixing cold and hot blocks,
-    G = 1, 4, 8 and two query tokens; fp32 and cache-dtype outputs; head sizes 128 and 64."""
+    G = 1, 4, 8 and two query tokens; fp32 and cache-dtype outputs; head sizes 128, 64 and 256."""
     from attn_ref import decode_attention_reference, within_tolerance
     from barqtrain_amd.paged import QuantPagePool
 
