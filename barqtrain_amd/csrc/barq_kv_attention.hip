@@ -468,7 +468,8 @@ __device__ __forceinline__ void load_chunk(const AttnArgs& a, const int (&pt)[kT
 
 // A chunk of a two-byte pool with whole-chunk pages whose positions past `end` read position
 // end - 1 (the causal mask gives them probability 0): every lane loads, no branch around the loads.
-template <int HD>
+// QORDER: K in the quantised pools' order (issue_query), for the two-byte pages of such a pool.
+template <int HD, bool QORDER = false>
 __device__ __forceinline__ void load_chunk_clamped(const AttnArgs& a, const int (&pt)[kTableRegs], int blk0,
                                                    const char* kbase, const char* vbase, int tc, int end, int n16,
                                                    int g, int vpos, int vdim, u32x4 (&kv)[Head<HD>::kSteps],
@@ -477,16 +478,53 @@ __device__ __forceinline__ void load_chunk_clamped(const AttnArgs& a, const int 
   constexpr int kVPos = Head<HD>::kVPos;
   constexpr int kVLoads = Head<HD>::kVLoads;
   const uint32_t blk = a.page_div.div((uint32_t)tc);
-  const int page = table_scalar(pt, (int)blk - blk0);
+  // (QORDER: a quantised block here, -2 - c, breaks the pool's order -- its caller reports it --
+  // and reads page 0 instead of memory before the pages)
+  const int page = QORDER ? max(table_scalar(pt, (int)blk - blk0), 0) : table_scalar(pt, (int)blk - blk0);
   const int64_t base =
       (int64_t)page * a.page_bytes + (int64_t)(tc - (int)(blk * (uint32_t)a.page_size)) * a.row_bytes;
   const int lastp = end - 1 - tc;  // >= 15 for a whole chunk
-  const char* kp = kbase + base + min(n16, lastp) * a.row_bytes + 16 * g;
+  const char* kp = kbase + base + min(n16, lastp) * a.row_bytes + (QORDER ? 16 * kSteps * g : 16 * g);
 #pragma unroll
-  for (int st = 0; st < kSteps; ++st) kv[st] = ld_page_k(kp + 64 * st);
+  for (int st = 0; st < kSteps; ++st) kv[st] = ld_page_k(kp + (QORDER ? 16 : 64) * st);
 #pragma unroll
   for (int s = 0; s < kVLoads; ++s)
     vv[s] = ld_page(vbase + base + min(kVPos * s + vpos, lastp) * a.row_bytes + 16 * vdim);
+}
+
+// A quantised chunk (its block's table entry is -2 - c, c its quantised block), positions past
+// `end` reading position end - 1 as load_chunk_clamped does: every lane loads, no branch around
+// the loads.  K as load_chunk lays it out; V: the 8 codes of each of the lane's positions, and
+// one scale byte a lane, position lane % 16's (spread to the lanes at the chunk's products).
+template <int HD>
+__device__ __forceinline__ void load_cold_clamped(const AttnArgs& a, const int (&pt)[kTableRegs], int blk0, int tc,
+                                                  int end, int n16, int g, int vpos, int vdim, int kvh,
+                                                  u32x4 (&kv)[Head<HD>::kSteps], uint2 (&vc)[Head<HD>::kVLoads],
+                                                  uint32_t& vs) {
+  constexpr int kSteps = Head<HD>::kSteps;
+  constexpr int kVPos = Head<HD>::kVPos;
+  constexpr int kVLoads = Head<HD>::kVLoads;
+  const uint32_t blk = a.page_div.div((uint32_t)tc);
+  const int c = -2 - table_scalar(pt, (int)blk - blk0);
+  const int t0 = tc - (int)(blk * (uint32_t)a.page_size);
+  const int lastp = end - 1 - tc;
+  const int64_t head = (int64_t)kvh * HD;
+  const int64_t code_page = (int64_t)c * a.page_size * a.kv_heads * HD;
+  const uint8_t* kc = a.kcodes + code_page + (int64_t)(t0 + min(n16, lastp)) * a.kv_heads * HD + head + 8 * kSteps * g;
+  const uint8_t* ks = a.kscales + ((int64_t)c * a.kv_heads) * HD + head + 8 * kSteps * g;
+#pragma unroll
+  for (int st = 0; st < kSteps; st += 2) {
+    const u32x4 cw = *(const u32x4*)(kc + 8 * st);
+    const u32x4 sw = *(const u32x4*)(ks + 8 * st);
+    kv[st] = u32x4{cw[0], cw[1], sw[0], sw[1]};
+    kv[st + 1] = u32x4{cw[2], cw[3], sw[2], sw[3]};
+  }
+#pragma unroll
+  for (int s = 0; s < kVLoads; ++s) {
+    const int t = t0 + min(kVPos * s + vpos, lastp);
+    vc[s] = *(const uint2*)(a.vcodes + code_page + (int64_t)t * a.kv_heads * HD + head + 8 * vdim);
+  }
+  vs = a.vscales[((int64_t)c * a.page_size + t0 + min(n16, lastp)) * a.kv_heads + kvh];
 }
 
 // One register of a quantised chunk (8 codes and their scale bytes: K's per channel, V's -- value
@@ -856,7 +894,8 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
     // loads it under a lane mask, that count is the smaller one on every path and each chunk also
     // waits for part of the next chunk's data.  So the next chunk, whole or partial, is loaded on
     // every path of the loop, clamped instead of masked, and the loop is left before a load.
-    // (The quantised and 8+ row variants keep the ring below: this form's registers spill there.)
+    // (The 8+ row variants keep the ring below: this form's registers spill there; quantised
+    // pools take the loops that follow.)
     auto load_clamped = [&](int t, u32x4 (&kv)[kSteps], u32x4 (&vv)[kVLoads]) {
       load_chunk_clamped<HD>(a, pt, blk0, kbase, vbase, t, t_end, n16, g, vpos, vdim, kv, vv);
     };
@@ -879,6 +918,76 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
         step(1);
       }
     }
+  } else if constexpr (PRE && COLD && R == 1 && HD == 64) {
+    // The same loop over a quantised pool: its quantised blocks lead every row, so the piece is a
+    // run of quantised chunks, then one of two-byte chunks (the residual window), each loop
+    // loading every chunk whole and clamped.  (One loop over both kinds, a branch choosing each
+    // chunk's loads, waits for every load in flight before each chunk's products.  At head size
+    // 128 these loops' registers spill, so it keeps that ring.)
+    auto cold_at = [&](int t) { return table_scalar(pt, (int)a.page_div.div((uint32_t)t) - blk0) < 0; };
+    u32x4 ck[2][kSteps];
+    uint2 cvc[2][kVLoads];
+    uint32_t cvs[2];
+    auto load_cold = [&](int t, u32x4 (&kv)[kSteps], uint2 (&vc)[kVLoads], uint32_t& vs) {
+      load_cold_clamped<HD>(a, pt, blk0, t, t_end, n16, g, vpos, vdim, kvh, kv, vc, vs);
+    };
+    bool misordered = false;  // a quantised block after a two-byte one (never made by the pool)
+    auto load_hot = [&](int t, u32x4 (&kv)[kSteps], u32x4 (&vv)[kVLoads]) {
+      misordered |= cold_at(t);
+      load_chunk_clamped<HD, true>(a, pt, blk0, kbase, vbase, t, t_end, n16, g, vpos, vdim, kv, vv);
+    };
+    auto step_cold = [&](u32x4 (&kv)[kSteps], const uint2 (&vc)[kVLoads], uint32_t vs) {
+      const bool kcodes = __builtin_amdgcn_ballot_w64(!scales_moderate<false>(kv)) == 0;
+      if (!kcodes) dequant_regs<E, false>(kv);
+      u32x4 vv[kVLoads];  // codes and the position's scale, as load_chunk lays a quantised V out
+#pragma unroll
+      for (int s = 0; s < kVLoads; ++s) vv[s] = u32x4{vc[s].x, vc[s].y, (uint32_t)__shfl((int)vs, kVPos * s + vpos), 0};
+      compute(tc, kv, vv, kcodes, true);
+      tc += kBlock;
+    };
+    auto step_hot = [&](int i) {
+      compute(tc, kr[i], vr[i], false, false);
+      tc += kBlock;
+    };
+    if (tc < t_end && cold_at(tc)) {
+      load_cold(tc, ck[0], cvc[0], cvs[0]);
+      for (;;) {
+        if (tc + kBlock >= t_end || !cold_at(tc + kBlock)) {
+          step_cold(ck[0], cvc[0], cvs[0]);
+          break;
+        }
+        load_cold(tc + kBlock, ck[1], cvc[1], cvs[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        step_cold(ck[0], cvc[0], cvs[0]);
+        if (tc + kBlock >= t_end || !cold_at(tc + kBlock)) {
+          step_cold(ck[1], cvc[1], cvs[1]);
+          break;
+        }
+        load_cold(tc + kBlock, ck[0], cvc[0], cvs[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        step_cold(ck[1], cvc[1], cvs[1]);
+      }
+    }
+    if (tc < t_end) {
+      load_hot(tc, kr[0], vr[0]);
+      for (;;) {
+        if (tc + kBlock >= t_end) {
+          step_hot(0);
+          break;
+        }
+        load_hot(tc + kBlock, kr[1], vr[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        step_hot(0);
+        if (tc + kBlock >= t_end) {
+          step_hot(1);
+          break;
+        }
+        load_hot(tc + kBlock, kr[0], vr[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        step_hot(1);
+      }
+    }
+    if (misordered && lane == 0) atomicOr(a.errors, BARQ_KV_ERRBIT_BAD_INDEX);
   } else {
     if (tc < t_end) {
       load_any(tc, kr[0], vr[0], cr[0]);

@@ -357,15 +357,17 @@ def test_decode_attention_reads_quantised_pages(hip, dtype, page, window, D):
     assert pool.errors() == 0
 
 
-@pytest.mark.parametrize("cap", [640, 1024])
-def test_decode_attention_on_quantised_pages_many_pairs(hip, cap):
+@pytest.mark.parametrize("cap,D", [(640, 128), (1024, 128), (640, 64), (1024, 64)])
+def test_decode_attention_on_quantised_pages_many_pairs(hip, cap, D):
     """Attention over a quantised pool with 128 (row, kv head) pairs of ragged rows (the one-launch
-    pair kernel: up to 44 chunks, and with up to 4 query rows up to 64): against the float64
-    reference over the dequantising gather's K/V."""
+    pair kernel: up to 44 chunks, and with up to 4 query rows up to 64; at head size 64 a loop over
+    the quantised chunks, then one over the window's, each chunk loaded whole and clamped): against
+    the float64 reference over the dequantising gather's K/V.  Rows shorter than the window, rows
+    whose pieces straddle the window's start, one and two query tokens."""
     from attn_ref import decode_attention_reference, within_tolerance
     from barqtrain_amd.paged import QuantPagePool
 
-    H, D, P, W = 4, 128, 16, 32
+    H, P, W = 4, 16, 32
     rng = np.random.default_rng(77 + cap)
     top = cap - 40
     lens = sorted([top, top - 15, 1, 16, 33] + rng.integers(40, top, size=27).tolist(), reverse=True)
@@ -382,12 +384,12 @@ def test_decode_attention_on_quantised_pages_many_pairs(hip, cap):
             done += n
     assert int(pool.cold_blocks.max()) > 0
     kd, vd = (t.double().cpu().numpy() for t in pool.gather(B))
-    for G in (4, 2):
-        q = hf_layout(B, G * H, 1, D, torch.bfloat16, gen).cuda()
+    for G, T in ((4, 1), (2, 1), (2, 2)):
+        q = hf_layout(B, G * H, T, D, torch.bfloat16, gen).cuda()
         want = decode_attention_reference(q.double().cpu().numpy(), kd, vd, lens, D ** -0.5)
         got = pool.attend(q, out_dtype=torch.float32)
         ok, ratio = within_tolerance(got.double().cpu().numpy(), want, **ATT_F32)
-        assert ok, f"G={G}: {ratio:.3g} x tolerance"
+        assert ok, f"G={G} T={T}: {ratio:.3g} x tolerance"
     assert pool.errors() == 0
 
 
@@ -519,14 +521,15 @@ def test_selection_larger_than_an_fp8_pool_on_gpu(hip):
     assert layer.pool.errors() == 0
 
 
-def test_decode_attention_on_quantised_pages_long_rows(hip):
+@pytest.mark.parametrize("D", [128, 64])
+def test_decode_attention_on_quantised_pages_long_rows(hip, D):
     """Attention over a quantised pool whose rows pass one table window (the long-row pair kernel
     over cold blocks: 5,000 and 1,500 positions, 8 pairs), against the float64 reference over the
     dequantising gather's K/V."""
     from attn_ref import decode_attention_reference, within_tolerance
     from barqtrain_amd.paged import QuantPagePool
 
-    H, D, P, W = 4, 128, 16, 64
+    H, P, W = 4, 16, 64
     lens = [5000, 1500]
     B, cap = len(lens), 5008
     pool = QuantPagePool(max_batch=B, max_blocks=cap // P, page_size=P, kv_heads=H, head_dim=D, dtype=torch.bfloat16,
