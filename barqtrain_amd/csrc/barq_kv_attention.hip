@@ -549,57 +549,18 @@ __device__ __forceinline__ u32x4 dequant_vector(const u32x4 x, bool value) {
 // A quantised chunk's K (VALUE false: codes and per-channel scales per register) or V (VALUE
 // true: codes and the position's scale) -> two-byte values.  When every vector of every lane
 // qualifies, exponent arithmetic decodes the registers unrolled; otherwise (a zero, subnormal or
-// NaN code, or an extreme scale somewhere in the wave) one rolled loop takes the registers one by
-// one, picked and put back through constant-index switches (a dynamic index would move the chunk
-// to scratch), so the rare path adds no register pressure to the common one.
+// NaN code, or an extreme scale somewhere in the wave) one out-of-line function takes the
+// registers by value and returns them decoded, so the rare path adds no register pressure to the
+// common one (inlined, even as a rolled loop, it made the quantised chunk loops spill).
 template <int N>
-__device__ __forceinline__ u32x4 chunk_reg(const u32x4 (&r)[N], int n) {
-  static_assert(N == 2 || N == 4 || N == 8, "chunk layouts of head sizes 64, 128 and 256");
-  if constexpr (N == 8) {
-    switch (n) {
-      case 0: return r[0];
-      case 1: return r[1];
-      case 2: return r[2];
-      case 3: return r[3];
-      case 4: return r[4];
-      case 5: return r[5];
-      case 6: return r[6];
-      default: return r[7];
-    }
-  } else if constexpr (N == 4) {
-    switch (n) {
-      case 0: return r[0];
-      case 1: return r[1];
-      case 2: return r[2];
-      default: return r[3];
-    }
-  } else {
-    return n == 0 ? r[0] : r[1];
-  }
-}
-template <int N>
-__device__ __forceinline__ void set_chunk_reg(u32x4 (&r)[N], int n, const u32x4 y) {
-  if constexpr (N == 8) {
-    switch (n) {
-      case 0: r[0] = y; break;
-      case 1: r[1] = y; break;
-      case 2: r[2] = y; break;
-      case 3: r[3] = y; break;
-      case 4: r[4] = y; break;
-      case 5: r[5] = y; break;
-      case 6: r[6] = y; break;
-      default: r[7] = y; break;
-    }
-  } else if constexpr (N == 4) {
-    switch (n) {
-      case 0: r[0] = y; break;
-      case 1: r[1] = y; break;
-      case 2: r[2] = y; break;
-      default: r[3] = y; break;
-    }
-  } else {
-    if (n == 0) r[0] = y; else r[1] = y;
-  }
+struct ChunkRegs {
+  u32x4 r[N];
+};
+template <int E, bool VALUE, int N>
+__device__ __noinline__ ChunkRegs<N> dequant_regs_exact(ChunkRegs<N> x) {
+#pragma unroll
+  for (int n = 0; n < N; ++n) x.r[n] = dequant_vector<E>(x.r[n], VALUE);
+  return x;
 }
 
 template <int E, bool VALUE, int N>
@@ -622,8 +583,12 @@ __device__ __forceinline__ void dequant_regs(u32x4 (&r)[N]) {
     }
     return;
   }
-#pragma unroll 1
-  for (int n = 0; n < N; ++n) set_chunk_reg(r, n, dequant_vector<E>(chunk_reg(r, n), VALUE));
+  ChunkRegs<N> x;
+#pragma unroll
+  for (int n = 0; n < N; ++n) x.r[n] = r[n];
+  x = dequant_regs_exact<E, VALUE, N>(x);
+#pragma unroll
+  for (int n = 0; n < N; ++n) r[n] = x.r[n];
 }
 
 // Fast operands from a quantised chunk (scale bytes in [64, 191], checked per chunk): the codes
@@ -918,12 +883,11 @@ __device__ void attend_piece(const AttnArgs& a, float (&lp)[kBlock][kMaxRows],
         step(1);
       }
     }
-  } else if constexpr (PRE && COLD && R == 1 && HD == 64) {
+  } else if constexpr (PRE && COLD && R == 1) {
     // The same loop over a quantised pool: its quantised blocks lead every row, so the piece is a
     // run of quantised chunks, then one of two-byte chunks (the residual window), each loop
     // loading every chunk whole and clamped.  (One loop over both kinds, a branch choosing each
-    // chunk's loads, waits for every load in flight before each chunk's products.  At head size
-    // 128 these loops' registers spill, so it keeps that ring.)
+    // chunk's loads, waits for every load in flight before each chunk's products.)
     auto cold_at = [&](int t) { return table_scalar(pt, (int)a.page_div.div((uint32_t)t) - blk0) < 0; };
     u32x4 ck[2][kSteps];
     uint2 cvc[2][kVLoads];
