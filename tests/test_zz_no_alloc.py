@@ -138,3 +138,17 @@ def test_noalloc_refuses_requests_beyond_scratch(capi):
                                                torch.cuda.current_stream().cuda_stream)
     assert rc == ERR_SCRATCH
     assert "scratch" in capi.barq_kv_status_string(rc).decode()
+
+
+def test_noalloc_head_256_limits(capi):
+    # Head size 256 doubles the records: batch 64 with 8 KV heads fits the scratch at G * tokens = 9
+    # ((2048 + 512) records of 9 * 258 floats, 23.8 MB) but not at 10; G * tokens = 16 is refused
+    # at any batch (33.9 MB at batch 1).
+    pool = CPool(max_batch=64, max_blocks=1, page_size=16, heads=8, dim=256, dtype=torch.bfloat16, num_pages=16)
+    assert capi.barq_kv_attention_workspace_bytes(pool.ref, 64, 9 * 8, 1, 0, 0) <= SCRATCH_BYTES
+    assert capi.barq_kv_attention_workspace_bytes(pool.ref, 64, 10 * 8, 1, 0, 0) > SCRATCH_BYTES
+    assert capi.barq_kv_attention_workspace_bytes(pool.ref, 1, 16 * 8, 1, 0, 0) > SCRATCH_BYTES
+    rc = capi.barq_kv_decode_attention_noalloc(pool.ref, ctypes.c_void_p(16), 1, 128, 1, 256, 256, 256,
+                                               ctypes.c_void_p(16), 256, 256, 256, 1.0, 0, 0, 0,
+                                               torch.cuda.current_stream().cuda_stream)
+    assert rc == ERR_SCRATCH
