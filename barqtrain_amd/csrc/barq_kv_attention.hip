@@ -1388,6 +1388,8 @@ hipError_t launch_typed(AttnArgs a, bool merge, hipStream_t stream) {
                          : COLD || pairs < 2 * kPairMinPairs ? kPairMaxChunksR1
                                                              : kPairMaxChunksR1Wide;
     if (nsplit > 2) max_chunks = std::min<int64_t>(kTableEntries, std::max(max_chunks, nsplit * kSplitChunksPerPart));
+    // Two workgroups a pair halve each one's chunks: 5 to 8 query rows take the bound of up to 4.
+    if (nsplit == 2 && R > 1 && pairs >= kPairMinPairs) max_chunks = std::max(max_chunks, kPairMaxChunksR1);
     if (a.range_chunks == 0 && pairs > 0 && chunks <= max_chunks) {
       if (nsplit > 2) {
         hipLaunchKernelGGL(split_any, dim3((unsigned)(nsplit * pairs)), dim3(kPairWaves * kWave), 0, stream, a);

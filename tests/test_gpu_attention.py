@@ -139,6 +139,21 @@ def test_head_dim_256(dtype, page):
     assert pool.errors() == 0
 
 
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 64)])
+def test_five_to_eight_rows_on_two_workgroups_a_pair(dtype, D):
+    """5 to 8 query rows over 128 pairs of rows of 45 to 64 chunks: two workgroups a pair (the
+    bound of up to 4 rows), ragged rows with empty, one-position and chunk-boundary lengths, one
+    and two query tokens, both output types."""
+    rng = np.random.default_rng(64 + D)
+    lens = [1024, 1023, 1009, 720, 705, 704, 0, 1, 17] + rng.integers(0, 1025, size=23).tolist()
+    pool, kd, vd, lens = make_rows(len(lens), 4, 16, lens, dtype, seed=640 + D, order_seed=641 + D, D=D)
+    ws = None
+    for i, (G, T) in enumerate([(8, 1), (5, 1), (3, 2), (4, 2)]):
+        ws = check(pool, kd, vd, lens, G, T, dtype, seed=700 + i, ws=ws)
+    check(pool, kd, vd, lens, 8, 1, dtype, seed=9, out_f32=False)
+    assert pool.errors() == 0
+
+
 @pytest.mark.parametrize("dtype,page,D", [(torch.bfloat16, 16, 128), (torch.float16, 32, 128), (torch.bfloat16, 16, 64)])
 def test_many_short_pairs_one_launch(dtype, page, D):
     """128+ (row, kv head) pairs of at most 704 positions with the automatic split take one

@@ -384,7 +384,7 @@ def test_decode_attention_on_quantised_pages_many_pairs(hip, cap, D):
             done += n
     assert int(pool.cold_blocks.max()) > 0
     kd, vd = (t.double().cpu().numpy() for t in pool.gather(B))
-    for G, T in ((4, 1), (2, 1), (2, 2)):
+    for G, T in ((4, 1), (2, 1), (2, 2), (8, 1)):
         q = hf_layout(B, G * H, T, D, torch.bfloat16, gen).cuda()
         want = decode_attention_reference(q.double().cpu().numpy(), kd, vd, lens, D ** -0.5)
         got = pool.attend(q, out_dtype=torch.float32)
